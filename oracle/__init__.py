@@ -1,0 +1,411 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes bindings to the CPU oracle (llmq_oracle.c).
+
+The oracle is a C restatement of llm_mojo's CPU arithmetic for the quantized
+matmul path (tensor.mojo, kernels.mojo, gguf.mojo, kvcache.mojo,
+gpt2t.mojo).  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg import this module, and only as the checker or the timed CPU baseline;
+the product (llm_mojo_amd/) never does.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+
+EPI_BIAS, EPI_GELU, EPI_RESID = 1, 2, 4
+GGML = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+
+
+def build():
+    """Compiles liboracle.so with oracle/Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class QM(ctypes.Structure):
+    """orc_qm: a QuantMatrix in the reference's own storage layout."""
+
+    _fields_ = [
+        ("bits", ctypes.c_int32),
+        ("sym", ctypes.c_int32),
+        ("a16", ctypes.c_int32),
+        ("blocked", ctypes.c_int32),
+        ("perch", ctypes.c_int32),
+        ("n", ctypes.c_int64),
+        ("k", ctypes.c_int64),
+        ("group", ctypes.c_int64),
+        ("data", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("zp", ctypes.c_void_p),
+    ]
+
+
+class KV(ctypes.Structure):
+    _fields_ = [
+        ("n_layer", ctypes.c_int32),
+        ("max_t", ctypes.c_int32),
+        ("n_head", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("ks", ctypes.c_void_p),
+        ("vs", ctypes.c_void_p),
+    ]
+
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+I32 = ctypes.c_int
+
+
+def _declare(L):
+    sig = {
+        "orc_set_round_half_even": (None, [I32]),
+        "orc_set_threads": (None, [I32]),
+        "orc_get_threads": (I32, []),
+        "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+        "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+        "orc_nibble_at": (None, [I32, I64, P, P]),
+        "orc_qm_from_f32": (I32, [P, P, I64, I64, I32]),
+        "orc_qm_code": (I32, [P, I64, I64]),
+        "orc_qm_nbytes": (I64, [P]),
+        "orc_qm_dequant_row": (None, [P, I64, P]),
+        "orc_qm_dot_row": (ctypes.c_float, [P, I64, P]),
+        "orc_qm_permute_x_i16": (I32, [P, P, I64, P, P]),
+        "orc_qm_dot_row_i16": (ctypes.c_float, [P, I64, P, P]),
+        "orc_qm_unpack_row_i16": (None, [P, I64, P, P]),
+        "orc_qm_group_sums": (None, [P, P, P]),
+        "orc_quantize_rows": (None, [P, I64, I64, P, P]),
+        "orc_matmul_rows_a16": (None, [P, P, P, P, I64, I64, I64, I32]),
+        "orc_gguf_block_size": (I32, [I32]),
+        "orc_gguf_block_bytes": (I32, [I32]),
+        "orc_k_scale_min": (None, [P, I32, P, P]),
+        "orc_gguf_dequant_row": (None, [I32, P, I64, P]),
+        "orc_gguf_dot_row": (ctypes.c_float, [I32, P, I64, P]),
+        "orc_gguf_dot_row_i16": (ctypes.c_float, [I32, P, I64, P]),
+        "orc_gguf_unpack_row_i16": (None, [I32, P, I64, P, P]),
+        "orc_gguf_gemv": (None, [I32, P, I64, I64, P, P, P, I32]),
+        "orc_gguf_head_i16": (None, [I32, P, I64, I64, P, I64, P]),
+        "orc_layernorm": (None, [P, P, P, P, I64, I64]),
+        "orc_kv_store": (None, [P, I32, I32, P, P]),
+        "orc_kv_attend_one": (None, [P, P, P, I32, I32, I32, I32]),
+        "orc_kv_attend": (None, [P, P, P, I32, I32, I32]),
+        "orc_rng_init": (None, [P, I64]),
+        "orc_rng_uniform": (ctypes.c_float, [P]),
+        "orc_argmax": (I64, [P, I64]),
+        "orc_gpt2_new": (P, [P, I32, I32, I32]),
+        "orc_gpt2_free": (None, [P]),
+        "orc_gpt2_mat": (P, [P, I32]),
+        "orc_gpt2_kv": (P, [P]),
+        "orc_gpt2_act": (P, [P, I32]),
+        "orc_gpt2_forward": (P, [P, P, I32, I32]),
+        "orc_gpt2_generate": (I32, [P, P, I32, I32, P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def set_round_half_even(on):
+    lib().orc_set_round_half_even(1 if on else 0)
+
+
+def set_threads(n):
+    lib().orc_set_threads(int(n))
+
+
+def f32_to_f16_bits(v):
+    return lib().orc_f32_to_f16(ctypes.c_float(v))
+
+
+def f16_bits_to_f32(h):
+    return lib().orc_f16_to_f32(ctypes.c_uint16(h))
+
+
+class QuantMatrix:
+    """QuantMatrix[bits, group, sym, a16] (tensor.mojo:230-661) on the CPU."""
+
+    def __init__(self, bits, group, sym, a16):
+        self.bits, self.group_param, self.sym, self.a16 = bits, group, sym, a16
+
+    @classmethod
+    def from_f32(cls, src, bits, group, sym=False, a16=True, reduce_rows=True):
+        src = np.ascontiguousarray(src, dtype=np.float32)
+        rows, cols = src.shape
+        self = cls(bits, group, sym, a16)
+        n, k = (cols, rows) if reduce_rows else (rows, cols)
+        g = k if group == 0 else group
+        self.data = np.zeros(n * k * bits // 8, np.uint8)
+        self.scale = np.zeros(n * k // g, np.uint16)
+        self.zp = np.zeros(n * k // g, np.uint8)
+        self.s = QM(bits, 1 if sym else 0, 1 if a16 else 0, 0, 0, 0, 0, group,
+                    self.data.ctypes.data, self.scale.ctypes.data, self.zp.ctypes.data)
+        rc = lib().orc_qm_from_f32(ctypes.byref(self.s), ptr(src), rows, cols, 1 if reduce_rows else 0)
+        if rc != 0:
+            raise ValueError("group size must divide the reduction axis and be a multiple of 32")
+        self.n, self.k, self.group = self.s.n, self.s.k, self.s.group
+        self.blocked = bool(self.s.blocked)
+        return self
+
+    @property
+    def ref(self):
+        return ctypes.byref(self.s)
+
+    def nbytes(self):
+        return lib().orc_qm_nbytes(self.ref)
+
+    def code(self, row, col):
+        return lib().orc_qm_code(self.ref, row, col)
+
+    def codes(self):
+        """All codes u[n, k] in natural column order (via nibble_at)."""
+        if self.bits == 8:
+            return self.data.reshape(self.n, self.k).copy()
+        d = self.data.reshape(self.n, self.k // 2)
+        cols = np.arange(self.k)
+        byte, high = nibble_layout(self.blocked, cols)
+        b = d[:, byte]
+        return np.where(high[None, :], b >> 4, b & 0xF).astype(np.uint8)
+
+    def scales_f32(self):
+        return self.scale.view(np.float16).astype(np.float32).reshape(self.n, self.k // self.group)
+
+    def zps(self):
+        return self.zp.reshape(self.n, self.k // self.group)
+
+    def dequant(self):
+        out = np.zeros((self.n, self.k), np.float32)
+        for r in range(self.n):
+            lib().orc_qm_dequant_row(self.ref, r, ptr(out[r]))
+        return out
+
+    def dot_row(self, row, x):
+        x = np.ascontiguousarray(x, np.float32)
+        return lib().orc_qm_dot_row(self.ref, row, ptr(x))
+
+    def permute_x_i16(self, xq):
+        xp = np.zeros(self.k, np.int16)
+        xs = np.zeros(self.k // 16, np.float32)
+        ok = lib().orc_qm_permute_x_i16(self.ref, ptr(xq), self.k, ptr(xp), ptr(xs))
+        return bool(ok), xp, xs
+
+    def dot_row_i16(self, row, x1, xs):
+        return lib().orc_qm_dot_row_i16(self.ref, row, ptr(x1), ptr(xs))
+
+    def unpack_row_i16(self, row):
+        dst = np.zeros(self.k, np.int16)
+        sc = np.zeros(self.k // self.group, np.float32)
+        lib().orc_qm_unpack_row_i16(self.ref, row, ptr(dst), ptr(sc))
+        return dst, sc
+
+    def group_sums(self, xq):
+        G = np.zeros(self.n * (self.k // self.group), np.int64)
+        lib().orc_qm_group_sums(self.ref, ptr(np.ascontiguousarray(xq, np.int16)), ptr(G))
+        return G.reshape(self.n, self.k // self.group)
+
+
+def nibble_layout(blocked, cols):
+    """Vectorised nibble_at (tensor.mojo:385-404): (byte, high) per column."""
+    cols = np.asarray(cols, np.int64)
+    if blocked:
+        w = cols % 256
+        e = w % 32
+        p = e // 2
+        lane = w // 32 + 8 * (p // 8)
+        chunk = (cols // 256) * 8 + p % 8
+        j = 2 * lane + e % 2
+    else:
+        chunk = cols // 32
+        j = cols % 32
+    return chunk * 16 + j % 16, j >= 16
+
+
+def quantize_rows(x):
+    x = np.ascontiguousarray(x, np.float32)
+    T, IN = x.shape
+    xq = np.zeros((T, IN), np.int16)
+    sx = np.zeros(T, np.float32)
+    lib().orc_quantize_rows(ptr(x), T, IN, ptr(xq), ptr(sx))
+    return xq, sx
+
+
+def matmul_rows_a16(x, w, b=None, flags=EPI_BIAS, out=None):
+    """out[T, OUT] (+)= act(x @ w^T + b) as kernels.matmul_rows_a16."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, IN = x.shape
+    if out is None:
+        out = np.zeros((T, w.n), np.float32)
+    if b is None:
+        b = np.zeros(w.n, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    lib().orc_matmul_rows_a16(ptr(out), ptr(x), w.ref, ptr(b), T, IN, w.n, flags)
+    return out
+
+
+def gguf_block_size(t):
+    return lib().orc_gguf_block_size(t)
+
+
+def gguf_block_bytes(t):
+    return lib().orc_gguf_block_bytes(t)
+
+
+def gguf_dequant(t, w, rows, cols):
+    w = np.ascontiguousarray(w, np.uint8)
+    rb = cols // gguf_block_size(t) * gguf_block_bytes(t)
+    out = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        lib().orc_gguf_dequant_row(t, w[r * rb:].ctypes.data, cols, ptr(out[r]))
+    return out
+
+
+def gguf_dot_row(t, row_bytes, cols, x):
+    return lib().orc_gguf_dot_row(t, ptr(np.ascontiguousarray(row_bytes, np.uint8)), cols,
+                                  ptr(np.ascontiguousarray(x, np.float32)))
+
+
+def gguf_gemv(t, w, rows, cols, x, b=None, flags=0, out=None):
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    if out is None:
+        out = np.zeros(rows, np.float32)
+    if b is None:
+        b = np.zeros(rows, np.float32)
+    lib().orc_gguf_gemv(t, ptr(w), rows, cols, ptr(x), ptr(np.ascontiguousarray(b, np.float32)), ptr(out), flags)
+    return out
+
+
+def gguf_head_i16(t, w, V, C, h):
+    h = np.ascontiguousarray(h, np.float32).reshape(-1, C)
+    T = h.shape[0]
+    out = np.zeros((T, V), np.float32)
+    lib().orc_gguf_head_i16(t, ptr(np.ascontiguousarray(w, np.uint8)), V, C, ptr(h), T, ptr(out))
+    return out
+
+
+def gguf_dot_row_i16(t, row_bytes, cols, xq):
+    return lib().orc_gguf_dot_row_i16(t, ptr(np.ascontiguousarray(row_bytes, np.uint8)), cols,
+                                      ptr(np.ascontiguousarray(xq, np.int16)))
+
+
+def gguf_unpack_row_i16(t, row_bytes, cols):
+    dst = np.zeros(cols, np.int16)
+    sc = np.zeros(cols // (256 if t == GGML["Q6_K"] else 32), np.float32)
+    lib().orc_gguf_unpack_row_i16(t, ptr(np.ascontiguousarray(row_bytes, np.uint8)), cols, ptr(dst), ptr(sc))
+    return dst, sc
+
+
+def k_scale_min(q12, j):
+    q12 = np.ascontiguousarray(q12, np.uint8)
+    sc = ctypes.c_int()
+    mn = ctypes.c_int()
+    lib().orc_k_scale_min(ptr(q12), j, ctypes.byref(sc), ctypes.byref(mn))
+    return sc.value, mn.value
+
+
+def layernorm(x, w, b):
+    x = np.ascontiguousarray(x, np.float32)
+    T, C = x.shape
+    out = np.zeros_like(x)
+    lib().orc_layernorm(ptr(out), ptr(x), ptr(np.ascontiguousarray(w, np.float32)),
+                        ptr(np.ascontiguousarray(b, np.float32)), T, C)
+    return out
+
+
+class QuantKV8:
+    """QuantKV[8] (kvcache.mojo:248-385) on the CPU."""
+
+    def __init__(self, n_layer, max_t, n_head, head_dim):
+        n = n_layer * max_t * n_head * head_dim
+        ns = n_layer * max_t * n_head
+        self.k = np.zeros(n, np.int8)
+        self.v = np.zeros(n, np.int8)
+        self.ks = np.zeros(ns, np.float32)
+        self.vs = np.zeros(ns, np.float32)
+        self.s = KV(n_layer, max_t, n_head, head_dim, self.k.ctypes.data, self.v.ctypes.data,
+                    self.ks.ctypes.data, self.vs.ctypes.data)
+        self.C = n_head * head_dim
+
+    def store(self, layer, pos, k, v):
+        lib().orc_kv_store(ctypes.byref(self.s), layer, pos, ptr(np.ascontiguousarray(k, np.float32)),
+                           ptr(np.ascontiguousarray(v, np.float32)))
+
+    def attend(self, qkv, layer, T, pos0):
+        qkv = np.ascontiguousarray(qkv, np.float32)
+        out = np.zeros((T, self.C), np.float32)
+        lib().orc_kv_attend(ctypes.byref(self.s), ptr(out), ptr(qkv), layer, T, pos0)
+        return out
+
+
+class Rng:
+    """gpt2t.mojo's Rng (777-789)."""
+
+    class _S(ctypes.Structure):
+        _fields_ = [("state", ctypes.c_uint64)]
+
+    def __init__(self, seed):
+        self.s = Rng._S()
+        lib().orc_rng_init(ctypes.byref(self.s), seed)
+
+    def uniform(self):
+        return lib().orc_rng_uniform(ctypes.byref(self.s))
+
+
+def argmax(logits):
+    logits = np.ascontiguousarray(logits, np.float32)
+    return lib().orc_argmax(ptr(logits), logits.size)
+
+
+class GPT2:
+    """The reference GPT-2 (gpt2t.mojo Model, int4-g32-a16 layers by default,
+    HEAD8_A16 head, QuantKV[8]) on the CPU."""
+
+    def __init__(self, params, bits=4, group=32, sym=False):
+        self._keep = [np.ascontiguousarray(p, np.float32) for p in params]
+        arr = (ctypes.c_void_p * len(self._keep))(*[p.ctypes.data for p in self._keep])
+        self.h = lib().orc_gpt2_new(arr, bits, group, 1 if sym else 0)
+        self._keep = None  # the model copied what it keeps
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_gpt2_free(self.h)
+            self.h = None
+
+    def forward(self, tokens, pos0):
+        toks = np.ascontiguousarray(tokens, np.int64)
+        p = lib().orc_gpt2_forward(self.h, ptr(toks), len(toks), pos0)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(50257,)).copy()
+
+    def generate(self, prompt, steps):
+        prompt = np.ascontiguousarray(prompt, np.int64)
+        out = np.zeros(steps, np.int64)
+        n = lib().orc_gpt2_generate(self.h, ptr(prompt), len(prompt), steps, ptr(out))
+        return out[:n]
+
+    def mat(self, i):
+        """The orc_qm of layer matrix i (l * 4 + j), or of the head for -1."""
+        return ctypes.cast(lib().orc_gpt2_mat(self.h, i), ctypes.POINTER(QM)).contents
+
+    def act(self, which, n):
+        p = lib().orc_gpt2_act(self.h, which)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(n,)).copy()

@@ -1,0 +1,1134 @@
+/*
+ * llmq_oracle.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of llm_mojo's CPU arithmetic for its quantized-weight
+ * matmul path: the QuantMatrix quantizer and code layouts, int16 activation
+ * quantization, the VPDPWSSD-based integer GEMV / GEMM kernels, the GGUF
+ * block decoders, the int8 KV cache with float attention, and the GPT-2 model
+ * step that calls them.  It is the parity checker for the HIP product and the
+ * CPU baseline timed next to it.  Nothing in llm_mojo_amd/ links, loads or
+ * calls this file; only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg do.
+ *
+ * Every function cites the reference file:line it follows (paths relative to
+ * the llm_mojo tree).  Floating-point operations follow the reference's order
+ * (16-lane SIMD accumulators are emulated lane by lane; fused multiply-adds
+ * only where the reference calls .fma), so the file must be compiled with
+ * -ffp-contract=off and without fast-math.
+ *
+ * Pinning status (what each function is checked against lives in tests/):
+ *   - tie rule of Mojo's round(): parity unpinned (Mojo 1.1 stdlib absent);
+ *     default half-away-from-zero, switchable with orc_set_round_half_even.
+ *   - order of SIMD.reduce_add / reduce_max: parity unpinned; emulated as a
+ *     halving tree (lanes 0-7 + 8-15, ...).  Moves fp32 bits only.
+ *   - last-ulp results of Mojo's exp / tanh: parity unpinned; libm's expf and
+ *     tanhf are used.  Moves fp32 bits only.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define L16 16
+
+/* ------------------------------------------------------------------------ */
+/* Scalar helpers                                                            */
+/* ------------------------------------------------------------------------ */
+
+static int g_half_even = 0;
+
+/* Mojo std.math.round (tensor.mojo:377,381; kernels.mojo:415;
+ * kvcache.mojo:330).  Tie rule unpinned: half away from zero by default. */
+void orc_set_round_half_even(int on) { g_half_even = on; }
+static inline float orc_round(float v) { return g_half_even ? nearbyintf(v) : roundf(v); }
+
+/* Int(float) for a value already rounded to an integer.  NaN (a scale that
+ * rounded to zero in float16: outside the reference's defined inputs) maps
+ * to 0, and out-of-range values saturate, so the clamp that follows is
+ * well defined. */
+static inline int64_t orc_to_int(float r) {
+    if (r != r) return 0;
+    if (r > 9.0e18f) return INT64_MAX / 2;
+    if (r < -9.0e18f) return INT64_MIN / 2;
+    return (int64_t)r;
+}
+
+/* float32 -> IEEE binary16 bits, round to nearest even (Mojo's
+ * .cast[DType.float16](), tensor.mojo:371). */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) /* inf, nan */
+        return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? (0x200u | ((ax >> 13) & 0x3ffu)) : 0));
+    if (ax >= 0x47800000u) return (uint16_t)(sign | 0x7c00u); /* >= 65536 */
+    uint32_t e = ax >> 23;
+    if (e < 102) return (uint16_t)sign; /* < 2^-25: rounds to zero */
+    if (e < 113) {                      /* f16 subnormal: n * 2^-24 */
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126 - e; /* 14..24 */
+        uint32_t n = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (n & 1))) n++;
+        return (uint16_t)(sign | n);
+    }
+    uint32_t h = ((e - 112) << 10) | ((ax & 0x7fffffu) >> 13);
+    uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) h++; /* carry may reach inf: correct */
+    return (uint16_t)(sign | h);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ff, x;
+    if (e == 0) {
+        if (m == 0) {
+            x = sign;
+        } else { /* subnormal: m * 2^-24, exact in float */
+            float v = (float)m * (1.0f / 16777216.0f);
+            memcpy(&x, &v, 4);
+            x |= sign;
+        }
+    } else if (e == 31) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else {
+        x = sign | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* SIMD[f32,16].reduce_add: order unpinned, emulated as a halving tree. */
+static inline float red16(const float *v) {
+    float a[8], b[4], c[2];
+    for (int i = 0; i < 8; i++) a[i] = v[i] + v[i + 8];
+    for (int i = 0; i < 4; i++) b[i] = a[i] + a[i + 4];
+    for (int i = 0; i < 2; i++) c[i] = b[i] + b[i + 2];
+    return c[0] + c[1];
+}
+
+/* dot_pairs (tensor.mojo:34-46): acc[i] + a[2i]*b[2i] + a[2i+1]*b[2i+1],
+ * int32 lanes with wraparound (VPDPWSSD). */
+static inline void dot_pairs(int32_t *acc, const int16_t *a, const int16_t *b) {
+    for (int i = 0; i < L16; i++) {
+        int64_t s = (int64_t)a[2 * i] * b[2 * i] + (int64_t)a[2 * i + 1] * b[2 * i + 1];
+        acc[i] = (int32_t)(uint32_t)((uint32_t)acc[i] + (uint32_t)(int32_t)s);
+    }
+}
+
+/* kernels.finish (274-282) / store_out (38-48): GELU, residual, store. */
+#define EPI_BIAS 1
+#define EPI_GELU 2
+#define EPI_RESID 4
+static inline float gelu_f(float r) {
+    const float s = 0.7978845608028654f;
+    float t = 0.044715f * r;
+    t = t * r;
+    t = t * r;
+    float u = r + t;
+    float th = tanhf(s * u);
+    float a = 0.5f * r;
+    return a * (1.0f + th);
+}
+static inline void finish(float *o, int64_t i, float r, int flags) {
+    if (flags & EPI_GELU) r = gelu_f(r);
+    if (flags & EPI_RESID) r += o[i];
+    o[i] = r;
+}
+
+/* ------------------------------------------------------------------------ */
+/* QuantMatrix (tensor.mojo:230-661)                                        */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    int32_t bits;     /* 4 or 8 */
+    int32_t sym;      /* SYMMETRIC */
+    int32_t a16;      /* A16 */
+    int32_t blocked;  /* BLOCKED = a16 && bits == 4 && GROUP == 32 (tensor.mojo:296) */
+    int32_t perch;    /* GROUP == 0: one group per row ("per-channel") */
+    int64_t n;        /* rows: outputs */
+    int64_t k;        /* cols: the reduction axis */
+    int64_t group;    /* weights per group (GROUP, or k for per-channel) */
+    uint8_t *data;    /* codes, n * k * bits / 8 */
+    uint16_t *scale;  /* float16 bits, n * k / group */
+    uint8_t *zp;      /* n * k / group */
+} orc_qm;
+
+/* nibble_at (tensor.mojo:385-404): byte within the row holding column col's
+ * code, and whether it is the high nibble. */
+static inline void nibble_at(int blocked, int64_t col, int64_t *byte, int *high) {
+    int64_t j, chunk;
+    if (blocked) {
+        int64_t w = col % 256, e = w % 32, p = e / 2;
+        int64_t lane = w / 32 + 8 * (p / 8);
+        chunk = (col / 256) * 8 + p % 8;
+        j = 2 * lane + e % 2;
+    } else {
+        chunk = col / 32;
+        j = col % 32;
+    }
+    *byte = chunk * 16 + j % 16;
+    *high = j >= 16;
+}
+void orc_nibble_at(int blocked, int64_t col, int64_t *byte, int *high) { nibble_at(blocked, col, byte, high); }
+
+/* set_code / code (tensor.mojo:406-429) */
+static inline void set_code(const orc_qm *m, int64_t row, int64_t col, int u) {
+    uint8_t *p = m->data + row * m->k * m->bits / 8;
+    if (m->bits == 8) {
+        p[col] = (uint8_t)u;
+        return;
+    }
+    int64_t b;
+    int hi;
+    nibble_at(m->blocked, col, &b, &hi);
+    if (hi)
+        p[b] = (uint8_t)((p[b] & 0x0f) | (u << 4));
+    else
+        p[b] = (uint8_t)((p[b] & 0xf0) | u);
+}
+static inline int get_code(const orc_qm *m, int64_t row, int64_t col) {
+    const uint8_t *p = m->data + row * m->k * m->bits / 8;
+    if (m->bits == 8) return p[col];
+    int64_t b;
+    int hi;
+    nibble_at(m->blocked, col, &b, &hi);
+    return hi ? (p[b] >> 4) : (p[b] & 0xf);
+}
+int orc_qm_code(const orc_qm *m, int64_t row, int64_t col) { return get_code(m, row, col); }
+
+static inline int clamp_code(int64_t u, int levels) { /* tensor.mojo:664-667 */
+    return (int)(u < 0 ? 0 : (u > levels ? levels : u));
+}
+
+/* QuantMatrix.from_f32 (tensor.mojo:334-383).  m->bits/sym/a16 and m->group
+ * (0 = per-channel) are inputs; m->data/scale/zp are caller-allocated with
+ * the sizes orc_qm_sizes reports.  Returns 0, or -1 for a bad group. */
+int orc_qm_from_f32(orc_qm *m, const float *src, int64_t rows, int64_t cols, int reduce_rows) {
+    int64_t n = reduce_rows ? cols : rows;
+    int64_t k = reduce_rows ? rows : cols;
+    int64_t group = m->group == 0 ? k : m->group;
+    if (k % group != 0 || group % 32 != 0) return -1;
+    m->blocked = m->a16 && m->bits == 4 && m->group == 32;
+    m->perch = m->group == 0;
+    m->n = n;
+    m->k = k;
+    m->group = group;
+    int levels = (1 << m->bits) - 1, half = 1 << (m->bits - 1);
+    int64_t gpr = k / group;
+    memset(m->data, 0, (size_t)(n * k * m->bits / 8));
+    float *vals = (float *)malloc(sizeof(float) * (size_t)group);
+    for (int64_t r = 0; r < n; r++) {
+        for (int64_t g = 0; g < gpr; g++) {
+            float lo = 0.0f, hi = 0.0f;
+            for (int64_t j = 0; j < group; j++) {
+                int64_t c = g * group + j;
+                float v = reduce_rows ? src[c * cols + r] : src[r * cols + c];
+                vals[j] = v;
+                lo = v < lo ? v : lo;
+                hi = v > hi ? v : hi;
+            }
+            float s;
+            if (m->sym) {
+                float a = -lo > hi ? -lo : hi;
+                s = a / (float)(half - 1);
+            } else {
+                s = (hi - lo) / (float)levels;
+            }
+            if (s == 0.0f) s = 1.0f;
+            uint16_t s16 = orc_f32_to_f16(s);
+            float sf = orc_f16_to_f32(s16);
+            int zp = m->sym ? half : clamp_code(orc_to_int(orc_round(-lo / sf)), levels);
+            m->scale[r * gpr + g] = s16;
+            m->zp[r * gpr + g] = (uint8_t)zp;
+            for (int64_t j = 0; j < group; j++) {
+                int64_t u = orc_to_int(orc_round(vals[j] / sf)) + zp;
+                set_code(m, r, g * group + j, clamp_code(u, levels));
+            }
+        }
+    }
+    free(vals);
+    return 0;
+}
+
+/* nbytes (tensor.mojo:629-632) */
+int64_t orc_qm_nbytes(const orc_qm *m) { return m->n * m->k * m->bits / 8 + (m->n * m->k / m->group) * 3; }
+
+/* row_op (tensor.mojo:431-476): dequantize a row (DOT=0) or the partial sums
+ * of its dot product with x (DOT=1), returned as the 16 lanes' reduce_add. */
+static float row_op(const orc_qm *m, int64_t row, float *dst, const float *x, int dot) {
+    const uint8_t *p = m->data + row * m->k * m->bits / 8;
+    int64_t gpr = m->k / m->group;
+    if (m->blocked) { /* scalar path (tensor.mojo:438-452) */
+        float d = 0.0f;
+        for (int64_t k = 0; k < m->k; k++) {
+            int64_t g = row * gpr + k / m->group;
+            float v = (float)(get_code(m, row, k) - (int)m->zp[g]) * orc_f16_to_f32(m->scale[g]);
+            if (dot)
+                d += v * x[k];
+            else
+                dst[k] = v;
+        }
+        return d; /* acc[0] = d; reduce_add of (d, 0, ...) is d */
+    }
+    float acc[L16] = {0};
+    for (int64_t g = 0; g < gpr; g++) {
+        float s = orc_f16_to_f32(m->scale[row * gpr + g]);
+        float zp = (float)m->zp[row * gpr + g];
+        float accg[L16] = {0};
+        for (int64_t c = 0; c < m->group / 32; c++) {
+            int64_t k0 = g * m->group + 32 * c;
+            float v0[L16], v1[L16];
+            for (int i = 0; i < L16; i++) {
+                if (m->bits == 4) {
+                    uint8_t b = p[k0 / 2 + i];
+                    v0[i] = (float)(b & 0xf) - zp;
+                    v1[i] = (float)(b >> 4) - zp;
+                } else {
+                    v0[i] = (float)p[k0 + i] - zp;
+                    v1[i] = (float)p[k0 + 16 + i] - zp;
+                }
+            }
+            for (int i = 0; i < L16; i++) {
+                if (dot) {
+                    accg[i] = fmaf(v0[i], x[k0 + i], accg[i]);
+                    accg[i] = fmaf(v1[i], x[k0 + 16 + i], accg[i]);
+                } else {
+                    dst[k0 + i] = v0[i] * s;
+                    dst[k0 + 16 + i] = v1[i] * s;
+                }
+            }
+        }
+        if (dot)
+            for (int i = 0; i < L16; i++) acc[i] = fmaf(accg[i], s, acc[i]);
+    }
+    return red16(acc);
+}
+void orc_qm_dequant_row(const orc_qm *m, int64_t row, float *dst) { (void)row_op(m, row, dst, dst, 0); }
+float orc_qm_dot_row(const orc_qm *m, int64_t row, const float *x) { return row_op(m, row, NULL, x, 1); }
+
+/* codes_i16 (tensor.mojo:484-496): 32 codes from column k0, minus zp. */
+static inline void codes_i16(const orc_qm *m, const uint8_t *p, int64_t k0, int16_t zp, int16_t *out) {
+    for (int i = 0; i < 16; i++) {
+        if (m->bits == 4) {
+            uint8_t b = p[k0 / 2 + i];
+            out[i] = (int16_t)((b & 0xf) - zp);
+            out[16 + i] = (int16_t)((b >> 4) - zp);
+        } else {
+            out[i] = (int16_t)(p[k0 + i] - zp);
+            out[16 + i] = (int16_t)(p[k0 + 16 + i] - zp);
+        }
+    }
+}
+
+/* permute_x_i16 (tensor.mojo:498-516).  Returns 1 (and fills dst, sums) for
+ * the BLOCKED layout, 0 otherwise. */
+int orc_qm_permute_x_i16(const orc_qm *m, const int16_t *xq, int64_t n, int16_t *dst, float *sums) {
+    if (!m->blocked) return 0;
+    for (int64_t blk = 0; blk < n / 256; blk++) {
+        for (int lane = 0; lane < 16; lane++) sums[blk * 16 + lane] = 0.0f;
+        for (int64_t w = 0; w < 256; w++) {
+            int64_t col = blk * 256 + w, e = w % 32, p = e / 2;
+            int64_t lane = w / 32 + 8 * (p / 8);
+            int16_t v = xq[col];
+            dst[blk * 256 + (p % 8) * 32 + 2 * lane + e % 2] = v;
+            sums[blk * 16 + lane] += (float)v;
+        }
+    }
+    return 1;
+}
+
+/* dot_row_i16 (tensor.mojo:518-577), all three branches. */
+float orc_qm_dot_row_i16(const orc_qm *m, int64_t row, const int16_t *xq, const float *xsums) {
+    const uint8_t *p = m->data + row * m->k * m->bits / 8;
+    int64_t gpr = m->k / m->group;
+    float accf[L16] = {0};
+    if (m->blocked) { /* 522-540 */
+        for (int64_t blk = 0; blk < m->k / 256; blk++) {
+            int32_t acc[L16] = {0};
+            for (int step = 0; step < 8; step++) {
+                const uint8_t *b = p + blk * 128 + step * 16;
+                int16_t u[32];
+                for (int i = 0; i < 16; i++) {
+                    u[i] = (int16_t)(b[i] & 0xf);
+                    u[16 + i] = (int16_t)(b[i] >> 4);
+                }
+                dot_pairs(acc, xq + blk * 256 + step * 32, u);
+            }
+            int64_t g0 = row * gpr + blk * 8;
+            for (int i = 0; i < L16; i++) {
+                float zp = (float)m->zp[g0 + i % 8];
+                float sc = orc_f16_to_f32(m->scale[g0 + i % 8]);
+                float xs = xsums[blk * 16 + i];
+                float t = (float)acc[i] - zp * xs;
+                accf[i] = fmaf(t, sc, accf[i]);
+            }
+        }
+        return red16(accf);
+    }
+    if (m->perch && m->bits == 8) { /* int8 per-channel, 541-566 */
+        int16_t zp = (int16_t)m->zp[row];
+        int32_t acc[L16] = {0};
+        int16_t w[32];
+        for (int64_t k = 0; k < m->k; k += 32) {
+            codes_i16(m, p, k, zp, w);
+            dot_pairs(acc, xq + k, w);
+        }
+        float s = orc_f16_to_f32(m->scale[row]);
+        for (int i = 0; i < L16; i++) accf[i] = fmaf((float)acc[i], s, 0.0f);
+        return red16(accf);
+    }
+    for (int64_t g = 0; g < gpr; g++) { /* generic, 567-577 */
+        int16_t zp = (int16_t)m->zp[row * gpr + g];
+        int32_t acc[L16] = {0};
+        int16_t w[32];
+        for (int64_t c = 0; c < m->group / 32; c++) {
+            int64_t k0 = g * m->group + 32 * c;
+            codes_i16(m, p, k0, zp, w);
+            dot_pairs(acc, xq + k0, w);
+        }
+        float s = orc_f16_to_f32(m->scale[row * gpr + g]);
+        for (int i = 0; i < L16; i++) accf[i] = fmaf((float)acc[i], s, accf[i]);
+    }
+    return red16(accf);
+}
+
+/* unpack_row_i16 (tensor.mojo:579-615) */
+void orc_qm_unpack_row_i16(const orc_qm *m, int64_t row, int16_t *dst, float *scales) {
+    const uint8_t *p = m->data + row * m->k * m->bits / 8;
+    int64_t gpr = m->k / m->group;
+    for (int64_t g = 0; g < gpr; g++) scales[g] = orc_f16_to_f32(m->scale[row * gpr + g]);
+    if (m->blocked) {
+        for (int64_t blk = 0; blk < m->k / 256; blk++) {
+            const uint8_t *zp8 = m->zp + row * gpr + blk * 8;
+            for (int step = 0; step < 8; step++) {
+                const uint8_t *b = p + blk * 128 + step * 16;
+                int16_t u[32];
+                for (int i = 0; i < 16; i++) {
+                    u[i] = (int16_t)(b[i] & 0xf);
+                    u[16 + i] = (int16_t)(b[i] >> 4);
+                }
+                for (int L = 0; L < 16; L++) {
+                    int16_t z = (int16_t)zp8[L % 8];
+                    int64_t at = blk * 128 + (L % 8) * 16 + (L / 8) * 8 + step;
+                    dst[2 * at] = (int16_t)(u[2 * L] - z);
+                    dst[2 * at + 1] = (int16_t)(u[2 * L + 1] - z);
+                }
+            }
+        }
+        return;
+    }
+    for (int64_t g = 0; g < gpr; g++) {
+        int16_t zp = (int16_t)m->zp[row * gpr + g];
+        for (int64_t c = 0; c < m->group / 32; c++) {
+            int64_t k0 = g * m->group + 32 * c;
+            codes_i16(m, p, k0, zp, dst + k0);
+        }
+    }
+}
+
+/* Exact per-group integer sums G[o, g] = sum_{k in g} xq_k * (u_{o,k} - zp_{o,g})
+ * (the invariant the integer kernels compute; tensor.mojo:262-275). */
+void orc_qm_group_sums(const orc_qm *m, const int16_t *xq, int64_t *G) {
+    int64_t gpr = m->k / m->group;
+    for (int64_t o = 0; o < m->n; o++)
+        for (int64_t g = 0; g < gpr; g++) {
+            int64_t s = 0;
+            int zp = m->zp[o * gpr + g];
+            for (int64_t j = 0; j < m->group; j++) {
+                int64_t k = g * m->group + j;
+                s += (int64_t)xq[k] * (get_code(m, o, k) - zp);
+            }
+            G[o * gpr + g] = s;
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Activations and the integer matmul driver (kernels.mojo:400-652)          */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_rows (kernels.mojo:400-416) */
+void orc_quantize_rows(const float *x, int64_t T, int64_t IN, int16_t *xq, float *sx) {
+    for (int64_t t = 0; t < T; t++) {
+        const float *row = x + t * IN;
+        float mx = 0.0f;
+        for (int64_t i = 0; i < IN; i++) {
+            float a = fabsf(row[i]);
+            mx = a > mx ? a : mx;
+        }
+        float s = mx / 32767.0f;
+        if (s == 0.0f) s = 1.0f;
+        sx[t] = s;
+        float inv = 1.0f / s;
+        for (int64_t i = 0; i < IN; i++) xq[t * IN + i] = (int16_t)orc_to_int(orc_round(row[i] * inv));
+    }
+}
+
+/* dot1_i16 (kernels.mojo:617-628): rows_i16 and head_i16's per-row dot. */
+static float dot1_i16(const int16_t *wq, const float *ws, const int16_t *xq, int64_t IN, int64_t G) {
+    float accf[L16] = {0};
+    for (int64_t g = 0; g < IN / G; g++) {
+        int32_t acc[L16] = {0};
+        for (int64_t k = g * G; k < (g + 1) * G; k += 32) dot_pairs(acc, xq + k, wq + k);
+        for (int i = 0; i < L16; i++) accf[i] = fmaf((float)acc[i], ws[g], accf[i]);
+    }
+    return red16(accf);
+}
+
+static int g_threads = 1;
+void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int orc_get_threads(void) { return g_threads; }
+
+/* tile_i16 (kernels.mojo:512-573) for TM tokens at t0 and the TN = 32 rows at
+ * o0 held in wt (VNNI pair layout) and st ([group][row]). */
+static void tile_i16(int TM, float *out, const int16_t *xq, const float *sx, const int16_t *wt, const float *st,
+                     const float *b, int64_t t0, int64_t o0, int64_t IN, int64_t OUT, int64_t G, int flags) {
+    const int TN = 32, SEG = 256;
+    float accf[4][32];
+    memset(accf, 0, sizeof(accf));
+    int64_t seg = G < SEG ? G : SEG;
+    for (int64_t k0 = 0; k0 < IN; k0 += seg) {
+        int64_t g = k0 / G;
+        int32_t acc[4][32];
+        memset(acc, 0, sizeof(acc));
+        for (int64_t kp = k0 / 2; kp < (k0 + seg) / 2; kp++) {
+            for (int m = 0; m < TM; m++) {
+                int64_t xoff = (t0 + m) * IN + 2 * kp;
+                int16_t x0 = xq[xoff], x1 = xq[xoff + 1];
+                for (int j = 0; j < TN; j++) {
+                    int16_t w0 = wt[(kp * TN + j) * 2], w1 = wt[(kp * TN + j) * 2 + 1];
+                    int64_t s = (int64_t)x0 * w0 + (int64_t)x1 * w1;
+                    acc[m][j] = (int32_t)(uint32_t)((uint32_t)acc[m][j] + (uint32_t)(int32_t)s);
+                }
+            }
+        }
+        for (int m = 0; m < TM; m++)
+            for (int j = 0; j < TN; j++) accf[m][j] = fmaf((float)acc[m][j], st[g * TN + j], accf[m][j]);
+    }
+    for (int m = 0; m < TM; m++) {
+        float sxm = sx[t0 + m];
+        for (int j = 0; j < TN; j++) {
+            float r = accf[m][j] * sxm;
+            if (flags & EPI_BIAS) r += b[o0 + j];
+            finish(out, (t0 + m) * OUT + o0 + j, r, flags);
+        }
+    }
+}
+
+/* matmul_rows_a16 (kernels.mojo:419-509): out[T, OUT] (+)= act(x @ w^T + b).
+ * flags: EPI_BIAS | EPI_GELU | EPI_RESID.  Rows (T == 1) or 32-row tiles
+ * (T > 1) are split across g_threads threads; the arithmetic per output does
+ * not depend on the split. */
+void orc_matmul_rows_a16(float *out, const float *x, const orc_qm *w, const float *b, int64_t T, int64_t IN,
+                         int64_t OUT, int flags) {
+    int16_t *xq = (int16_t *)malloc(sizeof(int16_t) * (size_t)(T * IN));
+    float *sx = (float *)malloc(sizeof(float) * (size_t)T);
+    orc_quantize_rows(x, T, IN, xq, sx);
+    if (T == 1) {
+        int16_t *xp = (int16_t *)malloc(sizeof(int16_t) * (size_t)IN);
+        float *xs = (float *)malloc(sizeof(float) * (size_t)(IN / 16 + 1));
+        const int16_t *x1 = orc_qm_permute_x_i16(w, xq, IN, xp, xs) ? xp : xq;
+        float s = sx[0];
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+        for (int64_t o = 0; o < OUT; o++) {
+            float r = orc_qm_dot_row_i16(w, o, x1, xs) * s;
+            if (flags & EPI_BIAS) r += b[o];
+            finish(out, o, r, flags);
+        }
+        free(xp);
+        free(xs);
+    } else {
+        int64_t G = w->group;
+        const int TN = 32;
+        int64_t full = OUT / TN;
+        int64_t ntasks = full + (OUT % TN != 0);
+#pragma omp parallel for schedule(dynamic) num_threads(g_threads) if (g_threads > 1)
+        for (int64_t ti = 0; ti < ntasks; ti++) {
+            int16_t *row = (int16_t *)malloc(sizeof(int16_t) * (size_t)IN);
+            float *rs = (float *)malloc(sizeof(float) * (size_t)(IN / G));
+            if (ti == full) { /* rows_i16 (kernels.mojo:576-614) */
+                for (int64_t o = full * TN; o < OUT; o++) {
+                    orc_qm_unpack_row_i16(w, o, row, rs);
+                    float bias = (flags & EPI_BIAS) ? b[o] : 0.0f;
+                    for (int64_t t = 0; t < T; t++) {
+                        float d = dot1_i16(row, rs, xq + t * IN, IN, G);
+                        finish(out, t * OUT + o, d * sx[t] + bias, flags);
+                    }
+                }
+            } else {
+                int64_t o0 = ti * TN;
+                int16_t *wt = (int16_t *)malloc(sizeof(int16_t) * (size_t)(IN * TN));
+                float *st = (float *)malloc(sizeof(float) * (size_t)(IN / G * TN));
+                for (int j = 0; j < TN; j++) {
+                    orc_qm_unpack_row_i16(w, o0 + j, row, rs);
+                    for (int64_t k = 0; k < IN; k++) wt[((k / 2) * TN + j) * 2 + k % 2] = row[k];
+                    for (int64_t g = 0; g < IN / G; g++) st[g * TN + j] = rs[g];
+                }
+                int64_t t = 0;
+                for (; t + 4 <= T; t += 4) tile_i16(4, out, xq, sx, wt, st, b, t, o0, IN, OUT, G, flags);
+                for (; t < T; t++) tile_i16(1, out, xq, sx, wt, st, b, t, o0, IN, OUT, G, flags);
+                free(wt);
+                free(st);
+            }
+            free(row);
+            free(rs);
+        }
+    }
+    free(xq);
+    free(sx);
+}
+
+/* ------------------------------------------------------------------------ */
+/* GGUF block formats (gguf.mojo:41-511)                                     */
+/* ------------------------------------------------------------------------ */
+
+enum { GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_0 = 2, GGML_Q4_1 = 3, GGML_Q8_0 = 8, GGML_Q4_K = 12, GGML_Q5_K = 13, GGML_Q6_K = 14 };
+
+int orc_gguf_block_size(int t) { /* gguf.mojo:72-78 */
+    if (t == GGML_F32 || t == GGML_F16) return 1;
+    if (t == GGML_Q4_0 || t == GGML_Q4_1 || t == GGML_Q8_0) return 32;
+    return 256;
+}
+int orc_gguf_block_bytes(int t) { /* gguf.mojo:81-98 */
+    switch (t) {
+    case GGML_F32: return 4;
+    case GGML_F16: return 2;
+    case GGML_Q4_0: return 18;
+    case GGML_Q4_1: return 20;
+    case GGML_Q8_0: return 34;
+    case GGML_Q4_K: return 144;
+    case GGML_Q5_K: return 176;
+    case GGML_Q6_K: return 210;
+    default: return 0;
+    }
+}
+static inline float f16_at(const uint8_t *p, int i) { return orc_f16_to_f32((uint16_t)(p[i] | (p[i + 1] << 8))); }
+
+/* put (gguf.mojo:166-175): store 16 values, or fma them into the lanes. */
+static inline void put(int dot, float *dst, const float *x, float *acc, int off, const float *v) {
+    if (dot)
+        for (int i = 0; i < L16; i++) acc[i] = fmaf(v[i], x[off + i], acc[i]);
+    else
+        for (int i = 0; i < L16; i++) dst[off + i] = v[i];
+}
+
+/* k_scale_min (gguf.mojo:205-221) */
+static inline void k_scale_min(const uint8_t *q, int j, int *sc, int *mn) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+        return;
+    }
+    *sc = (q[j + 4] & 0xf) | ((q[j - 4] >> 6) << 4);
+    *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+}
+void orc_k_scale_min(const uint8_t *q, int j, int *sc, int *mn) { k_scale_min(q, j, sc, mn); }
+
+/* One block at b: dequantize into dst, or fma with x into acc
+ * (dequant_q4_0 ... dequant_q6_k, gguf.mojo:178-297). */
+static void gguf_block(int t, int dot, const uint8_t *b, float *dst, const float *x, float *acc) {
+    float v[L16];
+    if (t == GGML_Q4_0) { /* 178-184 */
+        float d = f16_at(b, 0);
+        const uint8_t *q = b + 2;
+        for (int i = 0; i < 16; i++) v[i] = ((float)(q[i] & 0xf) - 8.0f) * d;
+        put(dot, dst, x, acc, 0, v);
+        for (int i = 0; i < 16; i++) v[i] = ((float)(q[i] >> 4) - 8.0f) * d;
+        put(dot, dst, x, acc, 16, v);
+    } else if (t == GGML_Q4_1) { /* 187-193 */
+        float d = f16_at(b, 0), mm = f16_at(b, 2);
+        const uint8_t *q = b + 4;
+        for (int i = 0; i < 16; i++) v[i] = d * (float)(q[i] & 0xf) + mm;
+        put(dot, dst, x, acc, 0, v);
+        for (int i = 0; i < 16; i++) v[i] = d * (float)(q[i] >> 4) + mm;
+        put(dot, dst, x, acc, 16, v);
+    } else if (t == GGML_Q8_0) { /* 196-202 */
+        float d = f16_at(b, 0);
+        for (int h = 0; h < 2; h++) {
+            for (int i = 0; i < 16; i++) v[i] = d * (float)(int8_t)b[2 + 16 * h + i];
+            put(dot, dst, x, acc, 16 * h, v);
+        }
+    } else if (t == GGML_Q4_K || t == GGML_Q5_K) { /* 224-268 */
+        float d = f16_at(b, 0), dmin = f16_at(b, 2);
+        const uint8_t *scales = b + 4;
+        int five = t == GGML_Q5_K;
+        for (int j = 0; j < 4; j++) {
+            int sc1, m1i, sc2, m2i;
+            k_scale_min(scales, 2 * j, &sc1, &m1i);
+            k_scale_min(scales, 2 * j + 1, &sc2, &m2i);
+            float d1 = d * (float)sc1, m1 = dmin * (float)m1i;
+            float d2 = d * (float)sc2, m2 = dmin * (float)m2i;
+            for (int h = 0; h < 2; h++) {
+                const uint8_t *q = five ? b + 48 + 32 * j + 16 * h : b + 16 + 32 * j + 16 * h;
+                const uint8_t *qh = b + 16 + 16 * h;
+                for (int i = 0; i < 16; i++) {
+                    int lo = q[i] & 0xf;
+                    if (five) lo |= ((qh[i] >> (2 * j)) & 1) << 4;
+                    v[i] = d1 * (float)lo - m1;
+                }
+                put(dot, dst, x, acc, 64 * j + 16 * h, v);
+                for (int i = 0; i < 16; i++) {
+                    int hi = q[i] >> 4;
+                    if (five) hi |= ((qh[i] >> (2 * j + 1)) & 1) << 4;
+                    v[i] = d2 * (float)hi - m2;
+                }
+                put(dot, dst, x, acc, 64 * j + 32 + 16 * h, v);
+            }
+        }
+    } else if (t == GGML_Q6_K) { /* 271-297 */
+        float d = f16_at(b, 208);
+        for (int n = 0; n < 2; n++) {
+            int ql = 64 * n, qhoff = 128 + 32 * n, sc = 192 + 8 * n;
+            for (int h = 0; h < 2; h++) {
+                const uint8_t *lo0 = b + ql + 16 * h, *lo1 = b + ql + 32 + 16 * h, *hi = b + qhoff + 16 * h;
+                int base = 128 * n + 16 * h;
+                for (int k = 0; k < 4; k++) {
+                    float s = (float)(int8_t)b[sc + h + 2 * k];
+                    float ds = d * s;
+                    for (int i = 0; i < 16; i++) {
+                        int q;
+                        if (k == 0) q = (lo0[i] & 0xf) | ((hi[i] & 3) << 4);
+                        else if (k == 1) q = (lo1[i] & 0xf) | (((hi[i] >> 2) & 3) << 4);
+                        else if (k == 2) q = (lo0[i] >> 4) | (((hi[i] >> 4) & 3) << 4);
+                        else q = (lo1[i] >> 4) | (((hi[i] >> 6) & 3) << 4);
+                        v[i] = ds * ((float)q - 32.0f);
+                    }
+                    put(dot, dst, x, acc, base + 32 * k, v);
+                }
+            }
+        }
+    }
+}
+
+/* GGUFMatrix.each_block / blocks (gguf.mojo:388-434) */
+static float gguf_row(int t, const uint8_t *p, int64_t cols, float *dst, const float *x, int dot) {
+    float acc[L16] = {0};
+    if (t == GGML_F32 || t == GGML_F16) {
+        float v[L16];
+        for (int64_t i = 0; i < cols; i += 16) {
+            for (int l = 0; l < 16; l++) {
+                if (t == GGML_F32) {
+                    float f;
+                    memcpy(&f, p + 4 * (i + l), 4);
+                    v[l] = f;
+                } else {
+                    v[l] = f16_at(p, (int)(2 * (i + l)));
+                }
+            }
+            put(dot, dst ? dst + i : NULL, x ? x + i : NULL, acc, 0, v);
+        }
+        return red16(acc);
+    }
+    int bs = orc_gguf_block_size(t), bb = orc_gguf_block_bytes(t);
+    for (int64_t blk = 0; blk < cols / bs; blk++)
+        gguf_block(t, dot, p + blk * bb, dst ? dst + blk * bs : NULL, x ? x + blk * bs : NULL, acc);
+    return red16(acc);
+}
+void orc_gguf_dequant_row(int t, const uint8_t *row, int64_t cols, float *dst) { (void)gguf_row(t, row, cols, dst, NULL, 0); }
+float orc_gguf_dot_row(int t, const uint8_t *row, int64_t cols, const float *x) { return gguf_row(t, row, cols, NULL, x, 1); }
+
+/* q6_k_i16 (gguf.mojo:322-336): weights 128n + 32k .. +31 as (q - 32) * scale. */
+static void q6_k_i16(const uint8_t *b, int n, int k, int16_t *out) {
+    const uint8_t *L = b + 64 * n + (k % 2 ? 32 : 0), *H = b + 128 + 32 * n;
+    for (int j = 0; j < 32; j++) {
+        int lo = k >= 2 ? (L[j] >> 4) : (L[j] & 0xf);
+        int q = lo | (((H[j] >> (2 * k)) & 3) << 4);
+        int s = (int8_t)b[192 + 8 * n + 2 * k + (j < 16 ? 0 : 1)];
+        out[j] = (int16_t)((q - 32) * s);
+    }
+}
+
+int orc_gguf_has_i16(int t) { return t == GGML_Q6_K || t == GGML_Q8_0; } /* gguf.mojo:456-457 */
+int orc_gguf_group_size(int t) { return t == GGML_Q6_K ? 256 : 32; }  /* 459-460 */
+
+/* GGUFMatrix.dot_row_i16 (gguf.mojo:462-487) */
+float orc_gguf_dot_row_i16(int t, const uint8_t *p, int64_t cols, const int16_t *xq) {
+    float accf[L16] = {0};
+    if (t == GGML_Q8_0) {
+        for (int64_t blk = 0; blk < cols / 32; blk++) {
+            const uint8_t *b = p + blk * 34;
+            int16_t w[32];
+            for (int j = 0; j < 32; j++) w[j] = (int16_t)(int8_t)b[2 + j];
+            int32_t acc[L16] = {0};
+            dot_pairs(acc, xq + blk * 32, w);
+            float d = f16_at(b, 0);
+            for (int i = 0; i < L16; i++) accf[i] = fmaf((float)acc[i], d, accf[i]);
+        }
+        return red16(accf);
+    }
+    for (int64_t sb = 0; sb < cols / 256; sb++) {
+        const uint8_t *b = p + sb * 210;
+        int32_t acc[L16] = {0};
+        int16_t w[32];
+        for (int n = 0; n < 2; n++)
+            for (int k = 0; k < 4; k++) {
+                q6_k_i16(b, n, k, w);
+                dot_pairs(acc, xq + sb * 256 + 128 * n + 32 * k, w);
+            }
+        float d = f16_at(b, 208);
+        for (int i = 0; i < L16; i++) accf[i] = fmaf((float)acc[i], d, accf[i]);
+    }
+    return red16(accf);
+}
+
+/* GGUFMatrix.unpack_row_i16 (gguf.mojo:489-505) */
+void orc_gguf_unpack_row_i16(int t, const uint8_t *p, int64_t cols, int16_t *dst, float *scales) {
+    if (t == GGML_Q8_0) {
+        for (int64_t blk = 0; blk < cols / 32; blk++) {
+            const uint8_t *b = p + blk * 34;
+            for (int j = 0; j < 32; j++) dst[blk * 32 + j] = (int16_t)(int8_t)b[2 + j];
+            scales[blk] = f16_at(b, 0);
+        }
+        return;
+    }
+    for (int64_t sb = 0; sb < cols / 256; sb++) {
+        const uint8_t *b = p + sb * 210;
+        for (int n = 0; n < 2; n++)
+            for (int k = 0; k < 4; k++) q6_k_i16(b, n, k, dst + sb * 256 + 128 * n + 32 * k);
+        scales[sb] = f16_at(b, 208);
+    }
+}
+
+/* matmul_rows T == 1 (kernels.mojo:301-312) / linear_team OUT_MAJOR branch
+ * (817-826): the GGUF decode GEMV, out[o] (+)= act(dot_row(o, x) + b[o]). */
+void orc_gguf_gemv(int t, const uint8_t *w, int64_t rows, int64_t cols, const float *x, const float *b, float *out,
+                   int flags) {
+    int64_t rb = cols / orc_gguf_block_size(t) * orc_gguf_block_bytes(t);
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int64_t o = 0; o < rows; o++) {
+        float r = orc_gguf_dot_row(t, w + o * rb, cols, x);
+        if (flags & EPI_BIAS) r += b[o];
+        finish(out, o, r, flags);
+    }
+}
+
+/* head_i16 (kernels.mojo:693-736) for Q6_K / Q8_0: logits[T, V]. */
+void orc_gguf_head_i16(int t, const uint8_t *w, int64_t V, int64_t C, const float *h, int64_t T, float *logits) {
+    int16_t *xq = (int16_t *)malloc(sizeof(int16_t) * (size_t)(T * C));
+    float *sx = (float *)malloc(sizeof(float) * (size_t)T);
+    orc_quantize_rows(h, T, C, xq, sx);
+    int64_t G = orc_gguf_group_size(t);
+    int64_t rb = C / orc_gguf_block_size(t) * orc_gguf_block_bytes(t);
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int64_t v = 0; v < V; v++) {
+        if (T == 1) {
+            logits[v] = orc_gguf_dot_row_i16(t, w + v * rb, C, xq) * sx[0];
+            continue;
+        }
+        int16_t *row = (int16_t *)malloc(sizeof(int16_t) * (size_t)C);
+        float *rs = (float *)malloc(sizeof(float) * (size_t)(C / G));
+        orc_gguf_unpack_row_i16(t, w + v * rb, C, row, rs);
+        for (int64_t tt = 0; tt < T; tt++) logits[tt * V + v] = dot1_i16(row, rs, xq + tt * C, C, G) * sx[tt];
+        free(row);
+        free(rs);
+    }
+    free(xq);
+    free(sx);
+}
+
+/* ------------------------------------------------------------------------ */
+/* LayerNorm and the int8 KV cache (kernels.mojo:179-210; kvcache.mojo)     */
+/* ------------------------------------------------------------------------ */
+
+/* layernorm (kernels.mojo:179-197), 16-lane partial sums. */
+void orc_layernorm(float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C) {
+    for (int64_t t = 0; t < T; t++) {
+        const float *xr = x + t * C;
+        float *o = out + t * C;
+        float s[L16] = {0}, sq[L16] = {0};
+        for (int64_t i = 0; i < C; i += 16)
+            for (int l = 0; l < 16; l++) s[l] += xr[i + l];
+        float mean = red16(s) / (float)C;
+        for (int64_t i = 0; i < C; i += 16)
+            for (int l = 0; l < 16; l++) {
+                float d = xr[i + l] - mean;
+                sq[l] += d * d;
+            }
+        float rstd = 1.0f / sqrtf(red16(sq) / (float)C + 1e-5f);
+        for (int64_t i = 0; i < C; i++) {
+            float n = (xr[i] - mean) * rstd;
+            o[i] = n * w[i] + b[i];
+        }
+    }
+}
+
+typedef struct {
+    int32_t n_layer, max_t, n_head, head_dim;
+    int8_t *k, *v;  /* [layer, pos, head, head_dim] */
+    float *ks, *vs; /* [layer, pos, head] */
+} orc_kv;
+
+/* QuantKV.quantize (kvcache.mojo:320-331) with QMAX = 127. */
+static float kv_quantize(const float *x, int n, int8_t *dst) {
+    float mx = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float a = fabsf(x[i]);
+        mx = a > mx ? a : mx;
+    }
+    float s = mx / 127.0f;
+    if (s == 0.0f) s = 1.0f;
+    float inv = 1.0f / s;
+    for (int i = 0; i < n; i++) dst[i] = (int8_t)orc_to_int(orc_round(x[i] * inv));
+    return s;
+}
+
+/* QuantKV.store (kvcache.mojo:333-342) */
+void orc_kv_store(orc_kv *kv, int layer, int pos, const float *k, const float *v) {
+    for (int h = 0; h < kv->n_head; h++) {
+        int64_t sl = ((int64_t)layer * kv->max_t + pos) * kv->n_head + h;
+        int o = h * kv->head_dim;
+        kv->ks[sl] = kv_quantize(k + o, kv->head_dim, kv->k + sl * kv->head_dim);
+        kv->vs[sl] = kv_quantize(v + o, kv->head_dim, kv->v + sl * kv->head_dim);
+    }
+}
+
+/* attend_float_one (kvcache.mojo:113-150) through QuantKV.score / add_value
+ * (344-370): token t (position pos0 + t), head h, of `layer`; q from qkv row
+ * t ([T, 3C]), output into row t of out ([T, C]).  HS must be a multiple of
+ * 16. */
+void orc_kv_attend_one(const orc_kv *kv, float *out, const float *qkv, int layer, int t, int h, int pos0) {
+    int HS = kv->head_dim, C = kv->n_head * HS;
+    float scale = 1.0f / sqrtf((float)HS);
+    int npos = pos0 + t + 1;
+    const float *q = qkv + (int64_t)t * 3 * C + h * HS;
+    float *scores = (float *)malloc(sizeof(float) * (size_t)npos);
+    float mx = -INFINITY;
+    for (int s = 0; s < npos; s++) {
+        int64_t sl = ((int64_t)layer * kv->max_t + s) * kv->n_head + h;
+        const int8_t *kp = kv->k + sl * HS;
+        float d[L16] = {0};
+        for (int i = 0; i < HS; i += 16)
+            for (int l = 0; l < 16; l++) d[l] += q[i + l] * (float)kp[i + l];
+        float sc = red16(d) * kv->ks[sl] * scale;
+        scores[s] = sc;
+        mx = sc > mx ? sc : mx;
+    }
+    for (int s = 0; s < npos; s++) scores[s] = expf(scores[s] - mx);
+    float total = 0.0f;
+    for (int s = 0; s < npos; s++) total += scores[s];
+    float *o = out + (int64_t)t * C + h * HS;
+    float *acc = (float *)calloc((size_t)HS, sizeof(float));
+    for (int s = 0; s < npos; s++) {
+        float p = scores[s] / total;
+        int64_t sl = ((int64_t)layer * kv->max_t + s) * kv->n_head + h;
+        const int8_t *vp = kv->v + sl * HS;
+        float ps = p * kv->vs[sl];
+        for (int i = 0; i < HS; i++) acc[i] = fmaf(ps, (float)vp[i], acc[i]);
+    }
+    for (int i = 0; i < HS; i++) o[i] = acc[i];
+    free(acc);
+    free(scores);
+}
+
+/* KVCache.attend (kvcache.mojo:62-79): every token and head. */
+void orc_kv_attend(const orc_kv *kv, float *out, const float *qkv, int layer, int T, int pos0) {
+#pragma omp parallel for schedule(dynamic) num_threads(g_threads) if (g_threads > 1 && T * (pos0 + T) >= 256)
+    for (int idx = 0; idx < kv->n_head * T; idx++) orc_kv_attend_one(kv, out, qkv, layer, idx / kv->n_head, idx % kv->n_head, pos0);
+}
+
+/* ------------------------------------------------------------------------ */
+/* GPT-2 (gpt2t.mojo:74-118, 198-609, 777-797)                              */
+/* ------------------------------------------------------------------------ */
+
+#define G_NL 12
+#define G_NH 12
+#define G_C 768
+#define G_HS 64
+#define G_MAXT 1024
+#define G_V 50257
+
+/* Rng (gpt2t.mojo:777-789): xorshift64*. */
+typedef struct {
+    uint64_t state;
+} orc_rng;
+void orc_rng_init(orc_rng *r, int64_t seed) { r->state = (uint64_t)seed * 0x9E3779B97F4A7C15ull + 1; }
+float orc_rng_uniform(orc_rng *r) {
+    r->state ^= r->state >> 12;
+    r->state ^= r->state << 25;
+    r->state ^= r->state >> 27;
+    uint64_t x = (r->state * 0x2545F4914F6CDD1Dull) >> 40;
+    return (float)x / (float)(1 << 24);
+}
+
+/* argmax (gpt2t.mojo:792-797): the first maximum wins (strict >). */
+int64_t orc_argmax(const float *logits, int64_t V) {
+    int64_t best = 0;
+    for (int64_t v = 1; v < V; v++)
+        if (logits[v] > logits[best]) best = v;
+    return best;
+}
+
+/* Per-layer float32 vectors, in gpt2t.mojo's VEC_NAMES order (108-118). */
+enum { LN1_W, LN1_B, QKV_B, PROJ_B, LN2_W, LN2_B, FC_B, FCPROJ_B, N_VECS };
+
+typedef struct {
+    orc_qm wte;              /* E: [V, C] int8 per-channel A16 (the tied embedding and head) */
+    orc_qm mats[G_NL * 4];   /* W: qkv, proj, fc, fcproj per layer ([OUT, IN]) */
+    float *vecs[G_NL * N_VECS];
+    float *wpe, *lnf_w, *lnf_b;
+    orc_kv kv;
+    float *x, *xn, *qkv, *att, *fc, *logits;
+} orc_gpt2;
+
+static void qm_alloc(orc_qm *m, int bits, int group, int sym, int a16, int64_t n, int64_t k) {
+    m->bits = bits;
+    m->sym = sym;
+    m->a16 = a16;
+    m->group = group;
+    int64_t g = group == 0 ? k : group;
+    m->data = (uint8_t *)malloc((size_t)(n * k * bits / 8));
+    m->scale = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(n * k / g));
+    m->zp = (uint8_t *)malloc((size_t)(n * k / g));
+}
+static void qm_free(orc_qm *m) {
+    free(m->data);
+    free(m->scale);
+    free(m->zp);
+}
+
+/* load_model (gpt2t.mojo:579-609) from float32 tensors in Hugging Face
+ * layout.  params: wte [V, C], wpe [MAX_T, C], ln_f.weight, ln_f.bias, then
+ * per layer the 12 tensors ln_1.weight, ln_1.bias, attn.c_attn.weight
+ * [C, 3C], attn.c_attn.bias, attn.c_proj.weight [C, C], attn.c_proj.bias,
+ * ln_2.weight, ln_2.bias, mlp.c_fc.weight [C, 4C], mlp.c_fc.bias,
+ * mlp.c_proj.weight [4C, C], mlp.c_proj.bias.  Layers in QuantMatrix[bits,
+ * group, sym, A16=True], the head in E = QuantMatrix[8, 0, False, True]
+ * (HEAD8_A16, gpt2t.mojo:1234), the cache QuantKV[8]. */
+orc_gpt2 *orc_gpt2_new(const float *const *params, int bits, int group, int sym) {
+    orc_gpt2 *m = (orc_gpt2 *)calloc(1, sizeof(orc_gpt2));
+    qm_alloc(&m->wte, 8, 0, 0, 1, G_V, G_C);
+    orc_qm_from_f32(&m->wte, params[0], G_V, G_C, 0);
+    static const int64_t rows[4] = {G_C, G_C, G_C, 4 * G_C}, cols[4] = {3 * G_C, G_C, 4 * G_C, G_C};
+    static const int mat_idx[4] = {2, 4, 8, 10};
+    static const int vec_idx[N_VECS] = {0, 1, 3, 5, 6, 7, 9, 11};
+    static const int64_t vec_len[N_VECS] = {G_C, G_C, 3 * G_C, G_C, G_C, G_C, 4 * G_C, G_C};
+    for (int l = 0; l < G_NL; l++) {
+        const float *const *lp = params + 4 + 12 * l;
+        for (int j = 0; j < 4; j++) {
+            orc_qm *q = &m->mats[l * 4 + j];
+            qm_alloc(q, bits, group, sym, 1, cols[j], rows[j]);
+            orc_qm_from_f32(q, lp[mat_idx[j]], rows[j], cols[j], 1);
+        }
+        for (int s = 0; s < N_VECS; s++) {
+            m->vecs[l * N_VECS + s] = (float *)malloc(sizeof(float) * (size_t)vec_len[s]);
+            memcpy(m->vecs[l * N_VECS + s], lp[vec_idx[s]], sizeof(float) * (size_t)vec_len[s]);
+        }
+    }
+    m->wpe = (float *)malloc(sizeof(float) * G_MAXT * G_C);
+    memcpy(m->wpe, params[1], sizeof(float) * G_MAXT * G_C);
+    m->lnf_w = (float *)malloc(sizeof(float) * G_C);
+    m->lnf_b = (float *)malloc(sizeof(float) * G_C);
+    memcpy(m->lnf_w, params[2], sizeof(float) * G_C);
+    memcpy(m->lnf_b, params[3], sizeof(float) * G_C);
+    m->kv.n_layer = G_NL;
+    m->kv.max_t = G_MAXT;
+    m->kv.n_head = G_NH;
+    m->kv.head_dim = G_HS;
+    size_t nkv = (size_t)G_NL * G_MAXT * G_C, ns = (size_t)G_NL * G_MAXT * G_NH;
+    m->kv.k = (int8_t *)calloc(nkv, 1);
+    m->kv.v = (int8_t *)calloc(nkv, 1);
+    m->kv.ks = (float *)calloc(ns, sizeof(float));
+    m->kv.vs = (float *)calloc(ns, sizeof(float));
+    m->x = (float *)malloc(sizeof(float) * G_MAXT * G_C);
+    m->xn = (float *)malloc(sizeof(float) * G_MAXT * G_C);
+    m->qkv = (float *)malloc(sizeof(float) * G_MAXT * 3 * G_C);
+    m->att = (float *)malloc(sizeof(float) * G_MAXT * G_C);
+    m->fc = (float *)malloc(sizeof(float) * G_MAXT * 4 * G_C);
+    m->logits = (float *)malloc(sizeof(float) * G_V);
+    return m;
+}
+
+void orc_gpt2_free(orc_gpt2 *m) {
+    if (!m) return;
+    qm_free(&m->wte);
+    for (int i = 0; i < G_NL * 4; i++) qm_free(&m->mats[i]);
+    for (int i = 0; i < G_NL * N_VECS; i++) free(m->vecs[i]);
+    free(m->wpe);
+    free(m->lnf_w);
+    free(m->lnf_b);
+    free(m->kv.k);
+    free(m->kv.v);
+    free(m->kv.ks);
+    free(m->kv.vs);
+    free(m->x);
+    free(m->xn);
+    free(m->qkv);
+    free(m->att);
+    free(m->fc);
+    free(m->logits);
+    free(m);
+}
+
+const orc_qm *orc_gpt2_mat(const orc_gpt2 *m, int i) { return i < 0 ? &m->wte : &m->mats[i]; }
+const orc_kv *orc_gpt2_kv(const orc_gpt2 *m) { return &m->kv; }
+float *orc_gpt2_act(orc_gpt2 *m, int which) {
+    switch (which) {
+    case 0: return m->x;
+    case 1: return m->xn;
+    case 2: return m->qkv;
+    case 3: return m->att;
+    case 4: return m->fc;
+    default: return m->logits;
+    }
+}
+
+/* Model.blocks (gpt2t.mojo:485-571): embed tokens at pos0.., all layers. */
+static void gpt2_blocks(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
+    const int C = G_C;
+    for (int t = 0; t < T; t++) { /* 495-502 */
+        float *xt = m->x + (int64_t)t * C;
+        orc_qm_dequant_row(&m->wte, tokens[t], xt);
+        const float *p = m->wpe + (int64_t)(pos0 + t) * C;
+        for (int i = 0; i < C; i++) xt[i] = xt[i] + p[i];
+    }
+    for (int l = 0; l < G_NL; l++) {
+        orc_qm *w = &m->mats[l * 4];
+        float **v = &m->vecs[l * N_VECS];
+        orc_layernorm(m->xn, m->x, v[LN1_W], v[LN1_B], T, C);
+        orc_matmul_rows_a16(m->qkv, m->xn, &w[0], v[QKV_B], T, C, 3 * C, EPI_BIAS);
+        for (int t = 0; t < T; t++) {
+            const float *row = m->qkv + (int64_t)t * 3 * C;
+            orc_kv_store(&m->kv, l, pos0 + t, row + C, row + 2 * C);
+        }
+        orc_kv_attend(&m->kv, m->att, m->qkv, l, T, pos0);
+        orc_matmul_rows_a16(m->x, m->att, &w[1], v[PROJ_B], T, C, C, EPI_BIAS | EPI_RESID);
+        orc_layernorm(m->xn, m->x, v[LN2_W], v[LN2_B], T, C);
+        orc_matmul_rows_a16(m->fc, m->xn, &w[2], v[FC_B], T, C, 4 * C, EPI_BIAS | EPI_GELU);
+        orc_matmul_rows_a16(m->x, m->fc, &w[3], v[FCPROJ_B], T, 4 * C, C, EPI_BIAS | EPI_RESID);
+    }
+}
+
+/* Model.forward (gpt2t.mojo:329-342) and Model.decode (350-447): runs the
+ * tokens at positions pos0.. and returns the last token's logits.  decode's
+ * team arithmetic equals the region-per-call kernels' (kernels.mojo:743-747),
+ * so one token goes through the same blocks() with T = 1. */
+const float *orc_gpt2_forward(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
+    gpt2_blocks(m, tokens, T, pos0);
+    const float *last = m->x + (int64_t)(T - 1) * G_C;
+    orc_layernorm(m->xn, last, m->lnf_w, m->lnf_b, 1, G_C);
+    orc_matmul_rows_a16(m->logits, m->xn, &m->wte, NULL, 1, G_C, G_V, 0);
+    return m->logits;
+}
+
+/* generate's greedy loop (gpt2t.mojo:949-981 with -t 0): prompt, then up to
+ * `steps` tokens (stopping at EOT 50256); returns the count generated.  The
+ * decode loop runs steps - 1 forwards for steps tokens. */
+int orc_gpt2_generate(orc_gpt2 *m, const int64_t *prompt, int n_prompt, int steps, int64_t *out_tokens) {
+    const float *logits = orc_gpt2_forward(m, prompt, n_prompt, 0);
+    int pos = n_prompt, generated = 0;
+    for (int i = 0; i < steps; i++) {
+        int64_t next = orc_argmax(logits, G_V);
+        if (next == 50256) break;
+        out_tokens[generated++] = next;
+        if (generated == steps) break;
+        logits = orc_gpt2_forward(m, &next, 1, pos);
+        pos++;
+    }
+    return generated;
+}

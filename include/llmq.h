@@ -1,0 +1,205 @@
+/*
+ * llmq.h -- C ABI of libllmq.so, the MI355X (gfx950) implementation of
+ * llm_mojo's quantized-weight matmul path.
+ *
+ * The reference selects weight formats through the Mojo trait WeightMatrix
+ * (tensor.mojo:49-147) and KV formats through KVCache (kvcache.mojo:31-87);
+ * its kernels (kernels.mojo) call those per output row.  A GPU format cannot
+ * be driven per row, so this library is driven per whole matmul (linear /
+ * head), per KV store / attention, or per decode step.  Each declaration
+ * below names the reference interface it stands in for.
+ *
+ * Conventions
+ *   - Every function returns LLMQ_OK (0) or a negative LLMQ_E* code; on error
+ *     llmq_last_error() describes it (thread-local).  Nothing throws across
+ *     this boundary.
+ *   - "host" pointers are CPU memory, "device" pointers are GPU memory.  All
+ *     compute entry points take device pointers and are stream-ordered on the
+ *     context's stream: they return before the GPU finishes; llmq_sync waits.
+ *   - Handles (llmq_mat, llmq_kv, llmq_gpt2) own their device memory and are
+ *     released exactly once with their *_free function (tensor.mojo:49-55).
+ *   - A context is used from one host thread at a time (the reference's
+ *     thread 0 of the decode team, kernels.mojo:802-806).
+ */
+#ifndef LLMQ_H
+#define LLMQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define LLMQ_API __attribute__((visibility("default")))
+#else
+#define LLMQ_API
+#endif
+
+enum {
+    LLMQ_OK = 0,
+    LLMQ_EINVAL = -1,      /* bad argument (the reference abort()s or raises) */
+    LLMQ_EHIP = -2,        /* a HIP runtime call failed */
+    LLMQ_ENOMEM = -3,      /* device allocation failed */
+    LLMQ_EUNSUPPORTED = -4 /* a format or shape this build does not cover */
+};
+
+/* Epilogue flags of linear: kernels.linear's RESID / GELU parameters and
+ * matmul_rows_a16's BIAS (kernels.mojo:38-48, 419-421, 655-673). */
+enum { LLMQ_BIAS = 1, LLMQ_GELU = 2, LLMQ_RESID = 4 };
+
+/* ggml tensor types accepted by llmq_mat_from_gguf (gguf.mojo:41-49). */
+enum {
+    LLMQ_GGML_F32 = 0, LLMQ_GGML_F16 = 1, LLMQ_GGML_Q4_0 = 2, LLMQ_GGML_Q4_1 = 3,
+    LLMQ_GGML_Q8_0 = 8, LLMQ_GGML_Q4_K = 12, LLMQ_GGML_Q5_K = 13, LLMQ_GGML_Q6_K = 14
+};
+
+typedef struct llmq_ctx llmq_ctx;
+typedef struct llmq_mat llmq_mat;
+typedef struct llmq_kv llmq_kv;
+typedef struct llmq_gpt2 llmq_gpt2;
+
+/* ---------------------------------------------------------------- context */
+
+/* No reference counterpart (the reference is CPU-only): one GPU, one stream. */
+LLMQ_API int llmq_init(int device, llmq_ctx **ctx);
+LLMQ_API int llmq_destroy(llmq_ctx *ctx);
+LLMQ_API const char *llmq_last_error(void);
+/* Makes the context issue its work on an existing HIP stream (e.g. a
+ * framework's current stream); NULL returns to the context's own stream. */
+LLMQ_API int llmq_set_stream(llmq_ctx *ctx, void *hip_stream);
+LLMQ_API int llmq_sync(llmq_ctx *ctx);
+/* Device memory helpers for callers without an allocator of their own. */
+LLMQ_API int llmq_malloc(llmq_ctx *ctx, size_t bytes, void **dptr);
+LLMQ_API int llmq_free(llmq_ctx *ctx, void *dptr);
+LLMQ_API int llmq_memcpy_h2d(llmq_ctx *ctx, void *dst, const void *src, size_t bytes);
+LLMQ_API int llmq_memcpy_d2h(llmq_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* ------------------------------------------------ weight matrices (formats) */
+
+/* QuantMatrix[bits, group, sym, a16].from_f32 (tensor.mojo:334-383):
+ * quantizes a row-major float32 host matrix src[rows, cols] on the GPU,
+ * bit-identical to the reference (float16 RNE scales, integer zero points,
+ * round-half-away codes).  reduce_rows as in the trait (tensor.mojo:76-85):
+ * 1 for layer matrices in Hugging Face [IN, OUT] layout (stored transposed,
+ * one output per row), 0 for wte [V, C].  bits 4 or 8; group 32, 64, 128 or
+ * 0 for per-channel.  a16 selects the int16-activation kernels (ACT16,
+ * tensor.mojo:66-69); the device layout is the same either way. */
+LLMQ_API int llmq_mat_from_f32(llmq_ctx *ctx, int bits, int group, int sym, int a16, const float *src,
+                               int64_t rows, int64_t cols, int reduce_rows, llmq_mat **out);
+/* Same, with src already in device memory. */
+LLMQ_API int llmq_mat_from_f32_device(llmq_ctx *ctx, int bits, int group, int sym, int a16, const float *src,
+                                      int64_t rows, int64_t cols, int reduce_rows, llmq_mat **out);
+/* GGUFMatrix(data, kind, rows, cols) (gguf.mojo:344-371): blocks used as
+ * stored, rows of cols // block_size blocks, copied from host memory. */
+LLMQ_API int llmq_mat_from_gguf(llmq_ctx *ctx, int ggml_type, const void *blocks, int64_t rows, int64_t cols,
+                                llmq_mat **out);
+/* WeightMatrix.free (tensor.mojo:145-147). */
+LLMQ_API int llmq_mat_free(llmq_mat *mat);
+/* WeightMatrix.nbytes (tensor.mojo:131-133; QuantMatrix 629-632,
+ * GGUFMatrix 507-508): bytes of the format as the reference counts them. */
+LLMQ_API int64_t llmq_mat_nbytes(const llmq_mat *mat);
+/* WeightMatrix.group_size (tensor.mojo:127-129, gguf.mojo:459-460). */
+LLMQ_API int64_t llmq_mat_group_size(const llmq_mat *mat);
+/* Shape: rows (outputs) and cols (the reduction axis) as stored. */
+LLMQ_API int llmq_mat_shape(const llmq_mat *mat, int64_t *rows, int64_t *cols);
+/* The codes, float16 scale bits and zero points in the reference's own
+ * QuantMatrix memory layout (tensor.mojo:302-307, nibble_at 385-404,
+ * BLOCKED for int4-g32-a16), copied to host buffers of nbytes-matching
+ * sizes: rows*cols*bits/8, rows*cols/group, rows*cols/group.  This is the
+ * layout QuantMatrix.save writes (tensor.mojo:634-643). */
+LLMQ_API int llmq_mat_export(llmq_ctx *ctx, const llmq_mat *mat, uint8_t *codes, uint16_t *scales, uint8_t *zps);
+/* WeightMatrix.dequant_row (tensor.mojo:94-96): row `row` as float32 into a
+ * host buffer of cols floats. */
+LLMQ_API int llmq_mat_dequant_row(llmq_ctx *ctx, const llmq_mat *mat, int64_t row, float *dst);
+
+/* --------------------------------------------------------- compute (device) */
+
+/* kernels.quantize_rows (kernels.mojo:400-416): xq[T, K] = round(x / sx),
+ * sx[t] = max|x[t]| / 32767 (1 for an all-zero row). */
+LLMQ_API int llmq_quantize_rows(llmq_ctx *ctx, const float *x, int64_t T, int64_t K, int16_t *xq, float *sx);
+/* kernels.linear (kernels.mojo:655-673; decode team form linear_team
+ * 774-866): out[T, OUT] (+)= act(x[T, IN] @ W^T + bias).  For an a16
+ * QuantMatrix the activations are quantized per row to int16 and the sums
+ * run in integers (matmul_rows_a16, 419-509); for a GGUF matrix the float
+ * path (matmul_rows, 285-312).  flags: LLMQ_BIAS | LLMQ_GELU | LLMQ_RESID. */
+LLMQ_API int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, const float *bias, int64_t T,
+                         int64_t IN, int64_t OUT, int flags);
+/* The same with LayerNorm (kernels.layernorm, 179-197; eps 1e-5) applied to
+ * each input row first: the LN -> linear pairs of Model.decode
+ * (gpt2t.mojo:390-399, 419-428) in one call. */
+LLMQ_API int llmq_ln_linear(llmq_ctx *ctx, float *out, const float *x, const float *ln_w, const float *ln_b,
+                            const llmq_mat *w, const float *bias, int64_t T, int64_t IN, int64_t OUT, int flags);
+/* kernels.head / head_team (kernels.mojo:676-690, 869-910): logits[T, V] =
+ * h[T, C] @ W[V, C]^T, no bias.  GGUF Q6_K / Q8_0 heads take the int16 path
+ * (head_i16, 693-736). */
+LLMQ_API int llmq_head(llmq_ctx *ctx, float *logits, const float *h, const llmq_mat *w, int64_t T, int64_t V,
+                       int64_t C);
+/* kernels.layernorm (kernels.mojo:179-197). */
+LLMQ_API int llmq_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T,
+                            int64_t C);
+/* Parity hook for the integer sums (tensor.mojo:262-275): runs the linear
+ * kernel on xf[T=1, IN] and also writes, per output row and per 16-byte code
+ * chunk of the device layout, the exact int32 partial
+ * sum_k xq_k * (u_k - zp) (chunks of 32 int4 or 16 int8 weights, in column
+ * order), plus the quantized activations xq[IN] and their scale sx[1].
+ * chunk_sums has OUT * IN / (bits == 4 ? 32 : 16) int32 entries. */
+LLMQ_API int llmq_debug_chunk_sums(llmq_ctx *ctx, const float *xf, const llmq_mat *w, float *out, int32_t *chunk_sums,
+                                   int16_t *xq, float *sx);
+
+/* ------------------------------------------------------ int8 KV cache */
+
+/* QuantKV[8].create (kvcache.mojo:297-311): int8 keys and values
+ * [layer, pos, head, head_dim] with float32 scales [layer, pos, head]. */
+LLMQ_API int llmq_kv_create(llmq_ctx *ctx, int n_layer, int max_t, int n_head, int head_dim, llmq_kv **out);
+LLMQ_API int llmq_kv_free(llmq_kv *kv);
+/* KVCache.nbytes (kvcache.mojo:377-379). */
+LLMQ_API int64_t llmq_kv_nbytes(const llmq_kv *kv);
+/* QuantKV.store for T consecutive tokens (kvcache.mojo:333-342, called per
+ * token at gpt2t.mojo:401-404, 526-530): keys and values are columns C.. and
+ * 2C.. of each row of qkv[T, 3C]. */
+LLMQ_API int llmq_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const float *qkv, int T);
+/* KVCache.attend (kvcache.mojo:62-79) with QuantKV's float attention
+ * (attend_float_one, 113-150): causal attention of T tokens at positions
+ * pos0.. over this layer's cache, which already holds them; out[T, C]. */
+LLMQ_API int llmq_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T,
+                            int pos0);
+/* Copies the cache's codes and scales to host buffers (parity tests). */
+LLMQ_API int llmq_kv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, float *ks, float *vs);
+
+/* ------------------------------------------------ GPT-2 (the caller) */
+
+/* load_model (gpt2t.mojo:579-609) from float32 host tensors in Hugging Face
+ * layout, in this order: wte [V, C], wpe [MAX_T, C], ln_f.weight,
+ * ln_f.bias, then per layer ln_1.weight, ln_1.bias, attn.c_attn.weight,
+ * attn.c_attn.bias, attn.c_proj.weight, attn.c_proj.bias, ln_2.weight,
+ * ln_2.bias, mlp.c_fc.weight, mlp.c_fc.bias, mlp.c_proj.weight,
+ * mlp.c_proj.bias (4 + 12 * 12 pointers).  Layers become
+ * QuantMatrix[bits, group, sym, A16=True] on the device, the tied head
+ * HEAD8_A16 = QuantMatrix[8, 0, False, True] (gpt2t.mojo:1231-1235), the
+ * cache QuantKV[8] (1238-1244). */
+LLMQ_API int llmq_gpt2_create(llmq_ctx *ctx, const float *const *params, int bits, int group, int sym,
+                              llmq_gpt2 **out);
+LLMQ_API int llmq_gpt2_free(llmq_gpt2 *m);
+/* Model.weight_bytes (gpt2t.mojo:312-319). */
+LLMQ_API int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m);
+/* Model.forward (gpt2t.mojo:329-342): tokens (host) at positions pos0..;
+ * the last token's logits [V] into a host buffer when logits != NULL. */
+LLMQ_API int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int pos0, float *logits);
+/* generate with -t 0 (gpt2t.mojo:929-1009): the prompt forward, then up to
+ * `steps` greedy tokens (argmax, first maximum wins, gpt2t.mojo:792-797),
+ * each fed back as the next input, entirely on the device.  Writes the
+ * generated ids to out_tokens (host), stopping at the first EOT (50256) as
+ * the reference does, and returns the count in *n_out.  prefill_ms and
+ * decode_ms (either may be NULL) are the reference's timing spans: the
+ * prompt forward, and the steps - 1 decode forwards plus the argmaxes. */
+LLMQ_API int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int steps, int64_t *out_tokens,
+                                int *n_out, double *prefill_ms, double *decode_ms);
+/* Device pointer to the model's logits [V] (after forward / generate). */
+LLMQ_API int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLMQ_H */

@@ -1,0 +1,134 @@
+"""ctypes binding of libllmq.so (include/llmq.h).
+
+The library is loaded from this package directory only.  There is no
+fallback: if libllmq.so is missing or does not load, importing the compute
+API raises, so nothing can silently run on the CPU instead.
+"""
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libllmq.so")
+
+LLMQ_BIAS, LLMQ_GELU, LLMQ_RESID = 1, 2, 4
+GGML = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+
+
+class LlmqError(RuntimeError):
+    pass
+
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+I32 = ctypes.c_int
+PP = ctypes.POINTER(ctypes.c_void_p)
+
+# name -> (restype, argtypes); the exported C ABI, as declared in include/llmq.h
+SIGNATURES = {
+    "llmq_init": (I32, [I32, PP]),
+    "llmq_destroy": (I32, [P]),
+    "llmq_last_error": (ctypes.c_char_p, []),
+    "llmq_set_stream": (I32, [P, P]),
+    "llmq_sync": (I32, [P]),
+    "llmq_malloc": (I32, [P, ctypes.c_size_t, PP]),
+    "llmq_free": (I32, [P, P]),
+    "llmq_memcpy_h2d": (I32, [P, P, P, ctypes.c_size_t]),
+    "llmq_memcpy_d2h": (I32, [P, P, P, ctypes.c_size_t]),
+    "llmq_mat_from_f32": (I32, [P, I32, I32, I32, I32, P, I64, I64, I32, PP]),
+    "llmq_mat_from_f32_device": (I32, [P, I32, I32, I32, I32, P, I64, I64, I32, PP]),
+    "llmq_mat_from_gguf": (I32, [P, I32, P, I64, I64, PP]),
+    "llmq_mat_free": (I32, [P]),
+    "llmq_mat_nbytes": (I64, [P]),
+    "llmq_mat_group_size": (I64, [P]),
+    "llmq_mat_shape": (I32, [P, ctypes.POINTER(I64), ctypes.POINTER(I64)]),
+    "llmq_mat_export": (I32, [P, P, P, P, P]),
+    "llmq_mat_dequant_row": (I32, [P, P, I64, P]),
+    "llmq_quantize_rows": (I32, [P, P, I64, I64, P, P]),
+    "llmq_linear": (I32, [P, P, P, P, P, I64, I64, I64, I32]),
+    "llmq_ln_linear": (I32, [P, P, P, P, P, P, P, I64, I64, I64, I32]),
+    "llmq_head": (I32, [P, P, P, P, I64, I64, I64]),
+    "llmq_layernorm": (I32, [P, P, P, P, P, I64, I64]),
+    "llmq_debug_chunk_sums": (I32, [P, P, P, P, P, P, P]),
+    "llmq_kv_create": (I32, [P, I32, I32, I32, I32, PP]),
+    "llmq_kv_free": (I32, [P]),
+    "llmq_kv_nbytes": (I64, [P]),
+    "llmq_kv_store": (I32, [P, P, I32, I32, P, I32]),
+    "llmq_kv_attend": (I32, [P, P, P, P, I32, I32, I32]),
+    "llmq_kv_export": (I32, [P, P, P, P, P, P]),
+    "llmq_gpt2_create": (I32, [P, P, I32, I32, I32, PP]),
+    "llmq_gpt2_free": (I32, [P]),
+    "llmq_gpt2_weight_bytes": (I64, [P]),
+    "llmq_gpt2_forward": (I32, [P, P, I32, I32, P]),
+    "llmq_gpt2_generate": (I32, [P, P, I32, I32, P, ctypes.POINTER(I32), ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(ctypes.c_double)]),
+    "llmq_gpt2_logits_device": (I32, [P, ctypes.POINTER(ctypes.c_void_p)]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded libllmq.so; raises LlmqError if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LlmqError(f"{LIB_PATH} is not built (python -m llm_mojo_amd.build); "
+                            "llm_mojo_amd has no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        msg = lib().llmq_last_error()
+        raise LlmqError(f"llmq error {rc}: {msg.decode() if msg else ''}")
+    return rc
+
+
+def dptr(t):
+    """Device address of a torch tensor (or an int address)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def hptr(a):
+    """Host address of a numpy array."""
+    return None if a is None else a.ctypes.data
+
+
+class Context:
+    """One GPU and the stream the library's work is ordered on."""
+
+    def __init__(self, device=0, stream=None):
+        h = ctypes.c_void_p()
+        check(lib().llmq_init(device, ctypes.byref(h)))
+        self.h = h
+        if stream is not None:
+            self.set_stream(stream)
+
+    def set_stream(self, stream):
+        """stream: a torch.cuda.Stream, a raw hipStream_t address, or None."""
+        s = getattr(stream, "cuda_stream", stream)
+        check(lib().llmq_set_stream(self.h, s))
+
+    def sync(self):
+        check(lib().llmq_sync(self.h))
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().llmq_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

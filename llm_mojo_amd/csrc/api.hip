@@ -1,0 +1,738 @@
+// The C ABI of libllmq.so (include/llmq.h): contexts, weight-format handles,
+// the int8 KV cache, the compute entry points and the GPT-2 caller.
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "common.h"
+
+static thread_local char g_err[512];
+
+int llmq_set_error(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define RC(call)                   \
+    do {                           \
+        int rc_ = (call);          \
+        if (rc_ != LLMQ_OK) return rc_; \
+    } while (0)
+
+extern "C" {
+
+const char *llmq_last_error(void) { return g_err; }
+
+int llmq_init(int device, llmq_ctx **out) {
+    LLMQ_REQUIRE(out, "llmq_init: null output");
+    int n = 0;
+    LLMQ_HIP(hipGetDeviceCount(&n));
+    LLMQ_REQUIRE(device >= 0 && device < n, "llmq_init: device %d of %d", device, n);
+    LLMQ_HIP(hipSetDevice(device));
+    llmq_ctx *c = new llmq_ctx();
+    c->device = device;
+    // A blocking stream: ordered with work on the null stream, which is where
+    // frameworks without an explicit stream put their copies.
+    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamDefault);
+    if (e != hipSuccess) {
+        delete c;
+        return llmq_set_error(LLMQ_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
+    }
+    c->stream = c->own_stream;
+    LLMQ_HIP(hipGetDeviceProperties(&c->prop, device));
+    *out = c;
+    return LLMQ_OK;
+}
+
+int llmq_destroy(llmq_ctx *ctx) {
+    if (!ctx) return LLMQ_OK;
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return LLMQ_OK;
+}
+
+int llmq_set_stream(llmq_ctx *ctx, void *s) {
+    LLMQ_REQUIRE(ctx, "set_stream: null context");
+    ctx->stream = s ? (hipStream_t)s : ctx->own_stream;
+    return LLMQ_OK;
+}
+
+int llmq_sync(llmq_ctx *ctx) {
+    LLMQ_REQUIRE(ctx, "sync: null context");
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    return LLMQ_OK;
+}
+
+int llmq_malloc(llmq_ctx *ctx, size_t bytes, void **p) {
+    LLMQ_REQUIRE(ctx && p, "malloc: bad arguments");
+    if (hipMalloc(p, bytes ? bytes : 1) != hipSuccess) return llmq_set_error(LLMQ_ENOMEM, "hipMalloc(%zu) failed", bytes);
+    return LLMQ_OK;
+}
+
+int llmq_free(llmq_ctx *ctx, void *p) {
+    (void)ctx;
+    if (p) LLMQ_HIP(hipFree(p));
+    return LLMQ_OK;
+}
+
+int llmq_memcpy_h2d(llmq_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    LLMQ_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    return LLMQ_OK;
+}
+
+int llmq_memcpy_d2h(llmq_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    LLMQ_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    return LLMQ_OK;
+}
+
+// ------------------------------------------------------------ weight formats
+
+static int mat_alloc_quant(llmq_ctx *ctx, int bits, int group, int sym, int a16, int64_t n, int64_t k,
+                           llmq_mat **out) {
+    LLMQ_REQUIRE(bits == 4 || bits == 8, "from_f32: BITS must be 4 or 8");
+    LLMQ_REQUIRE(n > 0 && k > 0, "from_f32: empty matrix");
+    const int64_t g = group == 0 ? k : group;
+    // tensor.mojo:340-341
+    LLMQ_REQUIRE(g > 0 && k % g == 0 && g % 32 == 0,
+                 "group size must divide the reduction axis and be a multiple of 32");
+    llmq_mat *m = new llmq_mat();
+    m->ctx = ctx;
+    m->kind = MAT_QUANT;
+    m->bits = bits;
+    m->group_param = group;
+    m->sym = sym ? 1 : 0;
+    m->a16 = a16 ? 1 : 0;
+    m->n = n;
+    m->k = k;
+    m->group = g;
+    m->ntiles = (n + LLMQ_TILE_ROWS - 1) / LLMQ_TILE_ROWS;
+    m->CK = k * bits / 8 / 16;
+    m->NG = k / g;
+    const size_t cb = (size_t)m->ntiles * m->CK * 256, gb = (size_t)m->ntiles * m->NG * LLMQ_TILE_ROWS;
+    if (hipMalloc(&m->codes, cb) != hipSuccess || hipMalloc(&m->scales, gb * 2) != hipSuccess ||
+        hipMalloc(&m->zps, gb) != hipSuccess) {
+        hipFree(m->codes);
+        hipFree(m->scales);
+        hipFree(m->zps);
+        delete m;
+        return llmq_set_error(LLMQ_ENOMEM, "from_f32: device allocation of %zu bytes failed", cb + 3 * gb);
+    }
+    LLMQ_HIP(hipMemsetAsync(m->codes, 0, cb, ctx->stream));
+    LLMQ_HIP(hipMemsetAsync(m->scales, 0, gb * 2, ctx->stream));
+    LLMQ_HIP(hipMemsetAsync(m->zps, 0, gb, ctx->stream));
+    *out = m;
+    return LLMQ_OK;
+}
+
+int llmq_mat_from_f32_device(llmq_ctx *ctx, int bits, int group, int sym, int a16, const float *src, int64_t rows,
+                             int64_t cols, int reduce_rows, llmq_mat **out) {
+    LLMQ_REQUIRE(ctx && src && out, "from_f32: bad arguments");
+    const int64_t n = reduce_rows ? cols : rows, k = reduce_rows ? rows : cols;
+    llmq_mat *m = nullptr;
+    RC(mat_alloc_quant(ctx, bits, group, sym, a16, n, k, &m));
+    int rc = launch_quant_weights(ctx, m, src, rows, cols, reduce_rows);
+    if (rc != LLMQ_OK) {
+        llmq_mat_free(m);
+        return rc;
+    }
+    *out = m;
+    return LLMQ_OK;
+}
+
+int llmq_mat_from_f32(llmq_ctx *ctx, int bits, int group, int sym, int a16, const float *src, int64_t rows,
+                      int64_t cols, int reduce_rows, llmq_mat **out) {
+    LLMQ_REQUIRE(ctx && src && out, "from_f32: bad arguments");
+    LLMQ_REQUIRE(rows > 0 && cols > 0, "from_f32: empty matrix");
+    float *d = nullptr;
+    const size_t bytes = sizeof(float) * (size_t)rows * cols;
+    if (hipMalloc(&d, bytes) != hipSuccess) return llmq_set_error(LLMQ_ENOMEM, "from_f32: staging %zu bytes", bytes);
+    int rc = LLMQ_OK;
+    if (hipMemcpyAsync(d, src, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
+        rc = llmq_set_error(LLMQ_EHIP, "from_f32: copy to device failed");
+    if (rc == LLMQ_OK) rc = llmq_mat_from_f32_device(ctx, bits, group, sym, a16, d, rows, cols, reduce_rows, out);
+    hipStreamSynchronize(ctx->stream);
+    hipFree(d);
+    return rc;
+}
+
+int llmq_mat_free(llmq_mat *m) {
+    if (!m) return LLMQ_OK;
+    if (m->ctx) hipStreamSynchronize(m->ctx->stream);
+    hipFree(m->codes);
+    hipFree(m->scales);
+    hipFree(m->zps);
+    hipFree(m->blocks);
+    delete m;
+    return LLMQ_OK;
+}
+
+int64_t llmq_mat_nbytes(const llmq_mat *m) {
+    if (!m) return 0;
+    if (m->kind == MAT_GGUF) return m->n * m->row_bytes;  // gguf.mojo:507-508
+    return m->n * m->k * m->bits / 8 + (m->n * m->k / m->group) * 3;  // tensor.mojo:629-632
+}
+
+int64_t llmq_mat_group_size(const llmq_mat *m) {
+    if (!m) return 0;
+    if (m->kind == MAT_GGUF) return m->ggml_type == LLMQ_GGML_Q6_K ? 256 : 32;  // gguf.mojo:459-460
+    return m->group;
+}
+
+int llmq_mat_shape(const llmq_mat *m, int64_t *rows, int64_t *cols) {
+    LLMQ_REQUIRE(m, "shape: null matrix");
+    if (rows) *rows = m->n;
+    if (cols) *cols = m->k;
+    return LLMQ_OK;
+}
+
+// nibble_at (tensor.mojo:385-404): byte and nibble of column col in the
+// reference layout (BLOCKED or Q4_0-style).
+static inline void ref_nibble_at(bool blocked, int64_t col, int64_t *byte, int *high) {
+    int64_t j, chunk;
+    if (blocked) {
+        const int64_t w = col % 256, e = w % 32, p = e / 2;
+        const int64_t lane = w / 32 + 8 * (p / 8);
+        chunk = (col / 256) * 8 + p % 8;
+        j = 2 * lane + e % 2;
+    } else {
+        chunk = col / 32;
+        j = col % 32;
+    }
+    *byte = chunk * 16 + j % 16;
+    *high = j >= 16;
+}
+
+int llmq_mat_export(llmq_ctx *ctx, const llmq_mat *m, uint8_t *codes, uint16_t *scales, uint8_t *zps) {
+    LLMQ_REQUIRE(ctx && m && m->kind == MAT_QUANT, "export: not a QuantMatrix");
+    const size_t cb = (size_t)m->ntiles * m->CK * 256, gb = (size_t)m->ntiles * m->NG * LLMQ_TILE_ROWS;
+    std::vector<uint8_t> c(cb), z(gb);
+    std::vector<uint16_t> s(gb);
+    LLMQ_HIP(hipMemcpyAsync(c.data(), m->codes, cb, hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipMemcpyAsync(s.data(), m->scales, gb * 2, hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipMemcpyAsync(z.data(), m->zps, gb, hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    const bool blocked = m->a16 && m->bits == 4 && m->group_param == 32;  // tensor.mojo:296
+    const int wpc = m->bits == 4 ? 32 : 16;
+    const int64_t row_bytes = m->k * m->bits / 8;
+    if (codes) memset(codes, 0, (size_t)(m->n * row_bytes));
+    for (int64_t o = 0; o < m->n; o++) {
+        const int64_t tile = o / LLMQ_TILE_ROWS, r = o % LLMQ_TILE_ROWS;
+        for (int64_t g = 0; g < m->NG; g++) {
+            const size_t gi = (size_t)(tile * m->NG + g) * LLMQ_TILE_ROWS + r;
+            if (scales) scales[o * m->NG + g] = s[gi];
+            if (zps) zps[o * m->NG + g] = z[gi];
+        }
+        if (!codes) continue;
+        uint8_t *dst = codes + o * row_bytes;
+        for (int64_t kk = 0; kk < m->k; kk++) {
+            const int64_t ch = kk / wpc, e = kk % wpc;
+            const uint8_t *chunk = c.data() + ((tile * m->CK + ch) * LLMQ_TILE_ROWS + r) * 16;
+            if (m->bits == 8) {
+                dst[kk] = chunk[e];
+            } else {
+                const int u = (chunk[e >> 1] >> (4 * (e & 1))) & 15;
+                int64_t b;
+                int hi;
+                ref_nibble_at(blocked, kk, &b, &hi);
+                dst[b] |= (uint8_t)(hi ? u << 4 : u);
+            }
+        }
+    }
+    return LLMQ_OK;
+}
+
+int llmq_mat_dequant_row(llmq_ctx *ctx, const llmq_mat *m, int64_t row, float *dst) {
+    LLMQ_REQUIRE(ctx && m && dst, "dequant_row: bad arguments");
+    LLMQ_REQUIRE(row >= 0 && row < m->n, "dequant_row: row %lld out of range", (long long)row);
+    LLMQ_REQUIRE(m->kind == MAT_QUANT, "dequant_row: GGUF rows are read from the file buffer");
+    const int64_t tile = row / LLMQ_TILE_ROWS, r = row % LLMQ_TILE_ROWS;
+    std::vector<uint8_t> c(m->CK * 16), z(m->NG);
+    std::vector<uint16_t> s(m->NG);
+    LLMQ_HIP(hipMemcpy2DAsync(c.data(), 16, m->codes + ((tile * m->CK) * LLMQ_TILE_ROWS + r) * 16, 256, 16, m->CK,
+                              hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipMemcpy2DAsync(s.data(), 2, m->scales + (tile * m->NG) * LLMQ_TILE_ROWS + r, 32, 2, m->NG,
+                              hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipMemcpy2DAsync(z.data(), 1, m->zps + (tile * m->NG) * LLMQ_TILE_ROWS + r, 16, 1, m->NG,
+                              hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    const int wpc = m->bits == 4 ? 32 : 16;
+    for (int64_t kk = 0; kk < m->k; kk++) {
+        const uint8_t *chunk = c.data() + (kk / wpc) * 16;
+        const int64_t e = kk % wpc;
+        const int u = m->bits == 8 ? chunk[e] : (chunk[e >> 1] >> (4 * (e & 1))) & 15;
+        const int64_t g = kk / m->group;
+        // row_op (tensor.mojo:463-473): (float(u) - float(zp)) * scale
+        __half h = __ushort_as_half(s[g]);
+        dst[kk] = ((float)u - (float)z[g]) * __half2float(h);
+    }
+    return LLMQ_OK;
+}
+
+int llmq_mat_from_gguf(llmq_ctx *ctx, int ggml_type, const void *blocks, int64_t rows, int64_t cols,
+                       llmq_mat **out) {
+    (void)ctx;
+    (void)ggml_type;
+    (void)blocks;
+    (void)rows;
+    (void)cols;
+    (void)out;
+    return llmq_set_error(LLMQ_EUNSUPPORTED, "from_gguf: GGUF block formats are not in this build yet");
+}
+
+// ------------------------------------------------------------------ compute
+
+int llmq_quantize_rows(llmq_ctx *ctx, const float *x, int64_t T, int64_t K, int16_t *xq, float *sx) {
+    LLMQ_REQUIRE(ctx && x && xq && sx, "quantize_rows: bad arguments");
+    return launch_quantize_rows(ctx, x, T, K, xq, sx);
+}
+
+static int check_linear(const llmq_mat *w, int64_t IN, int64_t OUT) {
+    LLMQ_REQUIRE(w, "linear: null matrix");
+    LLMQ_REQUIRE(w->k == IN && w->n == OUT, "linear: matrix is %lldx%lld, call says IN=%lld OUT=%lld",
+                 (long long)w->n, (long long)w->k, (long long)IN, (long long)OUT);
+    if (w->kind == MAT_QUANT && !w->a16)
+        return llmq_set_error(LLMQ_EUNSUPPORTED,
+                              "linear: float-activation QuantMatrix (A16=False) has no device kernel in this build");
+    LLMQ_REQUIRE(w->kind == MAT_QUANT, "linear: GGUF matrices are not in this build yet");
+    return LLMQ_OK;
+}
+
+int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, const float *bias, int64_t T,
+                int64_t IN, int64_t OUT, int flags) {
+    LLMQ_REQUIRE(ctx, "linear: null context");
+    RC(check_linear(w, IN, OUT));
+    GemvRequest rq;
+    rq.w = w;
+    rq.x = x;
+    rq.out = out;
+    rq.bias = bias;
+    rq.T = T;
+    rq.flags = flags;
+    return launch_gemv_a16(ctx, rq);
+}
+
+int llmq_ln_linear(llmq_ctx *ctx, float *out, const float *x, const float *ln_w, const float *ln_b, const llmq_mat *w,
+                   const float *bias, int64_t T, int64_t IN, int64_t OUT, int flags) {
+    LLMQ_REQUIRE(ctx && ln_w && ln_b, "ln_linear: bad arguments");
+    RC(check_linear(w, IN, OUT));
+    GemvRequest rq;
+    rq.w = w;
+    rq.x = x;
+    rq.ln_w = ln_w;
+    rq.ln_b = ln_b;
+    rq.out = out;
+    rq.bias = bias;
+    rq.T = T;
+    rq.flags = flags;
+    return launch_gemv_a16(ctx, rq);
+}
+
+int llmq_head(llmq_ctx *ctx, float *logits, const float *h, const llmq_mat *w, int64_t T, int64_t V, int64_t C) {
+    return llmq_linear(ctx, logits, h, w, nullptr, T, C, V, 0);
+}
+
+int llmq_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C) {
+    LLMQ_REQUIRE(ctx, "layernorm: null context");
+    return launch_layernorm(ctx, out, x, w, b, T, C);
+}
+
+int llmq_debug_chunk_sums(llmq_ctx *ctx, const float *xf, const llmq_mat *w, float *out, int32_t *chunk_sums,
+                          int16_t *xq, float *sx) {
+    LLMQ_REQUIRE(ctx && w, "debug_chunk_sums: bad arguments");
+    RC(check_linear(w, w->k, w->n));
+    GemvRequest rq;
+    rq.w = w;
+    rq.x = xf;
+    rq.out = out;
+    rq.T = 1;
+    rq.flags = 0;
+    rq.dbg = chunk_sums;
+    rq.xq_out = xq;
+    rq.sx_out = sx;
+    return launch_gemv_a16(ctx, rq);
+}
+
+// ------------------------------------------------------------- int8 KV cache
+
+int llmq_kv_create(llmq_ctx *ctx, int n_layer, int max_t, int n_head, int head_dim, llmq_kv **out) {
+    LLMQ_REQUIRE(ctx && out && n_layer > 0 && max_t > 0 && n_head > 0 && head_dim > 0, "kv_create: bad arguments");
+    LLMQ_REQUIRE(head_dim % 64 == 0 || head_dim == 16 || head_dim == 32, "kv_create: head_dim %d unsupported",
+                 head_dim);
+    llmq_kv *kv = new llmq_kv();
+    kv->ctx = ctx;
+    kv->n_layer = n_layer;
+    kv->max_t = max_t;
+    kv->n_head = n_head;
+    kv->head_dim = head_dim;
+    const size_t n = (size_t)n_layer * max_t * n_head * head_dim, ns = (size_t)n_layer * max_t * n_head;
+    if (hipMalloc(&kv->k, n) != hipSuccess || hipMalloc(&kv->v, n) != hipSuccess ||
+        hipMalloc(&kv->ks, ns * 4) != hipSuccess || hipMalloc(&kv->vs, ns * 4) != hipSuccess) {
+        llmq_kv_free(kv);
+        return llmq_set_error(LLMQ_ENOMEM, "kv_create: allocation failed");
+    }
+    LLMQ_HIP(hipMemsetAsync(kv->k, 0, n, ctx->stream));
+    LLMQ_HIP(hipMemsetAsync(kv->v, 0, n, ctx->stream));
+    LLMQ_HIP(hipMemsetAsync(kv->ks, 0, ns * 4, ctx->stream));
+    LLMQ_HIP(hipMemsetAsync(kv->vs, 0, ns * 4, ctx->stream));
+    *out = kv;
+    return LLMQ_OK;
+}
+
+int llmq_kv_free(llmq_kv *kv) {
+    if (!kv) return LLMQ_OK;
+    if (kv->ctx) hipStreamSynchronize(kv->ctx->stream);
+    hipFree(kv->k);
+    hipFree(kv->v);
+    hipFree(kv->ks);
+    hipFree(kv->vs);
+    delete kv;
+    return LLMQ_OK;
+}
+
+int64_t llmq_kv_nbytes(const llmq_kv *kv) {
+    if (!kv) return 0;
+    const int64_t n = (int64_t)kv->n_layer * kv->max_t * kv->n_head;
+    return 2 * n * (kv->head_dim + 4);  // kvcache.mojo:377-379 with BITS = 8
+}
+
+int llmq_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const float *qkv, int T) {
+    LLMQ_REQUIRE(ctx, "kv_store: null context");
+    return launch_kv_store(ctx, kv, layer, pos0, nullptr, qkv, T, 0);
+}
+
+int llmq_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0) {
+    LLMQ_REQUIRE(ctx, "kv_attend: null context");
+    return launch_kv_attend(ctx, kv, out, qkv, layer, T, pos0, nullptr, 0);
+}
+
+int llmq_kv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, float *ks, float *vs) {
+    LLMQ_REQUIRE(ctx && kv, "kv_export: bad arguments");
+    const size_t n = (size_t)kv->n_layer * kv->max_t * kv->n_head * kv->head_dim,
+                 ns = (size_t)kv->n_layer * kv->max_t * kv->n_head;
+    if (k) LLMQ_HIP(hipMemcpyAsync(k, kv->k, n, hipMemcpyDeviceToHost, ctx->stream));
+    if (v) LLMQ_HIP(hipMemcpyAsync(v, kv->v, n, hipMemcpyDeviceToHost, ctx->stream));
+    if (ks) LLMQ_HIP(hipMemcpyAsync(ks, kv->ks, ns * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (vs) LLMQ_HIP(hipMemcpyAsync(vs, kv->vs, ns * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    return LLMQ_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------- GPT-2
+
+namespace {
+constexpr int NL = 12, NH = 12, C = 768, HS = 64, MAXT = 1024, V = 50257, EOT = 50256;
+enum { LN1_W, LN1_B, QKV_B, PROJ_B, LN2_W, LN2_B, FC_B, FCPROJ_B, N_VECS };
+constexpr int VEC_LEN[N_VECS] = {C, C, 3 * C, C, C, C, 4 * C, C};
+constexpr int VEC_PARAM[N_VECS] = {0, 1, 3, 5, 6, 7, 9, 11};  // index within a layer's 12 params
+constexpr int64_t SMALL_FLOATS = (int64_t)NL * 13 * C + (int64_t)MAXT * C + 2 * C;  // gpt2t.mojo:576
+}  // namespace
+
+// Runs the enclosing GPT-2 call on the context's own (non-null) stream, which
+// a decode-step graph can be captured on, after the caller's stream's
+// earlier work; the caller's stream is restored on exit.
+struct OwnStream {
+    llmq_ctx *ctx;
+    hipStream_t saved;
+    explicit OwnStream(llmq_ctx *c) : ctx(c), saved(c->stream) {
+        if (saved != ctx->own_stream) {
+            hipStreamSynchronize(saved);
+            ctx->stream = ctx->own_stream;
+        }
+    }
+    ~OwnStream() {
+        if (saved != ctx->own_stream) {
+            hipStreamSynchronize(ctx->own_stream);
+            ctx->stream = saved;
+        }
+    }
+};
+
+struct llmq_gpt2 {
+    llmq_ctx *ctx = nullptr;
+    llmq_mat *wte = nullptr;
+    llmq_mat *mats[NL * 4] = {};
+    float *small = nullptr;
+    const float *vec[NL][N_VECS] = {};
+    const float *wpe = nullptr, *lnf_w = nullptr, *lnf_b = nullptr;
+    llmq_kv *kv = nullptr;
+    float *x = nullptr, *qkv = nullptr, *att = nullptr, *fc = nullptr, *logits = nullptr;
+    ArgmaxPart *parts = nullptr;
+    int nparts = 0;
+    int64_t *tokens = nullptr, *gen = nullptr;
+    int *state = nullptr;  // {pos, step} of the device-driven decode loop
+    hipGraphExec_t step_graph = nullptr;
+    hipGraph_t step_graph_def = nullptr;
+};
+
+// Model.blocks (gpt2t.mojo:485-571) for T tokens: tokens in m->tokens when
+// state == nullptr, else one token picked on the device from the previous
+// head's argmax partials (decode), with the position in state[0].
+static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step) {
+    llmq_ctx *ctx = m->ctx;
+    if (device_step)
+        RC(launch_embed(ctx, m->wte, m->wpe, nullptr, 1, 0, m->x, m->parts, m->nparts, m->gen, m->state, 1));
+    else
+        RC(launch_embed(ctx, m->wte, m->wpe, m->tokens, T, pos0, m->x, nullptr, 0, nullptr, nullptr, 1));
+    const int *pos_dev = device_step ? m->state : nullptr;
+    for (int l = 0; l < NL; l++) {
+        llmq_mat **w = &m->mats[l * 4];
+        const float *const *v = m->vec[l];
+        GemvRequest q;
+        q.w = w[0];
+        q.x = m->x;
+        q.ln_w = v[LN1_W];
+        q.ln_b = v[LN1_B];
+        q.out = m->qkv;
+        q.bias = v[QKV_B];
+        q.T = T;
+        q.flags = LLMQ_BIAS;
+        RC(launch_gemv_a16(ctx, q));
+        RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
+        RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, pos_dev, 3 * C));
+        GemvRequest p;
+        p.w = w[1];
+        p.x = m->att;
+        p.out = m->x;
+        p.bias = v[PROJ_B];
+        p.T = T;
+        p.flags = LLMQ_BIAS | LLMQ_RESID;
+        RC(launch_gemv_a16(ctx, p));
+        GemvRequest f;
+        f.w = w[2];
+        f.x = m->x;
+        f.ln_w = v[LN2_W];
+        f.ln_b = v[LN2_B];
+        f.out = m->fc;
+        f.bias = v[FC_B];
+        f.T = T;
+        f.flags = LLMQ_BIAS | LLMQ_GELU;
+        RC(launch_gemv_a16(ctx, f));
+        GemvRequest g;
+        g.w = w[3];
+        g.x = m->fc;
+        g.out = m->x;
+        g.bias = v[FCPROJ_B];
+        g.T = T;
+        g.flags = LLMQ_BIAS | LLMQ_RESID;
+        RC(launch_gemv_a16(ctx, g));
+    }
+    // Model.forward's tail (gpt2t.mojo:337-340): LN_f on the last row, head.
+    GemvRequest h;
+    h.w = m->wte;
+    h.x = m->x + (int64_t)(T - 1) * C;
+    h.ln_w = m->lnf_w;
+    h.ln_b = m->lnf_b;
+    h.out = m->logits;
+    h.T = 1;
+    h.flags = 0;
+    h.amax = m->parts;
+    h.amax_cap = m->nparts;
+    return launch_gemv_a16(ctx, h);
+}
+
+extern "C" {
+
+int llmq_gpt2_free(llmq_gpt2 *m) {
+    if (!m) return LLMQ_OK;
+    if (m->ctx) hipStreamSynchronize(m->ctx->stream);
+    if (m->step_graph) hipGraphExecDestroy(m->step_graph);
+    if (m->step_graph_def) hipGraphDestroy(m->step_graph_def);
+    llmq_mat_free(m->wte);
+    for (auto *w : m->mats) llmq_mat_free(w);
+    llmq_kv_free(m->kv);
+    hipFree(m->small);
+    hipFree(m->x);
+    hipFree(m->qkv);
+    hipFree(m->att);
+    hipFree(m->fc);
+    hipFree(m->logits);
+    hipFree(m->parts);
+    hipFree(m->tokens);
+    hipFree(m->gen);
+    hipFree(m->state);
+    delete m;
+    return LLMQ_OK;
+}
+
+int llmq_gpt2_create(llmq_ctx *ctx, const float *const *params, int bits, int group, int sym, llmq_gpt2 **out) {
+    LLMQ_REQUIRE(ctx && params && out, "gpt2_create: bad arguments");
+    llmq_gpt2 *m = new llmq_gpt2();
+    m->ctx = ctx;
+    int rc = LLMQ_OK;
+#define GO(call)                   \
+    do {                           \
+        rc = (call);               \
+        if (rc != LLMQ_OK) goto fail; \
+    } while (0)
+#define ALLOC(ptr, bytes)                                                                      \
+    do {                                                                                       \
+        if (hipMalloc(&(ptr), (bytes)) != hipSuccess) {                                        \
+            rc = llmq_set_error(LLMQ_ENOMEM, "gpt2_create: allocation of %zu bytes", (size_t)(bytes)); \
+            goto fail;                                                                         \
+        }                                                                                      \
+    } while (0)
+    {
+        // E = HEAD8_A16 = QuantMatrix[8, 0, False, True] (gpt2t.mojo:1234).
+        GO(llmq_mat_from_f32(ctx, 8, 0, 0, 1, params[0], V, C, 0, &m->wte));
+        static const int64_t rows[4] = {C, C, C, 4 * C}, cols[4] = {3 * C, C, 4 * C, C};
+        static const int mat_param[4] = {2, 4, 8, 10};
+        for (int l = 0; l < NL; l++)
+            for (int j = 0; j < 4; j++)
+                GO(llmq_mat_from_f32(ctx, bits, group, sym, 1, params[4 + 12 * l + mat_param[j]], rows[j], cols[j], 1,
+                                     &m->mats[l * 4 + j]));
+        ALLOC(m->small, sizeof(float) * SMALL_FLOATS);
+        std::vector<float> host((size_t)SMALL_FLOATS);
+        int64_t off = 0;
+        for (int l = 0; l < NL; l++)
+            for (int s = 0; s < N_VECS; s++) {
+                memcpy(host.data() + off, params[4 + 12 * l + VEC_PARAM[s]], sizeof(float) * VEC_LEN[s]);
+                m->vec[l][s] = m->small + off;
+                off += VEC_LEN[s];
+            }
+        memcpy(host.data() + off, params[1], sizeof(float) * MAXT * C);
+        m->wpe = m->small + off;
+        off += (int64_t)MAXT * C;
+        memcpy(host.data() + off, params[2], sizeof(float) * C);
+        m->lnf_w = m->small + off;
+        off += C;
+        memcpy(host.data() + off, params[3], sizeof(float) * C);
+        m->lnf_b = m->small + off;
+        if (hipMemcpy(m->small, host.data(), sizeof(float) * SMALL_FLOATS, hipMemcpyHostToDevice) != hipSuccess) {
+            rc = llmq_set_error(LLMQ_EHIP, "gpt2_create: copy of the small tensors failed");
+            goto fail;
+        }
+        GO(llmq_kv_create(ctx, NL, MAXT, NH, HS, &m->kv));
+        ALLOC(m->x, sizeof(float) * MAXT * C);
+        ALLOC(m->qkv, sizeof(float) * MAXT * 3 * C);
+        ALLOC(m->att, sizeof(float) * MAXT * C);
+        ALLOC(m->fc, sizeof(float) * MAXT * 4 * C);
+        ALLOC(m->logits, sizeof(float) * V);
+        m->nparts = gemv_a16_num_parts(m->wte);
+        ALLOC(m->parts, sizeof(ArgmaxPart) * m->nparts);
+        ALLOC(m->tokens, sizeof(int64_t) * MAXT);
+        ALLOC(m->gen, sizeof(int64_t) * MAXT);
+        ALLOC(m->state, sizeof(int) * 4);
+        if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
+            rc = llmq_set_error(LLMQ_EHIP, "gpt2_create: load failed");
+            goto fail;
+        }
+    }
+    *out = m;
+    return LLMQ_OK;
+fail:
+    llmq_gpt2_free(m);
+    return rc;
+#undef GO
+#undef ALLOC
+}
+
+int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m) {
+    if (!m) return 0;
+    int64_t n = llmq_mat_nbytes(m->wte);
+    for (auto *w : m->mats) n += llmq_mat_nbytes(w);
+    return n + SMALL_FLOATS * 4;  // gpt2t.mojo:312-319
+}
+
+int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int pos0, float *logits) {
+    LLMQ_REQUIRE(m && tokens && T >= 1, "gpt2_forward: bad arguments");
+    LLMQ_REQUIRE(pos0 >= 0 && pos0 + T <= MAXT, "gpt2_forward: positions %d..%d beyond %d", pos0, pos0 + T - 1, MAXT);
+    for (int t = 0; t < T; t++)
+        LLMQ_REQUIRE(tokens[t] >= 0 && tokens[t] < V, "gpt2_forward: token %lld out of range", (long long)tokens[t]);
+    OwnStream os_(m->ctx);
+    llmq_ctx *ctx = m->ctx;
+    LLMQ_HIP(hipMemcpyAsync(m->tokens, tokens, sizeof(int64_t) * T, hipMemcpyHostToDevice, ctx->stream));
+    RC(gpt2_enqueue(m, T, pos0, false));
+    if (logits) {
+        LLMQ_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * V, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    return LLMQ_OK;
+}
+
+int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr) {
+    LLMQ_REQUIRE(m && dptr, "gpt2_logits_device: bad arguments");
+    *dptr = m->logits;
+    return LLMQ_OK;
+}
+
+static int decode_step(llmq_gpt2 *m, bool use_graph) {
+    llmq_ctx *ctx = m->ctx;
+    if (!use_graph) return gpt2_enqueue(m, 1, 0, true);
+    if (!m->step_graph) {
+        LLMQ_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        int rc = gpt2_enqueue(m, 1, 0, true);
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+        if (rc != LLMQ_OK) {
+            if (g) hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return llmq_set_error(LLMQ_EHIP, "decode graph capture: %s", hipGetErrorString(e));
+        m->step_graph_def = g;
+        LLMQ_HIP(hipGraphInstantiate(&m->step_graph, g, nullptr, nullptr, 0));
+    }
+    LLMQ_HIP(hipGraphLaunch(m->step_graph, ctx->stream));
+    return LLMQ_OK;
+}
+
+int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int steps, int64_t *out_tokens, int *n_out,
+                       double *prefill_ms, double *decode_ms) {
+    LLMQ_REQUIRE(m && prompt && n_prompt >= 1 && steps >= 0 && out_tokens && n_out, "gpt2_generate: bad arguments");
+    LLMQ_REQUIRE(n_prompt <= MAXT, "gpt2_generate: prompt longer than %d", MAXT);
+    for (int t = 0; t < n_prompt; t++)
+        LLMQ_REQUIRE(prompt[t] >= 0 && prompt[t] < V, "gpt2_generate: token %lld out of range", (long long)prompt[t]);
+    steps = steps < MAXT - n_prompt ? steps : MAXT - n_prompt;  // gpt2t.mojo:945
+    OwnStream os_(m->ctx);
+    llmq_ctx *ctx = m->ctx;
+    const char *ge = getenv("LLMQ_GRAPH");
+    const bool use_graph = !(ge && ge[0] == '0');
+    hipEvent_t e0, e1, e2;
+    LLMQ_HIP(hipEventCreate(&e0));
+    LLMQ_HIP(hipEventCreate(&e1));
+    LLMQ_HIP(hipEventCreate(&e2));
+    LLMQ_HIP(hipMemcpyAsync(m->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, ctx->stream));
+    const int init_state[4] = {n_prompt - 1, -1, 0, 0};
+    LLMQ_HIP(hipMemcpyAsync(m->state, init_state, sizeof(init_state), hipMemcpyHostToDevice, ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    LLMQ_HIP(hipEventRecord(e0, ctx->stream));
+    RC(gpt2_enqueue(m, n_prompt, 0, false));
+    LLMQ_HIP(hipEventRecord(e1, ctx->stream));
+    for (int i = 0; i < steps; i++) {
+        if (i + 1 < steps)
+            RC(decode_step(m, use_graph));
+        else  // the last token: argmax only (gpt2t.mojo:975-976)
+            RC(launch_embed(ctx, m->wte, m->wpe, nullptr, 1, 0, m->x, m->parts, m->nparts, m->gen, m->state, 0));
+    }
+    LLMQ_HIP(hipEventRecord(e2, ctx->stream));
+    LLMQ_HIP(hipEventSynchronize(e2));
+    float a = 0, b = 0;
+    LLMQ_HIP(hipEventElapsedTime(&a, e0, e1));
+    LLMQ_HIP(hipEventElapsedTime(&b, e1, e2));
+    if (prefill_ms) *prefill_ms = a;
+    if (decode_ms) *decode_ms = b;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipEventDestroy(e2);
+    std::vector<int64_t> g(steps > 0 ? steps : 1);
+    if (steps > 0) LLMQ_HIP(hipMemcpy(g.data(), m->gen, sizeof(int64_t) * steps, hipMemcpyDeviceToHost));
+    int n = 0;
+    for (; n < steps; n++) {
+        if (g[n] == EOT) break;  // gpt2t.mojo:971-972
+        out_tokens[n] = g[n];
+    }
+    *n_out = n;
+    return LLMQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,273 @@
+// QuantKV[8] store and float attention over the int8 cache
+// (kvcache.mojo:248-385, attend_float_one 113-150), LayerNorm
+// (kernels.mojo:179-197) and the token embedding with the greedy argmax of
+// the previous step (gpt2t.mojo:378-385, 495-502, 792-797).
+#include "common.h"
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// QuantKV.store (kvcache.mojo:333-342) for token t = blockIdx.y, head h =
+// blockIdx.x: per head s = max|x| / 127 (1 if zero), codes round(x / s).
+// One wave per (token, head); head_dim is a multiple of 64.
+__global__ __launch_bounds__(64) void kv_store_kernel(const float *__restrict__ qkv, int64_t ld, int C, int pos0,
+                                                      const int *__restrict__ pos_dev, int layer, int max_t,
+                                                      int n_head, int hd, int8_t *__restrict__ K8,
+                                                      int8_t *__restrict__ V8, float *__restrict__ KS,
+                                                      float *__restrict__ VS) {
+    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int pos = (pos_dev ? *pos_dev : pos0) + t;
+    const int64_t sl = ((int64_t)layer * max_t + pos) * n_head + h;
+    for (int kv = 0; kv < 2; kv++) {
+        const float *src = qkv + (int64_t)t * ld + (int64_t)(1 + kv) * C + (int64_t)h * hd;
+        float m = 0.0f;
+        for (int i = lane; i < hd; i += 64) m = fmaxf(m, fabsf(src[i]));
+        m = wave_max(m);
+        float s = m / 127.0f;
+        if (s == 0.0f) s = 1.0f;
+        const float inv = 1.0f / s;
+        int8_t *dst = (kv ? V8 : K8) + sl * hd;
+        for (int i = lane; i < hd; i += 64) dst[i] = (int8_t)llmq_to_int(roundf(src[i] * inv));
+        if (lane == 0) (kv ? VS : KS)[sl] = s;
+    }
+}
+
+// attend_float_one (kvcache.mojo:113-150) through QuantKV.score / add_value
+// (344-370) for token t = blockIdx.y (position pos0 + t), head h = blockIdx.x.
+// Scores: q . k over head_dim, times the key's scale, times 1/sqrt(hd); softmax
+// with the running maximum; out = sum_s (p_s * vs_s) * v_s.  The summation
+// order differs from the reference's sequential one (fp32 rounding only).
+constexpr int kAttnThreads = 256;
+__global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__restrict__ qkv, int64_t ld, int C,
+                                                                 int pos0, const int *__restrict__ pos_dev,
+                                                                 int layer, int max_t, int n_head, int hd,
+                                                                 const int8_t *__restrict__ K8,
+                                                                 const int8_t *__restrict__ V8,
+                                                                 const float *__restrict__ KS,
+                                                                 const float *__restrict__ VS,
+                                                                 float *__restrict__ out, int64_t ldo) {
+    extern __shared__ float sm[];
+    float *q = sm;              // [hd]
+    float *scores = sm + hd;    // [npos]
+    __shared__ float red[kAttnThreads];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int npos = (pos_dev ? *pos_dev : pos0) + t + 1;
+    const float scale = 1.0f / sqrtf((float)hd);
+    for (int i = tid; i < hd; i += kAttnThreads) q[i] = qkv[(int64_t)t * ld + (int64_t)h * hd + i];
+    __syncthreads();
+    const int64_t base = (int64_t)layer * max_t * n_head + h;  // slot of position 0
+    float mx = -INFINITY;
+    for (int s = tid; s < npos; s += kAttnThreads) {
+        const int64_t sl = base + (int64_t)s * n_head;
+        const int8_t *kp = K8 + sl * hd;
+        float d = 0.0f;
+        for (int i = 0; i < hd; i += 16) {
+            const int4 w = *reinterpret_cast<const int4 *>(kp + i);
+            const int8_t *b = reinterpret_cast<const int8_t *>(&w);
+#pragma unroll
+            for (int e = 0; e < 16; e++) d = fmaf(q[i + e], (float)b[e], d);
+        }
+        const float sc = d * KS[sl] * scale;
+        scores[s] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float tot = 0.0f;
+    for (int s = tid; s < npos; s += kAttnThreads) {
+        const float e = expf(scores[s] - mx);
+        scores[s] = e;
+        tot += e;
+    }
+    tot = wave_sum(tot);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = tot;
+    __syncthreads();
+    const float total = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();
+    // out[i]: threads split positions into `parts` interleaved subsets.
+    const int parts = kAttnThreads / hd;  // hd divides 256
+    const int i = tid % hd, part = tid / hd;
+    float acc = 0.0f;
+    for (int s = part; s < npos; s += parts) {
+        const int64_t sl = base + (int64_t)s * n_head;
+        const float p = scores[s] / total;
+        const float ps = p * VS[sl];
+        acc = fmaf(ps, (float)V8[sl * hd + i], acc);
+    }
+    red[tid] = acc;
+    __syncthreads();
+    if (part == 0) {
+        float v = 0.0f;
+        for (int pp = 0; pp < parts; pp++) v += red[pp * hd + i];
+        out[(int64_t)t * ldo + (int64_t)h * hd + i] = v;
+    }
+}
+
+// LayerNorm over rows of C (kernels.mojo:179-197), one workgroup per row.
+__global__ __launch_bounds__(256) void layernorm_kernel(float *__restrict__ out, const float *__restrict__ x,
+                                                        const float *__restrict__ w, const float *__restrict__ b,
+                                                        int64_t C) {
+    __shared__ float red[4];
+    const float *xr = x + (int64_t)blockIdx.x * C;
+    float *o = out + (int64_t)blockIdx.x * C;
+    const int tid = threadIdx.x;
+    float sum = 0.0f;
+    for (int64_t i = tid; i < C; i += 256) sum += xr[i];
+    sum = wave_sum(sum);
+    if ((tid & 63) == 0) red[tid >> 6] = sum;
+    __syncthreads();
+    const float mean = (((red[0] + red[1]) + red[2]) + red[3]) / (float)C;
+    __syncthreads();
+    float sq = 0.0f;
+    for (int64_t i = tid; i < C; i += 256) {
+        float d = xr[i] - mean;
+        sq += d * d;
+    }
+    sq = wave_sum(sq);
+    if ((tid & 63) == 0) red[tid >> 6] = sq;
+    __syncthreads();
+    const float var = (((red[0] + red[1]) + red[2]) + red[3]) / (float)C;
+    const float rstd = 1.0f / sqrtf(var + 1e-5f);
+    for (int64_t i = tid; i < C; i += 256) {
+        float nn = (xr[i] - mean) * rstd;
+        o[i] = nn * w[i] + b[i];
+    }
+}
+
+// Embedding rows of E (any QuantMatrix in the row-tile layout), plus wpe.
+// In decode mode (parts != nullptr) the token is first picked as the argmax
+// over the previous head's per-workgroup partials (ties: smaller index), is
+// recorded in gen[step], and state = {pos, step} advances by one.
+__global__ __launch_bounds__(256) void embed_kernel(const uint4 *__restrict__ codes,
+                                                    const uint16_t *__restrict__ scales,
+                                                    const uint8_t *__restrict__ zps, int bits, int64_t CK,
+                                                    int64_t NG, int64_t CPG, const float *__restrict__ wpe,
+                                                    const int64_t *__restrict__ tokens, int pos0, int C,
+                                                    float *__restrict__ x, const ArgmaxPart *__restrict__ parts,
+                                                    int nparts, int64_t *__restrict__ gen, int *__restrict__ state,
+                                                    int do_embed, int64_t n_rows) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    __shared__ int64_t s_tok;
+    __shared__ int s_pos;
+    const int tid = threadIdx.x, t = blockIdx.x;
+    if (parts) {
+        float v = -INFINITY;
+        int idx = 0x7fffffff;
+        for (int p = tid; p < nparts; p += 256) {
+            ArgmaxPart c = parts[p];
+            if (c.v > v || (c.v == v && c.idx < idx)) {
+                v = c.v;
+                idx = c.idx;
+            }
+        }
+        bv[tid] = v;
+        bi[tid] = idx;
+        __syncthreads();
+        for (int off = 128; off > 0; off >>= 1) {
+            if (tid < off) {
+                float ov = bv[tid + off];
+                int oi = bi[tid + off];
+                if (ov > bv[tid] || (ov == bv[tid] && oi < bi[tid])) {
+                    bv[tid] = ov;
+                    bi[tid] = oi;
+                }
+            }
+            __syncthreads();
+        }
+        if (tid == 0) {
+            const int step = state[1] + 1;
+            const int pos = state[0] + 1;
+            gen[step] = bi[0];
+            state[0] = pos;
+            state[1] = step;
+            s_tok = bi[0];
+            s_pos = pos;
+        }
+        __syncthreads();
+    } else {
+        if (tid == 0) {
+            s_tok = tokens[t];
+            s_pos = pos0 + t;
+        }
+        __syncthreads();
+    }
+    if (!do_embed) return;
+    // An argmax over logits that are all NaN has no index: embed token 0
+    // rather than read outside the table.
+    const int64_t row = (s_tok >= 0 && s_tok < n_rows) ? s_tok : 0;
+    const int pos = s_pos;
+    const int64_t tile = row / LLMQ_TILE_ROWS, r = row % LLMQ_TILE_ROWS;
+    const int wpc = bits == 4 ? 32 : 16;
+    for (int k = tid; k < C; k += 256) {
+        const int64_t c = k / wpc, e = k % wpc;
+        const uint8_t *chunk = reinterpret_cast<const uint8_t *>(codes + (tile * CK + c) * LLMQ_TILE_ROWS + r);
+        int u = bits == 4 ? ((chunk[e >> 1] >> (4 * (e & 1))) & 15) : chunk[e];
+        const int64_t gi = (tile * NG + c / CPG) * LLMQ_TILE_ROWS + r;
+        const float s = __half2float(__ushort_as_half(scales[gi]));
+        const float v = ((float)u - (float)zps[gi]) * s;  // row_op (tensor.mojo:463-473)
+        x[(int64_t)t * C + k] = v + wpe[(int64_t)pos * C + k];
+    }
+}
+
+}  // namespace
+
+int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,
+                    int64_t ld) {
+    LLMQ_REQUIRE(kv && qkv && T >= 1, "kv_store: bad arguments");
+    LLMQ_REQUIRE(layer >= 0 && layer < kv->n_layer, "kv_store: layer %d out of range", layer);
+    LLMQ_REQUIRE(pos_dev || (pos0 >= 0 && pos0 + T <= kv->max_t), "kv_store: positions %d..%d beyond max_t %d", pos0,
+                 pos0 + T - 1, kv->max_t);
+    const int C = kv->n_head * kv->head_dim;
+    hipLaunchKernelGGL(kv_store_kernel, dim3(kv->n_head, T), dim3(64), 0, ctx->stream, qkv, ld ? ld : 3 * C, C, pos0,
+                       pos_dev, layer, kv->max_t, kv->n_head, kv->head_dim, kv->k, kv->v, kv->ks, kv->vs);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
+                     const int *pos_dev, int64_t ld) {
+    LLMQ_REQUIRE(kv && qkv && out && T >= 1, "kv_attend: bad arguments");
+    LLMQ_REQUIRE(layer >= 0 && layer < kv->n_layer, "kv_attend: layer %d out of range", layer);
+    LLMQ_REQUIRE(pos_dev || (pos0 >= 0 && pos0 + T <= kv->max_t), "kv_attend: positions beyond max_t");
+    LLMQ_REQUIRE(kv->head_dim % 16 == 0 && 256 % kv->head_dim == 0, "kv_attend: head_dim %d unsupported",
+                 kv->head_dim);
+    const int C = kv->n_head * kv->head_dim;
+    const size_t lds = sizeof(float) * ((size_t)kv->head_dim + kv->max_t);
+    hipLaunchKernelGGL(kv_attend_kernel, dim3(kv->n_head, T), dim3(kAttnThreads), lds, ctx->stream, qkv,
+                       ld ? ld : 3 * C, C, pos0, pos_dev, layer, kv->max_t, kv->n_head, kv->head_dim, kv->k, kv->v,
+                       kv->ks, kv->vs, out, (int64_t)C);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C) {
+    LLMQ_REQUIRE(T >= 1 && C >= 1 && out && x && w && b, "layernorm: bad arguments");
+    hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)T), dim3(256), 0, ctx->stream, out, x, w, b, C);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+int launch_embed(llmq_ctx *ctx, const llmq_mat *E, const float *wpe, const int64_t *tokens, int T, int pos0,
+                 float *x, const ArgmaxPart *parts, int nparts, int64_t *gen, int *state, int do_embed) {
+    LLMQ_REQUIRE(E && E->kind == MAT_QUANT, "embed: the embedding must be a QuantMatrix");
+    const int64_t cpg = E->group / (E->bits == 4 ? 32 : 16);
+    hipLaunchKernelGGL(embed_kernel, dim3(parts ? 1 : T), dim3(256), 0, ctx->stream,
+                       reinterpret_cast<const uint4 *>(E->codes), E->scales, E->zps, E->bits, E->CK, E->NG, cpg, wpe,
+                       tokens, pos0, (int)E->k, x, parts, nparts, gen, state, do_embed, E->n);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}

@@ -1,0 +1,125 @@
+// Internal declarations shared by libllmq's HIP sources (gfx950 only).
+//
+// Device layout of a QuantMatrix ("row tiles"): rows are grouped in tiles of
+// 16; within a tile the codes are stored chunk-major, 16 bytes per (chunk,
+// row), so one wave's 64 lanes (16 rows x 4 consecutive chunks) read 1 KiB
+// of contiguous memory with one 128-bit load each:
+//
+//   codes  byte ((tile * CK + c) * 16 + r) * 16 + b   (CK = 16-byte chunks per row)
+//   scales [tile][group][16] float16 bits
+//   zps    [tile][group][16] uint8
+//
+// A chunk holds 32 int4 codes (dword i, nibble j = weight 32c + 8i + j) or 16
+// int8 codes (byte b = weight 16c + b).  Rows past the matrix end (the last
+// tile of a vocabulary of 50257) hold zero codes and zero scales.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "llmq.h"
+
+#define LLMQ_TILE_ROWS 16
+
+struct llmq_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    hipDeviceProp_t prop{};
+};
+
+enum { MAT_QUANT = 0, MAT_GGUF = 1 };
+
+struct llmq_mat {
+    llmq_ctx *ctx = nullptr;
+    int kind = MAT_QUANT;
+    // QuantMatrix
+    int bits = 0, group_param = 0, sym = 0, a16 = 0;
+    int64_t n = 0, k = 0, group = 0;  // rows (outputs), cols (reduction), weights per group
+    int64_t ntiles = 0, CK = 0, NG = 0;
+    uint8_t *codes = nullptr;
+    uint16_t *scales = nullptr;
+    uint8_t *zps = nullptr;
+    // GGUFMatrix
+    int ggml_type = -1;
+    uint8_t *blocks = nullptr;
+    int64_t row_bytes = 0;
+};
+
+struct llmq_kv {
+    llmq_ctx *ctx = nullptr;
+    int n_layer = 0, max_t = 0, n_head = 0, head_dim = 0;
+    int8_t *k = nullptr, *v = nullptr;
+    float *ks = nullptr, *vs = nullptr;
+};
+
+// Error reporting (api.hip).
+int llmq_set_error(int code, const char *fmt, ...);
+#define LLMQ_HIP(call)                                                                         \
+    do {                                                                                       \
+        hipError_t e_ = (call);                                                                \
+        if (e_ != hipSuccess) return llmq_set_error(LLMQ_EHIP, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+#define LLMQ_REQUIRE(cond, ...)                                    \
+    do {                                                           \
+        if (!(cond)) return llmq_set_error(LLMQ_EINVAL, __VA_ARGS__); \
+    } while (0)
+
+// Argmax partial of one workgroup: the largest value and its (smallest) index.
+struct ArgmaxPart {
+    float v;
+    int idx;
+};
+
+// ---------------------------------------------------------------- launchers
+// Each returns LLMQ_OK or an error code (with llmq_set_error).
+
+int launch_quant_weights(llmq_ctx *ctx, llmq_mat *m, const float *dsrc, int64_t rows, int64_t cols, int reduce_rows);
+int launch_quantize_rows(llmq_ctx *ctx, const float *x, int64_t T, int64_t K, int16_t *xq, float *sx);
+
+struct GemvRequest {
+    const llmq_mat *w = nullptr;
+    const float *x = nullptr;  // [T, ldx]
+    int64_t ldx = 0;
+    const float *ln_w = nullptr, *ln_b = nullptr;  // LayerNorm on the input rows when set
+    float *out = nullptr;                          // [T, ldo]
+    int64_t ldo = 0;
+    const float *bias = nullptr;
+    int64_t T = 1;
+    int flags = 0;                 // LLMQ_BIAS | LLMQ_GELU | LLMQ_RESID
+    ArgmaxPart *amax = nullptr;    // per-workgroup argmax partials (T == 1)
+    int amax_cap = 0;              // capacity of amax, in partials
+    int *amax_count = nullptr;     // receives the number of partials written
+    int32_t *dbg = nullptr;        // per-chunk exact integer sums (T == 1, no LN)
+    int16_t *xq_out = nullptr;     // quantized activations of the first token block
+    float *sx_out = nullptr;
+};
+int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq);
+// Number of argmax partials launch_gemv_a16 writes for a T == 1 GEMV of w.
+int gemv_a16_num_parts(const llmq_mat *w);
+
+int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C);
+int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,
+                    int64_t ld);
+int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
+                     const int *pos_dev, int64_t ld);
+
+// Embedding: x[t] = E.dequant_row(token_t) + wpe[pos0 + t] (gpt2t.mojo:378-385,
+// 495-502).  With parts != nullptr the single token is first chosen as the
+// argmax of the previous head (gpt2t.mojo:792-797) from nparts partials,
+// written to gen[state[1]], and state = {pos, step} is advanced.
+int launch_embed(llmq_ctx *ctx, const llmq_mat *E, const float *wpe, const int64_t *tokens, int T, int pos0,
+                 float *x, const ArgmaxPart *parts, int nparts, int64_t *gen, int *state, int do_embed);
+
+// Device helpers.
+__device__ __forceinline__ int llmq_to_int(float r) {
+    // Int(round(v)) for a rounded float, saturating (NaN -> 0), so the code
+    // clamp that follows is defined for every input.
+    if (r != r) return 0;
+    if (r > 1.0e9f) return 1000000000;
+    if (r < -1.0e9f) return -1000000000;
+    return (int)r;
+}

@@ -1,0 +1,167 @@
+"""Host-side mirror of llm_mojo's format traits over libllmq.so.
+
+HipQuantMatrix mirrors QuantMatrix[BITS, GROUP, SYMMETRIC, A16] through the
+WeightMatrix trait (tensor.mojo:49-147, 230-661); QuantKV8 mirrors
+QuantKV[8] through KVCache (kvcache.mojo:31-87, 248-385).  The kernels are
+driven per whole matmul (kernels.linear / head), not per row, and work on
+device buffers (torch tensors or raw addresses).
+"""
+import ctypes
+
+import numpy as np
+
+from ._lib import LLMQ_BIAS, LLMQ_GELU, LLMQ_RESID, check, dptr, hptr, lib
+
+
+class HipQuantMatrix:
+    """A QuantMatrix held on the GPU (values are handles: free() once)."""
+
+    OUT_MAJOR = True
+    FROM_GGUF = False
+
+    def __init__(self, ctx, handle, bits, group, sym, a16):
+        self.ctx, self.h = ctx, handle
+        self.bits, self.group_param, self.sym, self.a16 = bits, group, sym, a16
+        rows, cols = ctypes.c_int64(), ctypes.c_int64()
+        check(lib().llmq_mat_shape(self.h, ctypes.byref(rows), ctypes.byref(cols)))
+        self.rows, self.cols = rows.value, cols.value
+
+    @property
+    def ACT16(self):
+        return self.a16
+
+    def name(self):
+        """QuantMatrix.name (tensor.mojo:325-331)."""
+        g = "ch" if self.group_param == 0 else f"g{self.group_param}"
+        s = f"int{self.bits}-{g}" + ("-sym" if self.sym else "")
+        return s + "-a16" if self.a16 else s
+
+    @classmethod
+    def from_f32(cls, ctx, src, bits, group, sym=False, a16=True, reduce_rows=True):
+        """QuantMatrix.from_f32 (tensor.mojo:334-383), quantized on the GPU.
+        src: a float32 [rows, cols] numpy array (host) or torch tensor (device)."""
+        h = ctypes.c_void_p()
+        if isinstance(src, np.ndarray):
+            src = np.ascontiguousarray(src, np.float32)
+            rows, cols = src.shape
+            check(lib().llmq_mat_from_f32(ctx.h, bits, group, 1 if sym else 0, 1 if a16 else 0, hptr(src), rows,
+                                          cols, 1 if reduce_rows else 0, ctypes.byref(h)))
+        else:
+            rows, cols = src.shape
+            check(lib().llmq_mat_from_f32_device(ctx.h, bits, group, 1 if sym else 0, 1 if a16 else 0, dptr(src),
+                                                 rows, cols, 1 if reduce_rows else 0, ctypes.byref(h)))
+        return cls(ctx, h, bits, group, sym, a16)
+
+    def nbytes(self):
+        return lib().llmq_mat_nbytes(self.h)
+
+    def group_size(self):
+        return lib().llmq_mat_group_size(self.h)
+
+    def has_i16(self):
+        return bool(self.a16)
+
+    def export(self):
+        """(codes, float16 scale bits, zero points) in the reference's own
+        QuantMatrix layout (BLOCKED for int4-g32-a16)."""
+        n, k = self.rows, self.cols
+        g = self.group_size()
+        codes = np.zeros(n * k * self.bits // 8, np.uint8)
+        scales = np.zeros(n * k // g, np.uint16)
+        zps = np.zeros(n * k // g, np.uint8)
+        check(lib().llmq_mat_export(self.ctx.h, self.h, hptr(codes), hptr(scales), hptr(zps)))
+        return codes, scales, zps
+
+    def dequant_row(self, row):
+        dst = np.zeros(self.cols, np.float32)
+        check(lib().llmq_mat_dequant_row(self.ctx.h, self.h, row, hptr(dst)))
+        return dst
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().llmq_mat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def quantize_rows(ctx, x, xq, sx):
+    """kernels.quantize_rows (kernels.mojo:400-416) on device tensors."""
+    T, K = x.shape
+    check(lib().llmq_quantize_rows(ctx.h, dptr(x), T, K, dptr(xq), dptr(sx)))
+
+
+def linear(ctx, out, x, w, bias=None, resid=False, gelu=False, ln=None):
+    """kernels.linear (kernels.mojo:655-673): out (+)= act(x @ w^T + bias);
+    ln=(weight, bias) applies LayerNorm to the input rows first."""
+    T, IN = x.shape
+    flags = (LLMQ_BIAS if bias is not None else 0) | (LLMQ_GELU if gelu else 0) | (LLMQ_RESID if resid else 0)
+    if ln is None:
+        check(lib().llmq_linear(ctx.h, dptr(out), dptr(x), w.h, dptr(bias), T, IN, w.rows, flags))
+    else:
+        check(lib().llmq_ln_linear(ctx.h, dptr(out), dptr(x), dptr(ln[0]), dptr(ln[1]), w.h, dptr(bias), T, IN,
+                                   w.rows, flags))
+
+
+def head(ctx, logits, h, w):
+    """kernels.head (kernels.mojo:676-690): logits[T, V] = h @ w^T."""
+    T, C = h.shape
+    check(lib().llmq_head(ctx.h, dptr(logits), dptr(h), w.h, T, w.rows, C))
+
+
+def layernorm(ctx, out, x, w, b):
+    T, C = x.shape
+    check(lib().llmq_layernorm(ctx.h, dptr(out), dptr(x), dptr(w), dptr(b), T, C))
+
+
+def debug_chunk_sums(ctx, x, w, out, chunk_sums, xq, sx):
+    check(lib().llmq_debug_chunk_sums(ctx.h, dptr(x), w.h, dptr(out), dptr(chunk_sums), dptr(xq), dptr(sx)))
+
+
+class QuantKV8:
+    """QuantKV[8] (kvcache.mojo:248-385) on the GPU."""
+
+    def __init__(self, ctx, n_layer, max_t, n_head, head_dim):
+        self.ctx = ctx
+        self.n_layer, self.max_t, self.n_head, self.head_dim = n_layer, max_t, n_head, head_dim
+        h = ctypes.c_void_p()
+        check(lib().llmq_kv_create(ctx.h, n_layer, max_t, n_head, head_dim, ctypes.byref(h)))
+        self.h = h
+
+    @staticmethod
+    def name():
+        return "int8"
+
+    def nbytes(self):
+        return lib().llmq_kv_nbytes(self.h)
+
+    def store(self, layer, pos0, qkv):
+        """QuantKV.store for every row of qkv [T, 3C] at positions pos0.."""
+        check(lib().llmq_kv_store(self.ctx.h, self.h, layer, pos0, dptr(qkv), qkv.shape[0]))
+
+    def attend(self, out, qkv, layer, pos0):
+        check(lib().llmq_kv_attend(self.ctx.h, self.h, dptr(out), dptr(qkv), layer, qkv.shape[0], pos0))
+
+    def export(self):
+        n = self.n_layer * self.max_t * self.n_head
+        k = np.zeros(n * self.head_dim, np.int8)
+        v = np.zeros(n * self.head_dim, np.int8)
+        ks = np.zeros(n, np.float32)
+        vs = np.zeros(n, np.float32)
+        check(lib().llmq_kv_export(self.ctx.h, self.h, hptr(k), hptr(v), hptr(ks), hptr(vs)))
+        return k, v, ks, vs
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().llmq_kv_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

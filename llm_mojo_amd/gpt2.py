@@ -1,0 +1,110 @@
+"""GPT-2 124M on libllmq.so: the caller of the quantized path
+(gpt2t.mojo Model / load_model / generate, 198-609, 929-1009).
+
+Layers are QuantMatrix[bits, group, sym, A16=True] (int4-g32-a16 by default),
+the tied embedding / head HEAD8_A16, the cache QuantKV[8], all resident on
+one GPU.  Greedy generation runs on the device: each step's argmax picks the
+next token without a round trip to the host.
+"""
+import ctypes
+
+import numpy as np
+
+from ._lib import check, hptr, lib
+
+N_LAYER, N_HEAD, C, HS, MAX_T, V, EOT = 12, 12, 768, 64, 1024, 50257, 50256
+
+# gpt2t.mojo:89-118 names, in the order llmq_gpt2_create takes them
+LAYER_PARAMS = [
+    "ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias", "attn.c_proj.weight",
+    "attn.c_proj.bias", "ln_2.weight", "ln_2.bias", "mlp.c_fc.weight", "mlp.c_fc.bias", "mlp.c_proj.weight",
+    "mlp.c_proj.bias",
+]
+SHAPES = {
+    "wte.weight": (V, C), "wpe.weight": (MAX_T, C), "ln_f.weight": (C,), "ln_f.bias": (C,),
+    "ln_1.weight": (C,), "ln_1.bias": (C,), "attn.c_attn.weight": (C, 3 * C), "attn.c_attn.bias": (3 * C,),
+    "attn.c_proj.weight": (C, C), "attn.c_proj.bias": (C,), "ln_2.weight": (C,), "ln_2.bias": (C,),
+    "mlp.c_fc.weight": (C, 4 * C), "mlp.c_fc.bias": (4 * C,), "mlp.c_proj.weight": (4 * C, C),
+    "mlp.c_proj.bias": (C,),
+}
+
+
+def param_names():
+    names = ["wte.weight", "wpe.weight", "ln_f.weight", "ln_f.bias"]
+    for l in range(N_LAYER):
+        names += [f"h.{l}.{p}" for p in LAYER_PARAMS]
+    return names
+
+
+def param_shape(name):
+    return SHAPES[name.split(".", 2)[2] if name.startswith("h.") else name]
+
+
+def params_list(tensors):
+    """The tensors of a {name: array} dict in param_names() order, checked."""
+    out = []
+    for name in param_names():
+        a = np.ascontiguousarray(tensors[name], np.float32)
+        if a.shape != param_shape(name):
+            raise ValueError(f"{name}: shape {a.shape}, expected {param_shape(name)}")
+        out.append(a)
+    return out
+
+
+def load_safetensors(path):
+    """Hugging Face GPT-2 float32 safetensors -> {name: array} (gpt2t.mojo
+    read_safetensors / tensor, with the same names)."""
+    from safetensors.numpy import load_file
+
+    return load_file(path)
+
+
+class GPT2:
+    """Model[W = QuantMatrix[bits, group, sym, A16], E = HEAD8_A16, KV = QuantKV[8]]."""
+
+    def __init__(self, ctx, tensors, bits=4, group=32, sym=False):
+        self.ctx = ctx
+        params = params_list(tensors)
+        arr = (ctypes.c_void_p * len(params))(*[p.ctypes.data for p in params])
+        h = ctypes.c_void_p()
+        check(lib().llmq_gpt2_create(ctx.h, arr, bits, group, 1 if sym else 0, ctypes.byref(h)))
+        self.h = h
+        self.bits, self.group, self.sym = bits, group, sym
+
+    def name(self):
+        """model_name (gpt2t.mojo:1222-1228)."""
+        g = "ch" if self.group == 0 else f"g{self.group}"
+        w = f"int{self.bits}-{g}" + ("-sym" if self.sym else "") + "-a16"
+        return w + "+head-int8-ch-a16+kv-int8"
+
+    def weight_bytes(self):
+        return lib().llmq_gpt2_weight_bytes(self.h)
+
+    def forward(self, tokens, pos0):
+        """Model.forward: the last token's logits [V] (host)."""
+        toks = np.ascontiguousarray(tokens, np.int64)
+        logits = np.zeros(V, np.float32)
+        check(lib().llmq_gpt2_forward(self.h, hptr(toks), len(toks), pos0, hptr(logits)))
+        return logits
+
+    def generate(self, prompt, steps):
+        """Greedy generate (-t 0): (tokens, prefill_ms, decode_ms) with the
+        reference's timing spans (gpt2t.mojo:949-1005)."""
+        prompt = np.ascontiguousarray(prompt, np.int64)
+        out = np.zeros(max(steps, 1), np.int64)
+        n = ctypes.c_int()
+        pm, dm = ctypes.c_double(), ctypes.c_double()
+        check(lib().llmq_gpt2_generate(self.h, hptr(prompt), len(prompt), steps, hptr(out), ctypes.byref(n),
+                                       ctypes.byref(pm), ctypes.byref(dm)))
+        return out[:n.value], pm.value, dm.value
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().llmq_gpt2_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -1,0 +1,94 @@
+"""Seeded synthetic inputs of the benchmark configurations (no network, no
+real checkpoints): GPT-2 124M random-init weights written as a Hugging Face
+layout safetensors file, and random prompt ids.
+
+Normals come from SplitMix64 (the published 64-bit mixer of Steele, Lea and
+Flood) through Box-Muller in float64, cast to float32; one stream per tensor,
+seeded by (seed, tensor index), so any tensor can be regenerated alone.
+Prompt ids use llm_mojo's own Rng (xorshift64*, gpt2t.mojo:777-789) as
+floor(uniform * 50257).
+"""
+import os
+
+import numpy as np
+
+from .gpt2 import C, MAX_T, V, param_names, param_shape
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def splitmix64(seed, n, start=0):
+    """n outputs of SplitMix64 seeded with `seed`, from position `start`."""
+    with np.errstate(over="ignore"):
+        i = np.arange(start + 1, start + n + 1, dtype=np.uint64)
+        z = np.uint64(seed) + i * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def normal(seed, n, std=1.0):
+    """n float32 samples of N(0, std^2) (Box-Muller on pairs of uniforms
+    from the top 53 bits)."""
+    m = (n + 1) // 2
+    out = np.empty(2 * m, np.float32)
+    step = 1 << 22
+    for s in range(0, m, step):
+        k = min(step, m - s)
+        z = splitmix64(seed, 2 * k, 2 * s)
+        u = (z >> np.uint64(11)).astype(np.float64) * (1.0 / (1 << 53))
+        u1 = 1.0 - u[0::2]  # (0, 1]
+        u2 = u[1::2]
+        r = np.sqrt(-2.0 * np.log(u1)) * std
+        out[2 * s:2 * (s + k):2] = (r * np.cos(2 * np.pi * u2)).astype(np.float32)
+        out[2 * s + 1:2 * (s + k):2] = (r * np.sin(2 * np.pi * u2)).astype(np.float32)
+    return out[:n]
+
+
+def gpt2_tensors(seed=1337, std=0.02):
+    """{name: float32 array}: weights N(0, std), biases 0, LayerNorm gain 1."""
+    out = {}
+    for i, name in enumerate(param_names()):
+        shape = param_shape(name)
+        if name.endswith(".bias"):
+            out[name] = np.zeros(shape, np.float32)
+        elif name.startswith("ln") or ".ln_" in name:
+            out[name] = np.ones(shape, np.float32)
+        else:
+            out[name] = normal(seed * 1000003 + i, int(np.prod(shape)), std).reshape(shape)
+    return out
+
+
+def gpt2_safetensors(path, seed=1337):
+    """Writes (once) and returns the path of the synthetic checkpoint."""
+    if not os.path.exists(path):
+        from safetensors.numpy import save_file
+
+        tmp = path + ".tmp"
+        save_file(gpt2_tensors(seed), tmp)
+        os.replace(tmp, path)
+    return path
+
+
+class Rng:
+    """gpt2t.mojo Rng (777-789): xorshift64*, uniform floats in [0, 1)."""
+
+    def __init__(self, seed):
+        self.state = (seed * 0x9E3779B97F4A7C15 + 1) & 0xFFFFFFFFFFFFFFFF
+
+    def uniform(self):
+        s = self.state
+        s ^= s >> 12
+        s ^= (s << 25) & 0xFFFFFFFFFFFFFFFF
+        s ^= s >> 27
+        self.state = s
+        r = ((s * 0x2545F4914F6CDD1D) & 0xFFFFFFFFFFFFFFFF) >> 40
+        return np.float32(r) / np.float32(1 << 24)
+
+
+def prompt_ids(seed, n):
+    rng = Rng(seed)
+    return np.array([min(V - 1, int(rng.uniform() * V)) for _ in range(n)], np.int64)
+
+
+__all__ = ["splitmix64", "normal", "gpt2_tensors", "gpt2_safetensors", "Rng", "prompt_ids", "C", "MAX_T", "V"]

@@ -67,6 +67,18 @@ def gemv_roofline(torch, lm, ctx, K=4096, N=11008, nbuf=36, reps=360):
             "buffers": nbuf, "gbs": alg / us / 1e3}
 
 
+def measured_traffic():
+    """HBM bytes per launch of the roofline GEMV from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/), scaled by what the
+    same counters read for a 1 GiB copy; None if absent."""
+    p = os.path.join(HERE, "profiles", "gemv_a16_int4_g32_4096x11008.traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def copy_bandwidth(torch, nbytes=1 << 30, reps=20):
     """Device-to-device copy bandwidth (read + write bytes), for scale."""
     a = torch.empty(nbytes // 4, device="cuda")
@@ -118,6 +130,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the roofline GEMV and the reference copy (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -131,6 +145,11 @@ def main():
     from llm_mojo_amd import synth
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.roofline_only:
+        ctx = lm.Context(0)
+        r = gemv_roofline(torch, lm, ctx)
+        print(json.dumps({"roofline_kernel": r, "copy_gbs": round(copy_bandwidth(torch), 1)}), flush=True)
+        return
     log("generating synthetic GPT-2 weights")
     tensors = synth.gpt2_tensors(SEED)
     prompt = synth.prompt_ids(SEED, PROMPT)
@@ -159,7 +178,7 @@ def main():
     if not args.no_roofline:
         r = gemv_roofline(torch, lm, ctx)
         roof = {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
+                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic()}
         extra["roofline_kernel"] = r
         extra["copy_gbs"] = round(copy_bandwidth(torch), 1)
         log("gemv", r, "copy GB/s", extra["copy_gbs"])

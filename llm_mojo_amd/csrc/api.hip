@@ -117,7 +117,11 @@ static int mat_alloc_quant(llmq_ctx *ctx, int bits, int group, int sym, int a16,
     m->ntiles = (n + LLMQ_TILE_ROWS - 1) / LLMQ_TILE_ROWS;
     m->CK = k * bits / 8 / 16;
     m->NG = k / g;
-    const size_t cb = (size_t)m->ntiles * m->CK * 256, gb = (size_t)m->ntiles * m->NG * LLMQ_TILE_ROWS;
+    // Readable padding after codes, scales and zero points: the GEMV reads up
+    // to LLMQ_PAD_CHUNKS chunks (and their groups) past a tile's end instead
+    // of branching around the loads.
+    const size_t cb = (size_t)(m->ntiles * m->CK + LLMQ_PAD_CHUNKS) * 256,
+                 gb = (size_t)(m->ntiles * m->NG + LLMQ_PAD_CHUNKS) * LLMQ_TILE_ROWS;
     if (hipMalloc(&m->codes, cb) != hipSuccess || hipMalloc(&m->scales, gb * 2) != hipSuccess ||
         hipMalloc(&m->zps, gb) != hipSuccess) {
         hipFree(m->codes);
@@ -411,7 +415,7 @@ int llmq_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const float *
 
 int llmq_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0) {
     LLMQ_REQUIRE(ctx, "kv_attend: null context");
-    return launch_kv_attend(ctx, kv, out, qkv, layer, T, pos0, nullptr, 0);
+    return launch_kv_attend(ctx, kv, out, qkv, layer, T, pos0, nullptr, 0, false);
 }
 
 int llmq_kv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, float *ks, float *vs) {
@@ -498,8 +502,8 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step) {
         q.T = T;
         q.flags = LLMQ_BIAS;
         RC(launch_gemv_a16(ctx, q));
-        RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
-        RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, pos_dev, 3 * C));
+        if (T > 1) RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
+        RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, pos_dev, 3 * C, T == 1));
         GemvRequest p;
         p.w = w[1];
         p.x = m->att;

@@ -47,43 +47,128 @@ __global__ __launch_bounds__(64) void kv_store_kernel(const float *__restrict__ 
 // Scores: q . k over head_dim, times the key's scale, times 1/sqrt(hd); softmax
 // with the running maximum; out = sum_s (p_s * vs_s) * v_s.  The summation
 // order differs from the reference's sequential one (fp32 rounding only).
+//
+// The thread that scores position s also copies that position's value row
+// and scale into LDS (STAGE), so the value pass reads no global memory.  With
+// STORE (one token per launch: decode) the workgroup first quantizes its
+// head's new key and value (QuantKV.store, kvcache.mojo:333-342), writes them
+// to the cache, and uses them from LDS for the current position.
 constexpr int kAttnThreads = 256;
+
+// Workgroup barrier ordering LDS only (global loads stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int HD, bool STAGE, bool STORE>
 __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__restrict__ qkv, int64_t ld, int C,
                                                                  int pos0, const int *__restrict__ pos_dev,
-                                                                 int layer, int max_t, int n_head, int hd,
-                                                                 const int8_t *__restrict__ K8,
-                                                                 const int8_t *__restrict__ V8,
-                                                                 const float *__restrict__ KS,
-                                                                 const float *__restrict__ VS,
+                                                                 int layer, int max_t, int n_head,
+                                                                 int8_t *__restrict__ K8, int8_t *__restrict__ V8,
+                                                                 float *__restrict__ KS, float *__restrict__ VS,
                                                                  float *__restrict__ out, int64_t ldo) {
-    extern __shared__ float sm[];
-    float *q = sm;              // [hd]
-    float *scores = sm + hd;    // [npos]
+    constexpr int NV = HD / 16;  // 16-byte pieces of a row
+    extern __shared__ __align__(16) float sm[];
+    float *q = sm;                // [HD]
+    float *scores = q + HD;       // [max_t]
+    float *vsc = scores + max_t;  // [max_t]  value scales (STAGE)
+    // [max_t][HD] value codes (STAGE), 16-byte aligned for the int4 copies
+    int8_t *vrow = reinterpret_cast<int8_t *>((reinterpret_cast<uintptr_t>(vsc + max_t) + 15) & ~(uintptr_t)15);
     __shared__ float red[kAttnThreads];
-    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    __shared__ __align__(16) int8_t knew[HD];
+    __shared__ float kscale_new;
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int npos = (pos_dev ? *pos_dev : pos0) + t + 1;
-    const float scale = 1.0f / sqrtf((float)hd);
-    for (int i = tid; i < hd; i += kAttnThreads) q[i] = qkv[(int64_t)t * ld + (int64_t)h * hd + i];
-    __syncthreads();
+    const int cur = npos - 1;
+    const float scale = 1.0f / sqrtf((float)HD);
     const int64_t base = (int64_t)layer * max_t * n_head + h;  // slot of position 0
+
+    // The rows of this thread's first position, requested before anything
+    // else (positions past the end re-read the last one and are not used).
+    int4 kr[NV], vr[NV];
+    float ksr, vsr;
+    auto load_row = [&](int s) {
+        const int64_t sl = base + (int64_t)s * n_head;
+        const int4 *kp = reinterpret_cast<const int4 *>(K8 + sl * HD);
+        const int4 *vp = reinterpret_cast<const int4 *>(V8 + sl * HD);
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            kr[i] = kp[i];
+            if (STAGE) vr[i] = vp[i];
+        }
+        ksr = KS[sl];
+        if (STAGE) vsr = VS[sl];
+    };
+    load_row(tid < npos ? tid : cur);
+    __builtin_amdgcn_sched_barrier(0);
+
+    for (int i = tid; i < HD; i += kAttnThreads) q[i] = qkv[(int64_t)t * ld + (int64_t)h * HD + i];
+    if (STORE && (wid == 1 || wid == 2)) {
+        // QuantKV.store for this head (kvcache.mojo:320-342)
+        const int kv = wid - 1;
+        const float *src = qkv + (int64_t)t * ld + (int64_t)(1 + kv) * C + (int64_t)h * HD;
+        float xs[HD / 64];
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < HD / 64; e++) {
+            xs[e] = src[lane + 64 * e];
+            m = fmaxf(m, fabsf(xs[e]));
+        }
+        m = wave_max(m);
+        float sc = m / 127.0f;
+        if (sc == 0.0f) sc = 1.0f;
+        const float inv = 1.0f / sc;
+        const int64_t sl = base + (int64_t)cur * n_head;
+#pragma unroll
+        for (int e = 0; e < HD / 64; e++) {
+            const int i = lane + 64 * e;
+            const int8_t code = (int8_t)llmq_to_int(roundf(xs[e] * inv));
+            (kv ? V8 : K8)[sl * HD + i] = code;
+            if (kv == 0)
+                knew[i] = code;
+            else if (STAGE)
+                vrow[(int64_t)cur * HD + i] = code;
+        }
+        if (lane == 0) {
+            (kv ? VS : KS)[sl] = sc;
+            if (kv == 0)
+                kscale_new = sc;
+            else if (STAGE)
+                vsc[cur] = sc;
+        }
+    }
+    lds_barrier();
+
     float mx = -INFINITY;
     for (int s = tid; s < npos; s += kAttnThreads) {
-        const int64_t sl = base + (int64_t)s * n_head;
-        const int8_t *kp = K8 + sl * hd;
-        float d = 0.0f;
-        for (int i = 0; i < hd; i += 16) {
-            const int4 w = *reinterpret_cast<const int4 *>(kp + i);
-            const int8_t *b = reinterpret_cast<const int8_t *>(&w);
+        if (s != tid) load_row(s);  // only past 256 positions
+        const bool fresh = STORE && s == cur;
+        if (fresh) {
 #pragma unroll
-            for (int e = 0; e < 16; e++) d = fmaf(q[i + e], (float)b[e], d);
+            for (int i = 0; i < NV; i++) kr[i] = *reinterpret_cast<const int4 *>(knew + 16 * i);
+            ksr = kscale_new;
         }
-        const float sc = d * KS[sl] * scale;
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int8_t *b = reinterpret_cast<const int8_t *>(&kr[i]);
+#pragma unroll
+            for (int e = 0; e < 16; e++) d = fmaf(q[16 * i + e], (float)b[e], d);
+        }
+        if (STAGE && !fresh) {
+#pragma unroll
+            for (int i = 0; i < NV; i++) *reinterpret_cast<int4 *>(vrow + (int64_t)s * HD + 16 * i) = vr[i];
+            vsc[s] = vsr;
+        }
+        const float sc = d * ksr * scale;
         scores[s] = sc;
         mx = fmaxf(mx, sc);
     }
     mx = wave_max(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
+    lds_barrier();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float tot = 0.0f;
     for (int s = tid; s < npos; s += kAttnThreads) {
@@ -92,27 +177,31 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
         tot += e;
     }
     tot = wave_sum(tot);
-    __syncthreads();
+    lds_barrier();
     if ((tid & 63) == 0) red[tid >> 6] = tot;
-    __syncthreads();
+    lds_barrier();
     const float total = ((red[0] + red[1]) + red[2]) + red[3];
-    __syncthreads();
+    lds_barrier();
     // out[i]: threads split positions into `parts` interleaved subsets.
-    const int parts = kAttnThreads / hd;  // hd divides 256
-    const int i = tid % hd, part = tid / hd;
+    constexpr int parts = kAttnThreads / HD;
+    const int i = tid % HD, part = tid / HD;
     float acc = 0.0f;
     for (int s = part; s < npos; s += parts) {
-        const int64_t sl = base + (int64_t)s * n_head;
         const float p = scores[s] / total;
-        const float ps = p * VS[sl];
-        acc = fmaf(ps, (float)V8[sl * hd + i], acc);
+        if (STAGE) {
+            acc = fmaf(p * vsc[s], (float)vrow[(int64_t)s * HD + i], acc);
+        } else {
+            const int64_t sl = base + (int64_t)s * n_head;
+            acc = fmaf(p * VS[sl], (float)V8[sl * HD + i], acc);
+        }
     }
     red[tid] = acc;
-    __syncthreads();
+    lds_barrier();
     if (part == 0) {
         float v = 0.0f;
-        for (int pp = 0; pp < parts; pp++) v += red[pp * hd + i];
-        out[(int64_t)t * ldo + (int64_t)h * hd + i] = v;
+#pragma unroll
+        for (int pp = 0; pp < parts; pp++) v += red[pp * HD + i];
+        out[(int64_t)t * ldo + (int64_t)h * HD + i] = v;
     }
 }
 
@@ -238,20 +327,54 @@ int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *
     return LLMQ_OK;
 }
 
+template <int HD, bool STAGE, bool STORE>
+static int attend_launch(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
+                         const int *pos_dev, int64_t ld, size_t lds) {
+    const int C = kv->n_head * kv->head_dim;
+    hipLaunchKernelGGL((kv_attend_kernel<HD, STAGE, STORE>), dim3(kv->n_head, T), dim3(kAttnThreads), lds, ctx->stream,
+                       qkv, ld ? ld : 3 * C, C, pos0, pos_dev, layer, kv->max_t, kv->n_head, kv->k, kv->v, kv->ks,
+                       kv->vs, out, (int64_t)C);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+// Raises a kernel's dynamic LDS limit to `bytes` once; false if the device
+// does not allow that much.
+template <int HD, bool STAGE, bool STORE>
+static bool allow_lds(size_t bytes) {
+    static size_t granted = 64 * 1024;
+    if (bytes <= granted) return true;
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&kv_attend_kernel<HD, STAGE, STORE>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    granted = bytes;
+    return true;
+}
+
+template <int HD>
+static int attend_hd(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
+                     const int *pos_dev, int64_t ld, bool store) {
+    const size_t base = sizeof(float) * ((size_t)HD + kv->max_t);
+    const size_t staged = base + (size_t)kv->max_t * (sizeof(float) + HD) + 16;
+    if (store && allow_lds<HD, true, true>(staged))
+        return attend_launch<HD, true, true>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, staged);
+    if (!store && allow_lds<HD, true, false>(staged))
+        return attend_launch<HD, true, false>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, staged);
+    return store ? attend_launch<HD, false, true>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, base)
+                 : attend_launch<HD, false, false>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, base);
+}
+
 int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
-                     const int *pos_dev, int64_t ld) {
+                     const int *pos_dev, int64_t ld, bool store) {
     LLMQ_REQUIRE(kv && qkv && out && T >= 1, "kv_attend: bad arguments");
     LLMQ_REQUIRE(layer >= 0 && layer < kv->n_layer, "kv_attend: layer %d out of range", layer);
     LLMQ_REQUIRE(pos_dev || (pos0 >= 0 && pos0 + T <= kv->max_t), "kv_attend: positions beyond max_t");
-    LLMQ_REQUIRE(kv->head_dim % 16 == 0 && 256 % kv->head_dim == 0, "kv_attend: head_dim %d unsupported",
-                 kv->head_dim);
-    const int C = kv->n_head * kv->head_dim;
-    const size_t lds = sizeof(float) * ((size_t)kv->head_dim + kv->max_t);
-    hipLaunchKernelGGL(kv_attend_kernel, dim3(kv->n_head, T), dim3(kAttnThreads), lds, ctx->stream, qkv,
-                       ld ? ld : 3 * C, C, pos0, pos_dev, layer, kv->max_t, kv->n_head, kv->head_dim, kv->k, kv->v,
-                       kv->ks, kv->vs, out, (int64_t)C);
-    LLMQ_HIP(hipGetLastError());
-    return LLMQ_OK;
+    LLMQ_REQUIRE(!store || T == 1, "kv_attend: the fused store takes one token");
+    if (kv->head_dim == 64) return attend_hd<64>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
+    if (kv->head_dim == 128) return attend_hd<128>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
+    return llmq_set_error(LLMQ_EUNSUPPORTED, "kv_attend: head_dim %d (64 or 128)", kv->head_dim);
 }
 
 int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C) {

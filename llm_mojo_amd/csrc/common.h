@@ -23,6 +23,10 @@
 #include "llmq.h"
 
 #define LLMQ_TILE_ROWS 16
+// Chunks (of 16 rows x 16 bytes) of readable padding after a matrix's codes,
+// and groups (of 16 rows) after its scales and zero points: covers the GEMV's
+// look-ahead of up to 8 steps x 4 chunks past the last tile.
+#define LLMQ_PAD_CHUNKS 64
 
 struct llmq_ctx {
     int device = 0;
@@ -104,8 +108,9 @@ int gemv_a16_num_parts(const llmq_mat *w);
 int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C);
 int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,
                     int64_t ld);
+// store: also quantize and store the token's key and value (T == 1).
 int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
-                     const int *pos_dev, int64_t ld);
+                     const int *pos_dev, int64_t ld, bool store);
 
 // Embedding: x[t] = E.dequant_row(token_t) + wpe[pos0 + t] (gpt2t.mojo:378-385,
 // 495-502).  With parts != nullptr the single token is first chosen as the

@@ -32,13 +32,13 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPrefetch = 4;  // steps of code loads kept in flight per lane
+constexpr int kSteps = 8;  // code steps per wave whose loads are all issued before the first use
 
 struct GemvArgs {
     const uint4 *codes;
     const uint16_t *scales;
     const uint8_t *zps;
-    int n, K, ntiles, CK, NG, CPG, T, ks, flags;
+    int n, K, ntiles, CK, NG, cpg_shift, T, ks, flags;  // group of chunk c: c >> cpg_shift
     int64_t ldx, ldo;
     const float *x, *ln_w, *ln_b, *bias;
     float *out;
@@ -58,19 +58,27 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;
 }
+// Workgroup barrier that orders LDS only: global loads issued before it stay
+// in flight (the weight stream overlaps the prologue).  Nothing in these
+// kernels communicates through global memory inside a launch.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 // Sum / max over the 256 threads; every thread gets the same bits.
 __device__ __forceinline__ float block_sum(float v, float *red) {
     v = wave_sum(v);
-    __syncthreads();
+    lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
+    lds_barrier();
     return ((red[0] + red[1]) + red[2]) + red[3];
 }
 __device__ __forceinline__ float block_max(float v, float *red) {
     v = wave_max(v);
-    __syncthreads();
+    lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
+    lds_barrier();
     return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
@@ -86,66 +94,87 @@ __device__ __forceinline__ float gelu_f(float r) {
     return h * (1.0f + th);
 }
 
-// One token row: optional LayerNorm (kernels.mojo:179-197), quantize_rows
-// (kernels.mojo:400-416), then the activation planes and per-chunk sums.
-template <int BITS, bool LN>
-__device__ void prep_token(const GemvArgs &a, const float *__restrict__ xr, uint32_t *xpl, int *xsum, float *red,
-                           float &s_out, int16_t *xq_dbg) {
-    const int K = a.K, tid = threadIdx.x;
+// Activations of one token row in registers: unit u = tid + 256 * i holds
+// VPT consecutive values (one plane dword of the int4 / int8 layout).
+template <int VPT, int UPT>
+__device__ __forceinline__ void load_units(const float *__restrict__ xr, int nunits, float (&v)[UPT][VPT]) {
     const float4 *x4 = reinterpret_cast<const float4 *>(xr);
-    float mean = 0.0f, rstd = 1.0f;
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = threadIdx.x + kThreads * i;
+        const bool ok = u < nunits;
+        const int uc = ok ? u : 0;  // always a valid address: no branch around the load
+#pragma unroll
+        for (int h = 0; h < VPT / 4; h++) {
+            const float4 f = x4[uc * (VPT / 4) + h];
+            v[i][4 * h] = ok ? f.x : 0.0f;
+            v[i][4 * h + 1] = ok ? f.y : 0.0f;
+            v[i][4 * h + 2] = ok ? f.z : 0.0f;
+            v[i][4 * h + 3] = ok ? f.w : 0.0f;
+        }
+    }
+}
+
+// One token row, from registers: optional LayerNorm (kernels.mojo:179-197),
+// quantize_rows (kernels.mojo:400-416), then the activation planes and
+// per-chunk sums into LDS.  Returns the row's scale sx.
+template <int BITS, int UPT, bool LN>
+__device__ float prep_token(const GemvArgs &a, float (&v)[UPT][BITS == 4 ? 8 : 4],
+                            const float (&lw)[UPT][BITS == 4 ? 8 : 4], const float (&lb)[UPT][BITS == 4 ? 8 : 4],
+                            uint32_t *xpl, int *xsum, float *red, int16_t *xq_dbg) {
+    constexpr int VPT = BITS == 4 ? 8 : 4;  // activations per unit (one plane dword)
+    constexpr int PD = BITS == 4 ? 16 : 8;  // plane dwords per chunk
+    const int K = a.K, nunits = K / VPT, tid = threadIdx.x;
     if (LN) {
         float sum = 0.0f;
-        for (int i = tid; i < K / 4; i += kThreads) {
-            float4 v = x4[i];
-            sum += ((v.x + v.y) + v.z) + v.w;
-        }
-        mean = block_sum(sum, red) / (float)K;
+#pragma unroll
+        for (int i = 0; i < UPT; i++)
+#pragma unroll
+            for (int e = 0; e < VPT; e++) sum += v[i][e];  // padding units hold zeros
+        const float mean = block_sum(sum, red) / (float)K;
         float sq = 0.0f;
-        for (int i = tid; i < K / 4; i += kThreads) {
-            float4 v = x4[i];
-            float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
-            sq += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            if (tid + kThreads * i >= nunits) continue;
+#pragma unroll
+            for (int e = 0; e < VPT; e++) {
+                float d = v[i][e] - mean;
+                sq += d * d;
+            }
         }
-        float var = block_sum(sq, red) / (float)K;
-        rstd = 1.0f / sqrtf(var + 1e-5f);
+        const float var = block_sum(sq, red) / (float)K;
+        const float rstd = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+        for (int i = 0; i < UPT; i++)
+#pragma unroll
+            for (int e = 0; e < VPT; e++) {
+                float nn = (v[i][e] - mean) * rstd;
+                v[i][e] = nn * lw[i][e] + lb[i][e];
+            }
     }
-    auto xn = [&](int i, float v) -> float {
-        if (!LN) return v;
-        float nn = (v - mean) * rstd;
-        return nn * a.ln_w[i] + a.ln_b[i];
-    };
     float m = 0.0f;
-    for (int i = tid; i < K / 4; i += kThreads) {
-        float4 v = x4[i];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(xn(4 * i, v.x)), fabsf(xn(4 * i + 1, v.y))),
-                           fmaxf(fabsf(xn(4 * i + 2, v.z)), fabsf(xn(4 * i + 3, v.w)))));
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        if (tid + kThreads * i >= nunits) continue;
+#pragma unroll
+        for (int e = 0; e < VPT; e++) m = fmaxf(m, fabsf(v[i][e]));
     }
     m = block_max(m, red);
     float s = m / 32767.0f;
     if (s == 0.0f) s = 1.0f;
     const float inv = 1.0f / s;
-    s_out = s;
-    constexpr int VPT = BITS == 4 ? 8 : 4;  // activations per thread per step (one plane dword)
-    constexpr int PD = BITS == 4 ? 16 : 8;  // plane dwords per chunk
-    for (int g = tid; g < K / VPT; g += kThreads) {
-        float vals[VPT];
 #pragma unroll
-        for (int h = 0; h < VPT / 4; h++) {
-            float4 v = x4[g * (VPT / 4) + h];
-            vals[4 * h] = v.x;
-            vals[4 * h + 1] = v.y;
-            vals[4 * h + 2] = v.z;
-            vals[4 * h + 3] = v.w;
-        }
+    for (int i = 0; i < UPT; i++) {
+        const int u = tid + kThreads * i;
+        if (u >= nunits) continue;  // whole groups of four units drop out together
         uint32_t p[4] = {0, 0, 0, 0};
         int qs = 0;
 #pragma unroll
         for (int e = 0; e < VPT; e++) {
-            int q = llmq_to_int(roundf(xn(g * VPT + e, vals[e]) * inv));
-            if (xq_dbg) xq_dbg[g * VPT + e] = (int16_t)q;
+            const int q = llmq_to_int(roundf(v[i][e] * inv));
+            if (xq_dbg) xq_dbg[u * VPT + e] = (int16_t)q;
             qs += q;
-            uint32_t X = (uint32_t)(q + 32768);
+            const uint32_t X = (uint32_t)(q + 32768);
             if (BITS == 4) {
                 p[0] |= (X & 15u) << (4 * e);
                 p[1] |= ((X >> 4) & 15u) << (4 * e);
@@ -156,26 +185,28 @@ __device__ void prep_token(const GemvArgs &a, const float *__restrict__ xr, uint
                 p[1] |= (X >> 8) << (8 * e);
             }
         }
-        const int c = g >> 2, i = g & 3;  // four threads fill one chunk
+        const int c = u >> 2, ii = u & 3;  // four units fill one chunk
 #pragma unroll
-        for (int pl = 0; pl < PD / 4; pl++) xpl[c * PD + pl * 4 + i] = p[pl];
+        for (int pl = 0; pl < PD / 4; pl++) xpl[c * PD + pl * 4 + ii] = p[pl];
         qs += __shfl_xor(qs, 1);
         qs += __shfl_xor(qs, 2);
-        if (i == 0) xsum[c] = qs;
+        if (ii == 0) xsum[c] = qs;
     }
+    return s;
 }
 
-template <int BITS, int MT, bool LN, bool PERCH, bool DBG>
-__global__ __launch_bounds__(kThreads) void gemv_a16_kernel(GemvArgs a) {
+template <int BITS, int MT, bool LN, bool DBG, int UPT, bool LOOP>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gemv_a16_kernel(GemvArgs a) {
+    constexpr int VPT = BITS == 4 ? 8 : 4;
     constexpr int PD = BITS == 4 ? 16 : 8;
-    extern __shared__ uint32_t smem[];
+    extern __shared__ __align__(16) uint32_t smem[];
     __shared__ float part[4 * MT * 16];
     __shared__ float pre_red[4];
     __shared__ float s_sx[MT];
     __shared__ ArgmaxPart s_best[4];
 
     const int CK = a.CK;
-    uint32_t *xpl = smem;                                // [MT][CK][PD]
+    uint32_t *xpl = smem;                                      // [MT][CK][PD]
     int *xsum = reinterpret_cast<int *>(smem + MT * CK * PD);  // [MT][CK]
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int tpw = 4 / a.ks;
@@ -185,73 +216,95 @@ __global__ __launch_bounds__(kThreads) void gemv_a16_kernel(GemvArgs a) {
     const int s0 = (S * kpart) / a.ks, s1 = (S * (kpart + 1)) / a.ks;
     const int r = lane & 15, j = lane >> 4;
     const bool tile_ok = tile < a.ntiles;
-    const uint4 *cb = a.codes + (size_t)tile * CK * 16 + r;
-    const size_t sbase = (size_t)tile * a.NG * 16 + r;
+    const int o = tile * 16 + r;
+    const bool row_ok = tile_ok && o < a.n;
+    const int tb = blockIdx.y, tok0 = tb * MT;
+    const int nunits = a.K / VPT;
 
-    uint4 buf[kPrefetch];
-    uint32_t bsc[kPrefetch], bzp[kPrefetch];
-    auto fetch = [&](int s, uint4 &d, uint32_t &sc, uint32_t &zp) {
-        const int c = 4 * s + j;
-        if (tile_ok && s < s1 && c < CK) {
-            d = cb[(size_t)c * 16];
-            if (!PERCH) {
-                const size_t gi = sbase + (size_t)(c / a.CPG) * 16;
-                sc = a.scales[gi];
-                zp = a.zps[gi];
-            }
-        } else {
-            d = make_uint4(0, 0, 0, 0);
-            sc = 0;
-            zp = 0;
+    // 1. Everything the epilogue reads, and the first token's activations,
+    //    are requested first: nothing later waits behind the weight stream.
+    const int oc = row_ok ? o : 0;  // clamped row: loads need no branch
+    float e_bias = 0.0f, e_res = 0.0f;
+    if (MT == 1) {
+        e_bias = a.bias[oc];  // a.bias is valid memory even without LLMQ_BIAS
+        e_res = a.out[(size_t)tok0 * a.ldo + oc];
+    }
+    float xv[UPT][VPT], lw[UPT][VPT], lb[UPT][VPT];
+    load_units<VPT, UPT>(a.x + (size_t)tok0 * a.ldx, nunits, xv);
+    if (LN) {
+        load_units<VPT, UPT>(a.ln_w, nunits, lw);
+        load_units<VPT, UPT>(a.ln_b, nunits, lb);
+    }
+
+    // 2. The wave's code chunks (up to kSteps steps), scales and zero points.
+    //    Loads are never behind a branch and use 32-bit offsets from the
+    //    matrix base, so the compiler counts them precisely and waits for
+    //    each only where it is used.  Steps past the wave's range read the
+    //    padding that follows every matrix (pad_chunks) and get scale 0.
+    const int tile_c = tile_ok ? tile : 0;
+    const uint32_t code_lane = ((uint32_t)tile_c * CK * 16u + (uint32_t)j * 16u + (uint32_t)r);  // in uint4
+    const uint32_t grp_lane = (uint32_t)tile_c * a.NG * 16u + (uint32_t)r;
+    uint4 wc[kSteps];
+    uint32_t wsc[kSteps], wzp[kSteps];
+    auto fetch = [&](int sb) {
+#pragma unroll
+        for (int u = 0; u < kSteps; u++) {
+            const uint32_t s = (uint32_t)(sb + u);
+            wc[u] = a.codes[code_lane + s * 64u];
+            const uint32_t gi = grp_lane + ((4u * s + (uint32_t)j) >> a.cpg_shift) * 16u;
+            wsc[u] = a.scales[gi];
+            wzp[u] = a.zps[gi];
         }
     };
-#pragma unroll
-    for (int u = 0; u < kPrefetch; u++) fetch(s0 + u, buf[u], bsc[u], bzp[u]);
-    float psc = 0.0f;
-    int pzp = 0;
-    if (PERCH && tile_ok) {
-        psc = __half2float(__ushort_as_half(a.scales[sbase]));
-        pzp = a.zps[sbase];
-    }
+    // Issue order matters: the prologue needs x before any weight has
+    // arrived, and vmcnt counts completions in issue order.
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(s0);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // Prologue: the token block's activations, quantized, into LDS.
-    const int tb = blockIdx.y;
-    for (int t = 0; t < MT; t++) {
-        const int tok = tb * MT + t;
-        if (tok < a.T) {
-            float s;
-            int16_t *dbgq = (a.xq_out && blockIdx.x == 0) ? a.xq_out + (size_t)tok * a.K : nullptr;
-            prep_token<BITS, LN>(a, a.x + (size_t)tok * a.ldx, xpl + t * CK * PD, xsum + t * CK, pre_red, s, dbgq);
-            if (tid == 0) {
-                s_sx[t] = s;
-                if (a.sx_out && blockIdx.x == 0) a.sx_out[tok] = s;
-            }
+    // 3. Prologue, overlapping the code loads: the token block's activations,
+    //    quantized, into LDS.  Token 0 is straight-line code so its x loads
+    //    stay ahead of the weight loads.
+    {
+        int16_t *dbgq = (a.xq_out && blockIdx.x == 0) ? a.xq_out + (size_t)tok0 * a.K : nullptr;
+        const float s = prep_token<BITS, UPT, LN>(a, xv, lw, lb, xpl, xsum, pre_red, dbgq);
+        if (tid == 0) {
+            s_sx[0] = s;
+            if (a.sx_out && blockIdx.x == 0) a.sx_out[tok0] = s;
         }
     }
-    __syncthreads();
+    for (int t = 1; t < MT; t++) {
+        const int tok = tok0 + t;
+        if (tok >= a.T) break;
+        load_units<VPT, UPT>(a.x + (size_t)tok * a.ldx, nunits, xv);
+        int16_t *dbgq = (a.xq_out && blockIdx.x == 0) ? a.xq_out + (size_t)tok * a.K : nullptr;
+        const float s = prep_token<BITS, UPT, LN>(a, xv, lw, lb, xpl + t * CK * PD, xsum + t * CK, pre_red, dbgq);
+        if (tid == 0) {
+            s_sx[t] = s;
+            if (a.sx_out && blockIdx.x == 0) a.sx_out[tok] = s;
+        }
+    }
+    lds_barrier();
 
+    // 4. Integer sums per chunk, float accumulation per row.  Single-batch
+    //    kernels (every wave has at most kSteps steps) are straight-line code;
+    //    LOOP kernels walk longer reduction axes one batch at a time.
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) acc[t] = 0.0f;
-
-    for (int s = s0; s < s1; s += kPrefetch) {
-        uint4 cur[kPrefetch];
-        uint32_t csc[kPrefetch], czp[kPrefetch];
-#pragma unroll
-        for (int u = 0; u < kPrefetch; u++) {
-            cur[u] = buf[u];
-            csc[u] = bsc[u];
-            czp[u] = bzp[u];
+    for (int sb = s0; sb < s1; sb += kSteps) {
+        if (LOOP && sb != s0) {
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(sb);
         }
 #pragma unroll
-        for (int u = 0; u < kPrefetch; u++) fetch(s + kPrefetch + u, buf[u], bsc[u], bzp[u]);
-#pragma unroll
-        for (int u = 0; u < kPrefetch; u++) {
-            const int ss = s + u, c = 4 * ss + j;
-            if (!(tile_ok && ss < s1 && c < CK)) continue;
-            const float scale = PERCH ? psc : __half2float(__ushort_as_half((unsigned short)csc[u]));
-            const int zp = PERCH ? pzp : (int)czp[u];
-            const uint4 d = cur[u];
+        for (int u = 0; u < kSteps; u++) {
+            const int ss = sb + u;
+            const bool ok = tile_ok && ss < s1 && 4 * ss + j < CK;
+            const int c = ok ? 4 * ss + j : 0;  // LDS reads stay in range; scale is 0
+            const float scale = ok ? __half2float(__ushort_as_half((unsigned short)wsc[u])) : 0.0f;
+            const int zp = (int)wzp[u];
+            const uint4 d = wc[u];
             uint32_t su;
             if (BITS == 4) {
                 su = __builtin_amdgcn_udot8(d.x, 0x11111111u, 0u, false);
@@ -269,39 +322,40 @@ __global__ __launch_bounds__(kThreads) void gemv_a16_kernel(GemvArgs a) {
                 const uint4 *P = reinterpret_cast<const uint4 *>(xpl + (t * CK + c) * PD);
                 uint32_t xu;
                 if (BITS == 4) {
-                    uint32_t S[4];
+                    uint32_t Sp[4];
 #pragma unroll
                     for (int p = 0; p < 4; p++) {
                         const uint4 q = P[p];
                         uint32_t v = __builtin_amdgcn_udot8(q.x, d.x, 0u, false);
                         v = __builtin_amdgcn_udot8(q.y, d.y, v, false);
                         v = __builtin_amdgcn_udot8(q.z, d.z, v, false);
-                        S[p] = __builtin_amdgcn_udot8(q.w, d.w, v, false);
+                        Sp[p] = __builtin_amdgcn_udot8(q.w, d.w, v, false);
                     }
-                    xu = S[0] + (S[1] << 4) + (S[2] << 8) + (S[3] << 12);
+                    xu = Sp[0] + (Sp[1] << 4) + (Sp[2] << 8) + (Sp[3] << 12);
                 } else {
-                    uint32_t S[2];
+                    uint32_t Sp[2];
 #pragma unroll
                     for (int p = 0; p < 2; p++) {
                         const uint4 q = P[p];
                         uint32_t v = __builtin_amdgcn_udot4(q.x, d.x, 0u, false);
                         v = __builtin_amdgcn_udot4(q.y, d.y, v, false);
                         v = __builtin_amdgcn_udot4(q.z, d.z, v, false);
-                        S[p] = __builtin_amdgcn_udot4(q.w, d.w, v, false);
+                        Sp[p] = __builtin_amdgcn_udot4(q.w, d.w, v, false);
                     }
-                    xu = S[0] + (S[1] << 8);
+                    xu = Sp[0] + (Sp[1] << 8);
                 }
                 const int G = (int)(xu - 32768u * su) - zp * xsum[t * CK + c];
-                if (DBG) {
-                    const int o = tile * 16 + r;
-                    if (o < a.n) a.dbg[(size_t)o * CK + c] = G;
-                }
+                if (DBG && row_ok && ok) a.dbg[(size_t)o * CK + c] = G;
                 acc[t] = fmaf((float)G, scale, acc[t]);
+                // Keep each (step, token)'s LDS reads next to their use: without
+                // this the scheduler hoists them all and runs out of registers.
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
+        if (!LOOP) break;
     }
 
-    // Rows: sum the four lanes of a row, then the ks waves of a tile.
+    // 5. Rows: sum the four lanes of a row, then the ks waves of a tile.
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         acc[t] += __shfl_xor(acc[t], 16);
@@ -310,7 +364,7 @@ __global__ __launch_bounds__(kThreads) void gemv_a16_kernel(GemvArgs a) {
     if (a.ks > 1) {
         if (j == 0)
             for (int t = 0; t < MT; t++) part[(wid * MT + t) * 16 + r] = acc[t];
-        __syncthreads();
+        lds_barrier();
         if (kpart == 0)
             for (int t = 0; t < MT; t++) {
                 float v = 0.0f;
@@ -319,18 +373,18 @@ __global__ __launch_bounds__(kThreads) void gemv_a16_kernel(GemvArgs a) {
             }
     }
 
-    const int o = tile * 16 + r;
+    // 6. Epilogue: scale, bias, GELU, residual, store.
     float best_v = -INFINITY;
     int best_i = 0x7fffffff;
-    if (kpart == 0 && tile_ok && o < a.n) {
+    if (kpart == 0 && row_ok) {
         for (int t = 0; t < MT; t++) {
-            const int tok = tb * MT + t;
+            const int tok = tok0 + t;
             if (tok >= a.T) break;
             float v = acc[t] * s_sx[t];
-            if (a.flags & LLMQ_BIAS) v += a.bias[o];
+            if (a.flags & LLMQ_BIAS) v += MT == 1 ? e_bias : a.bias[o];
             if (a.flags & LLMQ_GELU) v = gelu_f(v);
             float *dst = a.out + (size_t)tok * a.ldo + o;
-            if (a.flags & LLMQ_RESID) v += *dst;
+            if (a.flags & LLMQ_RESID) v += MT == 1 ? e_res : *dst;
             if (j == 0) *dst = v;
             if (MT == 1) {
                 best_v = v;
@@ -351,7 +405,7 @@ __global__ __launch_bounds__(kThreads) void gemv_a16_kernel(GemvArgs a) {
             }
         }
         if (lane == 0 && kpart == 0) s_best[wid / a.ks] = ArgmaxPart{best_v, best_i};
-        __syncthreads();
+        lds_barrier();
         if (tid == 0) {
             ArgmaxPart b = s_best[0];
             for (int q = 1; q < tpw; q++) {
@@ -369,46 +423,54 @@ int pick_ks(const llmq_mat *w, int64_t T) {
         if (v == 1 || v == 2 || v == 4) return v;
     }
     if (T > 1) return 1;
-    if (w->ntiles >= 2048) return 1;
-    if (w->ntiles >= 1024) return 2;
+    if (w->ntiles <= 1024) return 4;  // latency-bound sizes: the most waves
+    const int64_t S = (w->CK + 3) / 4;
+    for (int ks = 1; ks < 4; ks *= 2)
+        if ((S + ks - 1) / ks <= kSteps) return ks;
     return 4;
 }
 
-template <int BITS, int MT, bool LN, bool PERCH, bool DBG>
-void launch_t(llmq_ctx *ctx, const GemvArgs &a, dim3 grid, size_t lds) {
-    hipLaunchKernelGGL((gemv_a16_kernel<BITS, MT, LN, PERCH, DBG>), grid, dim3(kThreads), lds, ctx->stream, a);
+template <int BITS, int MT, bool LN, bool DBG, int UPT>
+void launch_t(llmq_ctx *ctx, const GemvArgs &a, dim3 grid, size_t lds, bool loop) {
+    if (loop)
+        hipLaunchKernelGGL((gemv_a16_kernel<BITS, MT, LN, DBG, UPT, true>), grid, dim3(kThreads), lds, ctx->stream, a);
+    else
+        hipLaunchKernelGGL((gemv_a16_kernel<BITS, MT, LN, DBG, UPT, false>), grid, dim3(kThreads), lds, ctx->stream,
+                           a);
 }
 
-template <int BITS, int MT, bool LN>
-void dispatch_perch(llmq_ctx *ctx, const GemvArgs &a, dim3 grid, size_t lds, bool perch, bool dbg) {
-    if (dbg && MT == 1 && !LN) {
-        if (perch)
-            launch_t<BITS, MT, LN, true, true>(ctx, a, grid, lds);
-        else
-            launch_t<BITS, MT, LN, false, true>(ctx, a, grid, lds);
-    } else if (perch) {
-        launch_t<BITS, MT, LN, true, false>(ctx, a, grid, lds);
+template <int BITS, int MT, int UPT>
+void dispatch_flags(llmq_ctx *ctx, const GemvArgs &a, dim3 grid, size_t lds, bool ln, bool dbg, bool loop) {
+    if (MT == 1 && dbg)
+        launch_t<BITS, 1, false, true, UPT>(ctx, a, grid, lds, loop);
+    else if (ln) {
+        if constexpr (UPT <= 2) launch_t<BITS, MT, true, false, UPT>(ctx, a, grid, lds, loop);
     } else {
-        launch_t<BITS, MT, LN, false, false>(ctx, a, grid, lds);
+        launch_t<BITS, MT, false, false, UPT>(ctx, a, grid, lds, loop);
     }
 }
 
 template <int BITS, int MT>
-void dispatch_ln(llmq_ctx *ctx, const GemvArgs &a, dim3 grid, size_t lds, bool ln, bool perch, bool dbg) {
-    if (ln)
-        dispatch_perch<BITS, MT, true>(ctx, a, grid, lds, perch, dbg);
+void dispatch_upt(llmq_ctx *ctx, const GemvArgs &a, int upt, dim3 grid, size_t lds, bool ln, bool dbg, bool loop) {
+    if (upt <= 1)
+        dispatch_flags<BITS, MT, 1>(ctx, a, grid, lds, ln, dbg, loop);
+    else if (upt <= 2)
+        dispatch_flags<BITS, MT, 2>(ctx, a, grid, lds, ln, dbg, loop);
+    else if (upt <= 4)
+        dispatch_flags<BITS, MT, 4>(ctx, a, grid, lds, ln, dbg, loop);
     else
-        dispatch_perch<BITS, MT, false>(ctx, a, grid, lds, perch, dbg);
+        dispatch_flags<BITS, MT, 8>(ctx, a, grid, lds, ln, dbg, loop);
 }
 
 template <int BITS>
-void dispatch_mt(llmq_ctx *ctx, const GemvArgs &a, int mt, dim3 grid, size_t lds, bool ln, bool perch, bool dbg) {
+void dispatch_mt(llmq_ctx *ctx, const GemvArgs &a, int mt, int upt, dim3 grid, size_t lds, bool ln, bool dbg,
+                 bool loop) {
     if (mt == 8)
-        dispatch_ln<BITS, 8>(ctx, a, grid, lds, ln, perch, dbg);
+        dispatch_upt<BITS, 8>(ctx, a, upt, grid, lds, ln, dbg, loop);
     else if (mt == 4)
-        dispatch_ln<BITS, 4>(ctx, a, grid, lds, ln, perch, dbg);
+        dispatch_upt<BITS, 4>(ctx, a, upt, grid, lds, ln, dbg, loop);
     else
-        dispatch_ln<BITS, 1>(ctx, a, grid, lds, ln, perch, dbg);
+        dispatch_upt<BITS, 1>(ctx, a, upt, grid, lds, ln, dbg, loop);
 }
 
 size_t lds_bytes(const llmq_mat *w, int mt) {
@@ -457,7 +519,14 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
     a.ntiles = (int)w->ntiles;
     a.CK = (int)w->CK;
     a.NG = (int)w->NG;
-    a.CPG = (int)(w->group / (w->bits == 4 ? 32 : 16));
+    const int64_t cpg = w->group / (w->bits == 4 ? 32 : 16);  // chunks per group
+    if (w->NG == 1) {
+        a.cpg_shift = 31;  // per-channel: every chunk is group 0
+    } else {
+        LLMQ_REQUIRE((cpg & (cpg - 1)) == 0, "linear: group %lld is not a power of two times 32",
+                     (long long)w->group);
+        a.cpg_shift = __builtin_ctzll((unsigned long long)cpg);
+    }
     a.T = (int)rq.T;
     a.ks = ks;
     a.flags = rq.flags;
@@ -466,7 +535,7 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
     a.x = rq.x;
     a.ln_w = rq.ln_w;
     a.ln_b = rq.ln_b;
-    a.bias = rq.bias;
+    a.bias = rq.bias ? rq.bias : rq.out;  // read (and ignored) without LLMQ_BIAS
     a.out = rq.out;
     a.amax = rq.amax;
     a.dbg = rq.dbg;
@@ -475,11 +544,21 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
     dim3 grid((unsigned)((w->ntiles + tpw - 1) / tpw), (unsigned)((rq.T + mt - 1) / mt));
     LLMQ_REQUIRE(!rq.amax || (int64_t)grid.x <= rq.amax_cap, "linear: %u argmax partials exceed capacity %d", grid.x,
                  rq.amax_cap);
-    const bool ln = rq.ln_w != nullptr, perch = w->NG == 1, dbg = rq.dbg != nullptr;
+    const bool ln = rq.ln_w != nullptr, dbg = rq.dbg != nullptr;
+    if (ln && (w->k / (w->bits == 4 ? 8 : 4) + kThreads - 1) / kThreads > 2)
+        return llmq_set_error(LLMQ_EUNSUPPORTED, "ln_linear: LayerNorm prologue supports IN <= %d",
+                              w->bits == 4 ? 4096 : 2048);
+    const int vpt = w->bits == 4 ? 8 : 4;
+    const int64_t units = w->k / vpt;
+    const int upt = (int)((units + kThreads - 1) / kThreads);
+    if (upt > 8)
+        return llmq_set_error(LLMQ_EUNSUPPORTED, "linear: reduction axis %lld too long", (long long)w->k);
+    const int64_t S = (w->CK + 3) / 4;
+    const bool loop = (S + ks - 1) / ks > kSteps;  // some wave has more than one batch
     if (w->bits == 4)
-        dispatch_mt<4>(ctx, a, mt, grid, lds, ln, perch, dbg);
+        dispatch_mt<4>(ctx, a, mt, upt, grid, lds, ln, dbg, loop);
     else
-        dispatch_mt<8>(ctx, a, mt, grid, lds, ln, perch, dbg);
+        dispatch_mt<8>(ctx, a, mt, upt, grid, lds, ln, dbg, loop);
     LLMQ_HIP(hipGetLastError());
     if (rq.amax_count) *rq.amax_count = (int)grid.x;
     return LLMQ_OK;

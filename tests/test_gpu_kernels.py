@@ -122,6 +122,8 @@ A16_CASES = [  # tests/a16_kernels.mojo:85-94 and the GPT-2 / Llama layer shapes
     ((4, 64, False), 1, 768, 768, False), ((4, 128, False), 1, 3072, 768, False),
     ((4, 32, False), 12, 768, 2304, False), ((4, 32, False), 17, 3072, 768, False),
     ((8, 32, False), 12, 768, 3072, False), ((4, 32, False), 1, 4096, 11008, False),
+    ((4, 32, False), 1, 11008, 4096, False), ((4, 32, False), 5, 4096, 1024, False),
+    ((8, 0, False), 1, 768, 50257, False),
 ]
 
 

@@ -175,6 +175,11 @@ int llmq_mat_free(llmq_mat *m) {
     hipFree(m->scales);
     hipFree(m->zps);
     hipFree(m->blocks);
+    hipFree(m->g_meta16);
+    hipFree(m->g_meta32);
+    hipFree(m->g_bits32);
+    hipFree(m->g_bits64);
+    hipFree(m->g_sb16);
     delete m;
     return LLMQ_OK;
 }
@@ -257,7 +262,18 @@ int llmq_mat_export(llmq_ctx *ctx, const llmq_mat *m, uint8_t *codes, uint16_t *
 int llmq_mat_dequant_row(llmq_ctx *ctx, const llmq_mat *m, int64_t row, float *dst) {
     LLMQ_REQUIRE(ctx && m && dst, "dequant_row: bad arguments");
     LLMQ_REQUIRE(row >= 0 && row < m->n, "dequant_row: row %lld out of range", (long long)row);
-    LLMQ_REQUIRE(m->kind == MAT_QUANT, "dequant_row: GGUF rows are read from the file buffer");
+    if (m->kind == MAT_GGUF) {
+        float *d = nullptr;
+        if (hipMalloc(&d, sizeof(float) * m->k) != hipSuccess)
+            return llmq_set_error(LLMQ_ENOMEM, "dequant_row: staging");
+        int rc = launch_gguf_dequant_row(ctx, m, row, d);
+        if (rc == LLMQ_OK &&
+            hipMemcpyAsync(dst, d, sizeof(float) * m->k, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
+            rc = llmq_set_error(LLMQ_EHIP, "dequant_row: copy failed");
+        hipStreamSynchronize(ctx->stream);
+        hipFree(d);
+        return rc;
+    }
     const int64_t tile = row / LLMQ_TILE_ROWS, r = row % LLMQ_TILE_ROWS;
     std::vector<uint8_t> c(m->CK * 16), z(m->NG);
     std::vector<uint16_t> s(m->NG);
@@ -283,13 +299,19 @@ int llmq_mat_dequant_row(llmq_ctx *ctx, const llmq_mat *m, int64_t row, float *d
 
 int llmq_mat_from_gguf(llmq_ctx *ctx, int ggml_type, const void *blocks, int64_t rows, int64_t cols,
                        llmq_mat **out) {
-    (void)ctx;
-    (void)ggml_type;
-    (void)blocks;
-    (void)rows;
-    (void)cols;
-    (void)out;
-    return llmq_set_error(LLMQ_EUNSUPPORTED, "from_gguf: GGUF block formats are not in this build yet");
+    LLMQ_REQUIRE(ctx && blocks && out, "from_gguf: bad arguments");
+    if (!gguf_is_supported(ggml_type))
+        return llmq_set_error(LLMQ_EUNSUPPORTED, "from_gguf: ggml type %d is not a supported block format",
+                              ggml_type);
+    llmq_mat *m = new llmq_mat();
+    m->ctx = ctx;
+    int rc = gguf_upload(ctx, m, ggml_type, static_cast<const uint8_t *>(blocks), rows, cols);
+    if (rc != LLMQ_OK) {
+        llmq_mat_free(m);
+        return rc;
+    }
+    *out = m;
+    return LLMQ_OK;
 }
 
 // ------------------------------------------------------------------ compute
@@ -306,7 +328,6 @@ static int check_linear(const llmq_mat *w, int64_t IN, int64_t OUT) {
     if (w->kind == MAT_QUANT && !w->a16)
         return llmq_set_error(LLMQ_EUNSUPPORTED,
                               "linear: float-activation QuantMatrix (A16=False) has no device kernel in this build");
-    LLMQ_REQUIRE(w->kind == MAT_QUANT, "linear: GGUF matrices are not in this build yet");
     return LLMQ_OK;
 }
 
@@ -314,6 +335,12 @@ int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, co
                 int64_t IN, int64_t OUT, int flags) {
     LLMQ_REQUIRE(ctx, "linear: null context");
     RC(check_linear(w, IN, OUT));
+    if (w->kind == MAT_GGUF) {
+        // matmul_rows (kernels.mojo:285-312): one token at a time on the GPU
+        for (int64_t t = 0; t < T; t++)
+            RC(launch_gguf_gemv(ctx, w, x + t * IN, out + t * OUT, bias, flags, nullptr, 0));
+        return LLMQ_OK;
+    }
     GemvRequest rq;
     rq.w = w;
     rq.x = x;
@@ -328,6 +355,7 @@ int llmq_ln_linear(llmq_ctx *ctx, float *out, const float *x, const float *ln_w,
                    const float *bias, int64_t T, int64_t IN, int64_t OUT, int flags) {
     LLMQ_REQUIRE(ctx && ln_w && ln_b, "ln_linear: bad arguments");
     RC(check_linear(w, IN, OUT));
+    LLMQ_REQUIRE(w->kind == MAT_QUANT, "ln_linear: GGUF matrices take llmq_layernorm then llmq_linear");
     GemvRequest rq;
     rq.w = w;
     rq.x = x;
@@ -353,6 +381,7 @@ int llmq_debug_chunk_sums(llmq_ctx *ctx, const float *xf, const llmq_mat *w, flo
                           int16_t *xq, float *sx) {
     LLMQ_REQUIRE(ctx && w, "debug_chunk_sums: bad arguments");
     RC(check_linear(w, w->k, w->n));
+    LLMQ_REQUIRE(w->kind == MAT_QUANT, "debug_chunk_sums: QuantMatrix only");
     GemvRequest rq;
     rq.w = w;
     rq.x = xf;

@@ -47,10 +47,12 @@ struct llmq_mat {
     uint8_t *codes = nullptr;
     uint16_t *scales = nullptr;
     uint8_t *zps = nullptr;
-    // GGUFMatrix
+    // GGUFMatrix: codes above plus the per-chunk / per-superblock fields
+    // (gguf.hip); NG counts superblocks per row for the K-quants.
     int ggml_type = -1;
     uint8_t *blocks = nullptr;
     int64_t row_bytes = 0;
+    void *g_meta16 = nullptr, *g_meta32 = nullptr, *g_bits32 = nullptr, *g_bits64 = nullptr, *g_sb16 = nullptr;
 };
 
 struct llmq_kv {
@@ -104,6 +106,14 @@ struct GemvRequest {
 int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq);
 // Number of argmax partials launch_gemv_a16 writes for a T == 1 GEMV of w.
 int gemv_a16_num_parts(const llmq_mat *w);
+
+// GGUF formats (gguf.hip).
+int gguf_is_supported(int ggml_type);
+int gguf_upload(llmq_ctx *ctx, llmq_mat *m, int ggml_type, const uint8_t *blocks, int64_t rows, int64_t cols);
+int gguf_num_parts(const llmq_mat *w);
+int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
+                     ArgmaxPart *amax, int amax_cap);
+int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
 
 int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C);
 int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,

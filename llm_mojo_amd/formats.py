@@ -89,6 +89,59 @@ class HipQuantMatrix:
             pass
 
 
+class HipGGUFMatrix:
+    """A GGUF tensor on the GPU: GGUFMatrix (gguf.mojo:344-511), blocks used
+    as stored (re-placed into the device row-tile layout)."""
+
+    OUT_MAJOR = True
+    FROM_GGUF = True
+    ACT16 = False
+
+    def __init__(self, ctx, handle, kind):
+        self.ctx, self.h, self.kind = ctx, handle, kind
+        rows, cols = ctypes.c_int64(), ctypes.c_int64()
+        check(lib().llmq_mat_shape(self.h, ctypes.byref(rows), ctypes.byref(cols)))
+        self.rows, self.cols = rows.value, cols.value
+
+    @staticmethod
+    def name():
+        return "gguf"
+
+    @classmethod
+    def from_blocks(cls, ctx, kind, blocks, rows, cols):
+        """blocks: uint8 [rows * row_bytes] as in a GGUF file; kind: ggml type id."""
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        h = ctypes.c_void_p()
+        check(lib().llmq_mat_from_gguf(ctx.h, kind, hptr(blocks), rows, cols, ctypes.byref(h)))
+        return cls(ctx, h, kind)
+
+    def nbytes(self):
+        return lib().llmq_mat_nbytes(self.h)
+
+    def group_size(self):
+        return lib().llmq_mat_group_size(self.h)
+
+    def has_i16(self):
+        """gguf.mojo:456-457: Q6_K and Q8_0 heads take the int16 path."""
+        return self.kind in (8, 14)
+
+    def dequant_row(self, row):
+        dst = np.zeros(self.cols, np.float32)
+        check(lib().llmq_mat_dequant_row(self.ctx.h, self.h, row, hptr(dst)))
+        return dst
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().llmq_mat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 def quantize_rows(ctx, x, xq, sx):
     """kernels.quantize_rows (kernels.mojo:400-416) on device tensors."""
     T, K = x.shape

@@ -86,6 +86,38 @@ class Rng:
         return np.float32(r) / np.float32(1 << 24)
 
 
+GGUF_BLOCK = {  # ggml type id: (weights per block, bytes per block), gguf.mojo:72-98
+    2: (32, 18), 3: (32, 20), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+
+def gguf_blocks(kind, rows, cols, seed):
+    """Random GGUF blocks of BASELINE config 2: every code field uniform over
+    its range (random bytes), 6-bit sub-scales / mins uniform (random bytes),
+    and the float16 scales |N(0, 0.01)| (Q4_1's min negative, as a min is)."""
+    bs, bb = GGUF_BLOCK[kind]
+    nb = rows * (cols // bs)
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+
+    def f16(col, neg=False):
+        v = np.abs(rng.normal(0, 0.01, nb)).astype(np.float16)
+        if neg:
+            v = -v
+        b[:, col:col + 2] = v.view(np.uint8).reshape(nb, 2)
+
+    if kind in (2, 8):
+        f16(0)
+    elif kind == 3:
+        f16(0)
+        f16(2, neg=True)
+    elif kind in (12, 13):
+        f16(0)
+        f16(2)
+    elif kind == 14:
+        f16(208)
+    return b.reshape(-1)
+
+
 def prompt_ids(seed, n):
     rng = Rng(seed)
     return np.array([min(V - 1, int(rng.uniform() * V)) for _ in range(n)], np.int64)

@@ -1,0 +1,58 @@
+"""GGUF block formats on the GPU against the oracle's restatement of
+gguf.mojo: dequantized rows bit-exact (the decoders' float formulas are the
+same operations), the float-activation decode GEMV within 1e-5 of max |out|
+(the reference's own bar for its GGUF checks)."""
+import numpy as np
+import pytest
+
+from tests import ggml_pack
+
+pytestmark = pytest.mark.gpu
+
+KINDS = ["Q4_0", "Q4_1", "Q8_0", "Q4_K", "Q5_K", "Q6_K"]
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_gguf_dequant_rows_exact(gpu, orc, kind):
+    torch, lm, ctx = gpu
+    t = orc.GGML[kind]
+    rows, cols = 20, 512
+    rng = np.random.default_rng(KINDS.index(kind))
+    blocks, _ = ggml_pack.random_blocks(kind, rows * cols // orc.gguf_block_size(t), rng)
+    print("gguf dequant", kind, flush=True)
+    g = lm.HipGGUFMatrix.from_blocks(ctx, t, blocks, rows, cols)
+    assert g.nbytes() == blocks.size
+    want = orc.gguf_dequant(t, blocks, rows, cols)
+    for r in (0, 7, rows - 1):
+        assert np.array_equal(g.dequant_row(r), want[r])
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("rows,cols", [(70, 512), (768, 2304), (1000, 4096)])
+def test_gguf_gemv_vs_oracle(gpu, orc, kind, rows, cols):
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    t = orc.GGML[kind]
+    blocks = synth.gguf_blocks(t, rows, cols, seed=rows + cols + t)
+    rng = np.random.default_rng(t)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    b = rng.normal(0, 0.1, rows).astype(np.float32)
+    print("gguf gemv", kind, rows, cols, flush=True)
+    g = lm.HipGGUFMatrix.from_blocks(ctx, t, blocks, rows, cols)
+    out = torch.zeros((1, rows), device="cuda")
+    lm.linear(ctx, out, dev(torch, x.reshape(1, -1)), g, dev(torch, b))
+    torch.cuda.synchronize()
+    want = orc.gguf_gemv(t, blocks, rows, cols, x, b, orc.EPI_BIAS)
+    got = out.cpu().numpy()[0]
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
+
+
+def test_gguf_unsupported_type(gpu):
+    torch, lm, ctx = gpu
+    with pytest.raises(lm.LlmqError, match="supported"):
+        lm.HipGGUFMatrix.from_blocks(ctx, 1, np.zeros(64, np.uint8), 1, 32)

@@ -651,7 +651,7 @@ int llmq_gpt2_create(llmq_ctx *ctx, const float *const *params, int bits, int gr
         ALLOC(m->att, sizeof(float) * MAXT * C);
         ALLOC(m->fc, sizeof(float) * MAXT * 4 * C);
         ALLOC(m->logits, sizeof(float) * V);
-        m->nparts = gemv_a16_num_parts(m->wte);
+        m->nparts = gemv_a16_num_parts(m->wte, true);
         ALLOC(m->parts, sizeof(ArgmaxPart) * m->nparts);
         ALLOC(m->tokens, sizeof(int64_t) * MAXT);
         ALLOC(m->gen, sizeof(int64_t) * MAXT);

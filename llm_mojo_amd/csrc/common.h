@@ -104,8 +104,13 @@ struct GemvRequest {
     float *sx_out = nullptr;
 };
 int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq);
-// Number of argmax partials launch_gemv_a16 writes for a T == 1 GEMV of w.
-int gemv_a16_num_parts(const llmq_mat *w);
+// Number of argmax partials launch_gemv_a16 writes for a T == 1 GEMV of w
+// (ln: with the LayerNorm prologue).
+int gemv_a16_num_parts(const llmq_mat *w, bool ln);
+// The T == 1 kernel (gemv1.hip) behind launch_gemv_a16.
+bool gemv1_supports(const llmq_mat *w, bool ln);
+int launch_gemv1(llmq_ctx *ctx, const GemvRequest &rq);
+int gemv1_num_parts(const llmq_mat *w, bool ln);
 
 // GGUF formats (gguf.hip).
 int gguf_is_supported(int ggml_type);

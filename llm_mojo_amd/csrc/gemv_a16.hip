@@ -480,7 +480,8 @@ size_t lds_bytes(const llmq_mat *w, int mt) {
 
 }  // namespace
 
-int gemv_a16_num_parts(const llmq_mat *w) {
+int gemv_a16_num_parts(const llmq_mat *w, bool ln) {
+    if (gemv1_supports(w, ln)) return gemv1_num_parts(w, ln);
     const int ks = pick_ks(w, 1);
     const int tpw = 4 / ks;
     return (int)((w->ntiles + tpw - 1) / tpw);
@@ -496,6 +497,7 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
     LLMQ_REQUIRE(!(rq.flags & LLMQ_BIAS) || rq.bias, "linear: LLMQ_BIAS without a bias");
     LLMQ_REQUIRE(!rq.amax || rq.T == 1, "linear: argmax partials need T == 1");
     LLMQ_REQUIRE(!rq.dbg || (rq.T == 1 && !rq.ln_w), "linear: chunk sums need T == 1 without LayerNorm");
+    if (rq.T == 1 && gemv1_supports(w, rq.ln_w != nullptr)) return launch_gemv1(ctx, rq);
     const size_t max_lds = 64 * 1024;
     int mt = 1;
     if (rq.T > 1) {

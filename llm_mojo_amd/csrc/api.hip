@@ -104,6 +104,13 @@ static int mat_alloc_quant(llmq_ctx *ctx, int bits, int group, int sym, int a16,
     // tensor.mojo:340-341
     LLMQ_REQUIRE(g > 0 && k % g == 0 && g % 32 == 0,
                  "group size must divide the reduction axis and be a multiple of 32");
+    // The BLOCKED layout of int4-g32-a16 (tensor.mojo:296, 394-404) places
+    // codes per 256-weight block; the reference has no layout for a partial
+    // block (its nibble_at addresses past the row), so such matrices are
+    // refused rather than exported wrongly.
+    LLMQ_REQUIRE(!(a16 && bits == 4 && g == 32 && k % 256 != 0),
+                 "int4-g32-a16 (BLOCKED layout) needs the reduction axis in whole 256-weight blocks, got %lld",
+                 (long long)k);
     llmq_mat *m = new llmq_mat();
     m->ctx = ctx;
     m->kind = MAT_QUANT;

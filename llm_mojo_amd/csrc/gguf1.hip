@@ -1,0 +1,538 @@
+// One-token GEMV over GGUF blocks with float activations: GGUFMatrix.dot_row
+// (gguf.mojo:389-417, the block decoders of gguf.mojo:178-297 with DOT=True)
+// as driven by matmul_rows / linear_team's OUT_MAJOR branch for T == 1
+// (kernels.mojo:285-312, 817-826), with store_out's bias / GELU / residual.
+//
+// Device layout (gguf.hip): per 16-row tile, each row's codes in 16-byte
+// chunks (32 4-bit codes, or 16 int8 codes for Q8_0), chunk-major; side
+// arrays per chunk (Q5_K 5th bits, Q6_K high bits), per block (Q4_0 / Q4_1 /
+// Q8_0 d, m) and per 256-weight superblock (K-quant d, dmin, 6-bit scales;
+// Q6_K int8 scales and d), each indexed [tile][index][16 rows].  The global
+// index of chunk c of tile t is t * CK + c, and block / superblock indices
+// are that >> 1 (Q8_0) or >> 3 (K-quants), so every field a wave needs is
+// one contiguous run even when the wave crosses a tile boundary.
+//
+// Arithmetic per chunk: a = sum x*u over its codes u (float32 FMAs on the
+// activations in LDS), with the block's scale and offset applied once:
+//   Q4_0  d * (a - 8 S)        Q4_1  d * a + m * S        Q8_0  d * (a' - 128 S)  (a' over q + 128)
+//   Q4_K  d*sc * a - dmin*m * S          Q5_K  the same with u = lo4 + 16 * bit5
+//   Q6_K  d*sc * (a - 32 S) per 16 weights, u = lo4 + 16 * hi2
+// with S = sum x over the chunk (or half chunk) from a per-16 table.  This
+// equals the reference's dequantize-then-FMA up to float32 rounding.
+//
+// Work mapping, loads and reductions follow the one-token integer kernel
+// (gemv1.hip): one 16-wave workgroup per CU with a contiguous run of whole
+// row tiles (4-wave workgroups of one tile for small matrices), a wave step
+// = 16 rows x 4 consecutive chunks read as one contiguous KiB, every load of
+// a wave issued up front as buffer loads (no-data lanes read past the extent:
+// zeros, no traffic), per-wave fields staged through LDS, fixed-order sums.
+#include "common.h"
+
+namespace {
+
+constexpr int kMaxSteps = 8;   // code steps a wave holds (16 for Q8_0, whose decode needs fewer registers)
+constexpr int kMaxTiles = 4;
+constexpr uint32_t kOOB = 0x80000000u;
+
+struct G1Args {
+    const uint8_t *codes, *meta, *bits, *sb, *d6;
+    uint32_t codes_bytes, meta_bytes, bits_bytes, sb_bytes, d6_bytes;
+    int n, K, ntiles, CK, tmax, flags;
+    const float *x, *bias;
+    float *out;
+    ArgmaxPart *amax;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short)bits)); }
+
+// Type traits: weights per chunk, and the staged per-wave fields (global
+// chunk index >> shift, bytes per (index, row)).
+template <int TYPE>
+struct T1 {
+    static constexpr bool KQ = TYPE == LLMQ_GGML_Q4_K || TYPE == LLMQ_GGML_Q5_K || TYPE == LLMQ_GGML_Q6_K;
+    static constexpr int WPC = TYPE == LLMQ_GGML_Q8_0 ? 16 : 32;
+    static constexpr int META_SHIFT = TYPE == LLMQ_GGML_Q8_0 ? 1 : (KQ ? 3 : 0);
+    // bytes per (index, row) of the main staged array: meta16 / meta32 / sb16
+    static constexpr int META_ESZ = KQ ? 16 : (TYPE == LLMQ_GGML_Q4_1 ? 4 : 2);
+    static constexpr int BITS_ESZ = TYPE == LLMQ_GGML_Q5_K ? 4 : (TYPE == LLMQ_GGML_Q6_K ? 8 : 0);  // per chunk
+};
+
+// Staged bytes per wave: the most indices a wave's 4 * STEPS chunks can
+// touch (plus one for a run that starts mid-block), 16 rows each, in whole
+// 1 KiB loads.
+template <int TYPE, int STEPS>
+struct Stage {
+    using T = T1<TYPE>;
+    static constexpr int IDX = (4 * STEPS >> T::META_SHIFT) + 2;
+    static constexpr int LOADS = (IDX * 16 * T::META_ESZ + 1023) / 1024;
+    static constexpr int D6_LOADS = TYPE == LLMQ_GGML_Q6_K ? (IDX * 32 + 1023) / 1024 : 0;
+};
+
+// k_scale_min (gguf.mojo:205-221) of sub-block j over the 12 scale bytes
+// s0..s2 (dwords), branch-free.
+__device__ __forceinline__ void k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int &sc, int &mn) {
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    const uint32_t b0 = (s0 >> sh) & 255u, b1 = (s1 >> sh) & 255u, b2 = (s2 >> sh) & 255u;
+    // j < 4: bytes j (b0) and j + 4 (b1); j >= 4: bytes j + 4 (b2), j - 4 (b0), j (b1)
+    const int sc_lo = (int)(b0 & 63u), mn_lo = (int)(b1 & 63u);
+    const int sc_hi = (int)((b2 & 15u) | ((b0 >> 6) << 4)), mn_hi = (int)((b2 >> 4) | ((b1 >> 6) << 4));
+    sc = j < 4 ? sc_lo : sc_hi;
+    mn = j < 4 ? mn_lo : mn_hi;
+}
+
+// Byte k of v as float (v_cvt_f32_ubyte<k>).
+template <int K>
+__device__ __forceinline__ float ub(uint32_t v) { return (float)((v >> (8 * K)) & 255u); }
+
+// a += sum of x[e] * byte e of w4 over the 4 bytes.
+__device__ __forceinline__ float dot4b(uint32_t w, float4 x, float a) {
+    a = fmaf(x.x, ub<0>(w), a);
+    a = fmaf(x.y, ub<1>(w), a);
+    a = fmaf(x.z, ub<2>(w), a);
+    return fmaf(x.w, ub<3>(w), a);
+}
+
+// Codes of 8 weights (dword i of a chunk: weight e in nibble e) as two byte
+// vectors: lo = weights 0, 2, 4, 6 and hi = weights 1, 3, 5, 7.  extra holds
+// per-weight high bits already in place (bits 4.. of each byte).
+__device__ __forceinline__ void split8(uint32_t w, uint32_t extra_lo, uint32_t extra_hi, uint32_t &lo, uint32_t &hi) {
+    lo = (w & 0x0F0F0F0Fu) | extra_lo;
+    hi = ((w >> 4) & 0x0F0F0F0Fu) | extra_hi;
+}
+
+// sum x[e] * u_e over 8 weights whose x are x[0..7] (two float4): u from the
+// two byte vectors of split8.
+__device__ __forceinline__ float dot8w(uint32_t lo, uint32_t hi, float4 xa, float4 xb, float a) {
+    a = fmaf(xa.x, ub<0>(lo), a);
+    a = fmaf(xa.y, ub<0>(hi), a);
+    a = fmaf(xa.z, ub<1>(lo), a);
+    a = fmaf(xa.w, ub<1>(hi), a);
+    a = fmaf(xb.x, ub<2>(lo), a);
+    a = fmaf(xb.y, ub<2>(hi), a);
+    a = fmaf(xb.z, ub<3>(lo), a);
+    return fmaf(xb.w, ub<3>(hi), a);
+}
+
+// Spread 4 bit fields of width W at positions 2W*k (k = 0..3, i.e. the even
+// weights of 8) of f to bit 4 of byte k.  W = 1 (Q5_K's 5th bits) or 2
+// (Q6_K's high bits).
+template <int W>
+__device__ __forceinline__ uint32_t spread4(uint32_t f) {
+    if (W == 1) {
+        uint32_t x = f & 0x55u;                 // bits 0, 2, 4, 6
+        x = (x | (x << 12)) & 0x00050005u;      // 0, 2, 16, 18
+        x = (x | (x << 6)) & 0x01010101u;       // 0, 8, 16, 24
+        return x << 4;
+    } else {
+        uint32_t x = f & 0x3333u;               // pairs at 0, 4, 8, 12
+        x = (x | (x << 8)) & 0x00330033u;       // 0, 4, 16, 20
+        x = (x | (x << 4)) & 0x03030303u;       // 0, 8, 16, 24
+        return x << 4;
+    }
+}
+
+template <int TYPE, int NW, int STEPS>
+__global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
+    using T = T1<TYPE>;
+    using St = Stage<TYPE, STEPS>;
+    constexpr int NT = NW * 64;
+    constexpr int WPC = T::WPC;
+    extern __shared__ __align__(16) float smem_f[];
+    __shared__ __align__(16) uint8_t s_meta[NW][St::LOADS * 1024];
+    __shared__ __align__(16) uint8_t s_d6[NW][St::D6_LOADS > 0 ? St::D6_LOADS * 1024 : 16];
+    __shared__ ArgmaxPart s_best[NW];
+
+    const int K = a.K, CK = a.CK;
+    float *xs = smem_f;                                // [K] activations
+    float *xsum16 = xs + K;                            // [K / 16] sums of 16
+    float *part = xsum16 + ((K / 16 + 3) & ~3);        // [tmax][NW][16 rows][4], 16-byte aligned
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, j = lane >> 4;
+    const int S = (CK + 3) >> 2;
+    const int t0 = (int)((blockIdx.x * (uint32_t)a.ntiles) / gridDim.x);
+    const int nt = (int)(((blockIdx.x + 1) * (uint32_t)a.ntiles) / gridDim.x) - t0;
+    const int W = nt * S;
+    const int g0 = (wid * W) / NW;
+    const int ns = ((wid + 1) * W) / NW - g0;
+    const int tA = ns > 0 ? (int)((uint32_t)g0 / (uint32_t)S) : 0;
+    const int sA = ns > 0 ? g0 - tA * S : 0;
+
+    // 1. Activations (four per thread and round), then the wave's staged
+    //    fields, codes and high bits, then the epilogue operands.
+    const int nunits = K / 4;
+    constexpr int UPT = 4;  // up to 16 KiB of activations per round of 1024 threads
+    const auto rx = make_rsrc(a.x, (uint32_t)K * 4u);
+    uint4 xv[UPT];
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const uint32_t u = (uint32_t)(tid + NT * i);
+        xv[i] = bload16(rx, u < (uint32_t)nunits ? u * 16u : kOOB);
+    }
+    // Global chunk indices of the wave's first and last valid chunks.
+    const int gE = g0 + max(ns, 1) - 1;
+    const int tE = (int)((uint32_t)gE / (uint32_t)S), sE = gE - tE * S;
+    const int cg_lo = (t0 + tA) * CK + 4 * sA;
+    const int cg_hi = (t0 + tE) * CK + min(4 * sE + 3, CK - 1);
+    const int mi_lo = cg_lo >> T::META_SHIFT;
+    const int mcount = ns > 0 ? (cg_hi >> T::META_SHIFT) - mi_lo + 1 : 1;
+    const auto rm = make_rsrc(T::KQ ? a.sb : a.meta, T::KQ ? a.sb_bytes : a.meta_bytes);
+    uint4 wm[St::LOADS];
+#pragma unroll
+    for (int i = 0; i < St::LOADS; i++) {
+        const uint32_t off = (uint32_t)(i * 1024 + lane * 16);
+        wm[i] = bload16(rm, off < (uint32_t)(mcount * 16 * T::META_ESZ) ? (uint32_t)mi_lo * 16u * T::META_ESZ + off : kOOB);
+    }
+    uint4 wd6[St::D6_LOADS > 0 ? St::D6_LOADS : 1];
+    if constexpr (St::D6_LOADS > 0) {
+        const auto rd = make_rsrc(a.d6, a.d6_bytes);
+#pragma unroll
+        for (int i = 0; i < St::D6_LOADS; i++) {
+            const uint32_t off = (uint32_t)(i * 1024 + lane * 16);
+            wd6[i] = bload16(rd, off < (uint32_t)(mcount * 32) ? (uint32_t)mi_lo * 32u + off : kOOB);
+        }
+    }
+    const uint32_t offA = ((uint32_t)(t0 + tA) * (uint32_t)CK + 4u * (uint32_t)sA) * 16u;  // chunk-row index
+    const uint32_t wrap_adj = (uint32_t)(CK - 4 * S) * 16u;
+    const uint32_t lane_cr = (uint32_t)j * 16u + (uint32_t)r;
+    const auto rc = make_rsrc(a.codes, a.codes_bytes);
+    uint4 wc[STEPS];
+#pragma unroll
+    for (int u = 0; u < STEPS; u++) {
+        const uint32_t cr = offA + (uint32_t)u * 64u + (sA + u >= S ? wrap_adj : 0u) + lane_cr;
+        wc[u] = bload16(rc, u < ns ? cr * 16u : kOOB);
+    }
+    uint2 wb[T::BITS_ESZ > 0 ? STEPS : 1];
+    if constexpr (T::BITS_ESZ > 0) {
+        const auto rb = make_rsrc(a.bits, a.bits_bytes);
+#pragma unroll
+        for (int u = 0; u < STEPS; u++) {
+            const uint32_t cr = offA + (uint32_t)u * 64u + (sA + u >= S ? wrap_adj : 0u) + lane_cr;
+            if (T::BITS_ESZ == 8)
+                wb[u] = bload8(rb, u < ns ? cr * 8u : kOOB);
+            else
+                wb[u] = make_uint2(bload4(rb, u < ns ? cr * 4u : kOOB), 0u);
+        }
+    }
+    const int o = (t0 + wid) * 16 + r;
+    const bool row_ok = wid < nt && o < a.n;
+    const auto rbias = make_rsrc(a.bias, (uint32_t)a.n * 4u);
+    const auto rout = make_rsrc(a.out, (uint32_t)a.n * 4u);
+    const float e_bias = __uint_as_float(bload4(rbias, row_ok ? (uint32_t)o * 4u : kOOB));
+    const float e_res = __uint_as_float(bload4(rout, row_ok ? (uint32_t)o * 4u : kOOB));
+
+    // 2. Activations and their sums of 16 into LDS; the wave's fields into
+    //    its slot.
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = tid + NT * i;
+        if (u < nunits) reinterpret_cast<uint4 *>(xs)[u] = xv[i];
+    }
+    for (int u = tid + NT * UPT; u < nunits; u += NT) reinterpret_cast<uint4 *>(xs)[u] = bload16(rx, (uint32_t)u * 16u);
+#pragma unroll
+    for (int i = 0; i < St::LOADS; i++) reinterpret_cast<uint4 *>(s_meta[wid])[i * 64 + lane] = wm[i];
+    if constexpr (St::D6_LOADS > 0) {
+#pragma unroll
+        for (int i = 0; i < St::D6_LOADS; i++) reinterpret_cast<uint4 *>(s_d6[wid])[i * 64 + lane] = wd6[i];
+    }
+    lds_barrier();
+    for (int g = tid; g < K / 16; g += NT) {
+        const float4 *p = reinterpret_cast<const float4 *>(xs + 16 * g);
+        const float4 v0 = p[0], v1 = p[1], v2 = p[2], v3 = p[3];
+        xsum16[g] = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w)) +
+                    (((v2.x + v2.y) + (v2.z + v2.w)) + ((v3.x + v3.y) + (v3.z + v3.w)));
+    }
+    lds_barrier();
+
+    // 3. Per step: the block's factors, then sum x*u over the chunk's codes.
+    //    contribution = pA * aA + pB * aB + qA * SA + qB * SB over the chunk's
+    //    halves (16 weights each; Q8_0's chunk is one half).
+    float accA = 0.0f, accB = 0.0f;
+#pragma unroll
+    for (int u = 0; u < STEPS; u++) {
+        if (u < ns) {  // wave-uniform: steps past the wave's range carry no codes
+            const bool second = sA + u >= S;
+            const int tl = tA + (second ? 1 : 0);
+            const int ss = sA + u - (second ? S : 0);
+            const int c_raw = 4 * ss + j;
+            const bool ok = c_raw < CK;
+            const int c = ok ? c_raw : 0;
+            const int mi = ok ? (((t0 + tl) * CK + c) >> T::META_SHIFT) - mi_lo : 0;
+            float pA, pB, qA, qB;
+            if (TYPE == LLMQ_GGML_Q4_0 || TYPE == LLMQ_GGML_Q8_0) {
+                const float d = h2f(reinterpret_cast<const uint16_t *>(s_meta[wid])[mi * 16 + r]);
+                pA = pB = d;
+                qA = qB = (TYPE == LLMQ_GGML_Q4_0 ? -8.0f : -128.0f) * d;
+            } else if (TYPE == LLMQ_GGML_Q4_1) {
+                const uint32_t dm = reinterpret_cast<const uint32_t *>(s_meta[wid])[mi * 16 + r];
+                pA = pB = h2f(dm);
+                qA = qB = h2f(dm >> 16);
+            } else if (TYPE == LLMQ_GGML_Q4_K || TYPE == LLMQ_GGML_Q5_K) {
+                const uint4 f = reinterpret_cast<const uint4 *>(s_meta[wid])[mi * 16 + r];
+                int sc, mn;
+                k_scale_min(f.y, f.z, f.w, c & 7, sc, mn);
+                pA = pB = h2f(f.x) * (float)sc;
+                qA = qB = -(h2f(f.x >> 16) * (float)mn);
+            } else {  // Q6_K: int8 scales 2(c & 7) and 2(c & 7) + 1, d of the superblock
+                const uint16_t sp = reinterpret_cast<const uint16_t *>(s_meta[wid])[(mi * 16 + r) * 8 + (c & 7)];
+                const float d = h2f(reinterpret_cast<const uint16_t *>(s_d6[wid])[mi * 16 + r]);
+                pA = d * (float)(int8_t)(sp & 255u);
+                pB = d * (float)(int8_t)(sp >> 8);
+                qA = -32.0f * pA;
+                qB = -32.0f * pB;
+            }
+            if (!ok) pA = pB = qA = qB = 0.0f;
+            const uint4 d4 = wc[u];
+            const float4 *xc = reinterpret_cast<const float4 *>(xs + c * WPC);
+            float aA = 0.0f, aB = 0.0f, SA, SB;
+            if (TYPE == LLMQ_GGML_Q8_0) {
+                // 16 int8 codes: bytes as q + 128
+                aA = dot4b(d4.x ^ 0x80808080u, xc[0], aA);
+                aA = dot4b(d4.y ^ 0x80808080u, xc[1], aA);
+                aA = dot4b(d4.z ^ 0x80808080u, xc[2], aA);
+                aA = dot4b(d4.w ^ 0x80808080u, xc[3], aA);
+                SA = xsum16[c];
+                SB = 0.0f;
+            } else {
+                uint32_t e[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};  // high bits per dword: even / odd weights
+                if (TYPE == LLMQ_GGML_Q5_K) {
+                    const uint32_t b = wb[u].x;
+    #pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t f = (b >> (8 * i)) & 255u;
+                        e[i][0] = spread4<1>(f);
+                        e[i][1] = spread4<1>(f >> 1);
+                    }
+                } else if (TYPE == LLMQ_GGML_Q6_K) {
+                    const uint2 b = wb[u];
+    #pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t f = ((i < 2 ? b.x : b.y) >> (16 * (i & 1))) & 0xFFFFu;
+                        e[i][0] = spread4<2>(f);
+                        e[i][1] = spread4<2>(f >> 2);
+                    }
+                }
+                const uint32_t dw[4] = {d4.x, d4.y, d4.z, d4.w};
+    #pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint32_t lo, hi;
+                    split8(dw[i], e[i][0], e[i][1], lo, hi);
+                    if (i < 2)
+                        aA = dot8w(lo, hi, xc[2 * i], xc[2 * i + 1], aA);
+                    else
+                        aB = dot8w(lo, hi, xc[2 * i], xc[2 * i + 1], aB);
+                }
+                SA = xsum16[2 * c];
+                SB = xsum16[2 * c + 1];
+            }
+            const float contrib = (pA * aA + qA * SA) + (pB * aB + qB * SB);
+            accA += second ? 0.0f : contrib;
+            accB += second ? contrib : 0.0f;
+        }
+    }
+
+    // 4. Per row: the 4 lanes of each wave and the waves that touched the
+    //    tile, in a fixed order, by wave t for local tile t.
+    for (int t = 0; t < a.tmax; t++) {
+        const float v = t == tA ? accA : (t == tA + 1 ? accB : 0.0f);
+        part[((t * NW + wid) * 16 + r) * 4 + j] = v;
+    }
+    lds_barrier();
+    float best_v = -INFINITY;
+    int best_i = 0x7fffffff;
+    if (wid < nt && j == 0) {
+        const float4 *p4 = reinterpret_cast<const float4 *>(part) + wid * NW * 16 + r;
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NW; q++) {
+            const float4 t = p4[q * 16];
+            v += (t.x + t.y) + (t.z + t.w);
+        }
+        if (row_ok) {
+            if (a.flags & LLMQ_BIAS) v += e_bias;
+            if (a.flags & LLMQ_GELU) {
+                const float sg = 0.7978845608028654f;
+                float t = 0.044715f * v;
+                t = t * v;
+                t = t * v;
+                v = (0.5f * v) * (1.0f + tanhf(sg * (v + t)));
+            }
+            if (a.flags & LLMQ_RESID) v += e_res;
+            a.out[o] = v;
+            best_v = v;
+            best_i = o;
+        }
+    }
+    if (a.amax) {
+        if (wid < nt) {
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(best_v, off);
+                const int oi = __shfl_xor(best_i, off);
+                if (ov > best_v || (ov == best_v && oi < best_i)) {
+                    best_v = ov;
+                    best_i = oi;
+                }
+            }
+            if (lane == 0) s_best[wid] = ArgmaxPart{best_v, best_i};
+        }
+        lds_barrier();
+        if (tid == 0) {
+            ArgmaxPart b = s_best[0];
+            for (int q = 1; q < nt; q++) {
+                const ArgmaxPart c = s_best[q];
+                if (c.v > b.v || (c.v == b.v && c.idx < b.idx)) b = c;
+            }
+            a.amax[blockIdx.x] = b;
+        }
+    }
+}
+
+struct Plan {
+    int nw, tmax, spw, steps, grid;
+};
+
+int steps_for(int spw) { return spw <= 2 ? 2 : spw <= 4 ? 4 : spw <= 8 ? 8 : 16; }
+int max_steps(const llmq_mat *w) { return w->ggml_type == LLMQ_GGML_Q8_0 ? 2 * kMaxSteps : kMaxSteps; }
+
+// As the one-token integer kernel's plan: 4-wave workgroups of one tile for
+// small matrices, else one 16-wave workgroup per CU with whole-tile runs.
+Plan make_plan(const llmq_mat *w) {
+    Plan p{};
+    const int S = (int)((w->CK + 3) / 4);
+    const int64_t work = w->ntiles * (int64_t)S;
+    int nw = (work >= 4096 || S > 8) ? 16 : 4;
+    if (const char *e = getenv("LLMQ_GEMV1_NW")) {
+        const int v = atoi(e);
+        if (v == 4 || v == 16) nw = v;
+    }
+    if (nw == 4 && (S + 3) / 4 > 4) nw = 16;
+    int64_t grid = w->ntiles;
+    if (nw == 16) {
+        grid = std::min<int64_t>(w->ntiles, 256);
+        const int cap = std::min(max_steps(w), S + 1);
+        int tmax = (int)((w->ntiles + grid - 1) / grid);
+        if (tmax > kMaxTiles || (tmax * S + 15) / 16 > cap) {
+            tmax = std::max(1, std::min(kMaxTiles, cap * 16 / S));
+            grid = (w->ntiles + tmax - 1) / tmax;
+        }
+    }
+    p.nw = nw;
+    p.grid = (int)grid;
+    p.tmax = (int)((w->ntiles + grid - 1) / grid);
+    p.spw = (p.tmax * S + nw - 1) / nw;
+    p.steps = steps_for(p.spw);
+    return p;
+}
+
+size_t lds_bytes(const llmq_mat *w, const Plan &p) {
+    return (size_t)w->k * 4 + (size_t)((w->k / 16 + 3) & ~3) * 4 + (size_t)p.tmax * p.nw * 64 * 4;
+}
+
+template <int TYPE, int NW, int STEPS>
+int launch_t(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
+    auto kern = gguf1_kernel<TYPE, NW, STEPS>;
+    hipFuncAttributes fa{};
+    LLMQ_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(kern)));
+    if (fa.sharedSizeBytes + lds > ctx->prop.sharedMemPerBlock)
+        return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf_gemv: reduction axis %d needs %zu bytes of LDS (%zu available)",
+                              a.K, fa.sharedSizeBytes + lds, (size_t)ctx->prop.sharedMemPerBlock);
+    static size_t lds_set = 0;  // the kernel's dynamic-LDS limit raised so far (one host thread per context)
+    if (lds > lds_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess)
+            return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf_gemv: %zu bytes of LDS not available", lds);
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)p.grid), dim3(NW * 64), lds, ctx->stream, a);
+    return LLMQ_OK;
+}
+
+template <int TYPE>
+int launch_type(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
+    if (p.nw == 4) {
+        if (p.steps == 2) return launch_t<TYPE, 4, 2>(ctx, a, p, lds);
+        if (p.steps == 4) return launch_t<TYPE, 4, 4>(ctx, a, p, lds);
+    } else {
+        if (p.steps == 2) return launch_t<TYPE, 16, 2>(ctx, a, p, lds);
+        if (p.steps == 4) return launch_t<TYPE, 16, 4>(ctx, a, p, lds);
+        if (p.steps == 8) return launch_t<TYPE, 16, 8>(ctx, a, p, lds);
+        if constexpr (TYPE == LLMQ_GGML_Q8_0)
+            if (p.steps == 16) return launch_t<TYPE, 16, 16>(ctx, a, p, lds);
+    }
+    return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf_gemv: no kernel for %d waves x %d steps", p.nw, p.steps);
+}
+
+}  // namespace
+
+int gguf_num_parts(const llmq_mat *w) { return make_plan(w).grid; }
+
+int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
+                     ArgmaxPart *amax, int amax_cap) {
+    LLMQ_REQUIRE(w && w->kind == MAT_GGUF, "gguf_gemv: not a GGUF matrix");
+    LLMQ_REQUIRE(x && out, "gguf_gemv: null pointer");
+    LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemv: LLMQ_BIAS without a bias");
+    LLMQ_REQUIRE(w->k % 16 == 0, "gguf_gemv: cols must be a multiple of 16");
+    const Plan p = make_plan(w);
+    const size_t lds = lds_bytes(w, p);
+    LLMQ_REQUIRE(p.spw <= max_steps(w) && p.spw <= (w->CK + 3) / 4 + 1,
+                 "gguf_gemv: no one-token kernel for %lld x %lld", (long long)w->n, (long long)w->k);
+    LLMQ_REQUIRE(!amax || p.grid <= amax_cap, "gguf_gemv: argmax capacity");
+    const int64_t ntc = (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 16;  // (chunk, row) entries incl. padding
+    const int64_t nts = (w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 16;  // (superblock, row) entries
+    G1Args a{};
+    a.codes = w->codes;
+    a.codes_bytes = (uint32_t)(ntc * 16);
+    a.meta = reinterpret_cast<const uint8_t *>(w->ggml_type == LLMQ_GGML_Q4_1 ? w->g_meta32 : w->g_meta16);
+    a.meta_bytes = (uint32_t)(w->ggml_type == LLMQ_GGML_Q4_1 ? ntc * 4 : ntc * 2);
+    a.bits = reinterpret_cast<const uint8_t *>(w->ggml_type == LLMQ_GGML_Q6_K ? w->g_bits64 : w->g_bits32);
+    a.bits_bytes = (uint32_t)(w->ggml_type == LLMQ_GGML_Q6_K ? ntc * 8 : ntc * 4);
+    a.sb = reinterpret_cast<const uint8_t *>(w->g_sb16);
+    a.sb_bytes = (uint32_t)(nts * 16);
+    a.d6 = reinterpret_cast<const uint8_t *>(w->g_meta16);
+    a.d6_bytes = (uint32_t)(nts * 2);
+    a.n = (int)w->n;
+    a.K = (int)w->k;
+    a.ntiles = (int)w->ntiles;
+    a.CK = (int)w->CK;
+    a.tmax = p.tmax;
+    a.flags = flags;
+    a.x = x;
+    a.bias = bias ? bias : out;  // read (and ignored) without LLMQ_BIAS
+    a.out = out;
+    a.amax = amax;
+    int rc;
+    switch (w->ggml_type) {
+    case LLMQ_GGML_Q4_0: rc = launch_type<LLMQ_GGML_Q4_0>(ctx, a, p, lds); break;
+    case LLMQ_GGML_Q4_1: rc = launch_type<LLMQ_GGML_Q4_1>(ctx, a, p, lds); break;
+    case LLMQ_GGML_Q8_0: rc = launch_type<LLMQ_GGML_Q8_0>(ctx, a, p, lds); break;
+    case LLMQ_GGML_Q4_K: rc = launch_type<LLMQ_GGML_Q4_K>(ctx, a, p, lds); break;
+    case LLMQ_GGML_Q5_K: rc = launch_type<LLMQ_GGML_Q5_K>(ctx, a, p, lds); break;
+    case LLMQ_GGML_Q6_K: rc = launch_type<LLMQ_GGML_Q6_K>(ctx, a, p, lds); break;
+    default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf_gemv: type %d", w->ggml_type);
+    }
+    if (rc != LLMQ_OK) return rc;
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}

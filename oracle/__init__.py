@@ -155,6 +155,9 @@ class QuantMatrix:
         self = cls(bits, group, sym, a16)
         n, k = (cols, rows) if reduce_rows else (rows, cols)
         g = k if group == 0 else group
+        if a16 and bits == 4 and g == 32 and k % 256:
+            # BLOCKED (tensor.mojo:296, 394-404) addresses whole 256-weight blocks
+            raise ValueError("int4-g32-a16 needs the reduction axis in whole 256-weight blocks")
         self.data = np.zeros(n * k * bits // 8, np.uint8)
         self.scale = np.zeros(n * k // g, np.uint16)
         self.zp = np.zeros(n * k // g, np.uint8)

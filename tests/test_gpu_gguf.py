@@ -32,8 +32,11 @@ def test_gguf_dequant_rows_exact(gpu, orc, kind):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("rows,cols", [(70, 512), (768, 2304), (1000, 4096)])
+@pytest.mark.parametrize("rows,cols", [(70, 512), (768, 2304), (1000, 4096), (6000, 4096), (300, 4352), (300, 11008)])
 def test_gguf_gemv_vs_oracle(gpu, orc, kind, rows, cols):
+    """(6000, 4096): 16-wave workgroups with runs of several row tiles, waves
+    crossing tile boundaries; (300, 4352): 17 superblocks a row; (300, 11008):
+    the longest rows (Q8_0: 16 code steps a wave)."""
     torch, lm, ctx = gpu
     from llm_mojo_amd import synth
 
@@ -48,6 +51,31 @@ def test_gguf_gemv_vs_oracle(gpu, orc, kind, rows, cols):
     lm.linear(ctx, out, dev(torch, x.reshape(1, -1)), g, dev(torch, b))
     torch.cuda.synchronize()
     want = orc.gguf_gemv(t, blocks, rows, cols, x, b, orc.EPI_BIAS)
+    got = out.cpu().numpy()[0]
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
+
+
+@pytest.mark.parametrize("kind", ["Q4_0", "Q4_1", "Q8_0"])
+def test_gguf_gemv_partial_steps(gpu, orc, kind, monkeypatch):
+    """cols = 544: 17 chunks of 32 (34 of Q8_0's 16) a row, so the last step
+    of every tile is partial; 16-wave workgroups (forced) with runs of 4 row
+    tiles, so waves cross tile boundaries mid-run."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    monkeypatch.setenv("LLMQ_GEMV1_NW", "16")
+    t = orc.GGML[kind]
+    rows, cols = 13000, 544
+    blocks = synth.gguf_blocks(t, rows, cols, seed=t)
+    rng = np.random.default_rng(t + 1)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    res = rng.normal(0, 0.1, rows).astype(np.float32)
+    print("gguf gemv partial", kind, flush=True)
+    g = lm.HipGGUFMatrix.from_blocks(ctx, t, blocks, rows, cols)
+    out = dev(torch, res.reshape(1, -1))
+    lm.linear(ctx, out, dev(torch, x.reshape(1, -1)), g, None, resid=True)
+    torch.cuda.synchronize()
+    want = orc.gguf_gemv(t, blocks, rows, cols, x, None, 0) + res
     got = out.cpu().numpy()[0]
     assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
 

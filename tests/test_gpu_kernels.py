@@ -80,12 +80,21 @@ def test_quantize_rows_bit_exact(gpu, orc):
 
 
 @pytest.mark.parametrize("bits,group,sym", FORMATS)
-@pytest.mark.parametrize("IN,OUT", [(768, 2304), (3072, 768), (768, 70)])
-def test_group_sums_exact(gpu, orc, bits, group, sym, IN, OUT):
+@pytest.mark.parametrize("IN,OUT,nw", [(768, 2304, None), (3072, 768, None), (768, 70, None), (4096, 6000, None),
+                                       (544, 13000, "16")])
+def test_group_sums_exact(gpu, orc, bits, group, sym, IN, OUT, nw, monkeypatch):
     """Per-chunk integer partials of the product kernel, summed per group,
     equal the exact int64 group sums; the kernel's activation codes and
-    scale equal quantize_rows'."""
+    scale equal quantize_rows'.  (4096, 6000): 16-wave workgroups with runs
+    of two row tiles; (544, 13000) with 16 waves forced: a partial last step
+    in every tile (17 int4 chunks a row) and waves crossing tile boundaries."""
     torch, lm, ctx = gpu
+    if IN % (group or IN):
+        pytest.skip("group does not divide the row")
+    if bits == 4 and group == 32 and IN % 256:
+        pytest.skip("int4-g32-a16 (BLOCKED) needs whole 256-weight blocks")
+    if nw:
+        monkeypatch.setenv("LLMQ_GEMV1_NW", nw)
     rng = np.random.default_rng(IN + OUT + bits + group)
     w = rng.uniform(-0.1, 0.1, (IN, OUT)).astype(np.float32)
     x = rng.normal(0, 1, (1, IN)).astype(np.float32)
@@ -245,7 +254,9 @@ def test_errors_are_reported(gpu):
     w = np.zeros((100, 8), np.float32)  # 100 is not a multiple of the group
     with pytest.raises(lm.LlmqError, match="group size"):
         lm.HipQuantMatrix.from_f32(ctx, w, 4, 32, False, True)
-    g = lm.HipQuantMatrix.from_f32(ctx, np.zeros((64, 8), np.float32), 4, 32, False, True)
+    with pytest.raises(lm.LlmqError, match="256-weight blocks"):  # BLOCKED needs whole blocks
+        lm.HipQuantMatrix.from_f32(ctx, np.zeros((544, 8), np.float32), 4, 32, False, True)
+    g = lm.HipQuantMatrix.from_f32(ctx, np.zeros((256, 8), np.float32), 4, 32, False, True)
     out = torch.zeros((1, 8), dtype=torch.float32, device="cuda")
     with pytest.raises(lm.LlmqError, match="IN="):
         lm.linear(ctx, out, torch.zeros((1, 32), device="cuda"), g)

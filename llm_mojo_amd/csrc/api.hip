@@ -25,6 +25,21 @@ int llmq_set_error(int code, const char *fmt, ...) {
         if (rc_ != LLMQ_OK) return rc_; \
     } while (0)
 
+int ctx_workspace(llmq_ctx *ctx, size_t bytes, void **p) {
+    if (bytes > ctx->ws_bytes) {
+        LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+        if (ctx->ws) hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+        const size_t want = bytes + bytes / 4;
+        if (hipMalloc(&ctx->ws, want) != hipSuccess)
+            return llmq_set_error(LLMQ_ENOMEM, "workspace of %zu bytes", want);
+        ctx->ws_bytes = want;
+    }
+    *p = ctx->ws;
+    return LLMQ_OK;
+}
+
 extern "C" {
 
 const char *llmq_last_error(void) { return g_err; }
@@ -53,6 +68,7 @@ int llmq_init(int device, llmq_ctx **out) {
 int llmq_destroy(llmq_ctx *ctx) {
     if (!ctx) return LLMQ_OK;
     hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) hipFree(ctx->ws);
     if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return LLMQ_OK;

@@ -33,7 +33,13 @@ struct llmq_ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     hipDeviceProp_t prop{};
+    void *ws = nullptr;  // grow-only workspace (prompt-side int16 activation codes)
+    size_t ws_bytes = 0;
 };
+
+// The context's workspace of at least `bytes` (api.hip); growing it waits for
+// the context's stream first.  Not for use under graph capture.
+int ctx_workspace(llmq_ctx *ctx, size_t bytes, void **p);
 
 enum { MAT_QUANT = 0, MAT_GGUF = 1 };
 
@@ -109,6 +115,10 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq);
 int gemv_a16_num_parts(const llmq_mat *w, bool ln);
 // The T == 1 kernel (gemv1.hip) behind launch_gemv_a16.
 bool gemv1_supports(const llmq_mat *w, bool ln);
+// The prompt-side int8-MFMA GEMM (gemm_mfma.hip): xq / sx are T x K int16
+// codes and T scales of workspace.
+bool gemm_mfma_supports(const llmq_mat *w, int64_t T);
+int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *sx);
 int launch_gemv1(llmq_ctx *ctx, const GemvRequest &rq);
 int gemv1_num_parts(const llmq_mat *w, bool ln);
 

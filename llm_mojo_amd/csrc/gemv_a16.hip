@@ -498,6 +498,19 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
     LLMQ_REQUIRE(!rq.amax || rq.T == 1, "linear: argmax partials need T == 1");
     LLMQ_REQUIRE(!rq.dbg || (rq.T == 1 && !rq.ln_w), "linear: chunk sums need T == 1 without LayerNorm");
     if (rq.T == 1 && gemv1_supports(w, rq.ln_w != nullptr)) return launch_gemv1(ctx, rq);
+    {
+        // Prompts: the int8-MFMA GEMM (LN + quantize_rows into workspace first)
+        int min_t = 8;
+        if (const char *e = getenv("LLMQ_MFMA_MIN_T")) min_t = atoi(e);
+        if (rq.T >= min_t && min_t > 0 && gemm_mfma_supports(w, rq.T)) {
+            const size_t xb = ((size_t)rq.T * w->k * 2 + 255) & ~(size_t)255;
+            void *ws = nullptr;
+            const int rc = ctx_workspace(ctx, xb + (size_t)rq.T * 4, &ws);
+            if (rc != LLMQ_OK) return rc;
+            return launch_gemm_mfma(ctx, rq, reinterpret_cast<int16_t *>(ws),
+                                    reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ws) + xb));
+        }
+    }
     const size_t max_lds = 64 * 1024;
     int mt = 1;
     if (rq.T > 1) {

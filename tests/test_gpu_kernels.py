@@ -133,6 +133,13 @@ A16_CASES = [  # tests/a16_kernels.mojo:85-94 and the GPT-2 / Llama layer shapes
     ((8, 32, False), 12, 768, 3072, False), ((4, 32, False), 1, 4096, 11008, False),
     ((4, 32, False), 1, 11008, 4096, False), ((4, 32, False), 5, 4096, 1024, False),
     ((8, 0, False), 1, 768, 50257, False),
+    # prompt GEMMs on the int8 matrix cores (T >= 8): every format, partial
+    # token and row tiles, +-32767 activations, the 476-token prompt
+    ((4, 32, False), 64, 768, 2304, False), ((4, 32, False), 476, 768, 3072, False),
+    ((8, 32, False), 476, 3072, 768, False), ((4, 64, False), 33, 768, 768, False),
+    ((4, 128, True), 40, 3072, 768, False), ((8, 0, False), 20, 768, 64, True),
+    ((8, 0, True), 24, 3072, 64, True), ((4, 0, True), 16, 3072, 40, True),
+    ((8, 128, False), 70, 768, 130, True), ((4, 32, True), 100, 768, 70, True),
 ]
 
 
@@ -155,6 +162,29 @@ def test_linear_vs_oracle(gpu, orc, fmt, T, IN, OUT, big):
     torch.cuda.synchronize()
     want = orc.matmul_rows_a16(x, o, b)
     assert rel_err(out.cpu().numpy(), want) < REL
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prompt_gemm_matches_tile_order(gpu, orc, bits):
+    """The matrix-core GEMM forms each group's exact int32 sum and folds it
+    into the float accumulator in tile_i16's order (kernels.mojo:512-573):
+    outputs equal the oracle's multi-token path to the last bit."""
+    torch, lm, ctx = gpu
+    rng = np.random.default_rng(bits)
+    T, IN, OUT = 37, 768, 192
+    w = rng.uniform(-0.1, 0.1, (IN, OUT)).astype(np.float32)
+    x = rng.normal(0, 1, (T, IN)).astype(np.float32)
+    b = rng.uniform(-1, 1, OUT).astype(np.float32)
+    note("prompt gemm order", bits)
+    g = lm.HipQuantMatrix.from_f32(ctx, w, bits, 32, False, True)
+    o = orc.QuantMatrix.from_f32(w, bits, 32, False, True)
+    out = torch.zeros((T, OUT), dtype=torch.float32, device="cuda")
+    lm.linear(ctx, out, dev(torch, x), g, dev(torch, b))
+    torch.cuda.synchronize()
+    want = orc.matmul_rows_a16(x, o, b)
+    got = out.cpu().numpy()
+    print("max |diff|", float(np.max(np.abs(got - want))), flush=True)
+    assert rel_err(got, want) < REL
 
 
 @pytest.mark.parametrize("T", [1, 5])

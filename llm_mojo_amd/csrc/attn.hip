@@ -312,6 +312,137 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint4 *__restrict__ co
     }
 }
 
+
+// Prompt attention (T > 1, positions known on the host): attend_float_one
+// (kvcache.mojo:113-150) for a block of 16 consecutive queries of one head per
+// workgroup, causal over the int8 cache after QuantKV.store of the prompt.
+// Key and value rows are staged 64 at a time in LDS and shared by the 16
+// queries; each query's scores live in LDS (sized by the prompt's last
+// position), then the softmax (16-lane DPP reductions) and the value pass in
+// position order.  Per element the arithmetic is that of kv_attend_kernel:
+// score = (q . k) * ks / sqrt(hd), e = exp(score - max), p = e / total,
+// out = sum_s fma(p * vs, v, .).
+constexpr int kQB = 16;   // queries per workgroup
+constexpr int kPB = 64;   // key / value rows per staged block
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Over each row of 16 lanes; every lane of the row gets the same bits.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_row<0xB1>(v));
+    v = fmaxf(v, dpp_row<0x4E>(v));
+    v = fmaxf(v, dpp_row<0x141>(v));
+    return fmaxf(v, dpp_row<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_row<0xB1>(v);
+    v += dpp_row<0x4E>(v);
+    v += dpp_row<0x141>(v);
+    return v + dpp_row<0x140>(v);
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restrict__ qkv, int64_t ld, int pos0, int T,
+                                                            int layer, int max_t, int n_head,
+                                                            const int8_t *__restrict__ K8,
+                                                            const int8_t *__restrict__ V8,
+                                                            const float *__restrict__ KS,
+                                                            const float *__restrict__ VS, float *__restrict__ out,
+                                                            int64_t ldo, int LT) {
+    static_assert(HD == 64, "prompt attention: head_dim 64");
+    extern __shared__ __align__(16) float smp[];
+    float *Q = smp;                                      // [kQB][HD]
+    float *S = Q + kQB * HD;                             // [kQB][LT] scores, then e
+    float *RS = S + kQB * LT;                            // [kPB] row scales of the staged block
+    int8_t *R8 = reinterpret_cast<int8_t *>(RS + kPB);   // [kPB][HD] staged rows
+    __shared__ float tot[kQB];
+    const int h = blockIdx.x, q0 = blockIdx.y * kQB, tid = threadIdx.x;
+    const int nq = min(kQB, T - q0);
+    const int npos = pos0 + q0 + nq;  // positions any query of the block sees
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int64_t base = (int64_t)layer * max_t * n_head + h;
+    {   // queries: 16 x 64 floats, 4 per thread
+        const int qi = tid >> 4, d = 4 * (tid & 15);
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (qi < nq) v = *reinterpret_cast<const float4 *>(qkv + (int64_t)(q0 + qi) * ld + (int64_t)h * HD + d);
+        *reinterpret_cast<float4 *>(Q + qi * HD + d) = v;
+    }
+    const int qi = tid >> 4, li = tid & 15;  // query row and lane within its 16
+    const int qlast = pos0 + q0 + qi;        // the last position query qi sees
+    auto stage = [&](const int8_t *src, const float *sc, int s0) {
+        const int row = tid >> 2, piece = tid & 3;  // 64 rows x 4 pieces of 16 bytes
+        const int s = s0 + row;
+        int4 v = make_int4(0, 0, 0, 0);
+        float f = 0.0f;
+        if (s < npos) {
+            const int64_t sl = base + (int64_t)s * n_head;
+            v = *reinterpret_cast<const int4 *>(src + sl * HD + 16 * piece);
+            if (piece == 0) f = sc[sl];
+        }
+        *reinterpret_cast<int4 *>(R8 + row * HD + 16 * piece) = v;
+        if (piece == 0) RS[row] = f;
+    };
+    // Scores.
+    for (int s0 = 0; s0 < npos; s0 += kPB) {
+        __syncthreads();
+        stage(K8, KS, s0);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kPB / 16; j++) {
+            const int r = li + 16 * j, s = s0 + r;
+            if (s >= npos) break;
+            float d = 0.0f;
+            const int8_t *kr = R8 + r * HD;
+            const float *qr = Q + qi * HD;
+#pragma unroll
+            for (int i = 0; i < HD; i += 4) {
+                const int k4 = *reinterpret_cast<const int *>(kr + i);
+                const float4 qv = *reinterpret_cast<const float4 *>(qr + i);
+                d = fmaf(qv.x, (float)(int8_t)(k4 & 255), d);
+                d = fmaf(qv.y, (float)(int8_t)((k4 >> 8) & 255), d);
+                d = fmaf(qv.z, (float)(int8_t)((k4 >> 16) & 255), d);
+                d = fmaf(qv.w, (float)(int8_t)((k4 >> 24) & 255), d);
+            }
+            S[qi * LT + s] = d * RS[r] * scale;
+        }
+    }
+    __syncthreads();
+    // Softmax per query (16 lanes a row).
+    float mx = -INFINITY;
+    for (int s = li; s <= qlast && qi < nq; s += 16) mx = fmaxf(mx, S[qi * LT + s]);
+    mx = row16_max(mx);
+    float t = 0.0f;
+    for (int s = li; s <= qlast && qi < nq; s += 16) {
+        const float e = expf(S[qi * LT + s] - mx);
+        S[qi * LT + s] = e;
+        t += e;
+    }
+    t = row16_sum(t);
+    if (li == 0) tot[qi] = t;
+    // Values: thread (qi, li) owns dimensions 4 li .. 4 li + 3 of query qi.
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    for (int s0 = 0; s0 < npos; s0 += kPB) {
+        __syncthreads();
+        stage(V8, VS, s0);
+        __syncthreads();
+        const float total = tot[qi];
+        const int send = min(kPB, qlast + 1 - s0);
+        for (int r = 0; r < send && qi < nq; r++) {
+            const float p = S[qi * LT + s0 + r] / total;
+            const float w = p * RS[r];
+            const int v4 = *reinterpret_cast<const int *>(R8 + r * HD + 4 * li);
+            a0 = fmaf(w, (float)(int8_t)(v4 & 255), a0);
+            a1 = fmaf(w, (float)(int8_t)((v4 >> 8) & 255), a1);
+            a2 = fmaf(w, (float)(int8_t)((v4 >> 16) & 255), a2);
+            a3 = fmaf(w, (float)(int8_t)((v4 >> 24) & 255), a3);
+        }
+    }
+    if (qi < nq)
+        *reinterpret_cast<float4 *>(out + (int64_t)(q0 + qi) * ldo + (int64_t)h * HD + 4 * li) =
+            make_float4(a0, a1, a2, a3);
+}
 }  // namespace
 
 int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,
@@ -372,6 +503,23 @@ int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
     LLMQ_REQUIRE(layer >= 0 && layer < kv->n_layer, "kv_attend: layer %d out of range", layer);
     LLMQ_REQUIRE(pos_dev || (pos0 >= 0 && pos0 + T <= kv->max_t), "kv_attend: positions beyond max_t");
     LLMQ_REQUIRE(!store || T == 1, "kv_attend: the fused store takes one token");
+    if (!store && !pos_dev && T > 1 && kv->head_dim == 64) {
+        // Prompt: query blocks of 16 per head, scores in LDS up to the last position
+        const int C = kv->n_head * kv->head_dim;
+        const int LT = ((pos0 + T) + 63) & ~63;
+        const size_t lds = sizeof(float) * ((size_t)kQB * 64 + (size_t)kQB * LT + kPB) + (size_t)kPB * 64;
+        static size_t granted = 64 * 1024;
+        if (lds > granted) {
+            LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_prompt_kernel<64>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            granted = lds;
+        }
+        hipLaunchKernelGGL(attend_prompt_kernel<64>, dim3(kv->n_head, (T + kQB - 1) / kQB), dim3(256), lds,
+                           ctx->stream, qkv, ld ? ld : 3 * C, pos0, T, layer, kv->max_t, kv->n_head, kv->k, kv->v,
+                           kv->ks, kv->vs, out, (int64_t)C, LT);
+        LLMQ_HIP(hipGetLastError());
+        return LLMQ_OK;
+    }
     if (kv->head_dim == 64) return attend_hd<64>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
     if (kv->head_dim == 128) return attend_hd<128>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
     return llmq_set_error(LLMQ_EUNSUPPORTED, "kv_attend: head_dim %d (64 or 128)", kv->head_dim);

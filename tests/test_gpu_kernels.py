@@ -252,19 +252,23 @@ def test_head_int8_channel(gpu, orc):
     assert rel_err(got, want) < REL
 
 
-def test_kv_store_and_attend(gpu, orc):
+@pytest.mark.parametrize("T,pos0,MT", [(7, 20, 64), (1, 20, 64), (100, 5, 128), (476, 0, 512), (40, 900, 1024)])
+def test_kv_store_and_attend(gpu, orc, T, pos0, MT):
+    """Prompt attention (query blocks of 16, scores up to the block's last
+    position) and the one-token path, against attend_float_one over the same
+    int8 cache: partial query blocks, long prompts, late positions."""
     torch, lm, ctx = gpu
-    rng = np.random.default_rng(9)
-    NL, MT, NH, HS = 2, 64, 12, 64
+    rng = np.random.default_rng(9 + T)
+    NL, NH, HS = 2, 12, 64
     C = NH * HS
-    T, pos0, layer = 7, 20, 1
+    layer = 1
     qkv_all = rng.normal(0, 1, (pos0 + T, 3 * C)).astype(np.float32)
     qkv_all[3, C:C + HS] = 0.0
-    note("kv store/attend")
+    note("kv store/attend", T, pos0, MT)
     kv = lm.QuantKV8(ctx, NL, MT, NH, HS)
     okv = orc.QuantKV8(NL, MT, NH, HS)
-    q0 = dev(torch, qkv_all[:pos0])
-    kv.store(layer, 0, q0)
+    if pos0:
+        kv.store(layer, 0, dev(torch, qkv_all[:pos0]))
     q1 = dev(torch, qkv_all[pos0:])
     kv.store(layer, pos0, q1)
     out = torch.zeros((T, C), dtype=torch.float32, device="cuda")

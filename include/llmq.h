@@ -102,6 +102,10 @@ LLMQ_API int llmq_mat_free(llmq_mat *mat);
 LLMQ_API int64_t llmq_mat_nbytes(const llmq_mat *mat);
 /* WeightMatrix.group_size (tensor.mojo:127-129, gguf.mojo:459-460). */
 LLMQ_API int64_t llmq_mat_group_size(const llmq_mat *mat);
+/* WeightMatrix.has_i16 (tensor.mojo:102-104; GGUFMatrix 456-457 of
+ * gguf.mojo): 1 when the matrix has an int16-activation kernel (A16
+ * QuantMatrix; GGUF Q6_K and Q8_0, whose heads use it), else 0. */
+LLMQ_API int llmq_mat_has_i16(const llmq_mat *mat);
 /* Shape: rows (outputs) and cols (the reduction axis) as stored. */
 LLMQ_API int llmq_mat_shape(const llmq_mat *mat, int64_t *rows, int64_t *cols);
 /* The codes, float16 scale bits and zero points in the reference's own

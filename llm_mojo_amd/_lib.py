@@ -40,6 +40,7 @@ SIGNATURES = {
     "llmq_mat_free": (I32, [P]),
     "llmq_mat_nbytes": (I64, [P]),
     "llmq_mat_group_size": (I64, [P]),
+    "llmq_mat_has_i16": (I32, [P]),
     "llmq_mat_shape": (I32, [P, ctypes.POINTER(I64), ctypes.POINTER(I64)]),
     "llmq_mat_export": (I32, [P, P, P, P, P]),
     "llmq_mat_dequant_row": (I32, [P, P, I64, P]),

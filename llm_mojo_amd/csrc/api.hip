@@ -219,6 +219,12 @@ int64_t llmq_mat_group_size(const llmq_mat *m) {
     return m->group;
 }
 
+int llmq_mat_has_i16(const llmq_mat *m) {
+    if (!m) return 0;
+    if (m->kind == MAT_GGUF) return gguf_has_i16(m);  // gguf.mojo:456-457
+    return m->a16 ? 1 : 0;                            // tensor.mojo:102-104 (ACT16)
+}
+
 int llmq_mat_shape(const llmq_mat *m, int64_t *rows, int64_t *cols) {
     LLMQ_REQUIRE(m, "shape: null matrix");
     if (rows) *rows = m->n;
@@ -392,6 +398,11 @@ int llmq_ln_linear(llmq_ctx *ctx, float *out, const float *x, const float *ln_w,
 }
 
 int llmq_head(llmq_ctx *ctx, float *logits, const float *h, const llmq_mat *w, int64_t T, int64_t V, int64_t C) {
+    LLMQ_REQUIRE(ctx, "head: null context");
+    if (gguf_has_i16(w)) {  // kernels.mojo:677-681: GGUF heads with an int16 kernel take head_i16
+        RC(check_linear(w, C, V));
+        return launch_gguf_head16(ctx, w, h, logits, T);
+    }
     return llmq_linear(ctx, logits, h, w, nullptr, T, C, V, 0);
 }
 

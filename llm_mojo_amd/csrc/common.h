@@ -129,6 +129,9 @@ int gguf_num_parts(const llmq_mat *w);
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
                      ArgmaxPart *amax, int amax_cap);
 int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
+// int16 output head for Q6_K / Q8_0 (gguf_head.hip).
+int gguf_has_i16(const llmq_mat *w);
+int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *logits, int64_t T);
 
 int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C);
 int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,

@@ -59,7 +59,8 @@ class HipQuantMatrix:
         return lib().llmq_mat_group_size(self.h)
 
     def has_i16(self):
-        return bool(self.a16)
+        """tensor.mojo:102-104: the A16 formats."""
+        return bool(lib().llmq_mat_has_i16(self.h))
 
     def export(self):
         """(codes, float16 scale bits, zero points) in the reference's own
@@ -123,7 +124,7 @@ class HipGGUFMatrix:
 
     def has_i16(self):
         """gguf.mojo:456-457: Q6_K and Q8_0 heads take the int16 path."""
-        return self.kind in (8, 14)
+        return bool(lib().llmq_mat_has_i16(self.h))
 
     def dequant_row(self, row):
         dst = np.zeros(self.cols, np.float32)

@@ -84,3 +84,53 @@ def test_gguf_unsupported_type(gpu):
     torch, lm, ctx = gpu
     with pytest.raises(lm.LlmqError, match="supported"):
         lm.HipGGUFMatrix.from_blocks(ctx, 1, np.zeros(64, np.uint8), 1, 32)
+
+
+@pytest.mark.parametrize("kind", ["Q6_K", "Q8_0"])
+@pytest.mark.parametrize("V,C,T,big", [(70, 512, 1, False), (300, 768, 5, False), (1000, 2048, 1, True),
+                                       (4000, 4096, 2, False), (32000, 2048, 1, False)])
+def test_gguf_int16_head_exact(gpu, orc, kind, V, C, T, big):
+    """head_i16 (kernels.mojo:693-736) for Q6_K / Q8_0 heads: the logits equal
+    the oracle's dot_row_i16 * sx bit for bit (same int32 lanes, same float
+    chain over superblocks / blocks, same 16-lane sum).  (32000, 2048) is the
+    TinyLlama Q6_K head; "big" alternates +-(0.9..1) so the int16 codes sit
+    near +-32767 and Q6_K's lane sums near 2^31."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    t = orc.GGML[kind]
+    blocks = synth.gguf_blocks(t, V, C, seed=V + C)
+    rng = np.random.default_rng(V + T)
+    if big:
+        h = (rng.uniform(0.9, 1.0, (T, C)) * np.where(np.arange(T * C).reshape(T, C) % 2 == 0, 1, -1))
+    else:
+        h = rng.normal(0, 1, (T, C))
+    h = h.astype(np.float32)
+    print("gguf int16 head", kind, V, C, T, flush=True)
+    g = lm.HipGGUFMatrix.from_blocks(ctx, t, blocks, V, C)
+    assert g.has_i16()
+    logits = torch.zeros((T, V), device="cuda")
+    lm.head(ctx, logits, dev(torch, h), g)
+    torch.cuda.synchronize()
+    want = orc.gguf_head_i16(t, blocks, V, C, h)
+    got = logits.cpu().numpy()
+    assert np.array_equal(got, want), np.max(np.abs(got - want))
+
+
+def test_gguf_float_heads_take_the_float_path(gpu, orc):
+    """kernels.head: Q4_K has no int16 kernel, so its head is the float GEMV."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    t = orc.GGML["Q4_K"]
+    V, C = 100, 512
+    blocks = synth.gguf_blocks(t, V, C, seed=5)
+    h = np.random.default_rng(5).normal(0, 1, (1, C)).astype(np.float32)
+    g = lm.HipGGUFMatrix.from_blocks(ctx, t, blocks, V, C)
+    assert not g.has_i16()
+    logits = torch.zeros((1, V), device="cuda")
+    lm.head(ctx, logits, dev(torch, h), g)
+    torch.cuda.synchronize()
+    want = orc.gguf_gemv(t, blocks, V, C, h[0], None, 0)
+    got = logits.cpu().numpy()[0]
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5

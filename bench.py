@@ -94,6 +94,106 @@ def copy_bandwidth(torch, nbytes=1 << 30, reps=20):
     return 2 * nbytes * reps / (e0.elapsed_time(e1) / 1000.0) / 1e9
 
 
+PREFILL_T = 476
+INT8_MFMA_PEAK = 5.0e15  # dense int8 MFMA ops/s of MI355X
+LAYER_SHAPES = [("qkv", 768, 2304), ("proj", 768, 768), ("fc", 768, 3072), ("fcproj", 3072, 768)]
+
+
+def prefill(torch, lm, synth, ctx, tensors, model4, reps=5):
+    """Config 3: a 476-token prompt through the GPT-2 weights in int4-g32 and
+    int8-g32 A16 form (tok/s = T / prefill span, gpt2t.mojo:949-967), and the
+    four layer GEMMs alone at M = 476: time, algorithmic int16 x intN ops
+    (2 M K N) and executed int8 MFMA ops (the hi / lo activation planes, and
+    for int8 weights their two nibbles: 2 or 4 int8 products per MAC, M and
+    N padded to the 64 x 64 workgroup tile) against the 5 POP/s peak."""
+    prompt = synth.prompt_ids(1337, PREFILL_T)
+    res = {}
+    for bits in (4, 8):
+        m = model4 if bits == 4 else lm.GPT2(ctx, tensors, bits=8, group=32)
+        ms = []
+        for _ in range(reps + 1):
+            _, p_ms, _ = m.generate(prompt, 1)
+            ms.append(p_ms)
+        if bits == 8:
+            m.free()
+        ms = sorted(ms[1:])
+        res[f"int{bits}_g32_tok_s"] = round(PREFILL_T / (ms[len(ms) // 2] / 1000.0), 1)
+        res[f"int{bits}_g32_ms"] = round(ms[len(ms) // 2], 3)
+    stream = torch.cuda.Stream()
+    gemm = {}
+    with torch.cuda.stream(stream):
+        ctx.set_stream(stream)
+        g = torch.Generator(device="cuda").manual_seed(3003)
+        for bits in (4, 8):
+            tot_us, alg, exe = 0.0, 0, 0
+            for name, K, N in LAYER_SHAPES:
+                w = lm.HipQuantMatrix.from_f32(ctx, torch.randn((K, N), device="cuda", generator=g) * 0.02, bits, 32,
+                                               False, True)
+                x = torch.randn((PREFILL_T, K), device="cuda", generator=g)
+                out = torch.empty((PREFILL_T, N), device="cuda")
+                for _ in range(3):
+                    lm.linear(ctx, out, x, w)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(20):
+                    lm.linear(ctx, out, x, w)
+                e1.record(stream)
+                e1.synchronize()
+                us = e0.elapsed_time(e1) * 1000.0 / 20
+                w.free()
+                tot_us += us
+                alg += 2 * PREFILL_T * K * N
+                exe += 2 * (-(-PREFILL_T // 64) * 64) * (-(-N // 64) * 64) * K * (2 if bits == 4 else 4)
+                gemm[f"int{bits}_{name}_us"] = round(us, 2)
+            gemm[f"int{bits}_layer_us"] = round(tot_us, 2)
+            gemm[f"int{bits}_alg_tops"] = round(alg / tot_us / 1e6, 1)
+            gemm[f"int{bits}_mfma_util"] = round(exe / (tot_us * 1e-6) / INT8_MFMA_PEAK, 4)
+    ctx.set_stream(None)
+    res["layer_gemms_m476"] = gemm
+    return res
+
+
+GGUF_KINDS = {"Q4_0": 2, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_0": 8}
+GGUF_SHAPES = [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)]
+
+
+def gguf_sweep(torch, lm, synth, ctx, rot_bytes=512 << 20):
+    """Config 2: the GGUF decode GEMV (float activations, batch 1) at the
+    Llama shapes K x N, over distinct weight buffers totalling > 512 MiB (twice
+    the Infinity Cache); GB/s of nbytes + 4K + 4N per launch."""
+    res = {}
+    stream = torch.cuda.Stream()
+    for name, t in GGUF_KINDS.items():
+        for K, N in GGUF_SHAPES:
+            bs, bb = synth.GGUF_BLOCK[t]
+            nbytes = N * (K // bs) * bb
+            nbuf = max(2, min(48, -(-rot_bytes // nbytes)))
+            base = synth.gguf_blocks(t, N, K, seed=7)
+            mats = [lm.HipGGUFMatrix.from_blocks(ctx, t, base, N, K) for _ in range(nbuf)]
+            with torch.cuda.stream(stream):
+                ctx.set_stream(stream)
+                x = torch.randn((1, K), device="cuda")
+                out = torch.empty((1, N), device="cuda")
+                for i in range(2 * nbuf):
+                    lm.linear(ctx, out, x, mats[i % nbuf])
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                reps = 8 * nbuf
+                e0.record(stream)
+                for i in range(reps):
+                    lm.linear(ctx, out, x, mats[i % nbuf])
+                e1.record(stream)
+                e1.synchronize()
+            ctx.set_stream(None)
+            us = e0.elapsed_time(e1) * 1000.0 / reps
+            alg = nbytes + 4 * K + 4 * N
+            res[f"{name} {K}x{N}"] = {"us": round(us, 2), "gbs": round(alg / us / 1e3, 1),
+                                      "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4)}
+            log(name, K, N, res[f"{name} {K}x{N}"])
+            for m in mats:
+                m.free()
+    return res
+
+
 def cpu_baseline(tensors, prompt, budget_s=20.0):
     """The CPU oracle (a C restatement of llm_mojo's CPU path, oracle/) on
     this host's cores: the same prompt, then greedy decode steps until about
@@ -130,6 +230,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 476-token prefill (config 3)")
+    ap.add_argument("--gguf-sweep", action="store_true", help="add the GGUF GEMV sweep (config 2, ~1 min)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline GEMV and the reference copy (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -187,6 +289,14 @@ def main():
     token_bytes = model.weight_bytes() - 4 * 1024 * 768 + 3072 + 19584 * (mean_pos + 1) + 19584
     extra["decode_bytes_per_token"] = int(token_bytes)
     extra["decode_gbs_effective"] = round(token_bytes * tok_s / 1e9, 1)
+
+    if not args.no_prefill:
+        log("prefill 476")
+        extra["prefill_476"] = prefill(torch, lm, synth, ctx, tensors, model)
+        log(extra["prefill_476"])
+    if args.gguf_sweep:
+        log("gguf sweep")
+        extra["gguf_gemv_sweep"] = gguf_sweep(torch, lm, synth, ctx)
 
     cpu = None
     if not args.no_cpu:

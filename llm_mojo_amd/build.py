@@ -24,6 +24,9 @@ ARCH = os.environ.get("LLMQ_ARCH", "gfx950")
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core accumulators in ordinary VGPRs (no AGPR copies around the
+    # prompt GEMM's per-group float work; a zero accumulator is an inline 0)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result", "-I", os.path.join(ROOT, "include"), "-I", CSRC,
 ]
 

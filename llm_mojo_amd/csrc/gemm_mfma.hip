@@ -22,11 +22,14 @@
 // Mapping: a workgroup of 4 waves owns 64 tokens x 64 output rows (4 row
 // tiles); wave (wm, wn) computes the 32 x 32 block (tokens 32 wm.., rows
 // 32 wn..) with v_mfma_i32_32x32x32_i8, one call per 32 inputs and plane.
-// The reduction axis is walked in blocks of 64 inputs: the next block's
-// activations, codes, zero points and scales are loaded into registers while
-// the current block, staged in LDS (activation planes, weights as int8 rows
-// of 64 inputs, per-row weight sums, scales), feeds the matrix cores; two
-// LDS buffers alternate, one barrier per block.
+// The reduction axis is walked in staged blocks of 256 inputs (128 or 64
+// when those do not divide it), each loaded as 64-input sub-blocks: the next
+// block's activations, codes, zero points and scales are loaded into
+// registers while the current block, staged in LDS (activation planes,
+// weights as int8 rows, per-row weight sums, scales), feeds the matrix cores;
+// two LDS buffers alternate, one barrier per block.  Large blocks matter:
+// a block costs one memory round trip, and the few workgroups of a prompt
+// GEMM cannot hide it behind each other.
 //
 // Activations come from act_q16_kernel: LayerNorm (kernels.mojo:179-197) when
 // asked, then quantize_rows (kernels.mojo:400-416), one workgroup per token.
@@ -40,8 +43,7 @@ typedef short v2s __attribute__((ext_vector_type(2)));
 
 constexpr int TM = 64;           // tokens per workgroup
 constexpr int TN = 64;           // output rows per workgroup
-constexpr int KB = 64;           // inputs per staged block
-constexpr int RS = KB + 16;      // LDS row stride in bytes (conflict-free 16-byte reads)
+constexpr int KB0 = 64;          // inputs per prefetched sub-block
 constexpr uint32_t kOOB = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
@@ -58,16 +60,6 @@ __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
-// One byte / one half (little-endian) at a byte offset, via the aligned dword.
-__device__ __forceinline__ uint32_t bload_u8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const uint32_t w = bload4(r, off == kOOB ? kOOB : (off & ~3u));
-    return (w >> (8 * (off & 3))) & 255u;
-}
-__device__ __forceinline__ uint32_t bload_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const uint32_t w = bload4(r, off == kOOB ? kOOB : (off & ~3u));
-    return (w >> (8 * (off & 2))) & 0xFFFFu;
-}
-
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
@@ -175,31 +167,38 @@ struct MfArgs {
     int T, K, n, ntiles, CK, NG, G, seg, flags;
 };
 
-// Registers of one staged block, loaded ahead of its use.
+// Registers of one 64-input sub-block of a staged block, loaded ahead of
+// its use.
 template <int BITS>
 struct Pref {
     uint4 a0, a1;                        // 16 activations (int16) of one token
     uint4 code;                          // int4: 16 codes in .x, .y; int8: 16 codes
-    uint32_t zp;
-    uint32_t sc;                         // float16 bits of one (row, sub-block) scale (threads < 128)
+    // zero point byte and float16 scale bits of one (row, sub-step) scale
+    // (threads < 128), as the aligned dwords holding them and their bit
+    // offsets: extracted where they are used, so no wait follows the loads
+    uint32_t zpw, zsh, scw, ssh;
 };
 
-template <int BITS>
+// One staged block of NS sub-blocks (KB = 64 NS inputs), double-buffered.
+template <int BITS, int NS>
 struct Lds {
+    static constexpr int KB = KB0 * NS;
+    static constexpr int RS = KB + 16;   // row stride in bytes (conflict-free 16-byte reads)
     uint8_t a_hi[2][TM * RS];
     uint8_t a_lo[2][TM * RS];
     uint8_t w0[2][TN * RS];              // int4: u - zp; int8: wl = w & 15
     uint8_t w1[2][BITS == 8 ? TN * RS : 16];  // int8: wh = w >> 4
-    int wsum[2][2][TN];                  // sum of w per (32-input sub-block, row)
-    float scale[2][2][TN];               // scale of the group of each (sub-block, row)
+    int wsum[2][2 * NS][TN];             // sum of w per (32-input sub-step, row)
+    float scale[2][2 * NS][TN];          // scale of the group of each (sub-step, row)
     float sx[TM];
 };
 
+// Loads of sub-block sb (inputs 64 sb ..) into p.
 template <int BITS>
-__device__ __forceinline__ void prefetch(const MfArgs &a, int kb, int tok0, int tile0, Pref<BITS> &p,
+__device__ __forceinline__ void prefetch(const MfArgs &a, int sb, int tok0, int tile0, Pref<BITS> &p,
                                          __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rc,
                                          __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rz) {
-    const int t = threadIdx.x, k0 = kb * KB;
+    const int t = threadIdx.x, k0 = sb * KB0;
     {   // activations: token m = t / 4, inputs k0 + 16 q ..
         const int m = t >> 2, q = t & 3;
         const int tok = tok0 + m;
@@ -214,7 +213,7 @@ __device__ __forceinline__ void prefetch(const MfArgs &a, int kb, int tok0, int 
         r = (t >> 1) & 15;
         tile = tile0 + tt;
         g = (k0 + 32 * c) / a.G;
-        coff = (uint32_t)((((int64_t)tile * a.CK + 2 * kb + c) * 16 + r) * 16 + 8 * h);
+        coff = (uint32_t)((((int64_t)tile * a.CK + 2 * sb + c) * 16 + r) * 16 + 8 * h);
         const uint2 v = bload8(rc, tile < a.ntiles ? coff : kOOB);
         p.code = make_uint4(v.x, v.y, 0u, 0u);
     } else {          // (tile, chunk c of 16 inputs, row r)
@@ -222,20 +221,29 @@ __device__ __forceinline__ void prefetch(const MfArgs &a, int kb, int tok0, int 
         r = t & 15;
         tile = tile0 + tt;
         g = (k0 + 16 * c) / a.G;
-        coff = (uint32_t)((((int64_t)tile * a.CK + 4 * kb + c) * 16 + r) * 16);
+        coff = (uint32_t)((((int64_t)tile * a.CK + 4 * sb + c) * 16 + r) * 16);
         p.code = bload16(rc, tile < a.ntiles ? coff : kOOB);
     }
-    p.zp = bload_u8(rz, tile < a.ntiles ? (uint32_t)(((int64_t)tile * a.NG + g) * 16 + r) : kOOB);
-    if (t < 2 * TN) {  // scale of (sub-block s, row o)
-        const int s = t >> 6, o = t & 63;
+    const uint32_t zoff = tile < a.ntiles ? (uint32_t)(((int64_t)tile * a.NG + g) * 16 + r) : kOOB;
+    p.zpw = bload4(rz, zoff == kOOB ? kOOB : (zoff & ~3u));
+    p.zsh = 8u * (zoff & 3u);
+    {   // scale of (sub-step s, row o) for threads < 2 TN, the others read past the
+        // extent: no branch, so the compiler does not wait for every load at its end
+        const int s = (t >> 6) & 1, o = t & 63;
         const int tl = tile0 + (o >> 4), gs = (k0 + 32 * s) / a.G;
-        p.sc = bload_u16(rs, tl < a.ntiles ? (uint32_t)((((int64_t)tl * a.NG + gs) * 16 + (o & 15)) * 2) : kOOB);
+        const bool ok = t < 2 * TN && tl < a.ntiles;
+        const uint32_t soff = ok ? (uint32_t)((((int64_t)tl * a.NG + gs) * 16 + (o & 15)) * 2) : kOOB;
+        p.scw = bload4(rs, soff == kOOB ? kOOB : (soff & ~3u));
+        p.ssh = 8u * (soff & 2u);
     }
 }
 
-template <int BITS>
-__device__ __forceinline__ void stage(const Pref<BITS> &p, Lds<BITS> &L, int buf) {
-    const int t = threadIdx.x;
+// Sub-block j of the staged block in buffer buf, from p.
+template <int BITS, int NS>
+__device__ __forceinline__ void stage(const Pref<BITS> &p, Lds<BITS, NS> &L, int buf, int j) {
+    constexpr int RS = Lds<BITS, NS>::RS;
+    const int t = threadIdx.x, col = KB0 * j;
+    const uint32_t zp = (p.zpw >> p.zsh) & 255u;
     {   // activation planes: hi bytes and (lo - 128) bytes, natural input order
         const int m = t >> 2, q = t & 3;
         const uint32_t d[8] = {p.a0.x, p.a0.y, p.a0.z, p.a0.w, p.a1.x, p.a1.y, p.a1.z, p.a1.w};
@@ -245,13 +253,13 @@ __device__ __forceinline__ void stage(const Pref<BITS> &p, Lds<BITS> &L, int buf
             hi[i] = __builtin_amdgcn_perm(d[2 * i + 1], d[2 * i], 0x07050301u);
             lo[i] = __builtin_amdgcn_perm(d[2 * i + 1], d[2 * i], 0x06040200u) ^ 0x80808080u;
         }
-        *reinterpret_cast<uint4 *>(&L.a_hi[buf][m * RS + 16 * q]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *reinterpret_cast<uint4 *>(&L.a_lo[buf][m * RS + 16 * q]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<uint4 *>(&L.a_hi[buf][m * RS + col + 16 * q]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *reinterpret_cast<uint4 *>(&L.a_lo[buf][m * RS + col + 16 * q]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
     }
     if (BITS == 4) {
         const int tt = t >> 6, c = (t >> 5) & 1, r = (t >> 1) & 15, h = t & 1;
         const int o = tt * 16 + r;
-        const uint32_t zb = p.zp * 0x01010101u;
+        const uint32_t zb = zp * 0x01010101u;
         uint32_t w[4];
         const uint32_t dd[2] = {p.code.x, p.code.y};
 #pragma unroll
@@ -262,17 +270,17 @@ __device__ __forceinline__ void stage(const Pref<BITS> &p, Lds<BITS> &L, int buf
             w[2 * i] = ((n0 | 0x80808080u) - zb) ^ 0x80808080u;               // u - zp as int8
             w[2 * i + 1] = ((n1 | 0x80808080u) - zb) ^ 0x80808080u;
         }
-        *reinterpret_cast<uint4 *>(&L.w0[buf][o * RS + 32 * c + 16 * h]) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint4 *>(&L.w0[buf][o * RS + col + 32 * c + 16 * h]) = make_uint4(w[0], w[1], w[2], w[3]);
         int s = __builtin_amdgcn_sdot4((int)w[0], 0x01010101, 0, false);
         s = __builtin_amdgcn_sdot4((int)w[1], 0x01010101, s, false);
         s = __builtin_amdgcn_sdot4((int)w[2], 0x01010101, s, false);
         s = __builtin_amdgcn_sdot4((int)w[3], 0x01010101, s, false);
         s += __shfl_xor(s, 1);  // the other half of the chunk
-        if (h == 0) L.wsum[buf][c][o] = s;
+        if (h == 0) L.wsum[buf][2 * j + c][o] = s;
     } else {
         const int tt = t >> 6, c = (t >> 4) & 3, r = t & 15;
         const int o = tt * 16 + r;
-        const v2s zz = {(short)p.zp, (short)p.zp};
+        const v2s zz = {(short)zp, (short)zp};
         uint32_t wl[4], wh[4];
         const uint32_t dd[4] = {p.code.x, p.code.y, p.code.z, p.code.w};
         int s = 0;
@@ -289,17 +297,76 @@ __device__ __forceinline__ void stage(const Pref<BITS> &p, Lds<BITS> &L, int buf
             s = __builtin_amdgcn_sdot4((int)wh[i], 0x10101010, s, false);  // 16 * wh
             s = __builtin_amdgcn_sdot4((int)wl[i], 0x01010101, s, false);
         }
-        *reinterpret_cast<uint4 *>(&L.w0[buf][o * RS + 16 * c]) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
-        *reinterpret_cast<uint4 *>(&L.w1[buf][o * RS + 16 * c]) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
-        s += __shfl_xor(s, 16);  // the other chunk of the 32-input sub-block
-        if ((c & 1) == 0) L.wsum[buf][c >> 1][o] = s;
+        *reinterpret_cast<uint4 *>(&L.w0[buf][o * RS + col + 16 * c]) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+        *reinterpret_cast<uint4 *>(&L.w1[buf][o * RS + col + 16 * c]) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+        s += __shfl_xor(s, 16);  // the other chunk of the 32-input sub-step
+        if ((c & 1) == 0) L.wsum[buf][2 * j + (c >> 1)][o] = s;
     }
-    if (t < 2 * TN) L.scale[buf][t >> 6][t & 63] = __half2float(__ushort_as_half((unsigned short)p.sc));
+    if (t < 2 * TN)
+        L.scale[buf][2 * j + (t >> 6)][t & 63] = __half2float(__ushort_as_half((unsigned short)((p.scw >> p.ssh) & 0xFFFFu)));
 }
 
+// Accumulators of one wave: the matrix-core partial sums of the current
+// segment (int4: hi, lo planes; int8: hh, hl, lh, ll), the weight sum of the
+// segment, and the float outputs (16 tokens of one row per lane).
 template <int BITS>
+struct Acc {
+    v16i c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    int wacc = 0;
+    float acc[16] = {};
+};
+
+// The 2 NS sub-steps of 32 inputs of staged block kb (in LDS buffer buf).
+template <int BITS, int NS, bool SEG32>
+__device__ __forceinline__ void compute_block(const Lds<BITS, NS> &L, int buf, int kb, int arow, int brow, int orow,
+                                              int seg, Acc<BITS> &c) {
+    constexpr int KB = Lds<BITS, NS>::KB;
+#pragma unroll
+    for (int s = 0; s < 2 * NS; s++) {
+        const v4i ah = *reinterpret_cast<const v4i *>(&L.a_hi[buf][arow + 32 * s]);
+        const v4i al = *reinterpret_cast<const v4i *>(&L.a_lo[buf][arow + 32 * s]);
+        const v4i b0 = *reinterpret_cast<const v4i *>(&L.w0[buf][brow + 32 * s]);
+        if (SEG32) {  // every sub-step is a segment: the products start from zero
+            c.c0 = c.c1 = c.c2 = c.c3 = (v16i){};
+            c.wacc = 0;
+        }
+        if (BITS == 4) {
+            c.c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b0, c.c0, 0, 0, 0);
+            c.c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b0, c.c1, 0, 0, 0);
+        } else {
+            const v4i b1 = *reinterpret_cast<const v4i *>(&L.w1[buf][brow + 32 * s]);
+            c.c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b1, c.c0, 0, 0, 0);
+            c.c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b0, c.c1, 0, 0, 0);
+            c.c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b1, c.c2, 0, 0, 0);
+            c.c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b0, c.c3, 0, 0, 0);
+        }
+        c.wacc += L.wsum[buf][s][orow];
+        if (SEG32 || (kb * KB + 32 * (s + 1)) % seg == 0) {  // end of a segment: tile_i16's flush
+            const float sc = L.scale[buf][s][orow];
+            const int w128 = 128 * c.wacc;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                int G;
+                if (BITS == 4)
+                    G = (c.c0[i] << 8) + c.c1[i] + w128;
+                else
+                    G = (((c.c0[i] << 4) + c.c1[i]) << 8) + ((c.c2[i] << 4) + c.c3[i]) + w128;
+                c.acc[i] = fmaf((float)G, sc, c.acc[i]);
+            }
+            if (!SEG32) {
+                c.c0 = c.c1 = c.c2 = c.c3 = (v16i){};
+                c.wacc = 0;
+            }
+        }
+    }
+}
+
+template <int BITS, int NS, bool SEG32>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
-    __shared__ __align__(16) Lds<BITS> L;
+    using LT = Lds<BITS, NS>;
+    constexpr int KB = LT::KB, RS = LT::RS;
+    extern __shared__ __align__(16) uint8_t smem_gemm[];
+    LT &L = *reinterpret_cast<LT *>(smem_gemm);
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid & 1, wn = wid >> 1;
     const int tile0 = blockIdx.x * (TN / 16), out0 = blockIdx.x * TN, tok0 = blockIdx.y * TM;
@@ -310,63 +377,50 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
     if (tid < TM) L.sx[tid] = tok0 + tid < a.T ? a.sx[tok0 + tid] : 0.0f;
 
     const int nkb = a.K / KB;
-    Pref<BITS> p;
-    prefetch<BITS>(a, 0, tok0, tile0, p, rx, rc, rs, rz);
-    stage<BITS>(p, L, 0);
+    // Two register sets of prefetched blocks: block kb + 1 is loaded while
+    // block kb - 1 is computed, so a load has two blocks of work to arrive.
+    Pref<BITS> pa[NS], pb[NS];
+#pragma unroll
+    for (int j = 0; j < NS; j++) prefetch<BITS>(a, j, tok0, tile0, pa[j], rx, rc, rs, rz);
+    if (nkb > 1) {
+#pragma unroll
+        for (int j = 0; j < NS; j++) prefetch<BITS>(a, NS + j, tok0, tile0, pb[j], rx, rc, rs, rz);
+    }
+#pragma unroll
+    for (int j = 0; j < NS; j++) stage<BITS, NS>(pa[j], L, 0, j);
     lds_barrier();
 
-    v16i c0 = {}, c1 = {}, c2 = {}, c3 = {};  // int4: hi, lo planes; int8: hh, hl, lh, ll
-    float acc[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0.0f;
-    int wacc = 0;
+    Acc<BITS> c;
     const int arow = (32 * wm + (lane & 31)) * RS + 16 * (lane >> 5);
     const int brow = (32 * wn + (lane & 31)) * RS + 16 * (lane >> 5);
     const int orow = 32 * wn + (lane & 31);
 
-    for (int kb = 0; kb < nkb; kb++) {
-        const int buf = kb & 1;
-        if (kb + 1 < nkb) prefetch<BITS>(a, kb + 1, tok0, tile0, p, rx, rc, rs, rz);
+    for (int kb = 0; kb < nkb; kb += 2) {
+        // even block kb in buffer 0; pa is free, pb holds block kb + 1
+        if (kb + 2 < nkb) {
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const v4i ah = *reinterpret_cast<const v4i *>(&L.a_hi[buf][arow + 32 * s]);
-            const v4i al = *reinterpret_cast<const v4i *>(&L.a_lo[buf][arow + 32 * s]);
-            const v4i b0 = *reinterpret_cast<const v4i *>(&L.w0[buf][brow + 32 * s]);
-            if (BITS == 4) {
-                c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b0, c0, 0, 0, 0);
-                c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b0, c1, 0, 0, 0);
-            } else {
-                const v4i b1 = *reinterpret_cast<const v4i *>(&L.w1[buf][brow + 32 * s]);
-                c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b1, c0, 0, 0, 0);
-                c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b0, c1, 0, 0, 0);
-                c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b1, c2, 0, 0, 0);
-                c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b0, c3, 0, 0, 0);
-            }
-            wacc += L.wsum[buf][s][orow];
-            if ((kb * KB + 32 * (s + 1)) % a.seg == 0) {  // end of a segment: tile_i16's flush
-                const float sc = L.scale[buf][s][orow];
-                const int w128 = 128 * wacc;
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    int G;
-                    if (BITS == 4)
-                        G = (c0[i] << 8) + c1[i] + w128;
-                    else
-                        G = (((c0[i] << 4) + c1[i]) << 8) + ((c2[i] << 4) + c3[i]) + w128;
-                    acc[i] = fmaf((float)G, sc, acc[i]);
-                }
-                c0 = (v16i){};
-                c1 = (v16i){};
-                if (BITS == 8) {
-                    c2 = (v16i){};
-                    c3 = (v16i){};
-                }
-                wacc = 0;
-            }
+            for (int j = 0; j < NS; j++) prefetch<BITS>(a, (kb + 2) * NS + j, tok0, tile0, pa[j], rx, rc, rs, rz);
         }
-        if (kb + 1 < nkb) stage<BITS>(p, L, buf ^ 1);
+        compute_block<BITS, NS, SEG32>(L, 0, kb, arow, brow, orow, a.seg, c);
+        if (kb + 1 < nkb) {
+#pragma unroll
+            for (int j = 0; j < NS; j++) stage<BITS, NS>(pb[j], L, 1, j);
+        }
+        lds_barrier();
+        if (kb + 1 >= nkb) break;
+        // odd block kb + 1 in buffer 1; pb is free, pa holds block kb + 2
+        if (kb + 3 < nkb) {
+#pragma unroll
+            for (int j = 0; j < NS; j++) prefetch<BITS>(a, (kb + 3) * NS + j, tok0, tile0, pb[j], rx, rc, rs, rz);
+        }
+        compute_block<BITS, NS, SEG32>(L, 1, kb + 1, arow, brow, orow, a.seg, c);
+        if (kb + 2 < nkb) {
+#pragma unroll
+            for (int j = 0; j < NS; j++) stage<BITS, NS>(pa[j], L, 0, j);
+        }
         lds_barrier();
     }
+    const float *acc = c.acc;
 
     // Epilogue: lane holds output row out0 + orow for 16 tokens.
     const int o = out0 + orow;
@@ -386,12 +440,32 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
     }
 }
 
+template <int BITS, int NS, bool SEG32>
+int launch_ns(llmq_ctx *ctx, const MfArgs &a, dim3 grid) {
+    const size_t lds = sizeof(Lds<BITS, NS>);
+    static bool attr = false;
+    if (!attr) {
+        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_i8_kernel<BITS, NS, SEG32>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    hipLaunchKernelGGL((gemm_i8_kernel<BITS, NS, SEG32>), grid, dim3(256), lds, ctx->stream, a);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+template <int BITS, bool SEG32>
+int launch_bits(llmq_ctx *ctx, const MfArgs &a, dim3 grid, int ns) {
+    if (ns == 2) return launch_ns<BITS, 2, SEG32>(ctx, a, grid);
+    return launch_ns<BITS, 1, SEG32>(ctx, a, grid);
+}
+
 }  // namespace
 
 bool gemm_mfma_supports(const llmq_mat *w, int64_t T) {
     if (w->kind != MAT_QUANT || T < 2) return false;
     const int64_t seg = w->group < 256 ? w->group : 256;
-    return w->k % KB == 0 && w->k % seg == 0 && w->group % 32 == 0 &&
+    return w->k % KB0 == 0 && w->k % seg == 0 && w->group % 32 == 0 &&
            (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 256 < (int64_t)kOOB && T * w->k * 2 < (int64_t)kOOB;
 }
 
@@ -438,10 +512,15 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     a.seg = (int)(w->group < 256 ? w->group : 256);
     a.flags = rq.flags;
     dim3 grid((unsigned)((w->n + TN - 1) / TN), (unsigned)((T + TM - 1) / TM));
-    if (w->bits == 4)
-        hipLaunchKernelGGL(gemm_i8_kernel<4>, grid, dim3(256), 0, ctx->stream, a);
-    else
-        hipLaunchKernelGGL(gemm_i8_kernel<8>, grid, dim3(256), 0, ctx->stream, a);
-    LLMQ_HIP(hipGetLastError());
-    return LLMQ_OK;
+    // staged block: int4 2 sub-blocks of 64 inputs (1 when K is an odd
+    // multiple of 64), int8 1 (its registers): two workgroups fit a CU
+    const int nsb = (int)(K / KB0);
+    int ns = w->bits == 4 && nsb % 2 == 0 ? 2 : 1;
+    if (const char *e = getenv("LLMQ_GEMM_NS")) {
+        const int v = atoi(e);
+        if ((v == 1 || v == 2) && nsb % v == 0) ns = v;
+    }
+    const bool seg32 = a.seg == 32;
+    if (w->bits == 4) return seg32 ? launch_bits<4, true>(ctx, a, grid, ns) : launch_bits<4, false>(ctx, a, grid, ns);
+    return seg32 ? launch_bits<8, true>(ctx, a, grid, ns) : launch_bits<8, false>(ctx, a, grid, ns);
 }

@@ -140,6 +140,8 @@ A16_CASES = [  # tests/a16_kernels.mojo:85-94 and the GPT-2 / Llama layer shapes
     ((4, 128, True), 40, 3072, 768, False), ((8, 0, False), 20, 768, 64, True),
     ((8, 0, True), 24, 3072, 64, True), ((4, 0, True), 16, 3072, 40, True),
     ((8, 128, False), 70, 768, 130, True), ((4, 32, True), 100, 768, 70, True),
+    # staged blocks of 64 and 128 inputs (reduction axes of 9 and 10 x 64)
+    ((4, 64, False), 40, 576, 100, False), ((8, 32, False), 20, 640, 64, True),
 ]
 
 

@@ -343,6 +343,23 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v + dpp_row<0x140>(v);
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Prompt attention for one head and 16 queries on the fp32 matrix cores
+// (v_mfma_f32_16x16x4f32; lane l holds A[l % 16][l / 16], B[l / 16][l % 16]
+// and D[4 (l / 16) + i][l % 16]).  KVCache.attend over QuantKV[8]
+// (kvcache.mojo:62-79, 113-150, 344-370): per query and position
+//   score = (sum_d q_d * f32(k_d)) * ks * (1 / sqrt(64)),  causal,
+//   e = exp(score - max),  p = e / total,  out = sum_s (p * vs) * f32(v_s)
+// with the sums over d and s taken by the matrix cores (float32 products
+// and accumulation, in their own order).
+//
+// Key / value rows are staged 64 at a time.  Scores: wave w takes keys
+// 16w..16w+15 of the block; MFMA step t covers dims 16k + t (k = lane / 16),
+// so a lane's 16 key bytes are one contiguous 16-byte read.  Values: wave w
+// takes dims 16w..16w+15; step t covers block keys 16k + t, so a lane reads
+// 16 consecutive weights of its query and 16 consecutive bytes of the
+// transposed value block.
 template <int HD>
 __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restrict__ qkv, int64_t ld, int pos0, int T,
                                                             int layer, int max_t, int n_head,
@@ -353,95 +370,119 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
                                                             int64_t ldo, int LT) {
     static_assert(HD == 64, "prompt attention: head_dim 64");
     extern __shared__ __align__(16) float smp[];
-    float *Q = smp;                                      // [kQB][HD]
-    float *S = Q + kQB * HD;                             // [kQB][LT] scores, then e
+    float *S = smp;                                      // [kQB][LT] scores, then e
     float *RS = S + kQB * LT;                            // [kPB] row scales of the staged block
-    int8_t *R8 = reinterpret_cast<int8_t *>(RS + kPB);   // [kPB][HD] staged rows
+    int8_t *R8 = reinterpret_cast<int8_t *>(RS + kPB);   // [kPB][HD] staged key rows / [HD][kPB] value columns
     __shared__ float tot[kQB];
     const int h = blockIdx.x, q0 = blockIdx.y * kQB, tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, c16 = lane & 15, k4 = lane >> 4;
     const int nq = min(kQB, T - q0);
     const int npos = pos0 + q0 + nq;  // positions any query of the block sees
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t base = (int64_t)layer * max_t * n_head + h;
-    {   // queries: 16 x 64 floats, 4 per thread
-        const int qi = tid >> 4, d = 4 * (tid & 15);
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (qi < nq) v = *reinterpret_cast<const float4 *>(qkv + (int64_t)(q0 + qi) * ld + (int64_t)h * HD + d);
-        *reinterpret_cast<float4 *>(Q + qi * HD + d) = v;
+
+    // A operand of the scores: query c16, dims 16 k4 + t
+    float qa[16];
+    {
+        const float *qr = qkv + (int64_t)(q0 + c16) * ld + (int64_t)h * HD + 16 * k4;
+#pragma unroll
+        for (int t = 0; t < 16; t += 4) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (c16 < nq) v = *reinterpret_cast<const float4 *>(qr + t);
+            qa[t] = v.x;
+            qa[t + 1] = v.y;
+            qa[t + 2] = v.z;
+            qa[t + 3] = v.w;
+        }
     }
-    const int qi = tid >> 4, li = tid & 15;  // query row and lane within its 16
-    const int qlast = pos0 + q0 + qi;        // the last position query qi sees
-    auto stage = [&](const int8_t *src, const float *sc, int s0) {
-        const int row = tid >> 2, piece = tid & 3;  // 64 rows x 4 pieces of 16 bytes
+    // One 16-byte piece of row s0 + row (64 rows x 4 pieces) and the row scale.
+    auto load_piece = [&](const int8_t *src, const float *sc, int s0, int4 &v, float &f) {
+        const int row = tid >> 2, piece = tid & 3;
         const int s = s0 + row;
-        int4 v = make_int4(0, 0, 0, 0);
-        float f = 0.0f;
+        v = make_int4(0, 0, 0, 0);
+        f = 0.0f;
         if (s < npos) {
             const int64_t sl = base + (int64_t)s * n_head;
             v = *reinterpret_cast<const int4 *>(src + sl * HD + 16 * piece);
-            if (piece == 0) f = sc[sl];
+            f = sc[sl];
         }
-        *reinterpret_cast<int4 *>(R8 + row * HD + 16 * piece) = v;
-        if (piece == 0) RS[row] = f;
     };
     // Scores.
     for (int s0 = 0; s0 < npos; s0 += kPB) {
+        int4 v;
+        float f;
+        load_piece(K8, KS, s0, v, f);
         __syncthreads();
-        stage(K8, KS, s0);
+        *reinterpret_cast<int4 *>(R8 + (tid >> 2) * HD + 16 * (tid & 3)) = v;
+        if ((tid & 3) == 0) RS[tid >> 2] = f;
         __syncthreads();
+        if (s0 + 16 * w < npos) {
+            const int key = 16 * w + c16;  // this lane's key of the block (B column)
+            const int4 kb = *reinterpret_cast<const int4 *>(R8 + key * HD + 16 * k4);
+            const uint32_t kw[4] = {(uint32_t)kb.x, (uint32_t)kb.y, (uint32_t)kb.z, (uint32_t)kb.w};
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < kPB / 16; j++) {
-            const int r = li + 16 * j, s = s0 + r;
-            if (s >= npos) break;
-            float d = 0.0f;
-            const int8_t *kr = R8 + r * HD;
-            const float *qr = Q + qi * HD;
-#pragma unroll
-            for (int i = 0; i < HD; i += 4) {
-                const int k4 = *reinterpret_cast<const int *>(kr + i);
-                const float4 qv = *reinterpret_cast<const float4 *>(qr + i);
-                d = fmaf(qv.x, (float)(int8_t)(k4 & 255), d);
-                d = fmaf(qv.y, (float)(int8_t)((k4 >> 8) & 255), d);
-                d = fmaf(qv.z, (float)(int8_t)((k4 >> 16) & 255), d);
-                d = fmaf(qv.w, (float)(int8_t)((k4 >> 24) & 255), d);
+            for (int t = 0; t < 16; t++) {
+                const float kf = (float)(int8_t)((kw[t >> 2] >> (8 * (t & 3))) & 255u);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t], kf, acc, 0, 0, 0);
             }
-            S[qi * LT + s] = d * RS[r] * scale;
+            const float ks = RS[key];
+#pragma unroll
+            for (int i = 0; i < 4; i++) S[(4 * k4 + i) * LT + s0 + key] = acc[i] * ks * scale;
         }
     }
     __syncthreads();
-    // Softmax per query (16 lanes a row).
-    float mx = -INFINITY;
-    for (int s = li; s <= qlast && qi < nq; s += 16) mx = fmaxf(mx, S[qi * LT + s]);
-    mx = row16_max(mx);
-    float t = 0.0f;
-    for (int s = li; s <= qlast && qi < nq; s += 16) {
-        const float e = expf(S[qi * LT + s] - mx);
-        S[qi * LT + s] = e;
-        t += e;
+    // Softmax per query (16 lanes a row): e in place, the total aside.
+    {
+        const int qi = tid >> 4, li = tid & 15;
+        const int qlast = pos0 + q0 + qi;
+        float mx = -INFINITY;
+        for (int s = li; s <= qlast && qi < nq; s += 16) mx = fmaxf(mx, S[qi * LT + s]);
+        mx = row16_max(mx);
+        float t = 0.0f;
+        for (int s = li; s <= qlast && qi < nq; s += 16) {
+            const float e = expf(S[qi * LT + s] - mx);
+            S[qi * LT + s] = e;
+            t += e;
+        }
+        t = row16_sum(t);
+        if (li == 0) tot[qi] = t;
     }
-    t = row16_sum(t);
-    if (li == 0) tot[qi] = t;
-    // Values: thread (qi, li) owns dimensions 4 li .. 4 li + 3 of query qi.
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    // Values: wave w owns dims 16w..16w+15 of the 16 queries.
+    const int qlast_a = pos0 + q0 + c16;  // the A row's query sees positions <= this
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int s0 = 0; s0 < npos; s0 += kPB) {
+        int4 v;
+        float f;
+        load_piece(V8, VS, s0, v, f);
+        __syncthreads();  // also orders the softmax writes before the first reads
+        {   // transposed: R8[d * kPB + row]
+            const int row = tid >> 2, d0 = 16 * (tid & 3);
+            const uint32_t vw[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+            for (int j = 0; j < 16; j++) R8[(d0 + j) * kPB + row] = (int8_t)((vw[j >> 2] >> (8 * (j & 3))) & 255u);
+        }
+        if ((tid & 3) == 0) RS[tid >> 2] = f;
         __syncthreads();
-        stage(V8, VS, s0);
-        __syncthreads();
-        const float total = tot[qi];
-        const int send = min(kPB, qlast + 1 - s0);
-        for (int r = 0; r < send && qi < nq; r++) {
-            const float p = S[qi * LT + s0 + r] / total;
-            const float w = p * RS[r];
-            const int v4 = *reinterpret_cast<const int *>(R8 + r * HD + 4 * li);
-            a0 = fmaf(w, (float)(int8_t)(v4 & 255), a0);
-            a1 = fmaf(w, (float)(int8_t)((v4 >> 8) & 255), a1);
-            a2 = fmaf(w, (float)(int8_t)((v4 >> 16) & 255), a2);
-            a3 = fmaf(w, (float)(int8_t)((v4 >> 24) & 255), a3);
+        const float total = tot[c16];
+        const int d = 16 * w + c16;  // this lane's dim (B column)
+        const int4 vb = *reinterpret_cast<const int4 *>(R8 + d * kPB + 16 * k4);
+        const uint32_t vw[4] = {(uint32_t)vb.x, (uint32_t)vb.y, (uint32_t)vb.z, (uint32_t)vb.w};
+        const float *er = S + c16 * LT + s0 + 16 * k4;
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const int s = s0 + 16 * k4 + t;
+            float a = 0.0f;
+            if (s <= qlast_a && c16 < nq) a = (er[t] / total) * RS[16 * k4 + t];  // p * vs
+            const float vf = (float)(int8_t)((vw[t >> 2] >> (8 * (t & 3))) & 255u);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vf, acc, 0, 0, 0);
         }
     }
-    if (qi < nq)
-        *reinterpret_cast<float4 *>(out + (int64_t)(q0 + qi) * ldo + (int64_t)h * HD + 4 * li) =
-            make_float4(a0, a1, a2, a3);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = 4 * k4 + i;
+        if (q < nq) out[(int64_t)(q0 + q) * ldo + (int64_t)h * HD + 16 * w + c16] = acc[i];
+    }
 }
 }  // namespace
 
@@ -507,7 +548,7 @@ int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
         // Prompt: query blocks of 16 per head, scores in LDS up to the last position
         const int C = kv->n_head * kv->head_dim;
         const int LT = ((pos0 + T) + 63) & ~63;
-        const size_t lds = sizeof(float) * ((size_t)kQB * 64 + (size_t)kQB * LT + kPB) + (size_t)kPB * 64;
+        const size_t lds = sizeof(float) * ((size_t)kQB * LT + kPB) + (size_t)kPB * 64;
         static size_t granted = 64 * 1024;
         if (lds > granted) {
             LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_prompt_kernel<64>),

@@ -38,12 +38,11 @@
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 typedef short v2s __attribute__((ext_vector_type(2)));
 
-constexpr int TM = 64;           // tokens per workgroup
-constexpr int TN = 64;           // output rows per workgroup
-constexpr int KB0 = 64;          // inputs per prefetched sub-block
+constexpr int TM = 16;           // tokens per workgroup
+constexpr int TN = 64;           // output rows per workgroup (a 16 x 16 block per wave)
+constexpr int KB = 128;          // inputs per staged block
 constexpr uint32_t kOOB = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
@@ -167,185 +166,181 @@ struct MfArgs {
     int T, K, n, ntiles, CK, NG, G, seg, flags;
 };
 
-// Registers of one 64-input sub-block of a staged block, loaded ahead of
-// its use.
-template <int BITS>
+// Registers of one staged block (KB = 128 inputs), loaded ahead of its use.
+// Thread t: activations of token t / 16, inputs 8 (t % 16) .. +7; int4
+// codes of (tile t / 64, 32-input chunk (t / 16) % 4, row t % 16); int8
+// codes of the same rows' two 16-input chunks of sub-step (t / 16) % 4; the
+// scale of (sub-step t / 64, row t % 64).  Zero point and scale come as
+// the aligned dwords holding them plus bit offsets, extracted where they are
+// used, so no wait follows the loads.
 struct Pref {
-    uint4 a0, a1;                        // 16 activations (int16) of one token
-    uint4 code;                          // int4: 16 codes in .x, .y; int8: 16 codes
-    // zero point byte and float16 scale bits of one (row, sub-step) scale
-    // (threads < 128), as the aligned dwords holding them and their bit
-    // offsets: extracted where they are used, so no wait follows the loads
+    uint4 a;        // 8 int16 activations
+    uint4 c0, c1;   // int4: one chunk (c0); int8: two chunks
     uint32_t zpw, zsh, scw, ssh;
 };
 
-// One staged block of NS sub-blocks (KB = 64 NS inputs), double-buffered.
-template <int BITS, int NS>
+template <int BITS>
 struct Lds {
-    static constexpr int KB = KB0 * NS;
-    static constexpr int RS = KB + 16;   // row stride in bytes (conflict-free 16-byte reads)
+    static constexpr int RS = KB + 16;   // row stride in bytes
     uint8_t a_hi[2][TM * RS];
     uint8_t a_lo[2][TM * RS];
     uint8_t w0[2][TN * RS];              // int4: u - zp; int8: wl = w & 15
     uint8_t w1[2][BITS == 8 ? TN * RS : 16];  // int8: wh = w >> 4
-    int wsum[2][2 * NS][TN];             // sum of w per (32-input sub-step, row)
-    float scale[2][2 * NS][TN];          // scale of the group of each (sub-step, row)
+    int wsum[2][KB / 32][TN];            // sum of w per (32-input sub-step, row)
+    float scale[2][KB / 32][TN];         // scale of the group of each (sub-step, row)
     float sx[TM];
 };
 
-// Loads of sub-block sb (inputs 64 sb ..) into p.
+// Loads of block kb (inputs 128 kb ..); everything at or past K reads zeros.
 template <int BITS>
-__device__ __forceinline__ void prefetch(const MfArgs &a, int sb, int tok0, int tile0, Pref<BITS> &p,
+__device__ __forceinline__ void prefetch(const MfArgs &a, int kb, int tok0, int tile0, Pref &p,
                                          __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rc,
                                          __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rz) {
-    const int t = threadIdx.x, k0 = sb * KB0;
-    {   // activations: token m = t / 4, inputs k0 + 16 q ..
-        const int m = t >> 2, q = t & 3;
+    const int t = threadIdx.x, k0 = kb * KB;
+    {
+        const int m = t >> 4, k = k0 + 8 * (t & 15);
         const int tok = tok0 + m;
-        const uint32_t off = tok < a.T ? (uint32_t)(((int64_t)tok * a.K + k0 + 16 * q) * 2) : kOOB;
-        p.a0 = bload16(rx, off);
-        p.a1 = bload16(rx, off == kOOB ? kOOB : off + 16u);
+        const uint32_t off = tok < a.T && k < a.K ? (uint32_t)(((int64_t)tok * a.K + k) * 2) : kOOB;
+        p.a = bload16(rx, off);
     }
-    int tile, r, g;
-    uint32_t coff;
-    if (BITS == 4) {  // (tile, chunk c of 32 inputs, row r, half h of 16 inputs)
-        const int tt = t >> 6, c = (t >> 5) & 1, h = t & 1;
-        r = (t >> 1) & 15;
-        tile = tile0 + tt;
-        g = (k0 + 32 * c) / a.G;
-        coff = (uint32_t)((((int64_t)tile * a.CK + 2 * sb + c) * 16 + r) * 16 + 8 * h);
-        const uint2 v = bload8(rc, tile < a.ntiles ? coff : kOOB);
-        p.code = make_uint4(v.x, v.y, 0u, 0u);
-    } else {          // (tile, chunk c of 16 inputs, row r)
-        const int tt = t >> 6, c = (t >> 4) & 3;
-        r = t & 15;
-        tile = tile0 + tt;
-        g = (k0 + 16 * c) / a.G;
-        coff = (uint32_t)((((int64_t)tile * a.CK + 4 * sb + c) * 16 + r) * 16);
-        p.code = bload16(rc, tile < a.ntiles ? coff : kOOB);
+    const int tt = t >> 6, sub = (t >> 4) & 3, r = t & 15;
+    const int tile = tile0 + tt, ks = k0 + 32 * sub;  // this thread's 32-input sub-step
+    const bool ok = tile < a.ntiles && ks < a.K;
+    if (BITS == 4) {
+        const uint32_t coff = (uint32_t)((((int64_t)tile * a.CK + ks / 32) * 16 + r) * 16);
+        p.c0 = bload16(rc, ok ? coff : kOOB);
+    } else {
+        const uint32_t coff = (uint32_t)((((int64_t)tile * a.CK + ks / 16) * 16 + r) * 16);
+        p.c0 = bload16(rc, ok ? coff : kOOB);
+        p.c1 = bload16(rc, ok ? coff + 256u : kOOB);  // next chunk, same row
     }
-    const uint32_t zoff = tile < a.ntiles ? (uint32_t)(((int64_t)tile * a.NG + g) * 16 + r) : kOOB;
+    const uint32_t zoff = ok ? (uint32_t)(((int64_t)tile * a.NG + ks / a.G) * 16 + r) : kOOB;
     p.zpw = bload4(rz, zoff == kOOB ? kOOB : (zoff & ~3u));
     p.zsh = 8u * (zoff & 3u);
-    {   // scale of (sub-step s, row o) for threads < 2 TN, the others read past the
-        // extent: no branch, so the compiler does not wait for every load at its end
-        const int s = (t >> 6) & 1, o = t & 63;
-        const int tl = tile0 + (o >> 4), gs = (k0 + 32 * s) / a.G;
-        const bool ok = t < 2 * TN && tl < a.ntiles;
-        const uint32_t soff = ok ? (uint32_t)((((int64_t)tl * a.NG + gs) * 16 + (o & 15)) * 2) : kOOB;
+    {
+        const int s = t >> 6, o = t & 63;
+        const int tl = tile0 + (o >> 4), kss = k0 + 32 * s;
+        const bool sok = tl < a.ntiles && kss < a.K;
+        const uint32_t soff = sok ? (uint32_t)((((int64_t)tl * a.NG + kss / a.G) * 16 + (o & 15)) * 2) : kOOB;
         p.scw = bload4(rs, soff == kOOB ? kOOB : (soff & ~3u));
         p.ssh = 8u * (soff & 2u);
     }
 }
 
-// Sub-block j of the staged block in buffer buf, from p.
-template <int BITS, int NS>
-__device__ __forceinline__ void stage(const Pref<BITS> &p, Lds<BITS, NS> &L, int buf, int j) {
-    constexpr int RS = Lds<BITS, NS>::RS;
-    const int t = threadIdx.x, col = KB0 * j;
+// int8 weights w (u - zp, 9 bits) of 16 codes as low nibbles wl and high
+// parts wh (w = 16 wh + wl); returns sum w.
+__device__ __forceinline__ int split_w8(uint4 code, uint32_t zp, uint32_t (&wl)[4], uint32_t (&wh)[4]) {
+    const v2s zz = {(short)zp, (short)zp};
+    const uint32_t dd[4] = {code.x, code.y, code.z, code.w};
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // 16-bit lanes (u0, u2) and (u1, u3), minus zp, split into nibble parts
+        const uint32_t ue = dd[i] & 0x00FF00FFu, uo = (dd[i] >> 8) & 0x00FF00FFu;
+        const v2s we = __builtin_bit_cast(v2s, ue) - zz, wo = __builtin_bit_cast(v2s, uo) - zz;
+        const uint32_t le = __builtin_bit_cast(uint32_t, we) & 0x000F000Fu, lo = __builtin_bit_cast(uint32_t, wo) & 0x000F000Fu;
+        const uint32_t he = __builtin_bit_cast(uint32_t, (v2s)(we >> (v2s){4, 4}));
+        const uint32_t ho = __builtin_bit_cast(uint32_t, (v2s)(wo >> (v2s){4, 4}));
+        wl[i] = __builtin_amdgcn_perm(lo, le, 0x06020400u);  // (w0, w1, w2, w3) low nibbles
+        wh[i] = __builtin_amdgcn_perm(ho, he, 0x06020400u);  // high parts as int8
+        s = __builtin_amdgcn_sdot4((int)wh[i], 0x10101010, s, false);  // 16 * wh
+        s = __builtin_amdgcn_sdot4((int)wl[i], 0x01010101, s, false);
+    }
+    return s;
+}
+
+// Block p into LDS buffer buf.
+template <int BITS>
+__device__ __forceinline__ void stage(const Pref &p, Lds<BITS> &L, int buf) {
+    constexpr int RS = Lds<BITS>::RS;
+    const int t = threadIdx.x;
     const uint32_t zp = (p.zpw >> p.zsh) & 255u;
     {   // activation planes: hi bytes and (lo - 128) bytes, natural input order
-        const int m = t >> 2, q = t & 3;
-        const uint32_t d[8] = {p.a0.x, p.a0.y, p.a0.z, p.a0.w, p.a1.x, p.a1.y, p.a1.z, p.a1.w};
-        uint32_t hi[4], lo[4];
+        const int m = t >> 4, col = 8 * (t & 15);
+        const uint32_t hi0 = __builtin_amdgcn_perm(p.a.y, p.a.x, 0x07050301u);
+        const uint32_t hi1 = __builtin_amdgcn_perm(p.a.w, p.a.z, 0x07050301u);
+        const uint32_t lo0 = __builtin_amdgcn_perm(p.a.y, p.a.x, 0x06040200u) ^ 0x80808080u;
+        const uint32_t lo1 = __builtin_amdgcn_perm(p.a.w, p.a.z, 0x06040200u) ^ 0x80808080u;
+        *reinterpret_cast<uint2 *>(&L.a_hi[buf][m * RS + col]) = make_uint2(hi0, hi1);
+        *reinterpret_cast<uint2 *>(&L.a_lo[buf][m * RS + col]) = make_uint2(lo0, lo1);
+    }
+    const int tt = t >> 6, sub = (t >> 4) & 3, r = t & 15;
+    const int o = tt * 16 + r;
+    if (BITS == 4) {
+        const uint32_t zb = zp * 0x01010101u;
+        const uint32_t dd[4] = {p.c0.x, p.c0.y, p.c0.z, p.c0.w};
+        uint32_t w[8];
+        int s = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            hi[i] = __builtin_amdgcn_perm(d[2 * i + 1], d[2 * i], 0x07050301u);
-            lo[i] = __builtin_amdgcn_perm(d[2 * i + 1], d[2 * i], 0x06040200u) ^ 0x80808080u;
-        }
-        *reinterpret_cast<uint4 *>(&L.a_hi[buf][m * RS + col + 16 * q]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *reinterpret_cast<uint4 *>(&L.a_lo[buf][m * RS + col + 16 * q]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-    }
-    if (BITS == 4) {
-        const int tt = t >> 6, c = (t >> 5) & 1, r = (t >> 1) & 15, h = t & 1;
-        const int o = tt * 16 + r;
-        const uint32_t zb = zp * 0x01010101u;
-        uint32_t w[4];
-        const uint32_t dd[2] = {p.code.x, p.code.y};
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
             const uint32_t lo = dd[i] & 0x0F0F0F0Fu, hi = (dd[i] >> 4) & 0x0F0F0F0Fu;
             const uint32_t n0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // weights 8i+0..3
             const uint32_t n1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // weights 8i+4..7
             w[2 * i] = ((n0 | 0x80808080u) - zb) ^ 0x80808080u;               // u - zp as int8
             w[2 * i + 1] = ((n1 | 0x80808080u) - zb) ^ 0x80808080u;
+            s = __builtin_amdgcn_sdot4((int)w[2 * i], 0x01010101, s, false);
+            s = __builtin_amdgcn_sdot4((int)w[2 * i + 1], 0x01010101, s, false);
         }
-        *reinterpret_cast<uint4 *>(&L.w0[buf][o * RS + col + 32 * c + 16 * h]) = make_uint4(w[0], w[1], w[2], w[3]);
-        int s = __builtin_amdgcn_sdot4((int)w[0], 0x01010101, 0, false);
-        s = __builtin_amdgcn_sdot4((int)w[1], 0x01010101, s, false);
-        s = __builtin_amdgcn_sdot4((int)w[2], 0x01010101, s, false);
-        s = __builtin_amdgcn_sdot4((int)w[3], 0x01010101, s, false);
-        s += __shfl_xor(s, 1);  // the other half of the chunk
-        if (h == 0) L.wsum[buf][2 * j + c][o] = s;
+        uint8_t *dst = &L.w0[buf][o * RS + 32 * sub];
+        *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint4 *>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+        L.wsum[buf][sub][o] = s;
     } else {
-        const int tt = t >> 6, c = (t >> 4) & 3, r = t & 15;
-        const int o = tt * 16 + r;
-        const v2s zz = {(short)zp, (short)zp};
-        uint32_t wl[4], wh[4];
-        const uint32_t dd[4] = {p.code.x, p.code.y, p.code.z, p.code.w};
-        int s = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            // 16-bit lanes (u0, u2) and (u1, u3), minus zp, split into nibble parts
-            const uint32_t ue = dd[i] & 0x00FF00FFu, uo = (dd[i] >> 8) & 0x00FF00FFu;
-            const v2s we = __builtin_bit_cast(v2s, ue) - zz, wo = __builtin_bit_cast(v2s, uo) - zz;
-            const uint32_t le = __builtin_bit_cast(uint32_t, we) & 0x000F000Fu, lo = __builtin_bit_cast(uint32_t, wo) & 0x000F000Fu;
-            const uint32_t he = __builtin_bit_cast(uint32_t, (v2s)(we >> (v2s){4, 4}));
-            const uint32_t ho = __builtin_bit_cast(uint32_t, (v2s)(wo >> (v2s){4, 4}));
-            wl[i] = __builtin_amdgcn_perm(lo, le, 0x06020400u);  // (w0, w1, w2, w3) low nibbles
-            wh[i] = __builtin_amdgcn_perm(ho, he, 0x06020400u);  // high parts as int8
-            s = __builtin_amdgcn_sdot4((int)wh[i], 0x10101010, s, false);  // 16 * wh
-            s = __builtin_amdgcn_sdot4((int)wl[i], 0x01010101, s, false);
-        }
-        *reinterpret_cast<uint4 *>(&L.w0[buf][o * RS + col + 16 * c]) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
-        *reinterpret_cast<uint4 *>(&L.w1[buf][o * RS + col + 16 * c]) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
-        s += __shfl_xor(s, 16);  // the other chunk of the 32-input sub-step
-        if ((c & 1) == 0) L.wsum[buf][2 * j + (c >> 1)][o] = s;
+        uint32_t wl[4], wh[4], wl1[4], wh1[4];
+        const int s = split_w8(p.c0, zp, wl, wh) + split_w8(p.c1, zp, wl1, wh1);
+        uint8_t *d0 = &L.w0[buf][o * RS + 32 * sub];
+        uint8_t *d1 = &L.w1[buf][o * RS + 32 * sub];
+        *reinterpret_cast<uint4 *>(d0) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+        *reinterpret_cast<uint4 *>(d0 + 16) = make_uint4(wl1[0], wl1[1], wl1[2], wl1[3]);
+        *reinterpret_cast<uint4 *>(d1) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+        *reinterpret_cast<uint4 *>(d1 + 16) = make_uint4(wh1[0], wh1[1], wh1[2], wh1[3]);
+        L.wsum[buf][sub][o] = s;
     }
-    if (t < 2 * TN)
-        L.scale[buf][2 * j + (t >> 6)][t & 63] = __half2float(__ushort_as_half((unsigned short)((p.scw >> p.ssh) & 0xFFFFu)));
+    L.scale[buf][t >> 6][t & 63] = __half2float(__ushort_as_half((unsigned short)((p.scw >> p.ssh) & 0xFFFFu)));
 }
 
 // Accumulators of one wave: the matrix-core partial sums of the current
 // segment (int4: hi, lo planes; int8: hh, hl, lh, ll), the weight sum of the
-// segment, and the float outputs (16 tokens of one row per lane).
-template <int BITS>
+// segment, and the float outputs (4 tokens of one row per lane).
 struct Acc {
-    v16i c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    v4i c0 = {}, c1 = {}, c2 = {}, c3 = {};
     int wacc = 0;
-    float acc[16] = {};
+    float acc[4] = {};
 };
 
-// The 2 NS sub-steps of 32 inputs of staged block kb (in LDS buffer buf).
-template <int BITS, int NS, bool SEG32>
-__device__ __forceinline__ void compute_block(const Lds<BITS, NS> &L, int buf, int kb, int arow, int brow, int orow,
-                                              int seg, Acc<BITS> &c) {
-    constexpr int KB = Lds<BITS, NS>::KB;
+__device__ __forceinline__ v4i mfma16(int64_t a, int64_t b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+// The 4 sub-steps of 32 inputs of staged block kb (in LDS buffer buf).
+template <int BITS, bool SEG32>
+__device__ __forceinline__ void compute_block(const Lds<BITS> &L, int buf, int kb, int arow, int brow, int orow,
+                                              int seg, Acc &c) {
 #pragma unroll
-    for (int s = 0; s < 2 * NS; s++) {
-        const v4i ah = *reinterpret_cast<const v4i *>(&L.a_hi[buf][arow + 32 * s]);
-        const v4i al = *reinterpret_cast<const v4i *>(&L.a_lo[buf][arow + 32 * s]);
-        const v4i b0 = *reinterpret_cast<const v4i *>(&L.w0[buf][brow + 32 * s]);
+    for (int s = 0; s < KB / 32; s++) {
+        const int64_t ah = *reinterpret_cast<const int64_t *>(&L.a_hi[buf][arow + 32 * s]);
+        const int64_t al = *reinterpret_cast<const int64_t *>(&L.a_lo[buf][arow + 32 * s]);
+        const int64_t b0 = *reinterpret_cast<const int64_t *>(&L.w0[buf][brow + 32 * s]);
         if (SEG32) {  // every sub-step is a segment: the products start from zero
-            c.c0 = c.c1 = c.c2 = c.c3 = (v16i){};
+            c.c0 = c.c1 = c.c2 = c.c3 = (v4i){};
             c.wacc = 0;
         }
         if (BITS == 4) {
-            c.c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b0, c.c0, 0, 0, 0);
-            c.c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b0, c.c1, 0, 0, 0);
+            c.c0 = mfma16(ah, b0, c.c0);
+            c.c1 = mfma16(al, b0, c.c1);
         } else {
-            const v4i b1 = *reinterpret_cast<const v4i *>(&L.w1[buf][brow + 32 * s]);
-            c.c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b1, c.c0, 0, 0, 0);
-            c.c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, b0, c.c1, 0, 0, 0);
-            c.c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b1, c.c2, 0, 0, 0);
-            c.c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, b0, c.c3, 0, 0, 0);
+            const int64_t b1 = *reinterpret_cast<const int64_t *>(&L.w1[buf][brow + 32 * s]);
+            c.c0 = mfma16(ah, b1, c.c0);
+            c.c1 = mfma16(ah, b0, c.c1);
+            c.c2 = mfma16(al, b1, c.c2);
+            c.c3 = mfma16(al, b0, c.c3);
         }
         c.wacc += L.wsum[buf][s][orow];
         if (SEG32 || (kb * KB + 32 * (s + 1)) % seg == 0) {  // end of a segment: tile_i16's flush
             const float sc = L.scale[buf][s][orow];
             const int w128 = 128 * c.wacc;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
+            for (int i = 0; i < 4; i++) {
                 int G;
                 if (BITS == 4)
                     G = (c.c0[i] << 8) + c.c1[i] + w128;
@@ -354,21 +349,19 @@ __device__ __forceinline__ void compute_block(const Lds<BITS, NS> &L, int buf, i
                 c.acc[i] = fmaf((float)G, sc, c.acc[i]);
             }
             if (!SEG32) {
-                c.c0 = c.c1 = c.c2 = c.c3 = (v16i){};
+                c.c0 = c.c1 = c.c2 = c.c3 = (v4i){};
                 c.wacc = 0;
             }
         }
     }
 }
 
-template <int BITS, int NS, bool SEG32>
+template <int BITS, bool SEG32>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
-    using LT = Lds<BITS, NS>;
-    constexpr int KB = LT::KB, RS = LT::RS;
-    extern __shared__ __align__(16) uint8_t smem_gemm[];
-    LT &L = *reinterpret_cast<LT *>(smem_gemm);
+    using LT = Lds<BITS>;
+    constexpr int RS = LT::RS;
+    __shared__ __align__(16) LT L;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int wm = wid & 1, wn = wid >> 1;
     const int tile0 = blockIdx.x * (TN / 16), out0 = blockIdx.x * TN, tok0 = blockIdx.y * TM;
     const auto rx = make_rsrc(a.xq, a.xq_bytes);
     const auto rc = make_rsrc(a.codes, a.codes_bytes);
@@ -376,62 +369,45 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
     const auto rz = make_rsrc(a.zps, a.zps_bytes);
     if (tid < TM) L.sx[tid] = tok0 + tid < a.T ? a.sx[tok0 + tid] : 0.0f;
 
-    const int nkb = a.K / KB;
+    const int nkb = (a.K + KB - 1) / KB;
     // Two register sets of prefetched blocks: block kb + 1 is loaded while
     // block kb - 1 is computed, so a load has two blocks of work to arrive.
-    Pref<BITS> pa[NS], pb[NS];
-#pragma unroll
-    for (int j = 0; j < NS; j++) prefetch<BITS>(a, j, tok0, tile0, pa[j], rx, rc, rs, rz);
-    if (nkb > 1) {
-#pragma unroll
-        for (int j = 0; j < NS; j++) prefetch<BITS>(a, NS + j, tok0, tile0, pb[j], rx, rc, rs, rz);
-    }
-#pragma unroll
-    for (int j = 0; j < NS; j++) stage<BITS, NS>(pa[j], L, 0, j);
+    Pref pa, pb;
+    prefetch<BITS>(a, 0, tok0, tile0, pa, rx, rc, rs, rz);
+    if (nkb > 1) prefetch<BITS>(a, 1, tok0, tile0, pb, rx, rc, rs, rz);
+    stage<BITS>(pa, L, 0);
     lds_barrier();
 
-    Acc<BITS> c;
-    const int arow = (32 * wm + (lane & 31)) * RS + 16 * (lane >> 5);
-    const int brow = (32 * wn + (lane & 31)) * RS + 16 * (lane >> 5);
-    const int orow = 32 * wn + (lane & 31);
+    Acc c;
+    // A: token lane % 16, inputs 8 (lane / 16) ..; B: row 16 wid + lane % 16
+    const int arow = (lane & 15) * RS + 8 * (lane >> 4);
+    const int brow = (16 * wid + (lane & 15)) * RS + 8 * (lane >> 4);
+    const int orow = 16 * wid + (lane & 15);
 
     for (int kb = 0; kb < nkb; kb += 2) {
         // even block kb in buffer 0; pa is free, pb holds block kb + 1
-        if (kb + 2 < nkb) {
-#pragma unroll
-            for (int j = 0; j < NS; j++) prefetch<BITS>(a, (kb + 2) * NS + j, tok0, tile0, pa[j], rx, rc, rs, rz);
-        }
-        compute_block<BITS, NS, SEG32>(L, 0, kb, arow, brow, orow, a.seg, c);
-        if (kb + 1 < nkb) {
-#pragma unroll
-            for (int j = 0; j < NS; j++) stage<BITS, NS>(pb[j], L, 1, j);
-        }
+        if (kb + 2 < nkb) prefetch<BITS>(a, kb + 2, tok0, tile0, pa, rx, rc, rs, rz);
+        compute_block<BITS, SEG32>(L, 0, kb, arow, brow, orow, a.seg, c);
+        if (kb + 1 < nkb) stage<BITS>(pb, L, 1);
         lds_barrier();
         if (kb + 1 >= nkb) break;
         // odd block kb + 1 in buffer 1; pb is free, pa holds block kb + 2
-        if (kb + 3 < nkb) {
-#pragma unroll
-            for (int j = 0; j < NS; j++) prefetch<BITS>(a, (kb + 3) * NS + j, tok0, tile0, pb[j], rx, rc, rs, rz);
-        }
-        compute_block<BITS, NS, SEG32>(L, 1, kb + 1, arow, brow, orow, a.seg, c);
-        if (kb + 2 < nkb) {
-#pragma unroll
-            for (int j = 0; j < NS; j++) stage<BITS, NS>(pa[j], L, 0, j);
-        }
+        if (kb + 3 < nkb) prefetch<BITS>(a, kb + 3, tok0, tile0, pb, rx, rc, rs, rz);
+        compute_block<BITS, SEG32>(L, 1, kb + 1, arow, brow, orow, a.seg, c);
+        if (kb + 2 < nkb) stage<BITS>(pa, L, 0);
         lds_barrier();
     }
-    const float *acc = c.acc;
 
-    // Epilogue: lane holds output row out0 + orow for 16 tokens.
+    // Epilogue: lane holds output row out0 + orow for tokens 4 (lane / 16) + i.
     const int o = out0 + orow;
     if (o >= a.n) return;
     const float bo = (a.flags & LLMQ_BIAS) ? a.bias[o] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int ml = 32 * wm + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    for (int i = 0; i < 4; i++) {
+        const int ml = 4 * (lane >> 4) + i;
         const int tok = tok0 + ml;
         if (tok >= a.T) continue;
-        float v = acc[i] * L.sx[ml];
+        float v = c.acc[i] * L.sx[ml];
         if (a.flags & LLMQ_BIAS) v += bo;
         if (a.flags & LLMQ_GELU) v = gelu_f(v);
         float *dst = a.out + (int64_t)tok * a.ldo + o;
@@ -440,32 +416,12 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
     }
 }
 
-template <int BITS, int NS, bool SEG32>
-int launch_ns(llmq_ctx *ctx, const MfArgs &a, dim3 grid) {
-    const size_t lds = sizeof(Lds<BITS, NS>);
-    static bool attr = false;
-    if (!attr) {
-        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_i8_kernel<BITS, NS, SEG32>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr = true;
-    }
-    hipLaunchKernelGGL((gemm_i8_kernel<BITS, NS, SEG32>), grid, dim3(256), lds, ctx->stream, a);
-    LLMQ_HIP(hipGetLastError());
-    return LLMQ_OK;
-}
-
-template <int BITS, bool SEG32>
-int launch_bits(llmq_ctx *ctx, const MfArgs &a, dim3 grid, int ns) {
-    if (ns == 2) return launch_ns<BITS, 2, SEG32>(ctx, a, grid);
-    return launch_ns<BITS, 1, SEG32>(ctx, a, grid);
-}
-
 }  // namespace
 
 bool gemm_mfma_supports(const llmq_mat *w, int64_t T) {
     if (w->kind != MAT_QUANT || T < 2) return false;
     const int64_t seg = w->group < 256 ? w->group : 256;
-    return w->k % KB0 == 0 && w->k % seg == 0 && w->group % 32 == 0 &&
+    return w->k % 32 == 0 && w->k % seg == 0 && w->group % 32 == 0 &&
            (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 256 < (int64_t)kOOB && T * w->k * 2 < (int64_t)kOOB;
 }
 
@@ -512,15 +468,18 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     a.seg = (int)(w->group < 256 ? w->group : 256);
     a.flags = rq.flags;
     dim3 grid((unsigned)((w->n + TN - 1) / TN), (unsigned)((T + TM - 1) / TM));
-    // staged block: int4 2 sub-blocks of 64 inputs (1 when K is an odd
-    // multiple of 64), int8 1 (its registers): two workgroups fit a CU
-    const int nsb = (int)(K / KB0);
-    int ns = w->bits == 4 && nsb % 2 == 0 ? 2 : 1;
-    if (const char *e = getenv("LLMQ_GEMM_NS")) {
-        const int v = atoi(e);
-        if ((v == 1 || v == 2) && nsb % v == 0) ns = v;
-    }
     const bool seg32 = a.seg == 32;
-    if (w->bits == 4) return seg32 ? launch_bits<4, true>(ctx, a, grid, ns) : launch_bits<4, false>(ctx, a, grid, ns);
-    return seg32 ? launch_bits<8, true>(ctx, a, grid, ns) : launch_bits<8, false>(ctx, a, grid, ns);
+    if (w->bits == 4) {
+        if (seg32)
+            hipLaunchKernelGGL((gemm_i8_kernel<4, true>), grid, dim3(256), 0, ctx->stream, a);
+        else
+            hipLaunchKernelGGL((gemm_i8_kernel<4, false>), grid, dim3(256), 0, ctx->stream, a);
+    } else {
+        if (seg32)
+            hipLaunchKernelGGL((gemm_i8_kernel<8, true>), grid, dim3(256), 0, ctx->stream, a);
+        else
+            hipLaunchKernelGGL((gemm_i8_kernel<8, false>), grid, dim3(256), 0, ctx->stream, a);
+    }
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
 }

@@ -365,10 +365,10 @@ int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, co
     LLMQ_REQUIRE(ctx, "linear: null context");
     RC(check_linear(w, IN, OUT));
     if (w->kind == MAT_GGUF) {
-        // matmul_rows (kernels.mojo:285-312): one token at a time on the GPU
-        for (int64_t t = 0; t < T; t++)
-            RC(launch_gguf_gemv(ctx, w, x + t * IN, out + t * OUT, bias, flags, nullptr, 0));
-        return LLMQ_OK;
+        // matmul_rows (kernels.mojo:285-349): the one-token GEMV, or the
+        // dequantize-and-multiply matmul for several tokens
+        if (T == 1) return launch_gguf_gemv(ctx, w, x, out, bias, flags, nullptr, 0);
+        return launch_gguf_gemm(ctx, w, x, IN, T, out, OUT, bias, flags);
     }
     GemvRequest rq;
     rq.w = w;

@@ -129,6 +129,9 @@ int gguf_num_parts(const llmq_mat *w);
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
                      ArgmaxPart *amax, int amax_cap);
 int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
+// Several-token GGUF matmul on the fp32 matrix cores (gguf_gemm.hip).
+int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t ldx, int64_t T, float *out,
+                     int64_t ldo, const float *bias, int flags);
 // int16 output head for Q6_K / Q8_0 (gguf_head.hip).
 int gguf_has_i16(const llmq_mat *w);
 int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *logits, int64_t T);

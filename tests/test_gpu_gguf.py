@@ -134,3 +134,33 @@ def test_gguf_float_heads_take_the_float_path(gpu, orc):
     want = orc.gguf_gemv(t, blocks, V, C, h[0], None, 0)
     got = logits.cpu().numpy()[0]
     assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("rows,cols,T", [(70, 512, 5), (300, 2048, 16), (200, 4352, 33), (256, 5632, 17),
+                                         (100, 544, 20)])
+def test_gguf_matmul_several_tokens(gpu, orc, kind, rows, cols, T):
+    """matmul_rows for T > 1 (kernels.mojo:314-349): every token's outputs
+    within 1e-5 of max |out| of the oracle's one-token GEMV (the same
+    dequantized weights; float sums in another order).  (200, 4352): 17
+    superblocks a row; (256, 5632): TinyLlama's FFN down projection shape;
+    (100, 544): a reduction axis that ends mid-block (Q4_0 / Q4_1 / Q8_0 only)."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    t = orc.GGML[kind]
+    if cols % orc.gguf_block_size(t):
+        pytest.skip("cols not a whole number of blocks")
+    blocks = synth.gguf_blocks(t, rows, cols, seed=rows + cols + T)
+    rng = np.random.default_rng(T)
+    x = rng.normal(0, 1, (T, cols)).astype(np.float32)
+    b = rng.normal(0, 0.1, rows).astype(np.float32)
+    res = rng.normal(0, 0.1, (T, rows)).astype(np.float32)
+    print("gguf matmul", kind, rows, cols, T, flush=True)
+    g = lm.HipGGUFMatrix.from_blocks(ctx, t, blocks, rows, cols)
+    out = dev(torch, res)
+    lm.linear(ctx, out, dev(torch, x), g, dev(torch, b), resid=True)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = np.stack([orc.gguf_gemv(t, blocks, rows, cols, x[i], b, orc.EPI_BIAS) for i in range(T)]) + res
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5

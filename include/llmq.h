@@ -203,6 +203,39 @@ LLMQ_API int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_promp
 /* Device pointer to the model's logits [V] (after forward / generate). */
 LLMQ_API int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr);
 
+/* ---------------------------------------------------------------- config 4
+ * A TinyLlama-shaped decoder over GGUF weights (RMSNorm,
+ * RoPE, grouped key / value heads, SwiGLU).  No counterpart in the reference,
+ * whose model code is GPT-2 only (gpt2t.mojo:74-81); it composes the GGUF
+ * kernels above (GGUFMatrix, gguf.mojo:344-511; matmul_rows and head_i16,
+ * kernels.mojo:285-349, 693-736) with the int8 cache (QuantKV[8],
+ * kvcache.mojo:248-385). */
+typedef struct llmq_llama llmq_llama;
+typedef struct {
+    int n_layer, dim, n_head, n_kv, head_dim, ffn, vocab, max_t, batch;
+    int layer_type, head_type, embd_type; /* ggml type ids of the layer, output and embedding matrices */
+    float eps, theta;                     /* RMSNorm epsilon, RoPE base */
+} llmq_llama_cfg;
+/* tensors: 2 + 9 n_layer host pointers: token_embd [vocab][dim]; per layer
+ * attn_norm (float32 [dim]), attn_q [dim][dim], attn_k [n_kv*64][dim],
+ * attn_v [n_kv*64][dim], attn_output [dim][dim], ffn_norm (float32 [dim]),
+ * ffn_gate [ffn][dim], ffn_up [ffn][dim], ffn_down [dim][ffn]; output_norm
+ * (float32 [dim]); output [vocab][dim].  Matrices are GGUF blocks as stored,
+ * [rows = outputs][row bytes]; batch sequences get their own cache. */
+LLMQ_API int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *const *tensors,
+                               llmq_llama **out);
+LLMQ_API int llmq_llama_free(llmq_llama *m);
+LLMQ_API int64_t llmq_llama_weight_bytes(const llmq_llama *m);
+/* T tokens of sequence seq at positions pos0.. (cache written); logits of the
+ * last token to a host buffer of vocab floats (may be null). */
+LLMQ_API int llmq_llama_forward(llmq_llama *m, int seq, const int64_t *tokens, int T, int pos0, float *logits);
+/* Prompts [batch][n_prompt] (batch <= cfg.batch) from position 0, then
+ * `steps` greedy tokens per sequence (the first from the prompt, then
+ * steps - 1 batched decode steps replayed from one captured graph);
+ * out_tokens [steps][batch]. */
+LLMQ_API int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int batch, int n_prompt, int steps,
+                                 int64_t *out_tokens, double *prefill_ms, double *decode_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,7 +63,20 @@ SIGNATURES = {
     "llmq_gpt2_generate": (I32, [P, P, I32, I32, P, ctypes.POINTER(I32), ctypes.POINTER(ctypes.c_double),
                                  ctypes.POINTER(ctypes.c_double)]),
     "llmq_gpt2_logits_device": (I32, [P, ctypes.POINTER(ctypes.c_void_p)]),
+    "llmq_llama_create": (I32, [P, P, P, PP]),
+    "llmq_llama_free": (I32, [P]),
+    "llmq_llama_weight_bytes": (I64, [P]),
+    "llmq_llama_forward": (I32, [P, I32, P, I32, I32, P]),
+    "llmq_llama_generate": (I32, [P, P, I32, I32, I32, P, ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(ctypes.c_double)]),
 }
+
+
+class LlamaCfg(ctypes.Structure):
+    """llmq_llama_cfg (include/llmq.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layer", "dim", "n_head", "n_kv", "head_dim", "ffn", "vocab", "max_t",
+                                            "batch", "layer_type", "head_type", "embd_type")] + \
+               [("eps", ctypes.c_float), ("theta", ctypes.c_float)]
 
 _lib = None
 

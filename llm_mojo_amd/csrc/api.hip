@@ -19,11 +19,6 @@ int llmq_set_error(int code, const char *fmt, ...) {
     return code;
 }
 
-#define RC(call)                   \
-    do {                           \
-        int rc_ = (call);          \
-        if (rc_ != LLMQ_OK) return rc_; \
-    } while (0)
 
 int ctx_workspace(llmq_ctx *ctx, size_t bytes, void **p) {
     if (bytes > ctx->ws_bytes) {
@@ -505,25 +500,6 @@ constexpr int VEC_PARAM[N_VECS] = {0, 1, 3, 5, 6, 7, 9, 11};  // index within a 
 constexpr int64_t SMALL_FLOATS = (int64_t)NL * 13 * C + (int64_t)MAXT * C + 2 * C;  // gpt2t.mojo:576
 }  // namespace
 
-// Runs the enclosing GPT-2 call on the context's own (non-null) stream, which
-// a decode-step graph can be captured on, after the caller's stream's
-// earlier work; the caller's stream is restored on exit.
-struct OwnStream {
-    llmq_ctx *ctx;
-    hipStream_t saved;
-    explicit OwnStream(llmq_ctx *c) : ctx(c), saved(c->stream) {
-        if (saved != ctx->own_stream) {
-            hipStreamSynchronize(saved);
-            ctx->stream = ctx->own_stream;
-        }
-    }
-    ~OwnStream() {
-        if (saved != ctx->own_stream) {
-            hipStreamSynchronize(ctx->own_stream);
-            ctx->stream = saved;
-        }
-    }
-};
 
 struct llmq_gpt2 {
     llmq_ctx *ctx = nullptr;

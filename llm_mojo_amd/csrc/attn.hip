@@ -345,7 +345,8 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Prompt attention for one head and 16 queries on the fp32 matrix cores
+// Prompt attention for one query head and 16 queries on the fp32 matrix cores
+// (its key / value head h / group of n_kv cached heads)
 // (v_mfma_f32_16x16x4f32; lane l holds A[l % 16][l / 16], B[l / 16][l % 16]
 // and D[4 (l / 16) + i][l % 16]).  KVCache.attend over QuantKV[8]
 // (kvcache.mojo:62-79, 113-150, 344-370): per query and position
@@ -362,7 +363,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // transposed value block.
 template <int HD>
 __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restrict__ qkv, int64_t ld, int pos0, int T,
-                                                            int layer, int max_t, int n_head,
+                                                            int layer, int max_t, int n_kv, int group,
                                                             const int8_t *__restrict__ K8,
                                                             const int8_t *__restrict__ V8,
                                                             const float *__restrict__ KS,
@@ -379,7 +380,7 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
     const int nq = min(kQB, T - q0);
     const int npos = pos0 + q0 + nq;  // positions any query of the block sees
     const float scale = 1.0f / sqrtf((float)HD);
-    const int64_t base = (int64_t)layer * max_t * n_head + h;
+    const int64_t base = (int64_t)layer * max_t * n_kv + h / group;  // the query head's key / value head
 
     // A operand of the scores: query c16, dims 16 k4 + t
     float qa[16];
@@ -402,7 +403,7 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
         v = make_int4(0, 0, 0, 0);
         f = 0.0f;
         if (s < npos) {
-            const int64_t sl = base + (int64_t)s * n_head;
+            const int64_t sl = base + (int64_t)s * n_kv;
             v = *reinterpret_cast<const int4 *>(src + sl * HD + 16 * piece);
             f = sc[sl];
         }
@@ -486,6 +487,26 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
 }
 }  // namespace
 
+int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, const float *KS, const float *VS,
+                         int layer, int max_t, int n_head, int n_kv, const float *qkv, int64_t ld, int pos0, int T,
+                         float *out, int64_t ldo) {
+    LLMQ_REQUIRE(n_kv > 0 && n_head % n_kv == 0, "attend: %d query heads over %d key / value heads", n_head, n_kv);
+    LLMQ_REQUIRE(T >= 1 && pos0 >= 0 && pos0 + T <= max_t, "attend: positions %d..%d beyond %d", pos0, pos0 + T - 1,
+                 max_t);
+    const int LT = ((pos0 + T) + 63) & ~63;
+    const size_t lds = sizeof(float) * ((size_t)kQB * LT + kPB) + (size_t)kPB * 64;
+    static size_t granted = 64 * 1024;
+    if (lds > granted) {
+        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_prompt_kernel<64>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        granted = lds;
+    }
+    hipLaunchKernelGGL(attend_prompt_kernel<64>, dim3(n_head, (T + kQB - 1) / kQB), dim3(256), lds, ctx->stream, qkv,
+                       ld, pos0, T, layer, max_t, n_kv, n_head / n_kv, K8, V8, KS, VS, out, ldo, LT);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
 int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,
                     int64_t ld) {
     LLMQ_REQUIRE(kv && qkv && T >= 1, "kv_store: bad arguments");
@@ -547,19 +568,8 @@ int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
     if (!store && !pos_dev && T > 1 && kv->head_dim == 64) {
         // Prompt: query blocks of 16 per head, scores in LDS up to the last position
         const int C = kv->n_head * kv->head_dim;
-        const int LT = ((pos0 + T) + 63) & ~63;
-        const size_t lds = sizeof(float) * ((size_t)kQB * LT + kPB) + (size_t)kPB * 64;
-        static size_t granted = 64 * 1024;
-        if (lds > granted) {
-            LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_prompt_kernel<64>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            granted = lds;
-        }
-        hipLaunchKernelGGL(attend_prompt_kernel<64>, dim3(kv->n_head, (T + kQB - 1) / kQB), dim3(256), lds,
-                           ctx->stream, qkv, ld ? ld : 3 * C, pos0, T, layer, kv->max_t, kv->n_head, kv->k, kv->v,
-                           kv->ks, kv->vs, out, (int64_t)C, LT);
-        LLMQ_HIP(hipGetLastError());
-        return LLMQ_OK;
+        return launch_attend_prompt(ctx, kv->k, kv->v, kv->ks, kv->vs, layer, kv->max_t, kv->n_head, kv->n_head, qkv,
+                                    ld ? ld : 3 * C, pos0, T, out, (int64_t)C);
     }
     if (kv->head_dim == 64) return attend_hd<64>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
     if (kv->head_dim == 128) return attend_hd<128>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);

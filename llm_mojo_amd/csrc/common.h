@@ -80,6 +80,32 @@ int llmq_set_error(int code, const char *fmt, ...);
         if (!(cond)) return llmq_set_error(LLMQ_EINVAL, __VA_ARGS__); \
     } while (0)
 
+#define RC(call)                   \
+    do {                           \
+        int rc_ = (call);          \
+        if (rc_ != LLMQ_OK) return rc_; \
+    } while (0)
+
+// Runs the enclosing model call on the context's own (non-null) stream, which
+// a decode-step graph can be captured on, after the caller's stream's
+// earlier work; the caller's stream is restored on exit.
+struct OwnStream {
+    llmq_ctx *ctx;
+    hipStream_t saved;
+    explicit OwnStream(llmq_ctx *c) : ctx(c), saved(c->stream) {
+        if (saved != ctx->own_stream) {
+            hipStreamSynchronize(saved);
+            ctx->stream = ctx->own_stream;
+        }
+    }
+    ~OwnStream() {
+        if (saved != ctx->own_stream) {
+            hipStreamSynchronize(ctx->own_stream);
+            ctx->stream = saved;
+        }
+    }
+};
+
 // Argmax partial of one workgroup: the largest value and its (smallest) index.
 struct ArgmaxPart {
     float v;
@@ -124,11 +150,19 @@ int gemv1_num_parts(const llmq_mat *w, bool ln);
 
 // GGUF formats (gguf.hip).
 int gguf_is_supported(int ggml_type);
+int gguf_block_size(int ggml_type);   // weights per block (gguf.mojo:72-83)
+int gguf_block_bytes(int ggml_type);  // bytes per block (gguf.mojo:86-98)
 int gguf_upload(llmq_ctx *ctx, llmq_mat *m, int ggml_type, const uint8_t *blocks, int64_t rows, int64_t cols);
 int gguf_num_parts(const llmq_mat *w);
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
                      ArgmaxPart *amax, int amax_cap);
 int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
+int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *rows, int n, float *dst, int64_t ldd);
+// Prompt attention over an int8 cache of n_kv heads (attn.hip): query head h
+// reads cached head h / (n_head / n_kv) of `layer` (a slot index).
+int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, const float *KS, const float *VS,
+                         int layer, int max_t, int n_head, int n_kv, const float *qkv, int64_t ld, int pos0, int T,
+                         float *out, int64_t ldo);
 // Several-token GGUF matmul on the fp32 matrix cores (gguf_gemm.hip).
 int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t ldx, int64_t T, float *out,
                      int64_t ldo, const float *bias, int flags);

@@ -63,7 +63,7 @@ __device__ __forceinline__ void k_scale_min(uint32_t s0, uint32_t s1, uint32_t s
 
 // Dequantize one row into float32 (GGUFMatrix.dequant_row, gguf.mojo:381-382).
 template <int TYPE>
-__global__ void gguf_dequant_row_kernel(GgufArgs a, int64_t row, float *dst) {
+__device__ __forceinline__ void dequant_row_body(const GgufArgs &a, int64_t row, float *dst) {
     using F = Fmt<TYPE>;
     const int64_t tile = row / 16, r = row % 16;
     for (int k = threadIdx.x; k < a.K; k += blockDim.x) {
@@ -104,21 +104,22 @@ __global__ void gguf_dequant_row_kernel(GgufArgs a, int64_t row, float *dst) {
     }
 }
 
-int gguf_block_size(int t) {
-    if (t == LLMQ_GGML_Q4_0 || t == LLMQ_GGML_Q4_1 || t == LLMQ_GGML_Q8_0) return 32;
-    if (t == LLMQ_GGML_Q4_K || t == LLMQ_GGML_Q5_K || t == LLMQ_GGML_Q6_K) return 256;
-    return 0;
+template <int TYPE>
+__global__ void gguf_dequant_row_kernel(GgufArgs a, int64_t row, float *dst) {
+    dequant_row_body<TYPE>(a, row, dst);
 }
-int gguf_block_bytes(int t) {
-    switch (t) {
-    case LLMQ_GGML_Q4_0: return 18;
-    case LLMQ_GGML_Q4_1: return 20;
-    case LLMQ_GGML_Q8_0: return 34;
-    case LLMQ_GGML_Q4_K: return 144;
-    case LLMQ_GGML_Q5_K: return 176;
-    case LLMQ_GGML_Q6_K: return 210;
-    default: return 0;
+
+// Rows rows[i] (device indices, e.g. token ids) into dst + i * ldd, one
+// workgroup a row; an index outside the matrix writes zeros.
+template <int TYPE>
+__global__ void gguf_dequant_rows_kernel(GgufArgs a, const int64_t *rows, float *dst, int64_t ldd) {
+    const int64_t row = rows[blockIdx.x];
+    float *d = dst + (int64_t)blockIdx.x * ldd;
+    if (row < 0 || row >= a.n) {
+        for (int k = threadIdx.x; k < a.K; k += blockDim.x) d[k] = 0.0f;
+        return;
     }
+    dequant_row_body<TYPE>(a, row, d);
 }
 
 GgufArgs make_args(const llmq_mat *m) {
@@ -138,6 +139,23 @@ GgufArgs make_args(const llmq_mat *m) {
 }
 
 }  // namespace
+
+int gguf_block_size(int t) {
+    if (t == LLMQ_GGML_Q4_0 || t == LLMQ_GGML_Q4_1 || t == LLMQ_GGML_Q8_0) return 32;
+    if (t == LLMQ_GGML_Q4_K || t == LLMQ_GGML_Q5_K || t == LLMQ_GGML_Q6_K) return 256;
+    return 0;
+}
+int gguf_block_bytes(int t) {
+    switch (t) {
+    case LLMQ_GGML_Q4_0: return 18;
+    case LLMQ_GGML_Q4_1: return 20;
+    case LLMQ_GGML_Q8_0: return 34;
+    case LLMQ_GGML_Q4_K: return 144;
+    case LLMQ_GGML_Q5_K: return 176;
+    case LLMQ_GGML_Q6_K: return 210;
+    default: return 0;
+    }
+}
 
 int gguf_is_supported(int t) { return gguf_block_size(t) != 0; }
 
@@ -256,6 +274,22 @@ int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float
     case LLMQ_GGML_Q4_K: hipLaunchKernelGGL(gguf_dequant_row_kernel<LLMQ_GGML_Q4_K>, dim3(1), dim3(256), 0, ctx->stream, a, row, dst); break;
     case LLMQ_GGML_Q5_K: hipLaunchKernelGGL(gguf_dequant_row_kernel<LLMQ_GGML_Q5_K>, dim3(1), dim3(256), 0, ctx->stream, a, row, dst); break;
     case LLMQ_GGML_Q6_K: hipLaunchKernelGGL(gguf_dequant_row_kernel<LLMQ_GGML_Q6_K>, dim3(1), dim3(256), 0, ctx->stream, a, row, dst); break;
+    default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf dequant: type %d", w->ggml_type);
+    }
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *rows, int n, float *dst, int64_t ldd) {
+    LLMQ_REQUIRE(w && w->kind == MAT_GGUF && rows && dst && n > 0, "gguf dequant rows: bad arguments");
+    GgufArgs a = make_args(w);
+    switch (w->ggml_type) {
+    case LLMQ_GGML_Q4_0: hipLaunchKernelGGL(gguf_dequant_rows_kernel<LLMQ_GGML_Q4_0>, dim3(n), dim3(256), 0, ctx->stream, a, rows, dst, ldd); break;
+    case LLMQ_GGML_Q4_1: hipLaunchKernelGGL(gguf_dequant_rows_kernel<LLMQ_GGML_Q4_1>, dim3(n), dim3(256), 0, ctx->stream, a, rows, dst, ldd); break;
+    case LLMQ_GGML_Q8_0: hipLaunchKernelGGL(gguf_dequant_rows_kernel<LLMQ_GGML_Q8_0>, dim3(n), dim3(256), 0, ctx->stream, a, rows, dst, ldd); break;
+    case LLMQ_GGML_Q4_K: hipLaunchKernelGGL(gguf_dequant_rows_kernel<LLMQ_GGML_Q4_K>, dim3(n), dim3(256), 0, ctx->stream, a, rows, dst, ldd); break;
+    case LLMQ_GGML_Q5_K: hipLaunchKernelGGL(gguf_dequant_rows_kernel<LLMQ_GGML_Q5_K>, dim3(n), dim3(256), 0, ctx->stream, a, rows, dst, ldd); break;
+    case LLMQ_GGML_Q6_K: hipLaunchKernelGGL(gguf_dequant_rows_kernel<LLMQ_GGML_Q6_K>, dim3(n), dim3(256), 0, ctx->stream, a, rows, dst, ldd); break;
     default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf dequant: type %d", w->ggml_type);
     }
     LLMQ_HIP(hipGetLastError());

@@ -1,0 +1,646 @@
+// A TinyLlama-shaped decoder over GGUF weights: the model of BASELINE.json's
+// config 4 (22 layers, d_model 2048, 32 query / 4 key-value heads of 64,
+// SwiGLU FFN 5632, RMSNorm, RoPE theta 10000, vocab 32000; Q4_K layers, Q6_K
+// head, int8 KV cache), decoding one or several independent sequences.
+//
+// The reference's model code is GPT-2 only (gpt2t.mojo:74-81), so nothing
+// here has a reference counterpart above the kernels it reuses: the GGUF
+// GEMV / matmul (GGUFMatrix, gguf.mojo:344-511; matmul_rows,
+// kernels.mojo:285-349), the int16 output head (head_i16, kernels.mojo:
+// 693-736), the int8 cache (QuantKV[8], kvcache.mojo:248-385) and the float
+// attention (attend_float_one, kvcache.mojo:113-150).  The rest follows the
+// usual Llama definition:
+//   h = x + Wo . attn(rope(Wq . n1), rope(Wk . n1), Wv . n1),  n1 = rmsnorm(x) * g1
+//   y = h + Wdown . (silu(Wgate . n2) * (Wup . n2)),           n2 = rmsnorm(h) * g2
+//   rmsnorm(x) = x / sqrt(mean(x^2) + eps);  rope rotates dims (2i, 2i+1) by
+//   pos * theta^(-2i / head_dim);  silu(g) = g / (1 + exp(-g)).
+//
+// Device layout: Wq, Wk, Wv are one matrix of n_head + 2 n_kv heads' rows
+// (one GEMV per layer); Wgate and Wup one of 2 ffn rows.  The cache holds
+// slot (sequence * n_layer + layer) of n_kv heads.  Decoding keeps the
+// position and step on the device, so one captured graph replays every step.
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "common.h"
+
+namespace {
+
+constexpr int HD = 64;  // head_dim
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+// Sum / max over a 256-thread workgroup, waves added in order.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+__device__ __forceinline__ float block_max(float v, float *red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// out[r] = x[r] / sqrt(mean(x[r]^2) + eps) * g, one workgroup a row.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, int64_t ldx,
+                                                      const float *__restrict__ g, float *__restrict__ out,
+                                                      int64_t ldo, int C, float eps) {
+    __shared__ float red[4];
+    const float *xr = x + (int64_t)blockIdx.x * ldx;
+    float *orow = out + (int64_t)blockIdx.x * ldo;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < C; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, red);
+    const float r = 1.0f / sqrtf(ss / (float)C + eps);
+    for (int i = threadIdx.x; i < C; i += 256) orow[i] = (xr[i] * r) * g[i];
+}
+
+// RoPE and the cache store for row `row` of qkv (token t = row % T of
+// sequence seq0 + row / T, position pos + t with pos = state[0] when given):
+// query heads are rotated in place; key heads are rotated, then key and
+// value heads quantized into the cache as QuantKV.store does
+// (kvcache.mojo:320-342: s = max|x| / 127, 1 if zero; codes round(x / s)).
+// One wave per (head, row); lane = dim.
+__global__ __launch_bounds__(64) void rope_store_kernel(float *__restrict__ qkv, int64_t ld, int T, int seq0,
+                                                        int pos0, const int *__restrict__ state, int n_head,
+                                                        int n_kv, int n_layer, int layer, int max_t, float theta,
+                                                        int8_t *__restrict__ K8, int8_t *__restrict__ V8,
+                                                        float *__restrict__ KS, float *__restrict__ VS) {
+    const int hh = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
+    const int seq = seq0 + row / T, t = row % T;
+    const int pos = (state ? state[0] : pos0) + t;
+    float *r = qkv + (int64_t)row * ld;
+    const bool is_q = hh < n_head;
+    float *src = r + hh * HD;  // query heads, then key heads
+    // rotation of pair (2i, 2i + 1), i = d / 2
+    const float freq = powf(theta, -(float)(2 * (d >> 1)) / (float)HD);
+    const float ang = (float)pos * freq;
+    const float c = cosf(ang), s = sinf(ang);
+    const float v = src[d], p = __shfl_xor(v, 1);
+    // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
+    const float rot = (d & 1) ? p * s + v * c : v * c - p * s;
+    if (is_q) {
+        src[d] = rot;
+        return;
+    }
+    const int kvh = hh - n_head;
+    const int64_t sl = (((int64_t)seq * n_layer + layer) * max_t + pos) * n_kv + kvh;
+    for (int kv = 0; kv < 2; kv++) {
+        const float x = kv == 0 ? rot : r[(n_head + n_kv + kvh) * HD + d];
+        const float m = wave_max(fabsf(x));
+        float sc = m / 127.0f;
+        if (sc == 0.0f) sc = 1.0f;
+        const float inv = 1.0f / sc;
+        (kv == 0 ? K8 : V8)[sl * HD + d] = (int8_t)llmq_to_int(roundf(x * inv));
+        if (d == 0) (kv == 0 ? KS : VS)[sl] = sc;
+    }
+}
+
+// One decode position for query head h = blockIdx.x of sequence b =
+// blockIdx.y at position state[0]: attend_float_one (kvcache.mojo:113-150)
+// over the int8 cache (QuantKV.score / add_value, 344-370) of key / value
+// head h / (n_head / n_kv).  Thread tid scores positions tid + NT i
+// (i < MAXP), loading all of their key and value rows first, and stages the
+// value rows in LDS; after the softmax it leaves w = p * vs per position.
+// Values: wave w takes positions w, w + NT / 64, .. with lane = dim; the
+// waves' partial sums are added in wave order.
+constexpr int kDecNT = 512;
+template <int MAXP>
+__global__ __launch_bounds__(kDecNT) void attend_decode_kernel(const float *__restrict__ qkv, int64_t ld,
+                                                               const int *__restrict__ state, int n_head, int n_kv,
+                                                               int n_layer, int layer, int max_t,
+                                                               const int8_t *__restrict__ K8,
+                                                               const int8_t *__restrict__ V8,
+                                                               const float *__restrict__ KS,
+                                                               const float *__restrict__ VS, float *__restrict__ out,
+                                                               int64_t ldo) {
+    constexpr int NW = kDecNT / 64;
+    extern __shared__ __align__(16) float sm[];
+    float *wt = sm;                                        // [max_t] scores, then p * vs
+    int8_t *vrow = reinterpret_cast<int8_t *>(sm + max_t);  // [max_t][HD] value rows
+    __shared__ __align__(16) float q[HD];
+    __shared__ float red[NW], vred[NW][HD];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int npos = state[0] + 1;
+    const int kvh = h / (n_head / n_kv);
+    const int64_t base = ((int64_t)b * n_layer + layer) * max_t * n_kv + kvh;  // slot of position 0
+    int4 kr[MAXP][HD / 16], vr[MAXP][HD / 16];
+    float ks[MAXP], vs[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; i++) {
+        const int s = tid + kDecNT * i;
+        const int64_t sl = base + (int64_t)(s < npos ? s : 0) * n_kv;
+        const int4 *kp = reinterpret_cast<const int4 *>(K8 + sl * HD);
+        const int4 *vp = reinterpret_cast<const int4 *>(V8 + sl * HD);
+#pragma unroll
+        for (int j = 0; j < HD / 16; j++) {
+            kr[i][j] = kp[j];
+            vr[i][j] = vp[j];
+        }
+        ks[i] = KS[sl];
+        vs[i] = VS[sl];
+    }
+    if (tid < HD) q[tid] = qkv[(int64_t)b * ld + h * HD + tid];
+#pragma unroll
+    for (int i = 0; i < MAXP; i++) {  // value rows to LDS as they arrive
+        const int s = tid + kDecNT * i;
+        if (s < npos) {
+#pragma unroll
+            for (int j = 0; j < HD / 16; j++) reinterpret_cast<int4 *>(vrow + (int64_t)s * HD)[j] = vr[i][j];
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)HD);
+    float sc[MAXP];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MAXP; i++) {
+        const int s = tid + kDecNT * i;
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < HD / 16; j++) {
+            const uint32_t kw[4] = {(uint32_t)kr[i][j].x, (uint32_t)kr[i][j].y, (uint32_t)kr[i][j].z,
+                                    (uint32_t)kr[i][j].w};
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                d = fmaf(q[16 * j + e], (float)(int8_t)((kw[e >> 2] >> (8 * (e & 3))) & 255u), d);
+        }
+        sc[i] = d * ks[i] * scale;
+        if (s < npos) mx = fmaxf(mx, sc[i]);
+    }
+    // workgroup max, then the sum of e, waves in order
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int i = 1; i < NW; i++) mx = fmaxf(mx, red[i]);
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXP; i++) {
+        sc[i] = expf(sc[i] - mx);
+        if (tid + kDecNT * i < npos) tot += sc[i];
+    }
+    tot = wave_sum(tot);
+    __syncthreads();
+    if (lane == 0) red[w] = tot;
+    __syncthreads();
+    tot = red[0];
+#pragma unroll
+    for (int i = 1; i < NW; i++) tot += red[i];
+#pragma unroll
+    for (int i = 0; i < MAXP; i++) {
+        const int s = tid + kDecNT * i;
+        if (s < npos) wt[s] = (sc[i] / tot) * vs[i];  // p * vs
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    for (int s = w; s < npos; s += NW) acc = fmaf(wt[s], (float)vrow[(int64_t)s * HD + lane], acc);
+    vred[w][lane] = acc;
+    __syncthreads();
+    if (tid < HD) {
+        float o = vred[0][tid];
+#pragma unroll
+        for (int i = 1; i < NW; i++) o += vred[i][tid];
+        out[(int64_t)b * ldo + h * HD + tid] = o;
+    }
+}
+
+// h[r][i] = silu(g) * u with g = gu[r][i], u = gu[r][F + i].
+__global__ void swiglu_kernel(const float *__restrict__ gu, int64_t ldg, float *__restrict__ h, int64_t ldh, int F) {
+    const int r = blockIdx.y;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < F; i += gridDim.x * blockDim.x) {
+        const float g = gu[(int64_t)r * ldg + i], u = gu[(int64_t)r * ldg + F + i];
+        h[(int64_t)r * ldh + i] = (g / (1.0f + expf(-g))) * u;
+    }
+}
+
+// Greedy pick (gpt2t.mojo:792-797: the first maximum) of logits row i for
+// sequence b0 + i: next token and gen[step * B + b0 + i], step = state[1]
+// (0 without state).
+__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int64_t ld, int V, int B,
+                                                     int b0, const int *__restrict__ state,
+                                                     int64_t *__restrict__ next, int64_t *__restrict__ gen) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const float *l = logits + (int64_t)blockIdx.x * ld;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < V; i += 256) {
+        const float x = l[i];
+        if (x > v) {
+            v = x;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o);
+        const int oi = __shfl_xor(idx, o);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = v;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        v = bv[0];
+        idx = bi[0];
+        for (int k = 1; k < 4; k++)
+            if (bv[k] > v || (bv[k] == v && bi[k] < idx)) {
+                v = bv[k];
+                idx = bi[k];
+            }
+        const int b = b0 + blockIdx.x;
+        const int step = state ? state[1] : 0;
+        next[b] = idx;
+        gen[(int64_t)step * B + b] = idx;
+    }
+}
+
+__global__ void advance_kernel(int *state) {
+    state[0] += 1;
+    state[1] += 1;
+}
+
+}  // namespace
+
+struct llmq_llama {
+    llmq_ctx *ctx = nullptr;
+    llmq_llama_cfg cfg{};
+    llmq_mat *embd = nullptr, *head = nullptr;
+    std::vector<llmq_mat *> wqkv, wo, wgu, wdown;
+    float *norms = nullptr;  // per layer attn / ffn gains, then the output gain
+    int8_t *k8 = nullptr, *v8 = nullptr;
+    float *ks = nullptr, *vs = nullptr;
+    // activations for up to `rows` tokens
+    int rows = 0;
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *hh = nullptr,
+          *logits = nullptr;
+    int64_t *tokens = nullptr, *next = nullptr, *gen = nullptr;
+    int64_t gen_cap = 0;
+    int graph_B = 0;  // batch size of the captured decode step
+    int *state = nullptr;
+    hipGraphExec_t step_graph = nullptr;
+    hipGraph_t step_graph_def = nullptr;
+};
+
+namespace {
+
+int qkv_cols(const llmq_llama_cfg &c) { return (c.n_head + 2 * c.n_kv) * c.head_dim; }
+
+void drop_graph(llmq_llama *m) {
+    if (m->step_graph) hipGraphExecDestroy(m->step_graph);
+    if (m->step_graph_def) hipGraphDestroy(m->step_graph_def);
+    m->step_graph = nullptr;
+    m->step_graph_def = nullptr;
+    m->graph_B = 0;
+}
+
+// Activation buffers for `rows` tokens; growing them drops the decode graph,
+// which holds their addresses.
+int ensure_rows(llmq_llama *m, int rows) {
+    if (rows <= m->rows) return LLMQ_OK;
+    const llmq_llama_cfg &c = m->cfg;
+    hipStreamSynchronize(m->ctx->stream);
+    drop_graph(m);
+    hipFree(m->x);
+    hipFree(m->xn);
+    hipFree(m->qkv);
+    hipFree(m->att);
+    hipFree(m->gu);
+    hipFree(m->hh);
+    hipFree(m->tokens);
+    m->x = m->xn = m->qkv = m->att = m->gu = m->hh = nullptr;
+    m->tokens = nullptr;
+    m->rows = 0;
+    const size_t r = (size_t)rows;
+    if (hipMalloc(&m->x, r * c.dim * 4) != hipSuccess || hipMalloc(&m->xn, r * c.dim * 4) != hipSuccess ||
+        hipMalloc(&m->qkv, r * qkv_cols(c) * 4) != hipSuccess || hipMalloc(&m->att, r * c.dim * 4) != hipSuccess ||
+        hipMalloc(&m->gu, r * 2 * c.ffn * 4) != hipSuccess || hipMalloc(&m->hh, r * c.ffn * 4) != hipSuccess ||
+        hipMalloc(&m->tokens, r * 8) != hipSuccess)
+        return llmq_set_error(LLMQ_ENOMEM, "llama: activations for %d tokens", rows);
+    m->rows = rows;
+    return LLMQ_OK;
+}
+
+const float *gain(const llmq_llama *m, int layer, int which) {  // which: 0 attn, 1 ffn
+    return m->norms + ((size_t)2 * layer + which) * m->cfg.dim;
+}
+
+// A GGUF matmul of R rows: the one-token GEMV for R == 1, else the
+// several-token matmul.
+int linear(llmq_llama *m, const llmq_mat *w, const float *x, int64_t ldx, int R, float *out, int64_t ldo,
+           int flags) {
+    if (R == 1) return launch_gguf_gemv(m->ctx, w, x, out, nullptr, flags, nullptr, 0);
+    return launch_gguf_gemm(m->ctx, w, x, ldx, R, out, ldo, nullptr, flags);
+}
+
+// The layers for R = nseq * T rows in m->x: T tokens of sequences seq0 ..
+// at positions pos0 + t (prefill: nseq = 1), or one token of every
+// sequence at position state[0] (decode: T = 1, state given).
+int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *state) {
+    llmq_ctx *ctx = m->ctx;
+    const llmq_llama_cfg &c = m->cfg;
+    const int QC = qkv_cols(c);
+    for (int l = 0; l < c.n_layer; l++) {
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(256), 0, ctx->stream, m->x, (int64_t)c.dim, gain(m, l, 0),
+                           m->xn, (int64_t)c.dim, c.dim, c.eps);
+        RC(linear(m, m->wqkv[l], m->xn, c.dim, R, m->qkv, QC, 0));
+        hipLaunchKernelGGL(rope_store_kernel, dim3(c.n_head + c.n_kv, R), dim3(64), 0, ctx->stream, m->qkv,
+                           (int64_t)QC, T, seq0, pos0, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, c.theta,
+                           m->k8, m->v8, m->ks, m->vs);
+        if (state) {
+            const size_t lds = (size_t)c.max_t * (4 + HD);
+            const int maxp = (c.max_t + kDecNT - 1) / kDecNT;
+#define ATT(P)                                                                                                    \
+    hipLaunchKernelGGL(attend_decode_kernel<P>, dim3(c.n_head, R), dim3(kDecNT), lds, ctx->stream, m->qkv,         \
+                       (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->k8, m->v8, m->ks, m->vs, m->att, \
+                       (int64_t)c.dim)
+            if (maxp == 1) ATT(1);
+            else if (maxp == 2) ATT(2);
+            else if (maxp == 3) ATT(3);
+            else ATT(4);
+#undef ATT
+        } else {
+            RC(launch_attend_prompt(ctx, m->k8, m->v8, m->ks, m->vs, seq0 * c.n_layer + l, c.max_t, c.n_head,
+                                    c.n_kv, m->qkv, QC, pos0, T, m->att, c.dim));
+        }
+        RC(linear(m, m->wo[l], m->att, c.dim, R, m->x, c.dim, LLMQ_RESID));
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(256), 0, ctx->stream, m->x, (int64_t)c.dim, gain(m, l, 1),
+                           m->xn, (int64_t)c.dim, c.dim, c.eps);
+        RC(linear(m, m->wgu[l], m->xn, c.dim, R, m->gu, 2 * c.ffn, 0));
+        hipLaunchKernelGGL(swiglu_kernel, dim3((c.ffn + 255) / 256, R), dim3(256), 0, ctx->stream, m->gu,
+                           (int64_t)2 * c.ffn, m->hh, (int64_t)c.ffn, c.ffn);
+        RC(linear(m, m->wdown[l], m->hh, c.ffn, R, m->x, c.dim, LLMQ_RESID));
+    }
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+// The output norm and head for nrows rows of m->x starting at row r0 (with
+// stride `every` rows), into m->logits.
+int llama_head(llmq_llama *m, int r0, int nrows, int every) {
+    llmq_ctx *ctx = m->ctx;
+    const llmq_llama_cfg &c = m->cfg;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, ctx->stream, m->x + (int64_t)r0 * c.dim,
+                       (int64_t)every * c.dim, m->norms + (size_t)2 * c.n_layer * c.dim, m->xn, (int64_t)c.dim, c.dim,
+                       c.eps);
+    if (gguf_has_i16(m->head)) return launch_gguf_head16(ctx, m->head, m->xn, m->logits, nrows);
+    return linear(m, m->head, m->xn, c.dim, nrows, m->logits, c.vocab, 0);
+}
+
+// One decode step of every sequence: embed the previous picks, the layers,
+// the head, the picks, then the position and step advance.
+int llama_step(llmq_llama *m, int B) {
+    llmq_ctx *ctx = m->ctx;
+    const llmq_llama_cfg &c = m->cfg;
+    RC(launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim));
+    RC(llama_layers(m, B, 1, 0, 0, m->state));
+    RC(llama_head(m, 0, B, 1));
+    hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab, B, 0,
+                       m->state, m->next, m->gen);
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, ctx->stream, m->state);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+// Prefill of sequence seq: T tokens (host) at positions pos0.., then its
+// last token's logits and greedy pick (gen row 0 when state is null).
+int llama_prefill(llmq_llama *m, int seq, const int64_t *tokens, int T, int pos0, int B, bool pick) {
+    llmq_ctx *ctx = m->ctx;
+    const llmq_llama_cfg &c = m->cfg;
+    RC(ensure_rows(m, T));
+    LLMQ_HIP(hipMemcpyAsync(m->tokens, tokens, sizeof(int64_t) * T, hipMemcpyHostToDevice, ctx->stream));
+    RC(launch_gguf_dequant_rows(ctx, m->embd, m->tokens, T, m->x, c.dim));
+    RC(llama_layers(m, T, T, seq, pos0, nullptr));
+    RC(llama_head(m, T - 1, 1, 1));
+    if (pick)
+        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab,
+                           B, seq, nullptr, m->next, m->gen);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+}  // namespace
+
+int llmq_llama_free(llmq_llama *m) {
+    if (!m) return LLMQ_OK;
+    if (m->ctx) hipStreamSynchronize(m->ctx->stream);
+    drop_graph(m);
+    llmq_mat_free(m->embd);
+    llmq_mat_free(m->head);
+    for (auto *w : m->wqkv) llmq_mat_free(w);
+    for (auto *w : m->wo) llmq_mat_free(w);
+    for (auto *w : m->wgu) llmq_mat_free(w);
+    for (auto *w : m->wdown) llmq_mat_free(w);
+    void *bufs[] = {m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
+                    m->tokens, m->next, m->gen, m->state};
+    for (void *p : bufs) hipFree(p);
+    delete m;
+    return LLMQ_OK;
+}
+
+int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *const *t, llmq_llama **out) {
+    LLMQ_REQUIRE(ctx && cfg && t && out, "llama_create: bad arguments");
+    const llmq_llama_cfg c = *cfg;
+    LLMQ_REQUIRE(c.n_layer > 0 && c.dim > 0 && c.n_head > 0 && c.n_kv > 0 && c.n_head % c.n_kv == 0 &&
+                     c.head_dim == HD && c.n_head * c.head_dim == c.dim && c.ffn > 0 && c.vocab > 0 &&
+                     c.max_t > 0 && c.batch > 0,
+                 "llama_create: unsupported shape (head_dim must be 64, n_head * head_dim == dim)");
+    LLMQ_REQUIRE(c.max_t <= 4 * kDecNT, "llama_create: max_t %d too long for the decode attention", c.max_t);
+    for (int ty : {c.layer_type, c.head_type, c.embd_type})
+        LLMQ_REQUIRE(gguf_is_supported(ty), "llama_create: ggml type %d is not a supported block format", ty);
+    llmq_llama *m = new llmq_llama();
+    m->ctx = ctx;
+    m->cfg = c;
+    int rc = LLMQ_OK;
+#define GO(call)                   \
+    do {                           \
+        rc = (call);               \
+        if (rc != LLMQ_OK) goto fail; \
+    } while (0)
+    {
+        const int bs = gguf_block_size(c.layer_type), bb = gguf_block_bytes(c.layer_type);
+        auto rb = [&](int64_t cols) { return (size_t)(cols / bs) * bb; };
+        auto mat = [&](const void *blocks, int ty, int64_t rows, int64_t cols, llmq_mat **w) {
+            return llmq_mat_from_gguf(ctx, ty, blocks, rows, cols, w);
+        };
+        // host tensors: token_embd; per layer attn_norm, q, k, v, o, ffn_norm, gate, up, down; output_norm, output
+        GO(mat(t[0], c.embd_type, c.vocab, c.dim, &m->embd));
+        const size_t nn = (size_t)(2 * c.n_layer + 1) * c.dim;
+        GO(hipMalloc(&m->norms, nn * 4) == hipSuccess ? LLMQ_OK : llmq_set_error(LLMQ_ENOMEM, "llama: norms"));
+        std::vector<float> norms(nn);
+        const int kvd = c.n_kv * HD;
+        for (int l = 0; l < c.n_layer; l++) {
+            const void *const *L = t + 1 + 9 * l;
+            memcpy(&norms[(size_t)2 * l * c.dim], L[0], (size_t)c.dim * 4);
+            memcpy(&norms[(size_t)(2 * l + 1) * c.dim], L[5], (size_t)c.dim * 4);
+            std::vector<uint8_t> cat;
+            auto append = [&](const void *p, int64_t rows, int64_t cols) {
+                const uint8_t *b = static_cast<const uint8_t *>(p);
+                cat.insert(cat.end(), b, b + rows * rb(cols));
+            };
+            append(L[1], c.dim, c.dim);
+            append(L[2], kvd, c.dim);
+            append(L[3], kvd, c.dim);
+            llmq_mat *w = nullptr;
+            GO(mat(cat.data(), c.layer_type, c.dim + 2 * kvd, c.dim, &w));
+            m->wqkv.push_back(w);
+            GO(mat(L[4], c.layer_type, c.dim, c.dim, &w));
+            m->wo.push_back(w);
+            cat.clear();
+            append(L[6], c.ffn, c.dim);
+            append(L[7], c.ffn, c.dim);
+            GO(mat(cat.data(), c.layer_type, 2 * c.ffn, c.dim, &w));
+            m->wgu.push_back(w);
+            GO(mat(L[8], c.layer_type, c.dim, c.ffn, &w));
+            m->wdown.push_back(w);
+        }
+        memcpy(&norms[(size_t)2 * c.n_layer * c.dim], t[1 + 9 * c.n_layer], (size_t)c.dim * 4);
+        GO(mat(t[2 + 9 * c.n_layer], c.head_type, c.vocab, c.dim, &m->head));
+        GO(hipMemcpy(m->norms, norms.data(), nn * 4, hipMemcpyHostToDevice) == hipSuccess
+               ? LLMQ_OK
+               : llmq_set_error(LLMQ_EHIP, "llama: norms copy"));
+        const size_t slots = (size_t)c.batch * c.n_layer * c.max_t * c.n_kv;
+        if (hipMalloc(&m->k8, slots * HD) != hipSuccess || hipMalloc(&m->v8, slots * HD) != hipSuccess ||
+            hipMalloc(&m->ks, slots * 4) != hipSuccess || hipMalloc(&m->vs, slots * 4) != hipSuccess ||
+            hipMalloc(&m->logits, (size_t)c.batch * c.vocab * 4) != hipSuccess ||
+            hipMalloc(&m->next, (size_t)c.batch * 8) != hipSuccess || hipMalloc(&m->state, 16) != hipSuccess)
+            GO(llmq_set_error(LLMQ_ENOMEM, "llama: cache of %zu slots", slots));
+        if (hipMemset(m->k8, 0, slots * HD) != hipSuccess || hipMemset(m->v8, 0, slots * HD) != hipSuccess ||
+            hipMemset(m->ks, 0, slots * 4) != hipSuccess || hipMemset(m->vs, 0, slots * 4) != hipSuccess)
+            GO(llmq_set_error(LLMQ_EHIP, "llama: cache clear"));
+        GO(ensure_rows(m, c.batch));
+        // the decode attention's LDS (scores and value rows of every position)
+        const int lds = c.max_t * (4 + HD);
+        const void *att[4] = {reinterpret_cast<const void *>(attend_decode_kernel<1>),
+                              reinterpret_cast<const void *>(attend_decode_kernel<2>),
+                              reinterpret_cast<const void *>(attend_decode_kernel<3>),
+                              reinterpret_cast<const void *>(attend_decode_kernel<4>)};
+        for (const void *k : att)
+            if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+                GO(llmq_set_error(LLMQ_EUNSUPPORTED, "llama: %d bytes of LDS for max_t %d", lds, c.max_t));
+    }
+#undef GO
+    *out = m;
+    return LLMQ_OK;
+fail:
+    llmq_llama_free(m);
+    return rc;
+}
+
+int64_t llmq_llama_weight_bytes(const llmq_llama *m) {
+    if (!m) return 0;
+    int64_t n = llmq_mat_nbytes(m->embd) + llmq_mat_nbytes(m->head);
+    for (auto *w : m->wqkv) n += llmq_mat_nbytes(w);
+    for (auto *w : m->wo) n += llmq_mat_nbytes(w);
+    for (auto *w : m->wgu) n += llmq_mat_nbytes(w);
+    for (auto *w : m->wdown) n += llmq_mat_nbytes(w);
+    return n + (int64_t)(2 * m->cfg.n_layer + 1) * m->cfg.dim * 4;
+}
+
+int llmq_llama_forward(llmq_llama *m, int seq, const int64_t *tokens, int T, int pos0, float *logits) {
+    LLMQ_REQUIRE(m && tokens && T >= 1, "llama_forward: bad arguments");
+    const llmq_llama_cfg &c = m->cfg;
+    LLMQ_REQUIRE(seq >= 0 && seq < c.batch, "llama_forward: sequence %d of %d", seq, c.batch);
+    LLMQ_REQUIRE(pos0 >= 0 && pos0 + T <= c.max_t, "llama_forward: positions %d..%d beyond %d", pos0, pos0 + T - 1,
+                 c.max_t);
+    for (int t = 0; t < T; t++)
+        LLMQ_REQUIRE(tokens[t] >= 0 && tokens[t] < c.vocab, "llama_forward: token %lld out of range",
+                     (long long)tokens[t]);
+    OwnStream os_(m->ctx);
+    RC(llama_prefill(m, seq, tokens, T, pos0, 1, false));
+    if (logits)
+        LLMQ_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * c.vocab, hipMemcpyDeviceToHost, m->ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(m->ctx->stream));
+    return LLMQ_OK;
+}
+
+int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int B, int n_prompt, int steps, int64_t *out_tokens,
+                        double *prefill_ms, double *decode_ms) {
+    LLMQ_REQUIRE(m && prompts && n_prompt >= 1 && steps >= 1 && out_tokens, "llama_generate: bad arguments");
+    const llmq_llama_cfg &c = m->cfg;
+    LLMQ_REQUIRE(B >= 1 && B <= c.batch, "llama_generate: %d sequences, capacity %d", B, c.batch);
+    LLMQ_REQUIRE(n_prompt + steps - 1 <= c.max_t, "llama_generate: %d + %d positions beyond %d", n_prompt, steps,
+                 c.max_t);
+    for (int64_t i = 0; i < (int64_t)B * n_prompt; i++)
+        LLMQ_REQUIRE(prompts[i] >= 0 && prompts[i] < c.vocab, "llama_generate: token %lld out of range",
+                     (long long)prompts[i]);
+    OwnStream os_(m->ctx);
+    llmq_ctx *ctx = m->ctx;
+    if (B != m->graph_B) drop_graph(m);  // a captured step serves one batch size
+    if ((int64_t)steps * B > m->gen_cap) {
+        hipFree(m->gen);
+        m->gen = nullptr;
+        m->gen_cap = 0;
+        if (hipMalloc(&m->gen, sizeof(int64_t) * steps * B) != hipSuccess)
+            return llmq_set_error(LLMQ_ENOMEM, "llama_generate: %d steps", steps);
+        m->gen_cap = (int64_t)steps * B;
+        drop_graph(m);  // it holds the old buffer's address
+    }
+    RC(ensure_rows(m, n_prompt));
+    const char *ge = getenv("LLMQ_GRAPH");
+    const bool use_graph = !(ge && ge[0] == '0');  // LLMQ_GRAPH=0: steps launched one by one
+    if (use_graph && steps > 1 && !m->step_graph) {
+        LLMQ_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        int rc = llama_step(m, B);
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+        if (rc != LLMQ_OK) {
+            if (g) hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return llmq_set_error(LLMQ_EHIP, "llama decode capture: %s", hipGetErrorString(e));
+        m->step_graph_def = g;
+        LLMQ_HIP(hipGraphInstantiate(&m->step_graph, g, nullptr, nullptr, 0));
+        m->graph_B = B;
+    }
+    hipEvent_t e0, e1, e2;
+    LLMQ_HIP(hipEventCreate(&e0));
+    LLMQ_HIP(hipEventCreate(&e1));
+    LLMQ_HIP(hipEventCreate(&e2));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    LLMQ_HIP(hipEventRecord(e0, ctx->stream));
+    for (int b = 0; b < B; b++) RC(llama_prefill(m, b, prompts + (int64_t)b * n_prompt, n_prompt, 0, B, true));
+    LLMQ_HIP(hipEventRecord(e1, ctx->stream));
+    const int init_state[4] = {n_prompt, 1, 0, 0};  // position of the first pick, gen row of the next
+    LLMQ_HIP(hipMemcpyAsync(m->state, init_state, sizeof(init_state), hipMemcpyHostToDevice, ctx->stream));
+    for (int i = 1; i < steps; i++) {
+        if (use_graph)
+            LLMQ_HIP(hipGraphLaunch(m->step_graph, ctx->stream));
+        else
+            RC(llama_step(m, B));
+    }
+    LLMQ_HIP(hipEventRecord(e2, ctx->stream));
+    LLMQ_HIP(hipEventSynchronize(e2));
+    float a = 0, bm = 0;
+    LLMQ_HIP(hipEventElapsedTime(&a, e0, e1));
+    LLMQ_HIP(hipEventElapsedTime(&bm, e1, e2));
+    if (prefill_ms) *prefill_ms = a;
+    if (decode_ms) *decode_ms = bm;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipEventDestroy(e2);
+    LLMQ_HIP(hipMemcpy(out_tokens, m->gen, sizeof(int64_t) * steps * B, hipMemcpyDeviceToHost));
+    return LLMQ_OK;
+}

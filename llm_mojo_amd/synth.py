@@ -90,17 +90,17 @@ GGUF_BLOCK = {  # ggml type id: (weights per block, bytes per block), gguf.mojo:
     2: (32, 18), 3: (32, 20), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
 
 
-def gguf_blocks(kind, rows, cols, seed):
+def gguf_blocks(kind, rows, cols, seed, scale=0.01):
     """Random GGUF blocks of BASELINE config 2: every code field uniform over
     its range (random bytes), 6-bit sub-scales / mins uniform (random bytes),
-    and the float16 scales |N(0, 0.01)| (Q4_1's min negative, as a min is)."""
+    and the float16 scales |N(0, scale)| (Q4_1's min negative, as a min is)."""
     bs, bb = GGUF_BLOCK[kind]
     nb = rows * (cols // bs)
     rng = np.random.default_rng(seed)
     b = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
 
     def f16(col, neg=False):
-        v = np.abs(rng.normal(0, 0.01, nb)).astype(np.float16)
+        v = np.abs(rng.normal(0, scale, nb)).astype(np.float16)
         if neg:
             v = -v
         b[:, col:col + 2] = v.view(np.uint8).reshape(nb, 2)
@@ -116,6 +116,32 @@ def gguf_blocks(kind, rows, cols, seed):
     elif kind == 14:
         f16(208)
     return b.reshape(-1)
+
+
+def llama_tensors(cfg, seed):
+    """Seeded random weights of the config-4 decoder, in llmq_llama_create's
+    order (llm_mojo_amd.llama.tensor_names): GGUF blocks whose float16 scales
+    keep weights near N(0, 0.02) in size (Q4_K d |N(0, 1e-4)|, Q6_K d
+    |N(0, 2e-5)|), norm gains 1."""
+    from .llama import tensor_names, tensor_shapes
+
+    shapes = tensor_shapes(cfg)
+    out = []
+    for i, name in enumerate(tensor_names(cfg["n_layer"])):
+        kind = name.rsplit(".", 1)[-1]
+        if kind.endswith("norm"):
+            out.append(np.ones(cfg["dim"], np.float32))
+            continue
+        t = cfg["head_type"] if kind == "output" else (cfg["embd_type"] if kind == "token_embd" else cfg["layer_type"])
+        rows, cols = shapes[kind]
+        out.append(gguf_blocks(t, rows, cols, seed * 1000 + i, scale=2e-5 if t == 14 else 1e-4))
+    return out
+
+
+def llama_prompts(seed, batch, n, vocab):
+    """batch x n token ids from the reference's Rng, id = floor(uniform * vocab)."""
+    rng = Rng(seed)
+    return np.array([[min(vocab - 1, int(rng.uniform() * vocab)) for _ in range(n)] for _ in range(batch)], np.int64)
 
 
 def prompt_ids(seed, n):

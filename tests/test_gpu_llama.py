@@ -1,0 +1,123 @@
+"""The config-4 decoder (llm_mojo_amd/llama.py) on the GPU against its NumPy
+statement (tests/llama_ref.py).  The reference has no such model, so these
+pin our own definition (model-level parity unpinned); the GGUF, cache and
+int16-head parts come from the oracle."""
+import numpy as np
+import pytest
+
+from tests.llama_ref import NumpyLlama
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layer=2, dim=256, n_head=4, n_kv=2, head_dim=64, ffn=512, vocab=1000, max_t=96, batch=2,
+             layer_type=12, head_type=14, embd_type=12, eps=1e-5, theta=10000.0)
+
+
+def rel(a, b):
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+def test_llama_forward_matches_numpy(gpu):
+    """Prefill of 20 tokens, then 3 more on the same cache: last-token
+    logits within 1e-3 of max |logit|."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    tensors = synth.llama_tensors(SMALL, 5)
+    toks = synth.llama_prompts(5, 1, 23, SMALL["vocab"])[0]
+    print("llama forward", flush=True)
+    m = lm.Llama(ctx, SMALL, tensors)
+    ref = NumpyLlama(SMALL, tensors)
+    got = m.forward(0, toks[:20], 0)
+    want = ref.forward(0, toks[:20], 0)
+    assert rel(got, want) < 1e-3, rel(got, want)
+    got = m.forward(0, toks[20:], 20)
+    want = ref.forward(0, toks[20:], 20)
+    assert rel(got, want) < 1e-3, rel(got, want)
+    m.free()
+
+
+def test_llama_generate_matches_numpy_greedy(gpu):
+    """Two sequences, 12-token prompts, 6 greedy tokens each (5 batched decode
+    steps through the captured graph) against NumPy greedy decoding; a step
+    whose NumPy top-2 margin is under 1e-3 of max |logit| ends the comparison
+    of that sequence."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    tensors = synth.llama_tensors(SMALL, 6)
+    prompts = synth.llama_prompts(6, 2, 12, SMALL["vocab"])
+    print("llama generate", flush=True)
+    m = lm.Llama(ctx, SMALL, tensors)
+    toks, pre_ms, dec_ms = m.generate(prompts, 6)
+    assert toks.shape == (6, 2)
+    ref = NumpyLlama(SMALL, tensors, n_seq=2)
+    for b in range(2):
+        logits = ref.forward(b, prompts[b], 0)
+        for i in range(6):
+            top = np.sort(logits)[-2:]
+            want = int(np.argmax(logits))
+            if top[1] - top[0] < 1e-3 * np.max(np.abs(logits)):
+                break
+            assert toks[i, b] == want, (b, i, toks[:, b], want)
+            logits = ref.forward(b, [want], 12 + i)
+    m.free()
+
+
+def test_llama_batch_rows_are_independent(gpu):
+    """The same prompt in both sequences of a batch gives the same tokens,
+    equal to a one-sequence run; a second call (graph replayed) repeats them."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    tensors = synth.llama_tensors(SMALL, 7)
+    p = synth.llama_prompts(7, 1, 10, SMALL["vocab"])
+    print("llama batch", flush=True)
+    m = lm.Llama(ctx, SMALL, tensors)
+    two, _, _ = m.generate(np.concatenate([p, p]), 8)
+    one, _, _ = m.generate(p, 8)
+    again, _, _ = m.generate(p, 8)
+    assert np.array_equal(two[:, 0], two[:, 1])
+    assert np.array_equal(two[:, 0], one[:, 0])
+    assert np.array_equal(one, again)
+    m.free()
+
+
+def test_llama_rejects_bad_shapes(gpu):
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    bad = dict(SMALL, n_kv=3)
+    with pytest.raises(lm.LlmqError, match="unsupported shape"):
+        lm.Llama(ctx, bad, synth.llama_tensors(SMALL, 1))
+    m = lm.Llama(ctx, SMALL, synth.llama_tensors(SMALL, 1))
+    with pytest.raises(lm.LlmqError, match="capacity"):
+        m.generate(np.zeros((3, 4), np.int64), 2)
+    with pytest.raises(lm.LlmqError, match="beyond"):
+        m.forward(0, np.zeros(4, np.int64), SMALL["max_t"] - 2)
+    m.free()
+
+
+def test_llama_long_context_decode(gpu):
+    """Decode attention past 1024 positions (three positions a thread of the
+    512-thread workgroup): a 1026-token prompt, then 3 greedy tokens, against
+    NumPy greedy decoding (the same margin rule)."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    cfg = dict(SMALL, max_t=1100, batch=1)
+    tensors = synth.llama_tensors(cfg, 8)
+    prompt = synth.llama_prompts(8, 1, 1026, cfg["vocab"])
+    print("llama long context", flush=True)
+    m = lm.Llama(ctx, cfg, tensors)
+    toks, _, _ = m.generate(prompt, 4)
+    ref = NumpyLlama(cfg, tensors)
+    logits = ref.forward(0, prompt[0], 0)
+    for i in range(4):
+        top = np.sort(logits)[-2:]
+        want = int(np.argmax(logits))
+        if top[1] - top[0] < 1e-3 * np.max(np.abs(logits)):
+            break
+        assert toks[i, 0] == want, (i, toks[:, 0], want)
+        logits = ref.forward(0, [want], 1026 + i)
+    m.free()

@@ -194,6 +194,38 @@ def gguf_sweep(torch, lm, synth, ctx, rot_bytes=512 << 20):
     return res
 
 
+LLAMA_PROMPT, LLAMA_GEN, LLAMA_SEED = 1024, 128, 4004
+
+
+def llama_decode(lm, synth, ctx):
+    """Config 4: the TinyLlama-shaped decoder (Q4_K layers, Q6_K head, int8
+    KV cache) with seeded random weights; a 1024-token random prompt per
+    sequence, then 128 greedy tokens at batch 1 and batch 16.  tok/s as the
+    reference defines it: generated tokens after the first (the decode steps)
+    over the decode span, summed over the batch."""
+    cfg = dict(lm.TINYLLAMA, batch=16)
+    m = lm.Llama(ctx, cfg, synth.llama_tensors(cfg, LLAMA_SEED))
+    res = {"weight_bytes": int(m.weight_bytes())}
+    # bytes one decode step reads at batch 1: every matrix but the embedding
+    # (one row), and the cache up to the mean position
+    embd = cfg["vocab"] * (cfg["dim"] // 256) * 144
+    kv_pos = cfg["n_layer"] * cfg["n_kv"] * 2 * (64 + 4)
+    mean_pos = LLAMA_PROMPT + (LLAMA_GEN - 1) / 2
+    step_bytes = res["weight_bytes"] - embd + embd // cfg["vocab"] + kv_pos * mean_pos
+    for B in (1, 16):
+        prompts = synth.llama_prompts(LLAMA_SEED, B, LLAMA_PROMPT, cfg["vocab"])
+        m.generate(prompts, 8)  # warm: graph capture
+        toks, pre_ms, dec_ms = m.generate(prompts, LLAMA_GEN)
+        tok_s = B * (LLAMA_GEN - 1) / (dec_ms / 1000.0)
+        res[f"bs{B}_decode_tok_s"] = round(tok_s, 1)
+        res[f"bs{B}_ms_per_step"] = round(dec_ms / (LLAMA_GEN - 1), 3)
+        res[f"bs{B}_prefill_tok_s"] = round(B * LLAMA_PROMPT / (pre_ms / 1000.0), 1)
+        if B == 1:
+            res["bs1_decode_gbs_effective"] = round(step_bytes * tok_s / 1e9, 1)
+    m.free()
+    return res
+
+
 def cpu_baseline(tensors, prompt, budget_s=20.0):
     """The CPU oracle (a C restatement of llm_mojo's CPU path, oracle/) on
     this host's cores: the same prompt, then greedy decode steps until about
@@ -231,6 +263,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 476-token prefill (config 3)")
+    ap.add_argument("--no-llama", action="store_true", help="skip the TinyLlama-shaped decoder (config 4)")
     ap.add_argument("--gguf-sweep", action="store_true", help="add the GGUF GEMV sweep (config 2, ~1 min)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline GEMV and the reference copy (for rocprofv3 --pmc runs)")
@@ -294,6 +327,10 @@ def main():
         log("prefill 476")
         extra["prefill_476"] = prefill(torch, lm, synth, ctx, tensors, model)
         log(extra["prefill_476"])
+    if not args.no_llama:
+        log("tinyllama-shaped decode")
+        extra["tinyllama_q4k_q6k"] = llama_decode(lm, synth, ctx)
+        log(extra["tinyllama_q4k_q6k"])
     if args.gguf_sweep:
         log("gguf sweep")
         extra["gguf_gemv_sweep"] = gguf_sweep(torch, lm, synth, ctx)

@@ -157,7 +157,7 @@ __global__ __launch_bounds__(kDecNT) void attend_decode_kernel(const float *__re
     }
     if (tid < HD) q[tid] = qkv[(int64_t)b * ld + h * HD + tid];
 #pragma unroll
-    for (int i = 0; i < MAXP; i++) {  // value rows to LDS as they arrive
+    for (int i = 0; i < MAXP; i++) {  // value rows to LDS
         const int s = tid + kDecNT * i;
         if (s < npos) {
 #pragma unroll
@@ -165,6 +165,15 @@ __global__ __launch_bounds__(kDecNT) void attend_decode_kernel(const float *__re
         }
     }
     __syncthreads();
+    float qr[HD];  // the query in registers
+#pragma unroll
+    for (int j = 0; j < HD / 4; j++) {
+        const float4 v = reinterpret_cast<const float4 *>(q)[j];
+        qr[4 * j] = v.x;
+        qr[4 * j + 1] = v.y;
+        qr[4 * j + 2] = v.z;
+        qr[4 * j + 3] = v.w;
+    }
     const float scale = 1.0f / sqrtf((float)HD);
     float sc[MAXP];
     float mx = -INFINITY;
@@ -178,7 +187,7 @@ __global__ __launch_bounds__(kDecNT) void attend_decode_kernel(const float *__re
                                     (uint32_t)kr[i][j].w};
 #pragma unroll
             for (int e = 0; e < 16; e++)
-                d = fmaf(q[16 * j + e], (float)(int8_t)((kw[e >> 2] >> (8 * (e & 3))) & 255u), d);
+                d = fmaf(qr[16 * j + e], (float)(int8_t)((kw[e >> 2] >> (8 * (e & 3))) & 255u), d);
         }
         sc[i] = d * ks[i] * scale;
         if (s < npos) mx = fmaxf(mx, sc[i]);
@@ -209,8 +218,21 @@ __global__ __launch_bounds__(kDecNT) void attend_decode_kernel(const float *__re
         if (s < npos) wt[s] = (sc[i] / tot) * vs[i];  // p * vs
     }
     __syncthreads();
+    // values in batches of 8 positions: the LDS reads of a batch are issued
+    // together, the products added in position order
     float acc = 0.0f;
-    for (int s = w; s < npos; s += NW) acc = fmaf(wt[s], (float)vrow[(int64_t)s * HD + lane], acc);
+    int s = w;
+    for (; s + 7 * NW < npos; s += 8 * NW) {
+        float pw[8], vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            pw[u] = wt[s + u * NW];
+            vv[u] = (float)vrow[(int64_t)(s + u * NW) * HD + lane];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = fmaf(pw[u], vv[u], acc);
+    }
+    for (; s < npos; s += NW) acc = fmaf(wt[s], (float)vrow[(int64_t)s * HD + lane], acc);
     vred[w][lane] = acc;
     __syncthreads();
     if (tid < HD) {

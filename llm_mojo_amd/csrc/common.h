@@ -154,8 +154,10 @@ int gguf_block_size(int ggml_type);   // weights per block (gguf.mojo:72-83)
 int gguf_block_bytes(int ggml_type);  // bytes per block (gguf.mojo:86-98)
 int gguf_upload(llmq_ctx *ctx, llmq_mat *m, int ggml_type, const uint8_t *blocks, int64_t rows, int64_t cols);
 int gguf_num_parts(const llmq_mat *w);
+// One-token GGUF GEMV (gguf1.hip); with rms_g the row is RMS-normalized
+// (times the gain rms_g) before the product.
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
-                     ArgmaxPart *amax, int amax_cap);
+                     ArgmaxPart *amax, int amax_cap, const float *rms_g = nullptr, float rms_eps = 0.0f);
 int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
 int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *rows, int n, float *dst, int64_t ldd);
 // Prompt attention over an int8 cache of n_kv heads (attn.hip): query head h
@@ -168,7 +170,9 @@ int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t l
                      int64_t ldo, const float *bias, int flags);
 // int16 output head for Q6_K / Q8_0 (gguf_head.hip).
 int gguf_has_i16(const llmq_mat *w);
-int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *logits, int64_t T);
+// with rms_g, each row of h is RMS-normalized (times rms_g) first
+int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *logits, int64_t T,
+                       const float *rms_g = nullptr, float rms_eps = 0.0f);
 
 int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C);
 int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,

@@ -41,6 +41,8 @@ struct G1Args {
     const float *x, *bias;
     float *out;
     ArgmaxPart *amax;
+    const float *rms_g;  // optional RMSNorm gain: x -> x / sqrt(mean(x^2) + eps) * g first
+    float rms_eps;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
@@ -162,6 +164,7 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     __shared__ __align__(16) uint8_t s_meta[NW][St::LOADS * 1024];
     __shared__ __align__(16) uint8_t s_d6[NW][St::D6_LOADS > 0 ? St::D6_LOADS * 1024 : 16];
     __shared__ ArgmaxPart s_best[NW];
+    __shared__ float s_red[NW];
 
     const int K = a.K, CK = a.CK;
     float *xs = smem_f;                                // [K] activations
@@ -257,6 +260,35 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
         for (int i = 0; i < St::D6_LOADS; i++) reinterpret_cast<uint4 *>(s_d6[wid])[i * 64 + lane] = wd6[i];
     }
     lds_barrier();
+    if (a.rms_g) {  // RMSNorm of the staged row (llama.hip's rmsnorm, fused)
+        float ss = 0.0f;
+        for (int u = tid; u < nunits; u += NT) {
+            const float4 v = reinterpret_cast<const float4 *>(xs)[u];
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) s_red[wid] = ss;
+        lds_barrier();
+        ss = s_red[0];
+#pragma unroll
+        for (int i = 1; i < NW; i++) ss += s_red[i];
+        const float r = 1.0f / sqrtf(ss / (float)K + a.rms_eps);
+        const float4 *g4 = reinterpret_cast<const float4 *>(a.rms_g);
+        for (int u = tid; u < nunits; u += NT) {
+            float4 v = reinterpret_cast<const float4 *>(xs)[u];
+            const float4 g = g4[u];
+            v.x = (v.x * r) * g.x;
+            v.y = (v.y * r) * g.y;
+            v.z = (v.z * r) * g.z;
+            v.w = (v.w * r) * g.w;
+            reinterpret_cast<float4 *>(xs)[u] = v;
+        }
+        lds_barrier();
+    }
     for (int g = tid; g < K / 16; g += NT) {
         const float4 *p = reinterpret_cast<const float4 *>(xs + 16 * g);
         const float4 v0 = p[0], v1 = p[1], v2 = p[2], v3 = p[3];
@@ -489,7 +521,7 @@ int launch_type(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
 int gguf_num_parts(const llmq_mat *w) { return make_plan(w).grid; }
 
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
-                     ArgmaxPart *amax, int amax_cap) {
+                     ArgmaxPart *amax, int amax_cap, const float *rms_g, float rms_eps) {
     LLMQ_REQUIRE(w && w->kind == MAT_GGUF, "gguf_gemv: not a GGUF matrix");
     LLMQ_REQUIRE(x && out, "gguf_gemv: null pointer");
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemv: LLMQ_BIAS without a bias");
@@ -522,6 +554,8 @@ int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *ou
     a.bias = bias ? bias : out;  // read (and ignored) without LLMQ_BIAS
     a.out = out;
     a.amax = amax;
+    a.rms_g = rms_g;
+    a.rms_eps = rms_eps;
     int rc;
     switch (w->ggml_type) {
     case LLMQ_GGML_Q4_0: rc = launch_type<LLMQ_GGML_Q4_0>(ctx, a, p, lds); break;

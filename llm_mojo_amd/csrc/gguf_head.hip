@@ -36,6 +36,8 @@ struct H16Args {
     int V, C, CK, NU;
     const float *h;
     float *logits;
+    const float *rms_g;  // optional RMSNorm gain applied to h first
+    float rms_eps;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
@@ -166,11 +168,41 @@ __global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
     const int tile = blockIdx.x, t = blockIdx.y;
     const float *h = a.h + (size_t)t * a.C;
 
-    // quantize_rows for this token: s = max|h| / 32767, q = round(h / s)
     const int n4 = a.C / 4;
+    // optional RMSNorm: h -> (h * rn) * g, rn = 1 / sqrt(mean(h^2) + eps)
+    float rn = 1.0f;
+    const float4 *g4 = reinterpret_cast<const float4 *>(a.rms_g);
+    if (a.rms_g) {
+        float ss = 0.0f;
+        for (int i = tid; i < n4; i += kNW * 64) {
+            const float4 v = reinterpret_cast<const float4 *>(h)[i];
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) red[wid] = ss;
+        __syncthreads();
+        ss = ((red[0] + red[1]) + red[2]) + red[3];
+        rn = 1.0f / sqrtf(ss / (float)a.C + a.rms_eps);
+        __syncthreads();
+    }
+    auto row4 = [&](int i) {
+        float4 v = reinterpret_cast<const float4 *>(h)[i];
+        if (a.rms_g) {
+            const float4 g = g4[i];
+            v.x = (v.x * rn) * g.x;
+            v.y = (v.y * rn) * g.y;
+            v.z = (v.z * rn) * g.z;
+            v.w = (v.w * rn) * g.w;
+        }
+        return v;
+    };
+    // quantize_rows for this token: s = max|h| / 32767, q = round(h / s)
     float m = 0.0f;
     for (int i = tid; i < n4; i += kNW * 64) {
-        const float4 v = reinterpret_cast<const float4 *>(h)[i];
+        const float4 v = row4(i);
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -181,7 +213,7 @@ __global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
     if (sx == 0.0f) sx = 1.0f;
     const float inv = 1.0f / sx;
     for (int i = tid; i < n4; i += kNW * 64) {
-        const float4 v = reinterpret_cast<const float4 *>(h)[i];
+        const float4 v = row4(i);
         const int q0 = round_to_int(v.x * inv), q1 = round_to_int(v.y * inv);
         const int q2 = round_to_int(v.z * inv), q3 = round_to_int(v.w * inv);
         xq32[2 * i] = ((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16);
@@ -245,7 +277,8 @@ int gguf_has_i16(const llmq_mat *w) {
     return w && w->kind == MAT_GGUF && (w->ggml_type == LLMQ_GGML_Q6_K || w->ggml_type == LLMQ_GGML_Q8_0);
 }
 
-int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *logits, int64_t T) {
+int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *logits, int64_t T,
+                       const float *rms_g, float rms_eps) {
     LLMQ_REQUIRE(gguf_has_i16(w), "gguf head: only Q6_K and Q8_0 have an int16 kernel");
     LLMQ_REQUIRE(h && logits && T > 0 && T <= 65535, "gguf head: bad arguments");
     const size_t lds = head16_lds(w);
@@ -265,6 +298,8 @@ int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *
     a.CK = (int)w->CK;
     a.h = h;
     a.logits = logits;
+    a.rms_g = rms_g;
+    a.rms_eps = rms_eps;
     if (w->ggml_type == LLMQ_GGML_Q6_K) {
         a.bits = reinterpret_cast<const uint8_t *>(w->g_bits64);
         a.bits_bytes = (uint32_t)(ntc * 8);

@@ -377,6 +377,16 @@ int linear(llmq_llama *m, const llmq_mat *w, const float *x, int64_t ldx, int R,
     return launch_gguf_gemm(m->ctx, w, x, ldx, R, out, ldo, nullptr, flags);
 }
 
+// rmsnorm(x) * g then the matmul: for one row the GEMV normalizes the row it
+// stages (no separate kernel), else the norm goes to m->xn first.
+int norm_linear(llmq_llama *m, const float *g, const llmq_mat *w, int R, float *out, int64_t ldo, int flags) {
+    const llmq_llama_cfg &c = m->cfg;
+    if (R == 1) return launch_gguf_gemv(m->ctx, w, m->x, out, nullptr, flags, nullptr, 0, g, c.eps);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(256), 0, m->ctx->stream, m->x, (int64_t)c.dim, g, m->xn,
+                       (int64_t)c.dim, c.dim, c.eps);
+    return launch_gguf_gemm(m->ctx, w, m->xn, c.dim, R, out, ldo, nullptr, flags);
+}
+
 // The layers for R = nseq * T rows in m->x: T tokens of sequences seq0 ..
 // at positions pos0 + t (prefill: nseq = 1), or one token of every
 // sequence at position state[0] (decode: T = 1, state given).
@@ -385,9 +395,7 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
     const llmq_llama_cfg &c = m->cfg;
     const int QC = qkv_cols(c);
     for (int l = 0; l < c.n_layer; l++) {
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(256), 0, ctx->stream, m->x, (int64_t)c.dim, gain(m, l, 0),
-                           m->xn, (int64_t)c.dim, c.dim, c.eps);
-        RC(linear(m, m->wqkv[l], m->xn, c.dim, R, m->qkv, QC, 0));
+        RC(norm_linear(m, gain(m, l, 0), m->wqkv[l], R, m->qkv, QC, 0));
         hipLaunchKernelGGL(rope_store_kernel, dim3(c.n_head + c.n_kv, R), dim3(64), 0, ctx->stream, m->qkv,
                            (int64_t)QC, T, seq0, pos0, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, c.theta,
                            m->k8, m->v8, m->ks, m->vs);
@@ -408,9 +416,7 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
                                     c.n_kv, m->qkv, QC, pos0, T, m->att, c.dim));
         }
         RC(linear(m, m->wo[l], m->att, c.dim, R, m->x, c.dim, LLMQ_RESID));
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(256), 0, ctx->stream, m->x, (int64_t)c.dim, gain(m, l, 1),
-                           m->xn, (int64_t)c.dim, c.dim, c.eps);
-        RC(linear(m, m->wgu[l], m->xn, c.dim, R, m->gu, 2 * c.ffn, 0));
+        RC(norm_linear(m, gain(m, l, 1), m->wgu[l], R, m->gu, 2 * c.ffn, 0));
         hipLaunchKernelGGL(swiglu_kernel, dim3((c.ffn + 255) / 256, R), dim3(256), 0, ctx->stream, m->gu,
                            (int64_t)2 * c.ffn, m->hh, (int64_t)c.ffn, c.ffn);
         RC(linear(m, m->wdown[l], m->hh, c.ffn, R, m->x, c.dim, LLMQ_RESID));
@@ -419,15 +425,17 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
     return LLMQ_OK;
 }
 
-// The output norm and head for nrows rows of m->x starting at row r0 (with
-// stride `every` rows), into m->logits.
-int llama_head(llmq_llama *m, int r0, int nrows, int every) {
+// The output norm and head for nrows consecutive rows of m->x from row r0,
+// into m->logits.
+int llama_head(llmq_llama *m, int r0, int nrows) {
     llmq_ctx *ctx = m->ctx;
     const llmq_llama_cfg &c = m->cfg;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, ctx->stream, m->x + (int64_t)r0 * c.dim,
-                       (int64_t)every * c.dim, m->norms + (size_t)2 * c.n_layer * c.dim, m->xn, (int64_t)c.dim, c.dim,
-                       c.eps);
-    if (gguf_has_i16(m->head)) return launch_gguf_head16(ctx, m->head, m->xn, m->logits, nrows);
+    const float *g = m->norms + (size_t)2 * c.n_layer * c.dim;
+    const float *x = m->x + (int64_t)r0 * c.dim;
+    // the int16 head normalizes the rows it quantizes
+    if (gguf_has_i16(m->head)) return launch_gguf_head16(ctx, m->head, x, m->logits, nrows, g, c.eps);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, ctx->stream, x, (int64_t)c.dim, g, m->xn,
+                       (int64_t)c.dim, c.dim, c.eps);
     return linear(m, m->head, m->xn, c.dim, nrows, m->logits, c.vocab, 0);
 }
 
@@ -438,7 +446,7 @@ int llama_step(llmq_llama *m, int B) {
     const llmq_llama_cfg &c = m->cfg;
     RC(launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim));
     RC(llama_layers(m, B, 1, 0, 0, m->state));
-    RC(llama_head(m, 0, B, 1));
+    RC(llama_head(m, 0, B));
     hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab, B, 0,
                        m->state, m->next, m->gen);
     hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, ctx->stream, m->state);
@@ -455,7 +463,7 @@ int llama_prefill(llmq_llama *m, int seq, const int64_t *tokens, int T, int pos0
     LLMQ_HIP(hipMemcpyAsync(m->tokens, tokens, sizeof(int64_t) * T, hipMemcpyHostToDevice, ctx->stream));
     RC(launch_gguf_dequant_rows(ctx, m->embd, m->tokens, T, m->x, c.dim));
     RC(llama_layers(m, T, T, seq, pos0, nullptr));
-    RC(llama_head(m, T - 1, 1, 1));
+    RC(llama_head(m, T - 1, 1));
     if (pick)
         hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab,
                            B, seq, nullptr, m->next, m->gen);

@@ -114,133 +114,118 @@ __global__ __launch_bounds__(64) void rope_store_kernel(float *__restrict__ qkv,
 // One decode position for query head h = blockIdx.x of sequence b =
 // blockIdx.y at position state[0]: attend_float_one (kvcache.mojo:113-150)
 // over the int8 cache (QuantKV.score / add_value, 344-370) of key / value
-// head h / (n_head / n_kv).  Thread tid scores positions tid + NT i
-// (i < MAXP), loading all of their key and value rows first, and stages the
-// value rows in LDS; after the softmax it leaves w = p * vs per position.
-// Values: wave w takes positions w, w + NT / 64, .. with lane = dim; the
-// waves' partial sums are added in wave order.
-constexpr int kDecNT = 512;
-template <int MAXP>
-__global__ __launch_bounds__(kDecNT) void attend_decode_kernel(const float *__restrict__ qkv, int64_t ld,
-                                                               const int *__restrict__ state, int n_head, int n_kv,
-                                                               int n_layer, int layer, int max_t,
-                                                               const int8_t *__restrict__ K8,
-                                                               const int8_t *__restrict__ V8,
-                                                               const float *__restrict__ KS,
-                                                               const float *__restrict__ VS, float *__restrict__ out,
-                                                               int64_t ldo) {
-    constexpr int NW = kDecNT / 64;
-    extern __shared__ __align__(16) float sm[];
-    float *wt = sm;                                        // [max_t] scores, then p * vs
-    int8_t *vrow = reinterpret_cast<int8_t *>(sm + max_t);  // [max_t][HD] value rows
+// head h / (n_head / n_kv), split over blocks of kSplit positions
+// (blockIdx.z) so a head's positions are scored in parallel.  A split writes
+// its maximum score m, its sum of e = exp(score - m) and its partial
+// sum_s (e * vs) * v; attend_combine_kernel rescales the splits to the
+// overall maximum and divides by the overall sum.  (The reference divides
+// each e by the total before the value products; the float rounding
+// differs, the sums are the same.)
+constexpr int kSplit = 128;
+constexpr int kPart = 2 + HD;  // floats of one split's result
+
+__global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__restrict__ qkv, int64_t ld,
+                                                              const int *__restrict__ state, int n_head, int n_kv,
+                                                              int n_layer, int layer, int max_t,
+                                                              const int8_t *__restrict__ K8,
+                                                              const int8_t *__restrict__ V8,
+                                                              const float *__restrict__ KS,
+                                                              const float *__restrict__ VS, float *__restrict__ part,
+                                                              int NS) {
     __shared__ __align__(16) float q[HD];
-    __shared__ float red[NW], vred[NW][HD];
-    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ __align__(16) int8_t vrow[kSplit][HD];
+    __shared__ float wv[kSplit], red[2], vred[2][HD];
+    const int h = blockIdx.x, b = blockIdx.y, j = blockIdx.z, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int npos = state[0] + 1;
+    float *P = part + (((int64_t)b * n_head + h) * NS + j) * kPart;
+    const int s0 = j * kSplit;
+    if (s0 >= npos) {  // an empty split (uniform over the workgroup)
+        if (tid < kPart) P[tid] = tid == 0 ? -INFINITY : 0.0f;
+        return;
+    }
+    const int cnt = min(kSplit, npos - s0);
+    const bool valid = tid < cnt;
     const int kvh = h / (n_head / n_kv);
-    const int64_t base = ((int64_t)b * n_layer + layer) * max_t * n_kv + kvh;  // slot of position 0
-    int4 kr[MAXP][HD / 16], vr[MAXP][HD / 16];
-    float ks[MAXP], vs[MAXP];
+    const int64_t sl = (((int64_t)b * n_layer + layer) * max_t + s0 + (valid ? tid : 0)) * n_kv + kvh;
+    int4 kr[HD / 16], vr[HD / 16];
 #pragma unroll
-    for (int i = 0; i < MAXP; i++) {
-        const int s = tid + kDecNT * i;
-        const int64_t sl = base + (int64_t)(s < npos ? s : 0) * n_kv;
-        const int4 *kp = reinterpret_cast<const int4 *>(K8 + sl * HD);
-        const int4 *vp = reinterpret_cast<const int4 *>(V8 + sl * HD);
-#pragma unroll
-        for (int j = 0; j < HD / 16; j++) {
-            kr[i][j] = kp[j];
-            vr[i][j] = vp[j];
-        }
-        ks[i] = KS[sl];
-        vs[i] = VS[sl];
+    for (int i = 0; i < HD / 16; i++) {
+        kr[i] = reinterpret_cast<const int4 *>(K8 + sl * HD)[i];
+        vr[i] = reinterpret_cast<const int4 *>(V8 + sl * HD)[i];
     }
+    const float ks = KS[sl], vs = VS[sl];
     if (tid < HD) q[tid] = qkv[(int64_t)b * ld + h * HD + tid];
+    if (valid) {
 #pragma unroll
-    for (int i = 0; i < MAXP; i++) {  // value rows to LDS
-        const int s = tid + kDecNT * i;
-        if (s < npos) {
+        for (int i = 0; i < HD / 16; i++) reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
+    }
+    __syncthreads();
+    float d = 0.0f;
 #pragma unroll
-            for (int j = 0; j < HD / 16; j++) reinterpret_cast<int4 *>(vrow + (int64_t)s * HD)[j] = vr[i][j];
+    for (int i = 0; i < HD / 16; i++) {
+        const uint32_t kw[4] = {(uint32_t)kr[i].x, (uint32_t)kr[i].y, (uint32_t)kr[i].z, (uint32_t)kr[i].w};
+        const float4 *q4 = reinterpret_cast<const float4 *>(q + 16 * i);
+#pragma unroll
+        for (int e4 = 0; e4 < 4; e4++) {
+            const float4 qv = q4[e4];
+            d = fmaf(qv.x, (float)(int8_t)(kw[e4] & 255u), d);
+            d = fmaf(qv.y, (float)(int8_t)((kw[e4] >> 8) & 255u), d);
+            d = fmaf(qv.z, (float)(int8_t)((kw[e4] >> 16) & 255u), d);
+            d = fmaf(qv.w, (float)(int8_t)(kw[e4] >> 24), d);
         }
     }
+    const float score = valid ? d * ks * (1.0f / sqrtf((float)HD)) : -INFINITY;
+    float m = wave_max(score);
+    if (lane == 0) red[w] = m;
     __syncthreads();
-    float qr[HD];  // the query in registers
-#pragma unroll
-    for (int j = 0; j < HD / 4; j++) {
-        const float4 v = reinterpret_cast<const float4 *>(q)[j];
-        qr[4 * j] = v.x;
-        qr[4 * j + 1] = v.y;
-        qr[4 * j + 2] = v.z;
-        qr[4 * j + 3] = v.w;
-    }
-    const float scale = 1.0f / sqrtf((float)HD);
-    float sc[MAXP];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < MAXP; i++) {
-        const int s = tid + kDecNT * i;
-        float d = 0.0f;
-#pragma unroll
-        for (int j = 0; j < HD / 16; j++) {
-            const uint32_t kw[4] = {(uint32_t)kr[i][j].x, (uint32_t)kr[i][j].y, (uint32_t)kr[i][j].z,
-                                    (uint32_t)kr[i][j].w};
-#pragma unroll
-            for (int e = 0; e < 16; e++)
-                d = fmaf(qr[16 * j + e], (float)(int8_t)((kw[e >> 2] >> (8 * (e & 3))) & 255u), d);
-        }
-        sc[i] = d * ks[i] * scale;
-        if (s < npos) mx = fmaxf(mx, sc[i]);
-    }
-    // workgroup max, then the sum of e, waves in order
-    mx = wave_max(mx);
-    if (lane == 0) red[w] = mx;
+    m = fmaxf(red[0], red[1]);
+    const float e = valid ? expf(score - m) : 0.0f;
+    wv[tid] = e * vs;
+    float t = wave_sum(e);
     __syncthreads();
-    mx = red[0];
-#pragma unroll
-    for (int i = 1; i < NW; i++) mx = fmaxf(mx, red[i]);
-    float tot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < MAXP; i++) {
-        sc[i] = expf(sc[i] - mx);
-        if (tid + kDecNT * i < npos) tot += sc[i];
-    }
-    tot = wave_sum(tot);
+    if (lane == 0) red[w] = t;
     __syncthreads();
-    if (lane == 0) red[w] = tot;
-    __syncthreads();
-    tot = red[0];
-#pragma unroll
-    for (int i = 1; i < NW; i++) tot += red[i];
-#pragma unroll
-    for (int i = 0; i < MAXP; i++) {
-        const int s = tid + kDecNT * i;
-        if (s < npos) wt[s] = (sc[i] / tot) * vs[i];  // p * vs
-    }
-    __syncthreads();
-    // values in batches of 8 positions: the LDS reads of a batch are issued
-    // together, the products added in position order
+    t = red[0] + red[1];
+    // values: wave w takes positions w, w + 2, ..; lane = dim
     float acc = 0.0f;
-    int s = w;
-    for (; s + 7 * NW < npos; s += 8 * NW) {
+    int sp = w;
+    for (; sp + 14 < cnt; sp += 16) {
         float pw[8], vv[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            pw[u] = wt[s + u * NW];
-            vv[u] = (float)vrow[(int64_t)(s + u * NW) * HD + lane];
+            pw[u] = wv[sp + 2 * u];
+            vv[u] = (float)vrow[sp + 2 * u][lane];
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) acc = fmaf(pw[u], vv[u], acc);
     }
-    for (; s < npos; s += NW) acc = fmaf(wt[s], (float)vrow[(int64_t)s * HD + lane], acc);
+    for (; sp < cnt; sp += 2) acc = fmaf(wv[sp], (float)vrow[sp][lane], acc);
     vred[w][lane] = acc;
     __syncthreads();
-    if (tid < HD) {
-        float o = vred[0][tid];
-#pragma unroll
-        for (int i = 1; i < NW; i++) o += vred[i][tid];
-        out[(int64_t)b * ldo + h * HD + tid] = o;
+    if (tid < HD) P[2 + tid] = vred[0][tid] + vred[1][tid];
+    if (tid == 0) {
+        P[0] = m;
+        P[1] = t;
     }
+}
+
+// The splits of (head blockIdx.x, sequence blockIdx.y) into the output:
+// out = sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j - M), splits in order.
+__global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int NS, int n_head,
+                                                            const int *__restrict__ state, float *__restrict__ out,
+                                                            int64_t ldo) {
+    const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x;
+    const int ns = min(NS, (state[0] + 1 + kSplit - 1) / kSplit);
+    const float *P = part + ((int64_t)b * n_head + h) * NS * kPart;
+    float M = -INFINITY;
+    for (int j = 0; j < ns; j++) M = fmaxf(M, P[j * kPart]);
+    float T = 0.0f, acc = 0.0f;
+    for (int j = 0; j < ns; j++) {
+        const float f = expf(P[j * kPart] - M);
+        T = fmaf(P[j * kPart + 1], f, T);
+        acc = fmaf(P[j * kPart + 2 + dd], f, acc);
+    }
+    out[(int64_t)b * ldo + h * HD + dd] = acc / T;
 }
 
 // h[r][i] = silu(g) * u with g = gu[r][i], u = gu[r][F + i].
@@ -316,6 +301,7 @@ struct llmq_llama {
     float *ks = nullptr, *vs = nullptr;
     // activations for up to `rows` tokens
     int rows = 0;
+    float *apart = nullptr;  // decode attention split results
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *hh = nullptr,
           *logits = nullptr;
     int64_t *tokens = nullptr, *next = nullptr, *gen = nullptr;
@@ -400,17 +386,12 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
                            (int64_t)QC, T, seq0, pos0, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, c.theta,
                            m->k8, m->v8, m->ks, m->vs);
         if (state) {
-            const size_t lds = (size_t)c.max_t * (4 + HD);
-            const int maxp = (c.max_t + kDecNT - 1) / kDecNT;
-#define ATT(P)                                                                                                    \
-    hipLaunchKernelGGL(attend_decode_kernel<P>, dim3(c.n_head, R), dim3(kDecNT), lds, ctx->stream, m->qkv,         \
-                       (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->k8, m->v8, m->ks, m->vs, m->att, \
-                       (int64_t)c.dim)
-            if (maxp == 1) ATT(1);
-            else if (maxp == 2) ATT(2);
-            else if (maxp == 3) ATT(3);
-            else ATT(4);
-#undef ATT
+            const int NS = (c.max_t + kSplit - 1) / kSplit;
+            hipLaunchKernelGGL(attend_split_kernel, dim3(c.n_head, R, NS), dim3(kSplit), 0, ctx->stream, m->qkv,
+                               (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->k8, m->v8, m->ks, m->vs,
+                               m->apart, NS);
+            hipLaunchKernelGGL(attend_combine_kernel, dim3(c.n_head, R), dim3(HD), 0, ctx->stream, m->apart, NS,
+                               c.n_head, state, m->att, (int64_t)c.dim);
         } else {
             RC(launch_attend_prompt(ctx, m->k8, m->v8, m->ks, m->vs, seq0 * c.n_layer + l, c.max_t, c.n_head,
                                     c.n_kv, m->qkv, QC, pos0, T, m->att, c.dim));
@@ -483,7 +464,7 @@ int llmq_llama_free(llmq_llama *m) {
     for (auto *w : m->wo) llmq_mat_free(w);
     for (auto *w : m->wgu) llmq_mat_free(w);
     for (auto *w : m->wdown) llmq_mat_free(w);
-    void *bufs[] = {m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
+    void *bufs[] = {m->apart, m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
                     m->tokens, m->next, m->gen, m->state};
     for (void *p : bufs) hipFree(p);
     delete m;
@@ -497,7 +478,6 @@ int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *cons
                      c.head_dim == HD && c.n_head * c.head_dim == c.dim && c.ffn > 0 && c.vocab > 0 &&
                      c.max_t > 0 && c.batch > 0,
                  "llama_create: unsupported shape (head_dim must be 64, n_head * head_dim == dim)");
-    LLMQ_REQUIRE(c.max_t <= 4 * kDecNT, "llama_create: max_t %d too long for the decode attention", c.max_t);
     for (int ty : {c.layer_type, c.head_type, c.embd_type})
         LLMQ_REQUIRE(gguf_is_supported(ty), "llama_create: ggml type %d is not a supported block format", ty);
     llmq_llama *m = new llmq_llama();
@@ -561,15 +541,10 @@ int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *cons
             hipMemset(m->ks, 0, slots * 4) != hipSuccess || hipMemset(m->vs, 0, slots * 4) != hipSuccess)
             GO(llmq_set_error(LLMQ_EHIP, "llama: cache clear"));
         GO(ensure_rows(m, c.batch));
-        // the decode attention's LDS (scores and value rows of every position)
-        const int lds = c.max_t * (4 + HD);
-        const void *att[4] = {reinterpret_cast<const void *>(attend_decode_kernel<1>),
-                              reinterpret_cast<const void *>(attend_decode_kernel<2>),
-                              reinterpret_cast<const void *>(attend_decode_kernel<3>),
-                              reinterpret_cast<const void *>(attend_decode_kernel<4>)};
-        for (const void *k : att)
-            if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-                GO(llmq_set_error(LLMQ_EUNSUPPORTED, "llama: %d bytes of LDS for max_t %d", lds, c.max_t));
+        {   // decode attention partials: batch x heads x splits
+            const size_t np = (size_t)c.batch * c.n_head * ((c.max_t + kSplit - 1) / kSplit) * kPart;
+            if (hipMalloc(&m->apart, np * 4) != hipSuccess) GO(llmq_set_error(LLMQ_ENOMEM, "llama: attention partials"));
+        }
     }
 #undef GO
     *out = m;

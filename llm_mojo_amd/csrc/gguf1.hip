@@ -43,7 +43,17 @@ struct G1Args {
     ArgmaxPart *amax;
     const float *rms_g;  // optional RMSNorm gain: x -> x / sqrt(mean(x^2) + eps) * g first
     float rms_eps;
+    int swiglu;          // x holds [gate | up] of 2K floats: the row is silu(gate) * up
 };
+
+// silu(g) * u per lane of two activation vectors (llama.hip's swiglu).
+__device__ __forceinline__ uint4 swiglu4(uint4 g, uint4 u) {
+    auto f = [](uint32_t gb, uint32_t ub) {
+        const float x = __uint_as_float(gb), y = __uint_as_float(ub);
+        return __float_as_uint((x / (1.0f + expf(-x))) * y);
+    };
+    return make_uint4(f(g.x, u.x), f(g.y, u.y), f(g.z, u.z), f(g.w, u.w));
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
@@ -186,12 +196,13 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     //    fields, codes and high bits, then the epilogue operands.
     const int nunits = K / 4;
     constexpr int UPT = 4;  // up to 16 KiB of activations per round of 1024 threads
-    const auto rx = make_rsrc(a.x, (uint32_t)K * 4u);
-    uint4 xv[UPT];
+    const auto rx = make_rsrc(a.x, (uint32_t)K * (a.swiglu ? 8u : 4u));
+    uint4 xv[UPT], xu[UPT];
 #pragma unroll
     for (int i = 0; i < UPT; i++) {
         const uint32_t u = (uint32_t)(tid + NT * i);
         xv[i] = bload16(rx, u < (uint32_t)nunits ? u * 16u : kOOB);
+        if (a.swiglu) xu[i] = bload16(rx, u < (uint32_t)nunits ? (u + (uint32_t)nunits) * 16u : kOOB);
     }
     // Global chunk indices of the wave's first and last valid chunks.
     const int gE = g0 + max(ns, 1) - 1;
@@ -250,9 +261,12 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
 #pragma unroll
     for (int i = 0; i < UPT; i++) {
         const int u = tid + NT * i;
-        if (u < nunits) reinterpret_cast<uint4 *>(xs)[u] = xv[i];
+        if (u < nunits) reinterpret_cast<uint4 *>(xs)[u] = a.swiglu ? swiglu4(xv[i], xu[i]) : xv[i];
     }
-    for (int u = tid + NT * UPT; u < nunits; u += NT) reinterpret_cast<uint4 *>(xs)[u] = bload16(rx, (uint32_t)u * 16u);
+    for (int u = tid + NT * UPT; u < nunits; u += NT) {
+        const uint4 v = bload16(rx, (uint32_t)u * 16u);
+        reinterpret_cast<uint4 *>(xs)[u] = a.swiglu ? swiglu4(v, bload16(rx, (uint32_t)(u + nunits) * 16u)) : v;
+    }
 #pragma unroll
     for (int i = 0; i < St::LOADS; i++) reinterpret_cast<uint4 *>(s_meta[wid])[i * 64 + lane] = wm[i];
     if constexpr (St::D6_LOADS > 0) {
@@ -521,7 +535,7 @@ int launch_type(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
 int gguf_num_parts(const llmq_mat *w) { return make_plan(w).grid; }
 
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
-                     ArgmaxPart *amax, int amax_cap, const float *rms_g, float rms_eps) {
+                     ArgmaxPart *amax, int amax_cap, const float *rms_g, float rms_eps, int swiglu) {
     LLMQ_REQUIRE(w && w->kind == MAT_GGUF, "gguf_gemv: not a GGUF matrix");
     LLMQ_REQUIRE(x && out, "gguf_gemv: null pointer");
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemv: LLMQ_BIAS without a bias");
@@ -556,6 +570,7 @@ int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *ou
     a.amax = amax;
     a.rms_g = rms_g;
     a.rms_eps = rms_eps;
+    a.swiglu = swiglu;
     int rc;
     switch (w->ggml_type) {
     case LLMQ_GGML_Q4_0: rc = launch_type<LLMQ_GGML_Q4_0>(ctx, a, p, lds); break;

@@ -398,9 +398,13 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
         }
         RC(linear(m, m->wo[l], m->att, c.dim, R, m->x, c.dim, LLMQ_RESID));
         RC(norm_linear(m, gain(m, l, 1), m->wgu[l], R, m->gu, 2 * c.ffn, 0));
-        hipLaunchKernelGGL(swiglu_kernel, dim3((c.ffn + 255) / 256, R), dim3(256), 0, ctx->stream, m->gu,
-                           (int64_t)2 * c.ffn, m->hh, (int64_t)c.ffn, c.ffn);
-        RC(linear(m, m->wdown[l], m->hh, c.ffn, R, m->x, c.dim, LLMQ_RESID));
+        if (R == 1) {  // the GEMV forms silu(gate) * up as it stages its row
+            RC(launch_gguf_gemv(ctx, m->wdown[l], m->gu, m->x, nullptr, LLMQ_RESID, nullptr, 0, nullptr, 0.0f, 1));
+        } else {
+            hipLaunchKernelGGL(swiglu_kernel, dim3((c.ffn + 255) / 256, R), dim3(256), 0, ctx->stream, m->gu,
+                               (int64_t)2 * c.ffn, m->hh, (int64_t)c.ffn, c.ffn);
+            RC(linear(m, m->wdown[l], m->hh, c.ffn, R, m->x, c.dim, LLMQ_RESID));
+        }
     }
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;

@@ -14,7 +14,8 @@
 // over units in order, the 16-lane halving sum) are the reference's, so a
 // row's logit is the same float whatever the tile or token count.
 //
-// Work mapping: one workgroup per (16-row tile, token), 4 waves.  Thread
+// Work mapping: one workgroup per (16-row tile, up to 8 tokens taken one
+// after another), 4 waves.  Thread
 // (r, q) of a wave (r = lane % 16, q = lane / 16) computes lanes 4q..4q+3 of
 // row r for a unit: Q6_K reads dword q of each of the unit's 8 chunks of 32
 // codes (weights 8q..8q+7) and the matching 16 high bits; Q8_0 reads bytes
@@ -33,7 +34,7 @@ typedef short short2v __attribute__((ext_vector_type(2)));
 struct H16Args {
     const uint8_t *codes, *bits, *sb, *d;
     uint32_t codes_bytes, bits_bytes, sb_bytes, d_bytes;
-    int V, C, CK, NU;
+    int V, C, CK, NU, T, tpb;  // tpb: tokens a workgroup takes, one after another
     const float *h;
     float *logits;
     const float *rms_g;  // optional RMSNorm gain applied to h first
@@ -165,7 +166,11 @@ __global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
     float *dv = lanev + U::R * 256;                                        // [R][16 rows]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tile = blockIdx.x, t = blockIdx.y;
+    const int tile = blockIdx.x;
+    const int tb = blockIdx.y * a.tpb, te = min(a.T, tb + a.tpb);
+    // Tokens one after another: the tile's weights come from HBM for the
+    // first and from L2 for the rest.
+    for (int t = tb; t < te; t++) {
     const float *h = a.h + (size_t)t * a.C;
 
     const int n4 = a.C / 4;
@@ -251,6 +256,8 @@ __global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
     accf += __shfl_xor(accf, 1);
     const int row = tile * 16 + pr;
     if (pl == 0 && row < a.V) a.logits[(size_t)t * a.V + row] = accf * sx;
+    __syncthreads();  // before the next token's codes overwrite the LDS
+    }
 }
 
 size_t head16_lds(const llmq_mat *w) {
@@ -266,7 +273,8 @@ int launch_t(llmq_ctx *ctx, const H16Args &a, int ntiles, int T, size_t lds) {
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         granted = lds;
     }
-    hipLaunchKernelGGL(gguf_head16_kernel<TYPE>, dim3(ntiles, T), dim3(kNW * 64), lds, ctx->stream, a);
+    hipLaunchKernelGGL(gguf_head16_kernel<TYPE>, dim3(ntiles, (T + a.tpb - 1) / a.tpb), dim3(kNW * 64), lds,
+                       ctx->stream, a);
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }
@@ -298,6 +306,8 @@ int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *
     a.CK = (int)w->CK;
     a.h = h;
     a.logits = logits;
+    a.T = (int)T;
+    a.tpb = T < 8 ? (int)T : 8;
     a.rms_g = rms_g;
     a.rms_eps = rms_eps;
     if (w->ggml_type == LLMQ_GGML_Q6_K) {

@@ -88,7 +88,7 @@ def test_gguf_unsupported_type(gpu):
 
 @pytest.mark.parametrize("kind", ["Q6_K", "Q8_0"])
 @pytest.mark.parametrize("V,C,T,big", [(70, 512, 1, False), (300, 768, 5, False), (1000, 2048, 1, True),
-                                       (4000, 4096, 2, False), (32000, 2048, 1, False)])
+                                       (4000, 4096, 2, False), (32000, 2048, 1, False), (300, 768, 20, False)])
 def test_gguf_int16_head_exact(gpu, orc, kind, V, C, T, big):
     """head_i16 (kernels.mojo:693-736) for Q6_K / Q8_0 heads: the logits equal
     the oracle's dot_row_i16 * sx bit for bit (same int32 lanes, same float

@@ -211,19 +211,33 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
 
 // The splits of (head blockIdx.x, sequence blockIdx.y) into the output:
 // out = sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j - M), splits in order.
+// Up to kMaxSplits splits, all loaded before use.
+constexpr int kMaxSplits = 16;
 __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int NS, int n_head,
                                                             const int *__restrict__ state, float *__restrict__ out,
                                                             int64_t ldo) {
     const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x;
     const int ns = min(NS, (state[0] + 1 + kSplit - 1) / kSplit);
     const float *P = part + ((int64_t)b * n_head + h) * NS * kPart;
-    float M = -INFINITY;
-    for (int j = 0; j < ns; j++) M = fmaxf(M, P[j * kPart]);
+    float mj[kMaxSplits], tj[kMaxSplits], aj[kMaxSplits];
+#pragma unroll
+    for (int j = 0; j < kMaxSplits; j++) {
+        const bool ok = j < ns;
+        mj[j] = ok ? P[j * kPart] : -INFINITY;
+        tj[j] = ok ? P[j * kPart + 1] : 0.0f;
+        aj[j] = ok ? P[j * kPart + 2 + dd] : 0.0f;
+    }
+    float M = mj[0];
+#pragma unroll
+    for (int j = 1; j < kMaxSplits; j++) M = fmaxf(M, mj[j]);
     float T = 0.0f, acc = 0.0f;
-    for (int j = 0; j < ns; j++) {
-        const float f = expf(P[j * kPart] - M);
-        T = fmaf(P[j * kPart + 1], f, T);
-        acc = fmaf(P[j * kPart + 2 + dd], f, acc);
+#pragma unroll
+    for (int j = 0; j < kMaxSplits; j++) {
+        if (j < ns) {
+            const float f = expf(mj[j] - M);
+            T = fmaf(tj[j], f, T);
+            acc = fmaf(aj[j], f, acc);
+        }
     }
     out[(int64_t)b * ldo + h * HD + dd] = acc / T;
 }
@@ -237,18 +251,35 @@ __global__ void swiglu_kernel(const float *__restrict__ gu, int64_t ldg, float *
     }
 }
 
-// Greedy pick (gpt2t.mojo:792-797: the first maximum) of logits row i for
-// sequence b0 + i: next token and gen[step * B + b0 + i], step = state[1]
-// (0 without state).
-__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int64_t ld, int V, int B,
-                                                     int b0, const int *__restrict__ state,
-                                                     int64_t *__restrict__ next, int64_t *__restrict__ gen) {
-    __shared__ float bv[4];
-    __shared__ int bi[4];
+// Greedy pick (gpt2t.mojo:792-797: the first maximum) of logits row i =
+// blockIdx.x for sequence b0 + i: the next token and gen[step * B + b0 + i],
+// step = state[1] (0 without state).  With `advance`, the last workgroup to
+// finish moves the decode state on (position and step + 1; state[2] counts
+// the finished workgroups and is cleared again).
+constexpr int kArgNT = 1024;
+__global__ __launch_bounds__(kArgNT) void argmax_kernel(const float *__restrict__ logits, int64_t ld, int V, int B,
+                                                        int b0, int *__restrict__ state, int advance,
+                                                        int64_t *__restrict__ next, int64_t *__restrict__ gen) {
+    constexpr int NW = kArgNT / 64;
+    __shared__ float bv[NW];
+    __shared__ int bi[NW];
     const float *l = logits + (int64_t)blockIdx.x * ld;
+    const int tid = threadIdx.x;
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < V; i += 256) {
+    int i = tid;
+    for (; i + 7 * kArgNT < V; i += 8 * kArgNT) {  // 8 loads in flight, compared in index order
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) x[u] = l[i + u * kArgNT];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (x[u] > v) {
+                v = x[u];
+                idx = i + u * kArgNT;
+            }
+    }
+    for (; i < V; i += kArgNT) {
         const float x = l[i];
         if (x > v) {
             v = x;
@@ -264,15 +295,15 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ l
             idx = oi;
         }
     }
-    if ((threadIdx.x & 63) == 0) {
-        bv[threadIdx.x >> 6] = v;
-        bi[threadIdx.x >> 6] = idx;
+    if ((tid & 63) == 0) {
+        bv[tid >> 6] = v;
+        bi[tid >> 6] = idx;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         v = bv[0];
         idx = bi[0];
-        for (int k = 1; k < 4; k++)
+        for (int k = 1; k < NW; k++)
             if (bv[k] > v || (bv[k] == v && bi[k] < idx)) {
                 v = bv[k];
                 idx = bi[k];
@@ -281,12 +312,15 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ l
         const int step = state ? state[1] : 0;
         next[b] = idx;
         gen[(int64_t)step * B + b] = idx;
+        if (advance) {
+            __threadfence();
+            if (atomicAdd(&state[2], 1) == (int)gridDim.x - 1) {  // every workgroup has read the step
+                state[2] = 0;
+                state[0] += 1;
+                state[1] += 1;
+            }
+        }
     }
-}
-
-__global__ void advance_kernel(int *state) {
-    state[0] += 1;
-    state[1] += 1;
 }
 
 }  // namespace
@@ -425,16 +459,15 @@ int llama_head(llmq_llama *m, int r0, int nrows) {
 }
 
 // One decode step of every sequence: embed the previous picks, the layers,
-// the head, the picks, then the position and step advance.
+// the head, the picks and the position and step advance.
 int llama_step(llmq_llama *m, int B) {
     llmq_ctx *ctx = m->ctx;
     const llmq_llama_cfg &c = m->cfg;
     RC(launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim));
     RC(llama_layers(m, B, 1, 0, 0, m->state));
     RC(llama_head(m, 0, B));
-    hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab, B, 0,
-                       m->state, m->next, m->gen);
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, ctx->stream, m->state);
+    hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(kArgNT), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab, B,
+                       0, m->state, 1, m->next, m->gen);
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }
@@ -450,8 +483,8 @@ int llama_prefill(llmq_llama *m, int seq, const int64_t *tokens, int T, int pos0
     RC(llama_layers(m, T, T, seq, pos0, nullptr));
     RC(llama_head(m, T - 1, 1));
     if (pick)
-        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab,
-                           B, seq, nullptr, m->next, m->gen);
+        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgNT), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab,
+                           B, seq, nullptr, 0, m->next, m->gen);
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }
@@ -482,6 +515,7 @@ int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *cons
                      c.head_dim == HD && c.n_head * c.head_dim == c.dim && c.ffn > 0 && c.vocab > 0 &&
                      c.max_t > 0 && c.batch > 0,
                  "llama_create: unsupported shape (head_dim must be 64, n_head * head_dim == dim)");
+    LLMQ_REQUIRE(c.max_t <= kSplit * kMaxSplits, "llama_create: max_t %d beyond %d", c.max_t, kSplit * kMaxSplits);
     for (int ty : {c.layer_type, c.head_type, c.embd_type})
         LLMQ_REQUIRE(gguf_is_supported(ty), "llama_create: ggml type %d is not a supported block format", ty);
     llmq_llama *m = new llmq_llama();

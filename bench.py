@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of llm_mojo's quantized matmul path on one MI355X.
 
-Metric (BASELINE.json): decode tok/s of GPT-2 124M int4-g32-a16 at batch 1
+Metric: decode tok/s of GPT-2 124M int4-g32-a16 at batch 1
 (config 0: seeded random-init weights, int8 per-channel head, int8 KV cache,
 a 12-token random prompt, then 100 greedy tokens), plus the achieved HBM
 bandwidth of the W4A16 group-32 GEMV at 4096 x 11008 against the 8 TB/s peak.

@@ -204,8 +204,8 @@ LLMQ_API int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_promp
 LLMQ_API int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr);
 
 /* ---------------------------------------------------------------- config 4
- * A TinyLlama-shaped decoder over GGUF weights (RMSNorm,
- * RoPE, grouped key / value heads, SwiGLU).  No counterpart in the reference,
+ * A TinyLlama-shaped decoder over GGUF weights (the benchmark's fifth
+ * configuration: RMSNorm, RoPE, grouped key / value heads, SwiGLU).  No counterpart in the reference,
  * whose model code is GPT-2 only (gpt2t.mojo:74-81); it composes the GGUF
  * kernels above (GGUFMatrix, gguf.mojo:344-511; matmul_rows and head_i16,
  * kernels.mojo:285-349, 693-736) with the int8 cache (QuantKV[8],

@@ -1,5 +1,5 @@
-// A TinyLlama-shaped decoder over GGUF weights: the model of BASELINE.json's
-// config 4 (22 layers, d_model 2048, 32 query / 4 key-value heads of 64,
+// A TinyLlama-shaped decoder over GGUF weights: the benchmark's fifth
+// configuration (22 layers, d_model 2048, 32 query / 4 key-value heads of 64,
 // SwiGLU FFN 5632, RMSNorm, RoPE theta 10000, vocab 32000; Q4_K layers, Q6_K
 // head, int8 KV cache), decoding one or several independent sequences.
 //

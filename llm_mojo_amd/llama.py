@@ -1,5 +1,5 @@
-"""A TinyLlama-shaped decoder over GGUF weights on libllmq.so (BASELINE
-config 4: Q4_K layers, Q6_K head, int8 KV cache, grouped key / value heads,
+"""A TinyLlama-shaped decoder over GGUF weights on libllmq.so (the
+benchmark's fifth configuration: Q4_K layers, Q6_K head, int8 KV cache, grouped key / value heads,
 RMSNorm, RoPE, SwiGLU).  The reference has no such model (its model code is
 GPT-2 only, gpt2t.mojo:74-81); the GGUF kernels it runs on are the
 reference's (gguf.mojo:344-511, kernels.mojo:285-349, 693-736).

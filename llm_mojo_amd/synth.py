@@ -91,7 +91,7 @@ GGUF_BLOCK = {  # ggml type id: (weights per block, bytes per block), gguf.mojo:
 
 
 def gguf_blocks(kind, rows, cols, seed, scale=0.01):
-    """Random GGUF blocks of BASELINE config 2: every code field uniform over
+    """Random GGUF blocks of the Llama GEMV sweep: every code field uniform over
     its range (random bytes), 6-bit sub-scales / mins uniform (random bytes),
     and the float16 scales |N(0, scale)| (Q4_1's min negative, as a min is)."""
     bs, bb = GGUF_BLOCK[kind]

@@ -1,6 +1,6 @@
 """End-to-end GPT-2 124M int4-g32-a16 (+ int8-ch head, int8 KV) on the GPU
 against the CPU oracle's restatement of gpt2t.mojo, on the seeded synthetic
-checkpoint of BASELINE.json config 0.
+checkpoint (seeded N(0, 0.02) weights).
 
 Code flips: int16 activation codes are round(x / s) of float32 values that
 reach the two sides through different float32 summation orders, so an

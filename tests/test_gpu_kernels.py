@@ -1,6 +1,6 @@
 """GPU parity of the HIP kernels against the CPU oracle, through the C ABI.
 
-Bars (BASELINE.json north_star): quantized codes, activation codes and the
+Bars: quantized codes, activation codes and the
 per-group integer sums bit-exact; float32 outputs within 1e-5 of max |out|
 (the reference's own A16 tolerance, tests/a16_kernels.mojo:70).
 """

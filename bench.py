@@ -94,6 +94,43 @@ def copy_bandwidth(torch, nbytes=1 << 30, reps=20):
     return 2 * nbytes * reps / (e0.elapsed_time(e1) / 1000.0) / 1e9
 
 
+GPT2_SHAPES = [("qkv", 768, 2304), ("proj", 768, 768), ("fc", 768, 3072), ("fcproj", 3072, 768)]
+GEMV_FORMATS = [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)]
+
+
+def gemv_micro(torch, lm, ctx, reps=200):
+    """Config 1: the one-token A16 GEMV at the GPT-2 shapes, int4 and int8 at
+    groups 32 / 64 / 128, and the int8 per-channel head (768 x 50257): one
+    matrix, launched back to back (it stays in the 256 MB Infinity Cache, as
+    in decode); GB/s of nbytes + 2K + 4N per launch.  The small matrices'
+    times (~4 us) are launch to launch, the kernel's own latency floor."""
+    stream = torch.cuda.Stream()
+    res = {}
+    with torch.cuda.stream(stream):
+        ctx.set_stream(stream)
+        g = torch.Generator(device="cuda").manual_seed(1001)
+        cases = [(f"int{b}-g{gr} {n}", K, N, b, gr) for b, gr in GEMV_FORMATS for n, K, N in GPT2_SHAPES]
+        cases.append(("int8-ch head", 768, 50257, 8, 0))
+        for name, K, N, bits, group in cases:
+            w = lm.HipQuantMatrix.from_f32(ctx, torch.randn((K, N), device="cuda", generator=g) * 0.02, bits, group,
+                                           False, True)
+            x = torch.randn((1, K), device="cuda", generator=g)
+            out = torch.empty((1, N), device="cuda")
+            for _ in range(10):
+                lm.linear(ctx, out, x, w)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                lm.linear(ctx, out, x, w)
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / reps
+            res[name] = {"us": round(us, 2), "gbs": round((w.nbytes() + 2 * K + 4 * N) / us / 1e3, 1)}
+            w.free()
+    ctx.set_stream(None)
+    return res
+
+
 PREFILL_T = 476
 INT8_MFMA_PEAK = 5.0e15  # dense int8 MFMA ops/s of MI355X
 LAYER_SHAPES = [("qkv", 768, 2304), ("proj", 768, 768), ("fc", 768, 3072), ("fcproj", 3072, 768)]
@@ -323,6 +360,8 @@ def main():
     extra["decode_bytes_per_token"] = int(token_bytes)
     extra["decode_gbs_effective"] = round(token_bytes * tok_s / 1e9, 1)
 
+    log("gemv micro")
+    extra["gemv_micro_llc"] = gemv_micro(torch, lm, ctx)
     if not args.no_prefill:
         log("prefill 476")
         extra["prefill_476"] = prefill(torch, lm, synth, ctx, tensors, model)

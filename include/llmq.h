@@ -172,6 +172,20 @@ LLMQ_API int llmq_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const 
 /* Copies the cache's codes and scales to host buffers (parity tests). */
 LLMQ_API int llmq_kv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, float *ks, float *vs);
 
+/* IntAttnKV.create (int_attention.mojo:99-113): the same int8 codes
+ * [layer, pos, head, head_dim] with the scales as int32 = round(scale * 2^24)
+ * [layer, pos, head].  Shape check of int_attention.mojo:100-101 (max_t % 16,
+ * head_dim % 32: LLMQ_EINVAL); this build covers head_dim 64 and 128.
+ * llmq_kv_store, llmq_kv_attend, llmq_kv_nbytes and llmq_kv_free take the
+ * handle like any cache: store is IntAttnKV.store (132-168), attend runs
+ * IntAttnKV.attend_one (170-269) for every token and head, in integers
+ * (intmath.masked_exp, intmath.mojo:93-123). */
+LLMQ_API int llmq_ikv_create(llmq_ctx *ctx, int n_layer, int max_t, int n_head, int head_dim, llmq_kv **out);
+/* 1 for an IntAttnKV cache, 0 for QuantKV[8]. */
+LLMQ_API int llmq_kv_is_integer(const llmq_kv *kv);
+/* Copies an IntAttnKV cache's codes and int32 scales to host buffers. */
+LLMQ_API int llmq_ikv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, int32_t *kq, int32_t *vq);
+
 /* ------------------------------------------------ GPT-2 (the caller) */
 
 /* load_model (gpt2t.mojo:579-609) from float32 host tensors in Hugging Face
@@ -185,6 +199,12 @@ LLMQ_API int llmq_kv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t 
  * cache QuantKV[8] (1238-1244). */
 LLMQ_API int llmq_gpt2_create(llmq_ctx *ctx, const float *const *params, int bits, int group, int sym,
                               llmq_gpt2 **out);
+/* The same with the attention chosen as gpt2t.mojo's --attention does
+ * (gpt2t.mojo:856, 1251-1257): LLMQ_ATTN_FLOAT (QuantKV[8], float
+ * attention) or LLMQ_ATTN_INT (IntAttnKV, integer attention). */
+enum { LLMQ_ATTN_FLOAT = 0, LLMQ_ATTN_INT = 1 };
+LLMQ_API int llmq_gpt2_create_ex(llmq_ctx *ctx, const float *const *params, int bits, int group, int sym,
+                                 int attention, llmq_gpt2 **out);
 LLMQ_API int llmq_gpt2_free(llmq_gpt2 *m);
 /* Model.weight_bytes (gpt2t.mojo:312-319). */
 LLMQ_API int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m);

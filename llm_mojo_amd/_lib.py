@@ -56,7 +56,11 @@ SIGNATURES = {
     "llmq_kv_store": (I32, [P, P, I32, I32, P, I32]),
     "llmq_kv_attend": (I32, [P, P, P, P, I32, I32, I32]),
     "llmq_kv_export": (I32, [P, P, P, P, P, P]),
+    "llmq_ikv_create": (I32, [P, I32, I32, I32, I32, PP]),
+    "llmq_kv_is_integer": (I32, [P]),
+    "llmq_ikv_export": (I32, [P, P, P, P, P, P]),
     "llmq_gpt2_create": (I32, [P, P, I32, I32, I32, PP]),
+    "llmq_gpt2_create_ex": (I32, [P, P, I32, I32, I32, I32, PP]),
     "llmq_gpt2_free": (I32, [P]),
     "llmq_gpt2_weight_bytes": (I64, [P]),
     "llmq_gpt2_forward": (I32, [P, P, I32, I32, P]),

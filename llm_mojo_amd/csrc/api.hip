@@ -425,29 +425,47 @@ int llmq_debug_chunk_sums(llmq_ctx *ctx, const float *xf, const llmq_mat *w, flo
 
 // ------------------------------------------------------------- int8 KV cache
 
-int llmq_kv_create(llmq_ctx *ctx, int n_layer, int max_t, int n_head, int head_dim, llmq_kv **out) {
-    LLMQ_REQUIRE(ctx && out && n_layer > 0 && max_t > 0 && n_head > 0 && head_dim > 0, "kv_create: bad arguments");
-    LLMQ_REQUIRE(head_dim % 64 == 0 || head_dim == 16 || head_dim == 32, "kv_create: head_dim %d unsupported",
-                 head_dim);
+static int kv_alloc(llmq_ctx *ctx, int n_layer, int max_t, int n_head, int head_dim, int integer, llmq_kv **out) {
     llmq_kv *kv = new llmq_kv();
     kv->ctx = ctx;
     kv->n_layer = n_layer;
     kv->max_t = max_t;
     kv->n_head = n_head;
     kv->head_dim = head_dim;
+    kv->integer = integer;
     const size_t n = (size_t)n_layer * max_t * n_head * head_dim, ns = (size_t)n_layer * max_t * n_head;
+    void **ks = integer ? reinterpret_cast<void **>(&kv->kq) : reinterpret_cast<void **>(&kv->ks);
+    void **vs = integer ? reinterpret_cast<void **>(&kv->vq) : reinterpret_cast<void **>(&kv->vs);
     if (hipMalloc(&kv->k, n) != hipSuccess || hipMalloc(&kv->v, n) != hipSuccess ||
-        hipMalloc(&kv->ks, ns * 4) != hipSuccess || hipMalloc(&kv->vs, ns * 4) != hipSuccess) {
+        hipMalloc(ks, ns * 4) != hipSuccess || hipMalloc(vs, ns * 4) != hipSuccess) {
         llmq_kv_free(kv);
         return llmq_set_error(LLMQ_ENOMEM, "kv_create: allocation failed");
     }
     LLMQ_HIP(hipMemsetAsync(kv->k, 0, n, ctx->stream));
     LLMQ_HIP(hipMemsetAsync(kv->v, 0, n, ctx->stream));
-    LLMQ_HIP(hipMemsetAsync(kv->ks, 0, ns * 4, ctx->stream));
-    LLMQ_HIP(hipMemsetAsync(kv->vs, 0, ns * 4, ctx->stream));
+    LLMQ_HIP(hipMemsetAsync(*ks, 0, ns * 4, ctx->stream));
+    LLMQ_HIP(hipMemsetAsync(*vs, 0, ns * 4, ctx->stream));
     *out = kv;
     return LLMQ_OK;
 }
+
+int llmq_kv_create(llmq_ctx *ctx, int n_layer, int max_t, int n_head, int head_dim, llmq_kv **out) {
+    LLMQ_REQUIRE(ctx && out && n_layer > 0 && max_t > 0 && n_head > 0 && head_dim > 0, "kv_create: bad arguments");
+    LLMQ_REQUIRE(head_dim % 64 == 0 || head_dim == 16 || head_dim == 32, "kv_create: head_dim %d unsupported",
+                 head_dim);
+    return kv_alloc(ctx, n_layer, max_t, n_head, head_dim, 0, out);
+}
+
+int llmq_ikv_create(llmq_ctx *ctx, int n_layer, int max_t, int n_head, int head_dim, llmq_kv **out) {
+    LLMQ_REQUIRE(ctx && out && n_layer > 0 && max_t > 0 && n_head > 0 && head_dim > 0, "ikv_create: bad arguments");
+    // IntAttnKV.create's shape check (int_attention.mojo:100-101, 283-284)
+    LLMQ_REQUIRE(max_t % 16 == 0 && head_dim % 32 == 0, "IntAttnKV needs max_t %% 16 == 0 and head_dim %% 32 == 0");
+    if (head_dim != 64 && head_dim != 128)
+        return llmq_set_error(LLMQ_EUNSUPPORTED, "ikv_create: head_dim %d (64 or 128)", head_dim);
+    return kv_alloc(ctx, n_layer, max_t, n_head, head_dim, 1, out);
+}
+
+int llmq_kv_is_integer(const llmq_kv *kv) { return kv ? kv->integer : 0; }
 
 int llmq_kv_free(llmq_kv *kv) {
     if (!kv) return LLMQ_OK;
@@ -456,6 +474,8 @@ int llmq_kv_free(llmq_kv *kv) {
     hipFree(kv->v);
     hipFree(kv->ks);
     hipFree(kv->vs);
+    hipFree(kv->kq);
+    hipFree(kv->vq);
     delete kv;
     return LLMQ_OK;
 }
@@ -478,12 +498,26 @@ int llmq_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qk
 
 int llmq_kv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, float *ks, float *vs) {
     LLMQ_REQUIRE(ctx && kv, "kv_export: bad arguments");
+    LLMQ_REQUIRE(!kv->integer, "kv_export: an IntAttnKV cache holds integer scales (llmq_ikv_export)");
     const size_t n = (size_t)kv->n_layer * kv->max_t * kv->n_head * kv->head_dim,
                  ns = (size_t)kv->n_layer * kv->max_t * kv->n_head;
     if (k) LLMQ_HIP(hipMemcpyAsync(k, kv->k, n, hipMemcpyDeviceToHost, ctx->stream));
     if (v) LLMQ_HIP(hipMemcpyAsync(v, kv->v, n, hipMemcpyDeviceToHost, ctx->stream));
     if (ks) LLMQ_HIP(hipMemcpyAsync(ks, kv->ks, ns * 4, hipMemcpyDeviceToHost, ctx->stream));
     if (vs) LLMQ_HIP(hipMemcpyAsync(vs, kv->vs, ns * 4, hipMemcpyDeviceToHost, ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    return LLMQ_OK;
+}
+
+int llmq_ikv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, int32_t *kq, int32_t *vq) {
+    LLMQ_REQUIRE(ctx && kv, "ikv_export: bad arguments");
+    LLMQ_REQUIRE(kv->integer, "ikv_export: not an IntAttnKV cache (llmq_kv_export)");
+    const size_t n = (size_t)kv->n_layer * kv->max_t * kv->n_head * kv->head_dim,
+                 ns = (size_t)kv->n_layer * kv->max_t * kv->n_head;
+    if (k) LLMQ_HIP(hipMemcpyAsync(k, kv->k, n, hipMemcpyDeviceToHost, ctx->stream));
+    if (v) LLMQ_HIP(hipMemcpyAsync(v, kv->v, n, hipMemcpyDeviceToHost, ctx->stream));
+    if (kq) LLMQ_HIP(hipMemcpyAsync(kq, kv->kq, ns * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (vq) LLMQ_HIP(hipMemcpyAsync(vq, kv->vq, ns * 4, hipMemcpyDeviceToHost, ctx->stream));
     LLMQ_HIP(hipStreamSynchronize(ctx->stream));
     return LLMQ_OK;
 }
@@ -609,7 +643,13 @@ int llmq_gpt2_free(llmq_gpt2 *m) {
 }
 
 int llmq_gpt2_create(llmq_ctx *ctx, const float *const *params, int bits, int group, int sym, llmq_gpt2 **out) {
+    return llmq_gpt2_create_ex(ctx, params, bits, group, sym, LLMQ_ATTN_FLOAT, out);
+}
+
+int llmq_gpt2_create_ex(llmq_ctx *ctx, const float *const *params, int bits, int group, int sym, int attention,
+                        llmq_gpt2 **out) {
     LLMQ_REQUIRE(ctx && params && out, "gpt2_create: bad arguments");
+    LLMQ_REQUIRE(attention == LLMQ_ATTN_FLOAT || attention == LLMQ_ATTN_INT, "gpt2_create: attention %d", attention);
     llmq_gpt2 *m = new llmq_gpt2();
     m->ctx = ctx;
     int rc = LLMQ_OK;
@@ -655,7 +695,11 @@ int llmq_gpt2_create(llmq_ctx *ctx, const float *const *params, int bits, int gr
             rc = llmq_set_error(LLMQ_EHIP, "gpt2_create: copy of the small tensors failed");
             goto fail;
         }
-        GO(llmq_kv_create(ctx, NL, MAXT, NH, HS, &m->kv));
+        // run_with[W, E, QuantKV[8] or IntAttnKV] (gpt2t.mojo:1238-1257)
+        if (attention == LLMQ_ATTN_INT)
+            GO(llmq_ikv_create(ctx, NL, MAXT, NH, HS, &m->kv));
+        else
+            GO(llmq_kv_create(ctx, NL, MAXT, NH, HS, &m->kv));
         ALLOC(m->x, sizeof(float) * MAXT * C);
         ALLOC(m->qkv, sizeof(float) * MAXT * 3 * C);
         ALLOC(m->att, sizeof(float) * MAXT * C);

@@ -54,6 +54,7 @@ __global__ __launch_bounds__(64) void kv_store_kernel(const float *__restrict__ 
 // head's new key and value (QuantKV.store, kvcache.mojo:333-342), writes them
 // to the cache, and uses them from LDS for the current position.
 constexpr int kAttnThreads = 256;
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 // Workgroup barrier ordering LDS only (global loads stay in flight).
 __device__ __forceinline__ void lds_barrier() {
@@ -77,8 +78,8 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
     // [max_t][HD] value codes (STAGE), 16-byte aligned for the int4 copies
     int8_t *vrow = reinterpret_cast<int8_t *>((reinterpret_cast<uintptr_t>(vsc + max_t) + 15) & ~(uintptr_t)15);
     __shared__ float red[kAttnThreads];
-    __shared__ __align__(16) int8_t knew[HD];
-    __shared__ float kscale_new;
+    __shared__ __align__(16) int8_t knew[HD], vnew[HD];
+    __shared__ float kscale_new, vscale_new;
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int npos = (pos_dev ? *pos_dev : pos0) + t + 1;
     const int cur = npos - 1;
@@ -87,12 +88,12 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
 
     // The rows of this thread's first position, requested before anything
     // else (positions past the end re-read the last one and are not used).
-    int4 kr[NV], vr[NV];
+    v4i kr[NV], vr[NV];  // native vectors: HIP's int4 struct copies kept vr in scratch
     float ksr, vsr;
     auto load_row = [&](int s) {
         const int64_t sl = base + (int64_t)s * n_head;
-        const int4 *kp = reinterpret_cast<const int4 *>(K8 + sl * HD);
-        const int4 *vp = reinterpret_cast<const int4 *>(V8 + sl * HD);
+        const v4i *kp = reinterpret_cast<const v4i *>(K8 + sl * HD);
+        const v4i *vp = reinterpret_cast<const v4i *>(V8 + sl * HD);
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             kr[i] = kp[i];
@@ -126,10 +127,14 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
             const int i = lane + 64 * e;
             const int8_t code = (int8_t)llmq_to_int(roundf(xs[e] * inv));
             (kv ? V8 : K8)[sl * HD + i] = code;
+            // LDS copies: the workgroup reads the new rows from there, not
+            // back from global memory.
             if (kv == 0)
                 knew[i] = code;
             else if (STAGE)
                 vrow[(int64_t)cur * HD + i] = code;
+            else
+                vnew[i] = code;
         }
         if (lane == 0) {
             (kv ? VS : KS)[sl] = sc;
@@ -137,6 +142,8 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
                 kscale_new = sc;
             else if (STAGE)
                 vsc[cur] = sc;
+            else
+                vscale_new = sc;
         }
     }
     lds_barrier();
@@ -147,7 +154,7 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
         const bool fresh = STORE && s == cur;
         if (fresh) {
 #pragma unroll
-            for (int i = 0; i < NV; i++) kr[i] = *reinterpret_cast<const int4 *>(knew + 16 * i);
+            for (int i = 0; i < NV; i++) kr[i] = *reinterpret_cast<const v4i *>(knew + 16 * i);
             ksr = kscale_new;
         }
         float d = 0.0f;
@@ -159,7 +166,7 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
         }
         if (STAGE && !fresh) {
 #pragma unroll
-            for (int i = 0; i < NV; i++) *reinterpret_cast<int4 *>(vrow + (int64_t)s * HD + 16 * i) = vr[i];
+            for (int i = 0; i < NV; i++) *reinterpret_cast<v4i *>(vrow + (int64_t)s * HD + 16 * i) = vr[i];
             vsc[s] = vsr;
         }
         const float sc = d * ksr * scale;
@@ -190,6 +197,8 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
         const float p = scores[s] / total;
         if (STAGE) {
             acc = fmaf(p * vsc[s], (float)vrow[(int64_t)s * HD + i], acc);
+        } else if (STORE && s == cur) {
+            acc = fmaf(p * vscale_new, (float)vnew[i], acc);
         } else {
             const int64_t sl = base + (int64_t)s * n_head;
             acc = fmaf(p * VS[sl], (float)V8[sl * HD + i], acc);
@@ -513,6 +522,7 @@ int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *
     LLMQ_REQUIRE(layer >= 0 && layer < kv->n_layer, "kv_store: layer %d out of range", layer);
     LLMQ_REQUIRE(pos_dev || (pos0 >= 0 && pos0 + T <= kv->max_t), "kv_store: positions %d..%d beyond max_t %d", pos0,
                  pos0 + T - 1, kv->max_t);
+    if (kv->integer) return launch_ikv_store(ctx, kv, layer, pos0, pos_dev, qkv, T, ld);
     const int C = kv->n_head * kv->head_dim;
     hipLaunchKernelGGL(kv_store_kernel, dim3(kv->n_head, T), dim3(64), 0, ctx->stream, qkv, ld ? ld : 3 * C, C, pos0,
                        pos_dev, layer, kv->max_t, kv->n_head, kv->head_dim, kv->k, kv->v, kv->ks, kv->vs);
@@ -565,6 +575,7 @@ int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
     LLMQ_REQUIRE(layer >= 0 && layer < kv->n_layer, "kv_attend: layer %d out of range", layer);
     LLMQ_REQUIRE(pos_dev || (pos0 >= 0 && pos0 + T <= kv->max_t), "kv_attend: positions beyond max_t");
     LLMQ_REQUIRE(!store || T == 1, "kv_attend: the fused store takes one token");
+    if (kv->integer) return launch_ikv_attend(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
     if (!store && !pos_dev && T > 1 && kv->head_dim == 64) {
         // Prompt: query blocks of 16 per head, scores in LDS up to the last position
         const int C = kv->n_head * kv->head_dim;

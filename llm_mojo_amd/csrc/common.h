@@ -64,8 +64,10 @@ struct llmq_mat {
 struct llmq_kv {
     llmq_ctx *ctx = nullptr;
     int n_layer = 0, max_t = 0, n_head = 0, head_dim = 0;
+    int integer = 0;  // 0: QuantKV[8] (float scales); 1: IntAttnKV (int32 scales * 2^24)
     int8_t *k = nullptr, *v = nullptr;
-    float *ks = nullptr, *vs = nullptr;
+    float *ks = nullptr, *vs = nullptr;     // QuantKV
+    int32_t *kq = nullptr, *vq = nullptr;   // IntAttnKV
 };
 
 // Error reporting (api.hip).
@@ -182,6 +184,12 @@ int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *
 // store: also quantize and store the token's key and value (T == 1).
 int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
                      const int *pos_dev, int64_t ld, bool store);
+// The same two steps for an IntAttnKV cache (kv->integer; int_attn.hip);
+// launch_kv_store / launch_kv_attend route there by themselves.
+int launch_ikv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,
+                     int64_t ld);
+int launch_ikv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
+                      const int *pos_dev, int64_t ld, bool store);
 
 // Embedding: x[t] = E.dequant_row(token_t) + wpe[pos0 + t] (gpt2t.mojo:378-385,
 // 495-502).  With parts != nullptr the single token is first chosen as the

@@ -179,11 +179,13 @@ def debug_chunk_sums(ctx, x, w, out, chunk_sums, xq, sx):
 class QuantKV8:
     """QuantKV[8] (kvcache.mojo:248-385) on the GPU."""
 
+    _create = "llmq_kv_create"
+
     def __init__(self, ctx, n_layer, max_t, n_head, head_dim):
         self.ctx = ctx
         self.n_layer, self.max_t, self.n_head, self.head_dim = n_layer, max_t, n_head, head_dim
         h = ctypes.c_void_p()
-        check(lib().llmq_kv_create(ctx.h, n_layer, max_t, n_head, head_dim, ctypes.byref(h)))
+        check(getattr(lib(), self._create)(ctx.h, n_layer, max_t, n_head, head_dim, ctypes.byref(h)))
         self.h = h
 
     @staticmethod
@@ -219,3 +221,24 @@ class QuantKV8:
             self.free()
         except Exception:
             pass
+
+
+class IntAttnKV(QuantKV8):
+    """IntAttnKV (int_attention.mojo:62-269) on the GPU: the int8 cache with
+    int32 scales (scale * 2^24) and attention computed in integers.  store,
+    attend, nbytes and free as for QuantKV8; export returns (k, v, kq, vq)."""
+
+    _create = "llmq_ikv_create"
+
+    @staticmethod
+    def name():
+        return "int8-intattn"  # int_attention.mojo:94-96
+
+    def export(self):
+        n = self.n_layer * self.max_t * self.n_head
+        k = np.zeros(n * self.head_dim, np.int8)
+        v = np.zeros(n * self.head_dim, np.int8)
+        kq = np.zeros(n, np.int32)
+        vq = np.zeros(n, np.int32)
+        check(lib().llmq_ikv_export(self.ctx.h, self.h, hptr(k), hptr(v), hptr(kq), hptr(vq)))
+        return k, v, kq, vq

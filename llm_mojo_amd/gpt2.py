@@ -59,23 +59,31 @@ def load_safetensors(path):
     return load_file(path)
 
 
-class GPT2:
-    """Model[W = QuantMatrix[bits, group, sym, A16], E = HEAD8_A16, KV = QuantKV[8]]."""
+ATTENTION = {"float": 0, "int": 1}  # LLMQ_ATTN_FLOAT, LLMQ_ATTN_INT
 
-    def __init__(self, ctx, tensors, bits=4, group=32, sym=False):
+
+class GPT2:
+    """Model[W = QuantMatrix[bits, group, sym, A16], E = HEAD8_A16, KV], with
+    KV = QuantKV[8] for attention="float" and IntAttnKV for "int" (gpt2t.mojo's
+    --attention, 1251-1257)."""
+
+    def __init__(self, ctx, tensors, bits=4, group=32, sym=False, attention="float"):
+        if attention not in ATTENTION:
+            raise ValueError(f"unknown --attention {attention} (float or int)")
         self.ctx = ctx
         params = params_list(tensors)
         arr = (ctypes.c_void_p * len(params))(*[p.ctypes.data for p in params])
         h = ctypes.c_void_p()
-        check(lib().llmq_gpt2_create(ctx.h, arr, bits, group, 1 if sym else 0, ctypes.byref(h)))
+        check(lib().llmq_gpt2_create_ex(ctx.h, arr, bits, group, 1 if sym else 0, ATTENTION[attention],
+                                        ctypes.byref(h)))
         self.h = h
-        self.bits, self.group, self.sym = bits, group, sym
+        self.bits, self.group, self.sym, self.attention = bits, group, sym, attention
 
     def name(self):
         """model_name (gpt2t.mojo:1222-1228)."""
         g = "ch" if self.group == 0 else f"g{self.group}"
         w = f"int{self.bits}-{g}" + ("-sym" if self.sym else "") + "-a16"
-        return w + "+head-int8-ch-a16+kv-int8"
+        return w + "+head-int8-ch-a16+kv-" + ("int8-intattn" if self.attention == "int" else "int8")
 
     def weight_bytes(self):
         return lib().llmq_gpt2_weight_bytes(self.h)

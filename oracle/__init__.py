@@ -105,11 +105,19 @@ def _declare(L):
         "orc_kv_store": (None, [P, I32, I32, P, P]),
         "orc_kv_attend_one": (None, [P, P, P, I32, I32, I32, I32]),
         "orc_kv_attend": (None, [P, P, P, I32, I32, I32]),
+        "orc_exp_multiplier": (I64, [ctypes.c_double]),
+        "orc_exp2_neg": (I64, [I64, I64]),
+        "orc_masked_exp": (I64, [P, P, I32, I32, I64, P]),
+        "orc_masked_softmax": (None, [P, P, I32, I32, I64, P]),
+        "orc_ikv_store": (None, [P, I32, I32, P, P]),
+        "orc_ikv_attend_one": (None, [P, P, P, I32, I32, I32, I32]),
+        "orc_ikv_attend": (None, [P, P, P, I32, I32, I32]),
         "orc_rng_init": (None, [P, I64]),
         "orc_rng_uniform": (ctypes.c_float, [P]),
         "orc_argmax": (I64, [P, I64]),
         "orc_gpt2_new": (P, [P, I32, I32, I32]),
         "orc_gpt2_free": (None, [P]),
+        "orc_gpt2_set_attention": (None, [P, I32]),
         "orc_gpt2_mat": (P, [P, I32]),
         "orc_gpt2_kv": (P, [P]),
         "orc_gpt2_act": (P, [P, I32]),
@@ -360,6 +368,70 @@ class QuantKV8:
         return out
 
 
+MASKED = -(1 << 31)  # intmath.mojo:35
+
+
+def exp_multiplier(scale):
+    """intmath.exp_multiplier (intmath.mojo:48-50)."""
+    return lib().orc_exp_multiplier(float(scale))
+
+
+def exp2_neg(d, mult):
+    """intmath.exp2_neg (intmath.mojo:53-65) for one score difference."""
+    return lib().orc_exp2_neg(int(d), int(mult))
+
+
+def _padded_i32(x, n):
+    nr = (n + 15) // 16 * 16
+    buf = np.zeros(max(nr, 16), np.int32)
+    buf[:len(x)] = x
+    return buf
+
+
+def masked_exp(x, n, mult, mask=None):
+    """intmath.masked_exp (intmath.mojo:93-123): (e [nr] in Q30, int64 total)."""
+    xb = _padded_i32(np.asarray(x, np.int32), n)
+    mb = _padded_i32(np.asarray(mask, np.int32), n) if mask is not None else None
+    e = np.zeros_like(xb)
+    t = lib().orc_masked_exp(ptr(xb), ptr(mb), 1 if mask is not None else 0, n, int(mult), ptr(e))
+    return e[:(n + 15) // 16 * 16], t
+
+
+def masked_softmax(x, n, mult, mask=None):
+    """intmath.masked_softmax (intmath.mojo:126-140): Q15 uint16 [nr]."""
+    xb = _padded_i32(np.asarray(x, np.int32), n)
+    mb = _padded_i32(np.asarray(mask, np.int32), n) if mask is not None else None
+    p = np.zeros(len(xb), np.uint16)
+    lib().orc_masked_softmax(ptr(xb), ptr(mb), 1 if mask is not None else 0, n, int(mult), ptr(p))
+    return p[:(n + 15) // 16 * 16]
+
+
+class IntAttnKV:
+    """IntAttnKV (int_attention.mojo:62-269) on the CPU: int8 keys and values
+    [layer, pos, head, head_dim], scales * 2^24 as int32 [layer, pos, head]."""
+
+    def __init__(self, n_layer, max_t, n_head, head_dim):
+        n = n_layer * max_t * n_head * head_dim
+        ns = n_layer * max_t * n_head
+        self.k = np.zeros(n, np.int8)
+        self.v = np.zeros(n, np.int8)
+        self.kq = np.zeros(ns, np.int32)
+        self.vq = np.zeros(ns, np.int32)
+        self.s = KV(n_layer, max_t, n_head, head_dim, self.k.ctypes.data, self.v.ctypes.data,
+                    self.kq.ctypes.data, self.vq.ctypes.data)
+        self.C = n_head * head_dim
+
+    def store(self, layer, pos, k, v):
+        lib().orc_ikv_store(ctypes.byref(self.s), layer, pos, ptr(np.ascontiguousarray(k, np.float32)),
+                            ptr(np.ascontiguousarray(v, np.float32)))
+
+    def attend(self, qkv, layer, T, pos0):
+        qkv = np.ascontiguousarray(qkv, np.float32)
+        out = np.zeros((T, self.C), np.float32)
+        lib().orc_ikv_attend(ctypes.byref(self.s), ptr(out), ptr(qkv), layer, T, pos0)
+        return out
+
+
 class Rng:
     """gpt2t.mojo's Rng (777-789)."""
 
@@ -381,13 +453,16 @@ def argmax(logits):
 
 class GPT2:
     """The reference GPT-2 (gpt2t.mojo Model, int4-g32-a16 layers by default,
-    HEAD8_A16 head, QuantKV[8]) on the CPU."""
+    HEAD8_A16 head, QuantKV[8], or IntAttnKV with attention="int") on the
+    CPU."""
 
-    def __init__(self, params, bits=4, group=32, sym=False):
+    def __init__(self, params, bits=4, group=32, sym=False, attention="float"):
         self._keep = [np.ascontiguousarray(p, np.float32) for p in params]
         arr = (ctypes.c_void_p * len(self._keep))(*[p.ctypes.data for p in self._keep])
         self.h = lib().orc_gpt2_new(arr, bits, group, 1 if sym else 0)
         self._keep = None  # the model copied what it keeps
+        # --attention int (gpt2t.mojo:1251-1257): IntAttnKV
+        lib().orc_gpt2_set_attention(self.h, 1 if attention == "int" else 0)
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -44,6 +44,7 @@ static int g_half_even = 0;
  * kvcache.mojo:330).  Tie rule unpinned: half away from zero by default. */
 void orc_set_round_half_even(int on) { g_half_even = on; }
 static inline float orc_round(float v) { return g_half_even ? nearbyintf(v) : roundf(v); }
+static inline double orc_round_d(double v) { return g_half_even ? nearbyint(v) : round(v); }
 
 /* Int(float) for a value already rounded to an integer.  NaN (a scale that
  * rounded to zero in float16: outside the reference's defined inputs) maps
@@ -933,6 +934,184 @@ void orc_kv_attend(const orc_kv *kv, float *out, const float *qkv, int layer, in
 }
 
 /* ------------------------------------------------------------------------ */
+/* Integer attention: intmath.mojo (masked softmax in fixed point) and      */
+/* int_attention.mojo (IntAttnKV).  The cache uses QuantKV's natural layout  */
+/* [layer, pos, head, head_dim]; the reference's VNNI blocking changes no    */
+/* arithmetic.                                                               */
+/* ------------------------------------------------------------------------ */
+
+#define IM_FB 16                       /* intmath.mojo:33 */
+#define IM_MB 24                       /* :34 */
+#define IM_MASKED INT32_MIN            /* :35 */
+#define IM_D_CAP ((int64_t)1 << 31)    /* :37 */
+#define IA_KS 24                       /* int_attention.mojo:62 */
+#define IA_SF 16                       /* :63 */
+
+/* exp_multiplier (intmath.mojo:50-52) */
+int64_t orc_exp_multiplier(double scale) {
+    return (int64_t)(scale * 1.4426950408889634 * (double)((int64_t)1 << (IM_FB + IM_MB)) + 0.5);
+}
+
+/* exp2_neg (intmath.mojo:55-67) for one lane: 2^(-d scale log2 e) in Q30. */
+int64_t orc_exp2_neg(int64_t d, int64_t mult) {
+    const int64_t C0 = 1073741824, C1 = -742598100, C2 = 248207216, C3 = -42480028; /* :42-45 */
+    int64_t y = ((d < IM_D_CAP ? d : IM_D_CAP) * mult) >> IM_MB;
+    int64_t q = y >> IM_FB;
+    int64_t r = y & (((int64_t)1 << IM_FB) - 1);
+    int64_t p = C3;
+    p = ((p * r) >> IM_FB) + C2;
+    p = ((p * r) >> IM_FB) + C1;
+    p = ((p * r) >> IM_FB) + C0;
+    return q >= 31 ? 0 : p >> (q < 63 ? q : 63);
+}
+
+/* masked_exp (intmath.mojo:96-123): e_i in Q30 for i < n (0 when masked or
+ * i >= n, up to n rounded to 16), returns the int64 sum. */
+int64_t orc_masked_exp(const int32_t *x, const int32_t *mask, int has_mask, int n, int64_t mult, int32_t *e) {
+    int nr = (n + 15) / 16 * 16;
+    int64_t m = INT64_MIN;
+    for (int i = 0; i < n; i++) {
+        if (has_mask && mask[i] == IM_MASKED) continue;
+        int64_t v = (int64_t)x[i] + (has_mask ? (int64_t)mask[i] : 0);
+        m = v > m ? v : m;
+    }
+    int64_t total = 0;
+    for (int i = 0; i < nr; i++) {
+        int64_t ev = 0;
+        if (i < n && !(has_mask && mask[i] == IM_MASKED)) {
+            int64_t v = (int64_t)x[i] + (has_mask ? (int64_t)mask[i] : 0);
+            ev = orc_exp2_neg(m - v, mult);
+        }
+        if (e) e[i] = (int32_t)ev;
+        total += ev;
+    }
+    return total;
+}
+
+/* masked_softmax (intmath.mojo:126-140): Q15 probabilities. */
+void orc_masked_softmax(const int32_t *x, const int32_t *mask, int has_mask, int n, int64_t mult, uint16_t *probs) {
+    int nr = (n + 15) / 16 * 16;
+    int32_t *e = (int32_t *)malloc(sizeof(int32_t) * (size_t)nr);
+    int64_t t = orc_masked_exp(x, mask, has_mask, n, mult, e);
+    int64_t inv = t > 0 ? ((int64_t)1 << 61) / t : 0;
+    for (int i = 0; i < nr; i++) probs[i] = (uint16_t)(((int64_t)e[i] * inv + ((int64_t)1 << 45)) >> 46);
+    free(e);
+}
+
+typedef struct {
+    int32_t n_layer, max_t, n_head, head_dim;
+    int8_t *k, *v;     /* [layer, pos, head, head_dim] */
+    int32_t *kq, *vq;  /* scales * 2^24, [layer, pos, head] */
+} orc_ikv;
+
+/* IntAttnKV.quantize_head (int_attention.mojo:140-168): int8 codes, and the
+ * scale * 2^24 as an int32. */
+static int32_t ikv_quantize(const float *x, int n, int8_t *dst) {
+    float mx = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float a = fabsf(x[i]);
+        mx = a > mx ? a : mx;
+    }
+    float s = mx / 127.0f;
+    if (s == 0.0f) s = 1.0f;
+    float inv = 1.0f / s;
+    for (int i = 0; i < n; i++) dst[i] = (int8_t)orc_to_int(orc_round(x[i] * inv));
+    return (int32_t)(int64_t)orc_round_d((double)s * (double)(1 << IA_KS));
+}
+
+/* IntAttnKV.store (int_attention.mojo:132-138) */
+void orc_ikv_store(orc_ikv *kv, int layer, int pos, const float *k, const float *v) {
+    for (int h = 0; h < kv->n_head; h++) {
+        int64_t sl = ((int64_t)layer * kv->max_t + pos) * kv->n_head + h;
+        kv->kq[sl] = ikv_quantize(k + h * kv->head_dim, kv->head_dim, kv->k + sl * kv->head_dim);
+        kv->vq[sl] = ikv_quantize(v + h * kv->head_dim, kv->head_dim, kv->v + sl * kv->head_dim);
+    }
+}
+
+/* IntAttnKV.attend_one (int_attention.mojo:170-269): token t (position
+ * pos0 + t) and head h; q from qkv row t ([T, 3C]), output into row t of
+ * out ([T, C]). */
+void orc_ikv_attend_one(const orc_ikv *kv, float *out, const float *qkv, int layer, int t, int h, int pos0) {
+    const int HS = kv->head_dim, C = kv->n_head * HS;
+    const int64_t mult = orc_exp_multiplier(1.0 / (double)(1 << IA_SF));
+    const int npos = pos0 + t + 1, nr = (npos + 15) / 16 * 16;
+    const float *q = qkv + (int64_t)t * 3 * C + h * HS;
+    const int64_t base = (int64_t)layer * kv->max_t * kv->n_head + h; /* slot of position 0 */
+    const int64_t stride = kv->n_head;
+    /* 1. query -> int16 */
+    float mq = 0.0f;
+    for (int d = 0; d < HS; d++) mq = fabsf(q[d]) > mq ? fabsf(q[d]) : mq;
+    float sq = mq / 32767.0f;
+    if (sq == 0.0f) sq = 1.0f;
+    float invq = 1.0f / sq;
+    int16_t *qi = (int16_t *)malloc(sizeof(int16_t) * (size_t)HS);
+    for (int d = 0; d < HS; d++) qi[d] = (int16_t)orc_to_int(orc_round(q[d] * invq));
+    const int64_t qm = (int64_t)orc_round_d((double)sq / sqrt((double)HS) * (double)((int64_t)1 << (IA_SF + IA_KS)));
+    /* 2-3. fixed-point scores (positions past npos are masked below) */
+    int32_t *scores = (int32_t *)calloc((size_t)nr, sizeof(int32_t));
+    int32_t *e = (int32_t *)calloc((size_t)nr, sizeof(int32_t));
+    for (int s = 0; s < npos; s++) {
+        const int8_t *kp = kv->k + (base + s * stride) * HS;
+        int32_t acc = 0;
+        for (int d = 0; d < HS; d++) acc += (int32_t)qi[d] * (int32_t)kp[d];
+        int64_t t1 = ((int64_t)acc * kv->kq[base + s * stride] + ((int64_t)1 << (IA_KS - 1))) >> IA_KS;
+        int64_t sfix = (t1 * qm + ((int64_t)1 << (IA_KS - 1))) >> IA_KS;
+        scores[s] = (int32_t)sfix;
+    }
+    /* 4. unnormalized integer softmax */
+    int64_t total = orc_masked_exp(scores, NULL, 0, npos, mult, e);
+    /* 5. value scales folded into int16 weights */
+    int64_t vmax = 0;
+    for (int s = 0; s < npos; s++) vmax = kv->vq[base + s * stride] > vmax ? kv->vq[base + s * stride] : vmax;
+    float *o = out + (int64_t)t * C + h * HS;
+    if (vmax == 0 || total == 0) {
+        for (int d = 0; d < HS; d++) o[d] = 0.0f;
+    } else {
+        const int64_t inv47 = ((int64_t)1 << 47) / vmax;
+        int16_t *w = (int16_t *)calloc((size_t)nr + 2, sizeof(int16_t));
+        for (int s = 0; s < npos; s++) {
+            int64_t r16 = ((int64_t)kv->vq[base + s * stride] * inv47) >> 31;
+            int64_t ww = ((int64_t)e[s] * r16 + ((int64_t)1 << 30)) >> 31;
+            if (ww > 32767) ww = 32767;
+            w[s] = e[s] == 0 ? 0 : (int16_t)ww;
+        }
+        /* weighted sums, int32 per 128 position pairs, then float */
+        float *accf = (float *)calloc((size_t)HS, sizeof(float));
+        int32_t *accv = (int32_t *)malloc(sizeof(int32_t) * (size_t)HS);
+        const int npairs = (npos + 1) / 2;
+        for (int seg = 0; seg < npairs; seg += 128) {
+            memset(accv, 0, sizeof(int32_t) * (size_t)HS);
+            int pend = seg + 128 < npairs ? seg + 128 : npairs;
+            for (int pp = seg; pp < pend; pp++) {
+                for (int j = 0; j < 2; j++) {
+                    int s = 2 * pp + j;
+                    if (s >= npos) continue; /* weight 0 */
+                    const int8_t *vp = kv->v + (base + s * stride) * HS;
+                    for (int d = 0; d < HS; d++) accv[d] = (int32_t)((uint32_t)accv[d] + (uint32_t)((int32_t)w[s] * vp[d]));
+                }
+            }
+            for (int d = 0; d < HS; d++) accf[d] += (float)accv[d];
+        }
+        /* 6. back to float */
+        const float fs = (float)((double)vmax * (double)(1 << 15) / ((double)(1 << IA_KS) * (double)total));
+        for (int d = 0; d < HS; d++) o[d] = accf[d] * fs;
+        free(accf);
+        free(accv);
+        free(w);
+    }
+    free(qi);
+    free(scores);
+    free(e);
+}
+
+/* KVCache.attend over IntAttnKV (kvcache.mojo:62-79): every token and head. */
+void orc_ikv_attend(const orc_ikv *kv, float *out, const float *qkv, int layer, int T, int pos0) {
+#pragma omp parallel for schedule(dynamic) num_threads(g_threads) if (g_threads > 1 && T * (pos0 + T) >= 256)
+    for (int idx = 0; idx < kv->n_head * T; idx++)
+        orc_ikv_attend_one(kv, out, qkv, layer, idx / kv->n_head, idx % kv->n_head, pos0);
+}
+
+/* ------------------------------------------------------------------------ */
 /* GPT-2 (gpt2t.mojo:74-118, 198-609, 777-797)                              */
 /* ------------------------------------------------------------------------ */
 
@@ -973,6 +1152,7 @@ typedef struct {
     float *vecs[G_NL * N_VECS];
     float *wpe, *lnf_w, *lnf_b;
     orc_kv kv;
+    int integer; /* 1: IntAttnKV over the same storage (int32 scales in ks / vs) */
     float *x, *xn, *qkv, *att, *fc, *logits;
 } orc_gpt2;
 
@@ -1067,6 +1247,16 @@ void orc_gpt2_free(orc_gpt2 *m) {
 
 const orc_qm *orc_gpt2_mat(const orc_gpt2 *m, int i) { return i < 0 ? &m->wte : &m->mats[i]; }
 const orc_kv *orc_gpt2_kv(const orc_gpt2 *m) { return &m->kv; }
+
+/* --attention int (gpt2t.mojo:1251-1257): IntAttnKV instead of QuantKV[8].
+ * The cache must be empty (set before the first forward). */
+void orc_gpt2_set_attention(orc_gpt2 *m, int integer) { m->integer = integer; }
+
+static orc_ikv gpt2_ikv(const orc_gpt2 *m) {
+    orc_ikv k = {m->kv.n_layer, m->kv.max_t, m->kv.n_head, m->kv.head_dim,
+                 m->kv.k,       m->kv.v,     (int32_t *)m->kv.ks, (int32_t *)m->kv.vs};
+    return k;
+}
 float *orc_gpt2_act(orc_gpt2 *m, int which) {
     switch (which) {
     case 0: return m->x;
@@ -1092,11 +1282,20 @@ static void gpt2_blocks(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
         float **v = &m->vecs[l * N_VECS];
         orc_layernorm(m->xn, m->x, v[LN1_W], v[LN1_B], T, C);
         orc_matmul_rows_a16(m->qkv, m->xn, &w[0], v[QKV_B], T, C, 3 * C, EPI_BIAS);
-        for (int t = 0; t < T; t++) {
-            const float *row = m->qkv + (int64_t)t * 3 * C;
-            orc_kv_store(&m->kv, l, pos0 + t, row + C, row + 2 * C);
+        if (m->integer) {
+            orc_ikv ik = gpt2_ikv(m);
+            for (int t = 0; t < T; t++) {
+                const float *row = m->qkv + (int64_t)t * 3 * C;
+                orc_ikv_store(&ik, l, pos0 + t, row + C, row + 2 * C);
+            }
+            orc_ikv_attend(&ik, m->att, m->qkv, l, T, pos0);
+        } else {
+            for (int t = 0; t < T; t++) {
+                const float *row = m->qkv + (int64_t)t * 3 * C;
+                orc_kv_store(&m->kv, l, pos0 + t, row + C, row + 2 * C);
+            }
+            orc_kv_attend(&m->kv, m->att, m->qkv, l, T, pos0);
         }
-        orc_kv_attend(&m->kv, m->att, m->qkv, l, T, pos0);
         orc_matmul_rows_a16(m->x, m->att, &w[1], v[PROJ_B], T, C, C, EPI_BIAS | EPI_RESID);
         orc_layernorm(m->xn, m->x, v[LN2_W], v[LN2_B], T, C);
         orc_matmul_rows_a16(m->fc, m->xn, &w[2], v[FC_B], T, C, 4 * C, EPI_BIAS | EPI_GELU);

@@ -141,8 +141,9 @@ def prefill(torch, lm, synth, ctx, tensors, model4, reps=5):
     int8-g32 A16 form (tok/s = T / prefill span, gpt2t.mojo:949-967), and the
     four layer GEMMs alone at M = 476: time, algorithmic int16 x intN ops
     (2 M K N) and executed int8 MFMA ops (the hi / lo activation planes, and
-    for int8 weights their two nibbles: 2 or 4 int8 products per MAC, M and
-    N padded to the 64 x 64 workgroup tile) against the 5 POP/s peak."""
+    for int8 weights their two nibbles: 2 or 4 int8 products per MAC, M
+    padded to the 16-token and N to the 64-column workgroup tile) against the
+    5 POP/s peak."""
     prompt = synth.prompt_ids(1337, PREFILL_T)
     res = {}
     for bits in (4, 8):
@@ -180,13 +181,34 @@ def prefill(torch, lm, synth, ctx, tensors, model4, reps=5):
                 w.free()
                 tot_us += us
                 alg += 2 * PREFILL_T * K * N
-                exe += 2 * (-(-PREFILL_T // 64) * 64) * (-(-N // 64) * 64) * K * (2 if bits == 4 else 4)
+                exe += 2 * (-(-PREFILL_T // 16) * 16) * (-(-N // 64) * 64) * K * (2 if bits == 4 else 4)
                 gemm[f"int{bits}_{name}_us"] = round(us, 2)
             gemm[f"int{bits}_layer_us"] = round(tot_us, 2)
             gemm[f"int{bits}_alg_tops"] = round(alg / tot_us / 1e6, 1)
             gemm[f"int{bits}_mfma_util"] = round(exe / (tot_us * 1e-6) / INT8_MFMA_PEAK, 4)
     ctx.set_stream(None)
     res["layer_gemms_m476"] = gemm
+    return res
+
+
+def int_attention(lm, synth, ctx, tensors, model, steps):
+    """--attention int (IntAttnKV, gpt2t.mojo:1251-1257): decode tok/s of
+    config 0's generation with integer attention beside float attention, after
+    the 12-token prompt and after a 476-token one (where attention reads
+    ~500 cached positions per layer and head)."""
+    mi = lm.GPT2(ctx, tensors, attention="int")
+    res = {}
+    for name, plen in (("prompt12", PROMPT), ("prompt476", PREFILL_T)):
+        prompt = synth.prompt_ids(SEED, plen)
+        for tag, m in (("float", model), ("int", mi)):
+            m.generate(prompt, GEN)  # warm-up (captures the decode graph)
+            n, dms = 0, 0.0
+            for _ in range(steps):
+                toks, _, d = m.generate(prompt, GEN)
+                n += len(toks)
+                dms += d
+            res[f"{tag}_{name}_decode_tok_s"] = round(n / (dms / 1000.0), 1)
+    mi.free()
     return res
 
 
@@ -302,6 +324,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 476-token prefill (config 3)")
     ap.add_argument("--no-llama", action="store_true", help="skip the TinyLlama-shaped decoder (config 4)")
     ap.add_argument("--gguf-sweep", action="store_true", help="add the GGUF GEMV sweep (config 2, ~1 min)")
+    ap.add_argument("--no-intattn", action="store_true", help="skip the integer-attention decode comparison")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline GEMV and the reference copy (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -362,6 +385,10 @@ def main():
 
     log("gemv micro")
     extra["gemv_micro_llc"] = gemv_micro(torch, lm, ctx)
+    if not args.no_intattn:
+        log("integer attention decode")
+        extra["gpt2_int_attention"] = int_attention(lm, synth, ctx, tensors, model, args.steps)
+        log(extra["gpt2_int_attention"])
     if not args.no_prefill:
         log("prefill 476")
         extra["prefill_476"] = prefill(torch, lm, synth, ctx, tensors, model)

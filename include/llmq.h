@@ -116,6 +116,13 @@ LLMQ_API int llmq_mat_shape(const llmq_mat *mat, int64_t *rows, int64_t *cols);
 LLMQ_API int llmq_mat_export(llmq_ctx *ctx, const llmq_mat *mat, uint8_t *codes, uint16_t *scales, uint8_t *zps);
 /* WeightMatrix.dequant_row (tensor.mojo:94-96): row `row` as float32 into a
  * host buffer of cols floats. */
+/* QuantMatrix.restore (tensor.mojo:646-656): a matrix from its codes in the
+ * reference's own layout (BLOCKED for int4-g32-a16, tensor.mojo:385-404;
+ * rows x cols * bits / 8 bytes), float16 scales and uint8 zero points
+ * (rows x cols / group each), as llmq_mat_export writes them; group 0 is
+ * one group per row. */
+LLMQ_API int llmq_mat_restore(llmq_ctx *ctx, int bits, int group, int sym, int a16, int64_t rows, int64_t cols,
+                              const uint8_t *codes, const uint16_t *scales, const uint8_t *zps, llmq_mat **out);
 LLMQ_API int llmq_mat_dequant_row(llmq_ctx *ctx, const llmq_mat *mat, int64_t row, float *dst);
 
 /* --------------------------------------------------------- compute (device) */
@@ -222,6 +229,17 @@ LLMQ_API int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_promp
                                 int *n_out, double *prefill_ms, double *decode_ms);
 /* Device pointer to the model's logits [V] (after forward / generate). */
 LLMQ_API int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr);
+
+/* Saved models (--save / --weights, gpt2t.mojo:612-698), in serialize.mojo's
+ * encoding and byte for byte the reference's file: save_model (630-650),
+ * load_saved (668-698) with the cache chosen as in llmq_gpt2_create_ex, and
+ * saved_formats (661-666), which copies the layer and head format names
+ * (e.g. "int4-g32-a16", "int8-ch-a16") into buffers of cap bytes.  The
+ * device model loads QuantMatrix A16 layers (int4 / int8) with the
+ * HEAD8_A16 head; other formats return LLMQ_EUNSUPPORTED. */
+LLMQ_API int llmq_gpt2_save(llmq_gpt2 *m, const char *path);
+LLMQ_API int llmq_gpt2_load(llmq_ctx *ctx, const char *path, int attention, llmq_gpt2 **out);
+LLMQ_API int llmq_saved_formats(const char *path, char *layers, char *head, int cap);
 
 /* ---------------------------------------------------------------- config 4
  * A TinyLlama-shaped decoder over GGUF weights (the benchmark's fifth

@@ -61,6 +61,10 @@ SIGNATURES = {
     "llmq_ikv_export": (I32, [P, P, P, P, P, P]),
     "llmq_gpt2_create": (I32, [P, P, I32, I32, I32, PP]),
     "llmq_gpt2_create_ex": (I32, [P, P, I32, I32, I32, I32, PP]),
+    "llmq_gpt2_save": (I32, [P, ctypes.c_char_p]),
+    "llmq_gpt2_load": (I32, [P, ctypes.c_char_p, I32, PP]),
+    "llmq_saved_formats": (I32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, I32]),
+    "llmq_mat_restore": (I32, [P, I32, I32, I32, I32, I64, I64, P, P, P, PP]),
     "llmq_gpt2_free": (I32, [P]),
     "llmq_gpt2_weight_bytes": (I64, [P]),
     "llmq_gpt2_forward": (I32, [P, P, I32, I32, P]),

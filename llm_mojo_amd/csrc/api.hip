@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "common.h"
+#include "gpt2.h"
 
 static thread_local char g_err[512];
 
@@ -283,6 +284,54 @@ int llmq_mat_export(llmq_ctx *ctx, const llmq_mat *m, uint8_t *codes, uint16_t *
     return LLMQ_OK;
 }
 
+int llmq_mat_restore(llmq_ctx *ctx, int bits, int group, int sym, int a16, int64_t rows, int64_t cols,
+                     const uint8_t *codes, const uint16_t *scales, const uint8_t *zps, llmq_mat **out) {
+    LLMQ_REQUIRE(ctx && codes && scales && zps && out, "restore: bad arguments");
+    llmq_mat *m = nullptr;
+    RC(mat_alloc_quant(ctx, bits, group, sym, a16, rows, cols, &m));
+    // The inverse of llmq_mat_export: reference layout -> row tiles.
+    const size_t cb = (size_t)m->ntiles * m->CK * 256, gb = (size_t)m->ntiles * m->NG * LLMQ_TILE_ROWS;
+    std::vector<uint8_t> c(cb, 0), z(gb, 0);
+    std::vector<uint16_t> sc(gb, 0);
+    const bool blocked = m->a16 && m->bits == 4 && m->group_param == 32;  // tensor.mojo:296
+    const int wpc = m->bits == 4 ? 32 : 16;
+    const int64_t row_bytes = m->k * m->bits / 8;
+    for (int64_t o = 0; o < m->n; o++) {
+        const int64_t tile = o / LLMQ_TILE_ROWS, r = o % LLMQ_TILE_ROWS;
+        for (int64_t g = 0; g < m->NG; g++) {
+            const size_t gi = (size_t)(tile * m->NG + g) * LLMQ_TILE_ROWS + r;
+            sc[gi] = scales[o * m->NG + g];
+            z[gi] = zps[o * m->NG + g];
+        }
+        const uint8_t *src = codes + o * row_bytes;
+        for (int64_t kk = 0; kk < m->k; kk++) {
+            const int64_t ch = kk / wpc, e = kk % wpc;
+            uint8_t *chunk = c.data() + ((tile * m->CK + ch) * LLMQ_TILE_ROWS + r) * 16;
+            if (m->bits == 8) {
+                chunk[e] = src[kk];
+            } else {
+                int64_t b;
+                int hi;
+                ref_nibble_at(blocked, kk, &b, &hi);
+                const int u = (src[b] >> (hi ? 4 : 0)) & 15;
+                chunk[e >> 1] |= (uint8_t)(u << (4 * (e & 1)));
+            }
+        }
+    }
+    int rc = LLMQ_OK;
+    if (hipMemcpyAsync(m->codes, c.data(), cb, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipMemcpyAsync(m->scales, sc.data(), gb * 2, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipMemcpyAsync(m->zps, z.data(), gb, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess)
+        rc = llmq_set_error(LLMQ_EHIP, "restore: copy to the device failed");
+    if (rc != LLMQ_OK) {
+        llmq_mat_free(m);
+        return rc;
+    }
+    *out = m;
+    return LLMQ_OK;
+}
+
 int llmq_mat_dequant_row(llmq_ctx *ctx, const llmq_mat *m, int64_t row, float *dst) {
     LLMQ_REQUIRE(ctx && m && dst, "dequant_row: bad arguments");
     LLMQ_REQUIRE(row >= 0 && row < m->n, "dequant_row: row %lld out of range", (long long)row);
@@ -526,32 +575,6 @@ int llmq_ikv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, int3
 
 // ------------------------------------------------------------------- GPT-2
 
-namespace {
-constexpr int NL = 12, NH = 12, C = 768, HS = 64, MAXT = 1024, V = 50257, EOT = 50256;
-enum { LN1_W, LN1_B, QKV_B, PROJ_B, LN2_W, LN2_B, FC_B, FCPROJ_B, N_VECS };
-constexpr int VEC_LEN[N_VECS] = {C, C, 3 * C, C, C, C, 4 * C, C};
-constexpr int VEC_PARAM[N_VECS] = {0, 1, 3, 5, 6, 7, 9, 11};  // index within a layer's 12 params
-constexpr int64_t SMALL_FLOATS = (int64_t)NL * 13 * C + (int64_t)MAXT * C + 2 * C;  // gpt2t.mojo:576
-}  // namespace
-
-
-struct llmq_gpt2 {
-    llmq_ctx *ctx = nullptr;
-    llmq_mat *wte = nullptr;
-    llmq_mat *mats[NL * 4] = {};
-    float *small = nullptr;
-    const float *vec[NL][N_VECS] = {};
-    const float *wpe = nullptr, *lnf_w = nullptr, *lnf_b = nullptr;
-    llmq_kv *kv = nullptr;
-    float *x = nullptr, *qkv = nullptr, *att = nullptr, *fc = nullptr, *logits = nullptr;
-    ArgmaxPart *parts = nullptr;
-    int nparts = 0;
-    int64_t *tokens = nullptr, *gen = nullptr;
-    int *state = nullptr;  // {pos, step} of the device-driven decode loop
-    hipGraphExec_t step_graph = nullptr;
-    hipGraph_t step_graph_def = nullptr;
-};
-
 // Model.blocks (gpt2t.mojo:485-571) for T tokens: tokens in m->tokens when
 // state == nullptr, else one token picked on the device from the previous
 // head's argmax partials (decode), with the position in state[0].
@@ -618,6 +641,46 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step) {
     return launch_gemv_a16(ctx, h);
 }
 
+// The model's small tensors (host, SMALL_FLOATS in Model.small's order),
+// its KV cache and activation buffers; the matrices are already in place.
+int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host) {
+    llmq_ctx *ctx = m->ctx;
+    auto alloc = [&](auto *&ptr, size_t bytes) -> int {
+        if (hipMalloc(&ptr, bytes) != hipSuccess)
+            return llmq_set_error(LLMQ_ENOMEM, "gpt2: allocation of %zu bytes", bytes);
+        return LLMQ_OK;
+    };
+    RC(alloc(m->small, sizeof(float) * SMALL_FLOATS));
+    int64_t off = 0;
+    for (int l = 0; l < NL; l++)
+        for (int s = 0; s < N_VECS; s++) {
+            m->vec[l][s] = m->small + off;
+            off += VEC_LEN[s];
+        }
+    m->wpe = m->small + off;
+    off += (int64_t)MAXT * C;
+    m->lnf_w = m->small + off;
+    m->lnf_b = m->small + off + C;
+    LLMQ_HIP(hipMemcpy(m->small, small_host, sizeof(float) * SMALL_FLOATS, hipMemcpyHostToDevice));
+    // run_with[W, E, QuantKV[8] or IntAttnKV] (gpt2t.mojo:1238-1257)
+    if (attention == LLMQ_ATTN_INT)
+        RC(llmq_ikv_create(ctx, NL, MAXT, NH, HS, &m->kv));
+    else
+        RC(llmq_kv_create(ctx, NL, MAXT, NH, HS, &m->kv));
+    RC(alloc(m->x, sizeof(float) * MAXT * C));
+    RC(alloc(m->qkv, sizeof(float) * MAXT * 3 * C));
+    RC(alloc(m->att, sizeof(float) * MAXT * C));
+    RC(alloc(m->fc, sizeof(float) * MAXT * 4 * C));
+    RC(alloc(m->logits, sizeof(float) * V));
+    m->nparts = gemv_a16_num_parts(m->wte, true);
+    RC(alloc(m->parts, sizeof(ArgmaxPart) * m->nparts));
+    RC(alloc(m->tokens, sizeof(int64_t) * MAXT));
+    RC(alloc(m->gen, sizeof(int64_t) * MAXT));
+    RC(alloc(m->state, sizeof(int) * 4));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    return LLMQ_OK;
+}
+
 extern "C" {
 
 int llmq_gpt2_free(llmq_gpt2 *m) {
@@ -658,13 +721,6 @@ int llmq_gpt2_create_ex(llmq_ctx *ctx, const float *const *params, int bits, int
         rc = (call);               \
         if (rc != LLMQ_OK) goto fail; \
     } while (0)
-#define ALLOC(ptr, bytes)                                                                      \
-    do {                                                                                       \
-        if (hipMalloc(&(ptr), (bytes)) != hipSuccess) {                                        \
-            rc = llmq_set_error(LLMQ_ENOMEM, "gpt2_create: allocation of %zu bytes", (size_t)(bytes)); \
-            goto fail;                                                                         \
-        }                                                                                      \
-    } while (0)
     {
         // E = HEAD8_A16 = QuantMatrix[8, 0, False, True] (gpt2t.mojo:1234).
         GO(llmq_mat_from_f32(ctx, 8, 0, 0, 1, params[0], V, C, 0, &m->wte));
@@ -674,46 +730,19 @@ int llmq_gpt2_create_ex(llmq_ctx *ctx, const float *const *params, int bits, int
             for (int j = 0; j < 4; j++)
                 GO(llmq_mat_from_f32(ctx, bits, group, sym, 1, params[4 + 12 * l + mat_param[j]], rows[j], cols[j], 1,
                                      &m->mats[l * 4 + j]));
-        ALLOC(m->small, sizeof(float) * SMALL_FLOATS);
         std::vector<float> host((size_t)SMALL_FLOATS);
         int64_t off = 0;
         for (int l = 0; l < NL; l++)
             for (int s = 0; s < N_VECS; s++) {
                 memcpy(host.data() + off, params[4 + 12 * l + VEC_PARAM[s]], sizeof(float) * VEC_LEN[s]);
-                m->vec[l][s] = m->small + off;
                 off += VEC_LEN[s];
             }
         memcpy(host.data() + off, params[1], sizeof(float) * MAXT * C);
-        m->wpe = m->small + off;
         off += (int64_t)MAXT * C;
         memcpy(host.data() + off, params[2], sizeof(float) * C);
-        m->lnf_w = m->small + off;
         off += C;
         memcpy(host.data() + off, params[3], sizeof(float) * C);
-        m->lnf_b = m->small + off;
-        if (hipMemcpy(m->small, host.data(), sizeof(float) * SMALL_FLOATS, hipMemcpyHostToDevice) != hipSuccess) {
-            rc = llmq_set_error(LLMQ_EHIP, "gpt2_create: copy of the small tensors failed");
-            goto fail;
-        }
-        // run_with[W, E, QuantKV[8] or IntAttnKV] (gpt2t.mojo:1238-1257)
-        if (attention == LLMQ_ATTN_INT)
-            GO(llmq_ikv_create(ctx, NL, MAXT, NH, HS, &m->kv));
-        else
-            GO(llmq_kv_create(ctx, NL, MAXT, NH, HS, &m->kv));
-        ALLOC(m->x, sizeof(float) * MAXT * C);
-        ALLOC(m->qkv, sizeof(float) * MAXT * 3 * C);
-        ALLOC(m->att, sizeof(float) * MAXT * C);
-        ALLOC(m->fc, sizeof(float) * MAXT * 4 * C);
-        ALLOC(m->logits, sizeof(float) * V);
-        m->nparts = gemv_a16_num_parts(m->wte, true);
-        ALLOC(m->parts, sizeof(ArgmaxPart) * m->nparts);
-        ALLOC(m->tokens, sizeof(int64_t) * MAXT);
-        ALLOC(m->gen, sizeof(int64_t) * MAXT);
-        ALLOC(m->state, sizeof(int) * 4);
-        if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
-            rc = llmq_set_error(LLMQ_EHIP, "gpt2_create: load failed");
-            goto fail;
-        }
+        GO(gpt2_finish(m, attention, host.data()));
     }
     *out = m;
     return LLMQ_OK;
@@ -721,7 +750,6 @@ fail:
     llmq_gpt2_free(m);
     return rc;
 #undef GO
-#undef ALLOC
 }
 
 int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m) {

@@ -1,0 +1,36 @@
+// GPT-2 124M model state shared by the model code (api.hip) and its saved
+// files (model_io.hip).  Shapes are gpt2t.mojo's compile-time constants
+// (74-81) and the small float tensors follow Model.small's order
+// (gpt2t.mojo:108-119, 574-576).
+#pragma once
+#include "common.h"
+
+namespace {
+constexpr int NL = 12, NH = 12, C = 768, HS = 64, MAXT = 1024, V = 50257, EOT = 50256;
+enum { LN1_W, LN1_B, QKV_B, PROJ_B, LN2_W, LN2_B, FC_B, FCPROJ_B, N_VECS };
+constexpr int VEC_LEN[N_VECS] = {C, C, 3 * C, C, C, C, 4 * C, C};
+constexpr int VEC_PARAM[N_VECS] = {0, 1, 3, 5, 6, 7, 9, 11};  // index within a layer's 12 params
+constexpr int64_t SMALL_FLOATS = (int64_t)NL * 13 * C + (int64_t)MAXT * C + 2 * C;  // gpt2t.mojo:576
+}  // namespace
+
+struct llmq_gpt2 {
+    llmq_ctx *ctx = nullptr;
+    llmq_mat *wte = nullptr;
+    llmq_mat *mats[NL * 4] = {};
+    float *small = nullptr;
+    const float *vec[NL][N_VECS] = {};
+    const float *wpe = nullptr, *lnf_w = nullptr, *lnf_b = nullptr;
+    llmq_kv *kv = nullptr;
+    float *x = nullptr, *qkv = nullptr, *att = nullptr, *fc = nullptr, *logits = nullptr;
+    ArgmaxPart *parts = nullptr;
+    int nparts = 0;
+    int64_t *tokens = nullptr, *gen = nullptr;
+    int *state = nullptr;  // {pos, step} of the device-driven decode loop
+    hipGraphExec_t step_graph = nullptr;
+    hipGraph_t step_graph_def = nullptr;
+};
+
+// Uploads the small tensors (host, SMALL_FLOATS floats in Model.small's
+// order) and allocates the cache (LLMQ_ATTN_FLOAT or LLMQ_ATTN_INT) and the
+// activations of a model whose matrices are in place (api.hip).
+int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host);

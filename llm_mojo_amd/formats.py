@@ -58,6 +58,22 @@ class HipQuantMatrix:
     def group_size(self):
         return lib().llmq_mat_group_size(self.h)
 
+    @classmethod
+    def restore(cls, ctx, bits, group, sym, a16, rows, cols, codes, scales, zps):
+        """QuantMatrix.restore (tensor.mojo:646-656): from codes in the
+        reference's own layout (BLOCKED for int4-g32-a16), float16 scale bits
+        and zero points, as export() returns them."""
+        codes = np.ascontiguousarray(codes, np.uint8)
+        scales = np.ascontiguousarray(scales, np.uint16)
+        zps = np.ascontiguousarray(zps, np.uint8)
+        g = cols if group == 0 else group
+        if codes.size != rows * cols * bits // 8 or scales.size != rows * cols // g or zps.size != scales.size:
+            raise ValueError("restore: buffer sizes do not match the shape")
+        h = ctypes.c_void_p()
+        check(lib().llmq_mat_restore(ctx.h, bits, group, 1 if sym else 0, 1 if a16 else 0, rows, cols, hptr(codes),
+                                     hptr(scales), hptr(zps), ctypes.byref(h)))
+        return cls(ctx, h, bits, group, sym, a16)
+
     def has_i16(self):
         """tensor.mojo:102-104: the A16 formats."""
         return bool(lib().llmq_mat_has_i16(self.h))

@@ -7,6 +7,7 @@ one GPU.  Greedy generation runs on the device: each step's argmax picks the
 next token without a round trip to the host.
 """
 import ctypes
+import os
 
 import numpy as np
 
@@ -62,6 +63,14 @@ def load_safetensors(path):
 ATTENTION = {"float": 0, "int": 1}  # LLMQ_ATTN_FLOAT, LLMQ_ATTN_INT
 
 
+def saved_formats(path):
+    """saved_formats (gpt2t.mojo:661-666): (layer format, head format) of a
+    saved model file."""
+    a, b = ctypes.create_string_buffer(128), ctypes.create_string_buffer(128)
+    check(lib().llmq_saved_formats(os.fsencode(path), a, b, 128))
+    return a.value.decode(), b.value.decode()
+
+
 class GPT2:
     """Model[W = QuantMatrix[bits, group, sym, A16], E = HEAD8_A16, KV], with
     KV = QuantKV[8] for attention="float" and IntAttnKV for "int" (gpt2t.mojo's
@@ -78,6 +87,28 @@ class GPT2:
                                         ctypes.byref(h)))
         self.h = h
         self.bits, self.group, self.sym, self.attention = bits, group, sym, attention
+
+    @classmethod
+    def load(cls, ctx, path, attention="float"):
+        """load_saved (gpt2t.mojo:668-698): a model from a file written by
+        save / the reference's --save."""
+        if attention not in ATTENTION:
+            raise ValueError(f"unknown --attention {attention} (float or int)")
+        h = ctypes.c_void_p()
+        check(lib().llmq_gpt2_load(ctx.h, os.fsencode(path), ATTENTION[attention], ctypes.byref(h)))
+        self = cls.__new__(cls)
+        self.ctx, self.h, self.attention = ctx, h, attention
+        layers, _ = saved_formats(path)
+        self.bits = int(layers[3])
+        g = layers.split("-")[1]
+        self.group = 0 if g == "ch" else int(g[1:])
+        self.sym = "-sym" in layers
+        return self
+
+    def save(self, path):
+        """save_model (gpt2t.mojo:630-650): the converted weights, byte for
+        byte the reference's saved-model format."""
+        check(lib().llmq_gpt2_save(self.h, os.fsencode(path)))
 
     def name(self):
         """model_name (gpt2t.mojo:1222-1228)."""

@@ -451,6 +451,99 @@ def argmax(logits):
     return lib().orc_argmax(ptr(logits), logits.size)
 
 
+# ------------------------------------------------------------ saved models
+# gpt2t.mojo:612-698 in serialize.mojo's encoding (integers 8 bytes
+# little-endian, strings a length and the bytes, raw buffers).
+
+SAVED_MAGIC = b"llm_mojo GPT-2 124M weights"  # gpt2t.mojo:621
+SAVED_VERSION = 1  # gpt2t.mojo:622
+VEC_PARAM = [0, 1, 3, 5, 6, 7, 9, 11]  # VEC_NAMES (gpt2t.mojo:108-118) within a layer's params
+
+
+def _i64(v):
+    return int(v).to_bytes(8, "little", signed=True)
+
+
+def _str(b):
+    return _i64(len(b)) + b
+
+
+def qm_name(q):
+    """QuantMatrix.name (tensor.mojo:325-331)."""
+    g = "ch" if q.perch else f"g{q.group}"
+    return f"int{q.bits}-{g}" + ("-sym" if q.sym else "") + ("-a16" if q.a16 else "")
+
+
+def qm_save_bytes(q):
+    """QuantMatrix.save (tensor.mojo:634-644): rows, cols, group, codes (in
+    the reference's own layout), float16 scales, zero points."""
+    groups = q.n * (q.k // q.group)
+    return (_i64(q.n) + _i64(q.k) + _i64(q.group) + ctypes.string_at(q.data, q.n * q.k * q.bits // 8)
+            + ctypes.string_at(q.scale, 2 * groups) + ctypes.string_at(q.zp, groups))
+
+
+def small_floats(params):
+    """Model.small (gpt2t.mojo:249-265, 574-576): per layer the VEC_NAMES
+    tensors, then wpe, ln_f.weight, ln_f.bias, as float32."""
+    parts = []
+    for l in range(12):
+        lp = params[4 + 12 * l: 16 + 12 * l]
+        parts += [np.ascontiguousarray(lp[i], np.float32).ravel() for i in VEC_PARAM]
+    parts += [np.ascontiguousarray(params[i], np.float32).ravel() for i in (1, 2, 3)]
+    return np.concatenate(parts)
+
+
+def save_model(model, params, path):
+    """save_model (gpt2t.mojo:630-650) for an oracle GPT2 built from params."""
+    wte, mats = model.mat(-1), [model.mat(i) for i in range(48)]
+    small = small_floats(params)
+    with open(path, "wb") as f:
+        f.write(_str(SAVED_MAGIC) + _i64(SAVED_VERSION) + _str(qm_name(mats[0]).encode())
+                + _str(qm_name(wte).encode()))
+        f.write(qm_save_bytes(wte))
+        for q in mats:
+            f.write(qm_save_bytes(q))
+        f.write(_i64(len(small)) + small.tobytes())
+
+
+def read_saved(path):
+    """load_saved's reading (gpt2t.mojo:653-698): formats, the 49 matrices as
+    (rows, cols, group, codes, scales, zps) and the small floats."""
+    b = open(path, "rb").read()
+    pos = 0
+
+    def i64():
+        nonlocal pos
+        v = int.from_bytes(b[pos:pos + 8], "little", signed=True)
+        pos += 8
+        return v
+
+    def raw(n):
+        nonlocal pos
+        if pos + n > len(b):
+            raise ValueError("unexpected end of " + str(path))
+        out = b[pos:pos + n]
+        pos += n
+        return out
+
+    if i64() != len(SAVED_MAGIC) or raw(len(SAVED_MAGIC)) != SAVED_MAGIC:
+        raise ValueError(f"{path} is not a saved llm_mojo model (see --save)")
+    if i64() != SAVED_VERSION:
+        raise ValueError("unsupported version")
+    layers = raw(i64()).decode()
+    head = raw(i64()).decode()
+    bits = [8] + [int(layers[3])] * 48
+    mats = []
+    for bt in bits:
+        rows, cols, group = i64(), i64(), i64()
+        groups = rows * (cols // group)
+        mats.append((rows, cols, group, np.frombuffer(raw(rows * cols * bt // 8), np.uint8),
+                     np.frombuffer(raw(2 * groups), np.uint16), np.frombuffer(raw(groups), np.uint8)))
+    n = i64()
+    small = np.frombuffer(raw(4 * n), np.float32)
+    return {"layers": layers, "head": head, "mats": mats, "small": small, "end": pos == len(b)}
+
+
 class GPT2:
     """The reference GPT-2 (gpt2t.mojo Model, int4-g32-a16 layers by default,
     HEAD8_A16 head, QuantKV[8], or IntAttnKV with attention="int") on the

@@ -95,6 +95,25 @@ LLMQ_API int llmq_mat_from_f32_device(llmq_ctx *ctx, int bits, int group, int sy
  * stored, rows of cols // block_size blocks, copied from host memory. */
 LLMQ_API int llmq_mat_from_gguf(llmq_ctx *ctx, int ggml_type, const void *blocks, int64_t rows, int64_t cols,
                                 llmq_mat **out);
+/* GGUFFile (gguf.mojo:519-636): a GGUF v2 / v3 file's tensor index over a
+ * read-only mapping of the file (every read bounds-checked).  Tensors are
+ * (name, ggml type, rows = product of dims[1..], cols = dims[0], offset in
+ * the data section, which starts at the general.alignment boundary, 32 by
+ * default).  llmq_gguf_find gives the index of a name or -1 (GGUFFile.has);
+ * llmq_gguf_tensor_data a host pointer to its bytes in the mapping;
+ * llmq_gguf_matrix is GGUFFile.matrix (gguf.mojo:622-633) on the device
+ * (llmq_mat_from_gguf: block formats; F32 / F16 tensors are read with
+ * llmq_gguf_tensor_data).  The handle must outlive the pointers it gave. */
+typedef struct llmq_gguf llmq_gguf;
+LLMQ_API int llmq_gguf_open(const char *path, llmq_gguf **out);
+LLMQ_API int llmq_gguf_close(llmq_gguf *g);
+LLMQ_API int64_t llmq_gguf_n_tensors(const llmq_gguf *g);
+LLMQ_API int llmq_gguf_find(const llmq_gguf *g, const char *name, int64_t *index);
+LLMQ_API int llmq_gguf_tensor_info(const llmq_gguf *g, int64_t index, const char **name, int *ggml_type,
+                                   int64_t *rows, int64_t *cols, int64_t *offset);
+LLMQ_API int llmq_gguf_tensor_data(const llmq_gguf *g, int64_t index, const void **data, int64_t *bytes);
+LLMQ_API int llmq_gguf_matrix(llmq_ctx *ctx, const llmq_gguf *g, const char *name, llmq_mat **out);
+
 /* WeightMatrix.free (tensor.mojo:145-147). */
 LLMQ_API int llmq_mat_free(llmq_mat *mat);
 /* WeightMatrix.nbytes (tensor.mojo:131-133; QuantMatrix 629-632,

@@ -61,6 +61,14 @@ SIGNATURES = {
     "llmq_ikv_export": (I32, [P, P, P, P, P, P]),
     "llmq_gpt2_create": (I32, [P, P, I32, I32, I32, PP]),
     "llmq_gpt2_create_ex": (I32, [P, P, I32, I32, I32, I32, PP]),
+    "llmq_gguf_open": (I32, [ctypes.c_char_p, PP]),
+    "llmq_gguf_close": (I32, [P]),
+    "llmq_gguf_n_tensors": (I64, [P]),
+    "llmq_gguf_find": (I32, [P, ctypes.c_char_p, ctypes.POINTER(I64)]),
+    "llmq_gguf_tensor_info": (I32, [P, I64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(I32),
+                                    ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(I64)]),
+    "llmq_gguf_tensor_data": (I32, [P, I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(I64)]),
+    "llmq_gguf_matrix": (I32, [P, P, ctypes.c_char_p, PP]),
     "llmq_gpt2_save": (I32, [P, ctypes.c_char_p]),
     "llmq_gpt2_load": (I32, [P, ctypes.c_char_p, I32, PP]),
     "llmq_saved_formats": (I32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, I32]),

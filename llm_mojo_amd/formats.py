@@ -7,6 +7,7 @@ driven per whole matmul (kernels.linear / head), not per row, and work on
 device buffers (torch tensors or raw addresses).
 """
 import ctypes
+import os
 
 import numpy as np
 
@@ -190,6 +191,76 @@ def layernorm(ctx, out, x, w, b):
 
 def debug_chunk_sums(ctx, x, w, out, chunk_sums, xq, sx):
     check(lib().llmq_debug_chunk_sums(ctx.h, dptr(x), w.h, dptr(out), dptr(chunk_sums), dptr(xq), dptr(sx)))
+
+
+class GGUFFile:
+    """GGUFFile (gguf.mojo:527-636): a GGUF v2 / v3 file's tensor index over
+    a read-only mapping of the file (libllmq's parser, bounds-checked)."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        check(lib().llmq_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self.h = h
+        self.path = path
+
+    def _index(self, name):
+        i = ctypes.c_int64()
+        check(lib().llmq_gguf_find(self.h, name.encode(), ctypes.byref(i)))
+        return i.value
+
+    def has(self, name):
+        """GGUFFile.has (gguf.mojo:635-636)."""
+        return self._index(name) >= 0
+
+    def names(self):
+        return [self.info_at(i)[0] for i in range(lib().llmq_gguf_n_tensors(self.h))]
+
+    def info_at(self, i):
+        nm, t = ctypes.c_char_p(), ctypes.c_int()
+        rows, cols, off = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+        check(lib().llmq_gguf_tensor_info(self.h, i, ctypes.byref(nm), ctypes.byref(t), ctypes.byref(rows),
+                                          ctypes.byref(cols), ctypes.byref(off)))
+        return nm.value.decode(), t.value, rows.value, cols.value, off.value
+
+    def info(self, name):
+        """(ggml type, rows, cols, offset) of a tensor (TensorInfo, gguf.mojo:519-524)."""
+        i = self._index(name)
+        if i < 0:
+            raise KeyError("tensor not in GGUF file: " + name)
+        return self.info_at(i)[1:]
+
+    def tensor_bytes(self, name):
+        """A copy of the tensor's bytes as stored."""
+        i = self._index(name)
+        if i < 0:
+            raise KeyError("tensor not in GGUF file: " + name)
+        p, n = ctypes.c_void_p(), ctypes.c_int64()
+        check(lib().llmq_gguf_tensor_data(self.h, i, ctypes.byref(p), ctypes.byref(n)))
+        return np.frombuffer(ctypes.string_at(p, n.value), np.uint8).copy()
+
+    def f32(self, name):
+        """An F32 tensor as float32 [rows, cols] (gguf_f32, gpt2t.mojo:721-726)."""
+        t, rows, cols, _ = self.info(name)
+        if t != 0:
+            raise ValueError(f"{name} is ggml type {t}, expected F32")
+        return self.tensor_bytes(name).view(np.float32).reshape(rows, cols)
+
+    def matrix(self, ctx, name):
+        """GGUFFile.matrix (gguf.mojo:622-633) on the device."""
+        h = ctypes.c_void_p()
+        check(lib().llmq_gguf_matrix(ctx.h, self.h, name.encode(), ctypes.byref(h)))
+        return HipGGUFMatrix(ctx, h, self.info(name)[0])
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().llmq_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class QuantKV8:

@@ -45,6 +45,33 @@ class Llama:
         check(lib().llmq_llama_create(ctx.h, ctypes.byref(self._c), ptrs, ctypes.byref(h)))
         self.h = h
 
+    @classmethod
+    def from_gguf(cls, ctx, path, cfg):
+        """The decoder from a llama.cpp GGUF file (GGUFFile, gguf.mojo:519-636):
+        tensors `<name>.weight` in tensor_names order, norms F32, matrices of
+        the cfg's types."""
+        from .formats import GGUFFile
+
+        g = GGUFFile(path)
+        shapes = tensor_shapes(cfg)
+        tensors = []
+        try:
+            for name in tensor_names(cfg["n_layer"]):
+                kind = name.rsplit(".", 1)[-1]
+                full = name + ".weight"
+                if kind.endswith("norm"):
+                    tensors.append(g.f32(full).reshape(-1))
+                    continue
+                want = cfg["head_type"] if kind == "output" else (
+                    cfg["embd_type"] if kind == "token_embd" else cfg["layer_type"])
+                t, rows, cols, _ = g.info(full)
+                if t != want or (rows, cols) != shapes[kind]:
+                    raise ValueError(f"{full}: ggml type {t} {rows}x{cols}, expected type {want} {shapes[kind]}")
+                tensors.append(g.tensor_bytes(full))
+        finally:
+            g.close()
+        return cls(ctx, cfg, tensors)
+
     def weight_bytes(self):
         return lib().llmq_llama_weight_bytes(self.h)
 

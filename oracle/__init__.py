@@ -451,6 +451,76 @@ def argmax(logits):
     return lib().orc_argmax(ptr(logits), logits.size)
 
 
+# ------------------------------------------------------------ GGUF files
+
+def gguf_index(path):
+    """GGUFFile.__init__ (gguf.mojo:535-590) restated: (data_start, {name:
+    (kind, cols, rows, offset)}), reading as the reference does (general.
+    alignment honoured, every other metadata value skipped by skip_value,
+    gguf.mojo:600-620)."""
+    import struct
+
+    b = open(path, "rb").read()
+
+    def u32(pos):
+        return struct.unpack_from("<I", b, pos)[0]
+
+    def u64(pos):
+        return struct.unpack_from("<Q", b, pos)[0]
+
+    def string_at(pos):
+        n = u64(pos)
+        return b[pos + 8:pos + 8 + n].decode("utf-8", "replace")
+
+    def skip_value(vtype, pos):
+        if vtype in (0, 1, 7):
+            return pos + 1
+        if vtype in (2, 3):
+            return pos + 2
+        if vtype in (4, 5, 6):
+            return pos + 4
+        if vtype in (10, 11, 12):
+            return pos + 8
+        if vtype == 8:
+            return pos + 8 + u64(pos)
+        if vtype == 9:
+            etype, count = u32(pos), u64(pos + 4)
+            q = pos + 12
+            for _ in range(count):
+                q = skip_value(etype, q)
+            return q
+        raise ValueError(f"unknown GGUF metadata type {vtype}")
+
+    if u32(0) != 0x46554747:
+        raise ValueError(f"{path} is not a GGUF file")
+    if u32(4) < 2:
+        raise ValueError(f"GGUF version {u32(4)} is not supported")
+    n_tensors, n_kv = u64(8), u64(16)
+    pos, alignment = 24, 32
+    for _ in range(n_kv):
+        key = string_at(pos)
+        pos += 8 + len(key.encode())
+        vtype = u32(pos)
+        pos += 4
+        if key == "general.alignment":
+            alignment = u32(pos)
+        pos = skip_value(vtype, pos)
+    tensors = {}
+    for _ in range(n_tensors):
+        name = string_at(pos)
+        pos += 8 + len(name.encode())
+        ndims = u32(pos)
+        pos += 4
+        cols = u64(pos)
+        rows = 1
+        for d in range(1, ndims):
+            rows *= u64(pos + 8 * d)
+        pos += 8 * ndims
+        tensors[name] = (u32(pos), cols, rows, u64(pos + 4))
+        pos += 12
+    return (pos + alignment - 1) // alignment * alignment, tensors
+
+
 # ------------------------------------------------------------ saved models
 # gpt2t.mojo:612-698 in serialize.mojo's encoding (integers 8 bytes
 # little-endian, strings a length and the bytes, raw buffers).

@@ -164,3 +164,47 @@ def test_gguf_matmul_several_tokens(gpu, orc, kind, rows, cols, T):
     got = out.cpu().numpy()
     want = np.stack([orc.gguf_gemv(t, blocks, rows, cols, x[i], b, orc.EPI_BIAS) for i in range(T)]) + res
     assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
+
+
+def test_gguf_file_matrices_and_llama(gpu, tmp_path):
+    """GGUFFile.matrix (gguf.mojo:622-633) gives the matrix the blocks give,
+    and a config-4 decoder read from a GGUF file computes what the same
+    tensors passed directly compute."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import llama, synth
+    from tests import gguf_write as gw
+
+    cfg = dict(n_layer=2, dim=256, n_head=4, n_kv=2, head_dim=64, ffn=512, vocab=1000, max_t=96, batch=1,
+               layer_type=12, head_type=14, embd_type=12, eps=1e-5, theta=10000.0)
+    tensors = synth.llama_tensors(cfg, 11)
+    shapes = llama.tensor_shapes(cfg)
+    entries = []
+    for name, a in zip(llama.tensor_names(cfg["n_layer"]), tensors):
+        kind = name.rsplit(".", 1)[-1]
+        if kind.endswith("norm"):
+            entries.append((name + ".weight", 0, [cfg["dim"]], gw.f32_bytes(a)))
+        else:
+            t = cfg["head_type"] if kind == "output" else (cfg["embd_type"] if kind == "token_embd" else 12)
+            rows, cols = shapes[kind]
+            entries.append((name + ".weight", t, [cols, rows], np.asarray(a, np.uint8).tobytes()))
+    path = tmp_path / "tiny.gguf"
+    gw.write(path, entries, [("general.architecture", gw.STRING, "llama")])
+    print("gguf file matrix", flush=True)
+    g = lm.GGUFFile(path)
+    m1 = g.matrix(ctx, "blk.1.ffn_down.weight")
+    m2 = lm.HipGGUFMatrix.from_blocks(ctx, 12, tensors[1 + 9 + 8], 256, 512)
+    x = torch.from_numpy(np.random.default_rng(1).normal(0, 1, (1, 512)).astype(np.float32)).cuda()
+    a = torch.zeros((1, 256), device="cuda")
+    b = torch.zeros((1, 256), device="cuda")
+    lm.linear(ctx, a, x, m1)
+    lm.linear(ctx, b, x, m2)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    g.close()
+    print("gguf file llama", flush=True)
+    toks = synth.llama_prompts(11, 1, 9, cfg["vocab"])[0]
+    f = lm.Llama.from_gguf(ctx, path, cfg)
+    d = lm.Llama(ctx, cfg, tensors)
+    assert np.array_equal(f.forward(0, toks, 0), d.forward(0, toks, 0))
+    f.free()
+    d.free()

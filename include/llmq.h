@@ -259,6 +259,13 @@ LLMQ_API int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr);
 LLMQ_API int llmq_gpt2_save(llmq_gpt2 *m, const char *path);
 LLMQ_API int llmq_gpt2_load(llmq_ctx *ctx, const char *path, int attention, llmq_gpt2 **out);
 LLMQ_API int llmq_saved_formats(const char *path, char *layers, char *head, int cap);
+/* load_gguf (gpt2t.mojo:728-760): GPT-2 124M from a llama.cpp GGUF file,
+ * its matrices used as stored (GGUF names of gpt2t.mojo:702-718; the head is
+ * output.weight, or token_embd.weight when absent; position_embd and the
+ * norms / biases F32).  Layers run the GGUF kernels on float activations,
+ * the head head_i16 for Q6_K / Q8_0; forward and generate as for
+ * llmq_gpt2_create's model (generate's greedy pick is made on the host). */
+LLMQ_API int llmq_gpt2_load_gguf(llmq_ctx *ctx, const char *path, int attention, llmq_gpt2 **out);
 
 /* ---------------------------------------------------------------- config 4
  * A TinyLlama-shaped decoder over GGUF weights (the benchmark's fifth

@@ -70,6 +70,7 @@ SIGNATURES = {
     "llmq_gguf_tensor_data": (I32, [P, I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(I64)]),
     "llmq_gguf_matrix": (I32, [P, P, ctypes.c_char_p, PP]),
     "llmq_gpt2_save": (I32, [P, ctypes.c_char_p]),
+    "llmq_gpt2_load_gguf": (I32, [P, ctypes.c_char_p, I32, PP]),
     "llmq_gpt2_load": (I32, [P, ctypes.c_char_p, I32, PP]),
     "llmq_saved_formats": (I32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, I32]),
     "llmq_mat_restore": (I32, [P, I32, I32, I32, I32, I64, I64, P, P, P, PP]),

@@ -5,6 +5,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <chrono>
 #include <vector>
 
 #include "common.h"
@@ -672,8 +673,12 @@ int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host) {
     RC(alloc(m->att, sizeof(float) * MAXT * C));
     RC(alloc(m->fc, sizeof(float) * MAXT * 4 * C));
     RC(alloc(m->logits, sizeof(float) * V));
-    m->nparts = gemv_a16_num_parts(m->wte, true);
-    RC(alloc(m->parts, sizeof(ArgmaxPart) * m->nparts));
+    if (m->gguf) {
+        RC(alloc(m->xn, sizeof(float) * MAXT * C));
+    } else {
+        m->nparts = gemv_a16_num_parts(m->wte, true);
+        RC(alloc(m->parts, sizeof(ArgmaxPart) * m->nparts));
+    }
     RC(alloc(m->tokens, sizeof(int64_t) * MAXT));
     RC(alloc(m->gen, sizeof(int64_t) * MAXT));
     RC(alloc(m->state, sizeof(int) * 4));
@@ -689,7 +694,9 @@ int llmq_gpt2_free(llmq_gpt2 *m) {
     if (m->step_graph) hipGraphExecDestroy(m->step_graph);
     if (m->step_graph_def) hipGraphDestroy(m->step_graph_def);
     llmq_mat_free(m->wte);
+    if (m->lm != m->wte) llmq_mat_free(m->lm);
     for (auto *w : m->mats) llmq_mat_free(w);
+    hipFree(m->xn);
     llmq_kv_free(m->kv);
     hipFree(m->small);
     hipFree(m->x);
@@ -755,6 +762,7 @@ fail:
 int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m) {
     if (!m) return 0;
     int64_t n = llmq_mat_nbytes(m->wte);
+    if (m->lm && m->lm != m->wte) n += llmq_mat_nbytes(m->lm);
     for (auto *w : m->mats) n += llmq_mat_nbytes(w);
     return n + SMALL_FLOATS * 4;  // gpt2t.mojo:312-319
 }
@@ -767,7 +775,7 @@ int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int pos0, floa
     OwnStream os_(m->ctx);
     llmq_ctx *ctx = m->ctx;
     LLMQ_HIP(hipMemcpyAsync(m->tokens, tokens, sizeof(int64_t) * T, hipMemcpyHostToDevice, ctx->stream));
-    RC(gpt2_enqueue(m, T, pos0, false));
+    RC(m->gguf ? gpt2g_enqueue(m, T, pos0) : gpt2_enqueue(m, T, pos0, false));
     if (logits) {
         LLMQ_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * V, hipMemcpyDeviceToHost, ctx->stream));
     }
@@ -778,6 +786,48 @@ int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int pos0, floa
 int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr) {
     LLMQ_REQUIRE(m && dptr, "gpt2_logits_device: bad arguments");
     *dptr = m->logits;
+    return LLMQ_OK;
+}
+
+// generate -t 0 for the GGUF model (gpt2t.mojo:949-1005): the argmax of each
+// step's logits on the host (first maximum, 792-797), fed back as the next
+// token; spans timed on the host around synchronized work.
+static int gpt2g_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int steps, int64_t *out_tokens,
+                          int *n_out, double *prefill_ms, double *decode_ms) {
+    OwnStream os_(m->ctx);
+    llmq_ctx *ctx = m->ctx;
+    std::vector<float> logits((size_t)V);
+    auto now = [] { return std::chrono::steady_clock::now(); };
+    auto argmax = [&](int64_t *tok) -> int {
+        LLMQ_HIP(hipMemcpyAsync(logits.data(), m->logits, sizeof(float) * V, hipMemcpyDeviceToHost, ctx->stream));
+        LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+        int64_t best = 0;
+        for (int64_t i = 1; i < V; i++)
+            if (logits[(size_t)i] > logits[(size_t)best]) best = i;
+        *tok = best;
+        return LLMQ_OK;
+    };
+    LLMQ_HIP(hipMemcpyAsync(m->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, ctx->stream));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    const auto t0 = now();
+    RC(gpt2g_enqueue(m, n_prompt, 0));
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    const auto t1 = now();
+    int n = 0, pos = n_prompt;
+    bool stopped = false;
+    for (int i = 0; i < steps; i++) {
+        int64_t tok;
+        RC(argmax(&tok));
+        if (!stopped && tok == EOT) stopped = true;  // gpt2t.mojo:971-972
+        if (!stopped) out_tokens[n++] = tok;
+        if (stopped || i + 1 == steps) break;
+        LLMQ_HIP(hipMemcpyAsync(m->tokens, &tok, sizeof(int64_t), hipMemcpyHostToDevice, ctx->stream));
+        RC(gpt2g_enqueue(m, 1, pos++));
+    }
+    const auto t2 = now();
+    if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    *n_out = n;
     return LLMQ_OK;
 }
 
@@ -808,6 +858,7 @@ int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int st
     for (int t = 0; t < n_prompt; t++)
         LLMQ_REQUIRE(prompt[t] >= 0 && prompt[t] < V, "gpt2_generate: token %lld out of range", (long long)prompt[t]);
     steps = steps < MAXT - n_prompt ? steps : MAXT - n_prompt;  // gpt2t.mojo:945
+    if (m->gguf) return gpt2g_generate(m, prompt, n_prompt, steps, out_tokens, n_out, prefill_ms, decode_ms);
     OwnStream os_(m->ctx);
     llmq_ctx *ctx = m->ctx;
     const char *ge = getenv("LLMQ_GRAPH");

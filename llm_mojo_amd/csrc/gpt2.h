@@ -28,7 +28,15 @@ struct llmq_gpt2 {
     int *state = nullptr;  // {pos, step} of the device-driven decode loop
     hipGraphExec_t step_graph = nullptr;
     hipGraph_t step_graph_def = nullptr;
+    // Model[GGUFMatrix, GGUFMatrix] (load_gguf, gpt2t.mojo:728-760): layers
+    // and head as stored in a GGUF file, float activations, LayerNorm into xn
+    int gguf = 0;
+    llmq_mat *lm = nullptr;  // the head when not tied to wte
+    float *xn = nullptr;
 };
+
+// The GGUF model's forward (gpt2_gguf.hip): tokens already in m->tokens.
+int gpt2g_enqueue(llmq_gpt2 *m, int T, int pos0);
 
 // Uploads the small tensors (host, SMALL_FLOATS floats in Model.small's
 // order) and allocates the cache (LLMQ_ATTN_FLOAT or LLMQ_ATTN_INT) and the

@@ -165,6 +165,7 @@ extern "C" {
 
 int llmq_gpt2_save(llmq_gpt2 *m, const char *path) {
     LLMQ_REQUIRE(m && path, "gpt2_save: bad arguments");
+    LLMQ_REQUIRE(!m->gguf, "gpt2_save: a model loaded from GGUF keeps its file; save covers QuantMatrix models");
     FILE *f = fopen(path, "wb");
     LLMQ_REQUIRE(f, "gpt2_save: cannot open %s for writing", path);
     FileCloser fc{f};

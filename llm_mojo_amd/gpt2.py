@@ -105,6 +105,19 @@ class GPT2:
         self.sym = "-sym" in layers
         return self
 
+    @classmethod
+    def from_gguf(cls, ctx, path, attention="float"):
+        """load_gguf (gpt2t.mojo:728-760): Model[GGUFMatrix, GGUFMatrix] from a
+        llama.cpp GGUF file of GPT-2 124M, matrices used as stored."""
+        if attention not in ATTENTION:
+            raise ValueError(f"unknown --attention {attention} (float or int)")
+        h = ctypes.c_void_p()
+        check(lib().llmq_gpt2_load_gguf(ctx.h, os.fsencode(path), ATTENTION[attention], ctypes.byref(h)))
+        self = cls.__new__(cls)
+        self.ctx, self.h, self.attention = ctx, h, attention
+        self.bits = self.group = self.sym = None
+        return self
+
     def save(self, path):
         """save_model (gpt2t.mojo:630-650): the converted weights, byte for
         byte the reference's saved-model format."""
@@ -112,6 +125,9 @@ class GPT2:
 
     def name(self):
         """model_name (gpt2t.mojo:1222-1228)."""
+        kv = "int8-intattn" if self.attention == "int" else "int8"
+        if self.bits is None:  # GGUFMatrix layers and head (gguf.mojo:374-375)
+            return "gguf+kv-" + kv
         g = "ch" if self.group == 0 else f"g{self.group}"
         w = f"int{self.bits}-{g}" + ("-sym" if self.sym else "") + "-a16"
         return w + "+head-int8-ch-a16+kv-" + ("int8-intattn" if self.attention == "int" else "int8")

@@ -246,6 +246,17 @@ LLMQ_API int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int p
  * prompt forward, and the steps - 1 decode forwards plus the argmaxes. */
 LLMQ_API int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int steps, int64_t *out_tokens,
                                 int *n_out, double *prefill_ms, double *decode_ms);
+/* Model.forward_all (gpt2t.mojo:448-459): the T tokens from position 0,
+ * then LN_f and the head on every row: logits[T, V] (device memory), row t
+ * predicting token t + 1. */
+LLMQ_API int llmq_gpt2_forward_all(llmq_gpt2 *m, const int64_t *tokens, int T, float *logits);
+/* score_rows (gpt2t.mojo:1040-1095) on the device for window rows r0..r1-1
+ * of logits[*, V] (device): stats (device, float64) receives NLL at
+ * stats[r]; with base != NULL (a baseline's logits, compare mode) also
+ * NLL_BASE, AGREE, KL(base || model), DIFF_MAX, DIFF_SUM at stats[k * ld + r]
+ * for k = 1..5.  targets (device, int64) holds each row's target token. */
+LLMQ_API int llmq_score_rows(llmq_ctx *ctx, const float *logits, const float *base, const int64_t *targets, int r0,
+                             int r1, int V, double *stats, int64_t ld);
 /* Device pointer to the model's logits [V] (after forward / generate). */
 LLMQ_API int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr);
 

@@ -70,6 +70,8 @@ SIGNATURES = {
     "llmq_gguf_tensor_data": (I32, [P, I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(I64)]),
     "llmq_gguf_matrix": (I32, [P, P, ctypes.c_char_p, PP]),
     "llmq_gpt2_save": (I32, [P, ctypes.c_char_p]),
+    "llmq_gpt2_forward_all": (I32, [P, P, I32, P]),
+    "llmq_score_rows": (I32, [P, P, P, P, I32, I32, I32, P, I64]),
     "llmq_gpt2_load_gguf": (I32, [P, ctypes.c_char_p, I32, PP]),
     "llmq_gpt2_load": (I32, [P, ctypes.c_char_p, I32, PP]),
     "llmq_saved_formats": (I32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, I32]),
@@ -133,6 +135,34 @@ def dptr(t):
 def hptr(a):
     """Host address of a numpy array."""
     return None if a is None else a.ctypes.data
+
+
+class DeviceBuffer:
+    """nbytes of device memory from llmq_malloc (freed with the object)."""
+
+    def __init__(self, ctx, nbytes):
+        self.ctx = ctx
+        p = ctypes.c_void_p()
+        check(lib().llmq_malloc(ctx.h, nbytes, ctypes.byref(p)))
+        self.ptr, self.nbytes = p.value, nbytes
+
+    def upload(self, a):
+        check(lib().llmq_memcpy_h2d(self.ctx.h, self.ptr, hptr(a), a.nbytes))
+
+    def download(self, a):
+        check(lib().llmq_memcpy_d2h(self.ctx.h, hptr(a), self.ptr, a.nbytes))
+        return a
+
+    def free(self):
+        if getattr(self, "ptr", None):
+            lib().llmq_free(self.ctx.h, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class Context:

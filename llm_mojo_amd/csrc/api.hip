@@ -579,7 +579,7 @@ int llmq_ikv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, int3
 // Model.blocks (gpt2t.mojo:485-571) for T tokens: tokens in m->tokens when
 // state == nullptr, else one token picked on the device from the previous
 // head's argmax partials (decode), with the position in state[0].
-static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step) {
+static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool with_head = true) {
     llmq_ctx *ctx = m->ctx;
     if (device_step)
         RC(launch_embed(ctx, m->wte, m->wpe, nullptr, 1, 0, m->x, m->parts, m->nparts, m->gen, m->state, 1));
@@ -628,6 +628,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step) {
         g.flags = LLMQ_BIAS | LLMQ_RESID;
         RC(launch_gemv_a16(ctx, g));
     }
+    if (!with_head) return LLMQ_OK;
     // Model.forward's tail (gpt2t.mojo:337-340): LN_f on the last row, head.
     GemvRequest h;
     h.w = m->wte;
@@ -779,6 +780,24 @@ int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int pos0, floa
     if (logits) {
         LLMQ_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * V, hipMemcpyDeviceToHost, ctx->stream));
     }
+    LLMQ_HIP(hipStreamSynchronize(ctx->stream));
+    return LLMQ_OK;
+}
+
+int llmq_gpt2_forward_all(llmq_gpt2 *m, const int64_t *tokens, int T, float *logits) {
+    LLMQ_REQUIRE(m && tokens && logits && T >= 1, "gpt2_forward_all: bad arguments");
+    LLMQ_REQUIRE(T <= MAXT, "gpt2_forward_all: %d tokens beyond %d", T, MAXT);
+    for (int t = 0; t < T; t++)
+        LLMQ_REQUIRE(tokens[t] >= 0 && tokens[t] < V, "gpt2_forward_all: token %lld out of range",
+                     (long long)tokens[t]);
+    OwnStream os_(m->ctx);
+    llmq_ctx *ctx = m->ctx;
+    LLMQ_HIP(hipMemcpyAsync(m->tokens, tokens, sizeof(int64_t) * T, hipMemcpyHostToDevice, ctx->stream));
+    RC(m->gguf ? gpt2g_enqueue(m, T, 0, false) : gpt2_enqueue(m, T, 0, false, false));
+    // Model.forward_all's tail (gpt2t.mojo:448-459): LN_f on every row (into
+    // att, free after the blocks), then the head for all T rows.
+    RC(launch_layernorm(ctx, m->att, m->x, m->lnf_w, m->lnf_b, T, C));
+    RC(llmq_head(ctx, logits, m->att, m->gguf ? m->lm : m->wte, T, V, C));
     LLMQ_HIP(hipStreamSynchronize(ctx->stream));
     return LLMQ_OK;
 }

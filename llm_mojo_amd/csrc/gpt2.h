@@ -36,7 +36,7 @@ struct llmq_gpt2 {
 };
 
 // The GGUF model's forward (gpt2_gguf.hip): tokens already in m->tokens.
-int gpt2g_enqueue(llmq_gpt2 *m, int T, int pos0);
+int gpt2g_enqueue(llmq_gpt2 *m, int T, int pos0, bool with_head = true);
 
 // Uploads the small tensors (host, SMALL_FLOATS floats in Model.small's
 // order) and allocates the cache (LLMQ_ATTN_FLOAT or LLMQ_ATTN_INT) and the

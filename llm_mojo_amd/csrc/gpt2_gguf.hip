@@ -65,7 +65,7 @@ struct GgufCloser {
 
 // Model.blocks and the head (gpt2t.mojo:329-342, 485-571) for the T tokens in
 // m->tokens at positions pos0..
-int gpt2g_enqueue(llmq_gpt2 *m, int T, int pos0) {
+int gpt2g_enqueue(llmq_gpt2 *m, int T, int pos0, bool with_head) {
     llmq_ctx *ctx = m->ctx;
     RC(launch_gguf_dequant_rows(ctx, m->wte, m->tokens, T, m->x, C));
     const int64_t n = (int64_t)T * C;
@@ -84,6 +84,7 @@ int gpt2g_enqueue(llmq_gpt2 *m, int T, int pos0) {
         RC(linear(m, w[2], m->xn, T, m->fc, v[FC_B], LLMQ_BIAS | LLMQ_GELU));
         RC(linear(m, w[3], m->fc, T, m->x, v[FCPROJ_B], LLMQ_BIAS | LLMQ_RESID));
     }
+    if (!with_head) return LLMQ_OK;
     // LN_f on the last row, then the head (gpt2t.mojo:337-340)
     RC(launch_layernorm(ctx, m->xn, m->x + (int64_t)(T - 1) * C, m->lnf_w, m->lnf_b, 1, C));
     if (gguf_has_i16(m->lm)) return launch_gguf_head16(ctx, m->lm, m->xn, m->logits, 1);

@@ -142,6 +142,13 @@ class GPT2:
         check(lib().llmq_gpt2_forward(self.h, hptr(toks), len(toks), pos0, hptr(logits)))
         return logits
 
+    def forward_all(self, tokens, logits):
+        """Model.forward_all (gpt2t.mojo:448-459): logits for every position
+        into logits (device address or torch tensor, [T, V] float32)."""
+        toks = np.ascontiguousarray(tokens, np.int64)
+        addr = logits if isinstance(logits, int) else logits.data_ptr()
+        check(lib().llmq_gpt2_forward_all(self.h, hptr(toks), len(toks), addr))
+
     def generate(self, prompt, steps):
         """Greedy generate (-t 0): (tokens, prefill_ms, decode_ms) with the
         reference's timing spans (gpt2t.mojo:949-1005)."""

@@ -118,6 +118,8 @@ def _declare(L):
         "orc_gpt2_new": (P, [P, I32, I32, I32]),
         "orc_gpt2_free": (None, [P]),
         "orc_gpt2_set_attention": (None, [P, I32]),
+        "orc_gpt2_forward_all": (None, [P, P, I32, P]),
+        "orc_score_rows": (None, [P, I64, P, P, P, I32, I32, I32]),
         "orc_gpt2_mat": (P, [P, I32]),
         "orc_gpt2_kv": (P, [P]),
         "orc_gpt2_act": (P, [P, I32]),
@@ -451,6 +453,18 @@ def argmax(logits):
     return lib().orc_argmax(ptr(logits), logits.size)
 
 
+def score_rows(logits, targets, r0, r1, base=None):
+    """score_rows (gpt2t.mojo:1040-1095): stats [6, rows] (NLL, NLL_BASE,
+    AGREE, KL, DIFF_MAX, DIFF_SUM; all but NLL zero without base)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    base = np.ascontiguousarray(base, np.float32) if base is not None else None
+    targets = np.ascontiguousarray(targets, np.int64)
+    rows, V = logits.shape
+    stats = np.zeros((6, rows))
+    lib().orc_score_rows(ptr(stats), rows, ptr(logits), ptr(base), ptr(targets), r0, r1, V)
+    return stats
+
+
 # ------------------------------------------------------------ GGUF files
 
 def gguf_index(path):
@@ -636,6 +650,13 @@ class GPT2:
         toks = np.ascontiguousarray(tokens, np.int64)
         p = lib().orc_gpt2_forward(self.h, ptr(toks), len(toks), pos0)
         return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(50257,)).copy()
+
+    def forward_all(self, tokens):
+        """Model.forward_all (gpt2t.mojo:448-459): logits [T, V]."""
+        toks = np.ascontiguousarray(tokens, np.int64)
+        out = np.zeros((len(toks), 50257), np.float32)
+        lib().orc_gpt2_forward_all(self.h, ptr(toks), len(toks), ptr(out))
+        return out
 
     def generate(self, prompt, steps):
         prompt = np.ascontiguousarray(prompt, np.int64)

@@ -1315,6 +1315,56 @@ const float *orc_gpt2_forward(orc_gpt2 *m, const int64_t *tokens, int T, int pos
     return m->logits;
 }
 
+/* Model.forward_all (gpt2t.mojo:448-459): tokens from position 0, LN_f on
+ * every row, the head on all T rows: logits[T, V], row t predicting t + 1. */
+void orc_gpt2_forward_all(orc_gpt2 *m, const int64_t *tokens, int T, float *logits) {
+    gpt2_blocks(m, tokens, T, 0);
+    orc_layernorm(m->xn, m->x, m->lnf_w, m->lnf_b, T, G_C);
+    orc_matmul_rows_a16(logits, m->xn, &m->wte, NULL, T, G_C, G_V, 0);
+}
+
+/* log_sum_exp (gpt2t.mojo:1027-1036): the row maximum, then exp(l - max) in
+ * float32 summed in float64 in vocabulary order. */
+static double log_sum_exp(const float *row, int V) {
+    float mx = row[0];
+    for (int v = 1; v < V; v++) mx = row[v] > mx ? row[v] : mx;
+    double s = 0.0;
+    for (int v = 0; v < V; v++) s += (double)expf(row[v] - mx);
+    return (double)mx + log(s);
+}
+
+/* score_rows (gpt2t.mojo:1040-1095) for rows r0..r1-1: stats[k * ld + r]
+ * for k = NLL, and with base != NULL NLL_BASE, AGREE, KL, DIFF_MAX,
+ * DIFF_SUM. */
+void orc_score_rows(double *stats, int64_t ld, const float *logits, const float *base, const int64_t *targets,
+                    int r0, int r1, int V) {
+    for (int r = r0; r < r1; r++) {
+        const float *lm = logits + (int64_t)r * V;
+        const int64_t target = targets[r];
+        const double lse = log_sum_exp(lm, V);
+        stats[r] = lse - (double)lm[target];
+        if (!base) continue;
+        const float *lb = base + (int64_t)r * V;
+        const double lse_b = log_sum_exp(lb, V);
+        double kl = 0.0, dmax = 0.0, dsum = 0.0;
+        int best = 0, best_b = 0;
+        for (int v = 0; v < V; v++) {
+            const double lpb = (double)lb[v] - lse_b;
+            kl += exp(lpb) * (lpb - ((double)lm[v] - lse));
+            const double d = fabs((double)lm[v] - (double)lb[v]);
+            dmax = d > dmax ? d : dmax;
+            dsum += d;
+            if (lm[v] > lm[best]) best = v;
+            if (lb[v] > lb[best_b]) best_b = v;
+        }
+        stats[1 * ld + r] = lse_b - (double)lb[target];
+        stats[2 * ld + r] = best == best_b ? 1.0 : 0.0;
+        stats[3 * ld + r] = kl;
+        stats[4 * ld + r] = dmax;
+        stats[5 * ld + r] = dsum;
+    }
+}
+
 /* generate's greedy loop (gpt2t.mojo:949-981 with -t 0): prompt, then up to
  * `steps` tokens (stopping at EOT 50256); returns the count generated.  The
  * decode loop runs steps - 1 forwards for steps tokens. */

@@ -589,18 +589,25 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
     for (int l = 0; l < NL; l++) {
         llmq_mat **w = &m->mats[l * 4];
         const float *const *v = m->vec[l];
-        GemvRequest q;
-        q.w = w[0];
-        q.x = m->x;
-        q.ln_w = v[LN1_W];
-        q.ln_b = v[LN1_B];
-        q.out = m->qkv;
-        q.bias = v[QKV_B];
-        q.T = T;
-        q.flags = LLMQ_BIAS;
-        RC(launch_gemv_a16(ctx, q));
-        if (T > 1) RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
-        RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, pos_dev, 3 * C, T == 1));
+        int fused = LLMQ_EUNSUPPORTED;
+        if (T == 1 && m->fuse_qkv_attn)  // qkv, the cache store and attention in one kernel
+            fused = launch_qkv_attn(ctx, w[0], m->x, v[LN1_W], v[LN1_B], v[QKV_B], m->kv, l, pos0, pos_dev,
+                                    m->qkv, m->att);
+        if (fused != LLMQ_OK && fused != LLMQ_EUNSUPPORTED) return fused;
+        if (fused == LLMQ_EUNSUPPORTED) {
+            GemvRequest q;
+            q.w = w[0];
+            q.x = m->x;
+            q.ln_w = v[LN1_W];
+            q.ln_b = v[LN1_B];
+            q.out = m->qkv;
+            q.bias = v[QKV_B];
+            q.T = T;
+            q.flags = LLMQ_BIAS;
+            RC(launch_gemv_a16(ctx, q));
+            if (T > 1) RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
+            RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, pos_dev, 3 * C, T == 1));
+        }
         GemvRequest p;
         p.w = w[1];
         p.x = m->att;
@@ -643,6 +650,8 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
     return launch_gemv_a16(ctx, h);
 }
 
+static void set_fuse_mode(llmq_gpt2 *m, int max_pos);
+
 // The model's small tensors (host, SMALL_FLOATS in Model.small's order),
 // its KV cache and activation buffers; the matrices are already in place.
 int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host) {
@@ -664,6 +673,8 @@ int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host) {
     m->lnf_w = m->small + off;
     m->lnf_b = m->small + off + C;
     LLMQ_HIP(hipMemcpy(m->small, small_host, sizeof(float) * SMALL_FLOATS, hipMemcpyHostToDevice));
+    const char *fe = getenv("LLMQ_FUSED_QKV");
+    m->fuse_env = fe && fe[0] == '0' ? 0 : (fe && fe[0] == '1' ? 1 : -1);
     // run_with[W, E, QuantKV[8] or IntAttnKV] (gpt2t.mojo:1238-1257)
     if (attention == LLMQ_ATTN_INT)
         RC(llmq_ikv_create(ctx, NL, MAXT, NH, HS, &m->kv));
@@ -776,6 +787,7 @@ int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int pos0, floa
     OwnStream os_(m->ctx);
     llmq_ctx *ctx = m->ctx;
     LLMQ_HIP(hipMemcpyAsync(m->tokens, tokens, sizeof(int64_t) * T, hipMemcpyHostToDevice, ctx->stream));
+    set_fuse_mode(m, pos0 + T);
     RC(m->gguf ? gpt2g_enqueue(m, T, pos0) : gpt2_enqueue(m, T, pos0, false));
     if (logits) {
         LLMQ_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * V, hipMemcpyDeviceToHost, ctx->stream));
@@ -850,6 +862,23 @@ static int gpt2g_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int
     return LLMQ_OK;
 }
 
+// The decode mode for contexts up to max_pos positions; a change drops the
+// captured step graph.
+static void set_fuse_mode(llmq_gpt2 *m, int max_pos) {
+    const int want = m->fuse_env >= 0 ? m->fuse_env : (max_pos > kFuseFrom ? 1 : 0);
+    if (want == m->fuse_qkv_attn) return;
+    m->fuse_qkv_attn = want;
+    if (m->step_graph) {
+        hipStreamSynchronize(m->ctx->stream);
+        hipGraphExecDestroy(m->step_graph);
+        m->step_graph = nullptr;
+    }
+    if (m->step_graph_def) {
+        hipGraphDestroy(m->step_graph_def);
+        m->step_graph_def = nullptr;
+    }
+}
+
 static int decode_step(llmq_gpt2 *m, bool use_graph) {
     llmq_ctx *ctx = m->ctx;
     if (!use_graph) return gpt2_enqueue(m, 1, 0, true);
@@ -878,6 +907,7 @@ int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int st
         LLMQ_REQUIRE(prompt[t] >= 0 && prompt[t] < V, "gpt2_generate: token %lld out of range", (long long)prompt[t]);
     steps = steps < MAXT - n_prompt ? steps : MAXT - n_prompt;  // gpt2t.mojo:945
     if (m->gguf) return gpt2g_generate(m, prompt, n_prompt, steps, out_tokens, n_out, prefill_ms, decode_ms);
+    set_fuse_mode(m, n_prompt + steps);
     OwnStream os_(m->ctx);
     llmq_ctx *ctx = m->ctx;
     const char *ge = getenv("LLMQ_GRAPH");

@@ -184,6 +184,12 @@ int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *
 // store: also quantize and store the token's key and value (T == 1).
 int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
                      const int *pos_dev, int64_t ld, bool store);
+// One decode token's qkv GEMV (LayerNorm fused) + KV store + attention, one
+// workgroup per head (qkv_attn.hip); LLMQ_EUNSUPPORTED (no error recorded)
+// when the shapes do not fit it.
+int launch_qkv_attn(llmq_ctx *ctx, const llmq_mat *w, const float *x, const float *ln_w, const float *ln_b,
+                    const float *bias, llmq_kv *kv, int layer, int pos0, const int *pos_dev, float *qkv_out,
+                    float *att);
 // The same two steps for an IntAttnKV cache (kv->integer; int_attn.hip);
 // launch_kv_store / launch_kv_attend route there by themselves.
 int launch_ikv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,

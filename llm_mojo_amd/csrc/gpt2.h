@@ -6,6 +6,7 @@
 #include "common.h"
 
 namespace {
+constexpr int kFuseFrom = 256;  // positions from which decode uses the fused qkv + attention kernel
 constexpr int NL = 12, NH = 12, C = 768, HS = 64, MAXT = 1024, V = 50257, EOT = 50256;
 enum { LN1_W, LN1_B, QKV_B, PROJ_B, LN2_W, LN2_B, FC_B, FCPROJ_B, N_VECS };
 constexpr int VEC_LEN[N_VECS] = {C, C, 3 * C, C, C, C, 4 * C, C};
@@ -30,6 +31,11 @@ struct llmq_gpt2 {
     hipGraph_t step_graph_def = nullptr;
     // Model[GGUFMatrix, GGUFMatrix] (load_gguf, gpt2t.mojo:728-760): layers
     // and head as stored in a GGUF file, float activations, LayerNorm into xn
+    // Decode tokens run qkv + attention as one kernel (qkv_attn.hip) past
+    // kFuseFrom cached positions, where it is faster; LLMQ_FUSED_QKV=0 / 1
+    // forces two kernels / the fused one.
+    int fuse_env = -1;
+    int fuse_qkv_attn = 0;  // the mode the enqueued (and captured) step uses
     int gguf = 0;
     llmq_mat *lm = nullptr;  // the head when not tied to wte
     float *xn = nullptr;

@@ -71,3 +71,36 @@ def test_gpt2_generate_on_device_matches_forward(gpu, orc, weights):
     first_diff = next((i for i in range(n) if toks[i] != want[i]), n)
     assert first_diff >= n - 2, (toks.tolist(), want.tolist())
     assert pre_ms > 0 and dec_ms > 0
+
+
+def test_gpt2_fused_qkv_attention(gpu, orc, weights, monkeypatch):
+    """Decode tokens through the fused qkv + attention kernel (used past 256
+    cached positions; forced here) against the oracle and the two-kernel
+    path, after a 300-token prompt, teacher-forced and on the device."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import gpt2, synth
+
+    prompt = synth.prompt_ids(4, 300)
+    monkeypatch.setenv("LLMQ_FUSED_QKV", "1")
+    mf = lm.GPT2(ctx, weights)
+    monkeypatch.setenv("LLMQ_FUSED_QKV", "0")
+    mu = lm.GPT2(ctx, weights)
+    ref = orc.GPT2(gpt2.params_list(weights))
+    print("fused prefill", flush=True)
+    lf, lu, lo = mf.forward(prompt, 0), mu.forward(prompt, 0), ref.forward(prompt, 0)
+    pos, errs, agree = len(prompt), [], 0
+    for i in range(8):
+        nxt = orc.argmax(lo)
+        print("fused decode step", i, flush=True)
+        lf, lu, lo = mf.forward([nxt], pos), mu.forward([nxt], pos), ref.forward([nxt], pos)
+        pos += 1
+        errs.append(max(np.max(np.abs(lf - lo)), np.max(np.abs(lf - lu))) / np.max(np.abs(lo)))
+        agree += int(np.argmax(lf) == orc.argmax(lo))
+    print("fused max rel err", max(errs), "top-1", agree, "/ 8", flush=True)
+    assert max(errs) < LOGIT_REL and agree >= 7
+    tf, _, _ = mf.generate(prompt, 12)
+    tu, _, _ = mu.generate(prompt, 12)
+    n = min(len(tf), len(tu))
+    assert next((i for i in range(n) if tf[i] != tu[i]), n) >= n - 2, (tf.tolist(), tu.tolist())
+    mf.free()
+    mu.free()

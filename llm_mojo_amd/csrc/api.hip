@@ -673,7 +673,7 @@ int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host) {
     m->lnf_w = m->small + off;
     m->lnf_b = m->small + off + C;
     LLMQ_HIP(hipMemcpy(m->small, small_host, sizeof(float) * SMALL_FLOATS, hipMemcpyHostToDevice));
-    const char *fe = getenv("LLMQ_FUSED_QKV");
+    const char *fe = getenv("LLMQ_DECODE_FUSION");
     m->fuse_env = fe && fe[0] == '0' ? 0 : (fe && fe[0] == '1' ? 1 : -1);
     // run_with[W, E, QuantKV[8] or IntAttnKV] (gpt2t.mojo:1238-1257)
     if (attention == LLMQ_ATTN_INT)

@@ -32,7 +32,7 @@ struct llmq_gpt2 {
     // Model[GGUFMatrix, GGUFMatrix] (load_gguf, gpt2t.mojo:728-760): layers
     // and head as stored in a GGUF file, float activations, LayerNorm into xn
     // Decode tokens run qkv + attention as one kernel (qkv_attn.hip) past
-    // kFuseFrom cached positions, where it is faster; LLMQ_FUSED_QKV=0 / 1
+    // kFuseFrom cached positions, where it is faster; LLMQ_DECODE_FUSION=0 / 1
     // forces two kernels / the fused one.
     int fuse_env = -1;
     int fuse_qkv_attn = 0;  // the mode the enqueued (and captured) step uses

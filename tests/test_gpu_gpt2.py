@@ -81,9 +81,9 @@ def test_gpt2_fused_qkv_attention(gpu, orc, weights, monkeypatch):
     from llm_mojo_amd import gpt2, synth
 
     prompt = synth.prompt_ids(4, 300)
-    monkeypatch.setenv("LLMQ_FUSED_QKV", "1")
+    monkeypatch.setenv("LLMQ_DECODE_FUSION", "1")
     mf = lm.GPT2(ctx, weights)
-    monkeypatch.setenv("LLMQ_FUSED_QKV", "0")
+    monkeypatch.setenv("LLMQ_DECODE_FUSION", "0")
     mu = lm.GPT2(ctx, weights)
     ref = orc.GPT2(gpt2.params_list(weights))
     print("fused prefill", flush=True)

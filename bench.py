@@ -212,6 +212,34 @@ def int_attention(lm, synth, ctx, tensors, model, steps):
     return res
 
 
+# README.md:75-90's QuantMatrix rows: --dtype, --head int8, the reference's
+# decode tok/s short / long on its CPU
+FORMAT_ROWS = [("int8-ch", (200, 175)), ("int4-g32", (150, 136)), ("int8-ch-a16", (283, 241)),
+               ("int4-ch-a16", (251, 214))]
+
+
+def format_table(lm, synth, ctx, tensors, steps):
+    """Decode tok/s of config 0's generation for the other QuantMatrix
+    formats of the reference's table (float activations and A16), after the
+    12-token prompt and after a 476-token one."""
+    res = {}
+    for dtype, ref in FORMAT_ROWS:
+        m = lm.GPT2(ctx, tensors, dtype=dtype, head="int8")
+        row = {"reference_cpu": ref}
+        for name, plen in (("prompt12", PROMPT), ("prompt476", PREFILL_T)):
+            prompt = synth.prompt_ids(SEED, plen)
+            m.generate(prompt, GEN)  # warm-up (captures the decode graph)
+            n, dms = 0, 0.0
+            for _ in range(steps):
+                toks, _, d = m.generate(prompt, GEN)
+                n += len(toks)
+                dms += d
+            row[f"{name}_decode_tok_s"] = round(n / (dms / 1000.0), 1)
+        res[dtype] = row
+        m.free()
+    return res
+
+
 GGUF_KINDS = {"Q4_0": 2, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_0": 8}
 GGUF_SHAPES = [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)]
 
@@ -325,6 +353,7 @@ def main():
     ap.add_argument("--no-llama", action="store_true", help="skip the TinyLlama-shaped decoder (config 4)")
     ap.add_argument("--gguf-sweep", action="store_true", help="add the GGUF GEMV sweep (config 2, ~1 min)")
     ap.add_argument("--no-intattn", action="store_true", help="skip the integer-attention decode comparison")
+    ap.add_argument("--no-formats", action="store_true", help="skip the decode table of the other formats")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline GEMV and the reference copy (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -389,6 +418,10 @@ def main():
         log("integer attention decode")
         extra["gpt2_int_attention"] = int_attention(lm, synth, ctx, tensors, model, args.steps)
         log(extra["gpt2_int_attention"])
+    if not args.no_formats:
+        log("format table")
+        extra["gpt2_formats"] = format_table(lm, synth, ctx, tensors, args.steps)
+        log(extra["gpt2_formats"])
     if not args.no_prefill:
         log("prefill 476")
         extra["prefill_476"] = prefill(torch, lm, synth, ctx, tensors, model)

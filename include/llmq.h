@@ -152,13 +152,17 @@ LLMQ_API int llmq_quantize_rows(llmq_ctx *ctx, const float *x, int64_t T, int64_
 /* kernels.linear (kernels.mojo:655-673; decode team form linear_team
  * 774-866): out[T, OUT] (+)= act(x[T, IN] @ W^T + bias).  For an a16
  * QuantMatrix the activations are quantized per row to int16 and the sums
- * run in integers (matmul_rows_a16, 419-509); for a GGUF matrix the float
- * path (matmul_rows, 285-312).  flags: LLMQ_BIAS | LLMQ_GELU | LLMQ_RESID. */
+ * run in integers (matmul_rows_a16, 419-509); for a GGUF matrix or a
+ * QuantMatrix with a16 = 0 the float path (matmul_rows, 285-349, over
+ * GGUFMatrix.dot_row / QuantMatrix.dot_row, tensor.mojo:431-482).
+ * flags: LLMQ_BIAS | LLMQ_GELU | LLMQ_RESID. */
 LLMQ_API int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, const float *bias, int64_t T,
                          int64_t IN, int64_t OUT, int flags);
 /* The same with LayerNorm (kernels.layernorm, 179-197; eps 1e-5) applied to
  * each input row first: the LN -> linear pairs of Model.decode
- * (gpt2t.mojo:390-399, 419-428) in one call. */
+ * (gpt2t.mojo:390-399, 419-428) in one call (one kernel for a16 matrices;
+ * for a16 = 0 the LayerNorm goes through the context's workspace, so that
+ * form is not for graph capture). */
 LLMQ_API int llmq_ln_linear(llmq_ctx *ctx, float *out, const float *x, const float *ln_w, const float *ln_b,
                             const llmq_mat *w, const float *bias, int64_t T, int64_t IN, int64_t OUT, int flags);
 /* kernels.head / head_team (kernels.mojo:676-690, 869-910): logits[T, V] =
@@ -231,6 +235,12 @@ LLMQ_API int llmq_gpt2_create(llmq_ctx *ctx, const float *const *params, int bit
 enum { LLMQ_ATTN_FLOAT = 0, LLMQ_ATTN_INT = 1 };
 LLMQ_API int llmq_gpt2_create_ex(llmq_ctx *ctx, const float *const *params, int bits, int group, int sym,
                                  int attention, llmq_gpt2 **out);
+/* The model gpt2t.mojo's main builds for --dtype / --head (1282-1348):
+ * dtype a QuantMatrix name (int8-ch, int4-ch, int4-g128, int4-g64, int4-g32,
+ * each optionally -sym, each optionally -a16), head "int8" (HEAD8, or
+ * HEAD8_A16 for -a16 layers) or "same" (the layers' format). */
+LLMQ_API int llmq_gpt2_create_fmt(llmq_ctx *ctx, const float *const *params, const char *dtype, const char *head,
+                                  int attention, llmq_gpt2 **out);
 LLMQ_API int llmq_gpt2_free(llmq_gpt2 *m);
 /* Model.weight_bytes (gpt2t.mojo:312-319). */
 LLMQ_API int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m);
@@ -265,8 +275,9 @@ LLMQ_API int llmq_gpt2_logits_device(llmq_gpt2 *m, float **dptr);
  * load_saved (668-698) with the cache chosen as in llmq_gpt2_create_ex, and
  * saved_formats (661-666), which copies the layer and head format names
  * (e.g. "int4-g32-a16", "int8-ch-a16") into buffers of cap bytes.  The
- * device model loads QuantMatrix A16 layers (int4 / int8) with the
- * HEAD8_A16 head; other formats return LLMQ_EUNSUPPORTED. */
+ * device model loads QuantMatrix layers with the int8 per-channel head
+ * (HEAD8 / HEAD8_A16 as the layers) or the layers' own format as head
+ * (main's --weights, 1298-1303); other files return LLMQ_EUNSUPPORTED. */
 LLMQ_API int llmq_gpt2_save(llmq_gpt2 *m, const char *path);
 LLMQ_API int llmq_gpt2_load(llmq_ctx *ctx, const char *path, int attention, llmq_gpt2 **out);
 LLMQ_API int llmq_saved_formats(const char *path, char *layers, char *head, int cap);

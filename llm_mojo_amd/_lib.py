@@ -61,6 +61,7 @@ SIGNATURES = {
     "llmq_ikv_export": (I32, [P, P, P, P, P, P]),
     "llmq_gpt2_create": (I32, [P, P, I32, I32, I32, PP]),
     "llmq_gpt2_create_ex": (I32, [P, P, I32, I32, I32, I32, PP]),
+    "llmq_gpt2_create_fmt": (I32, [P, P, ctypes.c_char_p, ctypes.c_char_p, I32, PP]),
     "llmq_gguf_open": (I32, [ctypes.c_char_p, PP]),
     "llmq_gguf_close": (I32, [P]),
     "llmq_gguf_n_tensors": (I64, [P]),

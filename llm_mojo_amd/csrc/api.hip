@@ -399,9 +399,6 @@ static int check_linear(const llmq_mat *w, int64_t IN, int64_t OUT) {
     LLMQ_REQUIRE(w, "linear: null matrix");
     LLMQ_REQUIRE(w->k == IN && w->n == OUT, "linear: matrix is %lldx%lld, call says IN=%lld OUT=%lld",
                  (long long)w->n, (long long)w->k, (long long)IN, (long long)OUT);
-    if (w->kind == MAT_QUANT && !w->a16)
-        return llmq_set_error(LLMQ_EUNSUPPORTED,
-                              "linear: float-activation QuantMatrix (A16=False) has no device kernel in this build");
     return LLMQ_OK;
 }
 
@@ -409,9 +406,11 @@ int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, co
                 int64_t IN, int64_t OUT, int flags) {
     LLMQ_REQUIRE(ctx, "linear: null context");
     RC(check_linear(w, IN, OUT));
-    if (w->kind == MAT_GGUF) {
-        // matmul_rows (kernels.mojo:285-349): the one-token GEMV, or the
-        // dequantize-and-multiply matmul for several tokens
+    if (is_float_act(w)) {
+        // matmul_rows (kernels.mojo:285-349) for GGUF and for QuantMatrix
+        // with A16 = False: the one-token GEMV (dot_row, tensor.mojo:431-482;
+        // gguf.mojo:389-417), or the dequantize-and-multiply matmul for
+        // several tokens
         if (T == 1) return launch_gguf_gemv(ctx, w, x, out, bias, flags, nullptr, 0);
         return launch_gguf_gemm(ctx, w, x, IN, T, out, OUT, bias, flags);
     }
@@ -430,6 +429,15 @@ int llmq_ln_linear(llmq_ctx *ctx, float *out, const float *x, const float *ln_w,
     LLMQ_REQUIRE(ctx && ln_w && ln_b, "ln_linear: bad arguments");
     RC(check_linear(w, IN, OUT));
     LLMQ_REQUIRE(w->kind == MAT_QUANT, "ln_linear: GGUF matrices take llmq_layernorm then llmq_linear");
+    if (!w->a16) {
+        // float activations: the LayerNorm into the context's workspace, then
+        // matmul_rows (not for use under graph capture, as the workspace)
+        void *ws = nullptr;
+        RC(ctx_workspace(ctx, sizeof(float) * (size_t)(T * IN), &ws));
+        float *xn = static_cast<float *>(ws);
+        RC(launch_layernorm(ctx, xn, x, ln_w, ln_b, T, IN));
+        return llmq_linear(ctx, out, xn, w, bias, T, IN, OUT, flags);
+    }
     GemvRequest rq;
     rq.w = w;
     rq.x = x;
@@ -460,7 +468,7 @@ int llmq_debug_chunk_sums(llmq_ctx *ctx, const float *xf, const llmq_mat *w, flo
                           int16_t *xq, float *sx) {
     LLMQ_REQUIRE(ctx && w, "debug_chunk_sums: bad arguments");
     RC(check_linear(w, w->k, w->n));
-    LLMQ_REQUIRE(w->kind == MAT_QUANT, "debug_chunk_sums: QuantMatrix only");
+    LLMQ_REQUIRE(w->kind == MAT_QUANT && w->a16, "debug_chunk_sums: integer-activation QuantMatrix (A16) only");
     GemvRequest rq;
     rq.w = w;
     rq.x = xf;
@@ -576,6 +584,20 @@ int llmq_ikv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, int3
 
 // ------------------------------------------------------------------- GPT-2
 
+// One linear of Model.blocks / the head (kernels.linear, kernels.mojo:655-673):
+// A16 layers take the integer kernels with the LayerNorm fused; float
+// activations (A16 = False) take LayerNorm into xn, then matmul_rows.
+static int gpt2_linear(llmq_gpt2 *m, const GemvRequest &rq) {
+    if (rq.w->a16) return launch_gemv_a16(m->ctx, rq);
+    const float *x = rq.x;
+    if (rq.ln_w) {
+        RC(launch_layernorm(m->ctx, m->xn, rq.x, rq.ln_w, rq.ln_b, rq.T, rq.w->k));
+        x = m->xn;
+    }
+    if (rq.T == 1) return launch_gguf_gemv(m->ctx, rq.w, x, rq.out, rq.bias, rq.flags, rq.amax, rq.amax_cap);
+    return launch_gguf_gemm(m->ctx, rq.w, x, rq.w->k, rq.T, rq.out, rq.w->n, rq.bias, rq.flags);
+}
+
 // Model.blocks (gpt2t.mojo:485-571) for T tokens: tokens in m->tokens when
 // state == nullptr, else one token picked on the device from the previous
 // head's argmax partials (decode), with the position in state[0].
@@ -604,7 +626,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
             q.bias = v[QKV_B];
             q.T = T;
             q.flags = LLMQ_BIAS;
-            RC(launch_gemv_a16(ctx, q));
+            RC(gpt2_linear(m, q));
             if (T > 1) RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
             RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, pos_dev, 3 * C, T == 1));
         }
@@ -615,7 +637,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
         p.bias = v[PROJ_B];
         p.T = T;
         p.flags = LLMQ_BIAS | LLMQ_RESID;
-        RC(launch_gemv_a16(ctx, p));
+        RC(gpt2_linear(m, p));
         GemvRequest f;
         f.w = w[2];
         f.x = m->x;
@@ -625,7 +647,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
         f.bias = v[FC_B];
         f.T = T;
         f.flags = LLMQ_BIAS | LLMQ_GELU;
-        RC(launch_gemv_a16(ctx, f));
+        RC(gpt2_linear(m, f));
         GemvRequest g;
         g.w = w[3];
         g.x = m->fc;
@@ -633,7 +655,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
         g.bias = v[FCPROJ_B];
         g.T = T;
         g.flags = LLMQ_BIAS | LLMQ_RESID;
-        RC(launch_gemv_a16(ctx, g));
+        RC(gpt2_linear(m, g));
     }
     if (!with_head) return LLMQ_OK;
     // Model.forward's tail (gpt2t.mojo:337-340): LN_f on the last row, head.
@@ -647,7 +669,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
     h.flags = 0;
     h.amax = m->parts;
     h.amax_cap = m->nparts;
-    return launch_gemv_a16(ctx, h);
+    return gpt2_linear(m, h);
 }
 
 static void set_fuse_mode(llmq_gpt2 *m, int max_pos);
@@ -685,10 +707,11 @@ int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host) {
     RC(alloc(m->att, sizeof(float) * MAXT * C));
     RC(alloc(m->fc, sizeof(float) * MAXT * 4 * C));
     RC(alloc(m->logits, sizeof(float) * V));
-    if (m->gguf) {
-        RC(alloc(m->xn, sizeof(float) * MAXT * C));
-    } else {
-        m->nparts = gemv_a16_num_parts(m->wte, true);
+    bool float_act = m->gguf != 0;  // LayerNorm output buffer for float-activation matrices
+    for (auto *w : m->mats) float_act = float_act || is_float_act(w);
+    if (float_act || is_float_act(m->wte)) RC(alloc(m->xn, sizeof(float) * MAXT * C));
+    if (!m->gguf) {  // the head's argmax partials for the device-driven decode loop
+        m->nparts = m->wte->a16 ? gemv_a16_num_parts(m->wte, true) : gguf_num_parts(m->wte);
         RC(alloc(m->parts, sizeof(ArgmaxPart) * m->nparts));
     }
     RC(alloc(m->tokens, sizeof(int64_t) * MAXT));
@@ -730,6 +753,32 @@ int llmq_gpt2_create(llmq_ctx *ctx, const float *const *params, int bits, int gr
 
 int llmq_gpt2_create_ex(llmq_ctx *ctx, const float *const *params, int bits, int group, int sym, int attention,
                         llmq_gpt2 **out) {
+    // E = HEAD8_A16 = QuantMatrix[8, 0, False, True] (gpt2t.mojo:1234).
+    return gpt2_create_formats(ctx, params, QFormat{bits, group, sym ? 1 : 0, 1}, QFormat{8, 0, 0, 1}, attention, out);
+}
+
+int llmq_gpt2_create_fmt(llmq_ctx *ctx, const float *const *params, const char *dtype, const char *head,
+                         int attention, llmq_gpt2 **out) {
+    LLMQ_REQUIRE(dtype && head, "gpt2_create: bad arguments");
+    QFormat w;
+    if (!parse_quant_name(dtype, &w))
+        return llmq_set_error(LLMQ_EUNSUPPORTED, "unknown --dtype %s (a QuantMatrix format: int8-ch, int4-ch, "
+                              "int4-g128, int4-g64, int4-g32, -sym, -a16)", dtype);
+    // run_quantized (gpt2t.mojo:1282-1292): int8 per channel, A16 as the layers, or the layers' own format
+    QFormat e;
+    if (strcmp(head, "int8") == 0)
+        e = QFormat{8, 0, 0, w.a16};
+    else if (strcmp(head, "same") == 0)
+        e = w;
+    else
+        return llmq_set_error(LLMQ_EINVAL, "unknown --head %s (int8 or same)", head);
+    return gpt2_create_formats(ctx, params, w, e, attention, out);
+}
+
+}  // extern "C"
+
+int gpt2_create_formats(llmq_ctx *ctx, const float *const *params, const QFormat &fw, const QFormat &fe,
+                        int attention, llmq_gpt2 **out) {
     LLMQ_REQUIRE(ctx && params && out, "gpt2_create: bad arguments");
     LLMQ_REQUIRE(attention == LLMQ_ATTN_FLOAT || attention == LLMQ_ATTN_INT, "gpt2_create: attention %d", attention);
     llmq_gpt2 *m = new llmq_gpt2();
@@ -741,14 +790,13 @@ int llmq_gpt2_create_ex(llmq_ctx *ctx, const float *const *params, int bits, int
         if (rc != LLMQ_OK) goto fail; \
     } while (0)
     {
-        // E = HEAD8_A16 = QuantMatrix[8, 0, False, True] (gpt2t.mojo:1234).
-        GO(llmq_mat_from_f32(ctx, 8, 0, 0, 1, params[0], V, C, 0, &m->wte));
+        GO(llmq_mat_from_f32(ctx, fe.bits, fe.group, fe.sym, fe.a16, params[0], V, C, 0, &m->wte));
         static const int64_t rows[4] = {C, C, C, 4 * C}, cols[4] = {3 * C, C, 4 * C, C};
         static const int mat_param[4] = {2, 4, 8, 10};
         for (int l = 0; l < NL; l++)
             for (int j = 0; j < 4; j++)
-                GO(llmq_mat_from_f32(ctx, bits, group, sym, 1, params[4 + 12 * l + mat_param[j]], rows[j], cols[j], 1,
-                                     &m->mats[l * 4 + j]));
+                GO(llmq_mat_from_f32(ctx, fw.bits, fw.group, fw.sym, fw.a16, params[4 + 12 * l + mat_param[j]], rows[j],
+                                     cols[j], 1, &m->mats[l * 4 + j]));
         std::vector<float> host((size_t)SMALL_FLOATS);
         int64_t off = 0;
         for (int l = 0; l < NL; l++)
@@ -770,6 +818,8 @@ fail:
     return rc;
 #undef GO
 }
+
+extern "C" {
 
 int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m) {
     if (!m) return 0;

@@ -169,6 +169,19 @@ int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *ro
 int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, const float *KS, const float *VS,
                          int layer, int max_t, int n_head, int n_kv, const float *qkv, int64_t ld, int pos0, int T,
                          float *out, int64_t ldo);
+// QuantMatrix with float activations (A16 = False) runs on the two GGUF
+// float-activation kernels (launch_gguf_gemv, launch_gguf_gemm) as two
+// internal types past the ggml range, over its own device layout (codes
+// [tile][chunk][16 rows][16 B] in natural order, f16 scales and u8 zero
+// points [tile][group][16 rows]).
+constexpr int kQmFloat4 = 1004, kQmFloat8 = 1008;
+inline bool is_float_act(const llmq_mat *w) { return w->kind == MAT_GGUF || (w->kind == MAT_QUANT && !w->a16); }
+inline int float_act_type(const llmq_mat *w) {
+    return w->kind == MAT_GGUF ? w->ggml_type : (w->bits == 8 ? kQmFloat8 : kQmFloat4);
+}
+// log2 of the chunks per group of a QuantMatrix (31 for per-channel: every
+// chunk of a row is group 0); groups are powers of two times 32 otherwise.
+int qm_cpg_shift(const llmq_mat *w);
 // Several-token GGUF matmul on the fp32 matrix cores (gguf_gemm.hip).
 int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t ldx, int64_t T, float *out,
                      int64_t ldo, const float *bias, int flags);

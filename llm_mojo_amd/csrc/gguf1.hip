@@ -38,6 +38,7 @@ struct G1Args {
     const uint8_t *codes, *meta, *bits, *sb, *d6;
     uint32_t codes_bytes, meta_bytes, bits_bytes, sb_bytes, d6_bytes;
     int n, K, ntiles, CK, tmax, flags;
+    int NG, cpg_shift;   // QuantMatrix: group of chunk c of tile t is t * NG + (c >> cpg_shift)
     const float *x, *bias;
     float *out;
     ArgmaxPart *amax;
@@ -80,14 +81,22 @@ __device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__usho
 
 // Type traits: weights per chunk, and the staged per-wave fields (global
 // chunk index >> shift, bytes per (index, row)).
+// QuantMatrix (kQmFloat4 / kQmFloat8): its f16 scales take the place of the
+// meta array and its u8 zero points that of the second staged array; the
+// group index comes from the matrix's own group size (META_SHIFT is the
+// smallest one, a 32-weight group, for the staging bound).
 template <int TYPE>
 struct T1 {
+    static constexpr bool QM = TYPE == kQmFloat4 || TYPE == kQmFloat8;
     static constexpr bool KQ = TYPE == LLMQ_GGML_Q4_K || TYPE == LLMQ_GGML_Q5_K || TYPE == LLMQ_GGML_Q6_K;
-    static constexpr int WPC = TYPE == LLMQ_GGML_Q8_0 ? 16 : 32;
-    static constexpr int META_SHIFT = TYPE == LLMQ_GGML_Q8_0 ? 1 : (KQ ? 3 : 0);
+    static constexpr bool BYTES = TYPE == LLMQ_GGML_Q8_0 || TYPE == kQmFloat8;  // 16 one-byte codes per chunk
+    static constexpr int WPC = BYTES ? 16 : 32;
+    static constexpr int META_SHIFT = BYTES ? 1 : (KQ ? 3 : 0);
     // bytes per (index, row) of the main staged array: meta16 / meta32 / sb16
     static constexpr int META_ESZ = KQ ? 16 : (TYPE == LLMQ_GGML_Q4_1 ? 4 : 2);
     static constexpr int BITS_ESZ = TYPE == LLMQ_GGML_Q5_K ? 4 : (TYPE == LLMQ_GGML_Q6_K ? 8 : 0);  // per chunk
+    // bytes per (index, row) of the second staged array: Q6_K's d, QuantMatrix's zero points
+    static constexpr int D6_ESZ = TYPE == LLMQ_GGML_Q6_K ? 2 : (QM ? 1 : 0);
 };
 
 // Staged bytes per wave: the most indices a wave's 4 * STEPS chunks can
@@ -98,7 +107,7 @@ struct Stage {
     using T = T1<TYPE>;
     static constexpr int IDX = (4 * STEPS >> T::META_SHIFT) + 2;
     static constexpr int LOADS = (IDX * 16 * T::META_ESZ + 1023) / 1024;
-    static constexpr int D6_LOADS = TYPE == LLMQ_GGML_Q6_K ? (IDX * 32 + 1023) / 1024 : 0;
+    static constexpr int D6_LOADS = (IDX * 16 * T::D6_ESZ + 1023) / 1024;
 };
 
 // k_scale_min (gguf.mojo:205-221) of sub-block j over the 12 scale bytes
@@ -209,8 +218,15 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     const int tE = (int)((uint32_t)gE / (uint32_t)S), sE = gE - tE * S;
     const int cg_lo = (t0 + tA) * CK + 4 * sA;
     const int cg_hi = (t0 + tE) * CK + min(4 * sE + 3, CK - 1);
-    const int mi_lo = cg_lo >> T::META_SHIFT;
-    const int mcount = ns > 0 ? (cg_hi >> T::META_SHIFT) - mi_lo + 1 : 1;
+    int mi_lo, mi_hi;
+    if constexpr (T::QM) {  // groups [tile][group]: contiguous over the wave's run as well
+        mi_lo = (t0 + tA) * a.NG + ((4 * sA) >> a.cpg_shift);
+        mi_hi = (t0 + tE) * a.NG + (min(4 * sE + 3, CK - 1) >> a.cpg_shift);
+    } else {
+        mi_lo = cg_lo >> T::META_SHIFT;
+        mi_hi = cg_hi >> T::META_SHIFT;
+    }
+    const int mcount = ns > 0 ? mi_hi - mi_lo + 1 : 1;
     const auto rm = make_rsrc(T::KQ ? a.sb : a.meta, T::KQ ? a.sb_bytes : a.meta_bytes);
     uint4 wm[St::LOADS];
 #pragma unroll
@@ -224,7 +240,8 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
 #pragma unroll
         for (int i = 0; i < St::D6_LOADS; i++) {
             const uint32_t off = (uint32_t)(i * 1024 + lane * 16);
-            wd6[i] = bload16(rd, off < (uint32_t)(mcount * 32) ? (uint32_t)mi_lo * 32u + off : kOOB);
+            wd6[i] = bload16(rd, off < (uint32_t)(mcount * 16 * T::D6_ESZ) ? (uint32_t)mi_lo * 16u * T::D6_ESZ + off
+                                                                            : kOOB);
         }
     }
     const uint32_t offA = ((uint32_t)(t0 + tA) * (uint32_t)CK + 4u * (uint32_t)sA) * 16u;  // chunk-row index
@@ -324,9 +341,16 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
             const int c_raw = 4 * ss + j;
             const bool ok = c_raw < CK;
             const int c = ok ? c_raw : 0;
-            const int mi = ok ? (((t0 + tl) * CK + c) >> T::META_SHIFT) - mi_lo : 0;
+            int mi;
+            if constexpr (T::QM)
+                mi = ok ? (t0 + tl) * a.NG + (c >> a.cpg_shift) - mi_lo : 0;
+            else
+                mi = ok ? (((t0 + tl) * CK + c) >> T::META_SHIFT) - mi_lo : 0;
             float pA, pB, qA, qB;
-            if (TYPE == LLMQ_GGML_Q4_0 || TYPE == LLMQ_GGML_Q8_0) {
+            if (T::QM) {  // s * (a - zp * S) over the chunk: pA = s, qA = -zp
+                pA = pB = h2f(reinterpret_cast<const uint16_t *>(s_meta[wid])[mi * 16 + r]);
+                qA = qB = -(float)s_d6[wid][mi * 16 + r];
+            } else if (TYPE == LLMQ_GGML_Q4_0 || TYPE == LLMQ_GGML_Q8_0) {
                 const float d = h2f(reinterpret_cast<const uint16_t *>(s_meta[wid])[mi * 16 + r]);
                 pA = pB = d;
                 qA = qB = (TYPE == LLMQ_GGML_Q4_0 ? -8.0f : -128.0f) * d;
@@ -352,12 +376,13 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
             const uint4 d4 = wc[u];
             const float4 *xc = reinterpret_cast<const float4 *>(xs + c * WPC);
             float aA = 0.0f, aB = 0.0f, SA, SB;
-            if (TYPE == LLMQ_GGML_Q8_0) {
-                // 16 int8 codes: bytes as q + 128
-                aA = dot4b(d4.x ^ 0x80808080u, xc[0], aA);
-                aA = dot4b(d4.y ^ 0x80808080u, xc[1], aA);
-                aA = dot4b(d4.z ^ 0x80808080u, xc[2], aA);
-                aA = dot4b(d4.w ^ 0x80808080u, xc[3], aA);
+            if (T::BYTES) {
+                // 16 one-byte codes: Q8_0's int8 as q + 128, QuantMatrix's u8 as they are
+                const uint32_t flip = TYPE == LLMQ_GGML_Q8_0 ? 0x80808080u : 0u;
+                aA = dot4b(d4.x ^ flip, xc[0], aA);
+                aA = dot4b(d4.y ^ flip, xc[1], aA);
+                aA = dot4b(d4.z ^ flip, xc[2], aA);
+                aA = dot4b(d4.w ^ flip, xc[3], aA);
                 SA = xsum16[c];
                 SB = 0.0f;
             } else {
@@ -392,7 +417,9 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
                 SA = xsum16[2 * c];
                 SB = xsum16[2 * c + 1];
             }
-            const float contrib = (pA * aA + qA * SA) + (pB * aB + qB * SB);
+            // QuantMatrix's chunk lies in one group: s * (a - zp S), the
+            // zero-point product exact inside the FMA
+            const float contrib = T::QM ? pA * fmaf(qA, SA + SB, aA + aB) : (pA * aA + qA * SA) + (pB * aB + qB * SB);
             accA += second ? 0.0f : contrib;
             accB += second ? contrib : 0.0f;
         }
@@ -460,7 +487,10 @@ struct Plan {
 };
 
 int steps_for(int spw) { return spw <= 2 ? 2 : spw <= 4 ? 4 : spw <= 8 ? 8 : 16; }
-int max_steps(const llmq_mat *w) { return w->ggml_type == LLMQ_GGML_Q8_0 ? 2 * kMaxSteps : kMaxSteps; }
+int max_steps(const llmq_mat *w) {
+    const int t = float_act_type(w);
+    return t == LLMQ_GGML_Q8_0 || t == kQmFloat8 ? 2 * kMaxSteps : kMaxSteps;
+}
 
 // As the one-token integer kernel's plan: 4-wave workgroups of one tile for
 // small matrices, else one 16-wave workgroup per CU with whole-tile runs.
@@ -524,7 +554,7 @@ int launch_type(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
         if (p.steps == 2) return launch_t<TYPE, 16, 2>(ctx, a, p, lds);
         if (p.steps == 4) return launch_t<TYPE, 16, 4>(ctx, a, p, lds);
         if (p.steps == 8) return launch_t<TYPE, 16, 8>(ctx, a, p, lds);
-        if constexpr (TYPE == LLMQ_GGML_Q8_0)
+        if constexpr (T1<TYPE>::BYTES)
             if (p.steps == 16) return launch_t<TYPE, 16, 16>(ctx, a, p, lds);
     }
     return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf_gemv: no kernel for %d waves x %d steps", p.nw, p.steps);
@@ -532,11 +562,18 @@ int launch_type(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
 
 }  // namespace
 
+int qm_cpg_shift(const llmq_mat *w) {
+    if (w->NG == 1) return 31;  // per-channel: every chunk is group 0
+    const int64_t cpg = w->group / (w->bits == 4 ? 32 : 16);  // chunks per group
+    if ((cpg & (cpg - 1)) != 0) return -1;
+    return __builtin_ctzll((unsigned long long)cpg);
+}
+
 int gguf_num_parts(const llmq_mat *w) { return make_plan(w).grid; }
 
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
                      ArgmaxPart *amax, int amax_cap, const float *rms_g, float rms_eps, int swiglu) {
-    LLMQ_REQUIRE(w && w->kind == MAT_GGUF, "gguf_gemv: not a GGUF matrix");
+    LLMQ_REQUIRE(w && is_float_act(w), "gguf_gemv: not a GGUF or float-activation QuantMatrix");
     LLMQ_REQUIRE(x && out, "gguf_gemv: null pointer");
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemv: LLMQ_BIAS without a bias");
     LLMQ_REQUIRE(w->k % 16 == 0, "gguf_gemv: cols must be a multiple of 16");
@@ -548,16 +585,28 @@ int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *ou
     const int64_t ntc = (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 16;  // (chunk, row) entries incl. padding
     const int64_t nts = (w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 16;  // (superblock, row) entries
     G1Args a{};
+    const int type = float_act_type(w);
     a.codes = w->codes;
     a.codes_bytes = (uint32_t)(ntc * 16);
-    a.meta = reinterpret_cast<const uint8_t *>(w->ggml_type == LLMQ_GGML_Q4_1 ? w->g_meta32 : w->g_meta16);
-    a.meta_bytes = (uint32_t)(w->ggml_type == LLMQ_GGML_Q4_1 ? ntc * 4 : ntc * 2);
-    a.bits = reinterpret_cast<const uint8_t *>(w->ggml_type == LLMQ_GGML_Q6_K ? w->g_bits64 : w->g_bits32);
-    a.bits_bytes = (uint32_t)(w->ggml_type == LLMQ_GGML_Q6_K ? ntc * 8 : ntc * 4);
-    a.sb = reinterpret_cast<const uint8_t *>(w->g_sb16);
-    a.sb_bytes = (uint32_t)(nts * 16);
-    a.d6 = reinterpret_cast<const uint8_t *>(w->g_meta16);
-    a.d6_bytes = (uint32_t)(nts * 2);
+    if (w->kind == MAT_QUANT) {
+        const int64_t ntg = (w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 16;  // (group, row) entries incl. padding
+        a.meta = reinterpret_cast<const uint8_t *>(w->scales);
+        a.meta_bytes = (uint32_t)(ntg * 2);
+        a.d6 = w->zps;
+        a.d6_bytes = (uint32_t)ntg;
+        a.NG = (int)w->NG;
+        a.cpg_shift = qm_cpg_shift(w);
+        LLMQ_REQUIRE(a.cpg_shift >= 0, "linear: group %lld is not a power of two times 32", (long long)w->group);
+    } else {
+        a.meta = reinterpret_cast<const uint8_t *>(w->ggml_type == LLMQ_GGML_Q4_1 ? w->g_meta32 : w->g_meta16);
+        a.meta_bytes = (uint32_t)(w->ggml_type == LLMQ_GGML_Q4_1 ? ntc * 4 : ntc * 2);
+        a.bits = reinterpret_cast<const uint8_t *>(w->ggml_type == LLMQ_GGML_Q6_K ? w->g_bits64 : w->g_bits32);
+        a.bits_bytes = (uint32_t)(w->ggml_type == LLMQ_GGML_Q6_K ? ntc * 8 : ntc * 4);
+        a.sb = reinterpret_cast<const uint8_t *>(w->g_sb16);
+        a.sb_bytes = (uint32_t)(nts * 16);
+        a.d6 = reinterpret_cast<const uint8_t *>(w->g_meta16);
+        a.d6_bytes = (uint32_t)(nts * 2);
+    }
     a.n = (int)w->n;
     a.K = (int)w->k;
     a.ntiles = (int)w->ntiles;
@@ -572,14 +621,16 @@ int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *ou
     a.rms_eps = rms_eps;
     a.swiglu = swiglu;
     int rc;
-    switch (w->ggml_type) {
+    switch (type) {
+    case kQmFloat4: rc = launch_type<kQmFloat4>(ctx, a, p, lds); break;
+    case kQmFloat8: rc = launch_type<kQmFloat8>(ctx, a, p, lds); break;
     case LLMQ_GGML_Q4_0: rc = launch_type<LLMQ_GGML_Q4_0>(ctx, a, p, lds); break;
     case LLMQ_GGML_Q4_1: rc = launch_type<LLMQ_GGML_Q4_1>(ctx, a, p, lds); break;
     case LLMQ_GGML_Q8_0: rc = launch_type<LLMQ_GGML_Q8_0>(ctx, a, p, lds); break;
     case LLMQ_GGML_Q4_K: rc = launch_type<LLMQ_GGML_Q4_K>(ctx, a, p, lds); break;
     case LLMQ_GGML_Q5_K: rc = launch_type<LLMQ_GGML_Q5_K>(ctx, a, p, lds); break;
     case LLMQ_GGML_Q6_K: rc = launch_type<LLMQ_GGML_Q6_K>(ctx, a, p, lds); break;
-    default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf_gemv: type %d", w->ggml_type);
+    default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf_gemv: type %d", type);
     }
     if (rc != LLMQ_OK) return rc;
     LLMQ_HIP(hipGetLastError());

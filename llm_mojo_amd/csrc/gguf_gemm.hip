@@ -26,6 +26,7 @@ struct GArgs {
     const uint8_t *codes, *meta, *bits, *sb;
     uint32_t codes_bytes, meta_bytes, bits_bytes, sb_bytes, x_bytes;
     int n, K, CK, NSB, T, flags;
+    int NG, cpg_shift;   // QuantMatrix: meta = f16 scales, bits = u8 zero points per (group, row)
     int64_t ldx, ldo;
     const float *x, *bias;
     float *out;
@@ -78,6 +79,21 @@ __device__ __forceinline__ void decode_chunk(const GArgs &a, uint32_t tile, uint
     const uint32_t e = (tile * (uint32_t)a.CK + c) * 16u + r;  // (chunk, row) entry
     const uint4 q4 = bload16(rc, ok ? e * 16u : kOOB);
     const uint32_t dw[4] = {q4.x, q4.y, q4.z, q4.w};
+    if (TYPE == kQmFloat4 || TYPE == kQmFloat8) {
+        // QuantMatrix.row_op (tensor.mojo:431-479): (f32(u) - f32(zp)) * f32(scale)
+        const uint32_t gi = (tile * (uint32_t)a.NG + (c >> a.cpg_shift)) * 16u + r;
+        const float s = h2f(bload_h(rm, gi, ok));
+        const uint32_t zw = bload4(make_rsrc(a.bits, a.bits_bytes), ok ? gi & ~3u : kOOB);
+        const float zp = (float)((zw >> (8 * (gi & 3u))) & 255u);
+        if (TYPE == kQmFloat8) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) w[i] = ((float)((dw[i >> 2] >> (8 * (i & 3))) & 255u) - zp) * s;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; i++) w[i] = ((float)((dw[i >> 3] >> (4 * (i & 7))) & 15u) - zp) * s;
+        }
+        return;
+    }
     if (TYPE == LLMQ_GGML_Q8_0) {
         const float d = h2f(bload_h(rm, (tile * (uint32_t)(a.CK / 2) + (c >> 1)) * 16u + r, ok));
 #pragma unroll
@@ -141,7 +157,7 @@ __device__ __forceinline__ float gelu_f(float r) {
 
 template <int TYPE, int NW>
 __global__ __launch_bounds__(NW * 64) void gguf_gemm_kernel(GArgs a) {
-    constexpr int WPC = TYPE == LLMQ_GGML_Q8_0 ? 16 : 32;
+    constexpr int WPC = TYPE == LLMQ_GGML_Q8_0 || TYPE == kQmFloat8 ? 16 : 32;
     __shared__ float part[NW][256];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -206,7 +222,7 @@ int launch_t(llmq_ctx *ctx, const GArgs &a, dim3 grid, int nw) {
 
 int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t ldx, int64_t T, float *out,
                      int64_t ldo, const float *bias, int flags) {
-    LLMQ_REQUIRE(w && w->kind == MAT_GGUF, "gguf_gemm: not a GGUF matrix");
+    LLMQ_REQUIRE(w && is_float_act(w), "gguf_gemm: not a GGUF or float-activation QuantMatrix");
     LLMQ_REQUIRE(x && out && T > 0, "gguf_gemm: bad arguments");
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemm: LLMQ_BIAS without a bias");
     LLMQ_REQUIRE(w->k % 32 == 0, "gguf_gemm: cols must be a multiple of 32");
@@ -215,10 +231,17 @@ int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t l
     LLMQ_REQUIRE(ntc * 16 < (int64_t)kOOB && T * ldx * 4 < (int64_t)kOOB, "gguf_gemm: operands too large");
     LLMQ_REQUIRE(T <= 16 * 65535LL, "gguf_gemm: too many tokens");
     GArgs a{};
-    const int t = w->ggml_type;
+    const int t = float_act_type(w);
     a.codes = w->codes;
     a.codes_bytes = (uint32_t)(ntc * 16);
-    if (t == LLMQ_GGML_Q4_1) {
+    if (w->kind == MAT_QUANT) {
+        const int64_t ntg = (w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 16;  // (group, row) entries incl. padding
+        a.meta = reinterpret_cast<const uint8_t *>(w->scales);
+        a.meta_bytes = (uint32_t)(ntg * 2);
+        a.NG = (int)w->NG;
+        a.cpg_shift = qm_cpg_shift(w);
+        LLMQ_REQUIRE(a.cpg_shift >= 0, "linear: group %lld is not a power of two times 32", (long long)w->group);
+    } else if (t == LLMQ_GGML_Q4_1) {
         a.meta = reinterpret_cast<const uint8_t *>(w->g_meta32);
         a.meta_bytes = (uint32_t)(ntc * 4);
     } else if (t == LLMQ_GGML_Q6_K) {
@@ -230,6 +253,10 @@ int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t l
     }
     a.bits = reinterpret_cast<const uint8_t *>(t == LLMQ_GGML_Q6_K ? w->g_bits64 : w->g_bits32);
     a.bits_bytes = (uint32_t)(t == LLMQ_GGML_Q6_K ? ntc * 8 : (t == LLMQ_GGML_Q5_K ? ntc * 4 : 0));
+    if (w->kind == MAT_QUANT) {
+        a.bits = w->zps;
+        a.bits_bytes = (uint32_t)((w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 16);
+    }
     a.sb = reinterpret_cast<const uint8_t *>(w->g_sb16);
     a.sb_bytes = w->g_sb16 ? (uint32_t)(nts * 16) : 0u;
     a.n = (int)w->n;
@@ -248,6 +275,8 @@ int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t l
     const int nw = nblk >= 8 ? 8 : 4;
     dim3 grid((unsigned)w->ntiles, (unsigned)((T + 15) / 16));
     switch (t) {
+    case kQmFloat4: return launch_t<kQmFloat4>(ctx, a, grid, nw);
+    case kQmFloat8: return launch_t<kQmFloat8>(ctx, a, grid, nw);
     case LLMQ_GGML_Q4_0: return launch_t<LLMQ_GGML_Q4_0>(ctx, a, grid, nw);
     case LLMQ_GGML_Q4_1: return launch_t<LLMQ_GGML_Q4_1>(ctx, a, grid, nw);
     case LLMQ_GGML_Q8_0: return launch_t<LLMQ_GGML_Q8_0>(ctx, a, grid, nw);

@@ -3,6 +3,8 @@
 // (74-81) and the small float tensors follow Model.small's order
 // (gpt2t.mojo:108-119, 574-576).
 #pragma once
+#include <string>
+
 #include "common.h"
 
 namespace {
@@ -41,6 +43,23 @@ struct llmq_gpt2 {
     float *xn = nullptr;
 };
 
+// A QuantMatrix format: QuantMatrix[bits, group (0: per channel), sym, A16].
+struct QFormat {
+    int bits = 0, group = 0, sym = 0, a16 = 0;
+    bool operator==(const QFormat &o) const {
+        return bits == o.bits && group == o.group && sym == o.sym && a16 == o.a16;
+    }
+};
+// QuantMatrix.name() (tensor.mojo:326-331): int{4,8}-{ch,g<G>}[-sym][-a16].
+std::string quant_name(const QFormat &f);
+// The format a name denotes (the inverse of quant_name); false for any other
+// name (model_io.hip).
+bool parse_quant_name(const std::string &s, QFormat *f);
+// Model[W, E] from the Hugging Face float32 tensors with layers in format w
+// and the tied embedding / head in format e (run_quantized's W and E,
+// gpt2t.mojo:1282-1292, 1231-1235); params as llmq_gpt2_create (api.hip).
+int gpt2_create_formats(llmq_ctx *ctx, const float *const *params, const QFormat &w, const QFormat &e,
+                        int attention, llmq_gpt2 **out);
 // The GGUF model's forward (gpt2_gguf.hip): tokens already in m->tokens.
 int gpt2g_enqueue(llmq_gpt2 *m, int T, int pos0, bool with_head = true);
 

@@ -16,11 +16,38 @@
 
 #include "gpt2.h"
 
+std::string quant_name(const QFormat &f) {
+    std::string s = "int" + std::to_string(f.bits) + "-" + (f.group == 0 ? std::string("ch") : "g" + std::to_string(f.group));
+    if (f.sym) s += "-sym";
+    return f.a16 ? s + "-a16" : s;
+}
+
+bool parse_quant_name(const std::string &s, QFormat *f) {
+    for (int b : {4, 8}) {
+        const std::string pre = "int" + std::to_string(b) + "-";
+        if (s.rfind(pre, 0) != 0) continue;
+        int g = 0;
+        if (s.compare(pre.size(), 2, "ch") != 0) {
+            if (s.size() <= pre.size() + 1 || s[pre.size()] != 'g') continue;
+            g = atoi(s.c_str() + pre.size() + 1);
+            if (g <= 0) continue;
+        }
+        for (int sy = 0; sy < 2; sy++)
+            for (int a = 0; a < 2; a++) {
+                const QFormat q{b, g, sy, a};
+                if (quant_name(q) == s) {
+                    *f = q;
+                    return true;
+                }
+            }
+    }
+    return false;
+}
+
 namespace {
 
 const char kMagic[] = "llm_mojo GPT-2 124M weights";  // gpt2t.mojo:621
 constexpr int64_t kVersion = 1;                        // gpt2t.mojo:622
-const char kHeadName[] = "int8-ch-a16";                // HEAD8_A16 (gpt2t.mojo:1234)
 
 struct Writer {  // ByteWriter (serialize.mojo:18-57)
     FILE *f = nullptr;
@@ -76,36 +103,6 @@ struct FileCloser {
     }
 };
 
-// QuantMatrix.name (tensor.mojo:325-331).
-std::string quant_name(int bits, int group, int sym, int a16) {
-    std::string s = "int" + std::to_string(bits) + "-" + (group == 0 ? std::string("ch") : "g" + std::to_string(group));
-    if (sym) s += "-sym";
-    return a16 ? s + "-a16" : s;
-}
-
-// The format parameters of a QuantMatrix name the device model runs
-// (QuantMatrix[4 or 8, group, sym, A16=True]); false for any other name.
-bool parse_quant_name(const std::string &s, int *bits, int *group, int *sym) {
-    for (int b : {4, 8})
-        for (int sy = 0; sy < 2; sy++) {
-            const std::string pre = "int" + std::to_string(b) + "-";
-            if (s.rfind(pre, 0) != 0) continue;
-            int g = 0;
-            if (s.compare(pre.size(), 2, "ch") != 0) {
-                if (s.size() <= pre.size() + 1 || s[pre.size()] != 'g') continue;
-                g = atoi(s.c_str() + pre.size() + 1);
-                if (g <= 0) continue;
-            }
-            if (quant_name(b, g, sy, 1) == s) {
-                *bits = b;
-                *group = g;
-                *sym = sy;
-                return true;
-            }
-        }
-    return false;
-}
-
 // QuantMatrix.save (tensor.mojo:634-644).
 int save_mat(Writer &w, llmq_ctx *ctx, const llmq_mat *m) {
     const int64_t groups = m->n * (m->k / m->group);
@@ -123,8 +120,8 @@ int save_mat(Writer &w, llmq_ctx *ctx, const llmq_mat *m) {
 
 // QuantMatrix.restore (tensor.mojo:646-656) into the device layout; the
 // shape must be the one the model expects.
-int restore_mat(Reader &r, llmq_ctx *ctx, int bits, int group, int sym, int64_t want_rows, int64_t want_cols,
-                llmq_mat **out) {
+int restore_mat(Reader &r, llmq_ctx *ctx, const QFormat &f, int64_t want_rows, int64_t want_cols, llmq_mat **out) {
+    const int bits = f.bits, group = f.group;
     int64_t rows, cols, g;
     RC(r.i64(&rows));
     RC(r.i64(&cols));
@@ -141,7 +138,7 @@ int restore_mat(Reader &r, llmq_ctx *ctx, int bits, int group, int sym, int64_t 
     RC(r.fill(codes.data(), codes.size()));
     RC(r.fill(scales.data(), scales.size() * 2));
     RC(r.fill(zps.data(), zps.size()));
-    return llmq_mat_restore(ctx, bits, group, sym, 1, rows, cols, codes.data(), scales.data(), zps.data(), out);
+    return llmq_mat_restore(ctx, bits, group, f.sym, f.a16, rows, cols, codes.data(), scales.data(), zps.data(), out);
 }
 
 // check_magic (gpt2t.mojo:653-661), then the two format names.
@@ -174,8 +171,9 @@ int llmq_gpt2_save(llmq_gpt2 *m, const char *path) {
     const llmq_mat *l0 = m->mats[0];
     w.str(kMagic);
     w.i64(kVersion);
-    w.str(quant_name(l0->bits, l0->group_param, l0->sym, l0->a16));
-    w.str(kHeadName);
+    const llmq_mat *e = m->wte;
+    w.str(quant_name(QFormat{l0->bits, l0->group_param, l0->sym, l0->a16}));
+    w.str(quant_name(QFormat{e->bits, e->group_param, e->sym, e->a16}));
     RC(save_mat(w, m->ctx, m->wte));
     for (const llmq_mat *q : m->mats) RC(save_mat(w, m->ctx, q));
     std::vector<float> small((size_t)SMALL_FLOATS);
@@ -217,16 +215,21 @@ int llmq_gpt2_load(llmq_ctx *ctx, const char *path, int attention, llmq_gpt2 **o
     r.path = path;
     std::string layers, head;
     RC(read_header(r, &layers, &head));
-    int bits, group, sym;
-    if (!parse_quant_name(layers, &bits, &group, &sym) || head != kHeadName)
-        return llmq_set_error(LLMQ_EUNSUPPORTED, "%s holds %s + head %s; the device model runs QuantMatrix "
-                              "A16 layers (int4 / int8) + head %s", path, layers.c_str(), head.c_str(), kHeadName);
+    // main's --weights (gpt2t.mojo:1298-1303): the head is "same" when both
+    // names agree, else int8 per channel (HEAD8 or HEAD8_A16 as W is A16)
+    QFormat fw, fe;
+    const bool ok = parse_quant_name(layers, &fw) && parse_quant_name(head, &fe) &&
+                    (fe == fw || fe == QFormat{8, 0, 0, fw.a16});
+    if (!ok)
+        return llmq_set_error(LLMQ_EUNSUPPORTED, "%s holds %s + head %s; the device model runs QuantMatrix layers "
+                              "with head int8-ch (-a16 as the layers) or the layers' own format", path,
+                              layers.c_str(), head.c_str());
     llmq_gpt2 *m = new llmq_gpt2();
     m->ctx = ctx;
-    int rc = restore_mat(r, ctx, 8, 0, 0, V, C, &m->wte);
+    int rc = restore_mat(r, ctx, fe, V, C, &m->wte);
     static const int64_t rows[4] = {3 * C, C, 4 * C, C}, cols[4] = {C, C, C, 4 * C};  // [OUT, IN]
     for (int i = 0; rc == LLMQ_OK && i < NL * 4; i++)
-        rc = restore_mat(r, ctx, bits, group, sym, rows[i % 4], cols[i % 4], &m->mats[i]);
+        rc = restore_mat(r, ctx, fw, rows[i % 4], cols[i % 4], &m->mats[i]);
     std::vector<float> small;
     if (rc == LLMQ_OK) {
         int64_t n = 0;

@@ -1,10 +1,12 @@
 """GPT-2 124M on libllmq.so: the caller of the quantized path
 (gpt2t.mojo Model / load_model / generate, 198-609, 929-1009).
 
-Layers are QuantMatrix[bits, group, sym, A16=True] (int4-g32-a16 by default),
-the tied embedding / head HEAD8_A16, the cache QuantKV[8], all resident on
-one GPU.  Greedy generation runs on the device: each step's argmax picks the
-next token without a round trip to the host.
+Layers are QuantMatrix[bits, group, sym, A16] (int4-g32-a16 by default; any
+of gpt2t.mojo's quantized --dtype names), the tied embedding / head int8 per
+channel (HEAD8_A16 / HEAD8) or the layers' format (--head same), the cache
+QuantKV[8] or IntAttnKV, all resident on one GPU.  Greedy generation runs on
+the device: each step's argmax picks the next token without a round trip to
+the host.
 """
 import ctypes
 import os
@@ -71,22 +73,51 @@ def saved_formats(path):
     return a.value.decode(), b.value.decode()
 
 
-class GPT2:
-    """Model[W = QuantMatrix[bits, group, sym, A16], E = HEAD8_A16, KV], with
-    KV = QuantKV[8] for attention="float" and IntAttnKV for "int" (gpt2t.mojo's
-    --attention, 1251-1257)."""
+def quant_name(bits, group, sym, a16):
+    """QuantMatrix.name (tensor.mojo:326-331)."""
+    g = "ch" if group == 0 else f"g{group}"
+    return f"int{bits}-{g}" + ("-sym" if sym else "") + ("-a16" if a16 else "")
 
-    def __init__(self, ctx, tensors, bits=4, group=32, sym=False, attention="float"):
+
+def head_format(dtype, head):
+    """run_quantized's E (gpt2t.mojo:1282-1292): "int8" is HEAD8_A16 for -a16
+    layers and HEAD8 otherwise; "same" is the layers' format."""
+    if head == "int8":
+        return "int8-ch-a16" if dtype.endswith("-a16") else "int8-ch"
+    if head == "same":
+        return dtype
+    raise ValueError(f"unknown --head {head} (int8 or same)")
+
+
+class GPT2:
+    """Model[W, E, KV] with W = QuantMatrix[bits, group, sym, A16] (dtype names
+    it as gpt2t.mojo's --dtype does, 1307-1348; else bits / group / sym with
+    A16), E chosen by head as --head does, KV = QuantKV[8] for
+    attention="float" and IntAttnKV for "int" (--attention, 1251-1257)."""
+
+    def __init__(self, ctx, tensors, bits=4, group=32, sym=False, attention="float", dtype=None, head="int8"):
         if attention not in ATTENTION:
             raise ValueError(f"unknown --attention {attention} (float or int)")
+        if dtype is None:
+            dtype = quant_name(bits, group, sym, True)
+        head_fmt = head_format(dtype, head)
         self.ctx = ctx
         params = params_list(tensors)
         arr = (ctypes.c_void_p * len(params))(*[p.ctypes.data for p in params])
         h = ctypes.c_void_p()
-        check(lib().llmq_gpt2_create_ex(ctx.h, arr, bits, group, 1 if sym else 0, ATTENTION[attention],
-                                        ctypes.byref(h)))
+        check(lib().llmq_gpt2_create_fmt(ctx.h, arr, dtype.encode(), head.encode(), ATTENTION[attention],
+                                         ctypes.byref(h)))
         self.h = h
-        self.bits, self.group, self.sym, self.attention = bits, group, sym, attention
+        self.attention = attention
+        self._set_formats(dtype, head_fmt)
+
+    def _set_formats(self, dtype, head_fmt):
+        self.dtype, self.head_fmt = dtype, head_fmt
+        self.bits = int(dtype[3])
+        g = dtype.split("-")[1]
+        self.group = 0 if g == "ch" else int(g[1:])
+        self.sym = "-sym" in dtype
+        self.a16 = dtype.endswith("-a16")
 
     @classmethod
     def load(cls, ctx, path, attention="float"):
@@ -98,11 +129,7 @@ class GPT2:
         check(lib().llmq_gpt2_load(ctx.h, os.fsencode(path), ATTENTION[attention], ctypes.byref(h)))
         self = cls.__new__(cls)
         self.ctx, self.h, self.attention = ctx, h, attention
-        layers, _ = saved_formats(path)
-        self.bits = int(layers[3])
-        g = layers.split("-")[1]
-        self.group = 0 if g == "ch" else int(g[1:])
-        self.sym = "-sym" in layers
+        self._set_formats(*saved_formats(path))
         return self
 
     @classmethod
@@ -115,7 +142,7 @@ class GPT2:
         check(lib().llmq_gpt2_load_gguf(ctx.h, os.fsencode(path), ATTENTION[attention], ctypes.byref(h)))
         self = cls.__new__(cls)
         self.ctx, self.h, self.attention = ctx, h, attention
-        self.bits = self.group = self.sym = None
+        self.dtype = self.head_fmt = self.bits = self.group = self.sym = self.a16 = None
         return self
 
     def save(self, path):
@@ -126,11 +153,10 @@ class GPT2:
     def name(self):
         """model_name (gpt2t.mojo:1222-1228)."""
         kv = "int8-intattn" if self.attention == "int" else "int8"
-        if self.bits is None:  # GGUFMatrix layers and head (gguf.mojo:374-375)
+        if self.dtype is None:  # GGUFMatrix layers and head (gguf.mojo:374-375)
             return "gguf+kv-" + kv
-        g = "ch" if self.group == 0 else f"g{self.group}"
-        w = f"int{self.bits}-{g}" + ("-sym" if self.sym else "") + "-a16"
-        return w + "+head-int8-ch-a16+kv-" + ("int8-intattn" if self.attention == "int" else "int8")
+        n = self.dtype if self.head_fmt == self.dtype else self.dtype + "+head-" + self.head_fmt
+        return n + "+kv-" + kv
 
     def weight_bytes(self):
         return lib().llmq_gpt2_weight_bytes(self.h)

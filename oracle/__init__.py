@@ -86,6 +86,7 @@ def _declare(L):
         "orc_qm_nbytes": (I64, [P]),
         "orc_qm_dequant_row": (None, [P, I64, P]),
         "orc_qm_dot_row": (ctypes.c_float, [P, I64, P]),
+        "orc_qm_matmul_rows": (None, [P, P, P, P, I64, I64, I64, I32]),
         "orc_qm_permute_x_i16": (I32, [P, P, I64, P, P]),
         "orc_qm_dot_row_i16": (ctypes.c_float, [P, I64, P, P]),
         "orc_qm_unpack_row_i16": (None, [P, I64, P, P]),
@@ -116,6 +117,7 @@ def _declare(L):
         "orc_rng_uniform": (ctypes.c_float, [P]),
         "orc_argmax": (I64, [P, I64]),
         "orc_gpt2_new": (P, [P, I32, I32, I32]),
+        "orc_gpt2_new_fmt": (P, [P, I32, I32, I32, I32, I32, I32, I32, I32]),
         "orc_gpt2_free": (None, [P]),
         "orc_gpt2_set_attention": (None, [P, I32]),
         "orc_gpt2_forward_all": (None, [P, P, I32, P]),
@@ -272,6 +274,20 @@ def matmul_rows_a16(x, w, b=None, flags=EPI_BIAS, out=None):
         b = np.zeros(w.n, np.float32)
     b = np.ascontiguousarray(b, np.float32)
     lib().orc_matmul_rows_a16(ptr(out), ptr(x), w.ref, ptr(b), T, IN, w.n, flags)
+    return out
+
+
+def matmul_rows(x, w, b=None, flags=EPI_BIAS, out=None):
+    """out[T, OUT] (+)= act(x @ w^T + b) as kernels.matmul_rows over a
+    QuantMatrix with A16 = False (float activations)."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, IN = x.shape
+    if out is None:
+        out = np.zeros((T, w.n), np.float32)
+    if b is None:
+        b = np.zeros(w.n, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    lib().orc_qm_matmul_rows(ptr(out), ptr(x), w.ref, ptr(b), T, IN, w.n, flags)
     return out
 
 
@@ -633,10 +649,14 @@ class GPT2:
     HEAD8_A16 head, QuantKV[8], or IntAttnKV with attention="int") on the
     CPU."""
 
-    def __init__(self, params, bits=4, group=32, sym=False, attention="float"):
+    def __init__(self, params, bits=4, group=32, sym=False, attention="float", a16=True, head=None):
+        """head: (bits, group, sym, a16) of E; None for the int8 per-channel
+        head with the layers' A16 (run_quantized's --head int8)."""
         self._keep = [np.ascontiguousarray(p, np.float32) for p in params]
         arr = (ctypes.c_void_p * len(self._keep))(*[p.ctypes.data for p in self._keep])
-        self.h = lib().orc_gpt2_new(arr, bits, group, 1 if sym else 0)
+        e = head if head is not None else (8, 0, False, a16)
+        self.h = lib().orc_gpt2_new_fmt(arr, bits, group, 1 if sym else 0, 1 if a16 else 0, e[0], e[1],
+                                        1 if e[2] else 0, 1 if e[3] else 0)
         self._keep = None  # the model copied what it keeps
         # --attention int (gpt2t.mojo:1251-1257): IntAttnKV
         lib().orc_gpt2_set_attention(self.h, 1 if attention == "int" else 0)

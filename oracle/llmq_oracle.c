@@ -796,6 +796,50 @@ void orc_gguf_unpack_row_i16(int t, const uint8_t *p, int64_t cols, int16_t *dst
     }
 }
 
+/* matmul_rows (kernels.mojo:285-349) over a QuantMatrix with A16 = 0
+ * (OUT_MAJOR, tensor.mojo:293; linear's branch, kernels.mojo:670-671):
+ * out[T, OUT] (+)= act(x @ w^T + b).  T == 1: dot_row (row_op) + b, finish
+ * (301-312).  T > 1: tiles of TN = 32 rows dequantized (dequant_row) and
+ * multiplied by mm_tile (52-85: one float32 FMA chain over i per output,
+ * then + b, store_out); the last OUT % 32 rows by rows_dot (352-397: 16-lane
+ * FMA partials over i, reduce_add, + b).  The vector width is taken as 16
+ * lanes (simd_width_of[float32] with AVX-512). */
+void orc_qm_matmul_rows(float *out, const float *x, const orc_qm *w, const float *b, int64_t T, int64_t IN,
+                        int64_t OUT, int flags) {
+    if (T == 1) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+        for (int64_t o = 0; o < OUT; o++) {
+            float r = orc_qm_dot_row(w, o, x);
+            if (flags & EPI_BIAS) r += b[o];
+            finish(out, o, r, flags);
+        }
+        return;
+    }
+    const int64_t TN = 32, full = OUT / TN;
+#pragma omp parallel for schedule(dynamic) num_threads(g_threads) if (g_threads > 1)
+    for (int64_t o = 0; o < OUT; o++) {
+        float *row = (float *)malloc(sizeof(float) * (size_t)IN);
+        orc_qm_dequant_row(w, o, row);
+        const float bias = (flags & EPI_BIAS) ? b[o] : 0.0f;
+        for (int64_t t = 0; t < T; t++) {
+            const float *xt = x + t * IN;
+            float r;
+            if (o < full * TN) { /* mm_tile */
+                r = 0.0f;
+                for (int64_t i = 0; i < IN; i++) r = fmaf(xt[i], row[i], r);
+                r += bias;
+            } else { /* rows_dot */
+                float d[L16] = {0};
+                for (int64_t i = 0; i < IN; i += L16)
+                    for (int l = 0; l < L16; l++) d[l] = fmaf(xt[i + l], row[i + l], d[l]);
+                r = red16(d) + bias;
+            }
+            finish(out, t * OUT + o, r, flags);
+        }
+        free(row);
+    }
+}
+
 /* matmul_rows T == 1 (kernels.mojo:301-312) / linear_team OUT_MAJOR branch
  * (817-826): the GGUF decode GEMV, out[o] (+)= act(dot_row(o, x) + b[o]). */
 void orc_gguf_gemv(int t, const uint8_t *w, int64_t rows, int64_t cols, const float *x, const float *b, float *out,
@@ -1180,9 +1224,19 @@ static void qm_free(orc_qm *m) {
  * mlp.c_proj.weight [4C, C], mlp.c_proj.bias.  Layers in QuantMatrix[bits,
  * group, sym, A16=True], the head in E = QuantMatrix[8, 0, False, True]
  * (HEAD8_A16, gpt2t.mojo:1234), the cache QuantKV[8]. */
+orc_gpt2 *orc_gpt2_new_fmt(const float *const *params, int bits, int group, int sym, int a16, int e_bits,
+                           int e_group, int e_sym, int e_a16);
 orc_gpt2 *orc_gpt2_new(const float *const *params, int bits, int group, int sym) {
+    return orc_gpt2_new_fmt(params, bits, group, sym, 1, 8, 0, 0, 1);
+}
+
+/* Model[W, E] for any QuantMatrix layer format W = [bits, group, sym, a16]
+ * and head format E = [e_bits, e_group, e_sym, e_a16] (run_quantized,
+ * gpt2t.mojo:1282-1292). */
+orc_gpt2 *orc_gpt2_new_fmt(const float *const *params, int bits, int group, int sym, int a16, int e_bits,
+                           int e_group, int e_sym, int e_a16) {
     orc_gpt2 *m = (orc_gpt2 *)calloc(1, sizeof(orc_gpt2));
-    qm_alloc(&m->wte, 8, 0, 0, 1, G_V, G_C);
+    qm_alloc(&m->wte, e_bits, e_group, e_sym, e_a16, G_V, G_C);
     orc_qm_from_f32(&m->wte, params[0], G_V, G_C, 0);
     static const int64_t rows[4] = {G_C, G_C, G_C, 4 * G_C}, cols[4] = {3 * G_C, G_C, 4 * G_C, G_C};
     static const int mat_idx[4] = {2, 4, 8, 10};
@@ -1192,7 +1246,7 @@ orc_gpt2 *orc_gpt2_new(const float *const *params, int bits, int group, int sym)
         const float *const *lp = params + 4 + 12 * l;
         for (int j = 0; j < 4; j++) {
             orc_qm *q = &m->mats[l * 4 + j];
-            qm_alloc(q, bits, group, sym, 1, cols[j], rows[j]);
+            qm_alloc(q, bits, group, sym, a16, cols[j], rows[j]);
             orc_qm_from_f32(q, lp[mat_idx[j]], rows[j], cols[j], 1);
         }
         for (int s = 0; s < N_VECS; s++) {
@@ -1268,6 +1322,16 @@ float *orc_gpt2_act(orc_gpt2 *m, int which) {
     }
 }
 
+/* kernels.linear / head (kernels.mojo:655-690) for a QuantMatrix: the
+ * integer kernels for A16, matmul_rows otherwise. */
+static void linear(float *out, const float *x, const orc_qm *w, const float *b, int64_t T, int64_t IN, int64_t OUT,
+                   int flags) {
+    if (w->a16)
+        orc_matmul_rows_a16(out, x, w, b, T, IN, OUT, flags);
+    else
+        orc_qm_matmul_rows(out, x, w, b, T, IN, OUT, flags);
+}
+
 /* Model.blocks (gpt2t.mojo:485-571): embed tokens at pos0.., all layers. */
 static void gpt2_blocks(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
     const int C = G_C;
@@ -1281,7 +1345,7 @@ static void gpt2_blocks(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
         orc_qm *w = &m->mats[l * 4];
         float **v = &m->vecs[l * N_VECS];
         orc_layernorm(m->xn, m->x, v[LN1_W], v[LN1_B], T, C);
-        orc_matmul_rows_a16(m->qkv, m->xn, &w[0], v[QKV_B], T, C, 3 * C, EPI_BIAS);
+        linear(m->qkv, m->xn, &w[0], v[QKV_B], T, C, 3 * C, EPI_BIAS);
         if (m->integer) {
             orc_ikv ik = gpt2_ikv(m);
             for (int t = 0; t < T; t++) {
@@ -1296,10 +1360,10 @@ static void gpt2_blocks(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
             }
             orc_kv_attend(&m->kv, m->att, m->qkv, l, T, pos0);
         }
-        orc_matmul_rows_a16(m->x, m->att, &w[1], v[PROJ_B], T, C, C, EPI_BIAS | EPI_RESID);
+        linear(m->x, m->att, &w[1], v[PROJ_B], T, C, C, EPI_BIAS | EPI_RESID);
         orc_layernorm(m->xn, m->x, v[LN2_W], v[LN2_B], T, C);
-        orc_matmul_rows_a16(m->fc, m->xn, &w[2], v[FC_B], T, C, 4 * C, EPI_BIAS | EPI_GELU);
-        orc_matmul_rows_a16(m->x, m->fc, &w[3], v[FCPROJ_B], T, 4 * C, C, EPI_BIAS | EPI_RESID);
+        linear(m->fc, m->xn, &w[2], v[FC_B], T, C, 4 * C, EPI_BIAS | EPI_GELU);
+        linear(m->x, m->fc, &w[3], v[FCPROJ_B], T, 4 * C, C, EPI_BIAS | EPI_RESID);
     }
 }
 
@@ -1311,7 +1375,7 @@ const float *orc_gpt2_forward(orc_gpt2 *m, const int64_t *tokens, int T, int pos
     gpt2_blocks(m, tokens, T, pos0);
     const float *last = m->x + (int64_t)(T - 1) * G_C;
     orc_layernorm(m->xn, last, m->lnf_w, m->lnf_b, 1, G_C);
-    orc_matmul_rows_a16(m->logits, m->xn, &m->wte, NULL, 1, G_C, G_V, 0);
+    linear(m->logits, m->xn, &m->wte, NULL, 1, G_C, G_V, 0);
     return m->logits;
 }
 
@@ -1320,7 +1384,7 @@ const float *orc_gpt2_forward(orc_gpt2 *m, const int64_t *tokens, int T, int pos
 void orc_gpt2_forward_all(orc_gpt2 *m, const int64_t *tokens, int T, float *logits) {
     gpt2_blocks(m, tokens, T, 0);
     orc_layernorm(m->xn, m->x, m->lnf_w, m->lnf_b, T, G_C);
-    orc_matmul_rows_a16(logits, m->xn, &m->wte, NULL, T, G_C, G_V, 0);
+    linear(logits, m->xn, &m->wte, NULL, T, G_C, G_V, 0);
 }
 
 /* log_sum_exp (gpt2t.mojo:1027-1036): the row maximum, then exp(l - max) in

@@ -282,6 +282,54 @@ def test_matmul_epilogues(orc):
     assert np.max(np.abs(nb - (plain - b))) < 1e-5
 
 
+# gpt2t.mojo's float-activation --dtype formats (1315-1334): QuantMatrix[B, G, S, A16=False]
+FLOAT_ACT = [(8, 0, False), (8, 0, True), (4, 0, False), (4, 0, True), (4, 128, False), (4, 128, True),
+             (4, 64, False), (4, 64, True), (4, 32, False), (4, 32, True)]
+
+
+@pytest.mark.parametrize("fmt", FLOAT_ACT)
+@pytest.mark.parametrize("T", [1, 5])
+def test_matmul_rows_float_vs_exact_float64(orc, fmt, T):
+    """matmul_rows over float activations: T == 1 through dot_row, T > 1
+    through mm_tile (rows 0..63) and rows_dot (the 6 tail rows), against
+    float64 on the same quantized values, 1e-5 of max |out|, with GELU and
+    the residual."""
+    bits, group, sym = fmt
+    rng = np.random.default_rng(T * 7 + bits + group)
+    IN, OUT = 512, 70
+    m = orc.QuantMatrix.from_f32(rng.uniform(-0.1, 0.1, (IN, OUT)).astype(np.float32), bits, group, sym, False)
+    x = rng.uniform(-1, 1, (T, IN)).astype(np.float32)
+    b = rng.uniform(-1, 1, OUT).astype(np.float32)
+    want = x.astype(np.float64) @ m.dequant().astype(np.float64).T + b
+    out = orc.matmul_rows(x, m, b)
+    assert np.max(np.abs(out - want)) / np.max(np.abs(want)) < 1e-5
+    g = orc.matmul_rows(x, m, b, orc.EPI_BIAS | orc.EPI_GELU)
+    gw = 0.5 * want * (1 + np.tanh(np.sqrt(2 / np.pi) * (want + 0.044715 * want ** 3)))
+    assert np.max(np.abs(g - gw)) < 1e-5
+    base = rng.normal(0, 1, (T, OUT)).astype(np.float32)
+    r = orc.matmul_rows(x, m, b, orc.EPI_BIAS | orc.EPI_RESID, out=base.copy())
+    assert np.max(np.abs(r - (want + base))) < 1e-5
+
+
+@pytest.mark.parametrize("fmt", [(8, 0, False), (4, 32, True), (4, 128, False)])
+def test_matmul_rows_float_one_hot_exact(orc, fmt):
+    """x = unit rows: every path (dot_row, mm_tile, rows_dot) returns the
+    selected dequantized column plus the bias bit for bit, which pins the
+    row / column indexing and the transposition."""
+    bits, group, sym = fmt
+    rng = np.random.default_rng(3)
+    IN, OUT = 256, 70
+    m = orc.QuantMatrix.from_f32(rng.normal(0, 0.05, (IN, OUT)).astype(np.float32), bits, group, sym, False)
+    deq = m.dequant()
+    b = rng.normal(0, 1, OUT).astype(np.float32)
+    cols = [3, 100, 255, 31, 32]
+    x = np.zeros((len(cols), IN), np.float32)
+    x[np.arange(len(cols)), cols] = 1.0
+    want = deq[:, cols].T + b
+    assert np.array_equal(orc.matmul_rows(x, m, b), want)
+    assert np.array_equal(orc.matmul_rows(x[1:2], m, b), want[1:2])
+
+
 # ---------------------------------------------------------------------- GGUF
 
 KINDS = ["Q4_0", "Q4_1", "Q8_0", "Q4_K", "Q5_K", "Q6_K"]

@@ -430,8 +430,10 @@ int llmq_ln_linear(llmq_ctx *ctx, float *out, const float *x, const float *ln_w,
     RC(check_linear(w, IN, OUT));
     LLMQ_REQUIRE(w->kind == MAT_QUANT, "ln_linear: GGUF matrices take llmq_layernorm then llmq_linear");
     if (!w->a16) {
-        // float activations: the LayerNorm into the context's workspace, then
-        // matmul_rows (not for use under graph capture, as the workspace)
+        // float activations: one token with the LayerNorm fused into the
+        // GEMV; several through the context's workspace, then matmul_rows
+        // (not for use under graph capture, as the workspace)
+        if (T == 1) return launch_gguf_gemv(ctx, w, x, out, bias, flags, nullptr, 0, nullptr, 0.0f, 0, ln_w, ln_b);
         void *ws = nullptr;
         RC(ctx_workspace(ctx, sizeof(float) * (size_t)(T * IN), &ws));
         float *xn = static_cast<float *>(ws);
@@ -589,12 +591,14 @@ int llmq_ikv_export(llmq_ctx *ctx, const llmq_kv *kv, int8_t *k, int8_t *v, int3
 // activations (A16 = False) take LayerNorm into xn, then matmul_rows.
 static int gpt2_linear(llmq_gpt2 *m, const GemvRequest &rq) {
     if (rq.w->a16) return launch_gemv_a16(m->ctx, rq);
+    if (rq.T == 1)  // LayerNorm fused into the GEMV's prologue
+        return launch_gguf_gemv(m->ctx, rq.w, rq.x, rq.out, rq.bias, rq.flags, rq.amax, rq.amax_cap, nullptr, 0.0f,
+                                0, rq.ln_w, rq.ln_b);
     const float *x = rq.x;
     if (rq.ln_w) {
         RC(launch_layernorm(m->ctx, m->xn, rq.x, rq.ln_w, rq.ln_b, rq.T, rq.w->k));
         x = m->xn;
     }
-    if (rq.T == 1) return launch_gguf_gemv(m->ctx, rq.w, x, rq.out, rq.bias, rq.flags, rq.amax, rq.amax_cap);
     return launch_gguf_gemm(m->ctx, rq.w, x, rq.w->k, rq.T, rq.out, rq.w->n, rq.bias, rq.flags);
 }
 

@@ -158,10 +158,11 @@ int gguf_upload(llmq_ctx *ctx, llmq_mat *m, int ggml_type, const uint8_t *blocks
 int gguf_num_parts(const llmq_mat *w);
 // One-token GGUF GEMV (gguf1.hip); with rms_g the row is RMS-normalized
 // (times the gain rms_g) before the product; with swiglu, x holds 2K floats
-// [gate | up] and the row is silu(gate) * up.
+// [gate | up] and the row is silu(gate) * up; with ln_w the row goes through
+// LayerNorm (eps 1e-5, weight ln_w, bias ln_b) first.
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
                      ArgmaxPart *amax, int amax_cap, const float *rms_g = nullptr, float rms_eps = 0.0f,
-                     int swiglu = 0);
+                     int swiglu = 0, const float *ln_w = nullptr, const float *ln_b = nullptr);
 int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
 int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *rows, int n, float *dst, int64_t ldd);
 // Prompt attention over an int8 cache of n_kv heads (attn.hip): query head h

@@ -45,6 +45,7 @@ struct G1Args {
     const float *rms_g;  // optional RMSNorm gain: x -> x / sqrt(mean(x^2) + eps) * g first
     float rms_eps;
     int swiglu;          // x holds [gate | up] of 2K floats: the row is silu(gate) * up
+    const float *ln_w, *ln_b;  // optional LayerNorm (eps 1e-5) of the row first
 };
 
 // silu(g) * u per lane of two activation vectors (llama.hip's swiglu).
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     __shared__ __align__(16) uint8_t s_meta[NW][St::LOADS * 1024];
     __shared__ __align__(16) uint8_t s_d6[NW][St::D6_LOADS > 0 ? St::D6_LOADS * 1024 : 16];
     __shared__ ArgmaxPart s_best[NW];
-    __shared__ float s_red[NW];
+    __shared__ float s_red[NW], s_red2[NW];
 
     const int K = a.K, CK = a.CK;
     float *xs = smem_f;                                // [K] activations
@@ -316,6 +317,47 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
             v.y = (v.y * r) * g.y;
             v.z = (v.z * r) * g.z;
             v.w = (v.w * r) * g.w;
+            reinterpret_cast<float4 *>(xs)[u] = v;
+        }
+        lds_barrier();
+    }
+    if (a.ln_w) {  // LayerNorm of the staged row (kernels.layernorm, kernels.mojo:179-197), fused
+        float sum = 0.0f;
+        for (int u = tid; u < nunits; u += NT) {
+            const float4 v = reinterpret_cast<const float4 *>(xs)[u];
+            sum += (v.x + v.y) + (v.z + v.w);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (lane == 0) s_red[wid] = sum;
+        lds_barrier();
+        sum = s_red[0];
+#pragma unroll
+        for (int i = 1; i < NW; i++) sum += s_red[i];
+        const float mean = sum / (float)K;
+        float sq = 0.0f;
+        for (int u = tid; u < nunits; u += NT) {
+            const float4 v = reinterpret_cast<const float4 *>(xs)[u];
+            const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+            sq += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+        if (lane == 0) s_red2[wid] = sq;
+        lds_barrier();
+        sq = s_red2[0];
+#pragma unroll
+        for (int i = 1; i < NW; i++) sq += s_red2[i];
+        const float rstd = 1.0f / sqrtf(sq / (float)K + 1e-5f);
+        const float4 *w4 = reinterpret_cast<const float4 *>(a.ln_w);
+        const float4 *b4 = reinterpret_cast<const float4 *>(a.ln_b);
+        for (int u = tid; u < nunits; u += NT) {
+            float4 v = reinterpret_cast<const float4 *>(xs)[u];
+            const float4 g = w4[u], c = b4[u];
+            v.x = ((v.x - mean) * rstd) * g.x + c.x;
+            v.y = ((v.y - mean) * rstd) * g.y + c.y;
+            v.z = ((v.z - mean) * rstd) * g.z + c.z;
+            v.w = ((v.w - mean) * rstd) * g.w + c.w;
             reinterpret_cast<float4 *>(xs)[u] = v;
         }
         lds_barrier();
@@ -572,7 +614,8 @@ int qm_cpg_shift(const llmq_mat *w) {
 int gguf_num_parts(const llmq_mat *w) { return make_plan(w).grid; }
 
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
-                     ArgmaxPart *amax, int amax_cap, const float *rms_g, float rms_eps, int swiglu) {
+                     ArgmaxPart *amax, int amax_cap, const float *rms_g, float rms_eps, int swiglu,
+                     const float *ln_w, const float *ln_b) {
     LLMQ_REQUIRE(w && is_float_act(w), "gguf_gemv: not a GGUF or float-activation QuantMatrix");
     LLMQ_REQUIRE(x && out, "gguf_gemv: null pointer");
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemv: LLMQ_BIAS without a bias");
@@ -619,6 +662,8 @@ int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *ou
     a.amax = amax;
     a.rms_g = rms_g;
     a.rms_eps = rms_eps;
+    a.ln_w = ln_w;
+    a.ln_b = ln_b;
     a.swiglu = swiglu;
     int rc;
     switch (type) {

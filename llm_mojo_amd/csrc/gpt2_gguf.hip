@@ -31,6 +31,16 @@ int linear(llmq_gpt2 *m, const llmq_mat *w, const float *x, int T, float *out, c
     return launch_gguf_gemm(m->ctx, w, x, w->k, T, out, w->n, bias, flags);
 }
 
+// LayerNorm then linear: fused into the GEMV's prologue for one token,
+// through xn for several.
+int ln_linear(llmq_gpt2 *m, const llmq_mat *w, const float *x, const float *ln_w, const float *ln_b, int T,
+              float *out, const float *bias, int flags) {
+    if (T == 1)
+        return launch_gguf_gemv(m->ctx, w, x, out, bias, flags, nullptr, 0, nullptr, 0.0f, 0, ln_w, ln_b);
+    RC(launch_layernorm(m->ctx, m->xn, x, ln_w, ln_b, T, w->k));
+    return linear(m, w, m->xn, T, out, bias, flags);
+}
+
 // A float32 tensor of the file (gguf_f32, gpt2t.mojo:721-726), n floats.
 int gguf_f32(const llmq_gguf *g, const std::string &name, int64_t n, float *dst) {
     int64_t i;
@@ -75,20 +85,19 @@ int gpt2g_enqueue(llmq_gpt2 *m, int T, int pos0, bool with_head) {
     for (int l = 0; l < NL; l++) {
         llmq_mat **w = &m->mats[l * 4];
         const float *const *v = m->vec[l];
-        RC(launch_layernorm(ctx, m->xn, m->x, v[LN1_W], v[LN1_B], T, C));
-        RC(linear(m, w[0], m->xn, T, m->qkv, v[QKV_B], LLMQ_BIAS));
+        RC(ln_linear(m, w[0], m->x, v[LN1_W], v[LN1_B], T, m->qkv, v[QKV_B], LLMQ_BIAS));
         if (T > 1) RC(launch_kv_store(ctx, m->kv, l, pos0, nullptr, m->qkv, T, 3 * C));
         RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, nullptr, 3 * C, T == 1));
         RC(linear(m, w[1], m->att, T, m->x, v[PROJ_B], LLMQ_BIAS | LLMQ_RESID));
-        RC(launch_layernorm(ctx, m->xn, m->x, v[LN2_W], v[LN2_B], T, C));
-        RC(linear(m, w[2], m->xn, T, m->fc, v[FC_B], LLMQ_BIAS | LLMQ_GELU));
+        RC(ln_linear(m, w[2], m->x, v[LN2_W], v[LN2_B], T, m->fc, v[FC_B], LLMQ_BIAS | LLMQ_GELU));
         RC(linear(m, w[3], m->fc, T, m->x, v[FCPROJ_B], LLMQ_BIAS | LLMQ_RESID));
     }
     if (!with_head) return LLMQ_OK;
     // LN_f on the last row, then the head (gpt2t.mojo:337-340)
-    RC(launch_layernorm(ctx, m->xn, m->x + (int64_t)(T - 1) * C, m->lnf_w, m->lnf_b, 1, C));
-    if (gguf_has_i16(m->lm)) return launch_gguf_head16(ctx, m->lm, m->xn, m->logits, 1);
-    return launch_gguf_gemv(ctx, m->lm, m->xn, m->logits, nullptr, 0, nullptr, 0);
+    const float *last = m->x + (int64_t)(T - 1) * C;
+    if (!gguf_has_i16(m->lm)) return ln_linear(m, m->lm, last, m->lnf_w, m->lnf_b, 1, m->logits, nullptr, 0);
+    RC(launch_layernorm(ctx, m->xn, last, m->lnf_w, m->lnf_b, 1, C));
+    return launch_gguf_head16(ctx, m->lm, m->xn, m->logits, 1);
 }
 
 extern "C" int llmq_gpt2_load_gguf(llmq_ctx *ctx, const char *path, int attention, llmq_gpt2 **out) {

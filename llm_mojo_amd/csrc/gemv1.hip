@@ -184,7 +184,7 @@ __device__ __forceinline__ void nibble_transpose(uint32_t &A, uint32_t &B) {
     B = b2;
 }
 
-template <int BITS, int NW, bool LN, int UPT, int STEPS, bool DBG>
+template <int BITS, int NW, bool LN, int UPT, int STEPS, int WIN, bool DBG>
 __global__ __launch_bounds__(NW * 64) void gemv1_kernel(Gemv1Args a) {
     constexpr int NT = NW * 64;
     constexpr int PD = BITS == 4 ? 16 : 8;  // plane dwords per chunk
@@ -257,11 +257,16 @@ __global__ __launch_bounds__(NW * 64) void gemv1_kernel(Gemv1Args a) {
         const uint32_t off = (uint32_t)(i * 1024 + lane * 16);
         wzp[i] = bload16(rz, off < (uint32_t)ng * 16u ? (uint32_t)glo * 16u + off : kOOB);
     }
-#pragma unroll
-    for (int u = 0; u < STEPS; u++) {
+    // The first WIN code steps go out now, step u + WIN once step u is
+    // consumed (WIN < STEPS for matrices streamed from HBM: fewer bytes in
+    // flight ahead of the activation row's own fetch, which gates the
+    // prologue, and the sums then overlap the stream).
+    auto code_off = [&](int u) -> uint32_t {
         const uint32_t off = offA + (uint32_t)u * 1024u + (sA + u >= S ? wrap_adj : 0u) + lane_off;
-        wc[u] = bload16(rc, u < ns ? off : kOOB);
-    }
+        return u < ns ? off : kOOB;
+    };
+#pragma unroll
+    for (int u = 0; u < WIN; u++) wc[u] = bload16(rc, code_off(u));
     const int o = (t0 + wid) * 16 + r;  // the row this lane finishes (wave wid < nt)
     const bool row_ok = wid < nt && o < a.n;
     const auto rb = make_rsrc(a.bias, (uint32_t)a.n * 4u);  // a.bias is valid memory even without LLMQ_BIAS
@@ -384,6 +389,11 @@ __global__ __launch_bounds__(NW * 64) void gemv1_kernel(Gemv1Args a) {
         const float scale = scl[u];
         const int zp = zpl[u];
         const uint4 d = wc[u];
+        if (u + WIN < STEPS) {
+            __builtin_amdgcn_sched_barrier(0);
+            wc[u + WIN] = bload16(rc, code_off(u + WIN));
+            __builtin_amdgcn_sched_barrier(0);
+        }
         uint32_t su;
         if (BITS == 4) {
             su = __builtin_amdgcn_udot8(d.x, 0x11111111u, 0u, false);
@@ -495,8 +505,14 @@ __global__ __launch_bounds__(NW * 64) void gemv1_kernel(Gemv1Args a) {
 }
 
 struct Plan {
-    int nw, tmax, spw, steps, upt, grid;
+    int nw, tmax, spw, steps, upt, grid, win;
 };
+
+// Matrices at least this large are taken as streamed from HBM (the
+// last-level cache is 256 MB, but a decode step over a large model streams
+// every matrix once): they keep kStreamWin code steps in flight per wave.
+constexpr int64_t kStreamBytes = 16ll << 20;
+constexpr int kStreamWin = 2;
 
 int steps_for(int spw) { return spw <= 2 ? 2 : spw <= 4 ? 4 : 8; }
 
@@ -536,6 +552,9 @@ Plan make_plan(const llmq_mat *w) {
     p.spw = (p.tmax * S + nw - 1) / nw;
     p.steps = steps_for(p.spw);
     p.upt = (units + nw * 64 - 1) / (nw * 64);
+    const int64_t code_bytes = w->ntiles * w->CK * 256;
+    p.win = (nw == 16 && code_bytes >= kStreamBytes) ? kStreamWin : p.steps;
+    if (const char *e = getenv("LLMQ_GEMV1_WIN")) p.win = atoi(e) == kStreamWin ? kStreamWin : p.steps;
     return p;
 }
 
@@ -547,24 +566,31 @@ size_t lds_bytes(const llmq_mat *w, const Plan &p) {
 
 
 template <int BITS, int NW, bool LN, int UPT, int STEPS>
-void launch_t(llmq_ctx *ctx, const Gemv1Args &a, int grid, size_t lds) {
+void launch_t(llmq_ctx *ctx, const Gemv1Args &a, int grid, size_t lds, int win) {
     if constexpr (!LN && UPT == 1) {
         if (a.dbg) {
-            hipLaunchKernelGGL((gemv1_kernel<BITS, NW, LN, UPT, STEPS, true>), dim3((unsigned)grid), dim3(NW * 64), lds,
-                               ctx->stream, a);
+            hipLaunchKernelGGL((gemv1_kernel<BITS, NW, LN, UPT, STEPS, STEPS, true>), dim3((unsigned)grid),
+                               dim3(NW * 64), lds, ctx->stream, a);
             return;
         }
     }
-    hipLaunchKernelGGL((gemv1_kernel<BITS, NW, LN, UPT, STEPS, false>), dim3((unsigned)grid), dim3(NW * 64), lds,
-                       ctx->stream, a);
+    if constexpr (NW == 16 && STEPS > kStreamWin) {
+        if (win == kStreamWin) {
+            hipLaunchKernelGGL((gemv1_kernel<BITS, NW, LN, UPT, STEPS, kStreamWin, false>), dim3((unsigned)grid),
+                               dim3(NW * 64), lds, ctx->stream, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((gemv1_kernel<BITS, NW, LN, UPT, STEPS, STEPS, false>), dim3((unsigned)grid), dim3(NW * 64),
+                       lds, ctx->stream, a);
 }
 
 template <int BITS, int NW, bool LN, int UPT>
 int launch_steps(llmq_ctx *ctx, const Gemv1Args &a, const Plan &p, size_t lds) {
     switch (p.steps) {
-        case 2: launch_t<BITS, NW, LN, UPT, 2>(ctx, a, p.grid, lds); return LLMQ_OK;
-        case 4: launch_t<BITS, NW, LN, UPT, 4>(ctx, a, p.grid, lds); return LLMQ_OK;
-        case 8: if constexpr (NW == 16) { launch_t<BITS, NW, LN, UPT, 8>(ctx, a, p.grid, lds); return LLMQ_OK; } break;
+        case 2: launch_t<BITS, NW, LN, UPT, 2>(ctx, a, p.grid, lds, p.win); return LLMQ_OK;
+        case 4: launch_t<BITS, NW, LN, UPT, 4>(ctx, a, p.grid, lds, p.win); return LLMQ_OK;
+        case 8: if constexpr (NW == 16) { launch_t<BITS, NW, LN, UPT, 8>(ctx, a, p.grid, lds, p.win); return LLMQ_OK; } break;
     }
     return llmq_set_error(LLMQ_EUNSUPPORTED, "linear: no kernel for %d waves x %d steps", NW, p.steps);
 }

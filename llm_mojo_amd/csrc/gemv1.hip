@@ -511,7 +511,7 @@ struct Plan {
 // Matrices at least this large are taken as streamed from HBM (the
 // last-level cache is 256 MB, but a decode step over a large model streams
 // every matrix once): they keep kStreamWin code steps in flight per wave.
-constexpr int64_t kStreamBytes = 16ll << 20;
+constexpr int64_t kStreamBytes = 20ll << 20;
 constexpr int kStreamWin = 2;
 
 int steps_for(int spw) { return spw <= 2 ? 2 : spw <= 4 ? 4 : 8; }

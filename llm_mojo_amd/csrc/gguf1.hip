@@ -174,7 +174,7 @@ __device__ __forceinline__ uint32_t spread4(uint32_t f) {
     }
 }
 
-template <int TYPE, int NW, int STEPS>
+template <int TYPE, int NW, int STEPS, int WIN>
 __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     using T = T1<TYPE>;
     using St = Stage<TYPE, STEPS>;
@@ -248,25 +248,21 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     const uint32_t offA = ((uint32_t)(t0 + tA) * (uint32_t)CK + 4u * (uint32_t)sA) * 16u;  // chunk-row index
     const uint32_t wrap_adj = (uint32_t)(CK - 4 * S) * 16u;
     const uint32_t lane_cr = (uint32_t)j * 16u + (uint32_t)r;
+    // Codes (and high bits) of step u; the first WIN steps go out now, step
+    // u + WIN as step u is consumed (WIN < STEPS for matrices streamed from
+    // HBM: fewer bytes queued ahead of the activation row's fetch).
     const auto rc = make_rsrc(a.codes, a.codes_bytes);
+    const auto rb = make_rsrc(a.bits, a.bits_bytes);
     uint4 wc[STEPS];
-#pragma unroll
-    for (int u = 0; u < STEPS; u++) {
+    uint2 wb[T::BITS_ESZ > 0 ? STEPS : 1];
+    auto load_step = [&](int u) {
         const uint32_t cr = offA + (uint32_t)u * 64u + (sA + u >= S ? wrap_adj : 0u) + lane_cr;
         wc[u] = bload16(rc, u < ns ? cr * 16u : kOOB);
-    }
-    uint2 wb[T::BITS_ESZ > 0 ? STEPS : 1];
-    if constexpr (T::BITS_ESZ > 0) {
-        const auto rb = make_rsrc(a.bits, a.bits_bytes);
+        if constexpr (T::BITS_ESZ == 8) wb[u] = bload8(rb, u < ns ? cr * 8u : kOOB);
+        if constexpr (T::BITS_ESZ == 4) wb[u] = make_uint2(bload4(rb, u < ns ? cr * 4u : kOOB), 0u);
+    };
 #pragma unroll
-        for (int u = 0; u < STEPS; u++) {
-            const uint32_t cr = offA + (uint32_t)u * 64u + (sA + u >= S ? wrap_adj : 0u) + lane_cr;
-            if (T::BITS_ESZ == 8)
-                wb[u] = bload8(rb, u < ns ? cr * 8u : kOOB);
-            else
-                wb[u] = make_uint2(bload4(rb, u < ns ? cr * 4u : kOOB), 0u);
-        }
-    }
+    for (int u = 0; u < WIN; u++) load_step(u);
     const int o = (t0 + wid) * 16 + r;
     const bool row_ok = wid < nt && o < a.n;
     const auto rbias = make_rsrc(a.bias, (uint32_t)a.n * 4u);
@@ -377,6 +373,11 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
 #pragma unroll
     for (int u = 0; u < STEPS; u++) {
         if (u < ns) {  // wave-uniform: steps past the wave's range carry no codes
+            if (u + WIN < STEPS) {
+                __builtin_amdgcn_sched_barrier(0);
+                load_step(u + WIN);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             const bool second = sA + u >= S;
             const int tl = tA + (second ? 1 : 0);
             const int ss = sA + u - (second ? S : 0);
@@ -525,8 +526,13 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
 }
 
 struct Plan {
-    int nw, tmax, spw, steps, grid;
+    int nw, tmax, spw, steps, grid, win;
 };
+
+// Matrices whose codes take at least this many bytes are taken as streamed
+// from HBM and keep kStreamWin steps in flight per wave.
+constexpr int64_t kStreamBytes = 20ll << 20;
+constexpr int kStreamWin = 2;
 
 int steps_for(int spw) { return spw <= 2 ? 2 : spw <= 4 ? 4 : spw <= 8 ? 8 : 16; }
 int max_steps(const llmq_mat *w) {
@@ -561,6 +567,8 @@ Plan make_plan(const llmq_mat *w) {
     p.tmax = (int)((w->ntiles + grid - 1) / grid);
     p.spw = (p.tmax * S + nw - 1) / nw;
     p.steps = steps_for(p.spw);
+    p.win = (nw == 16 && w->ntiles * w->CK * 256 >= kStreamBytes) ? kStreamWin : p.steps;
+    if (const char *e = getenv("LLMQ_GGUF1_WIN")) p.win = (nw == 16 && atoi(e) == kStreamWin) ? kStreamWin : p.steps;
     return p;
 }
 
@@ -568,9 +576,9 @@ size_t lds_bytes(const llmq_mat *w, const Plan &p) {
     return (size_t)w->k * 4 + (size_t)((w->k / 16 + 3) & ~3) * 4 + (size_t)p.tmax * p.nw * 64 * 4;
 }
 
-template <int TYPE, int NW, int STEPS>
-int launch_t(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
-    auto kern = gguf1_kernel<TYPE, NW, STEPS>;
+template <int TYPE, int NW, int STEPS, int WIN>
+int launch_w(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
+    auto kern = gguf1_kernel<TYPE, NW, STEPS, WIN>;
     hipFuncAttributes fa{};
     LLMQ_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(kern)));
     if (fa.sharedSizeBytes + lds > ctx->prop.sharedMemPerBlock)
@@ -585,6 +593,13 @@ int launch_t(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
     }
     hipLaunchKernelGGL(kern, dim3((unsigned)p.grid), dim3(NW * 64), lds, ctx->stream, a);
     return LLMQ_OK;
+}
+
+template <int TYPE, int NW, int STEPS>
+int launch_t(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
+    if constexpr (NW == 16 && STEPS > kStreamWin)
+        if (p.win == kStreamWin) return launch_w<TYPE, NW, STEPS, kStreamWin>(ctx, a, p, lds);
+    return launch_w<TYPE, NW, STEPS, STEPS>(ctx, a, p, lds);
 }
 
 template <int TYPE>

@@ -188,20 +188,32 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
     if ((tid & 63) == 0) red[tid >> 6] = tot;
     lds_barrier();
     const float total = ((red[0] + red[1]) + red[2]) + red[3];
+    // Each position's weight p * vs once (p = e / total), in place of the
+    // scores; the value sums below use it as they would have computed it.
+    for (int s = tid; s < npos; s += kAttnThreads) {
+        float vs;
+        if (STAGE)
+            vs = vsc[s];
+        else if (STORE && s == cur)
+            vs = vscale_new;
+        else
+            vs = VS[base + (int64_t)s * n_head];
+        scores[s] = (scores[s] / total) * vs;
+    }
     lds_barrier();
     // out[i]: threads split positions into `parts` interleaved subsets.
     constexpr int parts = kAttnThreads / HD;
     const int i = tid % HD, part = tid / HD;
     float acc = 0.0f;
     for (int s = part; s < npos; s += parts) {
-        const float p = scores[s] / total;
+        const float w = scores[s];
         if (STAGE) {
-            acc = fmaf(p * vsc[s], (float)vrow[(int64_t)s * HD + i], acc);
+            acc = fmaf(w, (float)vrow[(int64_t)s * HD + i], acc);
         } else if (STORE && s == cur) {
-            acc = fmaf(p * vscale_new, (float)vnew[i], acc);
+            acc = fmaf(w, (float)vnew[i], acc);
         } else {
             const int64_t sl = base + (int64_t)s * n_head;
-            acc = fmaf(p * VS[sl], (float)V8[sl * HD + i], acc);
+            acc = fmaf(w, (float)V8[sl * HD + i], acc);
         }
     }
     red[tid] = acc;

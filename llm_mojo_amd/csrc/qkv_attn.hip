@@ -299,13 +299,13 @@ __global__ __launch_bounds__(kNT) void qkv_attn_kernel(QkvAttnArgs a) {
         ex = expf(sc_mine - mx);
         scores[tid] = ex;
     }
-    const float total = block_sum(ex, red);  // its barriers order the scores writes
-    const int i = lane;                       // output dimension
+    const float total = block_sum(ex, red);
+    // Each position's weight p * vs once (p = e / total), by its own thread.
+    if (tid < npos) scores[tid] = (ex / total) * vsc[tid];
+    lds_barrier();
+    const int i = lane;  // output dimension
     float acc = 0.0f;
-    for (int s = wid; s < npos; s += kNW) {
-        const float p = scores[s] / total;
-        acc = fmaf(p * vsc[s], (float)vrow[(int64_t)s * kHD + i], acc);
-    }
+    for (int s = wid; s < npos; s += kNW) acc = fmaf(scores[s], (float)vrow[(int64_t)s * kHD + i], acc);
     part[wid][i] = acc;
     lds_barrier();
     if (tid < kHD) {

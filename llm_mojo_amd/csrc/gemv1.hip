@@ -516,24 +516,30 @@ constexpr int kStreamWin = 2;
 
 int steps_for(int spw) { return spw <= 2 ? 2 : spw <= 4 ? 4 : 8; }
 
-// Workgroup shape for a matrix.  Small latency-bound matrices: 4-wave
-// workgroups, one row tile each.  Long rows or large matrices (bandwidth-
-// bound): 16-wave workgroups, one per CU, each with a contiguous run of
-// whole tiles (so CUs differ by at most one tile of work) and the
-// per-workgroup prologue spread over 1024 threads.  Each wave holds at most
-// kMaxSteps steps and crosses at most one tile boundary; past that, more
-// workgroups.
+// Workgroup shape for a matrix.  Matrices below kStreamBytes of codes:
+// 4-wave workgroups, one row tile each (up to 8 steps a wave and 4
+// activation units a thread; longer rows fall back to 16 waves).  Large
+// (HBM-streamed) matrices: 16-wave workgroups, one per CU, each with a
+// contiguous run of whole tiles (so CUs differ by at most one tile of work)
+// and the per-workgroup prologue spread over 1024 threads.  Each wave holds
+// at most kMaxSteps steps and crosses at most one tile boundary; past that,
+// more workgroups.
 Plan make_plan(const llmq_mat *w) {
     Plan p{};
     const int S = (int)((w->CK + 3) / 4);
     const int64_t work = w->ntiles * (int64_t)S;  // wave steps of 1 KiB
     const int units = (int)(w->k / 4);           // four activations per thread
-    int nw = (work >= 4096 || S > 8) ? 16 : 4;
+    // 16-wave workgroups for matrices streamed from HBM (with the code-step
+    // window below); 4-wave workgroups of one row tile otherwise, which
+    // launch faster (measured: 3072x768 5.08 -> 4.84 us, 4096x4096 5.70 ->
+    // 5.33 us against 16 waves).
+    (void)work;
+    int nw = w->ntiles * w->CK * 256 >= kStreamBytes ? 16 : 4;
     if (const char *e = getenv("LLMQ_GEMV1_NW")) {
         const int v = atoi(e);
         if (v == 4 || v == 16) nw = v;
     }
-    if (nw == 4 && (units > 256 || (S + 3) / 4 > 4)) nw = 16;  // the 4-wave kernels take <= 4 steps, <= 1 unit
+    if (nw == 4 && (units > 1024 || (S + 3) / 4 > kMaxSteps)) nw = 16;  // 4-wave kernels: <= 8 steps, <= 4 units
     int64_t grid = w->ntiles;
     if (nw == 16) {
         int cus = 256;
@@ -567,7 +573,7 @@ size_t lds_bytes(const llmq_mat *w, const Plan &p) {
 
 template <int BITS, int NW, bool LN, int UPT, int STEPS>
 void launch_t(llmq_ctx *ctx, const Gemv1Args &a, int grid, size_t lds, int win) {
-    if constexpr (!LN && UPT == 1) {
+    if constexpr (!LN) {
         if (a.dbg) {
             hipLaunchKernelGGL((gemv1_kernel<BITS, NW, LN, UPT, STEPS, STEPS, true>), dim3((unsigned)grid),
                                dim3(NW * 64), lds, ctx->stream, a);
@@ -590,7 +596,7 @@ int launch_steps(llmq_ctx *ctx, const Gemv1Args &a, const Plan &p, size_t lds) {
     switch (p.steps) {
         case 2: launch_t<BITS, NW, LN, UPT, 2>(ctx, a, p.grid, lds, p.win); return LLMQ_OK;
         case 4: launch_t<BITS, NW, LN, UPT, 4>(ctx, a, p.grid, lds, p.win); return LLMQ_OK;
-        case 8: if constexpr (NW == 16) { launch_t<BITS, NW, LN, UPT, 8>(ctx, a, p.grid, lds, p.win); return LLMQ_OK; } break;
+        case 8: launch_t<BITS, NW, LN, UPT, 8>(ctx, a, p.grid, lds, p.win); return LLMQ_OK;
     }
     return llmq_set_error(LLMQ_EUNSUPPORTED, "linear: no kernel for %d waves x %d steps", NW, p.steps);
 }
@@ -599,6 +605,8 @@ template <int BITS>
 int launch_bits(llmq_ctx *ctx, const Gemv1Args &a, const Plan &p, size_t lds, bool ln) {
     if (p.nw == 4) {
         if (p.upt == 1) return ln ? launch_steps<BITS, 4, true, 1>(ctx, a, p, lds) : launch_steps<BITS, 4, false, 1>(ctx, a, p, lds);
+        if (!ln && p.upt == 2) return launch_steps<BITS, 4, false, 2>(ctx, a, p, lds);
+        if (!ln && p.upt <= 4) return launch_steps<BITS, 4, false, 4>(ctx, a, p, lds);
     } else if (ln) {
         if (p.upt == 1) return launch_steps<BITS, 16, true, 1>(ctx, a, p, lds);
     } else {

@@ -166,6 +166,29 @@ def test_linear_vs_oracle(gpu, orc, fmt, T, IN, OUT, big):
     assert rel_err(out.cpu().numpy(), want) < REL
 
 
+@pytest.mark.parametrize("fmt", [(4, 32, False), (4, 128, True), (8, 0, False), (4, 0, False)])
+@pytest.mark.parametrize("IN,OUT", [(3072, 768), (4096, 200)])
+def test_linear_four_wave_long_rows(gpu, orc, fmt, IN, OUT, monkeypatch):
+    """4-wave workgroups forced on long rows: one row tile per workgroup,
+    up to 8 steps a wave and up to 4 activation units a thread."""
+    torch, lm, ctx = gpu
+    bits, group, sym = fmt
+    monkeypatch.setenv("LLMQ_GEMV1_NW", "4")
+    rng = np.random.default_rng(IN + OUT + bits + group)
+    w = rng.uniform(-0.1, 0.1, (IN, OUT)).astype(np.float32)
+    x = rng.uniform(-1, 1, (1, IN)).astype(np.float32)
+    b = rng.uniform(-1, 1, OUT).astype(np.float32)
+    note("four-wave linear", fmt, IN, OUT)
+    g = lm.HipQuantMatrix.from_f32(ctx, w, bits, group, sym, True)
+    o = orc.QuantMatrix.from_f32(w, bits, group, sym, True)
+    out = torch.zeros((1, OUT), dtype=torch.float32, device="cuda")
+    lm.linear(ctx, out, dev(torch, x), g, dev(torch, b), resid=True)
+    torch.cuda.synchronize()
+    want = orc.matmul_rows_a16(x, o, b, orc.EPI_BIAS | orc.EPI_RESID, out=np.zeros((1, OUT), np.float32))
+    assert rel_err(out.cpu().numpy(), want) < REL
+    g.free()
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_prompt_gemm_matches_tile_order(gpu, orc, bits):
     """The matrix-core GEMM forms each group's exact int32 sum and folds it

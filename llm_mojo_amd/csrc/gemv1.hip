@@ -527,13 +527,11 @@ int steps_for(int spw) { return spw <= 2 ? 2 : spw <= 4 ? 4 : 8; }
 Plan make_plan(const llmq_mat *w) {
     Plan p{};
     const int S = (int)((w->CK + 3) / 4);
-    const int64_t work = w->ntiles * (int64_t)S;  // wave steps of 1 KiB
     const int units = (int)(w->k / 4);           // four activations per thread
     // 16-wave workgroups for matrices streamed from HBM (with the code-step
     // window below); 4-wave workgroups of one row tile otherwise, which
     // launch faster (measured: 3072x768 5.08 -> 4.84 us, 4096x4096 5.70 ->
     // 5.33 us against 16 waves).
-    (void)work;
     int nw = w->ntiles * w->CK * 256 >= kStreamBytes ? 16 : 4;
     if (const char *e = getenv("LLMQ_GEMV1_NW")) {
         const int v = atoi(e);

@@ -545,12 +545,10 @@ int max_steps(const llmq_mat *w) {
 Plan make_plan(const llmq_mat *w) {
     Plan p{};
     const int S = (int)((w->CK + 3) / 4);
-    const int64_t work = w->ntiles * (int64_t)S;
     // 16 waves for matrices streamed from HBM or with more than 4 steps a
     // wave in one tile; 4-wave workgroups of one row tile otherwise (they
     // launch faster; with 8 steps a wave the K-quants' decode work runs one
     // wave per SIMD and is slower: Q5_K 4096x4096 7.22 -> 7.84 us).
-    (void)work;
     int nw = w->ntiles * w->CK * 256 >= kStreamBytes ? 16 : 4;
     if (const char *e = getenv("LLMQ_GEMV1_NW")) {
         const int v = atoi(e);

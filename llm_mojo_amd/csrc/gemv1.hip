@@ -516,10 +516,11 @@ constexpr int kStreamWin = 2;
 
 int steps_for(int spw) { return spw <= 2 ? 2 : spw <= 4 ? 4 : 8; }
 
-// Workgroup shape for a matrix.  Matrices below kStreamBytes of codes:
-// 4-wave workgroups, one row tile each (up to 8 steps a wave and 4
-// activation units a thread; longer rows fall back to 16 waves).  Large
-// (HBM-streamed) matrices: 16-wave workgroups, one per CU, each with a
+// Workgroup shape for a matrix.  Matrices below kStreamBytes of codes, or
+// with short rows (at most 4 steps a wave in one tile): 4-wave workgroups,
+// one row tile each (up to 8 steps a wave and 4 activation units a thread;
+// longer rows fall back to 16 waves).  Large long-row (HBM-streamed)
+// matrices: 16-wave workgroups, one per CU, each with a
 // contiguous run of whole tiles (so CUs differ by at most one tile of work)
 // and the per-workgroup prologue spread over 1024 threads.  Each wave holds
 // at most kMaxSteps steps and crosses at most one tile boundary; past that,
@@ -528,11 +529,12 @@ Plan make_plan(const llmq_mat *w) {
     Plan p{};
     const int S = (int)((w->CK + 3) / 4);
     const int units = (int)(w->k / 4);           // four activations per thread
-    // 16-wave workgroups for matrices streamed from HBM (with the code-step
-    // window below); 4-wave workgroups of one row tile otherwise, which
-    // launch faster (measured: 3072x768 5.08 -> 4.84 us, 4096x4096 5.70 ->
-    // 5.33 us against 16 waves).
-    int nw = w->ntiles * w->CK * 256 >= kStreamBytes ? 16 : 4;
+    // 16-wave workgroups for long-row matrices streamed from HBM (with the
+    // code-step window below); 4-wave workgroups of one row tile otherwise,
+    // which launch faster (measured against 16 waves: 3072x768 5.08 ->
+    // 4.84 us, 4096x4096 5.70 -> 5.33 us, the 50257x768 int8 head 14.1 ->
+    // 10.8 us from HBM).
+    int nw = (w->ntiles * w->CK * 256 >= kStreamBytes && (S + 3) / 4 > 4) ? 16 : 4;
     if (const char *e = getenv("LLMQ_GEMV1_NW")) {
         const int v = atoi(e);
         if (v == 4 || v == 16) nw = v;

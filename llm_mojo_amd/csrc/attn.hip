@@ -269,8 +269,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint4 *__restrict__ co
                                                     float *__restrict__ x, const ArgmaxPart *__restrict__ parts,
                                                     int nparts, int64_t *__restrict__ gen, int *__restrict__ state,
                                                     int do_embed, int64_t n_rows) {
-    __shared__ float bv[256];
-    __shared__ int bi[256];
+    __shared__ float bv[4];  // per wave (256 threads)
+    __shared__ int bi[4];
     __shared__ int64_t s_tok;
     __shared__ int s_pos;
     const int tid = threadIdx.x, t = blockIdx.x;
@@ -284,21 +284,28 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint4 *__restrict__ co
                 idx = c.idx;
             }
         }
-        bv[tid] = v;
-        bi[tid] = idx;
-        __syncthreads();
-        for (int off = 128; off > 0; off >>= 1) {
-            if (tid < off) {
-                float ov = bv[tid + off];
-                int oi = bi[tid + off];
-                if (ov > bv[tid] || (ov == bv[tid] && oi < bi[tid])) {
-                    bv[tid] = ov;
-                    bi[tid] = oi;
-                }
+        // Within each wave by shuffles, then over the four waves in order
+        // (the larger value wins, equal values keep the smaller index).
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(v, off);
+            const int oi = __shfl_xor(idx, off);
+            if (ov > v || (ov == v && oi < idx)) {
+                v = ov;
+                idx = oi;
             }
-            __syncthreads();
         }
+        if ((tid & 63) == 0) {
+            bv[tid >> 6] = v;
+            bi[tid >> 6] = idx;
+        }
+        __syncthreads();
         if (tid == 0) {
+            for (int w = 1; w < 4; w++)
+                if (bv[w] > bv[0] || (bv[w] == bv[0] && bi[w] < bi[0])) {
+                    bv[0] = bv[w];
+                    bi[0] = bi[w];
+                }
             const int step = state[1] + 1;
             const int pos = state[0] + 1;
             gen[step] = bi[0];

@@ -277,12 +277,19 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint4 *__restrict__ co
     if (parts) {
         float v = -INFINITY;
         int idx = 0x7fffffff;
-        for (int p = tid; p < nparts; p += 256) {
-            ArgmaxPart c = parts[p];
-            if (c.v > v || (c.v == v && c.idx < idx)) {
-                v = c.v;
-                idx = c.idx;
-            }
+        // Sixteen partials a thread per round (one round for 4096), all
+        // loads issued before the compares; indices past the end re-read
+        // the last partial, which cannot change the result.
+        for (int p0 = tid; p0 < nparts; p0 += 256 * 16) {
+            ArgmaxPart c[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) c[k] = parts[min(p0 + 256 * k, nparts - 1)];
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (c[k].v > v || (c[k].v == v && c[k].idx < idx)) {
+                    v = c[k].v;
+                    idx = c[k].idx;
+                }
         }
         // Within each wave by shuffles, then over the four waves in order
         // (the larger value wins, equal values keep the smaller index).

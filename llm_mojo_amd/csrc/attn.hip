@@ -179,7 +179,7 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float tot = 0.0f;
     for (int s = tid; s < npos; s += kAttnThreads) {
-        const float e = expf(scores[s] - mx);
+        const float e = ref_expf(scores[s] - mx);
         scores[s] = e;
         tot += e;
     }
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
         mx = row16_max(mx);
         float t = 0.0f;
         for (int s = li; s <= qlast && qi < nq; s += 16) {
-            const float e = expf(S[qi * LT + s] - mx);
+            const float e = ref_expf(S[qi * LT + s] - mx);
             S[qi * LT + s] = e;
             t += e;
         }

@@ -227,3 +227,67 @@ __device__ __forceinline__ int llmq_to_int(float r) {
     if (r < -1.0e9f) return -1000000000;
     return (int)r;
 }
+
+// ------------------------------------------------------ exp, tanh and GELU
+// The float path's exp (attend_float_one's softmax, kvcache.mojo:131-138)
+// and tanh (store_out's GELU, kernels.mojo:43-45), written out so that every
+// kernel computes them with the same operations:
+//
+//   exp(x): Cody and Waite's reduction x = n ln2 + r (n = rint(x log2 e), ln2
+//   split into a 24-bit head and a tail, both products exact inside the
+//   fma), then e^r = 1 + r + r^2 P(r) with P of degree 4 fitted by weighted
+//   least squares at 4000 Chebyshev nodes on [-0.35, 0.35], evaluated by
+//   Horner's rule in fma, then scaled by 2^n through the exponent bits.
+//   Results stay normal: x < -87 returns 0 and x > 88.5 infinity.  Error
+//   under 1 ulp of the float64 exp over [-87, 88].
+//
+//   tanh(y): below |y| = 0.625, y + y^3 Q(y^2) with Q of degree 5 fitted the
+//   same way; above, 1 - 2 / (exp(2|y|) + 1) with the sign of y (no
+//   cancellation there: the quotient is below 0.45); 1 from |y| = 10.  Error
+//   under 1.3 ulp of the float64 tanh.
+//
+// Both are compiled with -ffp-contract=off: each operation rounds as
+// written.
+__device__ __forceinline__ float ref_expf(float x) {
+    if (x > 88.5f) return __builtin_huge_valf();
+    if (!(x >= -87.0f)) return x != x ? x : 0.0f;
+    const float n = rintf(x * 1.44269502f);
+    float r = fmaf(-n, 0.693145752f, x);
+    r = fmaf(-n, 1.42860677e-06f, r);
+    float p = 0.0013748823f;
+    p = fmaf(p, r, 0.008369628f);
+    p = fmaf(p, r, 0.041669644f);
+    p = fmaf(p, r, 0.16666512f);
+    p = fmaf(p, r, 0.49999988f);
+    const float r2 = r * r;
+    p = fmaf(p, r2, r);
+    p = p + 1.0f;
+    return p * __uint_as_float((uint32_t)((int)n + 127) << 23);
+}
+__device__ __forceinline__ float ref_tanhf(float y) {
+    const float a = fabsf(y);
+    if (a < 0.625f) {
+        const float s = y * y;
+        float p = 0.002148991f;
+        p = fmaf(p, s, -0.00818467f);
+        p = fmaf(p, s, 0.021704003f);
+        p = fmaf(p, s, -0.053947456f);
+        p = fmaf(p, s, 0.13333212f);
+        p = fmaf(p, s, -0.3333333f);
+        return fmaf(p * s, y, y);
+    }
+    const float t = a >= 10.0f ? 1.0f : 1.0f - 2.0f / (ref_expf(2.0f * a) + 1.0f);
+    return copysignf(t, y);
+}
+// GELU of kernels.store_out / finish (kernels.mojo:43-45, 277-279),
+// operation by operation: 0.5 r (1 + tanh(s (r + ((0.044715 r) r) r))).
+__device__ __forceinline__ float gelu_ref(float r) {
+    const float s = 0.7978845608028654f;
+    float t = 0.044715f * r;
+    t = t * r;
+    t = t * r;
+    const float u = r + t;
+    const float th = ref_tanhf(s * u);
+    const float h = 0.5f * r;
+    return h * (1.0f + th);
+}

@@ -65,17 +65,6 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__device__ __forceinline__ float gelu_f(float r) {
-    const float s = 0.7978845608028654f;
-    float t = 0.044715f * r;
-    t = t * r;
-    t = t * r;
-    float u = r + t;
-    float th = tanhf(s * u);
-    float h = 0.5f * r;
-    return h * (1.0f + th);
-}
-
 // ------------------------------------------------------------ activations
 
 __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
@@ -409,7 +398,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
         if (tok >= a.T) continue;
         float v = c.acc[i] * L.sx[ml];
         if (a.flags & LLMQ_BIAS) v += bo;
-        if (a.flags & LLMQ_GELU) v = gelu_f(v);
+        if (a.flags & LLMQ_GELU) v = gelu_ref(v);
         float *dst = a.out + (int64_t)tok * a.ldo + o;
         if (a.flags & LLMQ_RESID) v += *dst;
         *dst = v;

@@ -134,18 +134,6 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return s;
 }
 
-// GELU of kernels.store_out (kernels.mojo:43-45), operation by operation.
-__device__ __forceinline__ float gelu_f(float r) {
-    const float s = 0.7978845608028654f;
-    float t = 0.044715f * r;
-    t = t * r;
-    t = t * r;
-    float u = r + t;
-    float th = tanhf(s * u);
-    float h = 0.5f * r;
-    return h * (1.0f + th);
-}
-
 // Unit u = threadIdx.x + NT * i holds four consecutive activations
 // x[4u..4u+3]; units past the row hold zeros.
 template <int NT, int UPT>
@@ -470,7 +458,7 @@ __global__ __launch_bounds__(NW * 64) void gemv1_kernel(Gemv1Args a) {
         if (row_ok) {
             v = v * sx;
             if (a.flags & LLMQ_BIAS) v += e_bias;
-            if (a.flags & LLMQ_GELU) v = gelu_f(v);
+            if (a.flags & LLMQ_GELU) v = gelu_ref(v);
             if (a.flags & LLMQ_RESID) v += e_res;
             a.out[o] = v;
             best_v = v;

@@ -82,18 +82,6 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// GELU of kernels.store_out (kernels.mojo:43-45), operation by operation.
-__device__ __forceinline__ float gelu_f(float r) {
-    const float s = 0.7978845608028654f;
-    float t = 0.044715f * r;
-    t = t * r;
-    t = t * r;
-    float u = r + t;
-    float th = tanhf(s * u);
-    float h = 0.5f * r;
-    return h * (1.0f + th);
-}
-
 // Activations of one token row in registers: unit u = tid + 256 * i holds
 // VPT consecutive values (one plane dword of the int4 / int8 layout).
 template <int VPT, int UPT>
@@ -382,7 +370,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             if (tok >= a.T) break;
             float v = acc[t] * s_sx[t];
             if (a.flags & LLMQ_BIAS) v += MT == 1 ? e_bias : a.bias[o];
-            if (a.flags & LLMQ_GELU) v = gelu_f(v);
+            if (a.flags & LLMQ_GELU) v = gelu_ref(v);
             float *dst = a.out + (size_t)tok * a.ldo + o;
             if (a.flags & LLMQ_RESID) v += MT == 1 ? e_res : *dst;
             if (j == 0) *dst = v;

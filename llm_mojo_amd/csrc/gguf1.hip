@@ -487,13 +487,7 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
         }
         if (row_ok) {
             if (a.flags & LLMQ_BIAS) v += e_bias;
-            if (a.flags & LLMQ_GELU) {
-                const float sg = 0.7978845608028654f;
-                float t = 0.044715f * v;
-                t = t * v;
-                t = t * v;
-                v = (0.5f * v) * (1.0f + tanhf(sg * (v + t)));
-            }
+            if (a.flags & LLMQ_GELU) v = gelu_ref(v);
             if (a.flags & LLMQ_RESID) v += e_res;
             a.out[o] = v;
             best_v = v;

@@ -144,17 +144,6 @@ __device__ __forceinline__ void decode_chunk(const GArgs &a, uint32_t tile, uint
     }
 }
 
-__device__ __forceinline__ float gelu_f(float r) {
-    const float s = 0.7978845608028654f;
-    float t = 0.044715f * r;
-    t = t * r;
-    t = t * r;
-    float u = r + t;
-    float th = tanhf(s * u);
-    float h = 0.5f * r;
-    return h * (1.0f + th);
-}
-
 template <int TYPE, int NW>
 __global__ __launch_bounds__(NW * 64) void gguf_gemm_kernel(GArgs a) {
     constexpr int WPC = TYPE == LLMQ_GGML_Q8_0 || TYPE == kQmFloat8 ? 16 : 32;
@@ -200,7 +189,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_gemm_kernel(GArgs a) {
         const int o = (int)tile * 16 + rr, tk = t0 + tt;
         if (o < a.n && tk < a.T) {
             if (a.flags & LLMQ_BIAS) v += a.bias[o];
-            if (a.flags & LLMQ_GELU) v = gelu_f(v);
+            if (a.flags & LLMQ_GELU) v = gelu_ref(v);
             float *dst = a.out + (int64_t)tk * a.ldo + o;
             if (a.flags & LLMQ_RESID) v += *dst;
             *dst = v;

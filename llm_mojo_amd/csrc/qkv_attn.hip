@@ -296,7 +296,7 @@ __global__ __launch_bounds__(kNT) void qkv_attn_kernel(QkvAttnArgs a) {
     const float mx = block_max(sc_mine, red);
     float ex = 0.0f;
     if (tid < npos) {
-        ex = expf(sc_mine - mx);
+        ex = ref_expf(sc_mine - mx);
         scores[tid] = ex;
     }
     const float total = block_sum(ex, red);

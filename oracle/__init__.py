@@ -76,6 +76,11 @@ I32 = ctypes.c_int
 def _declare(L):
     sig = {
         "orc_set_round_half_even": (None, [I32]),
+        "orc_exp": (ctypes.c_float, [ctypes.c_float]),
+        "orc_tanh": (ctypes.c_float, [ctypes.c_float]),
+        "orc_exp_n": (None, [P, P, I64]),
+        "orc_tanh_n": (None, [P, P, I64]),
+        "orc_gelu_n": (None, [P, P, I64]),
         "orc_set_threads": (None, [I32]),
         "orc_get_threads": (I32, []),
         "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
@@ -253,6 +258,28 @@ def nibble_layout(blocked, cols):
         chunk = cols // 32
         j = cols % 32
     return chunk * 16 + j % 16, j >= 16
+
+
+def _map_f32(fn, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    getattr(lib(), fn)(ptr(x), ptr(y), x.size)
+    return y
+
+
+def ref_exp(x):
+    """The float path's exp (orc_exp), elementwise."""
+    return _map_f32("orc_exp_n", x)
+
+
+def ref_tanh(x):
+    """The float path's tanh (orc_tanh), elementwise."""
+    return _map_f32("orc_tanh_n", x)
+
+
+def gelu(x):
+    """store_out's GELU (kernels.mojo:43-45) on the oracle's tanh."""
+    return _map_f32("orc_gelu_n", x)
 
 
 def quantize_rows(x):

@@ -21,8 +21,11 @@
  *     default half-away-from-zero, switchable with orc_set_round_half_even.
  *   - order of SIMD.reduce_add / reduce_max: parity unpinned; emulated as a
  *     halving tree (lanes 0-7 + 8-15, ...).  Moves fp32 bits only.
- *   - last-ulp results of Mojo's exp / tanh: parity unpinned; libm's expf and
- *     tanhf are used.  Moves fp32 bits only.
+ *   - last-ulp results of Mojo's exp / tanh: parity unpinned (Mojo 1.1
+ *     stdlib absent).  The float path's exp and tanh are this build's own
+ *     (orc_exp / orc_tanh below, the same method as the HIP product), so the
+ *     oracle and the GPU round alike; tests pin them against float64 exp and
+ *     tanh (under 1 and 1.3 ulp).
  */
 #include <math.h>
 #include <stdint.h>
@@ -123,6 +126,59 @@ static inline void dot_pairs(int32_t *acc, const int16_t *a, const int16_t *b) {
     }
 }
 
+/* exp and tanh for the float path (attend_float_one's softmax,
+ * kvcache.mojo:131-138; store_out's GELU, kernels.mojo:43-45).  Method:
+ * exp by Cody and Waite's reduction x = n ln2 + r (n = rint(x log2 e), ln2 as
+ * a 24-bit head plus a tail, each product exact inside fmaf), e^r = 1 + r +
+ * r^2 P(r), P of degree 4 from a weighted least-squares fit at 4000
+ * Chebyshev nodes on [-0.35, 0.35], Horner's rule in fmaf, times 2^n through
+ * the exponent bits; x < -87 gives 0 (no subnormals), x > 88.5 infinity.
+ * tanh: y + y^3 Q(y^2) below |y| = 0.625 (Q of degree 5, fitted the same
+ * way), else 1 - 2 / (exp(2|y|) + 1) with y's sign, and 1 from |y| = 10. */
+static inline float f32_from_bits(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+float orc_exp(float x) {
+    if (x > 88.5f) return INFINITY;
+    if (!(x >= -87.0f)) return x != x ? x : 0.0f;
+    float n = rintf(x * 1.44269502f);
+    float r = fmaf(-n, 0.693145752f, x);
+    r = fmaf(-n, 1.42860677e-06f, r);
+    float p = 0.0013748823f;
+    p = fmaf(p, r, 0.008369628f);
+    p = fmaf(p, r, 0.041669644f);
+    p = fmaf(p, r, 0.16666512f);
+    p = fmaf(p, r, 0.49999988f);
+    float r2 = r * r;
+    p = fmaf(p, r2, r);
+    p = p + 1.0f;
+    return p * f32_from_bits((uint32_t)((int)n + 127) << 23);
+}
+float orc_tanh(float y) {
+    float a = fabsf(y);
+    if (a < 0.625f) {
+        float s = y * y;
+        float p = 0.002148991f;
+        p = fmaf(p, s, -0.00818467f);
+        p = fmaf(p, s, 0.021704003f);
+        p = fmaf(p, s, -0.053947456f);
+        p = fmaf(p, s, 0.13333212f);
+        p = fmaf(p, s, -0.3333333f);
+        return fmaf(p * s, y, y);
+    }
+    float t = a >= 10.0f ? 1.0f : 1.0f - 2.0f / (orc_exp(2.0f * a) + 1.0f);
+    return copysignf(t, y);
+}
+
+void orc_exp_n(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = orc_exp(x[i]);
+}
+void orc_tanh_n(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = orc_tanh(x[i]);
+}
+
 /* kernels.finish (274-282) / store_out (38-48): GELU, residual, store. */
 #define EPI_BIAS 1
 #define EPI_GELU 2
@@ -133,9 +189,12 @@ static inline float gelu_f(float r) {
     t = t * r;
     t = t * r;
     float u = r + t;
-    float th = tanhf(s * u);
+    float th = orc_tanh(s * u);
     float a = 0.5f * r;
     return a * (1.0f + th);
+}
+void orc_gelu_n(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = gelu_f(x[i]);
 }
 static inline void finish(float *o, int64_t i, float r, int flags) {
     if (flags & EPI_GELU) r = gelu_f(r);
@@ -954,7 +1013,7 @@ void orc_kv_attend_one(const orc_kv *kv, float *out, const float *qkv, int layer
         scores[s] = sc;
         mx = sc > mx ? sc : mx;
     }
-    for (int s = 0; s < npos; s++) scores[s] = expf(scores[s] - mx);
+    for (int s = 0; s < npos; s++) scores[s] = orc_exp(scores[s] - mx);
     float total = 0.0f;
     for (int s = 0; s < npos; s++) total += scores[s];
     float *o = out + (int64_t)t * C + h * HS;

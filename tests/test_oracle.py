@@ -461,3 +461,47 @@ def test_argmax_first_max_wins(orc):
     a = np.zeros(50257, np.float32)
     a[[7, 9, 50000]] = 3.0
     assert orc.argmax(a) == 7
+
+
+# -------------------------------------------------------- exp, tanh, GELU
+
+def _ulps(got, want64):
+    """|got - want| in units of the float32 spacing at want."""
+    sp = np.spacing(np.abs(want64).astype(np.float32)).astype(np.float64)
+    return np.abs(got.astype(np.float64) - want64) / sp
+
+
+def test_exp_within_one_ulp_of_float64(orc):
+    """orc_exp (the float path's softmax exp) against float64 exp over the
+    range softmax feeds it and beyond, plus its special values."""
+    x = np.concatenate([np.linspace(-87.0, 88.0, 3_000_001), np.linspace(-1, 1, 200_001)]).astype(np.float32)
+    got = orc.ref_exp(x)
+    assert _ulps(got, np.exp(x.astype(np.float64))).max() < 1.0
+    assert orc.ref_exp(np.float32([0.0]))[0] == 1.0
+    assert orc.ref_exp(np.float32([-87.5, -1e30, -np.inf]))[:].tolist() == [0.0, 0.0, 0.0]
+    assert np.isinf(orc.ref_exp(np.float32([89.0]))[0]) and np.isnan(orc.ref_exp(np.float32([np.nan]))[0])
+    # monotone on a fine grid (a dropped term or a wrong reduction breaks it)
+    g = orc.ref_exp(np.linspace(-20, 20, 400_001).astype(np.float32))
+    assert np.all(np.diff(g.astype(np.float64)) >= 0)
+
+
+def test_tanh_within_ulps_of_float64(orc):
+    x = np.concatenate([np.linspace(-12, 12, 2_400_001), np.linspace(-0.7, 0.7, 200_001),
+                        np.float32([1e-30, -1e-30, 0.0, 0.625, -0.625, 10.0, 50.0])]).astype(np.float32)
+    got = orc.ref_tanh(x)
+    assert _ulps(got, np.tanh(x.astype(np.float64))).max() < 1.5
+    assert np.array_equal(orc.ref_tanh(-x), -got)  # odd
+    assert orc.ref_tanh(np.float32([10.0, 1e6]))[:].tolist() == [1.0, 1.0]
+
+
+def test_gelu_closed_form(orc):
+    """store_out's GELU (kernels.mojo:43-45) in float64 against the oracle."""
+    r = np.linspace(-12, 12, 200_001).astype(np.float32)
+    r64 = r.astype(np.float64)
+    want = 0.5 * r64 * (1 + np.tanh(0.7978845608028654 * (r64 + 0.044715 * r64 ** 3)))
+    got = orc.gelu(r).astype(np.float64)
+    # 1 + tanh cancels for r << 0 in the reference's own formula, so the
+    # bound there is absolute, in units of |r| * 2^-24.
+    pos = r > 0
+    assert np.max(np.abs(got[pos] - want[pos]) / want[pos]) < 4e-7
+    assert np.max(np.abs(got - want) / (np.maximum(np.abs(r64), 1.0) * 2.0 ** -24)) < 4.0

@@ -181,6 +181,12 @@ LLMQ_API int llmq_layernorm(llmq_ctx *ctx, float *out, const float *x, const flo
  * chunk_sums has OUT * IN / (bits == 4 ? 32 : 16) int32 entries. */
 LLMQ_API int llmq_debug_chunk_sums(llmq_ctx *ctx, const float *xf, const llmq_mat *w, float *out, int32_t *chunk_sums,
                                    int16_t *xq, float *sx);
+/* Parity/debug: the float path's exp (op 0, attend_float_one's softmax,
+ * kvcache.mojo:131-138), tanh (op 1) and GELU (op 2, store_out,
+ * kernels.mojo:43-45) as every kernel computes them, elementwise over n
+ * device floats x into y.  No reference counterpart (the reference calls
+ * Mojo's exp / tanh); for bit-for-bit checks against the oracle. */
+LLMQ_API int llmq_debug_refmath(llmq_ctx *ctx, int op, const float *x, float *y, int64_t n);
 
 /* ------------------------------------------------------ int8 KV cache */
 
@@ -247,6 +253,13 @@ LLMQ_API int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m);
 /* Model.forward (gpt2t.mojo:329-342): tokens (host) at positions pos0..;
  * the last token's logits [V] into a host buffer when logits != NULL. */
 LLMQ_API int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int pos0, float *logits);
+/* Parity/debug: with codes != NULL (device, 49 * 3072 int16), every later
+ * one-token forward or decode step writes the int16 activation codes of
+ * each linear's input (quantize_rows, kernels.mojo:400-416): slot 4 l + k
+ * for layer l's qkv, proj, fc and fcproj (k = 0..3), slot 48 for the head,
+ * 3072 entries a slot (the first IN used).  NULL stops it.  No reference
+ * counterpart; it measures the int16 code-flip rate against the oracle. */
+LLMQ_API int llmq_gpt2_debug_codes(llmq_gpt2 *m, int16_t *codes);
 /* generate with -t 0 (gpt2t.mojo:929-1009): the prompt forward, then up to
  * `steps` greedy tokens (argmax, first maximum wins, gpt2t.mojo:792-797),
  * each fed back as the next input, entirely on the device.  Writes the

@@ -50,6 +50,8 @@ SIGNATURES = {
     "llmq_head": (I32, [P, P, P, P, I64, I64, I64]),
     "llmq_layernorm": (I32, [P, P, P, P, P, I64, I64]),
     "llmq_debug_chunk_sums": (I32, [P, P, P, P, P, P, P]),
+    "llmq_debug_refmath": (I32, [P, I32, P, P, I64]),
+    "llmq_gpt2_debug_codes": (I32, [P, P]),
     "llmq_kv_create": (I32, [P, I32, I32, I32, I32, PP]),
     "llmq_kv_free": (I32, [P]),
     "llmq_kv_nbytes": (I64, [P]),

@@ -466,6 +466,27 @@ int llmq_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, co
     return launch_layernorm(ctx, out, x, w, b, T, C);
 }
 
+}  // extern "C"
+
+namespace {
+__global__ void refmath_kernel(int op, const float *__restrict__ x, float *__restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    y[i] = op == 0 ? ref_expf(v) : (op == 1 ? ref_tanhf(v) : gelu_ref(v));
+}
+}  // namespace
+
+extern "C" {
+
+int llmq_debug_refmath(llmq_ctx *ctx, int op, const float *x, float *y, int64_t n) {
+    LLMQ_REQUIRE(ctx && x && y && n >= 0 && op >= 0 && op <= 2, "debug_refmath: bad arguments");
+    if (n == 0) return LLMQ_OK;
+    hipLaunchKernelGGL(refmath_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, op, x, y, n);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
 int llmq_debug_chunk_sums(llmq_ctx *ctx, const float *xf, const llmq_mat *w, float *out, int32_t *chunk_sums,
                           int16_t *xq, float *sx) {
     LLMQ_REQUIRE(ctx && w, "debug_chunk_sums: bad arguments");
@@ -602,6 +623,11 @@ static int gpt2_linear(llmq_gpt2 *m, const GemvRequest &rq) {
     return launch_gguf_gemm(m->ctx, rq.w, x, rq.w->k, rq.T, rq.out, rq.w->n, rq.bias, rq.flags);
 }
 
+// The slot of llmq_gpt2_debug_codes for one linear's input codes.
+static int16_t *dbg_slot(llmq_gpt2 *m, int T, int slot) {
+    return m->dbg_codes && T == 1 ? m->dbg_codes + (int64_t)slot * 4 * C : nullptr;
+}
+
 // Model.blocks (gpt2t.mojo:485-571) for T tokens: tokens in m->tokens when
 // state == nullptr, else one token picked on the device from the previous
 // head's argmax partials (decode), with the position in state[0].
@@ -630,6 +656,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
             q.bias = v[QKV_B];
             q.T = T;
             q.flags = LLMQ_BIAS;
+            q.xq_out = dbg_slot(m, T, 4 * l);
             RC(gpt2_linear(m, q));
             if (T > 1) RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
             RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, pos_dev, 3 * C, T == 1));
@@ -641,6 +668,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
         p.bias = v[PROJ_B];
         p.T = T;
         p.flags = LLMQ_BIAS | LLMQ_RESID;
+        p.xq_out = dbg_slot(m, T, 4 * l + 1);
         RC(gpt2_linear(m, p));
         GemvRequest f;
         f.w = w[2];
@@ -651,6 +679,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
         f.bias = v[FC_B];
         f.T = T;
         f.flags = LLMQ_BIAS | LLMQ_GELU;
+        f.xq_out = dbg_slot(m, T, 4 * l + 2);
         RC(gpt2_linear(m, f));
         GemvRequest g;
         g.w = w[3];
@@ -659,6 +688,7 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
         g.bias = v[FCPROJ_B];
         g.T = T;
         g.flags = LLMQ_BIAS | LLMQ_RESID;
+        g.xq_out = dbg_slot(m, T, 4 * l + 3);
         RC(gpt2_linear(m, g));
     }
     if (!with_head) return LLMQ_OK;
@@ -673,7 +703,14 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
     h.flags = 0;
     h.amax = m->parts;
     h.amax_cap = m->nparts;
-    return gpt2_linear(m, h);
+    h.xq_out = dbg_slot(m, 1, 4 * NL);
+    int written = -1;
+    h.amax_count = &written;
+    RC(gpt2_linear(m, h));
+    // the embed step's argmax reads exactly m->nparts partials
+    LLMQ_REQUIRE(written < 0 || written == m->nparts, "head: %d argmax partials, the model reads %d", written,
+                 m->nparts);
+    return LLMQ_OK;
 }
 
 static void set_fuse_mode(llmq_gpt2 *m, int max_pos);
@@ -717,6 +754,9 @@ int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host) {
     if (!m->gguf) {  // the head's argmax partials for the device-driven decode loop
         m->nparts = m->wte->a16 ? gemv_a16_num_parts(m->wte, true) : gguf_num_parts(m->wte);
         RC(alloc(m->parts, sizeof(ArgmaxPart) * m->nparts));
+        // no stale partial can win an argmax before the first head runs
+        const std::vector<ArgmaxPart> none((size_t)m->nparts, ArgmaxPart{-INFINITY, 0x7fffffff});
+        LLMQ_HIP(hipMemcpy(m->parts, none.data(), sizeof(ArgmaxPart) * m->nparts, hipMemcpyHostToDevice));
     }
     RC(alloc(m->tokens, sizeof(int64_t) * MAXT));
     RC(alloc(m->gen, sizeof(int64_t) * MAXT));
@@ -833,6 +873,19 @@ int64_t llmq_gpt2_weight_bytes(const llmq_gpt2 *m) {
     return n + SMALL_FLOATS * 4;  // gpt2t.mojo:312-319
 }
 
+int llmq_gpt2_debug_codes(llmq_gpt2 *m, int16_t *codes) {
+    LLMQ_REQUIRE(m && !m->gguf, "gpt2_debug_codes: needs a QuantMatrix model");
+    if (m->dbg_codes != codes && m->step_graph) {  // the captured step holds the old pointers
+        LLMQ_HIP(hipStreamSynchronize(m->ctx->stream));
+        LLMQ_HIP(hipGraphExecDestroy(m->step_graph));
+        m->step_graph = nullptr;
+        if (m->step_graph_def) LLMQ_HIP(hipGraphDestroy(m->step_graph_def));
+        m->step_graph_def = nullptr;
+    }
+    m->dbg_codes = codes;
+    return LLMQ_OK;
+}
+
 int llmq_gpt2_forward(llmq_gpt2 *m, const int64_t *tokens, int T, int pos0, float *logits) {
     LLMQ_REQUIRE(m && tokens && T >= 1, "gpt2_forward: bad arguments");
     LLMQ_REQUIRE(pos0 >= 0 && pos0 + T <= MAXT, "gpt2_forward: positions %d..%d beyond %d", pos0, pos0 + T - 1, MAXT);
@@ -919,7 +972,9 @@ static int gpt2g_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int
 // The decode mode for contexts up to max_pos positions; a change drops the
 // captured step graph.
 static void set_fuse_mode(llmq_gpt2 *m, int max_pos) {
-    const int want = m->fuse_env >= 0 ? m->fuse_env : (max_pos > kFuseFrom ? 1 : 0);
+    // The fused kernel's float sums run in another order than the
+    // reference's, so it is the default only with LLMQ_EXACT=0.
+    const int want = m->fuse_env >= 0 ? m->fuse_env : (!exact_order() && max_pos > kFuseFrom ? 1 : 0);
     if (want == m->fuse_qkv_attn) return;
     m->fuse_qkv_attn = want;
     if (m->step_graph) {

@@ -45,8 +45,10 @@ __global__ __launch_bounds__(64) void kv_store_kernel(const float *__restrict__ 
 // attend_float_one (kvcache.mojo:113-150) through QuantKV.score / add_value
 // (344-370) for token t = blockIdx.y (position pos0 + t), head h = blockIdx.x.
 // Scores: q . k over head_dim, times the key's scale, times 1/sqrt(hd); softmax
-// with the running maximum; out = sum_s (p_s * vs_s) * v_s.  The summation
-// order differs from the reference's sequential one (fp32 rounding only).
+// with the running maximum; out = sum_s (p_s * vs_s) * v_s, every float
+// operation in the reference's order: the score's 16 lane partials and
+// halving tree, the total added position by position, and each output
+// dimension's fma chain over positions (one thread per dimension).
 //
 // The thread that scores position s also copies that position's value row
 // and scale into LDS (STAGE), so the value pass reads no global memory.  With
@@ -157,19 +159,31 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
             for (int i = 0; i < NV; i++) kr[i] = *reinterpret_cast<const v4i *>(knew + 16 * i);
             ksr = kscale_new;
         }
-        float d = 0.0f;
+        // QuantKV.score (kvcache.mojo:344-353): 16 lanes d_l += q[16 i + l] *
+        // f32(k[16 i + l]) (multiply, then add), reduce_add, times the key's
+        // scale; then times 1 / sqrt(HD) (attend_float_one, 122-124).
+        float dl[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) dl[e] = 0.0f;
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const int8_t *b = reinterpret_cast<const int8_t *>(&kr[i]);
 #pragma unroll
-            for (int e = 0; e < 16; e++) d = fmaf(q[16 * i + e], (float)b[e], d);
+            for (int e = 0; e < 16; e++) dl[e] = dl[e] + q[16 * i + e] * (float)b[e];
         }
+#pragma unroll
+        for (int e = 0; e < 8; e++) dl[e] = dl[e] + dl[e + 8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) dl[e] = dl[e] + dl[e + 4];
+        dl[0] = dl[0] + dl[2];
+        dl[1] = dl[1] + dl[3];
+        const float d = dl[0] + dl[1];
         if (STAGE && !fresh) {
 #pragma unroll
             for (int i = 0; i < NV; i++) *reinterpret_cast<v4i *>(vrow + (int64_t)s * HD + 16 * i) = vr[i];
             vsc[s] = vsr;
         }
-        const float sc = d * ksr * scale;
+        const float sc = (d * ksr) * scale;
         scores[s] = sc;
         mx = fmaxf(mx, sc);
     }
@@ -177,19 +191,17 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     lds_barrier();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float tot = 0.0f;
-    for (int s = tid; s < npos; s += kAttnThreads) {
-        const float e = ref_expf(scores[s] - mx);
-        scores[s] = e;
-        tot += e;
+    for (int s = tid; s < npos; s += kAttnThreads) scores[s] = ref_expf(scores[s] - mx);
+    lds_barrier();
+    // The total in position order (attend_float_one, 139-141).
+    if (tid == 0) {
+        float t = 0.0f;
+        for (int s = 0; s < npos; s++) t += scores[s];
+        red[0] = t;
     }
-    tot = wave_sum(tot);
     lds_barrier();
-    if ((tid & 63) == 0) red[tid >> 6] = tot;
-    lds_barrier();
-    const float total = ((red[0] + red[1]) + red[2]) + red[3];
-    // Each position's weight p * vs once (p = e / total), in place of the
-    // scores; the value sums below use it as they would have computed it.
+    const float total = red[0];
+    // Each position's weight p * vs (p = e / total; add_value's ps, 366).
     for (int s = tid; s < npos; s += kAttnThreads) {
         float vs;
         if (STAGE)
@@ -201,58 +213,43 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
         scores[s] = (scores[s] / total) * vs;
     }
     lds_barrier();
-    // out[i]: threads split positions into `parts` interleaved subsets.
-    constexpr int parts = kAttnThreads / HD;
-    const int i = tid % HD, part = tid / HD;
-    float acc = 0.0f;
-    for (int s = part; s < npos; s += parts) {
-        const float w = scores[s];
-        if (STAGE) {
-            acc = fmaf(w, (float)vrow[(int64_t)s * HD + i], acc);
-        } else if (STORE && s == cur) {
-            acc = fmaf(w, (float)vnew[i], acc);
-        } else {
-            const int64_t sl = base + (int64_t)s * n_head;
-            acc = fmaf(w, (float)V8[sl * HD + i], acc);
+    // out[i] = acc_i, acc_i = fma(w_s, f32(v_s[i]), acc_i) over positions in
+    // order (add_value, 367-370): one thread per dimension.
+    if (tid < HD) {
+        const int i = tid;
+        float acc = 0.0f;
+        for (int s = 0; s < npos; s++) {
+            const float w = scores[s];
+            int8_t v;
+            if (STAGE)
+                v = vrow[(int64_t)s * HD + i];
+            else if (STORE && s == cur)
+                v = vnew[i];
+            else
+                v = V8[(base + (int64_t)s * n_head) * HD + i];
+            acc = fmaf(w, (float)v, acc);
         }
-    }
-    red[tid] = acc;
-    lds_barrier();
-    if (part == 0) {
-        float v = 0.0f;
-#pragma unroll
-        for (int pp = 0; pp < parts; pp++) v += red[pp * HD + i];
-        out[(int64_t)t * ldo + (int64_t)h * HD + i] = v;
+        out[(int64_t)t * ldo + (int64_t)h * HD + i] = acc;
     }
 }
 
-// LayerNorm over rows of C (kernels.mojo:179-197), one workgroup per row.
+// LayerNorm over rows of C (kernels.mojo:179-197), one workgroup per row,
+// with the statistics in the reference's order (16 lane partials, halving
+// tree) and the output as (x - mean) * rstd * w + b, each operation rounded.
 __global__ __launch_bounds__(256) void layernorm_kernel(float *__restrict__ out, const float *__restrict__ x,
                                                         const float *__restrict__ w, const float *__restrict__ b,
                                                         int64_t C) {
-    __shared__ float red[4];
+    extern __shared__ float xs[];  // [C]
+    __shared__ float bc[2];
     const float *xr = x + (int64_t)blockIdx.x * C;
     float *o = out + (int64_t)blockIdx.x * C;
     const int tid = threadIdx.x;
-    float sum = 0.0f;
-    for (int64_t i = tid; i < C; i += 256) sum += xr[i];
-    sum = wave_sum(sum);
-    if ((tid & 63) == 0) red[tid >> 6] = sum;
-    __syncthreads();
-    const float mean = (((red[0] + red[1]) + red[2]) + red[3]) / (float)C;
-    __syncthreads();
-    float sq = 0.0f;
+    for (int64_t i = tid; i < C; i += 256) xs[i] = xr[i];
+    llmq_lds_barrier();
+    float mean, rstd;
+    llmq_ln_stats(xs, (int)C, bc, mean, rstd);
     for (int64_t i = tid; i < C; i += 256) {
-        float d = xr[i] - mean;
-        sq += d * d;
-    }
-    sq = wave_sum(sq);
-    if ((tid & 63) == 0) red[tid >> 6] = sq;
-    __syncthreads();
-    const float var = (((red[0] + red[1]) + red[2]) + red[3]) / (float)C;
-    const float rstd = 1.0f / sqrtf(var + 1e-5f);
-    for (int64_t i = tid; i < C; i += 256) {
-        float nn = (xr[i] - mean) * rstd;
+        const float nn = (xs[i] - mean) * rstd;
         o[i] = nn * w[i] + b[i];
     }
 }
@@ -602,7 +599,7 @@ int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
     LLMQ_REQUIRE(pos_dev || (pos0 >= 0 && pos0 + T <= kv->max_t), "kv_attend: positions beyond max_t");
     LLMQ_REQUIRE(!store || T == 1, "kv_attend: the fused store takes one token");
     if (kv->integer) return launch_ikv_attend(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
-    if (!store && !pos_dev && T > 1 && kv->head_dim == 64) {
+    if (!store && !pos_dev && T > 1 && kv->head_dim == 64 && !exact_order()) {
         // Prompt: query blocks of 16 per head, scores in LDS up to the last position
         const int C = kv->n_head * kv->head_dim;
         return launch_attend_prompt(ctx, kv->k, kv->v, kv->ks, kv->vs, layer, kv->max_t, kv->n_head, kv->n_head, qkv,
@@ -615,7 +612,8 @@ int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
 
 int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C) {
     LLMQ_REQUIRE(T >= 1 && C >= 1 && out && x && w && b, "layernorm: bad arguments");
-    hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)T), dim3(256), 0, ctx->stream, out, x, w, b, C);
+    LLMQ_REQUIRE(C % 16 == 0 && C <= 16384, "layernorm: C must be a multiple of 16, at most 16384");
+    hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)T), dim3(256), (size_t)C * 4, ctx->stream, out, x, w, b, C);
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }

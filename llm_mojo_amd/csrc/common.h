@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include <string>
 
@@ -149,6 +150,16 @@ bool gemm_mfma_supports(const llmq_mat *w, int64_t T);
 int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *sx);
 int launch_gemv1(llmq_ctx *ctx, const GemvRequest &rq);
 int gemv1_num_parts(const llmq_mat *w, bool ln);
+// One-token kernels in the reference's float order (gemv_exact.hip) for
+// BLOCKED int4-g32-a16 and int8 per-channel A16 matrices; used unless
+// LLMQ_EXACT=0 (then gemv1, whose float sums run in another order).
+bool gemv_exact_supports(const llmq_mat *w);
+int gemv_exact_num_parts(const llmq_mat *w);
+int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq);
+inline bool exact_order() {
+    const char *e = getenv("LLMQ_EXACT");
+    return !(e && e[0] == '0');
+}
 
 // GGUF formats (gguf.hip).
 int gguf_is_supported(int ggml_type);
@@ -290,4 +301,74 @@ __device__ __forceinline__ float gelu_ref(float r) {
     const float th = ref_tanhf(s * u);
     const float h = 0.5f * r;
     return h * (1.0f + th);
+}
+
+// ------------------------------------------- buffer loads and LDS barriers
+// Raw buffer loads from a uniform base: an offset at or past the extent
+// reads zeros without touching memory (how lanes and steps that carry no
+// data are switched off without branches).  Extents stay below 2 GiB.
+constexpr uint32_t kLlmqOOB = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t llmq_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 llmq_bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t llmq_bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t llmq_bload2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t llmq_bload1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+// Workgroup barrier that orders LDS only (global loads stay in flight).
+__device__ __forceinline__ void llmq_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// ---------------------------------------- the reference's float reductions
+// SIMD[f32, 16].reduce_add as a halving tree, lanes (l, l + 8), then
+// (l, l + 4), (l, l + 2), (l, l + 1): each aligned group of 16 lanes holds
+// the 16 values, lane 0 of the group gets the sum (the other lanes hold
+// partial sums).  Float addition is commutative, so which lane of a pair
+// adds is immaterial; the pairing is what fixes the bits.
+__device__ __forceinline__ float llmq_red16(float v) {
+    v = v + __shfl_down(v, 8, 16);
+    v = v + __shfl_down(v, 4, 16);
+    v = v + __shfl_down(v, 2, 16);
+    return v + __shfl_down(v, 1, 16);
+}
+
+// layernorm's statistics (kernels.mojo:179-197) over x[0, C) in LDS, in
+// the reference's order: 16 lane partials s_l = x[l] + x[16 + l] + ...
+// (left to right), mean = reduce_add(s) / C; the same for (x - mean)^2
+// (multiply, then add); rstd = 1 / sqrt(reduce_add / C + 1e-5).  Called by
+// every thread of the workgroup (C a multiple of 16); wave 0 computes, bc
+// (2 floats of LDS) broadcasts.  Ends with a barrier.
+__device__ __forceinline__ void llmq_ln_stats(const float *xs, int C, float *bc, float &mean, float &rstd) {
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x & 15;
+        float s = 0.0f;
+        for (int i = l; i < C; i += 16) s += xs[i];
+        const float m = llmq_red16(s) / (float)C;
+        const float mb = __shfl(m, 0);
+        float q = 0.0f;
+        for (int i = l; i < C; i += 16) {
+            const float d = xs[i] - mb;
+            q += d * d;
+        }
+        const float r = 1.0f / sqrtf(llmq_red16(q) / (float)C + 1e-5f);
+        if (threadIdx.x == 0) {
+            bc[0] = mb;
+            bc[1] = r;
+        }
+    }
+    llmq_lds_barrier();
+    mean = bc[0];
+    rstd = bc[1];
 }

@@ -85,7 +85,8 @@ template <bool LN, int UPT>
 __global__ __launch_bounds__(256) void act_q16_kernel(const float *__restrict__ x, int64_t ldx,
                                                       const float *__restrict__ lw, const float *__restrict__ lb,
                                                       int K, int16_t *__restrict__ xq, float *__restrict__ sx) {
-    __shared__ float red[4];
+    __shared__ float red[4], bc[2];
+    extern __shared__ __align__(16) float xs[];  // [K] with LayerNorm
     const int t = blockIdx.x, tid = threadIdx.x, nunits = K / 4;
     const float4 *xr = reinterpret_cast<const float4 *>(x + (int64_t)t * ldx);
     float4 v[UPT];
@@ -95,19 +96,15 @@ __global__ __launch_bounds__(256) void act_q16_kernel(const float *__restrict__ 
         v[i] = u < nunits ? xr[u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     if (LN) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < UPT; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-        const float mean = block_reduce(s, red, false) / (float)K;
-        float q = 0.0f;
+        // the statistics in layernorm's own order (16 lane partials)
 #pragma unroll
         for (int i = 0; i < UPT; i++) {
-            if (tid + 256 * i >= nunits) continue;
-            const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
-            q += (a * a + b * b) + (c * c + d * d);
+            const int u = tid + 256 * i;
+            if (u < nunits) reinterpret_cast<float4 *>(xs)[u] = v[i];
         }
-        const float var = block_reduce(q, red, false) / (float)K;
-        const float rstd = 1.0f / sqrtf(var + 1e-5f);
+        llmq_lds_barrier();
+        float mean, rstd;
+        llmq_ln_stats(xs, K, bc, mean, rstd);
         const float4 *w4 = reinterpret_cast<const float4 *>(lw), *b4 = reinterpret_cast<const float4 *>(lb);
 #pragma unroll
         for (int i = 0; i < UPT; i++) {
@@ -421,7 +418,7 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     LLMQ_REQUIRE(gemm_mfma_supports(w, T), "linear: no MFMA GEMM for this matrix");
     const int upt = (int)((K / 4 + 255) / 256);
     const bool ln = rq.ln_w != nullptr;
-#define ACTQ(L, U) hipLaunchKernelGGL((act_q16_kernel<L, U>), dim3((unsigned)T), dim3(256), 0, ctx->stream, rq.x, ldx, \
+#define ACTQ(L, U) hipLaunchKernelGGL((act_q16_kernel<L, U>), dim3((unsigned)T), dim3(256), L ? K * 4 : 0, ctx->stream, rq.x, ldx, \
                                        rq.ln_w, rq.ln_b, (int)K, xq, sx)
     if (upt <= 1) {
         if (ln) ACTQ(true, 1); else ACTQ(false, 1);

@@ -469,6 +469,7 @@ size_t lds_bytes(const llmq_mat *w, int mt) {
 }  // namespace
 
 int gemv_a16_num_parts(const llmq_mat *w, bool ln) {
+    if (exact_order() && gemv_exact_supports(w)) return gemv_exact_num_parts(w);
     if (gemv1_supports(w, ln)) return gemv1_num_parts(w, ln);
     const int ks = pick_ks(w, 1);
     const int tpw = 4 / ks;
@@ -485,10 +486,15 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
     LLMQ_REQUIRE(!(rq.flags & LLMQ_BIAS) || rq.bias, "linear: LLMQ_BIAS without a bias");
     LLMQ_REQUIRE(!rq.amax || rq.T == 1, "linear: argmax partials need T == 1");
     LLMQ_REQUIRE(!rq.dbg || (rq.T == 1 && !rq.ln_w), "linear: chunk sums need T == 1 without LayerNorm");
+    // (the int8 head kernel keeps no per-chunk sums: chunk-sum requests for
+    // it take gemv1)
+    if (rq.T == 1 && exact_order() && gemv_exact_supports(w) && !(rq.dbg && w->bits == 8))
+        return launch_gemv_exact(ctx, rq);
     if (rq.T == 1 && gemv1_supports(w, rq.ln_w != nullptr)) return launch_gemv1(ctx, rq);
     {
-        // Prompts: the int8-MFMA GEMM (LN + quantize_rows into workspace first)
-        int min_t = 8;
+        // Prompts: the int8-MFMA GEMM (LN + quantize_rows into workspace
+        // first), whose float steps are tile_i16's, from two tokens on
+        int min_t = exact_order() ? 2 : 8;
         if (const char *e = getenv("LLMQ_MFMA_MIN_T")) min_t = atoi(e);
         if (rq.T >= min_t && min_t > 0 && gemm_mfma_supports(w, rq.T)) {
             const size_t xb = ((size_t)rq.T * w->k * 2 + 255) & ~(size_t)255;

@@ -41,6 +41,9 @@ struct llmq_gpt2 {
     int gguf = 0;
     llmq_mat *lm = nullptr;  // the head when not tied to wte
     float *xn = nullptr;
+    // llmq_gpt2_debug_codes: one-token forwards write each linear's int16
+    // input codes here ([49][3072], slot 4 l + k, 48 the head)
+    int16_t *dbg_codes = nullptr;
 };
 
 // A QuantMatrix format: QuantMatrix[bits, group (0: per channel), sym, A16].

@@ -193,6 +193,14 @@ def debug_chunk_sums(ctx, x, w, out, chunk_sums, xq, sx):
     check(lib().llmq_debug_chunk_sums(ctx.h, dptr(x), w.h, dptr(out), dptr(chunk_sums), dptr(xq), dptr(sx)))
 
 
+REFMATH_OPS = {"exp": 0, "tanh": 1, "gelu": 2}
+
+
+def debug_refmath(ctx, op, x, y):
+    """The kernels' exp / tanh / GELU over device floats x into y."""
+    check(lib().llmq_debug_refmath(ctx.h, REFMATH_OPS[op], dptr(x), dptr(y), x.numel()))
+
+
 class GGUFFile:
     """GGUFFile (gguf.mojo:527-636): a GGUF v2 / v3 file's tensor index over
     a read-only mapping of the file (libllmq's parser, bounds-checked)."""

@@ -168,6 +168,13 @@ class GPT2:
         check(lib().llmq_gpt2_forward(self.h, hptr(toks), len(toks), pos0, hptr(logits)))
         return logits
 
+    def debug_codes(self, codes):
+        """Capture each linear's int16 input codes of later one-token
+        forwards into codes (a device int16 tensor of 49 * 3072, or None to
+        stop): slot 4 l + k for layer l's qkv / proj / fc / fcproj, 48 the
+        head."""
+        check(lib().llmq_gpt2_debug_codes(self.h, None if codes is None else codes.data_ptr()))
+
     def forward_all(self, tokens, logits):
         """Model.forward_all (gpt2t.mojo:448-459): logits for every position
         into logits (device address or torch tensor, [T, V] float32)."""

@@ -124,6 +124,7 @@ def _declare(L):
         "orc_gpt2_new": (P, [P, I32, I32, I32]),
         "orc_gpt2_new_fmt": (P, [P, I32, I32, I32, I32, I32, I32, I32, I32]),
         "orc_gpt2_free": (None, [P]),
+        "orc_gpt2_set_capture": (None, [P, P]),
         "orc_gpt2_set_attention": (None, [P, I32]),
         "orc_gpt2_forward_all": (None, [P, P, I32, P]),
         "orc_score_rows": (None, [P, I64, P, P, P, I32, I32, I32]),
@@ -692,6 +693,12 @@ class GPT2:
         if getattr(self, "h", None):
             lib().orc_gpt2_free(self.h)
             self.h = None
+
+    def set_capture(self, codes):
+        """codes: int16 array of 49 * 3072 (or None): one-token forwards
+        store each linear's input codes there (slot 4 l + k, 48 the head)."""
+        self._capture = codes
+        lib().orc_gpt2_set_capture(self.h, ptr(codes))
 
     def forward(self, tokens, pos0):
         toks = np.ascontiguousarray(tokens, np.int64)

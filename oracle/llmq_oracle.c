@@ -1257,6 +1257,7 @@ typedef struct {
     orc_kv kv;
     int integer; /* 1: IntAttnKV over the same storage (int32 scales in ks / vs) */
     float *x, *xn, *qkv, *att, *fc, *logits;
+    int16_t *capture; /* one-token forwards: each linear's int16 input codes, [49][3072] */
 } orc_gpt2;
 
 static void qm_alloc(orc_qm *m, int bits, int group, int sym, int a16, int64_t n, int64_t k) {
@@ -1391,6 +1392,15 @@ static void linear(float *out, const float *x, const orc_qm *w, const float *b, 
         orc_qm_matmul_rows(out, x, w, b, T, IN, OUT, flags);
 }
 
+/* Test hook: with codes set, one-token forwards store quantize_rows' codes
+ * of every linear's input (slot 4 l + k: qkv, proj, fc, fcproj; 48 the
+ * head; 3072 entries a slot). */
+void orc_gpt2_set_capture(orc_gpt2 *m, int16_t *codes) { m->capture = codes; }
+static void capture(orc_gpt2 *m, int T, int slot, const float *x, int64_t IN) {
+    float sx;
+    if (m->capture && T == 1) orc_quantize_rows(x, 1, IN, m->capture + (int64_t)slot * 3072, &sx);
+}
+
 /* Model.blocks (gpt2t.mojo:485-571): embed tokens at pos0.., all layers. */
 static void gpt2_blocks(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
     const int C = G_C;
@@ -1404,6 +1414,7 @@ static void gpt2_blocks(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
         orc_qm *w = &m->mats[l * 4];
         float **v = &m->vecs[l * N_VECS];
         orc_layernorm(m->xn, m->x, v[LN1_W], v[LN1_B], T, C);
+        capture(m, T, 4 * l, m->xn, C);
         linear(m->qkv, m->xn, &w[0], v[QKV_B], T, C, 3 * C, EPI_BIAS);
         if (m->integer) {
             orc_ikv ik = gpt2_ikv(m);
@@ -1419,9 +1430,12 @@ static void gpt2_blocks(orc_gpt2 *m, const int64_t *tokens, int T, int pos0) {
             }
             orc_kv_attend(&m->kv, m->att, m->qkv, l, T, pos0);
         }
+        capture(m, T, 4 * l + 1, m->att, C);
         linear(m->x, m->att, &w[1], v[PROJ_B], T, C, C, EPI_BIAS | EPI_RESID);
         orc_layernorm(m->xn, m->x, v[LN2_W], v[LN2_B], T, C);
+        capture(m, T, 4 * l + 2, m->xn, C);
         linear(m->fc, m->xn, &w[2], v[FC_B], T, C, 4 * C, EPI_BIAS | EPI_GELU);
+        capture(m, T, 4 * l + 3, m->fc, 4 * C);
         linear(m->x, m->fc, &w[3], v[FCPROJ_B], T, 4 * C, C, EPI_BIAS | EPI_RESID);
     }
 }
@@ -1434,6 +1448,7 @@ const float *orc_gpt2_forward(orc_gpt2 *m, const int64_t *tokens, int T, int pos
     gpt2_blocks(m, tokens, T, pos0);
     const float *last = m->x + (int64_t)(T - 1) * G_C;
     orc_layernorm(m->xn, last, m->lnf_w, m->lnf_b, 1, G_C);
+    capture(m, T, 4 * G_NL, m->xn, G_C);
     linear(m->logits, m->xn, &m->wte, NULL, 1, G_C, G_V, 0);
     return m->logits;
 }

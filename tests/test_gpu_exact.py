@@ -1,0 +1,175 @@
+"""Bit-exact parity of config 0's float path on the GPU: every kernel that
+feeds an int16 activation code, a cache entry or a logit computes the
+oracle's float32 bits exactly (outputs compared with array_equal, not with
+a tolerance).  That is what lets the end-to-end decode
+(tests/test_gpu_gpt2.py) agree token for token: a one-ulp difference
+before quantize_rows can flip an int16 code, and a flipped code moves the
+logits by ~1e-3 of their range.
+
+Covered: the float path's exp / tanh / GELU; LayerNorm (16 lane partials and
+the halving tree of kernels.mojo:179-197); the one-token BLOCKED int4-g32
+GEMV (tensor.mojo:522-540) with and without LayerNorm, GELU and residual;
+the int8 per-channel head (tensor.mojo:541-566) with LN_f; several-token
+GEMMs in tile_i16's order (kernels.mojo:512-573); float attention over the
+int8 cache (attend_float_one, kvcache.mojo:113-150) for decode and prompts.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def note(*a):
+    print(*a, flush=True)
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def same_bits(got, want):
+    got = np.ascontiguousarray(got, np.float32)
+    want = np.ascontiguousarray(want, np.float32)
+    assert got.shape == want.shape
+    diff = got.view(np.uint32) != want.view(np.uint32)
+    if diff.any():
+        i = np.flatnonzero(diff.reshape(-1))[0]
+        raise AssertionError(f"{int(diff.sum())} of {diff.size} values differ, first at {i}: "
+                             f"{got.reshape(-1)[i]!r} vs {want.reshape(-1)[i]!r}")
+
+
+def test_refmath_bit_exact(gpu, orc):
+    torch, lm, ctx = gpu
+    x = np.concatenate([np.linspace(-100, 100, 2_000_001), np.linspace(-1, 1, 200_001),
+                        np.float32([0.0, -0.0, 1e-30, -1e-30, 0.625, -0.625, 10.0, -10.0, 88.5, -87.0, 1e30,
+                                    -1e30, np.inf, -np.inf])]).astype(np.float32)
+    xd = dev(torch, x)
+    yd = torch.empty_like(xd)
+    for op, ref in (("exp", orc.ref_exp), ("tanh", orc.ref_tanh), ("gelu", orc.gelu)):
+        note("refmath", op)
+        lm.debug_refmath(ctx, op, xd, yd)
+        torch.cuda.synchronize()
+        same_bits(yd.cpu().numpy(), ref(x))
+
+
+def test_layernorm_bit_exact(gpu, orc):
+    torch, lm, ctx = gpu
+    rng = np.random.default_rng(5)
+    for T, C, scale in ((1, 768, 1.0), (12, 768, 30.0), (3, 2048, 0.01)):
+        note("layernorm", T, C)
+        x = (rng.normal(0, scale, (T, C)) + rng.normal(0, 3, (T, 1))).astype(np.float32)
+        w = rng.normal(1, 0.1, C).astype(np.float32)
+        b = rng.normal(0, 0.1, C).astype(np.float32)
+        out = torch.zeros((T, C), dtype=torch.float32, device="cuda")
+        lm.layernorm(ctx, out, dev(torch, x), dev(torch, w), dev(torch, b))
+        torch.cuda.synchronize()
+        same_bits(out.cpu().numpy(), orc.layernorm(x, w, b))
+
+
+GEMV_SHAPES = [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 70), (4096, 4096), (4096, 11008)]
+
+
+@pytest.mark.parametrize("IN,OUT", GEMV_SHAPES)
+@pytest.mark.parametrize("mode", ["plain", "ln", "gelu", "resid", "sym"])
+def test_blocked_gemv_bit_exact(gpu, orc, IN, OUT, mode):
+    """One token through the BLOCKED int4-g32-a16 GEMV: exactly the
+    reference's dot_row_i16 * sx (+ bias, GELU, residual)."""
+    torch, lm, ctx = gpu
+    if mode == "ln" and IN != 768:
+        pytest.skip("LayerNorm precedes the 768-input matrices only")
+    rng = np.random.default_rng(IN * 7 + OUT)
+    w = rng.normal(0, 0.02, (IN, OUT)).astype(np.float32)
+    x = rng.normal(0, 1, (1, IN)).astype(np.float32)
+    b = rng.normal(0, 0.1, OUT).astype(np.float32)
+    r0 = rng.normal(0, 1, (1, OUT)).astype(np.float32)
+    sym = mode == "sym"
+    note("blocked gemv", IN, OUT, mode)
+    g = lm.HipQuantMatrix.from_f32(ctx, w, 4, 32, sym, True)
+    o = orc.QuantMatrix.from_f32(w, 4, 32, sym, True)
+    out = dev(torch, r0)
+    if mode == "ln":
+        lw = rng.normal(1, 0.1, IN).astype(np.float32)
+        lb = rng.normal(0, 0.1, IN).astype(np.float32)
+        lm.linear(ctx, out, dev(torch, x), g, dev(torch, b), ln=(dev(torch, lw), dev(torch, lb)))
+        want = orc.matmul_rows_a16(orc.layernorm(x, lw, lb), o, b)
+    else:
+        flags = orc.EPI_BIAS | (orc.EPI_GELU if mode == "gelu" else 0) | (orc.EPI_RESID if mode == "resid" else 0)
+        lm.linear(ctx, out, dev(torch, x), g, dev(torch, b), gelu=mode == "gelu", resid=mode == "resid")
+        want = orc.matmul_rows_a16(x, o, b, flags, out=r0.copy())
+    torch.cuda.synchronize()
+    same_bits(out.cpu().numpy(), want)
+    g.free()
+
+
+@pytest.mark.parametrize("V,C,ln", [(50257, 768, True), (50257, 768, False), (1000, 2048, False), (64, 4096, False)])
+def test_int8_channel_head_bit_exact(gpu, orc, V, C, ln):
+    """The int8 per-channel A16 head (HEAD8_A16): logits = dot_row_i16 * sx,
+    with LN_f fused as in the decode step."""
+    torch, lm, ctx = gpu
+    rng = np.random.default_rng(V + C)
+    wte = rng.normal(0, 0.02, (V, C)).astype(np.float32)
+    h = rng.normal(0, 1, (1, C)).astype(np.float32)
+    note("int8-ch head", V, C, ln)
+    g = lm.HipQuantMatrix.from_f32(ctx, wte, 8, 0, False, True, reduce_rows=False)
+    o = orc.QuantMatrix.from_f32(wte, 8, 0, False, True, reduce_rows=False)
+    out = torch.zeros((1, V), dtype=torch.float32, device="cuda")
+    if ln:
+        lw = rng.normal(1, 0.1, C).astype(np.float32)
+        lb = rng.normal(0, 0.1, C).astype(np.float32)
+        lm.linear(ctx, out, dev(torch, h), g, None, ln=(dev(torch, lw), dev(torch, lb)))
+        want = orc.matmul_rows_a16(orc.layernorm(h, lw, lb), o, None, 0)
+    else:
+        lm.linear(ctx, out, dev(torch, h), g, None)
+        want = orc.matmul_rows_a16(h, o, None, 0)
+    torch.cuda.synchronize()
+    same_bits(out.cpu().numpy(), want)
+    g.free()
+
+
+@pytest.mark.parametrize("fmt", [(4, 32, False), (8, 32, False), (8, 0, False)])
+@pytest.mark.parametrize("T", [2, 3, 5, 7, 12, 33])
+def test_prompt_gemm_bit_exact(gpu, orc, fmt, T):
+    """Several tokens (prompts) in tile_i16's order, GPT-2 layer shapes."""
+    torch, lm, ctx = gpu
+    bits, group, sym = fmt
+    rng = np.random.default_rng(T * 3 + bits)
+    for IN, OUT, flags in ((768, 2304, 0), (3072, 768, 1), (768, 3072, 2)):
+        w = rng.normal(0, 0.02, (IN, OUT)).astype(np.float32)
+        x = rng.normal(0, 1, (T, IN)).astype(np.float32)
+        b = rng.normal(0, 0.1, OUT).astype(np.float32)
+        r0 = rng.normal(0, 1, (T, OUT)).astype(np.float32)
+        note("prompt gemm", fmt, T, IN, OUT, flags)
+        g = lm.HipQuantMatrix.from_f32(ctx, w, bits, group, sym, True)
+        o = orc.QuantMatrix.from_f32(w, bits, group, sym, True)
+        out = dev(torch, r0)
+        lm.linear(ctx, out, dev(torch, x), g, dev(torch, b), resid=flags == 1, gelu=flags == 2)
+        ef = orc.EPI_BIAS | (orc.EPI_RESID if flags == 1 else 0) | (orc.EPI_GELU if flags == 2 else 0)
+        want = orc.matmul_rows_a16(x, o, b, ef, out=r0.copy())
+        torch.cuda.synchronize()
+        same_bits(out.cpu().numpy(), want)
+        g.free()
+
+
+@pytest.mark.parametrize("T,pos0", [(1, 0), (1, 11), (1, 111), (1, 300), (12, 0), (5, 40), (64, 100)])
+def test_attention_bit_exact(gpu, orc, T, pos0):
+    """attend_float_one over the int8 cache: one token (decode) and prompts."""
+    torch, lm, ctx = gpu
+    rng = np.random.default_rng(T * 1000 + pos0)
+    NL, NH, HS, MT = 2, 12, 64, 1024
+    C = NH * HS
+    layer = 1
+    qkv_all = rng.normal(0, 1, (pos0 + T, 3 * C)).astype(np.float32)
+    note("attention", T, pos0)
+    kv = lm.QuantKV8(ctx, NL, MT, NH, HS)
+    okv = orc.QuantKV8(NL, MT, NH, HS)
+    if pos0:
+        kv.store(layer, 0, dev(torch, qkv_all[:pos0]))
+    q1 = dev(torch, qkv_all[pos0:])
+    kv.store(layer, pos0, q1)
+    out = torch.zeros((T, C), dtype=torch.float32, device="cuda")
+    kv.attend(out, q1, layer, pos0)
+    torch.cuda.synchronize()
+    for p in range(pos0 + T):
+        okv.store(layer, p, qkv_all[p, C:2 * C], qkv_all[p, 2 * C:])
+    same_bits(out.cpu().numpy(), okv.attend(qkv_all[pos0:], layer, T, pos0))
+    kv.free()

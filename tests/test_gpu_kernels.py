@@ -27,8 +27,8 @@ def rel_err(got, want):
 
 
 FORMATS = [  # (bits, group, sym)
-    (4, 32, False), (4, 32, True), (4, 64, False), (4, 128, True), (4, 0, False), (8, 32, False), (8, 128, False),
-    (8, 0, False), (8, 0, True),
+    (4, 32, False), (4, 32, True), (4, 64, False), (4, 128, True), (4, 0, False), (8, 32, False), (8, 64, False),
+    (8, 128, False), (8, 0, False), (8, 0, True),
 ]
 
 
@@ -174,6 +174,7 @@ def test_linear_four_wave_long_rows(gpu, orc, fmt, IN, OUT, monkeypatch):
     torch, lm, ctx = gpu
     bits, group, sym = fmt
     monkeypatch.setenv("LLMQ_GEMV1_NW", "4")
+    monkeypatch.setenv("LLMQ_EXACT", "0")  # gemv1 itself (the exact kernels take BLOCKED and int8-ch)
     rng = np.random.default_rng(IN + OUT + bits + group)
     w = rng.uniform(-0.1, 0.1, (IN, OUT)).astype(np.float32)
     x = rng.uniform(-1, 1, (1, IN)).astype(np.float32)

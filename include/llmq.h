@@ -170,6 +170,22 @@ LLMQ_API int llmq_ln_linear(llmq_ctx *ctx, float *out, const float *x, const flo
  * (head_i16, 693-736). */
 LLMQ_API int llmq_head(llmq_ctx *ctx, float *logits, const float *h, const llmq_mat *w, int64_t T, int64_t V,
                        int64_t C);
+/* linear_team's prepared activations (kernels.mojo:774-866: thread 0 runs
+ * quantize_rows and permute_x_i16 once into the team's xq / xp / xs / sx,
+ * then every thread's rows read them): one token's row x[K] (device, after
+ * LayerNorm with ln_w / ln_b when given) quantized to int16 once, into the
+ * caller's device buffer act of llmq_act_bytes(K) bytes, in the forms the
+ * one-token integer GEMVs read (codes, nibble planes, per-half-group and
+ * per-lane sums, the scale).  K a multiple of 32, at most 16384. */
+LLMQ_API int64_t llmq_act_bytes(int64_t K);
+LLMQ_API int llmq_act_prepare(llmq_ctx *ctx, const float *x, int64_t K, const float *ln_w, const float *ln_b,
+                              void *act);
+/* linear_team's rows over prepared activations (kernels.mojo:793-816,
+ * dot_row_i16 * sx + bias, store_out): out[OUT] (+)= act(act @ W^T + bias)
+ * for one token, bit-identical to llmq_linear on the same row.  Takes
+ * int4-g32-a16 (BLOCKED) and int8 per-channel a16 matrices. */
+LLMQ_API int llmq_linear_act(llmq_ctx *ctx, float *out, const void *act, const llmq_mat *w, const float *bias,
+                             int64_t IN, int64_t OUT, int flags);
 /* kernels.layernorm (kernels.mojo:179-197). */
 LLMQ_API int llmq_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T,
                             int64_t C);
@@ -187,6 +203,12 @@ LLMQ_API int llmq_debug_chunk_sums(llmq_ctx *ctx, const float *xf, const llmq_ma
  * device floats x into y.  No reference counterpart (the reference calls
  * Mojo's exp / tanh); for bit-for-bit checks against the oracle. */
 LLMQ_API int llmq_debug_refmath(llmq_ctx *ctx, int op, const float *x, float *y, int64_t n);
+/* Measurement: reads `bytes` (a multiple of 16) of device memory at buf
+ * with `grid` workgroups of 256 threads, eight 128-bit loads in flight per
+ * thread, and writes one XOR of the words per workgroup to out[grid]: the
+ * read rate a kernel with no arithmetic reaches (the GEMV's floor).  No
+ * reference counterpart. */
+LLMQ_API int llmq_debug_read(llmq_ctx *ctx, const void *buf, int64_t bytes, uint32_t *out, int grid);
 
 /* ------------------------------------------------------ int8 KV cache */
 

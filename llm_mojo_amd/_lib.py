@@ -51,6 +51,10 @@ SIGNATURES = {
     "llmq_layernorm": (I32, [P, P, P, P, P, I64, I64]),
     "llmq_debug_chunk_sums": (I32, [P, P, P, P, P, P, P]),
     "llmq_debug_refmath": (I32, [P, I32, P, P, I64]),
+    "llmq_act_bytes": (I64, [I64]),
+    "llmq_debug_read": (I32, [P, P, I64, P, I32]),
+    "llmq_act_prepare": (I32, [P, P, I64, P, P, P]),
+    "llmq_linear_act": (I32, [P, P, P, P, P, I64, I64, I32]),
     "llmq_gpt2_debug_codes": (I32, [P, P]),
     "llmq_kv_create": (I32, [P, I32, I32, I32, I32, PP]),
     "llmq_kv_free": (I32, [P]),

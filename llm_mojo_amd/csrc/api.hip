@@ -461,6 +461,21 @@ int llmq_head(llmq_ctx *ctx, float *logits, const float *h, const llmq_mat *w, i
     return llmq_linear(ctx, logits, h, w, nullptr, T, C, V, 0);
 }
 
+int64_t llmq_act_bytes(int64_t K) { return K >= 32 && K % 32 == 0 ? llmq_act_layout(K).bytes : -1; }
+
+int llmq_act_prepare(llmq_ctx *ctx, const float *x, int64_t K, const float *ln_w, const float *ln_b, void *act) {
+    LLMQ_REQUIRE(ctx, "act_prepare: null context");
+    return launch_act_prepare(ctx, x, K, ln_w, ln_b, act);
+}
+
+int llmq_linear_act(llmq_ctx *ctx, float *out, const void *act, const llmq_mat *w, const float *bias, int64_t IN,
+                    int64_t OUT, int flags) {
+    LLMQ_REQUIRE(ctx && w, "linear_act: null argument");
+    LLMQ_REQUIRE(w->k == IN && w->n == OUT, "linear_act: IN=%lld OUT=%lld but the matrix is %lldx%lld",
+                 (long long)IN, (long long)OUT, (long long)w->k, (long long)w->n);
+    return launch_linear_act(ctx, out, act, w, bias, flags);
+}
+
 int llmq_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C) {
     LLMQ_REQUIRE(ctx, "layernorm: null context");
     return launch_layernorm(ctx, out, x, w, b, T, C);
@@ -469,6 +484,29 @@ int llmq_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, co
 }  // extern "C"
 
 namespace {
+// Streams `n16` 16-byte words with eight 128-bit loads in flight per thread
+// and folds them with XOR into one word per workgroup: the memory system's
+// read rate with no arithmetic to hide (bench.py's read floor).
+__global__ __launch_bounds__(256) void read_kernel(const uint4 *__restrict__ p, int64_t n16,
+                                                   uint32_t *__restrict__ out) {
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t lo = (int64_t)blockIdx.x * per, hi = lo + per < n16 ? lo + per : n16;
+    uint32_t acc = 0;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256 * 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = i + 256 * k < hi ? p[i + 256 * k] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+    __shared__ uint32_t red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 __global__ void refmath_kernel(int op, const float *__restrict__ x, float *__restrict__ y, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -478,6 +516,15 @@ __global__ void refmath_kernel(int op, const float *__restrict__ x, float *__res
 }  // namespace
 
 extern "C" {
+
+int llmq_debug_read(llmq_ctx *ctx, const void *buf, int64_t bytes, uint32_t *out, int grid) {
+    LLMQ_REQUIRE(ctx && buf && out && bytes > 0 && bytes % 16 == 0 && grid >= 1 && grid <= (1 << 20),
+                 "debug_read: bad arguments");
+    hipLaunchKernelGGL(read_kernel, dim3((unsigned)grid), dim3(256), 0, ctx->stream,
+                       static_cast<const uint4 *>(buf), bytes / 16, out);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
 
 int llmq_debug_refmath(llmq_ctx *ctx, int op, const float *x, float *y, int64_t n) {
     LLMQ_REQUIRE(ctx && x && y && n >= 0 && op >= 0 && op <= 2, "debug_refmath: bad arguments");

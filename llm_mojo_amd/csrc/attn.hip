@@ -195,8 +195,17 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
     lds_barrier();
     // The total in position order (attend_float_one, 139-141).
     if (tid == 0) {
+        // 16 scores per batch of LDS reads, then their adds in order
         float t = 0.0f;
-        for (int s = 0; s < npos; s++) t += scores[s];
+        int s = 0;
+        for (; s + 16 <= npos; s += 16) {
+            float e[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) e[k] = scores[s + k];
+#pragma unroll
+            for (int k = 0; k < 16; k++) t += e[k];
+        }
+        for (; s < npos; s++) t += scores[s];
         red[0] = t;
     }
     lds_barrier();
@@ -217,18 +226,25 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
     // order (add_value, 367-370): one thread per dimension.
     if (tid < HD) {
         const int i = tid;
+        auto value = [&](int s) -> int8_t {
+            if (STAGE) return vrow[(int64_t)s * HD + i];
+            if (STORE && s == cur) return vnew[i];
+            return V8[(base + (int64_t)s * n_head) * HD + i];
+        };
         float acc = 0.0f;
-        for (int s = 0; s < npos; s++) {
-            const float w = scores[s];
-            int8_t v;
-            if (STAGE)
-                v = vrow[(int64_t)s * HD + i];
-            else if (STORE && s == cur)
-                v = vnew[i];
-            else
-                v = V8[(base + (int64_t)s * n_head) * HD + i];
-            acc = fmaf(w, (float)v, acc);
+        int s = 0;
+        for (; s + 8 <= npos; s += 8) {  // a batch's loads, then its fma chain
+            float w[8];
+            int8_t v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                w[k] = scores[s + k];
+                v[k] = value(s + k);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc = fmaf(w[k], (float)v[k], acc);
         }
+        for (; s < npos; s++) acc = fmaf(scores[s], (float)value(s), acc);
         out[(int64_t)t * ldo + (int64_t)h * HD + i] = acc;
     }
 }

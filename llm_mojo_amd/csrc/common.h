@@ -156,6 +156,31 @@ int gemv1_num_parts(const llmq_mat *w, bool ln);
 bool gemv_exact_supports(const llmq_mat *w);
 int gemv_exact_num_parts(const llmq_mat *w);
 int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq);
+
+// A prepared activation record (llmq_act_prepare): one token's row after
+// quantize_rows, in the forms the one-token integer GEMVs read, at byte
+// offsets of one device buffer:
+//   planes [K / 32][16] u32  nibble planes of X = xq + 32768 per code dword
+//   hsum   [K / 32][2]  i32  sum of xq over each half of a 32-chunk
+//   xq     [K]          i16  the codes, natural order
+//   xsl    [16]         i32  sum of the pairs (2L, 2L + 1) of every 32-piece
+//   sx     float             the row's scale
+struct ActLayout {
+    int64_t planes, hsum, xq, xsl, sx, bytes;
+};
+__host__ __device__ inline ActLayout llmq_act_layout(int64_t K) {
+    ActLayout L;
+    const int64_t ck = K / 32;
+    L.planes = 0;
+    L.hsum = ck * 64;
+    L.xq = ck * 72;
+    L.xsl = (L.xq + 2 * K + 15) & ~(int64_t)15;
+    L.sx = L.xsl + 64;
+    L.bytes = L.sx + 16;
+    return L;
+}
+int launch_act_prepare(llmq_ctx *ctx, const float *x, int64_t K, const float *ln_w, const float *ln_b, void *rec);
+int launch_linear_act(llmq_ctx *ctx, float *out, const void *rec, const llmq_mat *w, const float *bias, int flags);
 inline bool exact_order() {
     const char *e = getenv("LLMQ_EXACT");
     return !(e && e[0] == '0');
@@ -350,19 +375,43 @@ __device__ __forceinline__ float llmq_red16(float v) {
 // (multiply, then add); rstd = 1 / sqrt(reduce_add / C + 1e-5).  Called by
 // every thread of the workgroup (C a multiple of 16); wave 0 computes, bc
 // (2 floats of LDS) broadcasts.  Ends with a barrier.
+// Lane l's partial sum of x[l], x[l + 16], ... (or of their squared
+// deviations from `mean` when SQ), left to right; the LDS reads of a batch
+// of 16 values are issued before its adds, so the chain waits once a batch.
+template <bool SQ>
+__device__ __forceinline__ float llmq_lane_chain(const float *xs, int C, int l, float mean) {
+    float s = 0.0f;
+    int i = l;
+    for (; i + 16 * 15 < C; i += 256) {
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = xs[i + 16 * k];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (SQ) {
+                const float d = v[k] - mean;
+                s += d * d;
+            } else {
+                s += v[k];
+            }
+        }
+    }
+    for (; i < C; i += 16) {
+        if (SQ) {
+            const float d = xs[i] - mean;
+            s += d * d;
+        } else {
+            s += xs[i];
+        }
+    }
+    return s;
+}
 __device__ __forceinline__ void llmq_ln_stats(const float *xs, int C, float *bc, float &mean, float &rstd) {
     if (threadIdx.x < 64) {
         const int l = threadIdx.x & 15;
-        float s = 0.0f;
-        for (int i = l; i < C; i += 16) s += xs[i];
-        const float m = llmq_red16(s) / (float)C;
+        const float m = llmq_red16(llmq_lane_chain<false>(xs, C, l, 0.0f)) / (float)C;
         const float mb = __shfl(m, 0);
-        float q = 0.0f;
-        for (int i = l; i < C; i += 16) {
-            const float d = xs[i] - mb;
-            q += d * d;
-        }
-        const float r = 1.0f / sqrtf(llmq_red16(q) / (float)C + 1e-5f);
+        const float r = 1.0f / sqrtf(llmq_red16(llmq_lane_chain<true>(xs, C, l, mb)) / (float)C + 1e-5f);
         if (threadIdx.x == 0) {
             bc[0] = mb;
             bc[1] = r;

@@ -32,11 +32,23 @@
 // int16 activation pair with the zero-extended code pair); lanes j, j + 2
 // and the waves of the tile are then added, the zero point applied as
 // acc - zp * sum x (exact), and the float steps run in the reference's order.
+//
+// Activations come either as float rows (each workgroup then runs
+// LayerNorm / quantize_rows / the plane transform in its prologue), or as a
+// prepared record (REC: linear_team's xq / xp / xs / sx, built once by
+// act_prep_kernel), which the GEMV streams against with no prologue.
 #include "common.h"
 
 namespace {
 
 constexpr int kPlaneStride = 20;  // dwords per 32-activation chunk in LDS (16 used; no bank conflicts)
+
+// A 128-bit buffer load of streamed weight codes, marked non-temporal (no
+// reuse expected: the caches keep the activations instead).
+__device__ __forceinline__ uint4 bload16_stream(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 // ------------------------------------------------------------- activations
 
@@ -116,6 +128,82 @@ __device__ __forceinline__ int dppi(int v) {
 }
 constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E;
 
+// quantize_rows' codes of the normalized row xv (scale sx) in the forms the
+// GEMVs read: with `planes` (PS dwords a 32-activation chunk), the four
+// nibble planes of X = xq + 32768 per code dword and the per-half-group
+// sums of xq; with `xq`, the codes themselves; with `xsl` (16 ints of LDS,
+// zeroed), reference lane L's sum of its activation pairs (2L, 2L + 1) of
+// every 32-activation piece (int8 per channel).  Every thread must take part
+// (DPP exchanges); the pointers may be LDS or global memory.
+template <int NT, int UPT, int PS>
+__device__ __forceinline__ void build_act(const float4 (&xv)[UPT], float sx, int K, uint32_t *planes, int *hsum,
+                                          int16_t *xq, int *xsl) {
+    const float inv = 1.0f / sx;
+    const int nunits = K >> 2;
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const int u = threadIdx.x + NT * i;
+        const int q0 = q_round(xv[i].x * inv), q1 = q_round(xv[i].y * inv);
+        const int q2 = q_round(xv[i].z * inv), q3 = q_round(xv[i].w * inv);
+        if (xq && u < nunits) {
+            const uint32_t lo = ((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16);
+            const uint32_t hi = ((uint32_t)q2 & 0xFFFFu) | ((uint32_t)q3 << 16);
+            reinterpret_cast<uint2 *>(xq)[u] = make_uint2(lo, hi);
+        }
+        if (xsl && u < nunits) {  // unit u holds pairs 2 (u & 7), 2 (u & 7) + 1 of its 32-piece
+            atomicAdd(&xsl[2 * (u & 7)], q0 + q1);
+            atomicAdd(&xsl[2 * (u & 7) + 1], q2 + q3);
+        }
+        if (planes) {
+            // sum over the half (4 consecutive units = 4 consecutive lanes)
+            int qs = (q0 + q1) + (q2 + q3);
+            qs += dppi<kQuadXor1>(qs);
+            qs += dppi<kQuadXor2>(qs);
+            uint32_t A = (uint32_t)(q0 + 32768) | ((uint32_t)(q1 + 32768) << 16);
+            uint32_t B = (uint32_t)(q2 + 32768) | ((uint32_t)(q3 + 32768) << 16);
+            nibble_transpose(A, B);
+            // units 2i, 2i + 1 of a chunk make the plane dwords of code
+            // dword i: the even unit stores planes 0, 1, the odd one 2, 3
+            const bool odd = u & 1;
+            const uint32_t other = (uint32_t)dppi<kQuadXor1>((int)(odd ? A : B));
+            const uint32_t mine = odd ? B : A;
+            const uint32_t lo_src = odd ? other : mine, hi_src = odd ? mine : other;
+            const uint32_t pa = __builtin_amdgcn_perm(hi_src, lo_src, 0x05040100u);
+            const uint32_t pb = __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);
+            if (u < nunits) {
+                const int c = u >> 3, e = u & 7;
+                reinterpret_cast<uint2 *>(planes + c * PS + 4 * (e >> 1) + 2 * (e & 1))[0] = make_uint2(pa, pb);
+                if ((u & 3) == 0) hsum[2 * c + (e >> 2)] = qs;
+            }
+        }
+    }
+}
+
+// The prepared record of one token's activations (linear_team's xq, xp,
+// xs, sx; llmq_act_prepare): one workgroup.
+template <int NT, int UPT, bool LN>
+__global__ __launch_bounds__(NT) void act_prep_kernel(const float *__restrict__ x, const float *__restrict__ ln_w,
+                                                      const float *__restrict__ ln_b, int K, uint8_t *__restrict__ rec) {
+    extern __shared__ __align__(16) float xs[];  // [K] (LayerNorm)
+    __shared__ float bc[2], red[NT / 64];
+    __shared__ int xsl[16];
+    const ActLayout L = llmq_act_layout(K);
+    const int nunits = K >> 2;
+    float4 xv[UPT], lw[UPT], lb[UPT];
+    load_row<NT, UPT>(x, nunits, xv);
+    if (LN) {
+        load_row<NT, UPT>(ln_w, nunits, lw);
+        load_row<NT, UPT>(ln_b, nunits, lb);
+    }
+    if (threadIdx.x < 16) xsl[threadIdx.x] = 0;
+    const float sx = act_prologue<NT, UPT, LN>(xv, lw, lb, K, xs, bc, red);
+    build_act<NT, UPT, 16>(xv, sx, K, reinterpret_cast<uint32_t *>(rec + L.planes), reinterpret_cast<int *>(rec + L.hsum),
+                           reinterpret_cast<int16_t *>(rec + L.xq), xsl);
+    llmq_lds_barrier();
+    if (threadIdx.x < 16) reinterpret_cast<int *>(rec + L.xsl)[threadIdx.x] = xsl[threadIdx.x];
+    if (threadIdx.x == 0) reinterpret_cast<float *>(rec + L.sx)[0] = sx;
+}
+
 // ---------------------------------------------------------------- BLOCKED
 
 struct BlkArgs {
@@ -125,123 +213,135 @@ struct BlkArgs {
     uint32_t codes_bytes, scales_bytes, zps_bytes;
     int n, K, CK, nwaves, flags;
     const float *x, *ln_w, *ln_b, *bias;
+    const uint8_t *rec;
     float *out;
     int32_t *dbg;
     int16_t *xq_out;
     float *sx_out;
 };
 
-template <int NW, bool LN, int UPT, int WIN, bool DBG>
+// Workgroup: NW waves over NW / KS row octets; the KS waves of an octet
+// split its blocks into contiguous runs and leave each block's exact
+// half-group sums and scale in LDS, from which the octet's first wave runs
+// the two fma chains over all blocks in order.  REC: the activations'
+// planes and half sums are read from the prepared record, a block's worth
+// with its codes.
+template <int NW, int KS, bool LN, int UPT, int WIN, bool DBG, bool REC>
 __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
-    constexpr int NT = NW * 64;
+    constexpr int NT = NW * 64, OPW = NW / KS;
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t *planes = smem;                                             // [CK][kPlaneStride]
     int *hsum = reinterpret_cast<int *>(smem + a.CK * kPlaneStride);     // [CK][2] sum of xq per half
     float *xs = reinterpret_cast<float *>(hsum + 2 * a.CK);              // [K] (LayerNorm)
+    // each octet's per-block exact half sums and scales, [OPW][nb][3][64]
+    float *hand = xs + (LN ? a.K : 0);
     __shared__ float bc[2], red[NW];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int gw = blockIdx.x * NW + wid;  // global wave: rows 8 gw .. 8 gw + 7
+    const int ol = wid / KS, ks = wid % KS;
+    const int gw = blockIdx.x * OPW + ol;  // global octet: rows 8 gw .. 8 gw + 7
     const bool live = gw < a.nwaves;
     const int tile = gw >> 1, rr = 8 * (gw & 1) + (lane & 7), g = lane >> 3;
     const int o = tile * 16 + rr;
     const int nb = a.K >> 8;
+    const int b_lo = (ks * nb) / KS, b_hi = ((ks + 1) * nb) / KS;
     const int nunits = a.K >> 2;
+    const ActLayout AL = llmq_act_layout(a.K);
 
     // Activations first, then the first WIN blocks of codes, scales and zero
-    // points, then the epilogue operands: all in flight before any wait.
+    // points (and record planes), then the epilogue operands: all in flight
+    // before any wait.
     float4 xv[UPT], lw[UPT], lb[UPT];
-    load_row<NT, UPT>(a.x, nunits, xv);
-    if (LN) {
-        load_row<NT, UPT>(a.ln_w, nunits, lw);
-        load_row<NT, UPT>(a.ln_b, nunits, lb);
+    if (!REC) {
+        load_row<NT, UPT>(a.x, nunits, xv);
+        if (LN) {
+            load_row<NT, UPT>(a.ln_w, nunits, lw);
+            load_row<NT, UPT>(a.ln_b, nunits, lb);
+        }
     }
     const auto rc = llmq_rsrc(a.codes, a.codes_bytes);
     const auto rs = llmq_rsrc(a.scales, a.scales_bytes);
     const auto rz = llmq_rsrc(a.zps, a.zps_bytes);
-    // block b of this lane: chunk c = 8 b + g of row o
+    const auto rr_ = llmq_rsrc(a.rec, REC ? (uint32_t)AL.bytes : 0u);
+    // block b of this lane: chunk c = 8 b + g of row o (g32: chunk = group)
     auto code_off = [&](int b) -> uint32_t {
         const uint32_t c = (uint32_t)(8 * b + g);
-        return live && b < nb ? (((uint32_t)tile * (uint32_t)a.CK + c) * 16u + (uint32_t)rr) * 16u : kLlmqOOB;
+        return live && b < b_hi ? (((uint32_t)tile * (uint32_t)a.CK + c) * 16u + (uint32_t)rr) * 16u : kLlmqOOB;
     };
     auto meta_off = [&](int b) -> uint32_t {  // [tile][group][16 rows]
         const uint32_t c = (uint32_t)(8 * b + g);
-        return live && b < nb ? ((uint32_t)tile * (uint32_t)a.CK + c) * 16u + (uint32_t)rr : kLlmqOOB;
+        return live && b < b_hi ? ((uint32_t)tile * (uint32_t)a.CK + c) * 16u + (uint32_t)rr : kLlmqOOB;
     };
+    // REC: the record's planes and half sums (72 bytes a chunk), 16 bytes
+    // a thread per round, requested before the weights
+    constexpr int RPT = REC ? 6 : 1;  // rounds: up to 6 * 16 * NT bytes (K = 8192 at NT = 256)
+    uint4 wr[RPT];
+    if constexpr (REC) {
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const uint32_t off = (uint32_t)(tid + NT * i) * 16u;
+            wr[i] = llmq_bload16(rr_, off < (uint32_t)AL.xq ? off : kLlmqOOB);
+        }
+    }
     uint4 wc[WIN];
     uint32_t wsc[WIN], wzp[WIN];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < WIN; u++) {
-        wc[u] = llmq_bload16(rc, code_off(u));
-        const uint32_t mo = meta_off(u);
+        wc[u] = bload16_stream(rc, code_off(b_lo + u));
+        const uint32_t mo = meta_off(b_lo + u);
         wsc[u] = llmq_bload2(rs, mo == kLlmqOOB ? kLlmqOOB : mo * 2u);
         wzp[u] = llmq_bload1(rz, mo);
     }
-    const bool row_ok = live && g == 0 && o < a.n;
+    const bool row_ok = live && ks == 0 && g == 0 && o < a.n;
     const auto rb = llmq_rsrc(a.bias, (uint32_t)a.n * 4u);
     const auto ro = llmq_rsrc(a.out, (uint32_t)a.n * 4u);
     const float e_bias = __uint_as_float(llmq_bload4(rb, row_ok ? (uint32_t)o * 4u : kLlmqOOB));
     const float e_res = __uint_as_float(llmq_bload4(ro, row_ok ? (uint32_t)o * 4u : kLlmqOOB));
+    float sx;
+    if constexpr (REC) sx = __uint_as_float(llmq_bload4(rr_, (uint32_t)AL.sx));
     __builtin_amdgcn_sched_barrier(0);
 
-    // Prologue: LayerNorm, quantize_rows, nibble planes and half sums.
-    const float sx = act_prologue<NT, UPT, LN>(xv, lw, lb, a.K, xs, bc, red);
-    const float inv = 1.0f / sx;
-    const bool xq_dbg = a.xq_out != nullptr && blockIdx.x == 0;
-    if (xq_dbg && tid == 0 && a.sx_out) a.sx_out[0] = sx;
+    if constexpr (!REC) {
+        // Prologue: LayerNorm, quantize_rows, nibble planes and half sums.
+        sx = act_prologue<NT, UPT, LN>(xv, lw, lb, a.K, xs, bc, red);
+        const bool xq_dbg = a.xq_out != nullptr && blockIdx.x == 0;
+        if (xq_dbg && tid == 0 && a.sx_out) a.sx_out[0] = sx;
+        build_act<NT, UPT, kPlaneStride>(xv, sx, a.K, planes, hsum, xq_dbg ? a.xq_out : nullptr, nullptr);
+    } else {
+        // the staged record into LDS: plane chunks re-strided, half sums as they are
 #pragma unroll
-    for (int i = 0; i < UPT; i++) {
-        const int u = tid + NT * i;
-        const int q0 = q_round(xv[i].x * inv), q1 = q_round(xv[i].y * inv);
-        const int q2 = q_round(xv[i].z * inv), q3 = q_round(xv[i].w * inv);
-        if (xq_dbg && u < nunits) {
-            const uint32_t lo = ((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16);
-            const uint32_t hi = ((uint32_t)q2 & 0xFFFFu) | ((uint32_t)q3 << 16);
-            reinterpret_cast<uint2 *>(a.xq_out)[u] = make_uint2(lo, hi);
-        }
-        // sum over the half (4 consecutive units = 4 consecutive lanes)
-        int qs = (q0 + q1) + (q2 + q3);
-        qs += dppi<kQuadXor1>(qs);
-        qs += dppi<kQuadXor2>(qs);
-        uint32_t A = (uint32_t)(q0 + 32768) | ((uint32_t)(q1 + 32768) << 16);
-        uint32_t B = (uint32_t)(q2 + 32768) | ((uint32_t)(q3 + 32768) << 16);
-        nibble_transpose(A, B);
-        // units 2i, 2i + 1 of a chunk make the plane dwords of code dword i:
-        // the even unit stores planes 0, 1 and the odd one planes 2, 3
-        const bool odd = u & 1;
-        const uint32_t other = (uint32_t)dppi<kQuadXor1>((int)(odd ? A : B));
-        const uint32_t mine = odd ? B : A;
-        const uint32_t lo_src = odd ? other : mine, hi_src = odd ? mine : other;
-        const uint32_t pa = __builtin_amdgcn_perm(hi_src, lo_src, 0x05040100u);
-        const uint32_t pb = __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);
-        if (u < nunits) {
-            const int c = u >> 3, e = u & 7;
-            reinterpret_cast<uint2 *>(planes + c * kPlaneStride + 4 * (e >> 1) + 2 * (e & 1))[0] = make_uint2(pa, pb);
-            if ((u & 3) == 0) hsum[2 * c + (e >> 2)] = qs;
+        for (int i = 0; i < RPT; i++) {
+            const uint32_t q = (uint32_t)(tid + NT * i);  // 16-byte piece of the record
+            if (q * 16u < (uint32_t)AL.hsum)
+                reinterpret_cast<uint4 *>(planes + (q >> 2) * kPlaneStride)[q & 3] = wr[i];
+            else if (q * 16u < (uint32_t)AL.xq)
+                reinterpret_cast<uint4 *>(hsum)[q - (uint32_t)AL.hsum / 16u] = wr[i];
         }
     }
     llmq_lds_barrier();
 
-    // Blocks in order: the integer half sums, then the two fma chains.
+    // The wave's blocks in order: the integer half sums, then (KS == 1) the
+    // two fma chains, or (KS > 1) the operands handed to wave 0 of the octet.
     float acc0 = 0.0f, acc1 = 0.0f;
+    float *hd = hand + (size_t)ol * nb * 192;
     const uint32_t K1 = 0x11111111u;
-    for (int b0 = 0; b0 < nb; b0 += WIN) {
+    for (int b0 = b_lo; b0 < b_hi; b0 += WIN) {
 #pragma unroll
         for (int u = 0; u < WIN; u++) {
             const int b = b0 + u;
-            if (b < nb) {  // wave-uniform
+            if (b < b_hi) {  // wave-uniform
             const uint4 d = wc[u];
+            const int c = 8 * b + g;
             const float sc = __half2float(__ushort_as_half((unsigned short)wsc[u]));
             const int zp = (int)wzp[u];
             __builtin_amdgcn_sched_barrier(0);
-            wc[u] = llmq_bload16(rc, code_off(b + WIN));
+            wc[u] = bload16_stream(rc, code_off(b + WIN));
             const uint32_t mo = meta_off(b + WIN);
             wsc[u] = llmq_bload2(rs, mo == kLlmqOOB ? kLlmqOOB : mo * 2u);
             wzp[u] = llmq_bload1(rz, mo);
             __builtin_amdgcn_sched_barrier(0);
-            const int c = 8 * b + g;
             const uint4 *P = reinterpret_cast<const uint4 *>(planes + c * kPlaneStride);
             const uint4 p0 = P[0], p1 = P[1], p2 = P[2], p3 = P[3];
             const int2 hs = reinterpret_cast<const int2 *>(hsum)[c];
@@ -271,8 +371,35 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
             const int G0 = (int)(xu0 - 32768u * su0) - zp * hs.x;
             const int G1 = (int)(xu1 - 32768u * su1) - zp * hs.y;
             if (DBG && live && o < a.n) a.dbg[(size_t)o * a.CK + c] = G0 + G1;
-            acc0 = fmaf((float)G0, sc, acc0);
-            acc1 = fmaf((float)G1, sc, acc1);
+            // to LDS: the chains run once every block is in (keeping them
+            // out of the loop leaves its iterations independent)
+            hd[(b * 3 + 0) * 64 + lane] = (float)G0;
+            hd[(b * 3 + 1) * 64 + lane] = (float)G1;
+            hd[(b * 3 + 2) * 64 + lane] = sc;
+            }
+        }
+    }
+    if constexpr (KS > 1) llmq_lds_barrier();  // (KS == 1: the wave reads its own writes)
+    {
+        if (ks == 0) {  // the octet's two chains over all blocks, in order
+            int b = 0;
+            for (; b + 4 <= nb; b += 4) {  // four blocks' operands, then their chains
+                float t0[4], t1[4], sc[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    t0[k] = hd[((b + k) * 3 + 0) * 64 + lane];
+                    t1[k] = hd[((b + k) * 3 + 1) * 64 + lane];
+                    sc[k] = hd[((b + k) * 3 + 2) * 64 + lane];
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    acc0 = fmaf(t0[k], sc[k], acc0);
+                    acc1 = fmaf(t1[k], sc[k], acc1);
+                }
+            }
+            for (; b < nb; b++) {
+                acc0 = fmaf(hd[(b * 3 + 0) * 64 + lane], hd[(b * 3 + 2) * 64 + lane], acc0);
+                acc1 = fmaf(hd[(b * 3 + 1) * 64 + lane], hd[(b * 3 + 2) * 64 + lane], acc1);
             }
         }
     }
@@ -299,6 +426,7 @@ struct Ch8Args {
     uint32_t codes_bytes;
     int n, K, CK, ntiles, flags;
     const float *x, *ln_w, *ln_b, *bias;
+    const uint8_t *rec;
     float *out;
     ArgmaxPart *amax;
     int16_t *xq_out;
@@ -307,15 +435,16 @@ struct Ch8Args {
 
 // Workgroup: NW waves over TPW row tiles (NW / TPW waves share a tile's
 // steps, contiguously).  Step s of a tile is chunks 4s .. 4s + 3 of its 16
-// rows; lane (r, j) = (lane & 15, lane >> 4) reads chunk 4s + j.
-template <int NW, int TPW, bool LN, int UPT, int SPW>
+// rows; lane (r, j) = (lane & 15, lane >> 4) reads chunk 4s + j.  REC: the
+// int16 codes and lane sums come from the prepared record.
+template <int NW, int TPW, bool LN, int UPT, int SPW, bool REC>
 __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
     constexpr int NT = NW * 64, WPT = NW / TPW;  // waves per tile
     extern __shared__ __align__(16) uint32_t smem[];
-    int16_t *xq = reinterpret_cast<int16_t *>(smem);                        // [K] natural order
-    int *part = reinterpret_cast<int *>(smem + a.K / 2);                     // [TPW][WPT][2][16 rows][8]
-    float *xs = reinterpret_cast<float *>(part + TPW * WPT * 2 * 16 * 8);    // [K] (LayerNorm)
-    __shared__ int xsl[16];        // sum of xq over reference lane L's pairs
+    int16_t *xq = reinterpret_cast<int16_t *>(smem);                                    // [K] natural order
+    int *part = reinterpret_cast<int *>(smem + (REC ? 0 : a.K / 2));                     // [TPW][WPT][2][16][8]
+    float *xs = reinterpret_cast<float *>(part + TPW * WPT * 2 * 16 * 8);                // [K] (LayerNorm)
+    __shared__ int xsl[16];  // sum of xq over reference lane L's pairs
     __shared__ float bc[2], red[NW];
     __shared__ ArgmaxPart s_best[NW];
 
@@ -328,47 +457,53 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
     const int S = a.CK >> 2;  // steps per tile (CK a multiple of 4)
     const int s0 = (wt * S) / WPT, ns = ((wt + 1) * S) / WPT - s0;
     const int nunits = a.K >> 2;
+    const ActLayout AL = llmq_act_layout(a.K);
+    const auto rr_ = llmq_rsrc(a.rec, REC ? (uint32_t)AL.bytes : 0u);
 
     float4 xv[UPT], lw[UPT], lb[UPT];
-    load_row<NT, UPT>(a.x, nunits, xv);
-    if (LN) {
-        load_row<NT, UPT>(a.ln_w, nunits, lw);
-        load_row<NT, UPT>(a.ln_b, nunits, lb);
+    if (!REC) {
+        load_row<NT, UPT>(a.x, nunits, xv);
+        if (LN) {
+            load_row<NT, UPT>(a.ln_w, nunits, lw);
+            load_row<NT, UPT>(a.ln_b, nunits, lb);
+        }
     }
     const auto rc = llmq_rsrc(a.codes, a.codes_bytes);
-    uint4 wc[SPW];
+    uint4 wc[SPW], wx[REC ? SPW : 1][2];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < SPW; u++) {
         const uint32_t c = (uint32_t)(4 * (s0 + u) + j);
-        wc[u] = llmq_bload16(rc, live && u < ns ? (((uint32_t)tile * (uint32_t)a.CK + c) * 16u + (uint32_t)r) * 16u
-                                                : kLlmqOOB);
+        const bool ok = live && u < ns;
+        wc[u] = bload16_stream(rc, ok ? (((uint32_t)tile * (uint32_t)a.CK + c) * 16u + (uint32_t)r) * 16u : kLlmqOOB);
+        if constexpr (REC) {  // the chunk's 16 int16 codes
+            wx[u][0] = llmq_bload16(rr_, ok ? (uint32_t)AL.xq + c * 32u : kLlmqOOB);
+            wx[u][1] = llmq_bload16(rr_, ok ? (uint32_t)AL.xq + c * 32u + 16u : kLlmqOOB);
+        }
     }
     const int o = tile * 16 + r;
     const bool row_ok = live && o < a.n;
     const float scale = row_ok ? __half2float(__ushort_as_half(a.scales[tile * 16 + r])) : 0.0f;
     const int zp = row_ok ? (int)a.zps[tile * 16 + r] : 0;
+    float sx;
+    if constexpr (REC) {
+        sx = __uint_as_float(llmq_bload4(rr_, (uint32_t)AL.sx));
+        if (tid < 16) xsl[tid] = (int)llmq_bload4(rr_, (uint32_t)AL.xsl + 4u * tid);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
-    const float sx = act_prologue<NT, UPT, LN>(xv, lw, lb, a.K, xs, bc, red);
-    const float inv = 1.0f / sx;
-    const bool xq_dbg = a.xq_out != nullptr && blockIdx.x == 0;
-    if (xq_dbg && tid == 0 && a.sx_out) a.sx_out[0] = sx;
-    if (tid < 16) xsl[tid] = 0;
-    llmq_lds_barrier();
+    if constexpr (!REC) {
+        if (tid < 16) xsl[tid] = 0;
+        sx = act_prologue<NT, UPT, LN>(xv, lw, lb, a.K, xs, bc, red);
+        const bool xq_dbg = a.xq_out != nullptr && blockIdx.x == 0;
+        if (xq_dbg && tid == 0 && a.sx_out) a.sx_out[0] = sx;
+        build_act<NT, UPT, 16>(xv, sx, a.K, nullptr, nullptr, xq, xsl);
+        if (xq_dbg) {
 #pragma unroll
-    for (int i = 0; i < UPT; i++) {
-        const int u = tid + NT * i;
-        const int q0 = q_round(xv[i].x * inv), q1 = q_round(xv[i].y * inv);
-        const int q2 = q_round(xv[i].z * inv), q3 = q_round(xv[i].w * inv);
-        if (u < nunits) {
-            const uint32_t lo = ((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16);
-            const uint32_t hi = ((uint32_t)q2 & 0xFFFFu) | ((uint32_t)q3 << 16);
-            reinterpret_cast<uint2 *>(xq)[u] = make_uint2(lo, hi);
-            if (xq_dbg) reinterpret_cast<uint2 *>(a.xq_out)[u] = make_uint2(lo, hi);
-            // unit u holds pairs 2 (u & 7) and 2 (u & 7) + 1 of its 32-piece
-            atomicAdd(&xsl[2 * (u & 7)], q0 + q1);
-            atomicAdd(&xsl[2 * (u & 7) + 1], q2 + q3);
+            for (int i = 0; i < UPT; i++) {
+                const int u = tid + NT * i;
+                if (u < nunits) reinterpret_cast<uint2 *>(a.xq_out)[u] = reinterpret_cast<const uint2 *>(xq)[u];
+            }
         }
     }
     llmq_lds_barrier();
@@ -382,8 +517,14 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
         if (u < ns) {  // wave-uniform
         const int c = 4 * (s0 + u) + j;
         const uint4 d = wc[u];
-        const uint4 x0 = reinterpret_cast<const uint4 *>(xq)[2 * c];      // pairs 0..3 of the chunk
-        const uint4 x1 = reinterpret_cast<const uint4 *>(xq)[2 * c + 1];  // pairs 4..7
+        uint4 x0, x1;
+        if constexpr (REC) {
+            x0 = wx[u][0];
+            x1 = wx[u][1];
+        } else {
+            x0 = reinterpret_cast<const uint4 *>(xq)[2 * c];      // pairs 0..3 of the chunk
+            x1 = reinterpret_cast<const uint4 *>(xq)[2 * c + 1];  // pairs 4..7
+        }
         const uint32_t xp[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
@@ -462,37 +603,45 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
 
 int upt_for(int K, int nt) { return (K / 4 + nt - 1) / nt; }
 
-template <int NW, bool LN, int UPT>
+template <int NW, int KS, bool LN, int UPT, bool REC>
 void blk_launch_win(llmq_ctx *ctx, const BlkArgs &a, int grid, size_t lds, int win) {
-#define BLK(W, D) hipLaunchKernelGGL((gemv_blk_kernel<NW, LN, UPT, W, D>), dim3((unsigned)grid), dim3(NW * 64), lds, \
-                                     ctx->stream, a)
+#define BLK(W, D) hipLaunchKernelGGL((gemv_blk_kernel<NW, KS, LN, UPT, W, D, REC>), dim3((unsigned)grid), \
+                                     dim3(NW * 64), lds, ctx->stream, a)
     if (a.dbg) {
-        if constexpr (!LN) {
+        if constexpr (!LN && !REC) {
             BLK(4, true);
             return;
         }
     }
-    if (win <= 4) BLK(4, false); else if (win <= 8) BLK(8, false); else BLK(16, false);
+    if (win <= 2) BLK(2, false); else if (win <= 4) BLK(4, false); else if (win <= 8) BLK(8, false); else BLK(16, false);
 #undef BLK
 }
 
-template <int NW, bool LN>
+template <int NW, int KS, bool LN>
 int blk_launch_upt(llmq_ctx *ctx, const BlkArgs &a, int grid, size_t lds, int win) {
+    if (a.rec) {
+        if constexpr (!LN) {
+            blk_launch_win<NW, KS, false, 1, true>(ctx, a, grid, lds, win);
+            return LLMQ_OK;
+        }
+    }
     switch (upt_for(a.K, NW * 64)) {
-        case 1: blk_launch_win<NW, LN, 1>(ctx, a, grid, lds, win); return LLMQ_OK;
-        case 2: blk_launch_win<NW, LN, 2>(ctx, a, grid, lds, win); return LLMQ_OK;
-        case 3: blk_launch_win<NW, LN, 3>(ctx, a, grid, lds, win); return LLMQ_OK;
-        case 4: blk_launch_win<NW, LN, 4>(ctx, a, grid, lds, win); return LLMQ_OK;
-        case 5: case 6: blk_launch_win<NW, LN, 6>(ctx, a, grid, lds, win); return LLMQ_OK;
-        case 7: case 8: blk_launch_win<NW, LN, 8>(ctx, a, grid, lds, win); return LLMQ_OK;
+        case 1: blk_launch_win<NW, KS, LN, 1, false>(ctx, a, grid, lds, win); return LLMQ_OK;
+        case 2: blk_launch_win<NW, KS, LN, 2, false>(ctx, a, grid, lds, win); return LLMQ_OK;
+        case 3: blk_launch_win<NW, KS, LN, 3, false>(ctx, a, grid, lds, win); return LLMQ_OK;
+        case 4: blk_launch_win<NW, KS, LN, 4, false>(ctx, a, grid, lds, win); return LLMQ_OK;
+        case 5: case 6: blk_launch_win<NW, KS, LN, 6, false>(ctx, a, grid, lds, win); return LLMQ_OK;
+        case 7: case 8: blk_launch_win<NW, KS, LN, 8, false>(ctx, a, grid, lds, win); return LLMQ_OK;
     }
     return llmq_set_error(LLMQ_EUNSUPPORTED, "linear: reduction axis %d too long for %d waves", a.K, NW);
 }
 
-}  // namespace
+template <int KS>
+int blk_launch_ks(llmq_ctx *ctx, const BlkArgs &a, bool ln, int grid, size_t lds, int win) {
+    return ln ? blk_launch_upt<4, KS, true>(ctx, a, grid, lds, win) : blk_launch_upt<4, KS, false>(ctx, a, grid, lds, win);
+}
 
-// Which matrices the exact one-token kernels take.
-bool gemv_exact_supports(const llmq_mat *w) {
+bool exact_supports(const llmq_mat *w) {
     if (w->kind != MAT_QUANT || !w->a16) return false;
     const int64_t code_bytes = (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 256;
     if (code_bytes >= (int64_t)kLlmqOOB || (w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 32 >= (int64_t)kLlmqOOB) return false;
@@ -502,23 +651,19 @@ bool gemv_exact_supports(const llmq_mat *w) {
 }
 
 // Workgroups (= argmax partials) of the head kernel for w.
-static void head8_shape(const llmq_mat *w, int *nw, int *tpw, int *grid) {
+void head8_shape(const llmq_mat *w, int *nw, int *tpw, int *grid) {
     // one tile per 4-wave workgroup: 12 steps of a 768-input row make 3 a wave
     *nw = 4;
     *tpw = 1;
     *grid = (int)w->ntiles;
 }
 
-int gemv_exact_num_parts(const llmq_mat *w) {
-    int nw, tpw, grid;
-    head8_shape(w, &nw, &tpw, &grid);
-    return w->bits == 8 ? grid : 0;
-}
-
-int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq) {
+// Shared by both activation forms: rq.x (floats) or rec (a prepared record).
+int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     const llmq_mat *w = rq.w;
-    LLMQ_REQUIRE(rq.T == 1 && gemv_exact_supports(w), "linear: no exact one-token kernel for this matrix");
+    LLMQ_REQUIRE(rq.T == 1 && exact_supports(w), "linear: no exact one-token kernel for this matrix");
     const bool ln = rq.ln_w != nullptr;
+    LLMQ_REQUIRE(!(rec && (ln || rq.dbg || rq.xq_out)), "linear: a prepared record takes no LayerNorm or debug output");
     const int K = (int)w->k;
     if (w->bits == 4) {
         LLMQ_REQUIRE(!rq.amax, "linear: argmax partials need the int8 head kernel");
@@ -537,26 +682,35 @@ int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq) {
         a.x = rq.x;
         a.ln_w = rq.ln_w;
         a.ln_b = rq.ln_b;
+        a.rec = rec;
         a.bias = rq.bias ? rq.bias : rq.out;
         a.out = rq.out;
         a.dbg = rq.dbg;
         a.xq_out = rq.xq_out;
         a.sx_out = rq.sx_out;
-        int nw = 4;
-        if (const char *e = getenv("LLMQ_BLK_NW")) nw = atoi(e) == 1 ? 1 : atoi(e) == 2 ? 2 : atoi(e) == 8 ? 8 : 4;
-        int win = K / 256 <= 4 ? 4 : K / 256 <= 8 ? 8 : 16;
+        // 4-wave workgroups; KS waves per row octet split its blocks so that
+        // long rows still spread over enough waves (and CUs); two blocks in
+        // flight per wave (measured best from 768 to 4096 inputs)
+        const int nb = K / 256;
+        int ks = nb >= 8 ? 4 : nb >= 4 ? 2 : 1;
         const int64_t bytes = w->ntiles * w->CK * 256;
-        if (bytes >= (20ll << 20)) win = 4;  // streamed from HBM: a few blocks in flight per wave
+        if (bytes >= (20ll << 20)) ks = nb >= 4 ? 2 : 1;
+        if (const char *e = getenv("LLMQ_BLK_KS")) ks = atoi(e) == 1 ? 1 : atoi(e) == 2 ? 2 : 4;
+        if (a.dbg) ks = 1;
+        int win = 2;
         if (const char *e = getenv("LLMQ_BLK_WIN")) win = atoi(e);
-        const int grid = (int)((a.nwaves + nw - 1) / nw);
-        const size_t lds = (size_t)w->CK * (kPlaneStride + 2) * 4 + (ln ? (size_t)K * 4 : 0);
+        if (a.dbg) win = 4;
+        const int opw = 4 / ks;
+        const int grid = (int)((a.nwaves + opw - 1) / opw);
+        LLMQ_REQUIRE(!rec || llmq_act_layout(K).xq <= 6 * 16 * 256, "linear_act: reduction axis %d too long", K);
+        const size_t lds = (size_t)w->CK * (kPlaneStride + 2) * 4 + (ln ? (size_t)K * 4 : 0) +
+                           (size_t)opw * nb * 3 * 64 * 4;
         LLMQ_REQUIRE(lds <= 64 * 1024, "linear: %zu bytes of LDS", lds);
         int rc;
-        switch (nw) {
-            case 1: rc = ln ? blk_launch_upt<1, true>(ctx, a, grid, lds, win) : blk_launch_upt<1, false>(ctx, a, grid, lds, win); break;
-            case 2: rc = ln ? blk_launch_upt<2, true>(ctx, a, grid, lds, win) : blk_launch_upt<2, false>(ctx, a, grid, lds, win); break;
-            case 8: rc = ln ? blk_launch_upt<8, true>(ctx, a, grid, lds, win) : blk_launch_upt<8, false>(ctx, a, grid, lds, win); break;
-            default: rc = ln ? blk_launch_upt<4, true>(ctx, a, grid, lds, win) : blk_launch_upt<4, false>(ctx, a, grid, lds, win); break;
+        switch (ks) {
+            case 1: rc = blk_launch_ks<1>(ctx, a, ln, grid, lds, win); break;
+            case 2: rc = blk_launch_ks<2>(ctx, a, ln, grid, lds, win); break;
+            default: rc = blk_launch_ks<4>(ctx, a, ln, grid, lds, win); break;
         }
         if (rc != LLMQ_OK) return rc;
         LLMQ_HIP(hipGetLastError());
@@ -580,30 +734,81 @@ int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq) {
     a.x = rq.x;
     a.ln_w = rq.ln_w;
     a.ln_b = rq.ln_b;
+    a.rec = rec;
     a.bias = rq.bias ? rq.bias : rq.out;
     a.out = rq.out;
     a.amax = rq.amax;
     a.xq_out = rq.xq_out;
     a.sx_out = rq.sx_out;
     const int S = (int)(w->CK / 4), spw = (S + (nw / tpw) - 1) / (nw / tpw);
-    const size_t lds = (size_t)K * 2 + (size_t)tpw * (nw / tpw) * 2 * 16 * 8 * 4 + (ln ? (size_t)K * 4 : 0);
+    const size_t lds = (rec ? 0 : (size_t)K * 2) + (size_t)tpw * (nw / tpw) * 2 * 16 * 8 * 4 + (ln ? (size_t)K * 4 : 0);
     LLMQ_REQUIRE(lds <= 64 * 1024, "head: %zu bytes of LDS", lds);
     const int upt = upt_for(K, nw * 64);
-#define H8(U, SP)                                                                                       \
-    do {                                                                                                \
-        if (ln)                                                                                         \
-            hipLaunchKernelGGL((head8_kernel<4, 1, true, U, SP>), dim3((unsigned)grid), dim3(256), lds,  \
-                               ctx->stream, a);                                                         \
-        else                                                                                            \
-            hipLaunchKernelGGL((head8_kernel<4, 1, false, U, SP>), dim3((unsigned)grid), dim3(256), lds, \
-                               ctx->stream, a);                                                         \
-    } while (0)
-    if (upt == 1 && spw <= 4) H8(1, 4);
-    else if (upt <= 4 && spw <= 4) H8(4, 4);
-    else if (upt <= 4 && spw <= 16) H8(4, 16);
-    else return llmq_set_error(LLMQ_EUNSUPPORTED, "head: reduction axis %d too long", K);
+#define H8(LNV, U, SP, R) \
+    hipLaunchKernelGGL((head8_kernel<4, 1, LNV, U, SP, R>), dim3((unsigned)grid), dim3(256), lds, ctx->stream, a)
+    if (rec) {
+        if (spw <= 4) H8(false, 1, 4, true);
+        else if (spw <= 16) H8(false, 1, 16, true);
+        else return llmq_set_error(LLMQ_EUNSUPPORTED, "head: reduction axis %d too long", K);
+    } else if (upt == 1 && spw <= 4) {
+        if (ln) H8(true, 1, 4, false); else H8(false, 1, 4, false);
+    } else if (upt <= 4 && spw <= 4) {
+        if (ln) H8(true, 4, 4, false); else H8(false, 4, 4, false);
+    } else if (upt <= 4 && spw <= 16) {
+        if (ln) H8(true, 4, 16, false); else H8(false, 4, 16, false);
+    } else {
+        return llmq_set_error(LLMQ_EUNSUPPORTED, "head: reduction axis %d too long", K);
+    }
 #undef H8
     LLMQ_HIP(hipGetLastError());
     if (rq.amax_count) *rq.amax_count = grid;
     return LLMQ_OK;
+}
+
+}  // namespace
+
+bool gemv_exact_supports(const llmq_mat *w) { return exact_supports(w); }
+
+int gemv_exact_num_parts(const llmq_mat *w) {
+    int nw, tpw, grid;
+    head8_shape(w, &nw, &tpw, &grid);
+    return w->bits == 8 ? grid : 0;
+}
+
+int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq) { return launch_exact(ctx, rq, nullptr); }
+
+int launch_act_prepare(llmq_ctx *ctx, const float *x, int64_t K, const float *ln_w, const float *ln_b, void *rec) {
+    LLMQ_REQUIRE(x && rec && K >= 32 && K % 32 == 0 && K <= 16384, "act_prepare: K must be a multiple of 32, at most 16384");
+    LLMQ_REQUIRE(!ln_w == !ln_b, "act_prepare: LayerNorm needs both weight and bias");
+    const bool ln = ln_w != nullptr;
+    const size_t lds = ln ? (size_t)K * 4 : 0;
+    uint8_t *r = static_cast<uint8_t *>(rec);
+#define AP(NT, U)                                                                                                  \
+    do {                                                                                                           \
+        if (ln)                                                                                                    \
+            hipLaunchKernelGGL((act_prep_kernel<NT, U, true>), dim3(1), dim3(NT), lds, ctx->stream, x, ln_w, ln_b, \
+                               (int)K, r);                                                                         \
+        else                                                                                                       \
+            hipLaunchKernelGGL((act_prep_kernel<NT, U, false>), dim3(1), dim3(NT), lds, ctx->stream, x, ln_w,      \
+                               ln_b, (int)K, r);                                                                   \
+    } while (0)
+    if (K <= 1024) AP(256, 1);
+    else if (K <= 4096) AP(1024, 1);
+    else AP(1024, 4);
+#undef AP
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+int launch_linear_act(llmq_ctx *ctx, float *out, const void *rec, const llmq_mat *w, const float *bias, int flags) {
+    LLMQ_REQUIRE(out && rec && w, "linear_act: bad arguments");
+    LLMQ_REQUIRE(exact_supports(w), "linear_act: takes int4-g32-a16 (BLOCKED) and int8 per-channel A16 matrices");
+    LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "linear_act: LLMQ_BIAS without a bias");
+    GemvRequest rq;
+    rq.w = w;
+    rq.out = out;
+    rq.bias = bias;
+    rq.T = 1;
+    rq.flags = flags;
+    return launch_exact(ctx, rq, static_cast<const uint8_t *>(rec));
 }

@@ -193,6 +193,32 @@ def debug_chunk_sums(ctx, x, w, out, chunk_sums, xq, sx):
     check(lib().llmq_debug_chunk_sums(ctx.h, dptr(x), w.h, dptr(out), dptr(chunk_sums), dptr(xq), dptr(sx)))
 
 
+def act_bytes(K):
+    """Bytes of a prepared activation record for a K-long row."""
+    return int(lib().llmq_act_bytes(K))
+
+
+def act_prepare(ctx, x, act, ln=None):
+    """linear_team's prepared activations of one token's row x ([1, K] or
+    [K] on the device; LayerNorm with ln=(weight, bias) first) into act (a
+    device uint8 tensor of act_bytes(K))."""
+    K = x.shape[-1]
+    check(lib().llmq_act_prepare(ctx.h, dptr(x), K, dptr(ln[0]) if ln else None, dptr(ln[1]) if ln else None,
+                                 dptr(act)))
+
+
+def linear_act(ctx, out, act, w, bias=None, resid=False, gelu=False):
+    """One token's linear over a prepared record (bit-identical to linear)."""
+    flags = (LLMQ_BIAS if bias is not None else 0) | (LLMQ_GELU if gelu else 0) | (LLMQ_RESID if resid else 0)
+    check(lib().llmq_linear_act(ctx.h, dptr(out), dptr(act), w.h, dptr(bias), w.cols, w.rows, flags))
+
+
+def debug_read(ctx, buf, out, grid):
+    """Pure read of a device tensor buf (the read floor): one XOR per
+    workgroup into out (uint32 / int32 tensor of grid entries)."""
+    check(lib().llmq_debug_read(ctx.h, dptr(buf), buf.numel() * buf.element_size(), dptr(out), grid))
+
+
 REFMATH_OPS = {"exp": 0, "tanh": 1, "gelu": 2}
 
 

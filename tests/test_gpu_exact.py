@@ -173,3 +173,67 @@ def test_attention_bit_exact(gpu, orc, T, pos0):
         okv.store(layer, p, qkv_all[p, C:2 * C], qkv_all[p, 2 * C:])
     same_bits(out.cpu().numpy(), okv.attend(qkv_all[pos0:], layer, T, pos0))
     kv.free()
+
+
+def act_layout(K):
+    ck = K // 32
+    xq = ck * 72
+    xsl = (xq + 2 * K + 15) & ~15
+    return {"planes": 0, "hsum": ck * 64, "xq": xq, "xsl": xsl, "sx": xsl + 64, "bytes": xsl + 80}
+
+
+@pytest.mark.parametrize("K,ln", [(768, False), (768, True), (3072, False), (4096, False), (11008, False)])
+def test_act_record_contents(gpu, orc, K, ln):
+    """llmq_act_prepare: the record's codes and scale are quantize_rows'
+    (after LayerNorm when given), its half and lane sums the codes' sums."""
+    torch, lm, ctx = gpu
+    rng = np.random.default_rng(K + ln)
+    x = rng.normal(0, 1, (1, K)).astype(np.float32)
+    L = act_layout(K)
+    assert lm.act_bytes(K) == L["bytes"]
+    rec = torch.zeros(L["bytes"], dtype=torch.uint8, device="cuda")
+    if ln:
+        lw = rng.normal(1, 0.1, K).astype(np.float32)
+        lb = rng.normal(0, 0.1, K).astype(np.float32)
+        lm.act_prepare(ctx, dev(torch, x), rec, ln=(dev(torch, lw), dev(torch, lb)))
+        x = orc.layernorm(x, lw, lb)
+    else:
+        lm.act_prepare(ctx, dev(torch, x), rec)
+    torch.cuda.synchronize()
+    b = rec.cpu().numpy()
+    q, s = orc.quantize_rows(x)
+    xq = b[L["xq"]:L["xq"] + 2 * K].view(np.int16)
+    assert np.array_equal(xq, q[0])
+    assert b[L["sx"]:L["sx"] + 4].view(np.float32)[0] == s[0]
+    hs = b[L["hsum"]:L["hsum"] + 8 * (K // 32)].view(np.int32)
+    assert np.array_equal(hs, q[0].astype(np.int64).reshape(-1, 16).sum(1))
+    xsl = b[L["xsl"]:L["xsl"] + 64].view(np.int32)
+    assert np.array_equal(xsl, q[0].astype(np.int64).reshape(-1, 16, 2).sum((0, 2)))
+
+
+@pytest.mark.parametrize("fmt,IN,OUT", [((4, 32), 768, 2304), ((4, 32), 3072, 768), ((4, 32), 4096, 11008),
+                                        ((8, 0), 768, 50257), ((8, 0), 4096, 200)])
+def test_linear_act_bit_exact(gpu, orc, fmt, IN, OUT):
+    """llmq_linear_act over a prepared record equals llmq_linear bit for bit
+    (and the oracle's matmul_rows_a16)."""
+    torch, lm, ctx = gpu
+    bits, group = fmt
+    rng = np.random.default_rng(IN + OUT)
+    w = rng.normal(0, 0.02, (IN, OUT)).astype(np.float32)
+    x = rng.normal(0, 1, (1, IN)).astype(np.float32)
+    b = rng.normal(0, 0.1, OUT).astype(np.float32)
+    note("linear_act", fmt, IN, OUT)
+    g = lm.HipQuantMatrix.from_f32(ctx, w, bits, group, False, True)
+    o = orc.QuantMatrix.from_f32(w, bits, group, False, True)
+    rec = torch.zeros(lm.act_bytes(IN), dtype=torch.uint8, device="cuda")
+    xd = dev(torch, x)
+    lm.act_prepare(ctx, xd, rec)
+    out1 = torch.zeros((1, OUT), dtype=torch.float32, device="cuda")
+    out2 = torch.zeros((1, OUT), dtype=torch.float32, device="cuda")
+    lm.linear_act(ctx, out1, rec, g, dev(torch, b), gelu=bits == 4)
+    lm.linear(ctx, out2, xd, g, dev(torch, b), gelu=bits == 4)
+    torch.cuda.synchronize()
+    same_bits(out1.cpu().numpy(), out2.cpu().numpy())
+    want = orc.matmul_rows_a16(x, o, b, orc.EPI_BIAS | (orc.EPI_GELU if bits == 4 else 0))
+    same_bits(out1.cpu().numpy(), want)
+    g.free()

@@ -34,10 +34,34 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def read_floor(torch, lm, ctx, stream, nbytes, nbuf, grid=2048, reps=None):
+    """Average duration of a pure read of nbytes (llmq_debug_read: 128-bit
+    loads, no arithmetic) over nbuf distinct buffers, on `stream`."""
+    bufs = [torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
+    out = torch.zeros(grid, dtype=torch.int32, device="cuda")
+    reps = reps or max(60, 4 * nbuf)
+    for i in range(2 * nbuf):
+        lm.debug_read(ctx, bufs[i % nbuf], out, grid)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        lm.debug_read(ctx, bufs[i % nbuf], out, grid)
+    e1.record(stream)
+    e1.synchronize()
+    del bufs
+    return e0.elapsed_time(e1) * 1000.0 / reps
+
+
 def gemv_roofline(torch, lm, ctx, K=4096, N=11008, nbuf=36, reps=360):
-    """Average duration of the W4A16 g32 GEMV over `nbuf` distinct weight
-    buffers (> 768 MiB in total, beyond the 256 MB Infinity Cache), timed
-    with HIP events on the stream the kernel runs on."""
+    """The W4A16 g32 GEMV over `nbuf` distinct weight buffers (> 768 MiB in
+    total, beyond the 256 MB Infinity Cache), timed with HIP events on the
+    stream it runs on.  The timed kernel is the GEMV proper over the token's
+    prepared int16 activations (llmq_linear_act; llmq_act_prepare runs once
+    before, as linear_team's thread 0 quantizes once per token), so its
+    algorithmic bytes are nbytes(W) + 2K (int16 activations) + 4N (f32
+    outputs).  Also reported: the float-input path (llmq_linear, the
+    activation prologue in every workgroup) and the read floor, a pure read
+    of the same bytes over as many buffers."""
     stream = torch.cuda.Stream()
     mats = []
     with torch.cuda.stream(stream):
@@ -49,22 +73,33 @@ def gemv_roofline(torch, lm, ctx, K=4096, N=11008, nbuf=36, reps=360):
             del src
         x = torch.randn((1, K), device="cuda", generator=g)
         out = torch.empty((1, N), device="cuda")
-        for i in range(2 * nbuf):
-            lm.linear(ctx, out, x, mats[i % nbuf])
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(reps):
-            lm.linear(ctx, out, x, mats[i % nbuf])
-        e1.record(stream)
-        e1.synchronize()
+        act = torch.zeros(lm.act_bytes(K), dtype=torch.uint8, device="cuda")
+        lm.act_prepare(ctx, x, act)
+
+        def timed(fn):
+            for i in range(2 * nbuf):
+                fn(i)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(reps):
+                fn(i)
+            e1.record(stream)
+            e1.synchronize()
+            return e0.elapsed_time(e1) * 1000.0 / reps
+
+        us = timed(lambda i: lm.linear_act(ctx, out, act, mats[i % nbuf]))
+        us_float = timed(lambda i: lm.linear(ctx, out, x, mats[i % nbuf]))
+        wbytes = mats[0].nbytes()
+        for m in mats:
+            m.free()
+        floor_us = read_floor(torch, lm, ctx, stream, wbytes, nbuf)
     ctx.set_stream(None)
-    us = e0.elapsed_time(e1) * 1000.0 / reps
-    wbytes = mats[0].nbytes()
     alg = wbytes + 2 * K + 4 * N  # nbytes + int16 activations + f32 outputs
-    for m in mats:
-        m.free()
-    return {"kernel": f"gemv_a16 int4-g32 {K}x{N}", "us": us, "alg_bytes": alg, "weight_bytes": wbytes,
-            "buffers": nbuf, "gbs": alg / us / 1e3}
+    return {"kernel": f"gemv_blk_kernel (W4A16 int4-g32, BLOCKED) {K}x{N}, prepared activations", "us": us,
+            "alg_bytes": alg, "weight_bytes": wbytes, "buffers": nbuf, "gbs": alg / us / 1e3,
+            "float_input_us": round(us_float, 2),
+            "read_floor_us": round(floor_us, 2), "read_floor_gbs": round(wbytes / floor_us / 1e3, 1),
+            "frac_of_read_floor": round(floor_us / us, 3)}
 
 
 def measured_traffic():
@@ -98,12 +133,14 @@ GPT2_SHAPES = [("qkv", 768, 2304), ("proj", 768, 768), ("fc", 768, 3072), ("fcpr
 GEMV_FORMATS = [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)]
 
 
-def gemv_micro(torch, lm, ctx, reps=200):
+def gemv_micro(torch, lm, ctx, reps=200, rot_bytes=320 << 20):
     """Config 1: the one-token A16 GEMV at the GPT-2 shapes, int4 and int8 at
-    groups 32 / 64 / 128, and the int8 per-channel head (768 x 50257): one
-    matrix, launched back to back (it stays in the 256 MB Infinity Cache, as
-    in decode); GB/s of nbytes + 2K + 4N per launch.  The small matrices'
-    times (~4 us) are launch to launch, the kernel's own latency floor."""
+    groups 32 / 64 / 128, and the int8 per-channel head (768 x 50257), two
+    ways: one matrix launched back to back (it stays in the 256 MB Infinity
+    Cache, as in decode: `llc`), and over distinct copies totalling > 320 MiB
+    (`hbm`, more than the 256 MB cache).  GB/s of nbytes + 2K + 4N per launch; each is set beside a pure
+    read of the same bytes the same way (`*_floor_us`: the memory system's
+    time for those bytes in one launch, LLC-resident or rotated)."""
     stream = torch.cuda.Stream()
     res = {}
     with torch.cuda.stream(stream):
@@ -111,22 +148,41 @@ def gemv_micro(torch, lm, ctx, reps=200):
         g = torch.Generator(device="cuda").manual_seed(1001)
         cases = [(f"int{b}-g{gr} {n}", K, N, b, gr) for b, gr in GEMV_FORMATS for n, K, N in GPT2_SHAPES]
         cases.append(("int8-ch head", 768, 50257, 8, 0))
-        for name, K, N, bits, group in cases:
-            w = lm.HipQuantMatrix.from_f32(ctx, torch.randn((K, N), device="cuda", generator=g) * 0.02, bits, group,
-                                           False, True)
-            x = torch.randn((1, K), device="cuda", generator=g)
-            out = torch.empty((1, N), device="cuda")
-            for _ in range(10):
-                lm.linear(ctx, out, x, w)
+        cases.insert(0, ("warm-up", 768, 2304, 4, 32))  # first launches of the process, not reported
+
+        def timed(fn, n):
+            for i in range(max(10, 2 * n)):
+                fn(i)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            for _ in range(reps):
-                lm.linear(ctx, out, x, w)
+            for i in range(reps):
+                fn(i)
             e1.record(stream)
             e1.synchronize()
-            us = e0.elapsed_time(e1) * 1000.0 / reps
-            res[name] = {"us": round(us, 2), "gbs": round((w.nbytes() + 2 * K + 4 * N) / us / 1e3, 1)}
-            w.free()
+            return e0.elapsed_time(e1) * 1000.0 / reps
+
+        for name, K, N, bits, group in cases:
+            src = torch.randn((K, N), device="cuda", generator=g) * 0.02
+            w = lm.HipQuantMatrix.from_f32(ctx, src, bits, group, False, True)
+            nb = w.nbytes()
+            nrot = max(2, -(-rot_bytes // nb))
+            x = torch.randn((1, K), device="cuda", generator=g)
+            out = torch.empty((1, N), device="cuda")
+            alg = nb + 2 * K + 4 * N
+            us = timed(lambda i: lm.linear(ctx, out, x, w), 1)
+            if name == "warm-up":
+                w.free()
+                continue
+            ws = [w] + [lm.HipQuantMatrix.from_f32(ctx, src, bits, group, False, True) for _ in range(nrot - 1)]
+            us_hbm = timed(lambda i: lm.linear(ctx, out, x, ws[i % nrot]), nrot)
+            for m in ws:
+                m.free()
+            llc_floor = read_floor(torch, lm, ctx, stream, nb, 1, grid=256, reps=reps)
+            hbm_floor = read_floor(torch, lm, ctx, stream, nb, nrot, grid=256, reps=reps)
+            res[name] = {"llc_us": round(us, 2), "llc_gbs": round(alg / us / 1e3, 1),
+                         "llc_floor_us": round(llc_floor, 2),
+                         "hbm_us": round(us_hbm, 2), "hbm_gbs": round(alg / us_hbm / 1e3, 1),
+                         "hbm_floor_us": round(hbm_floor, 2)}
     ctx.set_stream(None)
     return res
 
@@ -351,7 +407,7 @@ def main():
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 476-token prefill (config 3)")
     ap.add_argument("--no-llama", action="store_true", help="skip the TinyLlama-shaped decoder (config 4)")
-    ap.add_argument("--gguf-sweep", action="store_true", help="add the GGUF GEMV sweep (config 2, ~1 min)")
+    ap.add_argument("--no-gguf-sweep", action="store_true", help="skip the GGUF GEMV sweep (config 2)")
     ap.add_argument("--no-intattn", action="store_true", help="skip the integer-attention decode comparison")
     ap.add_argument("--no-formats", action="store_true", help="skip the decode table of the other formats")
     ap.add_argument("--roofline-only", action="store_true",
@@ -403,6 +459,8 @@ def main():
         r = gemv_roofline(torch, lm, ctx)
         roof = {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic()}
+        r["traffic_source"] = ("profiles/gemv_a16_int4_g32_4096x11008.traffic.json: rocprofv3 --pmc FETCH_SIZE "
+                               "and WRITE_SIZE of this kernel, scaled by the same counters on a copy of known size")
         extra["roofline_kernel"] = r
         extra["copy_gbs"] = round(copy_bandwidth(torch), 1)
         log("gemv", r, "copy GB/s", extra["copy_gbs"])
@@ -430,7 +488,7 @@ def main():
         log("tinyllama-shaped decode")
         extra["tinyllama_q4k_q6k"] = llama_decode(lm, synth, ctx)
         log(extra["tinyllama_q4k_q6k"])
-    if args.gguf_sweep:
+    if not args.no_gguf_sweep:
         log("gguf sweep")
         extra["gguf_gemv_sweep"] = gguf_sweep(torch, lm, synth, ctx)
 

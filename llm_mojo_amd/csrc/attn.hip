@@ -193,9 +193,14 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (int s = tid; s < npos; s += kAttnThreads) scores[s] = ref_expf(scores[s] - mx);
     lds_barrier();
-    // The total in position order (attend_float_one, 139-141).
-    if (tid == 0) {
-        // 16 scores per batch of LDS reads, then their adds in order
+    auto vscale = [&](int s) -> float {
+        if (STAGE) return vsc[s];
+        if (STORE && s == cur) return vscale_new;
+        return VS[base + (int64_t)s * n_head];
+    };
+    // The total in position order (attend_float_one, 139-141): 16 scores per
+    // batch of LDS reads, then their adds in order.
+    auto total_of = [&]() -> float {
         float t = 0.0f;
         int s = 0;
         for (; s + 16 <= npos; s += 16) {
@@ -206,26 +211,12 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
             for (int k = 0; k < 16; k++) t += e[k];
         }
         for (; s < npos; s++) t += scores[s];
-        red[0] = t;
-    }
-    lds_barrier();
-    const float total = red[0];
-    // Each position's weight p * vs (p = e / total; add_value's ps, 366).
-    for (int s = tid; s < npos; s += kAttnThreads) {
-        float vs;
-        if (STAGE)
-            vs = vsc[s];
-        else if (STORE && s == cur)
-            vs = vscale_new;
-        else
-            vs = VS[base + (int64_t)s * n_head];
-        scores[s] = (scores[s] / total) * vs;
-    }
-    lds_barrier();
+        return t;
+    };
     // out[i] = acc_i, acc_i = fma(w_s, f32(v_s[i]), acc_i) over positions in
-    // order (add_value, 367-370): one thread per dimension.
-    if (tid < HD) {
-        const int i = tid;
+    // order (add_value, 367-370), w_s = (e_s / total) * vs_s: one lane per
+    // dimension.
+    auto value_chain = [&](int i) -> float {
         auto value = [&](int s) -> int8_t {
             if (STAGE) return vrow[(int64_t)s * HD + i];
             if (STORE && s == cur) return vnew[i];
@@ -245,7 +236,27 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
             for (int k = 0; k < 8; k++) acc = fmaf(w[k], (float)v[k], acc);
         }
         for (; s < npos; s++) acc = fmaf(scores[s], (float)value(s), acc);
-        out[(int64_t)t * ldo + (int64_t)h * HD + i] = acc;
+        return acc;
+    };
+    if constexpr (HD == 64) {
+        // One wave finishes: every lane forms the same total, the lanes then
+        // turn positions lane, lane + 64, ... into weights, and run the 64
+        // value chains (LDS operations of a wave complete in order).
+        if (wid == 0) {
+            const float total = total_of();
+            for (int s = lane; s < npos; s += 64) scores[s] = (scores[s] / total) * vscale(s);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+            out[(int64_t)t * ldo + (int64_t)h * HD + lane] = value_chain(lane);
+        }
+    } else {
+        if (tid == 0) red[0] = total_of();
+        lds_barrier();
+        const float total = red[0];
+        for (int s = tid; s < npos; s += kAttnThreads) scores[s] = (scores[s] / total) * vscale(s);
+        lds_barrier();
+        if (tid < HD) out[(int64_t)t * ldo + (int64_t)h * HD + tid] = value_chain(tid);
     }
 }
 

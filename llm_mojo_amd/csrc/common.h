@@ -362,11 +362,16 @@ __device__ __forceinline__ void llmq_lds_barrier() {
 // the 16 values, lane 0 of the group gets the sum (the other lanes hold
 // partial sums).  Float addition is commutative, so which lane of a pair
 // adds is immaterial; the pairing is what fixes the bits.
+// DPP row_shl:n gives lane l the value of lane l + n of its row of 16.
+template <int CTRL>
+__device__ __forceinline__ float llmq_dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float llmq_red16(float v) {
-    v = v + __shfl_down(v, 8, 16);
-    v = v + __shfl_down(v, 4, 16);
-    v = v + __shfl_down(v, 2, 16);
-    return v + __shfl_down(v, 1, 16);
+    v = v + llmq_dppf<0x108>(v);
+    v = v + llmq_dppf<0x104>(v);
+    v = v + llmq_dppf<0x102>(v);
+    return v + llmq_dppf<0x101>(v);
 }
 
 // layernorm's statistics (kernels.mojo:179-197) over x[0, C) in LDS, in
@@ -410,7 +415,7 @@ __device__ __forceinline__ void llmq_ln_stats(const float *xs, int C, float *bc,
     if (threadIdx.x < 64) {
         const int l = threadIdx.x & 15;
         const float m = llmq_red16(llmq_lane_chain<false>(xs, C, l, 0.0f)) / (float)C;
-        const float mb = __shfl(m, 0);
+        const float mb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
         const float r = 1.0f / sqrtf(llmq_red16(llmq_lane_chain<true>(xs, C, l, mb)) / (float)C + 1e-5f);
         if (threadIdx.x == 0) {
             bc[0] = mb;
@@ -420,4 +425,53 @@ __device__ __forceinline__ void llmq_ln_stats(const float *xs, int C, float *bc,
     llmq_lds_barrier();
     mean = bc[0];
     rstd = bc[1];
+}
+
+// The same statistics from registers, for C = 16 NV: lane l (of wave 0,
+// any of its rows of 16) holds v[i] = x[16 i + l]; returns (mean, rstd) in
+// every lane of the wave.
+template <int NV>
+__device__ __forceinline__ float2 llmq_ln_stats_regs(const float (&v)[NV]) {
+    constexpr float C = (float)(16 * NV);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) s += v[i];
+    const float m = llmq_red16(s) / C;
+    const float mb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const float d = v[i] - mb;
+        q += d * d;
+    }
+    const float r = 1.0f / sqrtf(llmq_red16(q) / C + 1e-5f);
+    return make_float2(mb, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0)));
+}
+
+// v of lane l + 32 (l < 32) / l + 16 (even rows of 16): gfx950's lane swaps.
+__device__ __forceinline__ float llmq_from_lane_plus32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float llmq_from_lane_plus16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[1]);
+}
+__device__ __forceinline__ int llmq_from_lane_plus32(int v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)r[1];
+}
+
+// max over the wave, in every lane (order-free): DPP within rows of 16, then
+// the four rows' results.
+__device__ __forceinline__ float llmq_wave_max(float v) {
+    v = fmaxf(v, llmq_dppf<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, llmq_dppf<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, llmq_dppf<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, llmq_dppf<0x140>(v));  // row_mirror
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }

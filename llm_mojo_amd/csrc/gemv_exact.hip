@@ -68,22 +68,51 @@ __device__ __forceinline__ void load_row(const float *p, int nunits, float4 (&v)
     }
 }
 
+// Wave 0's copy of the row for LayerNorm's 16 lane chains (NV > 0): lane
+// l holds v[i] = x[16 i + l], loaded straight from memory.
+template <int NV>
+__device__ __forceinline__ void load_lnv(const float *x, float (&v)[NV > 0 ? NV : 1]) {
+    if constexpr (NV > 0) {
+        if (threadIdx.x < 64) {
+            const auto r = llmq_rsrc(x, (uint32_t)NV * 64u);
+            const uint32_t l = threadIdx.x & 15;
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = __uint_as_float(llmq_bload4(r, (16u * i + l) * 4u));
+        }
+    }
+}
+
 // LayerNorm (optional), then quantize_rows' scale: the row in xv is
-// replaced by the normalized one; returns sx.  xs: K floats of LDS, bc: 2,
-// red: NT / 64.  Ends with a barrier.
-template <int NT, int UPT, bool LN>
+// replaced by the normalized one; returns sx.  LayerNorm's statistics come
+// from wave 0's registers (NV > 0, see load_lnv) or from the row staged in
+// xs (K floats of LDS).  bc: 2 floats, red: NT / 64.  Ends with a barrier.
+template <int NT, int UPT, bool LN, int NV>
 __device__ __forceinline__ float act_prologue(float4 (&xv)[UPT], const float4 (&lw)[UPT], const float4 (&lb)[UPT],
-                                              int K, float *xs, float *bc, float *red) {
+                                              const float (&lnv)[NV > 0 ? NV : 1], int K, float *xs, float *bc,
+                                              float *red) {
     const int nunits = K / 4;
     if (LN) {
-#pragma unroll
-        for (int i = 0; i < UPT; i++) {
-            const int u = threadIdx.x + NT * i;
-            if (u < nunits) reinterpret_cast<float4 *>(xs)[u] = xv[i];
-        }
-        llmq_lds_barrier();
         float mean, rstd;
-        llmq_ln_stats(xs, K, bc, mean, rstd);
+        if constexpr (NV > 0) {
+            if (threadIdx.x < 64) {
+                const float2 st = llmq_ln_stats_regs<NV>(lnv);
+                if (threadIdx.x == 0) {
+                    bc[0] = st.x;
+                    bc[1] = st.y;
+                }
+            }
+            llmq_lds_barrier();
+            mean = bc[0];
+            rstd = bc[1];
+        } else {
+#pragma unroll
+            for (int i = 0; i < UPT; i++) {
+                const int u = threadIdx.x + NT * i;
+                if (u < nunits) reinterpret_cast<float4 *>(xs)[u] = xv[i];
+            }
+            llmq_lds_barrier();
+            llmq_ln_stats(xs, K, bc, mean, rstd);
+        }
 #pragma unroll
         for (int i = 0; i < UPT; i++) {
             xv[i].x = ((xv[i].x - mean) * rstd) * lw[i].x + lb[i].x;
@@ -97,8 +126,7 @@ __device__ __forceinline__ float act_prologue(float4 (&xv)[UPT], const float4 (&
 #pragma unroll
     for (int i = 0; i < UPT; i++)
         m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[i].x), fabsf(xv[i].y)), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w))));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = llmq_wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     llmq_lds_barrier();
     m = red[0];
@@ -196,7 +224,8 @@ __global__ __launch_bounds__(NT) void act_prep_kernel(const float *__restrict__ 
         load_row<NT, UPT>(ln_b, nunits, lb);
     }
     if (threadIdx.x < 16) xsl[threadIdx.x] = 0;
-    const float sx = act_prologue<NT, UPT, LN>(xv, lw, lb, K, xs, bc, red);
+    const float none[1] = {0.0f};
+    const float sx = act_prologue<NT, UPT, LN, 0>(xv, lw, lb, none, K, xs, bc, red);
     build_act<NT, UPT, 16>(xv, sx, K, reinterpret_cast<uint32_t *>(rec + L.planes), reinterpret_cast<int *>(rec + L.hsum),
                            reinterpret_cast<int16_t *>(rec + L.xq), xsl);
     llmq_lds_barrier();
@@ -226,7 +255,7 @@ struct BlkArgs {
 // the two fma chains over all blocks in order.  REC: the activations'
 // planes and half sums are read from the prepared record, a block's worth
 // with its codes.
-template <int NW, int KS, bool LN, int UPT, int WIN, bool DBG, bool REC>
+template <int NW, int KS, bool LN, int UPT, int WIN, bool DBG, bool REC, int NV>
 __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     constexpr int NT = NW * 64, OPW = NW / KS;
     extern __shared__ __align__(16) uint32_t smem[];
@@ -253,7 +282,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     // points (and record planes), then the epilogue operands: all in flight
     // before any wait.
     float4 xv[UPT], lw[UPT], lb[UPT];
+    float lnv[NV > 0 ? NV : 1];
     if (!REC) {
+        if (LN) load_lnv<NV>(a.x, lnv);
         load_row<NT, UPT>(a.x, nunits, xv);
         if (LN) {
             load_row<NT, UPT>(a.ln_w, nunits, lw);
@@ -305,7 +336,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
 
     if constexpr (!REC) {
         // Prologue: LayerNorm, quantize_rows, nibble planes and half sums.
-        sx = act_prologue<NT, UPT, LN>(xv, lw, lb, a.K, xs, bc, red);
+        sx = act_prologue<NT, UPT, LN, NV>(xv, lw, lb, lnv, a.K, xs, bc, red);
         const bool xq_dbg = a.xq_out != nullptr && blockIdx.x == 0;
         if (xq_dbg && tid == 0 && a.sx_out) a.sx_out[0] = sx;
         build_act<NT, UPT, kPlaneStride>(xv, sx, a.K, planes, hsum, xq_dbg ? a.xq_out : nullptr, nullptr);
@@ -405,9 +436,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     }
     // reduce_add: (L, L + 8) in-lane, then groups g, g + 4 / + 2 / + 1.
     float v = acc0 + acc1;
-    v = v + __shfl_down(v, 32);
-    v = v + __shfl_down(v, 16);
-    v = v + __shfl_down(v, 8);
+    v = v + llmq_from_lane_plus32(v);
+    v = v + llmq_from_lane_plus16(v);
+    v = v + llmq_dppf<0x108>(v);  // row_shl:8
     if (row_ok) {
         float r = v * sx;
         if (a.flags & LLMQ_BIAS) r += e_bias;
@@ -437,7 +468,7 @@ struct Ch8Args {
 // steps, contiguously).  Step s of a tile is chunks 4s .. 4s + 3 of its 16
 // rows; lane (r, j) = (lane & 15, lane >> 4) reads chunk 4s + j.  REC: the
 // int16 codes and lane sums come from the prepared record.
-template <int NW, int TPW, bool LN, int UPT, int SPW, bool REC>
+template <int NW, int TPW, bool LN, int UPT, int SPW, bool REC, int NV>
 __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
     constexpr int NT = NW * 64, WPT = NW / TPW;  // waves per tile
     extern __shared__ __align__(16) uint32_t smem[];
@@ -461,7 +492,9 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
     const auto rr_ = llmq_rsrc(a.rec, REC ? (uint32_t)AL.bytes : 0u);
 
     float4 xv[UPT], lw[UPT], lb[UPT];
+    float lnv[NV > 0 ? NV : 1];
     if (!REC) {
+        if (LN) load_lnv<NV>(a.x, lnv);
         load_row<NT, UPT>(a.x, nunits, xv);
         if (LN) {
             load_row<NT, UPT>(a.ln_w, nunits, lw);
@@ -494,7 +527,7 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
 
     if constexpr (!REC) {
         if (tid < 16) xsl[tid] = 0;
-        sx = act_prologue<NT, UPT, LN>(xv, lw, lb, a.K, xs, bc, red);
+        sx = act_prologue<NT, UPT, LN, NV>(xv, lw, lb, lnv, a.K, xs, bc, red);
         const bool xq_dbg = a.xq_out != nullptr && blockIdx.x == 0;
         if (xq_dbg && tid == 0 && a.sx_out) a.sx_out[0] = sx;
         build_act<NT, UPT, 16>(xv, sx, a.K, nullptr, nullptr, xq, xsl);
@@ -536,7 +569,7 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
     }
     // lanes j and j + 2 hold the same reference lanes
 #pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] += __shfl_down(acc[i], 32);
+    for (int i = 0; i < 8; i++) acc[i] += llmq_from_lane_plus32(acc[i]);
     // waves of the tile, through LDS (lanes j = 0, 1)
     if (j < 2) {
 #pragma unroll
@@ -560,7 +593,7 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
         }
         // reduce_add: (L, L + 8) pairs lanes j = 0, 1 (16 apart), the rest in-lane
 #pragma unroll
-        for (int i = 0; i < 8; i++) vl[i] = vl[i] + __shfl_down(vl[i], 16);
+        for (int i = 0; i < 8; i++) vl[i] = vl[i] + llmq_from_lane_plus16(vl[i]);
         const float b0 = vl[0] + vl[4], b1 = vl[1] + vl[5], b2 = vl[2] + vl[6], b3 = vl[3] + vl[7];
         const float c0 = b0 + b2, c1 = b1 + b3;
         const float v = c0 + c1;
@@ -603,9 +636,13 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
 
 int upt_for(int K, int nt) { return (K / 4 + nt - 1) / nt; }
 
-template <int NW, int KS, bool LN, int UPT, bool REC>
-void blk_launch_win(llmq_ctx *ctx, const BlkArgs &a, int grid, size_t lds, int win) {
-#define BLK(W, D) hipLaunchKernelGGL((gemv_blk_kernel<NW, KS, LN, UPT, W, D, REC>), dim3((unsigned)grid), \
+// LayerNorm's chains from registers for rows up to 768 / 1024 inputs
+// (48 / 64 values a lane), from LDS beyond.
+inline int ln_nv(int K) { return K == 768 ? 48 : K == 1024 ? 64 : 0; }
+
+template <int NW, int KS, bool LN, int UPT, bool REC, int NV>
+void blk_launch_nv(llmq_ctx *ctx, const BlkArgs &a, int grid, size_t lds, int win) {
+#define BLK(W, D) hipLaunchKernelGGL((gemv_blk_kernel<NW, KS, LN, UPT, W, D, REC, NV>), dim3((unsigned)grid), \
                                      dim3(NW * 64), lds, ctx->stream, a)
     if (a.dbg) {
         if constexpr (!LN && !REC) {
@@ -615,6 +652,15 @@ void blk_launch_win(llmq_ctx *ctx, const BlkArgs &a, int grid, size_t lds, int w
     }
     if (win <= 2) BLK(2, false); else if (win <= 4) BLK(4, false); else if (win <= 8) BLK(8, false); else BLK(16, false);
 #undef BLK
+}
+
+template <int NW, int KS, bool LN, int UPT, bool REC>
+void blk_launch_win(llmq_ctx *ctx, const BlkArgs &a, int grid, size_t lds, int win) {
+    if constexpr (LN && UPT == 1) {
+        if (ln_nv(a.K) == 48) return blk_launch_nv<NW, KS, LN, UPT, REC, 48>(ctx, a, grid, lds, win);
+        if (ln_nv(a.K) == 64) return blk_launch_nv<NW, KS, LN, UPT, REC, 64>(ctx, a, grid, lds, win);
+    }
+    blk_launch_nv<NW, KS, LN, UPT, REC, 0>(ctx, a, grid, lds, win);
 }
 
 template <int NW, int KS, bool LN>
@@ -744,18 +790,21 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     const size_t lds = (rec ? 0 : (size_t)K * 2) + (size_t)tpw * (nw / tpw) * 2 * 16 * 8 * 4 + (ln ? (size_t)K * 4 : 0);
     LLMQ_REQUIRE(lds <= 64 * 1024, "head: %zu bytes of LDS", lds);
     const int upt = upt_for(K, nw * 64);
-#define H8(LNV, U, SP, R) \
-    hipLaunchKernelGGL((head8_kernel<4, 1, LNV, U, SP, R>), dim3((unsigned)grid), dim3(256), lds, ctx->stream, a)
+#define H8(LNV, U, SP, R, NV) \
+    hipLaunchKernelGGL((head8_kernel<4, 1, LNV, U, SP, R, NV>), dim3((unsigned)grid), dim3(256), lds, ctx->stream, a)
     if (rec) {
-        if (spw <= 4) H8(false, 1, 4, true);
-        else if (spw <= 16) H8(false, 1, 16, true);
+        if (spw <= 4) H8(false, 1, 4, true, 0);
+        else if (spw <= 16) H8(false, 1, 16, true, 0);
         else return llmq_set_error(LLMQ_EUNSUPPORTED, "head: reduction axis %d too long", K);
     } else if (upt == 1 && spw <= 4) {
-        if (ln) H8(true, 1, 4, false); else H8(false, 1, 4, false);
+        if (ln && ln_nv(K) == 48) H8(true, 1, 4, false, 48);
+        else if (ln && ln_nv(K) == 64) H8(true, 1, 4, false, 64);
+        else if (ln) H8(true, 1, 4, false, 0);
+        else H8(false, 1, 4, false, 0);
     } else if (upt <= 4 && spw <= 4) {
-        if (ln) H8(true, 4, 4, false); else H8(false, 4, 4, false);
+        if (ln) H8(true, 4, 4, false, 0); else H8(false, 4, 4, false, 0);
     } else if (upt <= 4 && spw <= 16) {
-        if (ln) H8(true, 4, 16, false); else H8(false, 4, 16, false);
+        if (ln) H8(true, 4, 16, false, 0); else H8(false, 4, 16, false, 0);
     } else {
         return llmq_set_error(LLMQ_EUNSUPPORTED, "head: reduction axis %d too long", K);
     }

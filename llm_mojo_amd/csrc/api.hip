@@ -1038,19 +1038,9 @@ static void set_fuse_mode(llmq_gpt2 *m, int max_pos) {
 static int decode_step(llmq_gpt2 *m, bool use_graph) {
     llmq_ctx *ctx = m->ctx;
     if (!use_graph) return gpt2_enqueue(m, 1, 0, true);
-    if (!m->step_graph) {
-        LLMQ_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-        int rc = gpt2_enqueue(m, 1, 0, true);
-        hipGraph_t g = nullptr;
-        hipError_t e = hipStreamEndCapture(ctx->stream, &g);
-        if (rc != LLMQ_OK) {
-            if (g) hipGraphDestroy(g);
-            return rc;
-        }
-        if (e != hipSuccess) return llmq_set_error(LLMQ_EHIP, "decode graph capture: %s", hipGetErrorString(e));
-        m->step_graph_def = g;
-        LLMQ_HIP(hipGraphInstantiate(&m->step_graph, g, nullptr, nullptr, 0));
-    }
+    if (!m->step_graph)
+        RC(llmq_capture(ctx->stream, [&] { return gpt2_enqueue(m, 1, 0, true); }, &m->step_graph_def,
+                        &m->step_graph));
     LLMQ_HIP(hipGraphLaunch(m->step_graph, ctx->stream));
     return LLMQ_OK;
 }
@@ -1068,10 +1058,9 @@ int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int st
     llmq_ctx *ctx = m->ctx;
     const char *ge = getenv("LLMQ_GRAPH");
     const bool use_graph = !(ge && ge[0] == '0');
-    hipEvent_t e0, e1, e2;
-    LLMQ_HIP(hipEventCreate(&e0));
-    LLMQ_HIP(hipEventCreate(&e1));
-    LLMQ_HIP(hipEventCreate(&e2));
+    ScopedEvents ev;
+    RC(ev.create());
+    hipEvent_t e0 = ev.e[0], e1 = ev.e[1], e2 = ev.e[2];
     LLMQ_HIP(hipMemcpyAsync(m->tokens, prompt, sizeof(int64_t) * n_prompt, hipMemcpyHostToDevice, ctx->stream));
     const int init_state[4] = {n_prompt - 1, -1, 0, 0};
     LLMQ_HIP(hipMemcpyAsync(m->state, init_state, sizeof(init_state), hipMemcpyHostToDevice, ctx->stream));
@@ -1092,9 +1081,6 @@ int llmq_gpt2_generate(llmq_gpt2 *m, const int64_t *prompt, int n_prompt, int st
     LLMQ_HIP(hipEventElapsedTime(&b, e1, e2));
     if (prefill_ms) *prefill_ms = a;
     if (decode_ms) *decode_ms = b;
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
-    hipEventDestroy(e2);
     std::vector<int64_t> g(steps > 0 ? steps : 1);
     if (steps > 0) LLMQ_HIP(hipMemcpy(g.data(), m->gen, sizeof(int64_t) * steps, hipMemcpyDeviceToHost));
     int n = 0;

@@ -109,6 +109,50 @@ struct OwnStream {
     }
 };
 
+// Timing events of one call, destroyed on every return path.
+struct ScopedEvents {
+    hipEvent_t e[3] = {nullptr, nullptr, nullptr};
+    int create() {
+        for (auto &x : e)
+            if (hipEventCreate(&x) != hipSuccess) {
+                x = nullptr;
+                return llmq_set_error(LLMQ_EHIP, "hipEventCreate failed");
+            }
+        return LLMQ_OK;
+    }
+    ~ScopedEvents() {
+        for (auto x : e)
+            if (x) hipEventDestroy(x);
+    }
+};
+
+// Captures what enqueue() launches on stream s into an instantiated graph.
+// On success *def / *exec receive it; on any failure (a launch error during
+// capture, the end of capture, instantiation) nothing is kept, both stay as
+// they were and the stream has left capture mode.
+template <class F>
+int llmq_capture(hipStream_t s, F &&enqueue, hipGraph_t *def, hipGraphExec_t *exec) {
+    hipError_t b = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (b != hipSuccess) return llmq_set_error(LLMQ_EHIP, "hipStreamBeginCapture: %s", hipGetErrorString(b));
+    int rc = enqueue();
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc == LLMQ_OK && e != hipSuccess)
+        rc = llmq_set_error(LLMQ_EHIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    hipGraphExec_t x = nullptr;
+    if (rc == LLMQ_OK) {
+        hipError_t i = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+        if (i != hipSuccess) rc = llmq_set_error(LLMQ_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(i));
+    }
+    if (rc != LLMQ_OK) {
+        if (g) hipGraphDestroy(g);
+        return rc;
+    }
+    *def = g;
+    *exec = x;
+    return LLMQ_OK;
+}
+
 // Argmax partial of one workgroup: the largest value and its (smallest) index.
 struct ArgmaxPart {
     float v;

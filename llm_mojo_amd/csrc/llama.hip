@@ -645,23 +645,12 @@ int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int B, int n_prom
     const char *ge = getenv("LLMQ_GRAPH");
     const bool use_graph = !(ge && ge[0] == '0');  // LLMQ_GRAPH=0: steps launched one by one
     if (use_graph && steps > 1 && !m->step_graph) {
-        LLMQ_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-        int rc = llama_step(m, B);
-        hipGraph_t g = nullptr;
-        hipError_t e = hipStreamEndCapture(ctx->stream, &g);
-        if (rc != LLMQ_OK) {
-            if (g) hipGraphDestroy(g);
-            return rc;
-        }
-        if (e != hipSuccess) return llmq_set_error(LLMQ_EHIP, "llama decode capture: %s", hipGetErrorString(e));
-        m->step_graph_def = g;
-        LLMQ_HIP(hipGraphInstantiate(&m->step_graph, g, nullptr, nullptr, 0));
+        RC(llmq_capture(ctx->stream, [&] { return llama_step(m, B); }, &m->step_graph_def, &m->step_graph));
         m->graph_B = B;
     }
-    hipEvent_t e0, e1, e2;
-    LLMQ_HIP(hipEventCreate(&e0));
-    LLMQ_HIP(hipEventCreate(&e1));
-    LLMQ_HIP(hipEventCreate(&e2));
+    ScopedEvents ev;
+    RC(ev.create());
+    hipEvent_t e0 = ev.e[0], e1 = ev.e[1], e2 = ev.e[2];
     LLMQ_HIP(hipStreamSynchronize(ctx->stream));
     LLMQ_HIP(hipEventRecord(e0, ctx->stream));
     for (int b = 0; b < B; b++) RC(llama_prefill(m, b, prompts + (int64_t)b * n_prompt, n_prompt, 0, B, true));
@@ -681,9 +670,6 @@ int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int B, int n_prom
     LLMQ_HIP(hipEventElapsedTime(&bm, e1, e2));
     if (prefill_ms) *prefill_ms = a;
     if (decode_ms) *decode_ms = bm;
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
-    hipEventDestroy(e2);
     LLMQ_HIP(hipMemcpy(out_tokens, m->gen, sizeof(int64_t) * steps * B, hipMemcpyDeviceToHost));
     return LLMQ_OK;
 }

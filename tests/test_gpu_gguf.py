@@ -208,3 +208,36 @@ def test_gguf_file_matrices_and_llama(gpu, tmp_path):
     assert np.array_equal(f.forward(0, toks, 0), d.forward(0, toks, 0))
     f.free()
     d.free()
+
+
+CONFIG2_KINDS = ["Q4_0", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
+
+
+@pytest.mark.parametrize("kind", CONFIG2_KINDS)
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)])
+def test_gguf_gemv_config2_shapes(gpu, orc, kind, K, N):
+    """Config 2's own shapes (K x N, batch 1, float activations): every
+    matrix of 20 MB or more takes the streamed form (two code steps in
+    flight a wave), the K-quants included; 1e-5 of max |out| against the
+    oracle's gguf_gemv, and deterministic from run to run."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    t = orc.GGML[kind]
+    blocks = synth.gguf_blocks(t, N, K, seed=7 + t)
+    rng = np.random.default_rng(K + N + t)
+    x = rng.normal(0, 1, K).astype(np.float32)
+    print("config 2 gemv", kind, K, N, flush=True)
+    g = lm.HipGGUFMatrix.from_blocks(ctx, t, blocks, N, K)
+    out = torch.zeros((1, N), device="cuda")
+    out2 = torch.zeros((1, N), device="cuda")
+    xd = dev(torch, x.reshape(1, -1))
+    lm.linear(ctx, out, xd, g)
+    lm.linear(ctx, out2, xd, g)
+    torch.cuda.synchronize()
+    orc.set_threads(16)
+    want = orc.gguf_gemv(t, blocks, N, K, x, None, 0)
+    got = out.cpu().numpy()[0]
+    assert np.array_equal(got, out2.cpu().numpy()[0])
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
+    g.free()

@@ -121,3 +121,87 @@ def test_llama_long_context_decode(gpu):
         assert toks[i, 0] == want, (i, toks[:, 0], want)
         logits = ref.forward(0, [want], 1026 + i)
     m.free()
+
+
+def greedy_vs_numpy(toks, ref, seq, prompt, pos0):
+    """Compare greedy tokens with NumPy greedy decoding from `prompt`; a step
+    whose NumPy top-2 margin is under 1e-3 of max |logit| ends the comparison.
+    Returns the number of tokens compared."""
+    logits = ref.forward(seq, prompt, pos0)
+    for i in range(len(toks)):
+        top = np.sort(logits)[-2:]
+        want = int(np.argmax(logits))
+        if top[1] - top[0] < 1e-3 * np.max(np.abs(logits)):
+            return i
+        assert toks[i] == want, (i, list(toks), want)
+        logits = ref.forward(seq, [want], pos0 + len(prompt) + i)
+    return len(toks)
+
+
+def test_llama_full_width_layers_match_numpy(gpu):
+    """Two layers at the TinyLlama width (d 2048, 32 query / 4 key-value
+    heads, FFN 5632, Q4_K) under its 32000 x 2048 Q6_K int16 head: a
+    40-token prompt, then 4 positions more on the same cache, logits within
+    1e-3 of max |logit| and the same top-1."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+    from llm_mojo_amd.llama import TINYLLAMA
+
+    cfg = dict(TINYLLAMA, n_layer=2, max_t=64)
+    tensors = synth.llama_tensors(cfg, 9)
+    toks = synth.llama_prompts(9, 1, 44, cfg["vocab"])[0]
+    print("llama full width: load", flush=True)
+    m = lm.Llama(ctx, cfg, tensors)
+    ref = NumpyLlama(cfg, tensors)
+    for lo, hi in ((0, 40), (40, 41), (41, 44)):
+        print(f"llama full width: tokens {lo}..{hi}", flush=True)
+        got = m.forward(0, toks[lo:hi], lo)
+        want = ref.forward(0, toks[lo:hi], lo)
+        assert rel(got, want) < 1e-3, (lo, rel(got, want))
+        assert int(np.argmax(got)) == int(np.argmax(want))
+    m.free()
+
+
+@pytest.mark.timeout(400)
+def test_llama_full_depth_greedy_matches_numpy(gpu):
+    """All 22 layers of the TinyLlama shape: a 16-token prompt and 4 greedy
+    tokens from the device loop against NumPy greedy decoding (the margin
+    rule above)."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+    from llm_mojo_amd.llama import TINYLLAMA
+
+    cfg = dict(TINYLLAMA, max_t=64)
+    tensors = synth.llama_tensors(cfg, 11)
+    prompt = synth.llama_prompts(11, 1, 16, cfg["vocab"])
+    print("llama full depth: generate", flush=True)
+    m = lm.Llama(ctx, cfg, tensors)
+    toks, _, _ = m.generate(prompt, 4)
+    m.free()
+    print("llama full depth: numpy", flush=True)
+    ref = NumpyLlama(cfg, tensors)
+    n = greedy_vs_numpy(toks[:, 0], ref, 0, prompt[0], 0)
+    print("llama full depth: tokens compared", n, flush=True)
+    assert n >= 2
+
+
+def test_llama_full_shape_batch16_equals_batch1(gpu):
+    """The full TinyLlama shape at batch 16: 16 different 24-token prompts,
+    12 greedy tokens each through the captured batch-16 step; each
+    sequence's tokens equal its own batch-1 run."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+    from llm_mojo_amd.llama import TINYLLAMA
+
+    cfg = dict(TINYLLAMA, batch=16, max_t=64)
+    tensors = synth.llama_tensors(cfg, 10)
+    prompts = synth.llama_prompts(10, 16, 24, cfg["vocab"])
+    print("llama batch 16: generate", flush=True)
+    m = lm.Llama(ctx, cfg, tensors)
+    many, _, _ = m.generate(prompts, 12)
+    assert many.shape == (12, 16)
+    for b in range(16):
+        one, _, _ = m.generate(prompts[b:b + 1], 12)
+        assert np.array_equal(one[:, 0], many[:, b]), (b, one[:, 0].tolist(), many[:, b].tolist())
+    print("llama batch 16: 16 sequences equal their batch-1 runs", flush=True)
+    m.free()

@@ -109,8 +109,8 @@ int llmq_memcpy_d2h(llmq_ctx *ctx, void *dst, const void *src, size_t bytes) {
 
 // ------------------------------------------------------------ weight formats
 
-static int mat_alloc_quant(llmq_ctx *ctx, int bits, int group, int sym, int a16, int64_t n, int64_t k,
-                           llmq_mat **out) {
+// The shapes QuantMatrix storage accepts (n output rows, k inputs).
+static int quant_shape_ok(int bits, int group, int a16, int64_t n, int64_t k) {
     LLMQ_REQUIRE(bits == 4 || bits == 8, "from_f32: BITS must be 4 or 8");
     LLMQ_REQUIRE(n > 0 && k > 0, "from_f32: empty matrix");
     const int64_t g = group == 0 ? k : group;
@@ -124,6 +124,21 @@ static int mat_alloc_quant(llmq_ctx *ctx, int bits, int group, int sym, int a16,
     LLMQ_REQUIRE(!(a16 && bits == 4 && g == 32 && k % 256 != 0),
                  "int4-g32-a16 (BLOCKED layout) needs the reduction axis in whole 256-weight blocks, got %lld",
                  (long long)k);
+    {   // every kernel addresses one array with 32-bit buffer offsets (0x80000000 = a disabled load)
+        const int64_t nt = (n + LLMQ_TILE_ROWS - 1) / LLMQ_TILE_ROWS;
+        const int64_t cb = (nt * (k * bits / 8 / 16) + LLMQ_PAD_CHUNKS) * 256,
+                      sb = (nt * (k / g) + LLMQ_PAD_CHUNKS) * LLMQ_TILE_ROWS * 2;
+        LLMQ_REQUIRE(cb < (int64_t)kLlmqOOB && sb < (int64_t)kLlmqOOB,
+                     "from_f32: %lld x %lld matrix: code array of %lld bytes reaches the 2 GiB limit",
+                     (long long)n, (long long)k, (long long)cb);
+    }
+    return LLMQ_OK;
+}
+
+static int mat_alloc_quant(llmq_ctx *ctx, int bits, int group, int sym, int a16, int64_t n, int64_t k,
+                           llmq_mat **out) {
+    RC(quant_shape_ok(bits, group, a16, n, k));
+    const int64_t g = group == 0 ? k : group;
     llmq_mat *m = new llmq_mat();
     m->ctx = ctx;
     m->kind = MAT_QUANT;
@@ -176,6 +191,7 @@ int llmq_mat_from_f32(llmq_ctx *ctx, int bits, int group, int sym, int a16, cons
                       int64_t cols, int reduce_rows, llmq_mat **out) {
     LLMQ_REQUIRE(ctx && src && out, "from_f32: bad arguments");
     LLMQ_REQUIRE(rows > 0 && cols > 0, "from_f32: empty matrix");
+    RC(quant_shape_ok(bits, group, a16, reduce_rows ? cols : rows, reduce_rows ? rows : cols));
     float *d = nullptr;
     const size_t bytes = sizeof(float) * (size_t)rows * cols;
     if (hipMalloc(&d, bytes) != hipSuccess) return llmq_set_error(LLMQ_ENOMEM, "from_f32: staging %zu bytes", bytes);

@@ -178,6 +178,8 @@ int gguf_upload(llmq_ctx *ctx, llmq_mat *m, int t, const uint8_t *blocks, int64_
     m->NG = (t == LLMQ_GGML_Q4_K || t == LLMQ_GGML_Q5_K || t == LLMQ_GGML_Q6_K) ? cols / 256 : 0;  // superblocks
     const int64_t ntc = (m->ntiles * m->CK + LLMQ_PAD_CHUNKS) * 16;   // per-chunk entries (with padding)
     const int64_t nts = (m->ntiles * m->NG + LLMQ_PAD_CHUNKS) * 16;   // per-superblock entries
+    LLMQ_REQUIRE(ntc * 16 < (int64_t)kLlmqOOB, "from_gguf: %lld x %lld matrix: code array reaches the 2 GiB limit",
+                 (long long)rows, (long long)cols);
     std::vector<uint8_t> codes((size_t)ntc * 16, 0);
     std::vector<uint16_t> meta16;
     std::vector<uint32_t> meta32, bits32;
@@ -249,6 +251,9 @@ int gguf_upload(llmq_ctx *ctx, llmq_mat *m, int t, const uint8_t *blocks, int64_
     }
     auto up = [&](void **dptr, const void *src, size_t bytes) -> int {
         if (!bytes) return LLMQ_OK;
+        // kernels address each array with 32-bit buffer offsets (0x80000000 = a disabled load)
+        if (bytes >= kLlmqOOB)
+            return llmq_set_error(LLMQ_EINVAL, "from_gguf: an array of %zu bytes reaches the 2 GiB limit", bytes);
         if (hipMalloc(dptr, bytes) != hipSuccess) return llmq_set_error(LLMQ_ENOMEM, "from_gguf: %zu bytes", bytes);
         if (hipMemcpyAsync(*dptr, src, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
             return llmq_set_error(LLMQ_EHIP, "from_gguf: copy failed");

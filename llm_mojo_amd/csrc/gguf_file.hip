@@ -115,8 +115,12 @@ int parse(llmq_gguf *g, const char *path) {
         t.rows = 1;
         for (uint32_t d = 1; d < ndims; d++) {
             const uint64_t dim = c.uint(8);
-            t.rows = dim == 0 || dim > ((uint64_t)1 << 40) ? 0 : t.rows * (int64_t)dim;
-            if (t.rows > ((int64_t)1 << 40)) t.rows = 0;
+            int64_t r = 0;  // 0 marks an impossible shape (refused below)
+            if (t.rows > 0 && dim > 0 && dim <= ((uint64_t)1 << 40) && !__builtin_mul_overflow(t.rows, (int64_t)dim, &r) &&
+                r <= ((int64_t)1 << 40))
+                t.rows = r;
+            else
+                t.rows = 0;
         }
         t.type = (int)c.uint(4);
         t.offset = (int64_t)c.uint(8);
@@ -200,7 +204,9 @@ int llmq_gguf_tensor_data(const llmq_gguf *g, int64_t i, const void **data, int6
     const auto &t = g->tensors[(size_t)i];
     const int64_t n = tensor_bytes(t);
     LLMQ_REQUIRE(n > 0, "%s: unsupported format (ggml type %d)", t.name.c_str(), t.type);
-    LLMQ_REQUIRE(t.offset >= 0 && g->data_start + t.offset + n <= (int64_t)g->size,
+    // unsigned comparisons with no sum that can wrap
+    const uint64_t size = g->size, start = (uint64_t)g->data_start, off = (uint64_t)t.offset, len = (uint64_t)n;
+    LLMQ_REQUIRE(t.offset >= 0 && start <= size && len <= size - start && off <= size - start - len,
                  "%s: tensor data past the end of the file", t.name.c_str());
     *data = g->buf + g->data_start + t.offset;
     if (bytes) *bytes = n;

@@ -98,3 +98,29 @@ def test_reader_errors(lm, tmp_path):
     assert g.tensor_bytes("position_embd.weight").size == 160
     with pytest.raises(KeyError):
         g.info("nope")
+
+
+def test_reader_refuses_overflowing_fields(lm, tmp_path):
+    """Index fields whose arithmetic would wrap are refused with LLMQ_EINVAL
+    (-1), never read through: a tensor offset of 2^63 - 16 (the end of its
+    data would wrap past 2^63) and dimensions whose product exceeds 2^63."""
+    data = bytes(34)  # one Q8_0 block
+    p = tmp_path / "offset.gguf"
+    gw.write(p, [("t", 8, [32, 1], data)])
+    blob = bytearray(p.read_bytes())
+    at = 24 + 8 + 1 + 4 + 2 * 8 + 4  # header, name "t", n_dims, two dims, type: the u64 offset
+    assert int.from_bytes(blob[at:at + 8], "little") == 0
+    blob[at:at + 8] = (2 ** 63 - 16).to_bytes(8, "little")
+    p.write_bytes(bytes(blob))
+    g = lm.GGUFFile(p)
+    with pytest.raises(lm.LlmqError, match=r"error -1: .*past the end"):
+        g.tensor_bytes("t")
+    g.close()
+    p = tmp_path / "dims.gguf"
+    gw.write(p, [("t", 8, [32, 2 ** 33, 2 ** 33], data)])  # 2^66 rows
+    with pytest.raises(lm.LlmqError, match=r"error -1: .*impossible shape"):
+        lm.GGUFFile(p)
+    p = tmp_path / "dims2.gguf"
+    gw.write(p, [("t", 8, [32, 2 ** 40, 2 ** 40, 3], data)])
+    with pytest.raises(lm.LlmqError, match=r"error -1: .*impossible shape"):
+        lm.GGUFFile(p)

@@ -320,3 +320,23 @@ def test_errors_are_reported(gpu):
     out = torch.zeros((1, 8), dtype=torch.float32, device="cuda")
     with pytest.raises(lm.LlmqError, match="IN="):
         lm.linear(ctx, out, torch.zeros((1, 32), device="cuda"), g)
+
+
+def test_arrays_past_2gib_are_refused(gpu):
+    """Kernels address each matrix array with 32-bit buffer offsets, so a
+    matrix whose code array would reach 2 GiB is refused at creation, before
+    its source is read (the sources here are deliberately tiny)."""
+    import ctypes
+
+    torch, lm, ctx = gpu
+    src = torch.zeros(64, dtype=torch.float32, device="cuda")
+    h = ctypes.c_void_p()
+    # int8, 65536 x 65536: 4 GiB of codes
+    rc = lm.lib().llmq_mat_from_f32_device(ctx.h, 8, 0, 0, 1, ctypes.c_void_p(src.data_ptr()), 65536, 65536, 0,
+                                           ctypes.byref(h))
+    assert rc != 0 and not h.value
+    assert b"2 GiB" in lm.lib().llmq_last_error()
+    with pytest.raises(lm.LlmqError, match="2 GiB"):  # Q8_0 131072 x 32768: 4 GiB of codes
+        lm.HipGGUFMatrix.from_blocks(ctx, 8, np.zeros(34, np.uint8), 131072, 32768)
+    ok = lm.HipQuantMatrix.from_f32(ctx, torch.zeros((64, 256), dtype=torch.float32, device="cuda"), 8, 0)
+    assert ok.nbytes() > 0

@@ -158,6 +158,22 @@ LLMQ_API int llmq_quantize_rows(llmq_ctx *ctx, const float *x, int64_t T, int64_
  * flags: LLMQ_BIAS | LLMQ_GELU | LLMQ_RESID. */
 LLMQ_API int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, const float *bias, int64_t T,
                          int64_t IN, int64_t OUT, int flags);
+/* No counterpart in the reference: llmq_linear for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results
+ * (bit for bit) as llmq_linear; where llmq_linear grows the context's
+ * workspace (the prompt GEMM's int16 activation codes and row scales), this
+ * form uses a fixed per-GPU scratch array of LLMQ_NOALLOC_SCRATCH_BYTES
+ * that each GPU the library runs on holds until the process ends.  It
+ * calls no hipMalloc / hipFree.  Sizes needing more scratch than that
+ * (T x IN x 2 bytes rounded up to 256, plus T x 4) return LLMQ_EINVAL.
+ * Every call on one GPU shares the array: calls that overlap in time on one
+ * GPU (different streams or threads) race; calls ordered on one stream do
+ * not.  Nothing in the scratch needs to start at zero (each call writes all
+ * it reads). */
+#define LLMQ_NOALLOC_SCRATCH_BYTES (8 << 20)
+LLMQ_API int llmq_linear_noalloc(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, const float *bias,
+                                 int64_t T, int64_t IN, int64_t OUT, int flags);
 /* The same with LayerNorm (kernels.layernorm, 179-197; eps 1e-5) applied to
  * each input row first: the LN -> linear pairs of Model.decode
  * (gpt2t.mojo:390-399, 419-428) in one call (one kernel for a16 matrices;

@@ -46,6 +46,7 @@ SIGNATURES = {
     "llmq_mat_dequant_row": (I32, [P, P, I64, P]),
     "llmq_quantize_rows": (I32, [P, P, I64, I64, P, P]),
     "llmq_linear": (I32, [P, P, P, P, P, I64, I64, I64, I32]),
+    "llmq_linear_noalloc": (I32, [P, P, P, P, P, I64, I64, I64, I32]),
     "llmq_ln_linear": (I32, [P, P, P, P, P, P, P, I64, I64, I64, I32]),
     "llmq_head": (I32, [P, P, P, P, I64, I64, I64]),
     "llmq_layernorm": (I32, [P, P, P, P, P, I64, I64]),

@@ -6,12 +6,37 @@
 #include <string.h>
 
 #include <chrono>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
 #include "gpt2.h"
 
 static thread_local char g_err[512];
+
+// The scratch of llmq_linear_noalloc: the prompt GEMM's int16 activation
+// codes (256-byte aligned) and per-row scales, which llmq_linear keeps in the
+// context's grow-only workspace.  Each GPU the library runs on holds its own
+// copy for the life of the process.  The array's name is a host-side stand-in
+// (never passed to a kernel): host code uses the device address that
+// hipGetSymbolAddress returns, looked up once per device by llmq_init.
+static __device__ __align__(256) uint8_t scratch[LLMQ_NOALLOC_SCRATCH_BYTES];
+
+static int scratch_address(int device, void **p) {
+    static std::mutex mu;
+    static void *addr[64] = {};
+    LLMQ_REQUIRE(device >= 0 && device < 64, "llmq_init: device %d beyond 64", device);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[device]) {  // with `device` current
+        void *a = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !a)
+            return llmq_set_error(LLMQ_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        addr[device] = a;
+    }
+    *p = addr[device];
+    return LLMQ_OK;
+}
 
 int llmq_set_error(int code, const char *fmt, ...) {
     va_list ap;
@@ -57,7 +82,15 @@ int llmq_init(int device, llmq_ctx **out) {
         return llmq_set_error(LLMQ_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
     }
     c->stream = c->own_stream;
-    LLMQ_HIP(hipGetDeviceProperties(&c->prop, device));
+    int rc = LLMQ_OK;
+    e = hipGetDeviceProperties(&c->prop, device);
+    if (e != hipSuccess) rc = llmq_set_error(LLMQ_EHIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    if (rc == LLMQ_OK) rc = scratch_address(device, &c->scratch);
+    if (rc != LLMQ_OK) {
+        hipStreamDestroy(c->own_stream);
+        delete c;
+        return rc;
+    }
     *out = c;
     return LLMQ_OK;
 }
@@ -437,6 +470,33 @@ int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, co
     rq.bias = bias;
     rq.T = T;
     rq.flags = flags;
+    return launch_gemv_a16(ctx, rq);
+}
+
+int llmq_linear_noalloc(llmq_ctx *ctx, float *out, const float *x, const llmq_mat *w, const float *bias, int64_t T,
+                        int64_t IN, int64_t OUT, int flags) {
+    LLMQ_REQUIRE(ctx && ctx->scratch, "linear_noalloc: null context");
+    RC(check_linear(w, IN, OUT));
+    LLMQ_REQUIRE(T >= 1, "linear_noalloc: T must be >= 1");
+    // the most the prompt GEMM keeps there: T x IN int16 codes (rounded up to
+    // 256 bytes) and T float scales
+    const int64_t need = ((T * IN * 2 + 255) & ~(int64_t)255) + T * 4;
+    LLMQ_REQUIRE(need <= (int64_t)LLMQ_NOALLOC_SCRATCH_BYTES,
+                 "linear_noalloc: %lld tokens x %lld inputs need %lld bytes of scratch, the maximum is %d",
+                 (long long)T, (long long)IN, (long long)need, LLMQ_NOALLOC_SCRATCH_BYTES);
+    if (is_float_act(w)) {  // as llmq_linear: these kernels use no scratch
+        if (T == 1) return launch_gguf_gemv(ctx, w, x, out, bias, flags, nullptr, 0);
+        return launch_gguf_gemm(ctx, w, x, IN, T, out, OUT, bias, flags);
+    }
+    GemvRequest rq;
+    rq.w = w;
+    rq.x = x;
+    rq.out = out;
+    rq.bias = bias;
+    rq.T = T;
+    rq.flags = flags;
+    rq.ws = ctx->scratch;
+    rq.ws_cap = LLMQ_NOALLOC_SCRATCH_BYTES;
     return launch_gemv_a16(ctx, rq);
 }
 

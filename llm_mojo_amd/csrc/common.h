@@ -36,6 +36,7 @@ struct llmq_ctx {
     hipDeviceProp_t prop{};
     void *ws = nullptr;  // grow-only workspace (prompt-side int16 activation codes)
     size_t ws_bytes = 0;
+    void *scratch = nullptr;  // this device's no-allocation scratch (llmq_linear_noalloc), from llmq_init
 };
 
 // The context's workspace of at least `bytes` (api.hip); growing it waits for
@@ -181,6 +182,8 @@ struct GemvRequest {
     int32_t *dbg = nullptr;        // per-chunk exact integer sums (T == 1, no LN)
     int16_t *xq_out = nullptr;     // quantized activations of the first token block
     float *sx_out = nullptr;
+    void *ws = nullptr;            // caller-given workspace in place of the context's (never grown)
+    size_t ws_cap = 0;             // its size in bytes
 };
 int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq);
 // Number of argmax partials launch_gemv_a16 writes for a T == 1 GEMV of w

@@ -498,9 +498,14 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
         if (const char *e = getenv("LLMQ_MFMA_MIN_T")) min_t = atoi(e);
         if (rq.T >= min_t && min_t > 0 && gemm_mfma_supports(w, rq.T)) {
             const size_t xb = ((size_t)rq.T * w->k * 2 + 255) & ~(size_t)255;
-            void *ws = nullptr;
-            const int rc = ctx_workspace(ctx, xb + (size_t)rq.T * 4, &ws);
-            if (rc != LLMQ_OK) return rc;
+            const size_t need = xb + (size_t)rq.T * 4;
+            void *ws = rq.ws;
+            if (ws) {
+                LLMQ_REQUIRE(need <= rq.ws_cap, "linear: %lld tokens x %lld inputs need %zu bytes of workspace, %zu given",
+                             (long long)rq.T, (long long)w->k, need, rq.ws_cap);
+            } else {
+                RC(ctx_workspace(ctx, need, &ws));
+            }
             return launch_gemm_mfma(ctx, rq, reinterpret_cast<int16_t *>(ws),
                                     reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ws) + xb));
         }

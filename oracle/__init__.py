@@ -76,6 +76,8 @@ I32 = ctypes.c_int
 def _declare(L):
     sig = {
         "orc_set_round_half_even": (None, [I32]),
+        "orc_ties": (None, [P]),
+        "orc_reset_ties": (None, []),
         "orc_exp": (ctypes.c_float, [ctypes.c_float]),
         "orc_tanh": (ctypes.c_float, [ctypes.c_float]),
         "orc_exp_n": (None, [P, P, I64]),
@@ -146,6 +148,19 @@ def ptr(a):
 
 def set_round_half_even(on):
     lib().orc_set_round_half_even(1 if on else 0)
+
+
+TIE_SITES = ("weights", "activations", "kv", "other")
+
+
+def ties(reset=False):
+    """Exact .5 ties the rounding sites met since the last reset (the cases
+    where the unpinned tie rule decides a code): {site: count}."""
+    out = np.zeros(4, np.int64)
+    lib().orc_ties(out.ctypes.data)
+    if reset:
+        lib().orc_reset_ties()
+    return dict(zip(TIE_SITES, (int(v) for v in out)))
 
 
 def set_threads(n):

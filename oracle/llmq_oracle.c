@@ -19,6 +19,9 @@
  * Pinning status (what each function is checked against lives in tests/):
  *   - tie rule of Mojo's round(): parity unpinned (Mojo 1.1 stdlib absent);
  *     default half-away-from-zero, switchable with orc_set_round_half_even.
+ *     Exact ties are counted per rounding site (orc_ties): config 0 meets
+ *     136 in its weights and ~30 per forward in its int16 activation codes;
+ *     the two rules give the same greedy tokens there (tests/).
  *   - order of SIMD.reduce_add / reduce_max: parity unpinned; emulated as a
  *     halving tree (lanes 0-7 + 8-15, ...).  Moves fp32 bits only.
  *   - last-ulp results of Mojo's exp / tanh: parity unpinned (Mojo 1.1
@@ -46,8 +49,23 @@ static int g_half_even = 0;
 /* Mojo std.math.round (tensor.mojo:377,381; kernels.mojo:415;
  * kvcache.mojo:330).  Tie rule unpinned: half away from zero by default. */
 void orc_set_round_half_even(int on) { g_half_even = on; }
-static inline float orc_round(float v) { return g_half_even ? nearbyintf(v) : roundf(v); }
 static inline double orc_round_d(double v) { return g_half_even ? nearbyint(v) : round(v); }
+
+/* Exact .5 ties met by each rounding site (where the tie rule decides the
+ * result): 0 weight codes and zero points (from_f32), 1 int16 activation
+ * codes (quantize_rows), 2 int8 KV codes (QuantKV.store), 3 the rest. */
+static int64_t g_ties[4];
+void orc_ties(int64_t *out) {
+    for (int i = 0; i < 4; i++) out[i] = __atomic_load_n(&g_ties[i], __ATOMIC_RELAXED);
+}
+void orc_reset_ties(void) {
+    for (int i = 0; i < 4; i++) __atomic_store_n(&g_ties[i], 0, __ATOMIC_RELAXED);
+}
+static inline float orc_round_at(float v, int site) {
+    if (fabsf(v - truncf(v)) == 0.5f) __atomic_fetch_add(&g_ties[site], 1, __ATOMIC_RELAXED);
+    return g_half_even ? nearbyintf(v) : roundf(v);
+}
+static inline float orc_round(float v) { return orc_round_at(v, 3); }
 
 /* Int(float) for a value already rounded to an integer.  NaN (a scale that
  * rounded to zero in float16: outside the reference's defined inputs) maps
@@ -304,11 +322,11 @@ int orc_qm_from_f32(orc_qm *m, const float *src, int64_t rows, int64_t cols, int
             if (s == 0.0f) s = 1.0f;
             uint16_t s16 = orc_f32_to_f16(s);
             float sf = orc_f16_to_f32(s16);
-            int zp = m->sym ? half : clamp_code(orc_to_int(orc_round(-lo / sf)), levels);
+            int zp = m->sym ? half : clamp_code(orc_to_int(orc_round_at(-lo / sf, 0)), levels);
             m->scale[r * gpr + g] = s16;
             m->zp[r * gpr + g] = (uint8_t)zp;
             for (int64_t j = 0; j < group; j++) {
-                int64_t u = orc_to_int(orc_round(vals[j] / sf)) + zp;
+                int64_t u = orc_to_int(orc_round_at(vals[j] / sf, 0)) + zp;
                 set_code(m, r, g * group + j, clamp_code(u, levels));
             }
         }
@@ -526,7 +544,7 @@ void orc_quantize_rows(const float *x, int64_t T, int64_t IN, int16_t *xq, float
         if (s == 0.0f) s = 1.0f;
         sx[t] = s;
         float inv = 1.0f / s;
-        for (int64_t i = 0; i < IN; i++) xq[t * IN + i] = (int16_t)orc_to_int(orc_round(row[i] * inv));
+        for (int64_t i = 0; i < IN; i++) xq[t * IN + i] = (int16_t)orc_to_int(orc_round_at(row[i] * inv, 1));
     }
 }
 
@@ -978,7 +996,7 @@ static float kv_quantize(const float *x, int n, int8_t *dst) {
     float s = mx / 127.0f;
     if (s == 0.0f) s = 1.0f;
     float inv = 1.0f / s;
-    for (int i = 0; i < n; i++) dst[i] = (int8_t)orc_to_int(orc_round(x[i] * inv));
+    for (int i = 0; i < n; i++) dst[i] = (int8_t)orc_to_int(orc_round_at(x[i] * inv, 2));
     return s;
 }
 

@@ -77,6 +77,10 @@ def _declare(L):
     sig = {
         "orc_set_round_half_even": (None, [I32]),
         "orc_ties": (None, [P]),
+        "orc_cpu_vnni": (I32, []),
+        "orc_cpu_generate": (I32, [P, P, I32, I32, I32, P, P]),
+        "orc_cpu_decode": (P, [P, I64, I32, I32]),
+        "orc_cpu_head_seconds": (ctypes.c_double, [P, I32, I32]),
         "orc_reset_ties": (None, []),
         "orc_exp": (ctypes.c_float, [ctypes.c_float]),
         "orc_tanh": (ctypes.c_float, [ctypes.c_float]),
@@ -151,6 +155,12 @@ def set_round_half_even(on):
 
 
 TIE_SITES = ("weights", "activations", "kv", "other")
+
+
+def cpu_vnni():
+    """1 when this CPU runs the baseline's VPDPWSSD path (cpuid: AVX-512
+    F/BW/DQ/VL/VNNI, F16C, FMA, OS-enabled), 0 for the scalar emulation."""
+    return int(lib().orc_cpu_vnni())
 
 
 def ties(reset=False):
@@ -719,6 +729,30 @@ class GPT2:
         toks = np.ascontiguousarray(tokens, np.int64)
         p = lib().orc_gpt2_forward(self.h, ptr(toks), len(toks), pos0)
         return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(50257,)).copy()
+
+    def cpu_generate(self, prompt, steps, threads):
+        """The CPU baseline: the prompt through forward(), then greedy decode
+        through the team decode (gpt2t.mojo:350-447) on `threads` threads
+        with VPDPWSSD dots where the CPU has AVX-512 VNNI (cpu_vnni()).
+        Returns (tokens, prompt seconds, decode seconds)."""
+        toks = np.ascontiguousarray(prompt, np.int64)
+        out = np.zeros(max(steps, 1), np.int64)
+        secs = np.zeros(2, np.float64)
+        n = lib().orc_cpu_generate(self.h, ptr(toks), len(toks), steps, threads, ptr(out), ptr(secs))
+        if n < 0:
+            raise ValueError("cpu_generate: bad arguments or no threads")
+        return out[:n], float(secs[0]), float(secs[1])
+
+    def cpu_decode(self, token, pos, threads):
+        """One token at pos through the team decode: its logits."""
+        p = lib().orc_cpu_decode(self.h, int(token), int(pos), int(threads))
+        if not p:
+            raise ValueError("cpu_decode: bad arguments or no threads")
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(50257,)).copy()
+
+    def cpu_head_seconds(self, threads, reps=50):
+        """Median seconds of the int8 per-channel head on a team of `threads`."""
+        return float(lib().orc_cpu_head_seconds(self.h, int(threads), int(reps)))
 
     def forward_all(self, tokens):
         """Model.forward_all (gpt2t.mojo:448-459): logits [T, V]."""

@@ -1537,3 +1537,470 @@ int orc_gpt2_generate(orc_gpt2 *m, const int64_t *prompt, int n_prompt, int step
     }
     return generated;
 }
+
+/* ------------------------------------------------------------------------ */
+/* CPU baseline: the team decode (gpt2t.mojo:350-447) on AVX-512 VNNI        */
+/* ------------------------------------------------------------------------ */
+/* A restatement of the reference's decode as it runs on its own CPU: one
+ * parallel region per token, a team of nt threads meeting at a spin-then-
+ * yield barrier after each operation (team.mojo:36-82), thread 0 doing the
+ * serial pieces (embedding, LayerNorm, quantize_rows / permute_x_i16, the
+ * cache store), rows of every linear split into nt contiguous ranges
+ * (linear_team, kernels.mojo:774-866), heads dealt round-robin.  The integer
+ * dots run on VPDPWSSD (_mm512_dpwssd_epi32, the reference's dot_pairs,
+ * tensor.mojo:34-46) for the BLOCKED int4-g32 rows (tensor.mojo:522-540)
+ * and the int8 per-channel head (541-566, four rows at a time with the
+ * next rows prefetched).  Every float operation is the scalar oracle's, in
+ * its order, so the results are bit-identical to orc_gpt2_forward (tests/).
+ * Without AVX-512 VNNI (checked by cpuid) the scalar lane emulation runs
+ * instead and orc_cpu_vnni() reports 0. */
+#include <cpuid.h>
+#include <immintrin.h>
+#include <pthread.h>
+#include <sched.h>
+#include <time.h>
+
+#define VNNI __attribute__((target("avx512f,avx512bw,avx512dq,avx512vl,avx512vnni,f16c,fma")))
+
+/* cpuid leaf 7: AVX512F (EBX 16), AVX512DQ (17), AVX512BW (30), AVX512VL
+ * (31), AVX512_VNNI (ECX 11); leaf 1: F16C (ECX 29), FMA (12), OSXSAVE
+ * (27); XCR0 must enable the SSE, AVX and the three AVX-512 state parts. */
+int orc_cpu_vnni(void) {
+    unsigned a, b, c, d;
+    if (!__get_cpuid(1, &a, &b, &c, &d)) return 0;
+    if (!(c & (1u << 27)) || !(c & (1u << 29)) || !(c & (1u << 12))) return 0;
+    unsigned lo, hi;
+    __asm__ volatile("xgetbv" : "=a"(lo), "=d"(hi) : "c"(0));
+    if ((lo & 0xE6u) != 0xE6u) return 0;
+    if (!__get_cpuid_count(7, 0, &a, &b, &c, &d)) return 0;
+    const unsigned need_b = (1u << 16) | (1u << 17) | (1u << 30) | (1u << 31);
+    return (b & need_b) == need_b && (c & (1u << 11)) ? 1 : 0;
+}
+
+/* dot_row_i16, BLOCKED branch (tensor.mojo:522-540): per 256-weight block
+ * eight VPDPWSSD steps of 32 codes (low nibbles of the step's 16 bytes, then
+ * high nibbles) against the permuted activations, then per lane
+ * accf = fma(f32(acc) - zp * xs, scale, accf) with lane i in group i % 8. */
+VNNI static float dot_blocked_vnni(const orc_qm *m, int64_t row, const int16_t *xp, const float *xs) {
+    const uint8_t *p = m->data + row * m->k / 2;
+    const int64_t gpr = m->k / 32;
+    const __m128i nib = _mm_set1_epi8(0x0f);
+    __m512 accf = _mm512_setzero_ps();
+    for (int64_t blk = 0; blk < m->k / 256; blk++) {
+        __m512i acc = _mm512_setzero_si512();
+        for (int step = 0; step < 8; step++) {
+            const __m128i b = _mm_loadu_si128((const __m128i *)(p + blk * 128 + step * 16));
+            const __m256i lo = _mm256_cvtepu8_epi16(_mm_and_si128(b, nib));
+            const __m256i hi = _mm256_cvtepu8_epi16(_mm_and_si128(_mm_srli_epi16(b, 4), nib));
+            const __m512i u = _mm512_inserti64x4(_mm512_castsi256_si512(lo), hi, 1);
+            acc = _mm512_dpwssd_epi32(acc, _mm512_loadu_si512((const void *)(xp + blk * 256 + step * 32)), u);
+        }
+        const int64_t g0 = row * gpr + blk * 8;
+        const __m256i zp8 = _mm256_cvtepu8_epi32(_mm_loadl_epi64((const __m128i *)(m->zp + g0)));
+        const __m512 zp = _mm512_cvtepi32_ps(_mm512_broadcast_i32x8(zp8));
+        const __m512 sc = _mm512_broadcast_f32x8(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(m->scale + g0))));
+        const __m512 t = _mm512_sub_ps(_mm512_cvtepi32_ps(acc), _mm512_mul_ps(zp, _mm512_loadu_ps(xs + blk * 16)));
+        accf = _mm512_fmadd_ps(t, sc, accf);
+    }
+    float v[L16];
+    _mm512_storeu_ps(v, accf);
+    return red16(v);
+}
+
+/* dot_row_i16, int8 per-channel branch (tensor.mojo:541-566): codes - zp
+ * as int16, VPDPWSSD over 32 inputs a step, then fma(f32(acc), scale, 0).
+ * Four rows at a time share the activation loads (the reference's 4x
+ * unroll), the rows eight ahead prefetched; a single row for the tail. */
+VNNI static inline float ch8_finish(const orc_qm *m, int64_t row, __m512i acc) {
+    const float s = orc_f16_to_f32(m->scale[row]);
+    float v[L16];
+    _mm512_storeu_ps(v, _mm512_fmadd_ps(_mm512_cvtepi32_ps(acc), _mm512_set1_ps(s), _mm512_setzero_ps()));
+    return red16(v);
+}
+VNNI static inline __m512i ch8_step(const uint8_t *p, __m512i zp, __m512i xv, __m512i acc) {
+    const __m512i w = _mm512_sub_epi16(_mm512_cvtepu8_epi16(_mm256_loadu_si256((const __m256i *)p)), zp);
+    return _mm512_dpwssd_epi32(acc, xv, w);
+}
+VNNI static void dot_ch8_vnni4(const orc_qm *m, int64_t r, const int16_t *xq, float *out) {
+    const int64_t K = m->k;
+    const uint8_t *p0 = m->data + r * K, *p1 = p0 + K, *p2 = p1 + K, *p3 = p2 + K;
+    const __m512i z0 = _mm512_set1_epi16((short)m->zp[r]), z1 = _mm512_set1_epi16((short)m->zp[r + 1]),
+                  z2 = _mm512_set1_epi16((short)m->zp[r + 2]), z3 = _mm512_set1_epi16((short)m->zp[r + 3]);
+    __m512i a0 = _mm512_setzero_si512(), a1 = a0, a2 = a0, a3 = a0;
+    const char *pf = (const char *)(p0 + 8 * K);
+    const int64_t pf_end = (m->n - r - 8) * K; /* bytes the prefetch may touch */
+    for (int64_t k = 0; k < K; k += 32) {
+        if (k * 4 < pf_end) _mm_prefetch(pf + 4 * k, _MM_HINT_T0);
+        if (k * 4 + 64 < pf_end) _mm_prefetch(pf + 4 * k + 64, _MM_HINT_T0);
+        const __m512i xv = _mm512_loadu_si512((const void *)(xq + k));
+        a0 = ch8_step(p0 + k, z0, xv, a0);
+        a1 = ch8_step(p1 + k, z1, xv, a1);
+        a2 = ch8_step(p2 + k, z2, xv, a2);
+        a3 = ch8_step(p3 + k, z3, xv, a3);
+    }
+    out[0] = ch8_finish(m, r, a0);
+    out[1] = ch8_finish(m, r + 1, a1);
+    out[2] = ch8_finish(m, r + 2, a2);
+    out[3] = ch8_finish(m, r + 3, a3);
+}
+VNNI static float dot_ch8_vnni1(const orc_qm *m, int64_t r, const int16_t *xq) {
+    const uint8_t *p = m->data + r * m->k;
+    const __m512i z = _mm512_set1_epi16((short)m->zp[r]);
+    __m512i a = _mm512_setzero_si512();
+    for (int64_t k = 0; k < m->k; k += 32) a = ch8_step(p + k, z, _mm512_loadu_si512((const void *)(xq + k)), a);
+    return ch8_finish(m, r, a);
+}
+
+/* quantize_rows (kernels.mojo:400-416) for one row, 16 values a step:
+ * the same max, scale and product as orc_quantize_rows, and half-away
+ * rounding built exactly as t = trunc(v), t + sign(v) where |v - t| >= 0.5
+ * (roundf's result for every |v| < 2^23); ties are counted as the scalar
+ * path counts them.  IN must be a multiple of 16. */
+VNNI static void quantize_row_vnni(const float *x, int64_t IN, int16_t *xq, float *sx) {
+    __m512 mxv = _mm512_setzero_ps();
+    const __m512 absmask = _mm512_castsi512_ps(_mm512_set1_epi32(0x7fffffff));
+    for (int64_t i = 0; i < IN; i += 16) mxv = _mm512_max_ps(mxv, _mm512_and_ps(_mm512_loadu_ps(x + i), absmask));
+    const float mx = _mm512_reduce_max_ps(mxv);
+    float s = mx / 32767.0f;
+    if (s == 0.0f) s = 1.0f;
+    *sx = s;
+    const __m512 inv = _mm512_set1_ps(1.0f / s), half = _mm512_set1_ps(0.5f), one = _mm512_set1_ps(1.0f);
+    const __m512 signmask = _mm512_castsi512_ps(_mm512_set1_epi32((int)0x80000000u));
+    int64_t ties = 0;
+    for (int64_t i = 0; i < IN; i += 16) {
+        const __m512 v = _mm512_mul_ps(_mm512_loadu_ps(x + i), inv);
+        const __m512 t = _mm512_roundscale_ps(v, _MM_FROUND_TO_ZERO | _MM_FROUND_NO_EXC);
+        const __m512 d = _mm512_and_ps(_mm512_sub_ps(v, t), absmask);
+        const __mmask16 up = _mm512_cmp_ps_mask(d, half, _CMP_GE_OQ);
+        ties += __builtin_popcount((unsigned)_mm512_cmp_ps_mask(d, half, _CMP_EQ_OQ));
+        const __m512 step = _mm512_or_ps(one, _mm512_and_ps(v, signmask));
+        const __m512 r = _mm512_mask_add_ps(t, up, t, step);
+        _mm256_storeu_si256((__m256i *)(xq + i), _mm512_cvtepi32_epi16(_mm512_cvttps_epi32(r)));
+    }
+    if (ties) __atomic_fetch_add(&g_ties[1], ties, __ATOMIC_RELAXED);
+}
+
+/* attend_float_one (kvcache.mojo:113-150) for head h of one token at
+ * position pos, as orc_kv_attend_one computes it (the 16-lane score
+ * partials, the scale products, the sequential total, the fma chain per
+ * dimension), 16 values a step.  head_dim 64. */
+VNNI static void attend_one_vnni(const orc_kv *kv, float *out, const float *qkv, int layer, int h, int pos) {
+    const int HS = 64, C = kv->n_head * HS, npos = pos + 1;
+    const float scale = 1.0f / sqrtf((float)HS);
+    const float *q = qkv + h * HS;
+    const __m512 q0 = _mm512_loadu_ps(q), q1 = _mm512_loadu_ps(q + 16), q2 = _mm512_loadu_ps(q + 32),
+                 q3 = _mm512_loadu_ps(q + 48);
+    float scores[G_MAXT];
+    float mx = -INFINITY;
+    for (int s = 0; s < npos; s++) {
+        const int64_t sl = ((int64_t)layer * kv->max_t + s) * kv->n_head + h;
+        const int8_t *kp = kv->k + sl * HS;
+        __m512 d = _mm512_setzero_ps();
+        d = _mm512_add_ps(d, _mm512_mul_ps(q0, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)kp)))));
+        d = _mm512_add_ps(d, _mm512_mul_ps(q1, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)(kp + 16))))));
+        d = _mm512_add_ps(d, _mm512_mul_ps(q2, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)(kp + 32))))));
+        d = _mm512_add_ps(d, _mm512_mul_ps(q3, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)(kp + 48))))));
+        float dv[L16];
+        _mm512_storeu_ps(dv, d);
+        const float sc = red16(dv) * kv->ks[sl] * scale;
+        scores[s] = sc;
+        mx = sc > mx ? sc : mx;
+    }
+    for (int s = 0; s < npos; s++) scores[s] = orc_exp(scores[s] - mx);
+    float total = 0.0f;
+    for (int s = 0; s < npos; s++) total += scores[s];
+    __m512 a0 = _mm512_setzero_ps(), a1 = a0, a2 = a0, a3 = a0;
+    for (int s = 0; s < npos; s++) {
+        const float p = scores[s] / total;
+        const int64_t sl = ((int64_t)layer * kv->max_t + s) * kv->n_head + h;
+        const int8_t *vp = kv->v + sl * HS;
+        const __m512 ps = _mm512_set1_ps(p * kv->vs[sl]);
+        a0 = _mm512_fmadd_ps(ps, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)vp))), a0);
+        a1 = _mm512_fmadd_ps(ps, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)(vp + 16)))), a1);
+        a2 = _mm512_fmadd_ps(ps, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)(vp + 32)))), a2);
+        a3 = _mm512_fmadd_ps(ps, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)(vp + 48)))), a3);
+    }
+    float *o = out + h * HS;
+    (void)C;
+    _mm512_storeu_ps(o, a0);
+    _mm512_storeu_ps(o + 16, a1);
+    _mm512_storeu_ps(o + 32, a2);
+    _mm512_storeu_ps(o + 48, a3);
+}
+
+/* Team (team.mojo:36-82): arrival count and generation on separate cache
+ * lines; the last arrival resets the count, then advances the generation;
+ * the others spin (PAUSE) for up to 1000 polls, then yield. */
+typedef struct {
+    _Alignas(64) int64_t count;
+    _Alignas(64) int64_t gen;
+    _Alignas(64) int nt;
+} orc_team_bar;
+
+static void team_wait(orc_team_bar *t) {
+    const int64_t g = __atomic_load_n(&t->gen, __ATOMIC_ACQUIRE);
+    if (__atomic_fetch_add(&t->count, 1, __ATOMIC_ACQ_REL) == t->nt - 1) {
+        __atomic_store_n(&t->count, 0, __ATOMIC_RELAXED);
+        __atomic_store_n(&t->gen, g + 1, __ATOMIC_RELEASE);
+    } else {
+        int spins = 0;
+        while (__atomic_load_n(&t->gen, __ATOMIC_ACQUIRE) == g) {
+            if (spins < 1000) {
+                __builtin_ia32_pause();
+                spins++;
+            } else {
+                sched_yield();
+            }
+        }
+    }
+}
+
+typedef struct {
+    orc_gpt2 *m;
+    orc_team_bar bar;
+    int vnni, stop, job; /* job 0: a decode step; 1: the head alone */
+    int64_t token;
+    int pos;
+    /* linear_team's shared activations (gpt2t.mojo:370-373) */
+    int16_t xq[4 * G_C], xp[4 * G_C];
+    float xs[4 * G_C / 16], sx;
+    int permuted;
+} orc_team;
+
+static void team_split(int64_t n, int tid, int nt, int64_t *b, int64_t *e) { /* team.mojo split */
+    const int64_t per = (n + nt - 1) / nt;
+    *b = tid * per < n ? tid * per : n;
+    *e = (tid + 1) * per < n ? (tid + 1) * per : n;
+}
+
+/* linear_team (kernels.mojo:774-866), ACT16 branch; ends with a barrier. */
+static void team_linear(orc_team *c, int tid, float *out, const float *x, const orc_qm *w, const float *b,
+                        int64_t IN, int64_t OUT, int flags) {
+    if (tid == 0) {
+        if (c->vnni && IN % 16 == 0)
+            quantize_row_vnni(x, IN, c->xq, &c->sx);
+        else
+            orc_quantize_rows(x, 1, IN, c->xq, &c->sx);
+        c->permuted = orc_qm_permute_x_i16(w, c->xq, IN, c->xp, c->xs);
+    }
+    team_wait(&c->bar);
+    const int16_t *x1 = c->permuted ? c->xp : c->xq;
+    const float s = c->sx;
+    int64_t o0, o1;
+    team_split(OUT, tid, c->bar.nt, &o0, &o1);
+    if (c->vnni && w->perch && w->bits == 8) {
+        for (int64_t o = o0; o < o1; o += 4) {
+            const int n = o1 - o < 4 ? (int)(o1 - o) : 4;
+            float d[4];
+            if (n == 4)
+                dot_ch8_vnni4(w, o, x1, d);
+            else
+                for (int j = 0; j < n; j++) d[j] = dot_ch8_vnni1(w, o + j, x1);
+            for (int j = 0; j < n; j++) {
+                float r = d[j] * s;
+                if (flags & EPI_BIAS) r += b[o + j];
+                finish(out, o + j, r, flags);
+            }
+        }
+    } else {
+        for (int64_t o = o0; o < o1; o++) {
+            float r = (c->vnni && w->blocked ? dot_blocked_vnni(w, o, x1, c->xs) : orc_qm_dot_row_i16(w, o, x1, c->xs)) * s;
+            if (flags & EPI_BIAS) r += b[o];
+            finish(out, o, r, flags);
+        }
+    }
+    team_wait(&c->bar);
+}
+
+/* Model.decode's worker (gpt2t.mojo:375-444) for one token. */
+static void team_decode(orc_team *c, int tid) {
+    orc_gpt2 *m = c->m;
+    const int C = G_C, nt = c->bar.nt;
+    if (tid == 0) {
+        orc_qm_dequant_row(&m->wte, c->token, m->x);
+        const float *p = m->wpe + (int64_t)c->pos * C;
+        for (int i = 0; i < C; i++) m->x[i] = m->x[i] + p[i];
+    }
+    for (int l = 0; l < G_NL; l++) {
+        const orc_qm *w = &m->mats[l * 4];
+        float **v = &m->vecs[l * N_VECS];
+        if (tid == 0) orc_layernorm(m->xn, m->x, v[LN1_W], v[LN1_B], 1, C);
+        team_wait(&c->bar);
+        team_linear(c, tid, m->qkv, m->xn, &w[0], v[QKV_B], C, 3 * C, EPI_BIAS);
+        if (tid == 0) orc_kv_store(&m->kv, l, c->pos, m->qkv + C, m->qkv + 2 * C);
+        team_wait(&c->bar);
+        for (int h = tid; h < G_NH; h += nt) {
+            if (c->vnni && m->kv.head_dim == 64)
+                attend_one_vnni(&m->kv, m->att, m->qkv, l, h, c->pos);
+            else
+                orc_kv_attend_one(&m->kv, m->att, m->qkv, l, 0, h, c->pos);
+        }
+        team_wait(&c->bar);
+        team_linear(c, tid, m->x, m->att, &w[1], v[PROJ_B], C, C, EPI_BIAS | EPI_RESID);
+        if (tid == 0) orc_layernorm(m->xn, m->x, v[LN2_W], v[LN2_B], 1, C);
+        team_wait(&c->bar);
+        team_linear(c, tid, m->fc, m->xn, &w[2], v[FC_B], C, 4 * C, EPI_BIAS | EPI_GELU);
+        team_linear(c, tid, m->x, m->fc, &w[3], v[FCPROJ_B], 4 * C, C, EPI_BIAS | EPI_RESID);
+    }
+    if (tid == 0) orc_layernorm(m->xn, m->x, m->lnf_w, m->lnf_b, 1, C);
+    team_wait(&c->bar);
+    team_linear(c, tid, m->logits, m->xn, &m->wte, NULL, C, G_V, 0); /* head_team, kernels.mojo:869-910 */
+}
+
+/* The team's work for one start: a decode step, or the head alone. */
+static void team_job(orc_team *c, int tid) {
+    if (c->job == 0)
+        team_decode(c, tid);
+    else
+        team_linear(c, tid, c->m->logits, c->m->xn, &c->m->wte, NULL, G_C, G_V, 0);
+}
+
+typedef struct {
+    orc_team *c;
+    int tid;
+} orc_team_arg;
+
+typedef struct {
+    orc_team *c;
+    pthread_t th[256];
+    orc_team_arg args[256];
+} orc_team_threads;
+
+static void *team_worker(void *p) {
+    orc_team_arg *a = (orc_team_arg *)p;
+    for (;;) {
+        team_wait(&a->c->bar); /* a job starts (or the team stops) */
+        if (__atomic_load_n(&a->c->stop, __ATOMIC_ACQUIRE)) return NULL;
+        team_job(a->c, a->tid);
+    }
+}
+
+/* Starts nt - 1 workers (the caller is thread 0); NULL if that fails. */
+static orc_team_threads *team_start(orc_gpt2 *m, int nt) {
+    if (nt < 1 || nt > 256) return NULL;
+    orc_team_threads *T = (orc_team_threads *)calloc(1, sizeof(orc_team_threads));
+    orc_team *c = (orc_team *)aligned_alloc(64, (sizeof(orc_team) + 63) / 64 * 64);
+    if (!T || !c) {
+        free(T);
+        free(c);
+        return NULL;
+    }
+    memset(c, 0, sizeof(*c));
+    c->m = m;
+    c->bar.nt = nt;
+    c->vnni = orc_cpu_vnni();
+    T->c = c;
+    int started = 0;
+    for (int t = 1; t < nt; t++) {
+        T->args[t].c = c;
+        T->args[t].tid = t;
+        if (pthread_create(&T->th[t], NULL, team_worker, &T->args[t]) != 0) break;
+        started++;
+    }
+    if (started != nt - 1) { /* release the ones made */
+        c->bar.nt = started + 1;
+        __atomic_store_n(&c->stop, 1, __ATOMIC_RELEASE);
+        team_wait(&c->bar);
+        for (int t = 1; t <= started; t++) pthread_join(T->th[t], NULL);
+        free(c);
+        free(T);
+        return NULL;
+    }
+    return T;
+}
+
+static void team_stop(orc_team_threads *T) {
+    __atomic_store_n(&T->c->stop, 1, __ATOMIC_RELEASE);
+    team_wait(&T->c->bar);
+    for (int t = 1; t < T->c->bar.nt; t++) pthread_join(T->th[t], NULL);
+    free(T->c);
+    free(T);
+}
+
+/* Runs one job on the whole team (the caller as thread 0). */
+static void team_run(orc_team *c, int job) {
+    c->job = job;
+    team_wait(&c->bar);
+    team_job(c, 0);
+}
+
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+/* generate's greedy loop (gpt2t.mojo:949-981): the prompt through
+ * Model.forward (the oracle's, on g_threads OpenMP threads), then each
+ * further token through the team decode on nt threads (nt - 1 workers plus
+ * the caller, started before the timed loop).  secs[0] = the prompt's wall
+ * time, secs[1] = the decode loop's (the forwards plus the argmax picks, as
+ * gpt2t.mojo:968-1005 times it).  Returns the count generated, or -1. */
+int orc_cpu_generate(orc_gpt2 *m, const int64_t *prompt, int n_prompt, int steps, int nt, int64_t *out_tokens,
+                     double *secs) {
+    if (nt < 1 || nt > 256 || n_prompt < 1 || steps < 1 || n_prompt + steps > G_MAXT) return -1;
+    const double t0 = now_s();
+    const float *logits = orc_gpt2_forward(m, prompt, n_prompt, 0);
+    const double t1 = now_s();
+    orc_team_threads *T = team_start(m, nt);
+    if (!T) return -1;
+    const double t2 = now_s();
+    int pos = n_prompt, generated = 0;
+    for (int i = 0; i < steps; i++) {
+        int64_t next = orc_argmax(logits, G_V);
+        if (next == 50256) break;
+        out_tokens[generated++] = next;
+        if (generated == steps) break;
+        T->c->token = next;
+        T->c->pos = pos++;
+        team_run(T->c, 0);
+        logits = m->logits;
+    }
+    const double t3 = now_s();
+    team_stop(T);
+    if (secs) {
+        secs[0] = t1 - t0;
+        secs[1] = t3 - t2;
+    }
+    return generated;
+}
+
+/* One token through the team decode at position pos (the cache holds
+ * positions < pos); returns the logits (the model's buffer), NULL on a bad
+ * argument. */
+const float *orc_cpu_decode(orc_gpt2 *m, int64_t token, int pos, int nt) {
+    if (pos < 0 || pos >= G_MAXT || token < 0 || token >= G_V) return NULL;
+    orc_team_threads *T = team_start(m, nt);
+    if (!T) return NULL;
+    T->c->token = token;
+    T->c->pos = pos;
+    team_run(T->c, 0);
+    team_stop(T);
+    return m->logits;
+}
+
+/* The int8 per-channel head alone on a team of nt, one token: the median
+ * seconds of `reps` calls (the reference's per-kernel anchor,
+ * research/test_head.mojo:45-51).  Overwrites the model's xn and logits. */
+double orc_cpu_head_seconds(orc_gpt2 *m, int nt, int reps) {
+    if (reps < 1 || reps > 10000) return -1.0;
+    orc_team_threads *T = team_start(m, nt);
+    if (!T) return -1.0;
+    for (int i = 0; i < G_C; i++) m->xn[i] = (float)((i * 37) % 101 - 50) / 50.0f;
+    double *t = (double *)malloc(sizeof(double) * (size_t)reps);
+    for (int r = 0; r < reps; r++) {
+        const double a = now_s();
+        team_run(T->c, 1);
+        t[r] = now_s() - a;
+    }
+    team_stop(T);
+    for (int i = 1; i < reps; i++)
+        for (int j = i; j > 0 && t[j] < t[j - 1]; j--) {
+            const double x = t[j];
+            t[j] = t[j - 1];
+            t[j - 1] = x;
+        }
+    const double med = t[reps / 2];
+    free(t);
+    return med;
+}

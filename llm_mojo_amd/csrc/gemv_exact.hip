@@ -462,12 +462,16 @@ struct Ch8Args {
     ArgmaxPart *amax;
     int16_t *xq_out;
     float *sx_out;
+    int iters;  // tile groups a workgroup takes
 };
 
-// Workgroup: NW waves over TPW row tiles (NW / TPW waves share a tile's
-// steps, contiguously).  Step s of a tile is chunks 4s .. 4s + 3 of its 16
-// rows; lane (r, j) = (lane & 15, lane >> 4) reads chunk 4s + j.  REC: the
-// int16 codes and lane sums come from the prepared record.
+// Workgroup: NW waves over TPW row tiles at a time (NW / TPW waves share a
+// tile's steps, contiguously), for a.iters such groups of tiles, group
+// blockIdx.x + i * gridDim.x, the next group's codes requested while the
+// current one computes: the activation prologue runs once per workgroup.
+// Step s of a tile is chunks 4s .. 4s + 3 of its 16 rows; lane (r, j) =
+// (lane & 15, lane >> 4) reads chunk 4s + j.  REC: the int16 codes and lane
+// sums come from the prepared record.
 template <int NW, int TPW, bool LN, int UPT, int SPW, bool REC, int NV>
 __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
     constexpr int NT = NW * 64, WPT = NW / TPW;  // waves per tile
@@ -482,14 +486,13 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, j = lane >> 4;
-    const int tl = wid / WPT, wt = wid % WPT;  // tile of the workgroup, wave within the tile
-    const int tile = blockIdx.x * TPW + tl;
-    const bool live = tile < a.ntiles;
+    const int tl = wid / WPT, wt = wid % WPT;  // tile of the group, wave within the tile
     const int S = a.CK >> 2;  // steps per tile (CK a multiple of 4)
     const int s0 = (wt * S) / WPT, ns = ((wt + 1) * S) / WPT - s0;
     const int nunits = a.K >> 2;
     const ActLayout AL = llmq_act_layout(a.K);
     const auto rr_ = llmq_rsrc(a.rec, REC ? (uint32_t)AL.bytes : 0u);
+    auto tile_of = [&](int it) { return (int)((blockIdx.x + (uint32_t)it * gridDim.x) * TPW) + tl; };
 
     float4 xv[UPT], lw[UPT], lb[UPT];
     float lnv[NV > 0 ? NV : 1];
@@ -502,22 +505,33 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
         }
     }
     const auto rc = llmq_rsrc(a.codes, a.codes_bytes);
-    uint4 wc[SPW], wx[REC ? SPW : 1][2];
-    __builtin_amdgcn_sched_barrier(0);
+    const auto rs = llmq_rsrc(a.scales, (uint32_t)a.ntiles * 32u);
+    const auto rz = llmq_rsrc(a.zps, (uint32_t)a.ntiles * 16u);
+    uint4 wc[SPW], wn[SPW], wx[REC ? SPW : 1][2];
+    uint32_t sc_c, zp_c, sc_n = 0, zp_n = 0;  // this lane's row scale bits and zero point
+    // one tile's codes (the steps of this wave) and its row's scale / zero point
+    auto load_tile = [&](int tile, uint4 *w, uint32_t &scb, uint32_t &zpb) {
+        const bool ok_t = tile < a.ntiles;
 #pragma unroll
-    for (int u = 0; u < SPW; u++) {
-        const uint32_t c = (uint32_t)(4 * (s0 + u) + j);
-        const bool ok = live && u < ns;
-        wc[u] = bload16_stream(rc, ok ? (((uint32_t)tile * (uint32_t)a.CK + c) * 16u + (uint32_t)r) * 16u : kLlmqOOB);
-        if constexpr (REC) {  // the chunk's 16 int16 codes
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t c = (uint32_t)(4 * (s0 + u) + j);
+            const bool ok = ok_t && u < ns;
+            w[u] = bload16_stream(rc, ok ? (((uint32_t)tile * (uint32_t)a.CK + c) * 16u + (uint32_t)r) * 16u : kLlmqOOB);
+        }
+        scb = llmq_bload2(rs, ok_t ? ((uint32_t)tile * 16u + (uint32_t)r) * 2u : kLlmqOOB);
+        zpb = llmq_bload1(rz, ok_t ? (uint32_t)tile * 16u + (uint32_t)r : kLlmqOOB);
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile(tile_of(0), wc, sc_c, zp_c);
+    if constexpr (REC) {  // the chunks' int16 codes: the same for every tile
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const uint32_t c = (uint32_t)(4 * (s0 + u) + j);
+            const bool ok = u < ns;
             wx[u][0] = llmq_bload16(rr_, ok ? (uint32_t)AL.xq + c * 32u : kLlmqOOB);
             wx[u][1] = llmq_bload16(rr_, ok ? (uint32_t)AL.xq + c * 32u + 16u : kLlmqOOB);
         }
     }
-    const int o = tile * 16 + r;
-    const bool row_ok = live && o < a.n;
-    const float scale = row_ok ? __half2float(__ushort_as_half(a.scales[tile * 16 + r])) : 0.0f;
-    const int zp = row_ok ? (int)a.zps[tile * 16 + r] : 0;
     float sx;
     if constexpr (REC) {
         sx = __uint_as_float(llmq_bload4(rr_, (uint32_t)AL.sx));
@@ -541,71 +555,93 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
     }
     llmq_lds_barrier();
 
-    // 8 int32 lanes of sum x u: lane (r, j) holds reference lanes
-    // 8 (j & 1) + i, i = 0..7 (chunk 4s + j has parity j & 1).
-    int acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    typedef short s2 __attribute__((ext_vector_type(2)));
-#pragma unroll
-    for (int u = 0; u < SPW; u++) {
-        if (u < ns) {  // wave-uniform
-        const int c = 4 * (s0 + u) + j;
-        const uint4 d = wc[u];
-        uint4 x0, x1;
-        if constexpr (REC) {
-            x0 = wx[u][0];
-            x1 = wx[u][1];
-        } else {
-            x0 = reinterpret_cast<const uint4 *>(xq)[2 * c];      // pairs 0..3 of the chunk
-            x1 = reinterpret_cast<const uint4 *>(xq)[2 * c + 1];  // pairs 4..7
-        }
-        const uint32_t xp[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t up = __builtin_amdgcn_perm(0u, dw[i >> 1], (i & 1) ? 0x0c030c02u : 0x0c010c00u);
-            acc[i] = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, xp[i]), __builtin_bit_cast(s2, up), acc[i], false);
-        }
-        }
-    }
-    // lanes j and j + 2 hold the same reference lanes
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] += llmq_from_lane_plus32(acc[i]);
-    // waves of the tile, through LDS (lanes j = 0, 1)
-    if (j < 2) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) part[(((tl * WPT + wt) * 2 + j) * 16 + r) * 8 + i] = acc[i];
-    }
-    llmq_lds_barrier();
     float best_v = -INFINITY;
     int best_i = 0x7fffffff;
-    if (wt == 0) {
-        // lane (r, j < 2): reference lanes 8 j + i of row r, as floats
-        float vl[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        if (j < 2) {
+    typedef short s2 __attribute__((ext_vector_type(2)));
+    for (int it = 0; it < a.iters; it++) {
+        const int tile = tile_of(it);
+        if (it + 1 < a.iters) load_tile(tile_of(it + 1), wn, sc_n, zp_n);
+        // 8 int32 lanes of sum x u: lane (r, j) holds reference lanes
+        // 8 (j & 1) + i, i = 0..7 (chunk 4s + j has parity j & 1).
+        int acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            if (u < ns) {  // wave-uniform
+            const int c = 4 * (s0 + u) + j;
+            const uint4 d = wc[u];
+            uint4 x0, x1;
+            if constexpr (REC) {
+                x0 = wx[u][0];
+                x1 = wx[u][1];
+            } else {
+                x0 = reinterpret_cast<const uint4 *>(xq)[2 * c];      // pairs 0..3 of the chunk
+                x1 = reinterpret_cast<const uint4 *>(xq)[2 * c + 1];  // pairs 4..7
+            }
+            const uint32_t xp[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                int t = 0;
-#pragma unroll
-                for (int w = 0; w < WPT; w++) t += part[(((tl * WPT + w) * 2 + j) * 16 + r) * 8 + i];
-                const int G = t - zp * xsl[8 * j + i];
-                vl[i] = fmaf((float)G, scale, 0.0f);
+                const uint32_t up = __builtin_amdgcn_perm(0u, dw[i >> 1], (i & 1) ? 0x0c030c02u : 0x0c010c00u);
+                acc[i] = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, xp[i]), __builtin_bit_cast(s2, up), acc[i], false);
+            }
             }
         }
-        // reduce_add: (L, L + 8) pairs lanes j = 0, 1 (16 apart), the rest in-lane
+        // lanes j and j + 2 hold the same reference lanes
 #pragma unroll
-        for (int i = 0; i < 8; i++) vl[i] = vl[i] + llmq_from_lane_plus16(vl[i]);
-        const float b0 = vl[0] + vl[4], b1 = vl[1] + vl[5], b2 = vl[2] + vl[6], b3 = vl[3] + vl[7];
-        const float c0 = b0 + b2, c1 = b1 + b3;
-        const float v = c0 + c1;
-        if (j == 0 && row_ok) {
-            float y = v * sx;
-            if (a.flags & LLMQ_BIAS) y += a.bias[o];
-            if (a.flags & LLMQ_GELU) y = gelu_ref(y);
-            if (a.flags & LLMQ_RESID) y += a.out[o];
-            a.out[o] = y;
-            best_v = y;
-            best_i = o;
+        for (int i = 0; i < 8; i++) acc[i] += llmq_from_lane_plus32(acc[i]);
+        if constexpr (WPT > 1) {  // waves of the tile, through LDS (lanes j = 0, 1)
+            if (j < 2) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) part[(((tl * WPT + wt) * 2 + j) * 16 + r) * 8 + i] = acc[i];
+            }
+            llmq_lds_barrier();
+            if (wt == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    int t = 0;
+#pragma unroll
+                    for (int w = 0; w < WPT; w++) t += part[(((tl * WPT + w) * 2 + j) * 16 + r) * 8 + i];
+                    acc[i] = t;
+                }
+            }
         }
+        if (wt == 0) {
+            const int o = tile * 16 + r;
+            const bool row_ok = tile < a.ntiles && o < a.n;
+            const float scale = row_ok ? __half2float(__ushort_as_half((unsigned short)sc_c)) : 0.0f;
+            const int zp = row_ok ? (int)zp_c : 0;
+            // lane (r, j < 2): reference lanes 8 j + i of row r, as floats
+            float vl[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            if (j < 2) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int G = acc[i] - zp * xsl[8 * j + i];
+                    vl[i] = fmaf((float)G, scale, 0.0f);
+                }
+            }
+            // reduce_add: (L, L + 8) pairs lanes j = 0, 1 (16 apart), the rest in-lane
+#pragma unroll
+            for (int i = 0; i < 8; i++) vl[i] = vl[i] + llmq_from_lane_plus16(vl[i]);
+            const float b0 = vl[0] + vl[4], b1 = vl[1] + vl[5], b2 = vl[2] + vl[6], b3 = vl[3] + vl[7];
+            const float c0 = b0 + b2, c1 = b1 + b3;
+            const float v = c0 + c1;
+            if (j == 0 && row_ok) {
+                float y = v * sx;
+                if (a.flags & LLMQ_BIAS) y += a.bias[o];
+                if (a.flags & LLMQ_GELU) y = gelu_ref(y);
+                if (a.flags & LLMQ_RESID) y += a.out[o];
+                a.out[o] = y;
+                if (y > best_v || (y == best_v && o < best_i)) {
+                    best_v = y;
+                    best_i = o;
+                }
+            }
+        }
+        if constexpr (WPT > 1) llmq_lds_barrier();  // part is rewritten by the next group
+#pragma unroll
+        for (int u = 0; u < SPW; u++) wc[u] = wn[u];
+        sc_c = sc_n;
+        zp_c = zp_n;
     }
     if (a.amax) {
         // largest output of the workgroup; equal values keep the smaller
@@ -696,12 +732,22 @@ bool exact_supports(const llmq_mat *w) {
     return false;
 }
 
-// Workgroups (= argmax partials) of the head kernel for w.
-void head8_shape(const llmq_mat *w, int *nw, int *tpw, int *grid) {
-    // one tile per 4-wave workgroup: 12 steps of a 768-input row make 3 a wave
+// Shape of the head kernel for w: nw waves, tpw tiles at a time, grid
+// workgroups (= argmax partials), iters tile groups each.  A wave per tile
+// and about two workgroups a CU (measured on the 50257 x 768 head: 13.3 us
+// with a workgroup per tile, 9.4 us so; LLMQ_HEAD_TPW / LLMQ_HEAD_GRID
+// override, for measurement).
+void head8_shape(const llmq_mat *w, int *nw, int *tpw, int *grid, int *iters) {
     *nw = 4;
-    *tpw = 1;
-    *grid = (int)w->ntiles;
+    int t = 4, g = 512;
+    if (const char *e = getenv("LLMQ_HEAD_TPW")) t = atoi(e);
+    if (t != 2 && t != 4) t = 1;
+    if (const char *e = getenv("LLMQ_HEAD_GRID")) g = atoi(e);  // 0: a workgroup per tile group
+    const int groups = (int)((w->ntiles + t - 1) / t);
+    if (g <= 0 || g > groups) g = groups;
+    *tpw = t;
+    *iters = (groups + g - 1) / g;
+    *grid = (groups + *iters - 1) / *iters;
 }
 
 // Shared by both activation forms: rq.x (floats) or rec (a prepared record).
@@ -764,8 +810,8 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     }
     // int8 per channel
     LLMQ_REQUIRE(!rq.dbg, "linear: chunk sums are not kept by the int8 head kernel");
-    int nw, tpw, grid;
-    head8_shape(w, &nw, &tpw, &grid);
+    int nw, tpw, grid, iters;
+    head8_shape(w, &nw, &tpw, &grid, &iters);
     LLMQ_REQUIRE(!rq.amax || grid <= rq.amax_cap, "linear: %d argmax partials exceed capacity %d", grid, rq.amax_cap);
     Ch8Args a;
     a.codes = reinterpret_cast<const uint4 *>(w->codes);
@@ -786,21 +832,38 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     a.amax = rq.amax;
     a.xq_out = rq.xq_out;
     a.sx_out = rq.sx_out;
+    a.iters = iters;
     const int S = (int)(w->CK / 4), spw = (S + (nw / tpw) - 1) / (nw / tpw);
     const size_t lds = (rec ? 0 : (size_t)K * 2) + (size_t)tpw * (nw / tpw) * 2 * 16 * 8 * 4 + (ln ? (size_t)K * 4 : 0);
     LLMQ_REQUIRE(lds <= 64 * 1024, "head: %zu bytes of LDS", lds);
     const int upt = upt_for(K, nw * 64);
-#define H8(LNV, U, SP, R, NV) \
-    hipLaunchKernelGGL((head8_kernel<4, 1, LNV, U, SP, R, NV>), dim3((unsigned)grid), dim3(256), lds, ctx->stream, a)
+#define H8T(T, LNV, U, SP, R, NV) \
+    hipLaunchKernelGGL((head8_kernel<4, T, LNV, U, SP, R, NV>), dim3((unsigned)grid), dim3(256), lds, ctx->stream, a)
+#define H8(LNV, U, SP, R, NV)                      \
+    do {                                           \
+        if (tpw == 4) H8T(4, LNV, U, SP, R, NV);   \
+        else if (tpw == 2) H8T(2, LNV, U, SP, R, NV); \
+        else H8T(1, LNV, U, SP, R, NV);            \
+    } while (0)
     if (rec) {
         if (spw <= 4) H8(false, 1, 4, true, 0);
+        else if (spw <= 8) H8(false, 1, 8, true, 0);
+        else if (spw <= 12) H8(false, 1, 12, true, 0);
         else if (spw <= 16) H8(false, 1, 16, true, 0);
         else return llmq_set_error(LLMQ_EUNSUPPORTED, "head: reduction axis %d too long", K);
-    } else if (upt == 1 && spw <= 4) {
-        if (ln && ln_nv(K) == 48) H8(true, 1, 4, false, 48);
-        else if (ln && ln_nv(K) == 64) H8(true, 1, 4, false, 64);
-        else if (ln) H8(true, 1, 4, false, 0);
-        else H8(false, 1, 4, false, 0);
+    } else if (upt == 1 && spw <= 12) {
+        const int sp = spw <= 4 ? 4 : spw <= 8 ? 8 : 12;
+#define H8S(LNV, NV)                                  \
+    do {                                              \
+        if (sp == 4) H8(LNV, 1, 4, false, NV);        \
+        else if (sp == 8) H8(LNV, 1, 8, false, NV);   \
+        else H8(LNV, 1, 12, false, NV);               \
+    } while (0)
+        if (ln && ln_nv(K) == 48) H8S(true, 48);
+        else if (ln && ln_nv(K) == 64) H8S(true, 64);
+        else if (ln) H8S(true, 0);
+        else H8S(false, 0);
+#undef H8S
     } else if (upt <= 4 && spw <= 4) {
         if (ln) H8(true, 4, 4, false, 0); else H8(false, 4, 4, false, 0);
     } else if (upt <= 4 && spw <= 16) {
@@ -808,6 +871,7 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     } else {
         return llmq_set_error(LLMQ_EUNSUPPORTED, "head: reduction axis %d too long", K);
     }
+#undef H8T
 #undef H8
     LLMQ_HIP(hipGetLastError());
     if (rq.amax_count) *rq.amax_count = grid;
@@ -819,8 +883,8 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
 bool gemv_exact_supports(const llmq_mat *w) { return exact_supports(w); }
 
 int gemv_exact_num_parts(const llmq_mat *w) {
-    int nw, tpw, grid;
-    head8_shape(w, &nw, &tpw, &grid);
+    int nw, tpw, grid, iters;
+    head8_shape(w, &nw, &tpw, &grid, &iters);
     return w->bits == 8 ? grid : 0;
 }
 

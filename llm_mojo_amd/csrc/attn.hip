@@ -260,6 +260,214 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
     }
 }
 
+// Prompt attention in the reference's order (KVCache.attend calls
+// attend_float_one for every token and head, kvcache.mojo:62-79, 113-150),
+// the arithmetic of kv_attend_kernel operation by operation, for TQ tokens
+// of one head per workgroup of NTH threads, which share the staged key and
+// value rows (head_dim 64; the cache already holds every token of the
+// prompt).  Workgroup y takes block nblk - 1 - y, then block y, so every
+// workgroup has about the same causal work.  Per block:
+//  1. keys staged NTH / 4 positions at a time as floats; lane (i = lane % TQ,
+//     p = lane / TQ) of wave w scores token i, its query in registers,
+//     against position (st NW + w) PW + p of the chunk (16 lane partials,
+//     halving tree, times the key's scale, times 1/sqrt(64));
+//  2. per token (NTH / TQ threads): maximum, exponentials, the total added
+//     in position order by one lane, the weights (e / total) * vs;
+//  3. per token and dimension the fma chain over positions in order, values
+//     staged as floats, 64 TQ / NTH dimensions of one token a thread.
+// One wave issues a VALU instruction every ~6 cycles, so the larger
+// workgroup (two waves a SIMD) is the faster one.
+constexpr int kKStr = 68;  // floats per staged key row (bank spread)
+
+template <int NTH, int TQ>
+__global__ __launch_bounds__(NTH) void attend_prompt_exact_kernel(const float *__restrict__ qkv, int64_t ld, int pos0,
+                                                                  int T, int layer, int max_t, int n_head,
+                                                                  const int8_t *__restrict__ K8,
+                                                                  const int8_t *__restrict__ V8,
+                                                                  const float *__restrict__ KS,
+                                                                  const float *__restrict__ VS, float *__restrict__ out,
+                                                                  int64_t ldo, int NP) {
+    constexpr int HD = 64, NW = NTH / 64, PW = 64 / TQ, TPT = NTH / TQ, DPT = HD / TPT, PC = NTH / 4;
+    static_assert(DPT >= 1 && DPT <= 4 && TPT <= 64, "shape");
+    extern __shared__ __align__(16) float sm[];
+    float *kf = sm;              // [PC][kKStr] keys; phase 3: [PC][HD] values
+    float *ksc = kf + PC * kKStr; // [PC]
+    float *vsc = ksc + PC;        // [NP]
+    float *sc = vsc + NP;         // [TQ][NP + 1] scores, then exponentials, then weights
+    const int NPS = NP + 1;       // rows of different tokens on different banks
+    const int h = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t base = (int64_t)layer * max_t * n_head + h;  // slot of position 0
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int nblk = (T + TQ - 1) / TQ;
+    for (int pass = 0; pass < 2; pass++) {
+        const int blk = pass == 0 ? nblk - 1 - (int)blockIdx.y : (int)blockIdx.y;
+        if (pass == 1 && blk >= nblk - 1 - (int)blockIdx.y) break;  // the middle block, done once
+        if (pass == 1) lds_barrier();  // the first block's reads of LDS are done
+        const int t0 = blk * TQ;
+        const int npb = pos0 + (t0 + TQ < T ? t0 + TQ : T);  // positions the block reads
+
+        // 16 codes of position c0 + (tid >> 2) (keys: with the key and value
+        // scales): fetched into registers one chunk ahead, then committed to
+        // LDS as floats
+        int4 raw = make_int4(0, 0, 0, 0);
+        float rks = 0.0f, rvs = 0.0f;
+        auto fetch = [&](const int8_t *src, int c0, bool keys) {
+            const int sl = tid >> 2, pc = tid & 3, s = c0 + sl;
+            if (s < npb) {
+                const int64_t slot = base + (int64_t)s * n_head;
+                raw = *reinterpret_cast<const int4 *>(src + slot * HD + pc * 16);
+                if (keys && pc == 0) {
+                    rks = KS[slot];
+                    rvs = VS[slot];
+                }
+            }
+        };
+        auto commit = [&](int c0, int stride, bool keys) {
+            const int sl = tid >> 2, pc = tid & 3, s = c0 + sl;
+            if (s < npb) {
+                const int8_t *bb = reinterpret_cast<const int8_t *>(&raw);
+                float4 *dst = reinterpret_cast<float4 *>(kf + sl * stride + pc * 16);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    dst[k] = make_float4((float)bb[4 * k], (float)bb[4 * k + 1], (float)bb[4 * k + 2],
+                                         (float)bb[4 * k + 3]);
+                if (keys && pc == 0) {
+                    ksc[sl] = rks;
+                    vsc[s] = rvs;
+                }
+            }
+        };
+        fetch(K8, 0, true);
+
+        // 1. scores
+        const int qi = lane % TQ, qp = lane / TQ;
+        const bool qok = t0 + qi < T;
+        const int qpos = pos0 + t0 + qi;
+        float q[HD];
+        {
+            const float4 *src =
+                reinterpret_cast<const float4 *>(qkv + (int64_t)(qok ? t0 + qi : t0) * ld + (int64_t)h * HD);
+#pragma unroll
+            for (int k = 0; k < HD / 4; k++) {
+                const float4 v = src[k];
+                q[4 * k] = v.x;
+                q[4 * k + 1] = v.y;
+                q[4 * k + 2] = v.z;
+                q[4 * k + 3] = v.w;
+            }
+        }
+        for (int c0 = 0; c0 < npb; c0 += PC) {
+            commit(c0, kKStr, true);
+            lds_barrier();
+            if (c0 + PC < npb) fetch(K8, c0 + PC, true);  // in flight while this chunk is scored
+#pragma unroll 1
+            for (int st = 0; st < PC / (NW * PW); st++) {
+                const int sl = (st * NW + w) * PW + qp, s = c0 + sl;
+                if (s < npb) {
+                    const float4 *kr = reinterpret_cast<const float4 *>(kf + sl * kKStr);
+                    float dl[16];
+#pragma unroll
+                    for (int e = 0; e < 16; e++) dl[e] = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < HD / 16; i++) {
+                        const float4 k0 = kr[4 * i], k1 = kr[4 * i + 1], k2 = kr[4 * i + 2], k3 = kr[4 * i + 3];
+                        const float kk[16] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w,
+                                              k2.x, k2.y, k2.z, k2.w, k3.x, k3.y, k3.z, k3.w};
+#pragma unroll
+                        for (int e = 0; e < 16; e++) dl[e] = dl[e] + q[16 * i + e] * kk[e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; e++) dl[e] = dl[e] + dl[e + 8];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) dl[e] = dl[e] + dl[e + 4];
+                    dl[0] = dl[0] + dl[2];
+                    dl[1] = dl[1] + dl[3];
+                    const float d = dl[0] + dl[1];
+                    if (qok && s <= qpos) sc[qi * NPS + s] = (d * ksc[sl]) * scale;
+                }
+            }
+            lds_barrier();
+        }
+
+        fetch(V8, 0, false);  // the first value chunk, in flight during step 2
+
+        // 2. per token: maximum, exponentials, total in order, weights
+        {
+            const int ti = tid / TPT, tl = tid % TPT;
+            const bool tok = t0 + ti < T;
+            const int tpos = tok ? pos0 + t0 + ti : -1;
+            float *row = sc + ti * NPS;
+            float mx = -INFINITY;
+            for (int s = tl; s <= tpos; s += TPT) mx = fmaxf(mx, row[s]);
+#pragma unroll
+            for (int off = TPT / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+#pragma unroll 4
+            for (int s = tl; s <= tpos; s += TPT) row[s] = ref_expf(row[s] - mx);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+            float total = 0.0f;
+            if (tl == 0 && tok) {
+                int s = 0;
+                for (; s + 16 <= tpos + 1; s += 16) {
+                    float e[16];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) e[k] = row[s + k];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) total += e[k];
+                }
+                for (; s <= tpos; s++) total += row[s];
+            }
+            total = __shfl(total, (lane / TPT) * TPT);
+#pragma unroll 4
+            for (int s = tl; s <= tpos; s += TPT) row[s] = (row[s] / total) * vsc[s];
+        }
+        lds_barrier();
+
+        // 3. the value chains: thread (token ti, dimensions DPT dg ..)
+        {
+            const int ti = tid / TPT, dg = tid % TPT;
+            const int ipos = t0 + ti < T ? pos0 + t0 + ti : -1;
+            const float *wr = sc + ti * NPS;
+            float acc[DPT];
+#pragma unroll
+            for (int k = 0; k < DPT; k++) acc[k] = 0.0f;
+            auto step = [&](float wv, const float *vp) {
+#pragma unroll
+                for (int k = 0; k < DPT; k++) acc[k] = fmaf(wv, vp[k], acc[k]);
+            };
+            for (int c0 = 0; c0 < npb; c0 += PC) {
+                commit(c0, HD, false);
+                lds_barrier();
+                if (c0 + PC < npb) fetch(V8, c0 + PC, false);
+                const int cn = ipos + 1 - c0 < PC ? ipos + 1 - c0 : PC;  // this token's positions here
+                int sl = 0;
+                for (; sl + 8 <= cn; sl += 8) {  // a batch's reads, then its fmas in order
+                    float wv[8], v[8][DPT];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        wv[k] = wr[c0 + sl + k];
+#pragma unroll
+                        for (int m = 0; m < DPT; m++) v[k][m] = kf[(sl + k) * HD + dg * DPT + m];
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; k++)
+#pragma unroll
+                        for (int m = 0; m < DPT; m++) acc[m] = fmaf(wv[k], v[k][m], acc[m]);
+                }
+                for (; sl < cn; sl++) step(wr[c0 + sl], kf + sl * HD + dg * DPT);
+                lds_barrier();
+            }
+            if (ipos >= 0) {
+                float *o = out + (int64_t)(t0 + ti) * ldo + (int64_t)h * HD + dg * DPT;
+#pragma unroll
+                for (int k = 0; k < DPT; k++) o[k] = acc[k];
+            }
+        }
+    }
+}
+
 // LayerNorm over rows of C (kernels.mojo:179-197), one workgroup per row,
 // with the statistics in the reference's order (16 lane partials, halving
 // tree) and the output as (x - mean) * rstd * w + b, each operation rounded.
@@ -619,6 +827,29 @@ static int attend_hd(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
                  : attend_launch<HD, false, false>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, base);
 }
 
+// The exact-order prompt attention (head_dim 64); LLMQ_PROMPT_NTH /
+// LLMQ_PROMPT_TQ choose other workgroup shapes, for measurement.
+template <int NTH, int TQ>
+static int prompt_exact_launch(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T,
+                               int pos0, int64_t ld) {
+    const int C = kv->n_head * 64;
+    const int PC = NTH / 4;
+    const int NP = (pos0 + T + PC - 1) / PC * PC;
+    const size_t lds = sizeof(float) * ((size_t)PC * kKStr + PC + NP + (size_t)TQ * (NP + 1));
+    static size_t granted = 64 * 1024;
+    if (lds > granted) {
+        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_prompt_exact_kernel<NTH, TQ>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        granted = lds;
+    }
+    const int nblk = (T + TQ - 1) / TQ;
+    hipLaunchKernelGGL((attend_prompt_exact_kernel<NTH, TQ>), dim3(kv->n_head, (nblk + 1) / 2), dim3(NTH), lds,
+                       ctx->stream, qkv, ld ? ld : 3 * C, pos0, T, layer, kv->max_t, kv->n_head, kv->k, kv->v, kv->ks,
+                       kv->vs, out, (int64_t)C, NP);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
 int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T, int pos0,
                      const int *pos_dev, int64_t ld, bool store) {
     LLMQ_REQUIRE(kv && qkv && out && T >= 1, "kv_attend: bad arguments");
@@ -631,6 +862,16 @@ int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
         const int C = kv->n_head * kv->head_dim;
         return launch_attend_prompt(ctx, kv->k, kv->v, kv->ks, kv->vs, layer, kv->max_t, kv->n_head, kv->n_head, qkv,
                                     ld ? ld : 3 * C, pos0, T, out, (int64_t)C);
+    }
+    if (!store && !pos_dev && T > 1 && kv->head_dim == 64 && (ld ? ld : 3 * kv->n_head * 64) % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(qkv) & 15) == 0) {
+        const char *e = getenv("LLMQ_PROMPT_TQ"), *n = getenv("LLMQ_PROMPT_NTH");
+        // 512 threads, 16 tokens: 44 us a layer at 476 tokens (256 / 8, 256 / 16: 48-51 us)
+        const int tq = e ? atoi(e) : 16, nth = n ? atoi(n) : 512;
+        if (nth == 256) return tq == 8 ? prompt_exact_launch<256, 8>(ctx, kv, out, qkv, layer, T, pos0, ld)
+                                       : prompt_exact_launch<256, 16>(ctx, kv, out, qkv, layer, T, pos0, ld);
+        return tq == 8 ? prompt_exact_launch<512, 8>(ctx, kv, out, qkv, layer, T, pos0, ld)
+                       : prompt_exact_launch<512, 16>(ctx, kv, out, qkv, layer, T, pos0, ld);
     }
     if (kv->head_dim == 64) return attend_hd<64>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
     if (kv->head_dim == 128) return attend_hd<128>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);

@@ -739,9 +739,12 @@ bool exact_supports(const llmq_mat *w) {
 // override, for measurement).
 void head8_shape(const llmq_mat *w, int *nw, int *tpw, int *grid, int *iters) {
     *nw = 4;
-    int t = 4, g = 512;
+    // a tile's steps in at most 12 registers a wave (S = CK / 4 steps a tile)
+    const int64_t S = w->CK / 4;
+    int t = S <= 12 ? 4 : S <= 24 ? 2 : 1, g = 512;
     if (const char *e = getenv("LLMQ_HEAD_TPW")) t = atoi(e);
     if (t != 2 && t != 4) t = 1;
+    while (t > 1 && (S + 4 / t - 1) / (4 / t) > 16) t /= 2;
     if (const char *e = getenv("LLMQ_HEAD_GRID")) g = atoi(e);  // 0: a workgroup per tile group
     const int groups = (int)((w->ntiles + t - 1) / t);
     if (g <= 0 || g > groups) g = groups;

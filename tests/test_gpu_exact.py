@@ -150,7 +150,8 @@ def test_prompt_gemm_bit_exact(gpu, orc, fmt, T):
         g.free()
 
 
-@pytest.mark.parametrize("T,pos0", [(1, 0), (1, 11), (1, 111), (1, 300), (12, 0), (5, 40), (64, 100)])
+@pytest.mark.parametrize("T,pos0", [(1, 0), (1, 11), (1, 111), (1, 300), (12, 0), (5, 40), (64, 100), (17, 0),
+                                   (476, 0), (300, 700)])
 def test_attention_bit_exact(gpu, orc, T, pos0):
     """attend_float_one over the int8 cache: one token (decode) and prompts."""
     torch, lm, ctx = gpu

@@ -19,17 +19,24 @@
 // stays within 256 * 32767 * 255 < 2^31, the reference's own flush bound;
 // intermediate wraparound cancels).
 //
-// Mapping: a workgroup of 4 waves owns 64 tokens x 64 output rows (4 row
-// tiles); wave (wm, wn) computes the 32 x 32 block (tokens 32 wm.., rows
-// 32 wn..) with v_mfma_i32_32x32x32_i8, one call per 32 inputs and plane.
-// The reduction axis is walked in staged blocks of 256 inputs (128 or 64
-// when those do not divide it), each loaded as 64-input sub-blocks: the next
-// block's activations, codes, zero points and scales are loaded into
-// registers while the current block, staged in LDS (activation planes,
-// weights as int8 rows, per-row weight sums, scales), feeds the matrix cores;
-// two LDS buffers alternate, one barrier per block.  Large blocks matter:
-// a block costs one memory round trip, and the few workgroups of a prompt
-// GEMM cannot hide it behind each other.
+// Mapping: a workgroup of 4 waves owns 16 MT tokens x 64 output rows (4 row
+// tiles); wave w computes rows 16 w .. 16 w + 15 for all 16 MT tokens with
+// v_mfma_i32_16x16x32_i8 (A: 16 tokens x 32 inputs of one plane, B: 32
+// inputs x 16 rows), the wave's weight fragment serving its MT token
+// groups.  One call covers exactly one 32-input group, so the group sums
+// tile_i16 scales (int4-g32: every call) come straight out of the
+// accumulators; the 16x16x64 form would add two groups' products together
+// before they can be scaled.  The reduction axis is walked in staged blocks
+// of 128 inputs: activations, codes, zero points and scales of block kb + 2
+// are loaded into registers while block kb, staged in LDS (activation
+// planes, weights as int8 rows, per-row weight sums, scales), feeds the
+// matrix cores; two LDS buffers alternate, one barrier per block.
+//
+// What bounds it: tile_i16's per-group float chain, per output and group
+// of 32 inputs a shift-add, an add, a convert and an fma (4 VALU against
+// 2 MFMA of 8192 products per 16 x 16 outputs), and the round trip of each
+// staged block (~1 us per block per workgroup at 476 tokens, measured with
+// per-workgroup timestamps).
 //
 // Activations come from act_q16_kernel: LayerNorm (kernels.mojo:179-197) when
 // asked, then quantize_rows (kernels.mojo:400-416), one workgroup per token.
@@ -40,7 +47,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef short v2s __attribute__((ext_vector_type(2)));
 
-constexpr int TM = 16;           // tokens per workgroup
 constexpr int TN = 64;           // output rows per workgroup (a 16 x 16 block per wave)
 constexpr int KB = 128;          // inputs per staged block
 constexpr uint32_t kOOB = 0x80000000u;
@@ -159,35 +165,37 @@ struct MfArgs {
 // scale of (sub-step t / 64, row t % 64).  Zero point and scale come as
 // the aligned dwords holding them plus bit offsets, extracted where they are
 // used, so no wait follows the loads.
+template <int MT>
 struct Pref {
-    uint4 a;        // 8 int16 activations
+    uint4 a[MT];    // 8 int16 activations of tokens t / 16 + 16 j
     uint4 c0, c1;   // int4: one chunk (c0); int8: two chunks
     uint32_t zpw, zsh, scw, ssh;
 };
 
-template <int BITS>
+template <int BITS, int MT>
 struct Lds {
     static constexpr int RS = KB + 16;   // row stride in bytes
-    uint8_t a_hi[2][TM * RS];
-    uint8_t a_lo[2][TM * RS];
+    uint8_t a_hi[2][16 * MT * RS];
+    uint8_t a_lo[2][16 * MT * RS];
     uint8_t w0[2][TN * RS];              // int4: u - zp; int8: wl = w & 15
     uint8_t w1[2][BITS == 8 ? TN * RS : 16];  // int8: wh = w >> 4
     int wsum[2][KB / 32][TN];            // sum of w per (32-input sub-step, row)
     float scale[2][KB / 32][TN];         // scale of the group of each (sub-step, row)
-    float sx[TM];
+    float sx[16 * MT];
 };
 
 // Loads of block kb (inputs 128 kb ..); everything at or past K reads zeros.
-template <int BITS>
-__device__ __forceinline__ void prefetch(const MfArgs &a, int kb, int tok0, int tile0, Pref &p,
+template <int BITS, int MT>
+__device__ __forceinline__ void prefetch(const MfArgs &a, int kb, int tok0, int tile0, Pref<MT> &p,
                                          __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rc,
                                          __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rz) {
     const int t = threadIdx.x, k0 = kb * KB;
-    {
-        const int m = t >> 4, k = k0 + 8 * (t & 15);
+#pragma unroll
+    for (int j = 0; j < MT; j++) {
+        const int m = (t >> 4) + 16 * j, k = k0 + 8 * (t & 15);
         const int tok = tok0 + m;
         const uint32_t off = tok < a.T && k < a.K ? (uint32_t)(((int64_t)tok * a.K + k) * 2) : kOOB;
-        p.a = bload16(rx, off);
+        p.a[j] = bload16(rx, off);
     }
     const int tt = t >> 6, sub = (t >> 4) & 3, r = t & 15;
     const int tile = tile0 + tt, ks = k0 + 32 * sub;  // this thread's 32-input sub-step
@@ -236,17 +244,18 @@ __device__ __forceinline__ int split_w8(uint4 code, uint32_t zp, uint32_t (&wl)[
 }
 
 // Block p into LDS buffer buf.
-template <int BITS>
-__device__ __forceinline__ void stage(const Pref &p, Lds<BITS> &L, int buf) {
-    constexpr int RS = Lds<BITS>::RS;
+template <int BITS, int MT>
+__device__ __forceinline__ void stage(const Pref<MT> &p, Lds<BITS, MT> &L, int buf) {
+    constexpr int RS = Lds<BITS, MT>::RS;
     const int t = threadIdx.x;
     const uint32_t zp = (p.zpw >> p.zsh) & 255u;
-    {   // activation planes: hi bytes and (lo - 128) bytes, natural input order
-        const int m = t >> 4, col = 8 * (t & 15);
-        const uint32_t hi0 = __builtin_amdgcn_perm(p.a.y, p.a.x, 0x07050301u);
-        const uint32_t hi1 = __builtin_amdgcn_perm(p.a.w, p.a.z, 0x07050301u);
-        const uint32_t lo0 = __builtin_amdgcn_perm(p.a.y, p.a.x, 0x06040200u) ^ 0x80808080u;
-        const uint32_t lo1 = __builtin_amdgcn_perm(p.a.w, p.a.z, 0x06040200u) ^ 0x80808080u;
+#pragma unroll
+    for (int j = 0; j < MT; j++) {  // activation planes: hi bytes and (lo - 128) bytes, natural input order
+        const int m = (t >> 4) + 16 * j, col = 8 * (t & 15);
+        const uint32_t hi0 = __builtin_amdgcn_perm(p.a[j].y, p.a[j].x, 0x07050301u);
+        const uint32_t hi1 = __builtin_amdgcn_perm(p.a[j].w, p.a[j].z, 0x07050301u);
+        const uint32_t lo0 = __builtin_amdgcn_perm(p.a[j].y, p.a[j].x, 0x06040200u) ^ 0x80808080u;
+        const uint32_t lo1 = __builtin_amdgcn_perm(p.a[j].w, p.a[j].z, 0x06040200u) ^ 0x80808080u;
         *reinterpret_cast<uint2 *>(&L.a_hi[buf][m * RS + col]) = make_uint2(hi0, hi1);
         *reinterpret_cast<uint2 *>(&L.a_lo[buf][m * RS + col]) = make_uint2(lo0, lo1);
     }
@@ -288,117 +297,132 @@ __device__ __forceinline__ void stage(const Pref &p, Lds<BITS> &L, int buf) {
 // Accumulators of one wave: the matrix-core partial sums of the current
 // segment (int4: hi, lo planes; int8: hh, hl, lh, ll), the weight sum of the
 // segment, and the float outputs (4 tokens of one row per lane).
+template <int MT>
 struct Acc {
-    v4i c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    v4i c0[MT] = {}, c1[MT] = {}, c2[MT] = {}, c3[MT] = {};
     int wacc = 0;
-    float acc[4] = {};
+    float acc[MT][4] = {};
 };
 
 __device__ __forceinline__ v4i mfma16(int64_t a, int64_t b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
 }
 
-// The 4 sub-steps of 32 inputs of staged block kb (in LDS buffer buf).
-template <int BITS, bool SEG32>
-__device__ __forceinline__ void compute_block(const Lds<BITS> &L, int buf, int kb, int arow, int brow, int orow,
-                                              int seg, Acc &c) {
+// The 4 sub-steps of 32 inputs of staged block kb (in LDS buffer buf): per
+// sub-step the wave's weight fragment serves its MT token groups.
+template <int BITS, bool SEG32, int MT>
+__device__ __forceinline__ void compute_block(const Lds<BITS, MT> &L, int buf, int kb, int arow, int brow, int orow,
+                                              int seg, Acc<MT> &c) {
+    constexpr int RS = Lds<BITS, MT>::RS;
 #pragma unroll
     for (int s = 0; s < KB / 32; s++) {
-        const int64_t ah = *reinterpret_cast<const int64_t *>(&L.a_hi[buf][arow + 32 * s]);
-        const int64_t al = *reinterpret_cast<const int64_t *>(&L.a_lo[buf][arow + 32 * s]);
         const int64_t b0 = *reinterpret_cast<const int64_t *>(&L.w0[buf][brow + 32 * s]);
+        int64_t b1 = 0;
+        if (BITS == 8) b1 = *reinterpret_cast<const int64_t *>(&L.w1[buf][brow + 32 * s]);
         if (SEG32) {  // every sub-step is a segment: the products start from zero
-            c.c0 = c.c1 = c.c2 = c.c3 = (v4i){};
+#pragma unroll
+            for (int j = 0; j < MT; j++) c.c0[j] = c.c1[j] = c.c2[j] = c.c3[j] = (v4i){};
             c.wacc = 0;
         }
-        if (BITS == 4) {
-            c.c0 = mfma16(ah, b0, c.c0);
-            c.c1 = mfma16(al, b0, c.c1);
-        } else {
-            const int64_t b1 = *reinterpret_cast<const int64_t *>(&L.w1[buf][brow + 32 * s]);
-            c.c0 = mfma16(ah, b1, c.c0);
-            c.c1 = mfma16(ah, b0, c.c1);
-            c.c2 = mfma16(al, b1, c.c2);
-            c.c3 = mfma16(al, b0, c.c3);
+#pragma unroll
+        for (int j = 0; j < MT; j++) {
+            const int64_t ah = *reinterpret_cast<const int64_t *>(&L.a_hi[buf][arow + 16 * j * RS + 32 * s]);
+            const int64_t al = *reinterpret_cast<const int64_t *>(&L.a_lo[buf][arow + 16 * j * RS + 32 * s]);
+            if (BITS == 4) {
+                c.c0[j] = mfma16(ah, b0, c.c0[j]);
+                c.c1[j] = mfma16(al, b0, c.c1[j]);
+            } else {
+                c.c0[j] = mfma16(ah, b1, c.c0[j]);
+                c.c1[j] = mfma16(ah, b0, c.c1[j]);
+                c.c2[j] = mfma16(al, b1, c.c2[j]);
+                c.c3[j] = mfma16(al, b0, c.c3[j]);
+            }
         }
         c.wacc += L.wsum[buf][s][orow];
         if (SEG32 || (kb * KB + 32 * (s + 1)) % seg == 0) {  // end of a segment: tile_i16's flush
             const float sc = L.scale[buf][s][orow];
             const int w128 = 128 * c.wacc;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                int G;
-                if (BITS == 4)
-                    G = (c.c0[i] << 8) + c.c1[i] + w128;
-                else
-                    G = (((c.c0[i] << 4) + c.c1[i]) << 8) + ((c.c2[i] << 4) + c.c3[i]) + w128;
-                c.acc[i] = fmaf((float)G, sc, c.acc[i]);
+            for (int j = 0; j < MT; j++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    int G;
+                    if (BITS == 4)
+                        G = (c.c0[j][i] << 8) + c.c1[j][i] + w128;
+                    else
+                        G = (((c.c0[j][i] << 4) + c.c1[j][i]) << 8) + ((c.c2[j][i] << 4) + c.c3[j][i]) + w128;
+                    c.acc[j][i] = fmaf((float)G, sc, c.acc[j][i]);
+                }
             }
             if (!SEG32) {
-                c.c0 = c.c1 = c.c2 = c.c3 = (v4i){};
+#pragma unroll
+                for (int j = 0; j < MT; j++) c.c0[j] = c.c1[j] = c.c2[j] = c.c3[j] = (v4i){};
                 c.wacc = 0;
             }
         }
     }
 }
 
-template <int BITS, bool SEG32>
+template <int BITS, bool SEG32, int MT>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
-    using LT = Lds<BITS>;
-    constexpr int RS = LT::RS;
+    using LT = Lds<BITS, MT>;
+    constexpr int RS = LT::RS, TMW = 16 * MT;  // tokens of the workgroup
     __shared__ __align__(16) LT L;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int tile0 = blockIdx.x * (TN / 16), out0 = blockIdx.x * TN, tok0 = blockIdx.y * TM;
+    const int tile0 = blockIdx.x * (TN / 16), out0 = blockIdx.x * TN, tok0 = blockIdx.y * TMW;
     const auto rx = make_rsrc(a.xq, a.xq_bytes);
     const auto rc = make_rsrc(a.codes, a.codes_bytes);
     const auto rs = make_rsrc(a.scales, a.scales_bytes);
     const auto rz = make_rsrc(a.zps, a.zps_bytes);
-    if (tid < TM) L.sx[tid] = tok0 + tid < a.T ? a.sx[tok0 + tid] : 0.0f;
+    if (tid < TMW) L.sx[tid] = tok0 + tid < a.T ? a.sx[tok0 + tid] : 0.0f;
 
     const int nkb = (a.K + KB - 1) / KB;
     // Two register sets of prefetched blocks: block kb + 1 is loaded while
     // block kb - 1 is computed, so a load has two blocks of work to arrive.
-    Pref pa, pb;
-    prefetch<BITS>(a, 0, tok0, tile0, pa, rx, rc, rs, rz);
-    if (nkb > 1) prefetch<BITS>(a, 1, tok0, tile0, pb, rx, rc, rs, rz);
-    stage<BITS>(pa, L, 0);
+    Pref<MT> pa, pb;
+    prefetch<BITS, MT>(a, 0, tok0, tile0, pa, rx, rc, rs, rz);
+    if (nkb > 1) prefetch<BITS, MT>(a, 1, tok0, tile0, pb, rx, rc, rs, rz);
+    stage<BITS, MT>(pa, L, 0);
     lds_barrier();
 
-    Acc c;
-    // A: token lane % 16, inputs 8 (lane / 16) ..; B: row 16 wid + lane % 16
+    Acc<MT> c;
+    // A: token 16 j + lane % 16, inputs 8 (lane / 16) ..; B: row 16 wid + lane % 16
     const int arow = (lane & 15) * RS + 8 * (lane >> 4);
     const int brow = (16 * wid + (lane & 15)) * RS + 8 * (lane >> 4);
     const int orow = 16 * wid + (lane & 15);
 
     for (int kb = 0; kb < nkb; kb += 2) {
         // even block kb in buffer 0; pa is free, pb holds block kb + 1
-        if (kb + 2 < nkb) prefetch<BITS>(a, kb + 2, tok0, tile0, pa, rx, rc, rs, rz);
-        compute_block<BITS, SEG32>(L, 0, kb, arow, brow, orow, a.seg, c);
-        if (kb + 1 < nkb) stage<BITS>(pb, L, 1);
+        if (kb + 2 < nkb) prefetch<BITS, MT>(a, kb + 2, tok0, tile0, pa, rx, rc, rs, rz);
+        compute_block<BITS, SEG32, MT>(L, 0, kb, arow, brow, orow, a.seg, c);
+        if (kb + 1 < nkb) stage<BITS, MT>(pb, L, 1);
         lds_barrier();
         if (kb + 1 >= nkb) break;
         // odd block kb + 1 in buffer 1; pb is free, pa holds block kb + 2
-        if (kb + 3 < nkb) prefetch<BITS>(a, kb + 3, tok0, tile0, pb, rx, rc, rs, rz);
-        compute_block<BITS, SEG32>(L, 1, kb + 1, arow, brow, orow, a.seg, c);
-        if (kb + 2 < nkb) stage<BITS>(pa, L, 0);
+        if (kb + 3 < nkb) prefetch<BITS, MT>(a, kb + 3, tok0, tile0, pb, rx, rc, rs, rz);
+        compute_block<BITS, SEG32, MT>(L, 1, kb + 1, arow, brow, orow, a.seg, c);
+        if (kb + 2 < nkb) stage<BITS, MT>(pa, L, 0);
         lds_barrier();
     }
 
-    // Epilogue: lane holds output row out0 + orow for tokens 4 (lane / 16) + i.
+    // Epilogue: lane holds output row out0 + orow for tokens 16 j + 4 (lane / 16) + i.
     const int o = out0 + orow;
     if (o >= a.n) return;
     const float bo = (a.flags & LLMQ_BIAS) ? a.bias[o] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int ml = 4 * (lane >> 4) + i;
-        const int tok = tok0 + ml;
-        if (tok >= a.T) continue;
-        float v = c.acc[i] * L.sx[ml];
-        if (a.flags & LLMQ_BIAS) v += bo;
-        if (a.flags & LLMQ_GELU) v = gelu_ref(v);
-        float *dst = a.out + (int64_t)tok * a.ldo + o;
-        if (a.flags & LLMQ_RESID) v += *dst;
-        *dst = v;
+    for (int j = 0; j < MT; j++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int ml = 16 * j + 4 * (lane >> 4) + i;
+            const int tok = tok0 + ml;
+            if (tok >= a.T) continue;
+            float v = c.acc[j][i] * L.sx[ml];
+            if (a.flags & LLMQ_BIAS) v += bo;
+            if (a.flags & LLMQ_GELU) v = gelu_ref(v);
+            float *dst = a.out + (int64_t)tok * a.ldo + o;
+            if (a.flags & LLMQ_RESID) v += *dst;
+            *dst = v;
+        }
     }
 }
 
@@ -453,19 +477,27 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     a.G = (int)w->group;
     a.seg = (int)(w->group < 256 ? w->group : 256);
     a.flags = rq.flags;
-    dim3 grid((unsigned)((w->n + TN - 1) / TN), (unsigned)((T + TM - 1) / TM));
+    // tokens a workgroup: 16 MT; 32 for the wide matrices (476 tokens: qkv
+    // 21.0 -> 20.1 us, fc 23.3 -> 20.4 us), 16 for the narrow ones (more
+    // workgroups); LLMQ_MFMA_MT overrides, for measurement
+    int mt = w->n >= 2048 ? 2 : 1;
+    if (const char *e = getenv("LLMQ_MFMA_MT")) mt = atoi(e) == 1 ? 1 : atoi(e) == 4 ? 4 : 2;
+    dim3 grid((unsigned)((w->n + TN - 1) / TN), (unsigned)((T + 16 * mt - 1) / (16 * mt)));
     const bool seg32 = a.seg == 32;
+#define GK(B, S, M) hipLaunchKernelGGL((gemm_i8_kernel<B, S, M>), grid, dim3(256), 0, ctx->stream, a)
+#define GKM(B, S)                        \
+    do {                                 \
+        if (mt == 1) GK(B, S, 1);        \
+        else if (mt == 2) GK(B, S, 2);   \
+        else GK(B, S, 4);                \
+    } while (0)
     if (w->bits == 4) {
-        if (seg32)
-            hipLaunchKernelGGL((gemm_i8_kernel<4, true>), grid, dim3(256), 0, ctx->stream, a);
-        else
-            hipLaunchKernelGGL((gemm_i8_kernel<4, false>), grid, dim3(256), 0, ctx->stream, a);
+        if (seg32) GKM(4, true); else GKM(4, false);
     } else {
-        if (seg32)
-            hipLaunchKernelGGL((gemm_i8_kernel<8, true>), grid, dim3(256), 0, ctx->stream, a);
-        else
-            hipLaunchKernelGGL((gemm_i8_kernel<8, false>), grid, dim3(256), 0, ctx->stream, a);
+        if (seg32) GKM(8, true); else GKM(8, false);
     }
+#undef GKM
+#undef GK
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }

@@ -248,6 +248,11 @@ int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *ou
                      int swiglu = 0, const float *ln_w = nullptr, const float *ln_b = nullptr);
 int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
 int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *rows, int n, float *dst, int64_t ldd);
+// Greedy pick of each of B sequences from a head's argmax partials (nparts
+// per sequence), the decode state advanced, and the picked rows of the GGUF
+// embedding E into dst + b * ldd (gguf.hip).
+int launch_gguf_pick_embed(llmq_ctx *ctx, const llmq_mat *E, const ArgmaxPart *parts, int nparts, int B, int *state,
+                           int64_t *next, int64_t *gen, float *dst, int64_t ldd);
 // Prompt attention over an int8 cache of n_kv heads (attn.hip): query head h
 // reads cached head h / (n_head / n_kv) of `layer` (a slot index).
 int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, const float *KS, const float *VS,
@@ -271,9 +276,13 @@ int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t l
                      int64_t ldo, const float *bias, int flags);
 // int16 output head for Q6_K / Q8_0 (gguf_head.hip).
 int gguf_has_i16(const llmq_mat *w);
-// with rms_g, each row of h is RMS-normalized (times rms_g) first
+// with rms_g, each row of h is RMS-normalized (times rms_g) first; with
+// amax, each workgroup leaves each token's largest logit over its rows in
+// amax[token * gguf_head16_parts(w) + workgroup]
 int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *logits, int64_t T,
-                       const float *rms_g = nullptr, float rms_eps = 0.0f);
+                       const float *rms_g = nullptr, float rms_eps = 0.0f, ArgmaxPart *amax = nullptr,
+                       int amax_cap = 0);
+int gguf_head16_parts(const llmq_mat *w);
 
 int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, const float *b, int64_t T, int64_t C);
 int launch_kv_store(llmq_ctx *ctx, llmq_kv *kv, int layer, int pos0, const int *pos_dev, const float *qkv, int T,

@@ -122,6 +122,67 @@ __global__ void gguf_dequant_rows_kernel(GgufArgs a, const int64_t *rows, float 
     dequant_row_body<TYPE>(a, row, d);
 }
 
+// Greedy pick and embedding of sequence b = blockIdx.x after a head that
+// left per-workgroup argmax partials: the largest value over parts[b * nparts
+// ..] (the smallest index among equal ones: the first maximum,
+// gpt2t.mojo:792-797) is the next token, written to next[b] and
+// gen[state[1] * B + b]; its row of E goes to dst + b * ldd.  The last
+// workgroup to finish moves the decode state on (position and step + 1;
+// state[2] counts the finished workgroups and is cleared again).
+template <int TYPE>
+__global__ __launch_bounds__(256) void gguf_pick_embed_kernel(GgufArgs a, const ArgmaxPart *__restrict__ parts,
+                                                              int nparts, int B, int *__restrict__ state,
+                                                              int64_t *__restrict__ next, int64_t *__restrict__ gen,
+                                                              float *__restrict__ dst, int64_t ldd) {
+    __shared__ ArgmaxPart s_b[4];
+    __shared__ int s_pick;
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const ArgmaxPart *P = parts + (int64_t)b * nparts;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < nparts; i += 256) {
+        const ArgmaxPart c = P[i];
+        if (c.v > bv || (c.v == bv && c.idx < bi)) {
+            bv = c.v;
+            bi = c.idx;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) s_b[tid >> 6] = ArgmaxPart{bv, bi};
+    __syncthreads();
+    if (tid == 0) {
+        ArgmaxPart best = s_b[0];
+        for (int w = 1; w < 4; w++)
+            if (s_b[w].v > best.v || (s_b[w].v == best.v && s_b[w].idx < best.idx)) best = s_b[w];
+        const int step = state[1];
+        next[b] = best.idx;
+        gen[(int64_t)step * B + b] = best.idx;
+        s_pick = best.idx;
+        __threadfence();
+        if (atomicAdd(&state[2], 1) == (int)gridDim.x - 1) {  // every workgroup has read the step
+            state[2] = 0;
+            state[0] += 1;
+            state[1] += 1;
+        }
+    }
+    __syncthreads();
+    const int64_t row = s_pick;
+    float *d = dst + (int64_t)b * ldd;
+    if (row < 0 || row >= a.n) {
+        for (int k = tid; k < a.K; k += 256) d[k] = 0.0f;
+        return;
+    }
+    dequant_row_body<TYPE>(a, row, d);
+}
+
 GgufArgs make_args(const llmq_mat *m) {
     GgufArgs a{};
     a.codes = reinterpret_cast<const uint4 *>(m->codes);
@@ -297,6 +358,28 @@ int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *ro
     case LLMQ_GGML_Q6_K: hipLaunchKernelGGL(gguf_dequant_rows_kernel<LLMQ_GGML_Q6_K>, dim3(n), dim3(256), 0, ctx->stream, a, rows, dst, ldd); break;
     default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf dequant: type %d", w->ggml_type);
     }
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+int launch_gguf_pick_embed(llmq_ctx *ctx, const llmq_mat *E, const ArgmaxPart *parts, int nparts, int B, int *state,
+                           int64_t *next, int64_t *gen, float *dst, int64_t ldd) {
+    LLMQ_REQUIRE(E && E->kind == MAT_GGUF && parts && nparts > 0 && B > 0 && state && next && gen && dst,
+                 "gguf pick embed: bad arguments");
+    GgufArgs a = make_args(E);
+#define PE(T)                                                                                                   \
+    hipLaunchKernelGGL(gguf_pick_embed_kernel<T>, dim3(B), dim3(256), 0, ctx->stream, a, parts, nparts, B, state, \
+                       next, gen, dst, ldd)
+    switch (E->ggml_type) {
+    case LLMQ_GGML_Q4_0: PE(LLMQ_GGML_Q4_0); break;
+    case LLMQ_GGML_Q4_1: PE(LLMQ_GGML_Q4_1); break;
+    case LLMQ_GGML_Q8_0: PE(LLMQ_GGML_Q8_0); break;
+    case LLMQ_GGML_Q4_K: PE(LLMQ_GGML_Q4_K); break;
+    case LLMQ_GGML_Q5_K: PE(LLMQ_GGML_Q5_K); break;
+    case LLMQ_GGML_Q6_K: PE(LLMQ_GGML_Q6_K); break;
+    default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf pick embed: type %d", E->ggml_type);
+    }
+#undef PE
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }

@@ -138,9 +138,17 @@ __device__ __forceinline__ float dot4b(uint32_t w, float4 x, float a) {
 // Codes of 8 weights (dword i of a chunk: weight e in nibble e) as two byte
 // vectors: lo = weights 0, 2, 4, 6 and hi = weights 1, 3, 5, 7.  extra holds
 // per-weight high bits already in place (bits 4.. of each byte).
+// (The masks go through v_and_or_b32 as inline assembly: with the masked
+// bits visible the compiler turns each byte's conversion into a bit-field
+// extract plus v_cvt_f32_ubyte0 instead of one v_cvt_f32_ubyte<k>.)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+    return r;
+}
 __device__ __forceinline__ void split8(uint32_t w, uint32_t extra_lo, uint32_t extra_hi, uint32_t &lo, uint32_t &hi) {
-    lo = (w & 0x0F0F0F0Fu) | extra_lo;
-    hi = ((w >> 4) & 0x0F0F0F0Fu) | extra_hi;
+    lo = and_or(w, 0x0F0F0F0Fu, extra_lo);
+    hi = and_or(w >> 4, 0x0F0F0F0Fu, extra_hi);
 }
 
 // sum x[e] * u_e over 8 weights whose x are x[0..7] (two float4): u from the

@@ -14,31 +14,31 @@
 // over units in order, the 16-lane halving sum) are the reference's, so a
 // row's logit is the same float whatever the tile or token count.
 //
-// Work mapping: one workgroup per (16-row tile, up to 8 tokens taken one
-// after another), 4 waves.  Thread
-// (r, q) of a wave (r = lane % 16, q = lane / 16) computes lanes 4q..4q+3 of
-// row r for a unit: Q6_K reads dword q of each of the unit's 8 chunks of 32
-// codes (weights 8q..8q+7) and the matching 16 high bits; Q8_0 reads bytes
-// 8(q%2)..+7 of half 2u + q/2.  Units go through LDS in rounds of R: the
-// waves write each unit's 16 x 16 lane values as floats, then thread (r, L)
-// of the workgroup runs lane L's fma chain over the round's units.
+// Work mapping: 4-wave workgroups, a wave per 16-row tile at a time
+// (gguf_head16_kernel).  Thread (r, q) of a wave (r = lane % 16, q = lane /
+// 16) computes lanes 4q..4q+3 of row r for every unit in order, so each
+// lane's float chain and the 16-lane sum stay in registers; Q6_K reads dword
+// q of each of the unit's 8 chunks of 32 codes (weights 8q..8q+7) and the
+// matching 16 high bits, Q8_0 bytes 8(q%2)..+7 of half 2u + q/2.
 #include "common.h"
 
 namespace {
 
 constexpr uint32_t kOOB = 0x80000000u;
-constexpr int kNW = 4;  // waves per workgroup
+constexpr int kNW = 4;    // waves per workgroup
+constexpr int kMaxC = 4096;  // longest row the kernel takes
 
 typedef short short2v __attribute__((ext_vector_type(2)));
 
 struct H16Args {
     const uint8_t *codes, *bits, *sb, *d;
     uint32_t codes_bytes, bits_bytes, sb_bytes, d_bytes;
-    int V, C, CK, NU, T, tpb;  // tpb: tokens a workgroup takes, one after another
+    int V, C, CK, NU, T, ntiles;
     const float *h;
     float *logits;
     const float *rms_g;  // optional RMSNorm gain applied to h first
     float rms_eps;
+    ArgmaxPart *amax;    // optional per-workgroup argmax partials
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
@@ -78,205 +78,352 @@ __device__ __forceinline__ uint32_t spread2(uint32_t f) {
     return x << 4;
 }
 
+// A unit's raw fields as thread (r, q) of a wave reads them: row r of the
+// tile, lanes 4q..4q+3 of the unit's int32 accumulator.  Q6_K: dword q of
+// each of the superblock's 8 chunks of 32 codes (weights 8q..8q+7 of the
+// chunk) and the matching 16 high bits, the 16 int8 scales, d; Q8_0: bytes
+// 8(q%2)..+7 of half 2u + q/2 of the block (weights 8q..8q+7) and d.
 template <int TYPE>
-struct Unit {
-    static constexpr int WEIGHTS = TYPE == LLMQ_GGML_Q6_K ? 256 : 32;
-    static constexpr int UPW = TYPE == LLMQ_GGML_Q6_K ? 1 : 4;  // units a wave takes per round
-    static constexpr int R = kNW * UPW;                         // units per round
+struct RawUnit;
+template <>
+struct RawUnit<LLMQ_GGML_Q6_K> {
+    uint32_t cw[8], hw[8];
+    uint4 sc;
+    uint32_t dw;
+};
+template <>
+struct RawUnit<LLMQ_GGML_Q8_0> {
+    uint2 cw;
+    uint32_t dw;
 };
 
-// Lanes 4q..4q+3 of row r's int32 accumulator for Q6_K superblock u of
-// tile `tile`, and its d.  xq32: the token's int16 activations as pairs.
-__device__ __forceinline__ void q6k_unit(const H16Args &a, int tile, int u, int r, int q, const uint32_t *xq32,
-                                         int (&acc)[4], float &d) {
+// Loads of unit u of tile `tile` (nothing read when !ok: out-of-range
+// offsets return zeros).
+template <int TYPE>
+__device__ __forceinline__ RawUnit<TYPE> load_unit(const H16Args &a, bool ok, int tile, int u, int r, int q) {
+    RawUnit<TYPE> w;
     const auto rc = make_rsrc(a.codes, a.codes_bytes);
-    const auto rb = make_rsrc(a.bits, a.bits_bytes);
-    const auto rs = make_rsrc(a.sb, a.sb_bytes);
     const auto rd = make_rsrc(a.d, a.d_bytes);
-    const uint32_t c0 = (uint32_t)tile * (uint32_t)a.CK + 8u * (uint32_t)u;  // global index of the unit's first chunk
-    uint32_t cw[8], hw[8];
+    if constexpr (TYPE == LLMQ_GGML_Q6_K) {
+        const auto rb = make_rsrc(a.bits, a.bits_bytes);
+        const auto rs = make_rsrc(a.sb, a.sb_bytes);
+        const uint32_t c0 = (uint32_t)tile * (uint32_t)a.CK + 8u * (uint32_t)u;  // the unit's first chunk
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-        const uint32_t e = (c0 + c) * 16u + (uint32_t)r;  // (chunk, row) entry
-        cw[c] = bload4(rc, e * 16u + 4u * (uint32_t)q);
-        hw[c] = bload4(rb, e * 8u + 4u * (uint32_t)(q >> 1));
+        for (int c = 0; c < 8; c++) {
+            const uint32_t e = (c0 + c) * 16u + (uint32_t)r;  // (chunk, row) entry
+            w.cw[c] = bload4(rc, ok ? e * 16u + 4u * (uint32_t)q : kOOB);
+            w.hw[c] = bload4(rb, ok ? e * 8u + 4u * (uint32_t)(q >> 1) : kOOB);
+        }
+        const uint32_t se = ((uint32_t)tile * (uint32_t)a.NU + (uint32_t)u) * 16u + (uint32_t)r;
+        w.sc = bload16(rs, ok ? se * 16u : kOOB);
+        w.dw = bload4(rd, ok ? (se * 2u) & ~3u : kOOB);
+    } else {
+        const uint32_t e = ((uint32_t)tile * (uint32_t)a.CK + 2u * (uint32_t)u + (uint32_t)(q >> 1)) * 16u + (uint32_t)r;
+        w.cw = bload8(rc, ok ? e * 16u + 8u * (uint32_t)(q & 1) : kOOB);
+        const uint32_t de = ((uint32_t)tile * (uint32_t)(a.CK / 2) + (uint32_t)u) * 16u + (uint32_t)r;
+        w.dw = bload4(rd, ok ? (de * 2u) & ~3u : kOOB);
     }
-    const uint32_t se = ((uint32_t)tile * (uint32_t)a.NU + (uint32_t)u) * 16u + (uint32_t)r;
-    const uint4 sc4 = bload16(rs, se * 16u);
-    const uint32_t dw = bload4(rd, (se * 2u) & ~3u);
-    d = h2f(dw >> (16 * (se & 1u)));
-    const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[j] = 0;
+    return w;
+}
+
+// Q6_K: the unit's weights (q - 32) * sc as int16 pairs, wp[c][j] = weights
+// 8q + 2j, 8q + 2j + 1 of chunk c, |.| <= 4096.
+__device__ __forceinline__ void q6k_pairs(const RawUnit<LLMQ_GGML_Q6_K> &w, int q, uint32_t (&wp)[8][4]) {
+    const uint32_t scw[4] = {w.sc.x, w.sc.y, w.sc.z, w.sc.w};
 #pragma unroll
     for (int c = 0; c < 8; c++) {
         // int8 scale of this chunk's half: scale 2c + (weights >= 16)
         const uint32_t sbyte = (scw[c >> 1] >> (8 * (2 * (c & 1) + (q >> 1)))) & 255u;
         const uint32_t s16 = (uint32_t)(int)(int8_t)sbyte & 0xFFFFu;
         const uint32_t spair = s16 | (s16 << 16);
-        const uint32_t hb = hw[c] >> (16 * (q & 1));  // 2 high bits of weight 8q + i at bits 2i
-        const uint32_t qe = (cw[c] & 0x0F0F0F0Fu) | spread2(hb);             // even weights, 6-bit codes
-        const uint32_t qo = ((cw[c] >> 4) & 0x0F0F0F0Fu) | spread2(hb >> 2);  // odd weights
-        const uint4 xv = *reinterpret_cast<const uint4 *>(xq32 + 128 * u + 16 * c + 4 * q);
-        const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
+        const uint32_t hb = w.hw[c] >> (16 * (q & 1));  // 2 high bits of weight 8q + i at bits 2i
+        const uint32_t qe = (w.cw[c] & 0x0F0F0F0Fu) | spread2(hb);             // even weights, 6-bit codes
+        const uint32_t qo = ((w.cw[c] >> 4) & 0x0F0F0F0Fu) | spread2(hb >> 2);  // odd weights
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             // [q_e, 0, q_o, 0]: the pair as two 16-bit codes
             const uint32_t sel = (uint32_t)j | (0x0Cu << 8) | ((uint32_t)(4 + j) << 16) | (0x0Cu << 24);
-            const uint32_t p = __builtin_amdgcn_perm(qo, qe, sel);
-            short2v w = __builtin_bit_cast(short2v, p) - (short2v){32, 32};
-            w = w * __builtin_bit_cast(short2v, spair);  // (q - 32) * sc, |.| <= 4096
-            acc[j] = sdot2(xp[j], __builtin_bit_cast(uint32_t, w), acc[j]);
+            short2v v = __builtin_bit_cast(short2v, __builtin_amdgcn_perm(qo, qe, sel)) - (short2v){32, 32};
+            v = v * __builtin_bit_cast(short2v, spair);
+            wp[c][j] = __builtin_bit_cast(uint32_t, v);
         }
     }
 }
 
-// Lanes 4q..4q+3 of row r's int32 accumulator for Q8_0 block u, and its d.
-// The codes are placed in the high byte of each 16-bit half (256 * code),
-// so one dot gives 256 * (x0 w0 + x1 w1); |that| <= 2 * 32767 * 128 * 256 <
-// 2^31, and the arithmetic shift by 8 is exact.
-__device__ __forceinline__ void q80_unit(const H16Args &a, int tile, int u, int r, int q, const uint32_t *xq32,
-                                         int (&acc)[4], float &d) {
-    const auto rc = make_rsrc(a.codes, a.codes_bytes);
-    const auto rd = make_rsrc(a.d, a.d_bytes);
-    const uint32_t e = ((uint32_t)tile * (uint32_t)a.CK + 2u * (uint32_t)u + (uint32_t)(q >> 1)) * 16u + (uint32_t)r;
-    const uint2 cw = bload8(rc, e * 16u + 8u * (uint32_t)(q & 1));
-    const uint32_t de = ((uint32_t)tile * (uint32_t)(a.CK / 2) + (uint32_t)u) * 16u + (uint32_t)r;
-    const uint32_t dw = bload4(rd, (de * 2u) & ~3u);
-    d = h2f(dw >> (16 * (de & 1u)));
-    const uint4 xv = *reinterpret_cast<const uint4 *>(xq32 + 16 * u + 4 * q);
-    const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
-    const uint32_t ww[2] = {cw.x, cw.y};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t b = 2u * (uint32_t)(j & 1);  // pair j: bytes 2j, 2j + 1 of the 8
-        const uint32_t sel = 0x0Cu | (b << 8) | (0x0Cu << 16) | ((b + 1u) << 24);
-        const uint32_t p = __builtin_amdgcn_perm(0u, ww[j >> 1], sel);
-        acc[j] = sdot2(xp[j], p, 0) >> 8;
-    }
-}
-
-template <int TYPE>
-__global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
-    using U = Unit<TYPE>;
-    extern __shared__ __align__(16) uint32_t smem_u[];
-    __shared__ float red[kNW];
-    uint32_t *xq32 = smem_u;                                               // [C / 2] int16 pairs
-    float *lanev = reinterpret_cast<float *>(smem_u + a.C / 2);            // [R][16 rows][16 lanes]
-    float *dv = lanev + U::R * 256;                                        // [R][16 rows]
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tile = blockIdx.x;
-    const int tb = blockIdx.y * a.tpb, te = min(a.T, tb + a.tpb);
-    // Tokens one after another: the tile's weights come from HBM for the
-    // first and from L2 for the rest.
-    for (int t = tb; t < te; t++) {
-    const float *h = a.h + (size_t)t * a.C;
-
+// quantize_rows (kernels.mojo:400-416) of token t (after the optional
+// RMSNorm): s = max|h| / 32767 (1 if zero), codes round(h / s) as int16
+// pairs into xt, s into *sx.  COOP: the whole workgroup (me = thread),
+// else one wave (me = lane); the row stays in registers, RV float4 a thread.
+template <int RV, bool COOP>
+__device__ __forceinline__ void quantize_token(const H16Args &a, int t, int me, uint32_t *xt, float *s_red,
+                                               float *sx_out) {
+    constexpr int NTH = COOP ? kNW * 64 : 64;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int n4 = a.C / 4;
-    // optional RMSNorm: h -> (h * rn) * g, rn = 1 / sqrt(mean(h^2) + eps)
-    float rn = 1.0f;
+    const float4 *h4 = reinterpret_cast<const float4 *>(a.h + (size_t)t * a.C);
     const float4 *g4 = reinterpret_cast<const float4 *>(a.rms_g);
+    float4 v[RV];
+#pragma unroll
+    for (int k = 0; k < RV; k++) {
+        const int i = me + k * NTH;
+        v[k] = i < n4 ? h4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     if (a.rms_g) {
         float ss = 0.0f;
-        for (int i = tid; i < n4; i += kNW * 64) {
-            const float4 v = reinterpret_cast<const float4 *>(h)[i];
-            ss = fmaf(v.x, v.x, ss);
-            ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss);
-            ss = fmaf(v.w, v.w, ss);
+#pragma unroll
+        for (int k = 0; k < RV; k++) {
+            ss = fmaf(v[k].x, v[k].x, ss);
+            ss = fmaf(v[k].y, v[k].y, ss);
+            ss = fmaf(v[k].z, v[k].z, ss);
+            ss = fmaf(v[k].w, v[k].w, ss);
         }
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-        if (lane == 0) red[wid] = ss;
-        __syncthreads();
-        ss = ((red[0] + red[1]) + red[2]) + red[3];
-        rn = 1.0f / sqrtf(ss / (float)a.C + a.rms_eps);
-        __syncthreads();
-    }
-    auto row4 = [&](int i) {
-        float4 v = reinterpret_cast<const float4 *>(h)[i];
-        if (a.rms_g) {
-            const float4 g = g4[i];
-            v.x = (v.x * rn) * g.x;
-            v.y = (v.y * rn) * g.y;
-            v.z = (v.z * rn) * g.z;
-            v.w = (v.w * rn) * g.w;
+        if (COOP) {
+            if (lane == 0) s_red[wid] = ss;
+            __syncthreads();
+            ss = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
+            __syncthreads();
         }
-        return v;
-    };
-    // quantize_rows for this token: s = max|h| / 32767, q = round(h / s)
-    float m = 0.0f;
-    for (int i = tid; i < n4; i += kNW * 64) {
-        const float4 v = row4(i);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        const float rn = 1.0f / sqrtf(ss / (float)a.C + a.rms_eps);
+#pragma unroll
+        for (int k = 0; k < RV; k++) {
+            const int i = me + k * NTH;
+            if (i < n4) {
+                const float4 gg = g4[i];
+                v[k].x = (v[k].x * rn) * gg.x;
+                v[k].y = (v[k].y * rn) * gg.y;
+                v[k].z = (v[k].z * rn) * gg.z;
+                v[k].w = (v[k].w * rn) * gg.w;
+            }
+        }
     }
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RV; k++)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if (lane == 0) red[wid] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (COOP) {
+        if (lane == 0) s_red[wid] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+        __syncthreads();
+    }
     float sx = m / 32767.0f;
     if (sx == 0.0f) sx = 1.0f;
     const float inv = 1.0f / sx;
-    for (int i = tid; i < n4; i += kNW * 64) {
-        const float4 v = row4(i);
-        const int q0 = round_to_int(v.x * inv), q1 = round_to_int(v.y * inv);
-        const int q2 = round_to_int(v.z * inv), q3 = round_to_int(v.w * inv);
-        xq32[2 * i] = ((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16);
-        xq32[2 * i + 1] = ((uint32_t)q2 & 0xFFFFu) | ((uint32_t)q3 << 16);
+#pragma unroll
+    for (int k = 0; k < RV; k++) {
+        const int i = me + k * NTH;
+        if (i < n4) {
+            const int q0 = round_to_int(v[k].x * inv), q1 = round_to_int(v[k].y * inv);
+            const int q2 = round_to_int(v[k].z * inv), q3 = round_to_int(v[k].w * inv);
+            *reinterpret_cast<uint2 *>(xt + 2 * i) = make_uint2(((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16),
+                                                                ((uint32_t)q2 & 0xFFFFu) | ((uint32_t)q3 << 16));
+        }
+    }
+    if (me == 0) *sx_out = sx;
+}
+
+// One workgroup of kNW waves; wave g = blockIdx.x * kNW + wid takes tiles
+// g, g + G, .. (G = gridDim.x * kNW) and streams their units in order, the
+// loads of the next PD units in flight while one is computed.  Thread
+// (r = lane % 16, q = lane / 16) keeps lanes 4q..4q+3 of row r's float
+// chain for each of up to TM tokens (tokens blockIdx.y * TM ..): the chain
+// over units and the 16-lane sum stay in registers and shuffles.  The
+// tokens are normalized and quantized once per workgroup, a wave a token.
+// With amax set, each workgroup also leaves the largest logit of each token
+// over its tiles (and its smallest row) in amax[token * gridDim.x + wg].
+template <int TYPE, int TM>
+__global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
+    extern __shared__ __align__(16) uint32_t xq32[];  // [TM][C / 2] int16 pairs
+    __shared__ float s_sx[TM], s_red[kNW];
+    __shared__ ArgmaxPart s_best[kNW][TM];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const int t0 = blockIdx.y * TM, nt = min(TM, a.T - t0);
+    const int C2 = a.C / 2, NU = a.NU;
+    const int g = blockIdx.x * kNW + wid, G = gridDim.x * kNW;
+    // unit stream: item s is unit s % NU of tile g + (s / NU) * G
+    auto item_tile = [&](int s) { return g + (s / NU) * G; };
+    auto load_item = [&](int s) {
+        const int tile = item_tile(s);
+        return load_unit<TYPE>(a, tile < a.ntiles, tile, s % NU, r, q);
+    };
+    constexpr int PD = TM <= 2 ? 3 : 2;  // units in flight behind the one computed
+    RawUnit<TYPE> ring[PD];
+#pragma unroll
+    for (int k = 0; k < PD; k++) ring[k] = load_item(k);
+
+    // Tokens: optional RMSNorm, then quantize_rows (kernels.mojo:400-416).
+    // Fewer tokens than waves: the workgroup takes them one by one; else a
+    // wave per token.
+    if (TM < kNW || nt < kNW) {
+        for (int t = 0; t < nt; t++) quantize_token<kMaxC / 4 / (kNW * 64), true>(a, t0 + t, tid, xq32 + (size_t)t * C2, s_red, &s_sx[t]);
+    } else {
+        for (int t = wid; t < nt; t += kNW) quantize_token<kMaxC / 4 / 64, false>(a, t0 + t, lane, xq32 + (size_t)t * C2, s_red, &s_sx[t]);
     }
     __syncthreads();
-
-    const int r = lane & 15, q = lane >> 4;  // phase 1: row r, lanes 4q..4q+3
-    const int pr = tid >> 4, pl = tid & 15;  // phase 2: row pr, lane pl
-    float accf = 0.0f;
-    for (int u0 = 0; u0 < a.NU; u0 += U::R) {
+    float sx[TM];
 #pragma unroll
-        for (int i = 0; i < U::UPW; i++) {
-            const int ul = wid * U::UPW + i, u = u0 + ul;
-            if (u >= a.NU) break;
-            int acc[4];
-            float d;
-            if (TYPE == LLMQ_GGML_Q6_K)
-                q6k_unit(a, tile, u, r, q, xq32, acc, d);
-            else
-                q80_unit(a, tile, u, r, q, xq32, acc, d);
-            *reinterpret_cast<float4 *>(lanev + (ul * 16 + r) * 16 + 4 * q) =
-                make_float4((float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]);
-            if (q == 0) dv[ul * 16 + r] = d;
+    for (int t = 0; t < TM; t++) sx[t] = s_sx[t < nt ? t : 0];
+
+    float accf[TM][4];
+    float best_v[TM];
+    int best_i[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) accf[t][j] = 0.0f;
+        best_v[t] = -INFINITY;
+        best_i[t] = 0x7fffffff;
+    }
+    for (int s0 = 0;; s0 += PD) {
+#pragma unroll
+    for (int k = 0; k < PD; k++) {
+        const int s = s0 + k;
+        const int tile = item_tile(s);
+        if (tile >= a.ntiles) goto done;  // uniform over the wave
+        const int u = s % NU;
+        const RawUnit<TYPE> b0 = ring[k];
+        ring[k] = load_item(s + PD);
+        if constexpr (TYPE == LLMQ_GGML_Q6_K) {
+            const float d = h2f(b0.dw >> (16 * (r & 1)));
+            uint32_t wp[8][4];
+            q6k_pairs(b0, q, wp);
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                if (t < nt) {
+                    const uint32_t *xt = xq32 + (size_t)t * C2 + 128 * u + 4 * q;
+                    int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+                    for (int c = 0; c < 8; c++) {
+                        const uint4 xv = *reinterpret_cast<const uint4 *>(xt + 16 * c);
+                        acc[0] = sdot2(xv.x, wp[c][0], acc[0]);
+                        acc[1] = sdot2(xv.y, wp[c][1], acc[1]);
+                        acc[2] = sdot2(xv.z, wp[c][2], acc[2]);
+                        acc[3] = sdot2(xv.w, wp[c][3], acc[3]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; j++) accf[t][j] = fmaf((float)acc[j], d, accf[t][j]);
+                }
+            }
+        } else {
+            // codes in the high byte of each 16-bit half (256 * code): one
+            // dot gives 256 * (x0 w0 + x1 w1), |.| < 2^31, and the shift by
+            // 8 is exact
+            const float d = h2f(b0.dw >> (16 * (r & 1)));
+            const uint32_t ww[2] = {b0.cw.x, b0.cw.y};
+            uint32_t wp[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t bb = 2u * (uint32_t)(j & 1);  // pair j: bytes 2j, 2j + 1 of the 8
+                wp[j] = __builtin_amdgcn_perm(0u, ww[j >> 1], 0x0Cu | (bb << 8) | (0x0Cu << 16) | ((bb + 1u) << 24));
+            }
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                if (t < nt) {
+                    const uint4 xv = *reinterpret_cast<const uint4 *>(xq32 + (size_t)t * C2 + 16 * u + 4 * q);
+                    const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) accf[t][j] = fmaf((float)(sdot2(xp[j], wp[j], 0) >> 8), d, accf[t][j]);
+                }
+            }
         }
-        __syncthreads();
-        const int nu = min(U::R, a.NU - u0);
-        for (int ul = 0; ul < nu; ul++) accf = fmaf(lanev[(ul * 16 + pr) * 16 + pl], dv[ul * 16 + pr], accf);
-        __syncthreads();
+        if (u == NU - 1) {
+            // red16 (lane L = 4q + j): v[L] + v[L + 8] (q ^ 2), then + 4
+            // (q ^ 1), + 2 and + 1 (j) on q == 0
+            const int row = tile * 16 + r;
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                if (t < nt) {
+                    float v[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        v[j] = accf[t][j] + __shfl_xor(accf[t][j], 32);
+                        v[j] += __shfl_xor(v[j], 16);
+                        accf[t][j] = 0.0f;
+                    }
+                    const float lg = ((v[0] + v[2]) + (v[1] + v[3])) * sx[t];
+                    if (q == 0 && row < a.V) {
+                        a.logits[(size_t)(t0 + t) * a.V + row] = lg;
+                        if (lg > best_v[t] || (lg == best_v[t] && row < best_i[t])) {
+                            best_v[t] = lg;
+                            best_i[t] = row;
+                        }
+                    }
+                }
+            }
+        }
     }
-    // red16: v[i] + v[i + 8], then + 4, + 2, + 1 (lane pl < 8, 4, 2, 1 keeps the sums)
-    accf += __shfl_xor(accf, 8);
-    accf += __shfl_xor(accf, 4);
-    accf += __shfl_xor(accf, 2);
-    accf += __shfl_xor(accf, 1);
-    const int row = tile * 16 + pr;
-    if (pl == 0 && row < a.V) a.logits[(size_t)t * a.V + row] = accf * sx;
-    __syncthreads();  // before the next token's codes overwrite the LDS
+    }
+done:
+    if (!a.amax) return;
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+        float bv = best_v[t];
+        int bi = best_i[t];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) s_best[wid][t] = ArgmaxPart{bv, bi};
+    }
+    __syncthreads();
+    if (tid < nt) {
+        ArgmaxPart b = s_best[0][tid];
+#pragma unroll
+        for (int w = 1; w < kNW; w++) {
+            const ArgmaxPart c = s_best[w][tid];
+            if (c.v > b.v || (c.v == b.v && c.idx < b.idx)) b = c;
+        }
+        a.amax[(size_t)(t0 + tid) * gridDim.x + blockIdx.x] = b;
     }
 }
 
-size_t head16_lds(const llmq_mat *w) {
-    const int R = w->ggml_type == LLMQ_GGML_Q6_K ? Unit<LLMQ_GGML_Q6_K>::R : Unit<LLMQ_GGML_Q8_0>::R;
-    return (size_t)w->k * 2 + (size_t)R * 256 * 4 + (size_t)R * 16 * 4;
+// Tokens a workgroup takes (the register chains per thread).
+int head16_tm(int64_t T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16; }
+
+// Workgroups: enough waves for every tile once, at most 512 workgroups
+// (then waves take several tiles); LLMQ_HEAD16_GRID overrides.
+int head16_grid(const llmq_mat *w) {
+    int g = (int)std::min<int64_t>((w->ntiles + kNW - 1) / kNW, 512);
+    if (const char *e = getenv("LLMQ_HEAD16_GRID")) {
+        const int v = atoi(e);
+        if (v >= 1 && v <= 4096) g = v;
+    }
+    return std::max(g, 1);
 }
 
-template <int TYPE>
-int launch_t(llmq_ctx *ctx, const H16Args &a, int ntiles, int T, size_t lds) {
-    static size_t granted = 64 * 1024;
+template <int TYPE, int TM>
+int launch_tm(llmq_ctx *ctx, const H16Args &a, int grid, int T) {
+    const size_t lds = (size_t)TM * a.C * 2;
+    static size_t granted = 64 * 1024;  // one host thread per context
     if (lds > granted) {
-        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gguf_head16_kernel<TYPE>),
+        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gguf_head16_kernel<TYPE, TM>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         granted = lds;
     }
-    hipLaunchKernelGGL(gguf_head16_kernel<TYPE>, dim3(ntiles, (T + a.tpb - 1) / a.tpb), dim3(kNW * 64), lds,
+    hipLaunchKernelGGL((gguf_head16_kernel<TYPE, TM>), dim3(grid, (T + TM - 1) / TM), dim3(kNW * 64), lds,
                        ctx->stream, a);
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
+}
+
+template <int TYPE>
+int launch_t(llmq_ctx *ctx, const H16Args &a, int grid, int T) {
+    switch (head16_tm(T)) {
+    case 1: return launch_tm<TYPE, 1>(ctx, a, grid, T);
+    case 2: return launch_tm<TYPE, 2>(ctx, a, grid, T);
+    case 4: return launch_tm<TYPE, 4>(ctx, a, grid, T);
+    case 8: return launch_tm<TYPE, 8>(ctx, a, grid, T);
+    default: return launch_tm<TYPE, 16>(ctx, a, grid, T);
+    }
 }
 
 }  // namespace
@@ -285,16 +432,22 @@ int gguf_has_i16(const llmq_mat *w) {
     return w && w->kind == MAT_GGUF && (w->ggml_type == LLMQ_GGML_Q6_K || w->ggml_type == LLMQ_GGML_Q8_0);
 }
 
+int gguf_head16_parts(const llmq_mat *w) { return head16_grid(w); }
+
 int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *logits, int64_t T,
-                       const float *rms_g, float rms_eps) {
+                       const float *rms_g, float rms_eps, ArgmaxPart *amax, int amax_cap) {
     LLMQ_REQUIRE(gguf_has_i16(w), "gguf head: only Q6_K and Q8_0 have an int16 kernel");
-    LLMQ_REQUIRE(h && logits && T > 0 && T <= 65535, "gguf head: bad arguments");
-    const size_t lds = head16_lds(w);
+    LLMQ_REQUIRE(h && logits && T > 0 && (T + 15) / 16 <= 65535, "gguf head: bad arguments");
+    LLMQ_REQUIRE(w->k <= kMaxC, "gguf head: %lld columns beyond %d", (long long)w->k, kMaxC);
+    const int grid = head16_grid(w);
+    LLMQ_REQUIRE(!amax || (int64_t)grid * T <= amax_cap, "gguf head: argmax capacity %d below %lld", amax_cap,
+                 (long long)grid * T);
+    const size_t lds = (size_t)head16_tm(T) * w->k * 2;
     int dev = 0, cap = 0;
     LLMQ_HIP(hipGetDevice(&dev));
     LLMQ_HIP(hipDeviceGetAttribute(&cap, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
-    LLMQ_REQUIRE(lds <= (size_t)cap, "gguf head: %lld columns need %zu bytes of LDS (have %d)", (long long)w->k, lds,
-                 cap);
+    LLMQ_REQUIRE(lds + 1024 <= (size_t)cap, "gguf head: %lld columns need %zu bytes of LDS (have %d)",
+                 (long long)w->k, lds, cap);
     const int64_t ntc = (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 16;
     const int64_t nts = (w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 16;
     LLMQ_REQUIRE(ntc * 16 < (int64_t)kOOB, "gguf head: matrix too large for 32-bit offsets");
@@ -304,12 +457,13 @@ int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *
     a.V = (int)w->n;
     a.C = (int)w->k;
     a.CK = (int)w->CK;
+    a.ntiles = (int)w->ntiles;
     a.h = h;
     a.logits = logits;
     a.T = (int)T;
-    a.tpb = T < 8 ? (int)T : 8;
     a.rms_g = rms_g;
     a.rms_eps = rms_eps;
+    a.amax = amax;
     if (w->ggml_type == LLMQ_GGML_Q6_K) {
         a.bits = reinterpret_cast<const uint8_t *>(w->g_bits64);
         a.bits_bytes = (uint32_t)(ntc * 8);
@@ -318,10 +472,10 @@ int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *
         a.d = reinterpret_cast<const uint8_t *>(w->g_meta16);
         a.d_bytes = (uint32_t)(nts * 2);
         a.NU = (int)w->NG;
-        return launch_t<LLMQ_GGML_Q6_K>(ctx, a, (int)w->ntiles, (int)T, lds);
+        return launch_t<LLMQ_GGML_Q6_K>(ctx, a, grid, (int)T);
     }
     a.d = reinterpret_cast<const uint8_t *>(w->g_meta16);
     a.d_bytes = (uint32_t)(ntc * 2);
     a.NU = (int)(w->k / 32);
-    return launch_t<LLMQ_GGML_Q8_0>(ctx, a, (int)w->ntiles, (int)T, lds);
+    return launch_t<LLMQ_GGML_Q8_0>(ctx, a, grid, (int)T);
 }

@@ -19,6 +19,7 @@
 // (one GEMV per layer); Wgate and Wup one of 2 ffn rows.  The cache holds
 // slot (sequence * n_layer + layer) of n_kv heads.  Decoding keeps the
 // position and step on the device, so one captured graph replays every step.
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -70,27 +71,27 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     for (int i = threadIdx.x; i < C; i += 256) orow[i] = (xr[i] * r) * g[i];
 }
 
-// RoPE and the cache store for row `row` of qkv (token t = row % T of
-// sequence seq0 + row / T, position pos + t with pos = state[0] when given):
+// RoPE and the cache store of a prompt: row `row` of qkv is token t = row % T
+// of sequence seq0 + row / T, at position pos0 + t.
 // query heads are rotated in place; key heads are rotated, then key and
 // value heads quantized into the cache as QuantKV.store does
 // (kvcache.mojo:320-342: s = max|x| / 127, 1 if zero; codes round(x / s)).
 // One wave per (head, row); lane = dim.
 __global__ __launch_bounds__(64) void rope_store_kernel(float *__restrict__ qkv, int64_t ld, int T, int seq0,
-                                                        int pos0, const int *__restrict__ state, int n_head,
-                                                        int n_kv, int n_layer, int layer, int max_t, float theta,
-                                                        int8_t *__restrict__ K8, int8_t *__restrict__ V8,
-                                                        float *__restrict__ KS, float *__restrict__ VS) {
+                                                        int pos0, int n_head,
+                                                        int n_kv, int n_layer, int layer, int max_t,
+                                                        const float2 *__restrict__ rope, int8_t *__restrict__ K8,
+                                                        int8_t *__restrict__ V8, float *__restrict__ KS,
+                                                        float *__restrict__ VS) {
     const int hh = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
     const int seq = seq0 + row / T, t = row % T;
-    const int pos = (state ? state[0] : pos0) + t;
+    const int pos = pos0 + t;
     float *r = qkv + (int64_t)row * ld;
     const bool is_q = hh < n_head;
     float *src = r + hh * HD;  // query heads, then key heads
-    // rotation of pair (2i, 2i + 1), i = d / 2
-    const float freq = powf(theta, -(float)(2 * (d >> 1)) / (float)HD);
-    const float ang = (float)pos * freq;
-    const float c = cosf(ang), s = sinf(ang);
+    // rotation of pair (2i, 2i + 1), i = d / 2, by the table's angle
+    const float2 cs = rope[pos * (HD / 2) + (d >> 1)];
+    const float c = cs.x, s = cs.y;
     const float v = src[d], p = __shfl_xor(v, 1);
     // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
     const float rot = (d & 1) ? p * s + v * c : v * c - p * s;
@@ -112,134 +113,188 @@ __global__ __launch_bounds__(64) void rope_store_kernel(float *__restrict__ qkv,
 }
 
 // One decode position for query head h = blockIdx.x of sequence b =
-// blockIdx.y at position state[0]: attend_float_one (kvcache.mojo:113-150)
-// over the int8 cache (QuantKV.score / add_value, 344-370) of key / value
-// head h / (n_head / n_kv), split over blocks of kSplit positions
-// (blockIdx.z) so a head's positions are scored in parallel.  A split writes
-// its maximum score m, its sum of e = exp(score - m) and its partial
-// sum_s (e * vs) * v; attend_combine_kernel rescales the splits to the
-// overall maximum and divides by the overall sum.  (The reference divides
-// each e by the total before the value products; the float rounding
-// differs, the sums are the same.)
-constexpr int kSplit = 128;
-constexpr int kPart = 2 + HD;  // floats of one split's result
+// blockIdx.y at position pos = state[0], one workgroup for all positions:
+// RoPE of the query and of the new key, the new key and value quantized
+// into the cache (rope_store_kernel's arithmetic), then attend_float_one
+// (kvcache.mojo:113-150) over the int8 cache (QuantKV.score / add_value,
+// 344-370) of key / value head h / (n_head / n_kv):
+//   out = sum_p (e_p vs_p) v_p / sum_p e_p,  e_p = exp(score_p - max score)
+// (the reference divides each e by the total before the value products;
+// the float rounding differs, the sums are the same).  Position pos's key
+// and value come from LDS: its cache row is written by the first query head
+// of each key / value group and read by no workgroup of this launch.
+//
+// Thread t scores positions t, t + kAttnT, ..; for the values, thread
+// (g = t / 4, c = t % 4) sums dims 16c..16c+15 over positions g, g + kVG,
+// .., and the kVG partial vectors are added in a fixed order.  Every key and
+// value load is issued at the start.  A score is q . (u - 128) over the
+// key's codes u = k + 128 (one byte conversion each): q . u - 128 sum(q).
+constexpr int kAttnT = 1024;
+constexpr int kMaxT = 2048;                 // positions a workgroup holds
+constexpr int kKPT = kMaxT / kAttnT;        // key rows a thread loads
+constexpr int kVG = kAttnT / 4;             // value row groups
+constexpr int kVPT = kMaxT / kVG;           // value rows a thread loads
 
-__global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__restrict__ qkv, int64_t ld,
-                                                              const int *__restrict__ state, int n_head, int n_kv,
-                                                              int n_layer, int layer, int max_t,
-                                                              const int8_t *__restrict__ K8,
-                                                              const int8_t *__restrict__ V8,
-                                                              const float *__restrict__ KS,
-                                                              const float *__restrict__ VS, float *__restrict__ part,
-                                                              int NS) {
+__global__ __launch_bounds__(kAttnT) void attend_decode_kernel(const float *__restrict__ qkv, int64_t ld,
+                                                               const int *__restrict__ state, int n_head, int n_kv,
+                                                               int n_layer, int layer, int max_t,
+                                                               const float2 *__restrict__ rope,
+                                                               int8_t *__restrict__ K8, int8_t *__restrict__ V8,
+                                                               float *__restrict__ KS, float *__restrict__ VS,
+                                                               float *__restrict__ out, int64_t ldo) {
     __shared__ __align__(16) float q[HD];
-    __shared__ __align__(16) int8_t vrow[kSplit][HD];
-    __shared__ float wv[kSplit], red[2], vred[2][HD];
-    const int h = blockIdx.x, b = blockIdx.y, j = blockIdx.z, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int npos = state[0] + 1;
-    float *P = part + (((int64_t)b * n_head + h) * NS + j) * kPart;
-    const int s0 = j * kSplit;
-    if (s0 >= npos) {  // an empty split (uniform over the workgroup)
-        if (tid < kPart) P[tid] = tid == 0 ? -INFINITY : 0.0f;
-        return;
-    }
-    const int cnt = min(kSplit, npos - s0);
-    const bool valid = tid < cnt;
-    const int kvh = h / (n_head / n_kv);
-    const int64_t sl = (((int64_t)b * n_layer + layer) * max_t + s0 + (valid ? tid : 0)) * n_kv + kvh;
-    int4 kr[HD / 16], vr[HD / 16];
+    __shared__ __align__(16) int8_t knew[HD], vnew[HD];
+    __shared__ float snew[2], red[kAttnT / 64], s_qsum;
+    __shared__ float wts[kMaxT];                  // scores, then e * vs
+    __shared__ __align__(16) float vpart[kVG][HD + 4];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int pos = state[0], npos = pos + 1;
+    const int grp = n_head / n_kv, kvh = h / grp;
+    const int64_t slot0 = ((int64_t)b * n_layer + layer) * max_t;
+    const int4 *K4 = reinterpret_cast<const int4 *>(K8);
+    const int4 *V4 = reinterpret_cast<const int4 *>(V8);
+    // every load of the cache up front (position pos: a row never used)
+    int4 kr[kKPT][HD / 16];
+    float ksc[kKPT], vsc[kKPT];
 #pragma unroll
-    for (int i = 0; i < HD / 16; i++) {
-        kr[i] = reinterpret_cast<const int4 *>(K8 + sl * HD)[i];
-        vr[i] = reinterpret_cast<const int4 *>(V8 + sl * HD)[i];
-    }
-    const float ks = KS[sl], vs = VS[sl];
-    if (tid < HD) q[tid] = qkv[(int64_t)b * ld + h * HD + tid];
-    if (valid) {
+    for (int k = 0; k < kKPT; k++) {
+        const int p = tid + k * kAttnT;
+        if (p < npos) {
+            const int64_t sl = (slot0 + p) * n_kv + kvh;
 #pragma unroll
-        for (int i = 0; i < HD / 16; i++) reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
-    }
-    __syncthreads();
-    float d = 0.0f;
-#pragma unroll
-    for (int i = 0; i < HD / 16; i++) {
-        const uint32_t kw[4] = {(uint32_t)kr[i].x, (uint32_t)kr[i].y, (uint32_t)kr[i].z, (uint32_t)kr[i].w};
-        const float4 *q4 = reinterpret_cast<const float4 *>(q + 16 * i);
-#pragma unroll
-        for (int e4 = 0; e4 < 4; e4++) {
-            const float4 qv = q4[e4];
-            d = fmaf(qv.x, (float)(int8_t)(kw[e4] & 255u), d);
-            d = fmaf(qv.y, (float)(int8_t)((kw[e4] >> 8) & 255u), d);
-            d = fmaf(qv.z, (float)(int8_t)((kw[e4] >> 16) & 255u), d);
-            d = fmaf(qv.w, (float)(int8_t)(kw[e4] >> 24), d);
+            for (int i = 0; i < HD / 16; i++) kr[k][i] = K4[sl * (HD / 16) + i];
+            ksc[k] = KS[sl];
+            vsc[k] = VS[sl];
         }
     }
-    const float score = valid ? d * ks * (1.0f / sqrtf((float)HD)) : -INFINITY;
-    float m = wave_max(score);
-    if (lane == 0) red[w] = m;
-    __syncthreads();
-    m = fmaxf(red[0], red[1]);
-    const float e = valid ? expf(score - m) : 0.0f;
-    wv[tid] = e * vs;
-    float t = wave_sum(e);
-    __syncthreads();
-    if (lane == 0) red[w] = t;
-    __syncthreads();
-    t = red[0] + red[1];
-    // values: wave w takes positions w, w + 2, ..; lane = dim
-    float acc = 0.0f;
-    int sp = w;
-    for (; sp + 14 < cnt; sp += 16) {
-        float pw[8], vv[8];
+    const int g = tid >> 2, c = tid & 3;
+    int4 vr[kVPT];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            pw[u] = wv[sp + 2 * u];
-            vv[u] = (float)vrow[sp + 2 * u][lane];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) acc = fmaf(pw[u], vv[u], acc);
+    for (int i = 0; i < kVPT; i++) {
+        const int p = g + i * kVG;
+        if (p < npos) vr[i] = V4[((slot0 + p) * n_kv + kvh) * (HD / 16) + c];
     }
-    for (; sp < cnt; sp += 2) acc = fmaf(wv[sp], (float)vrow[sp][lane], acc);
-    vred[w][lane] = acc;
-    __syncthreads();
-    if (tid < HD) P[2 + tid] = vred[0][tid] + vred[1][tid];
-    if (tid == 0) {
-        P[0] = m;
-        P[1] = t;
-    }
-}
-
-// The splits of (head blockIdx.x, sequence blockIdx.y) into the output:
-// out = sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j - M), splits in order.
-// Up to kMaxSplits splits, all loaded before use.
-constexpr int kMaxSplits = 16;
-__global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int NS, int n_head,
-                                                            const int *__restrict__ state, float *__restrict__ out,
-                                                            int64_t ldo) {
-    const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x;
-    const int ns = min(NS, (state[0] + 1 + kSplit - 1) / kSplit);
-    const float *P = part + ((int64_t)b * n_head + h) * NS * kPart;
-    float mj[kMaxSplits], tj[kMaxSplits], aj[kMaxSplits];
-#pragma unroll
-    for (int j = 0; j < kMaxSplits; j++) {
-        const bool ok = j < ns;
-        mj[j] = ok ? P[j * kPart] : -INFINITY;
-        tj[j] = ok ? P[j * kPart + 1] : 0.0f;
-        aj[j] = ok ? P[j * kPart + 2 + dd] : 0.0f;
-    }
-    float M = mj[0];
-#pragma unroll
-    for (int j = 1; j < kMaxSplits; j++) M = fmaxf(M, mj[j]);
-    float T = 0.0f, acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxSplits; j++) {
-        if (j < ns) {
-            const float f = expf(mj[j] - M);
-            T = fmaf(tj[j], f, T);
-            acc = fmaf(aj[j], f, acc);
+    // RoPE: wave 0 rotates the query; wave 1 the new key, then quantizes the
+    // new key and value (rotation of pair (2i, 2i + 1), i = d / 2:
+    // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c))
+    const float *r = qkv + (int64_t)b * ld;
+    if (w < 2) {
+        const int d = lane;
+        const float2 csn = rope[pos * (HD / 2) + (d >> 1)];
+        const float cs = csn.x, sn = csn.y;
+        const float v = r[(w == 0 ? h : n_head + kvh) * HD + d], pv = __shfl_xor(v, 1);
+        const float rot = (d & 1) ? pv * sn + v * cs : v * cs - pv * sn;
+        if (w == 0) {
+            q[d] = rot;
+            const float qs = wave_sum(rot);
+            if (d == 0) s_qsum = qs;
+        } else {
+            const int64_t sn_ = (slot0 + pos) * n_kv + kvh;
+            for (int kv = 0; kv < 2; kv++) {
+                const float x = kv == 0 ? rot : r[(n_head + n_kv + kvh) * HD + d];
+                const float m = wave_max(fabsf(x));
+                float sc = m / 127.0f;
+                if (sc == 0.0f) sc = 1.0f;
+                const float inv = 1.0f / sc;
+                const int8_t code = (int8_t)llmq_to_int(roundf(x * inv));
+                (kv == 0 ? knew : vnew)[d] = code;
+                if (d == 0) snew[kv] = sc;
+                if (h % grp == 0) {  // one writer per key / value head
+                    (kv == 0 ? K8 : V8)[sn_ * HD + d] = code;
+                    if (d == 0) (kv == 0 ? KS : VS)[sn_] = sc;
+                }
+            }
         }
     }
-    out[(int64_t)b * ldo + h * HD + dd] = acc / T;
+    __syncthreads();
+    // scores
+    const float q128 = 128.0f * s_qsum;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kKPT; k++) {
+        const int p = tid + k * kAttnT;
+        if (p < npos) {
+            const bool nw = p == pos;
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < HD / 16; i++) {
+                const int4 k4 = nw ? reinterpret_cast<const int4 *>(knew)[i] : kr[k][i];
+                const uint32_t kw[4] = {(uint32_t)k4.x ^ 0x80808080u, (uint32_t)k4.y ^ 0x80808080u,
+                                        (uint32_t)k4.z ^ 0x80808080u, (uint32_t)k4.w ^ 0x80808080u};
+                const float4 *q4 = reinterpret_cast<const float4 *>(q + 16 * i);
+#pragma unroll
+                for (int e4 = 0; e4 < 4; e4++) {
+                    const float4 qv = q4[e4];
+                    d = fmaf(qv.x, (float)(kw[e4] & 255u), d);
+                    d = fmaf(qv.y, (float)((kw[e4] >> 8) & 255u), d);
+                    d = fmaf(qv.z, (float)((kw[e4] >> 16) & 255u), d);
+                    d = fmaf(qv.w, (float)(kw[e4] >> 24), d);
+                }
+            }
+            const float s = (d - q128) * (nw ? snew[0] : ksc[k]) * (1.0f / sqrtf((float)HD));
+            wts[p] = s;
+            mx = fmaxf(mx, s);
+        }
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int i = 1; i < kAttnT / 64; i++) mx = fmaxf(mx, red[i]);
+    float tsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kKPT; k++) {
+        const int p = tid + k * kAttnT;
+        if (p < npos) {
+            const float e = expf(wts[p] - mx);
+            wts[p] = e * (p == pos ? snew[1] : vsc[k]);
+            tsum += e;
+        }
+    }
+    tsum = wave_sum(tsum);
+    __syncthreads();  // every max read before red is reused
+    if (lane == 0) red[w] = tsum;
+    __syncthreads();
+    tsum = red[0];
+#pragma unroll
+    for (int i = 1; i < kAttnT / 64; i++) tsum += red[i];
+    // values: dims 16c..16c+15 over positions g, g + kVG, ..
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kVPT; i++) {
+        const int p = g + i * kVG;
+        if (p < npos) {
+            const int4 v4 = p == pos ? reinterpret_cast<const int4 *>(vnew)[c] : vr[i];
+            const uint32_t vw[4] = {(uint32_t)v4.x, (uint32_t)v4.y, (uint32_t)v4.z, (uint32_t)v4.w};
+            const float wp = wts[p];
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[e] = fmaf(wp, (float)(int8_t)((vw[e >> 2] >> (8 * (e & 3))) & 255u), acc[e]);
+        }
+    }
+#pragma unroll
+    for (int e4 = 0; e4 < 4; e4++)
+        *reinterpret_cast<float4 *>(&vpart[g][16 * c + 4 * e4]) =
+            make_float4(acc[4 * e4], acc[4 * e4 + 1], acc[4 * e4 + 2], acc[4 * e4 + 3]);
+    __syncthreads();
+    // dim d = tid % 64, group slice tid / 64: 16 groups each, then the 8 slices
+    {
+        const int d = tid & 63, sl = tid >> 6;
+        float v = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kVG / (kAttnT / 64); i++) v += vpart[sl * (kVG / (kAttnT / 64)) + i][d];
+        __syncthreads();
+        vpart[sl][d] = v;
+        __syncthreads();
+        if (tid < HD) {
+            float o = vpart[0][tid];
+#pragma unroll
+            for (int i = 1; i < kAttnT / 64; i++) o += vpart[i][tid];
+            out[(int64_t)b * ldo + h * HD + tid] = o / tsum;
+        }
+    }
 }
 
 // h[r][i] = silu(g) * u with g = gu[r][i], u = gu[r][F + i].
@@ -335,7 +390,8 @@ struct llmq_llama {
     float *ks = nullptr, *vs = nullptr;
     // activations for up to `rows` tokens
     int rows = 0;
-    float *apart = nullptr;  // decode attention split results
+    ArgmaxPart *hparts = nullptr;  // head argmax partials, batch x gguf_head16_parts
+    float2 *rope = nullptr;        // (cos, sin) of position p, pair i at [p * head_dim / 2 + i]
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *hh = nullptr,
           *logits = nullptr;
     int64_t *tokens = nullptr, *next = nullptr, *gen = nullptr;
@@ -416,17 +472,14 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
     const int QC = qkv_cols(c);
     for (int l = 0; l < c.n_layer; l++) {
         RC(norm_linear(m, gain(m, l, 0), m->wqkv[l], R, m->qkv, QC, 0));
-        hipLaunchKernelGGL(rope_store_kernel, dim3(c.n_head + c.n_kv, R), dim3(64), 0, ctx->stream, m->qkv,
-                           (int64_t)QC, T, seq0, pos0, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, c.theta,
-                           m->k8, m->v8, m->ks, m->vs);
-        if (state) {
-            const int NS = (c.max_t + kSplit - 1) / kSplit;
-            hipLaunchKernelGGL(attend_split_kernel, dim3(c.n_head, R, NS), dim3(kSplit), 0, ctx->stream, m->qkv,
-                               (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->k8, m->v8, m->ks, m->vs,
-                               m->apart, NS);
-            hipLaunchKernelGGL(attend_combine_kernel, dim3(c.n_head, R), dim3(HD), 0, ctx->stream, m->apart, NS,
-                               c.n_head, state, m->att, (int64_t)c.dim);
+        if (state) {  // RoPE, the cache store and attention in one launch
+            hipLaunchKernelGGL(attend_decode_kernel, dim3(c.n_head, R), dim3(kAttnT), 0, ctx->stream, m->qkv,
+                               (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope, m->k8, m->v8,
+                               m->ks, m->vs, m->att, (int64_t)c.dim);
         } else {
+            hipLaunchKernelGGL(rope_store_kernel, dim3(c.n_head + c.n_kv, R), dim3(64), 0, ctx->stream, m->qkv,
+                               (int64_t)QC, T, seq0, pos0, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope,
+                               m->k8, m->v8, m->ks, m->vs);
             RC(launch_attend_prompt(ctx, m->k8, m->v8, m->ks, m->vs, seq0 * c.n_layer + l, c.max_t, c.n_head,
                                     c.n_kv, m->qkv, QC, pos0, T, m->att, c.dim));
         }
@@ -445,31 +498,41 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
 }
 
 // The output norm and head for nrows consecutive rows of m->x from row r0,
-// into m->logits.
-int llama_head(llmq_llama *m, int r0, int nrows) {
+// into m->logits; with parts, an int16 head also leaves its argmax partials
+// there (false is returned through *has_parts for a float head).
+int llama_head(llmq_llama *m, int r0, int nrows, ArgmaxPart *parts = nullptr, bool *has_parts = nullptr) {
     llmq_ctx *ctx = m->ctx;
     const llmq_llama_cfg &c = m->cfg;
     const float *g = m->norms + (size_t)2 * c.n_layer * c.dim;
     const float *x = m->x + (int64_t)r0 * c.dim;
+    if (has_parts) *has_parts = false;
     // the int16 head normalizes the rows it quantizes
-    if (gguf_has_i16(m->head)) return launch_gguf_head16(ctx, m->head, x, m->logits, nrows, g, c.eps);
+    if (gguf_has_i16(m->head)) {
+        if (has_parts) *has_parts = parts != nullptr;
+        return launch_gguf_head16(ctx, m->head, x, m->logits, nrows, g, c.eps, parts,
+                                  parts ? nrows * gguf_head16_parts(m->head) : 0);
+    }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, ctx->stream, x, (int64_t)c.dim, g, m->xn,
                        (int64_t)c.dim, c.dim, c.eps);
     return linear(m, m->head, m->xn, c.dim, nrows, m->logits, c.vocab, 0);
 }
 
-// One decode step of every sequence: embed the previous picks, the layers,
-// the head, the picks and the position and step advance.
+// One decode step of every sequence from the embedded picks in m->x: the
+// layers, the head, the picks with the position and step advance, and the
+// picks' embeddings for the next step.
 int llama_step(llmq_llama *m, int B) {
     llmq_ctx *ctx = m->ctx;
     const llmq_llama_cfg &c = m->cfg;
-    RC(launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim));
     RC(llama_layers(m, B, 1, 0, 0, m->state));
-    RC(llama_head(m, 0, B));
+    bool parts = false;
+    RC(llama_head(m, 0, B, m->hparts, &parts));
+    if (parts)
+        return launch_gguf_pick_embed(ctx, m->embd, m->hparts, gguf_head16_parts(m->head), B, m->state, m->next,
+                                      m->gen, m->x, c.dim);
     hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(kArgNT), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab, B,
                        0, m->state, 1, m->next, m->gen);
     LLMQ_HIP(hipGetLastError());
-    return LLMQ_OK;
+    return launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim);
 }
 
 // Prefill of sequence seq: T tokens (host) at positions pos0.., then its
@@ -501,7 +564,7 @@ int llmq_llama_free(llmq_llama *m) {
     for (auto *w : m->wo) llmq_mat_free(w);
     for (auto *w : m->wgu) llmq_mat_free(w);
     for (auto *w : m->wdown) llmq_mat_free(w);
-    void *bufs[] = {m->apart, m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
+    void *bufs[] = {m->hparts, m->rope, m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
                     m->tokens, m->next, m->gen, m->state};
     for (void *p : bufs) hipFree(p);
     delete m;
@@ -515,7 +578,7 @@ int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *cons
                      c.head_dim == HD && c.n_head * c.head_dim == c.dim && c.ffn > 0 && c.vocab > 0 &&
                      c.max_t > 0 && c.batch > 0,
                  "llama_create: unsupported shape (head_dim must be 64, n_head * head_dim == dim)");
-    LLMQ_REQUIRE(c.max_t <= kSplit * kMaxSplits, "llama_create: max_t %d beyond %d", c.max_t, kSplit * kMaxSplits);
+    LLMQ_REQUIRE(c.max_t <= kMaxT, "llama_create: max_t %d beyond %d", c.max_t, kMaxT);
     for (int ty : {c.layer_type, c.head_type, c.embd_type})
         LLMQ_REQUIRE(gguf_is_supported(ty), "llama_create: ggml type %d is not a supported block format", ty);
     llmq_llama *m = new llmq_llama();
@@ -579,9 +642,22 @@ int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *cons
             hipMemset(m->ks, 0, slots * 4) != hipSuccess || hipMemset(m->vs, 0, slots * 4) != hipSuccess)
             GO(llmq_set_error(LLMQ_EHIP, "llama: cache clear"));
         GO(ensure_rows(m, c.batch));
-        {   // decode attention partials: batch x heads x splits
-            const size_t np = (size_t)c.batch * c.n_head * ((c.max_t + kSplit - 1) / kSplit) * kPart;
-            if (hipMalloc(&m->apart, np * 4) != hipSuccess) GO(llmq_set_error(LLMQ_ENOMEM, "llama: attention partials"));
+        if (gguf_has_i16(m->head) &&
+            hipMalloc(&m->hparts, sizeof(ArgmaxPart) * c.batch * gguf_head16_parts(m->head)) != hipSuccess)
+            GO(llmq_set_error(LLMQ_ENOMEM, "llama: head partials"));
+        {   // RoPE: angle pos * theta^(-2i / head_dim) (both in float), cos and sin rounded from double
+            std::vector<float> tab((size_t)c.max_t * HD);
+            for (int p = 0; p < c.max_t; p++)
+                for (int i = 0; i < HD / 2; i++) {
+                    const float freq = powf(c.theta, -(float)(2 * i) / (float)HD);
+                    const double ang = (double)((float)p * freq);
+                    tab[((size_t)p * (HD / 2) + i) * 2] = (float)cos(ang);
+                    tab[((size_t)p * (HD / 2) + i) * 2 + 1] = (float)sin(ang);
+                }
+            if (hipMalloc(&m->rope, tab.size() * 4) != hipSuccess)
+                GO(llmq_set_error(LLMQ_ENOMEM, "llama: RoPE table"));
+            if (hipMemcpy(m->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+                GO(llmq_set_error(LLMQ_EHIP, "llama: RoPE table copy"));
         }
     }
 #undef GO
@@ -657,6 +733,7 @@ int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int B, int n_prom
     LLMQ_HIP(hipEventRecord(e1, ctx->stream));
     const int init_state[4] = {n_prompt, 1, 0, 0};  // position of the first pick, gen row of the next
     LLMQ_HIP(hipMemcpyAsync(m->state, init_state, sizeof(init_state), hipMemcpyHostToDevice, ctx->stream));
+    RC(launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim));  // the first picks, embedded
     for (int i = 1; i < steps; i++) {
         if (use_graph)
             LLMQ_HIP(hipGraphLaunch(m->step_graph, ctx->stream));

@@ -242,10 +242,16 @@ int gguf_num_parts(const llmq_mat *w);
 // One-token GGUF GEMV (gguf1.hip); with rms_g the row is RMS-normalized
 // (times the gain rms_g) before the product; with swiglu, x holds 2K floats
 // [gate | up] and the row is silu(gate) * up; with ln_w the row goes through
-// LayerNorm (eps 1e-5, weight ln_w, bias ln_b) first.
+// LayerNorm (eps 1e-5, weight ln_w, bias ln_b) first.  With apart, x is
+// not read: the row is the combination of decode attention splits (64-dim
+// heads, ns_max splits of asplit positions a head, position astate[0];
+// llama.hip's attend_split_kernel layout), which gguf_gemv_attn_ok(w,
+// ns_max) says the kernel can take.
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
                      ArgmaxPart *amax, int amax_cap, const float *rms_g = nullptr, float rms_eps = 0.0f,
-                     int swiglu = 0, const float *ln_w = nullptr, const float *ln_b = nullptr);
+                     int swiglu = 0, const float *ln_w = nullptr, const float *ln_b = nullptr,
+                     const float *apart = nullptr, const int *astate = nullptr, int asplit = 0, int ans_max = 0);
+bool gguf_gemv_attn_ok(const llmq_mat *w, int ns_max);
 int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
 int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *rows, int n, float *dst, int64_t ldd);
 // Greedy pick of each of B sequences from a head's argmax partials (nparts

@@ -46,7 +46,16 @@ struct G1Args {
     float rms_eps;
     int swiglu;          // x holds [gate | up] of 2K floats: the row is silu(gate) * up
     const float *ln_w, *ln_b;  // optional LayerNorm (eps 1e-5) of the row first
+    const float *apart;        // attention splits to combine into the row (AC kernels)
+    const int *astate;         // decode position: astate[0] + 1 positions
+    int asplit, ans_max;       // positions a split covers, splits a head in apart
 };
+
+// Attention splits (llama.hip's attend_split_kernel): per 64-dim head,
+// ans_max records of kAPart floats (m, t, 2 unused, 64 partial sums).
+constexpr int kAPart = 68;
+constexpr int kACMax = 8;  // splits an AC kernel combines
+constexpr int kACUnits = 2;  // float4 row units a thread combines (K <= 2 * 4 * threads)
 
 // silu(g) * u per lane of two activation vectors (llama.hip's swiglu).
 __device__ __forceinline__ uint4 swiglu4(uint4 g, uint4 u) {
@@ -182,7 +191,7 @@ __device__ __forceinline__ uint32_t spread4(uint32_t f) {
     }
 }
 
-template <int TYPE, int NW, int STEPS, int WIN>
+template <int TYPE, int NW, int STEPS, int WIN, bool AC>
 __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     using T = T1<TYPE>;
     using St = Stage<TYPE, STEPS>;
@@ -216,11 +225,57 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     constexpr int UPT = 4;  // up to 16 KiB of activations per round of 1024 threads
     const auto rx = make_rsrc(a.x, (uint32_t)K * (a.swiglu ? 8u : 4u));
     uint4 xv[UPT], xu[UPT];
+    if constexpr (AC) {
+        // The row is the attention output: per head h = u / 16 and dims
+        // 4 (u % 16).., out = sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j -
+        // M) over the ns valid splits, in order (attend_combine_kernel's
+        // arithmetic).
+        const int ns = min(a.ans_max, (a.astate[0] + a.asplit) / a.asplit);
+        const auto rp = make_rsrc(a.apart, (uint32_t)(K / 64) * (uint32_t)a.ans_max * kAPart * 4u);
+        float2 mt[kACUnits][kACMax];
+        uint4 av[kACUnits][kACMax];
 #pragma unroll
-    for (int i = 0; i < UPT; i++) {
-        const uint32_t u = (uint32_t)(tid + NT * i);
-        xv[i] = bload16(rx, u < (uint32_t)nunits ? u * 16u : kOOB);
-        if (a.swiglu) xu[i] = bload16(rx, u < (uint32_t)nunits ? (u + (uint32_t)nunits) * 16u : kOOB);
+        for (int i = 0; i < kACUnits; i++) {
+            const int u = tid + NT * i;
+            const bool ok = u < nunits;
+            const uint32_t base = (uint32_t)((u >> 4) * a.ans_max) * kAPart * 4u;
+#pragma unroll
+            for (int jj = 0; jj < kACMax; jj++) {
+                const bool lj = ok && jj < ns;
+                const uint2 w2 = bload8(rp, lj ? base + (uint32_t)jj * kAPart * 4u : kOOB);
+                mt[i][jj] = make_float2(__uint_as_float(w2.x), __uint_as_float(w2.y));
+                av[i][jj] = bload16(rp, lj ? base + (uint32_t)jj * kAPart * 4u + 16u + 16u * (uint32_t)(u & 15) : kOOB);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < UPT; i++) xv[i] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int i = 0; i < kACUnits && i < UPT; i++) {
+            float M = ns > 0 ? mt[i][0].x : -INFINITY;
+#pragma unroll
+            for (int jj = 1; jj < kACMax; jj++) M = fmaxf(M, jj < ns ? mt[i][jj].x : -INFINITY);
+            float T = 0.0f, o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < kACMax; jj++) {
+                if (jj < ns) {
+                    const float f = expf(mt[i][jj].x - M);
+                    T = fmaf(mt[i][jj].y, f, T);
+                    o0 = fmaf(__uint_as_float(av[i][jj].x), f, o0);
+                    o1 = fmaf(__uint_as_float(av[i][jj].y), f, o1);
+                    o2 = fmaf(__uint_as_float(av[i][jj].z), f, o2);
+                    o3 = fmaf(__uint_as_float(av[i][jj].w), f, o3);
+                }
+            }
+            xv[i] = make_uint4(__float_as_uint(o0 / T), __float_as_uint(o1 / T), __float_as_uint(o2 / T),
+                               __float_as_uint(o3 / T));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const uint32_t u = (uint32_t)(tid + NT * i);
+            xv[i] = bload16(rx, u < (uint32_t)nunits ? u * 16u : kOOB);
+            if (a.swiglu) xu[i] = bload16(rx, u < (uint32_t)nunits ? (u + (uint32_t)nunits) * 16u : kOOB);
+        }
     }
     // Global chunk indices of the wave's first and last valid chunks.
     const int gE = g0 + max(ns, 1) - 1;
@@ -581,9 +636,9 @@ size_t lds_bytes(const llmq_mat *w, const Plan &p) {
     return (size_t)w->k * 4 + (size_t)((w->k / 16 + 3) & ~3) * 4 + (size_t)p.tmax * p.nw * 64 * 4;
 }
 
-template <int TYPE, int NW, int STEPS, int WIN>
+template <int TYPE, int NW, int STEPS, int WIN, bool AC = false>
 int launch_w(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
-    auto kern = gguf1_kernel<TYPE, NW, STEPS, WIN>;
+    auto kern = gguf1_kernel<TYPE, NW, STEPS, WIN, AC>;
     hipFuncAttributes fa{};
     LLMQ_HIP(hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(kern)));
     if (fa.sharedSizeBytes + lds > ctx->prop.sharedMemPerBlock)
@@ -610,6 +665,10 @@ int launch_t(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
 template <int TYPE>
 int launch_type(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
     if (p.nw == 4) {
+        if (a.apart) {  // attention-combine staging: 4-wave plans only (gguf_gemv_attn_ok)
+            if (p.steps == 2) return launch_w<TYPE, 4, 2, 2, true>(ctx, a, p, lds);
+            if (p.steps == 4) return launch_w<TYPE, 4, 4, 4, true>(ctx, a, p, lds);
+        }
         if (p.steps == 2) return launch_t<TYPE, 4, 2>(ctx, a, p, lds);
         if (p.steps == 4) return launch_t<TYPE, 4, 4>(ctx, a, p, lds);
     } else {
@@ -633,11 +692,20 @@ int qm_cpg_shift(const llmq_mat *w) {
 
 int gguf_num_parts(const llmq_mat *w) { return make_plan(w).grid; }
 
+bool gguf_gemv_attn_ok(const llmq_mat *w, int ns_max) {
+    if (!w || !is_float_act(w) || w->k % 64 != 0 || ns_max < 1 || ns_max > kACMax) return false;
+    const Plan p = make_plan(w);
+    return p.nw == 4 && (p.steps == 2 || p.steps == 4) && w->k / 4 <= (int64_t)kACUnits * 4 * 64;
+}
+
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
                      ArgmaxPart *amax, int amax_cap, const float *rms_g, float rms_eps, int swiglu,
-                     const float *ln_w, const float *ln_b) {
+                     const float *ln_w, const float *ln_b, const float *apart, const int *astate, int asplit,
+                     int ans_max) {
     LLMQ_REQUIRE(w && is_float_act(w), "gguf_gemv: not a GGUF or float-activation QuantMatrix");
-    LLMQ_REQUIRE(x && out, "gguf_gemv: null pointer");
+    LLMQ_REQUIRE((x || apart) && out, "gguf_gemv: null pointer");
+    LLMQ_REQUIRE(!apart || (gguf_gemv_attn_ok(w, ans_max) && astate && asplit > 0 && !rms_g && !swiglu && !ln_w),
+                 "gguf_gemv: attention-split input not supported for %lld x %lld", (long long)w->n, (long long)w->k);
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemv: LLMQ_BIAS without a bias");
     LLMQ_REQUIRE(w->k % 16 == 0, "gguf_gemv: cols must be a multiple of 16");
     const Plan p = make_plan(w);
@@ -685,6 +753,10 @@ int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *ou
     a.ln_w = ln_w;
     a.ln_b = ln_b;
     a.swiglu = swiglu;
+    a.apart = apart;
+    a.astate = astate;
+    a.asplit = asplit;
+    a.ans_max = ans_max;
     int rc;
     switch (type) {
     case kQmFloat4: rc = launch_type<kQmFloat4>(ctx, a, p, lds); break;

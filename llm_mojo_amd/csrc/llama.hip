@@ -113,188 +113,199 @@ __global__ __launch_bounds__(64) void rope_store_kernel(float *__restrict__ qkv,
 }
 
 // One decode position for query head h = blockIdx.x of sequence b =
-// blockIdx.y at position pos = state[0], one workgroup for all positions:
-// RoPE of the query and of the new key, the new key and value quantized
-// into the cache (rope_store_kernel's arithmetic), then attend_float_one
-// (kvcache.mojo:113-150) over the int8 cache (QuantKV.score / add_value,
-// 344-370) of key / value head h / (n_head / n_kv):
-//   out = sum_p (e_p vs_p) v_p / sum_p e_p,  e_p = exp(score_p - max score)
-// (the reference divides each e by the total before the value products;
-// the float rounding differs, the sums are the same).  Position pos's key
-// and value come from LDS: its cache row is written by the first query head
-// of each key / value group and read by no workgroup of this launch.
+// blockIdx.y at position pos = state[0]: RoPE of the query and of the new
+// key, the new key and value quantized into the cache (rope_store_kernel's
+// arithmetic), then attend_float_one (kvcache.mojo:113-150) over the int8
+// cache (QuantKV.score / add_value, 344-370) of key / value head
+// h / (n_head / n_kv), split over blocks of kSplit positions (blockIdx.z),
+// a thread a position, so a head's positions are scored on several CUs.  A
+// split writes its maximum score m, its sum of e = exp(score - m) and its
+// partial sum_s (e * vs) * v (layout kPart: m, t, 2 unused, 64 sums); the
+// splits are combined by attend_combine_kernel or by the Wo GEMV as it
+// stages its input row (gguf1.hip): rescaled to the overall maximum, in split
+// order, divided by the overall sum.  (The reference divides each e by the
+// total before the value products; the float rounding differs, the sums are
+// the same.)
 //
-// Thread t scores positions t, t + kAttnT, ..; for the values, thread
-// (g = t / 4, c = t % 4) sums dims 16c..16c+15 over positions g, g + kVG,
-// .., and the kVG partial vectors are added in a fixed order.  Every key and
-// value load is issued at the start.  A score is q . (u - 128) over the
+// The split holding pos takes the new key and value from LDS: the cache row
+// at pos is written by the first query head of each key / value group and
+// read by no workgroup of this launch.  A score is q . (u - 128) over the
 // key's codes u = k + 128 (one byte conversion each): q . u - 128 sum(q).
-constexpr int kAttnT = 1024;
-constexpr int kMaxT = 2048;                 // positions a workgroup holds
-constexpr int kKPT = kMaxT / kAttnT;        // key rows a thread loads
-constexpr int kVG = kAttnT / 4;             // value row groups
-constexpr int kVPT = kMaxT / kVG;           // value rows a thread loads
+constexpr int kSplit = 256;
+constexpr int kPart = 4 + HD;  // floats of one split's result
+constexpr int kMaxSplits = 8;
+constexpr int kSW = kSplit / 64;  // waves of a split
 
-__global__ __launch_bounds__(kAttnT) void attend_decode_kernel(const float *__restrict__ qkv, int64_t ld,
-                                                               const int *__restrict__ state, int n_head, int n_kv,
-                                                               int n_layer, int layer, int max_t,
-                                                               const float2 *__restrict__ rope,
-                                                               int8_t *__restrict__ K8, int8_t *__restrict__ V8,
-                                                               float *__restrict__ KS, float *__restrict__ VS,
-                                                               float *__restrict__ out, int64_t ldo) {
+__global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__restrict__ qkv, int64_t ld,
+                                                              const int *__restrict__ state, int n_head, int n_kv,
+                                                              int n_layer, int layer, int max_t,
+                                                              const float2 *__restrict__ rope,
+                                                              int8_t *__restrict__ K8, int8_t *__restrict__ V8,
+                                                              float *__restrict__ KS, float *__restrict__ VS,
+                                                              float *__restrict__ part, int NS) {
     __shared__ __align__(16) float q[HD];
-    __shared__ __align__(16) int8_t knew[HD], vnew[HD];
-    __shared__ float snew[2], red[kAttnT / 64], s_qsum;
-    __shared__ float wts[kMaxT];                  // scores, then e * vs
-    __shared__ __align__(16) float vpart[kVG][HD + 4];
-    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ __align__(16) int8_t vrow[kSplit][HD];
+    __shared__ __align__(16) int8_t knew[HD];
+    __shared__ float wv[kSplit], red[kSW], vred[kSW][HD], snew[2], s_qsum;
+    const int h = blockIdx.x, b = blockIdx.y, j = blockIdx.z, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int pos = state[0], npos = pos + 1;
+    const int s0 = j * kSplit;
+    if (s0 >= npos) return;  // an empty split (uniform over the workgroup; never read)
+    const int cnt = min(kSplit, npos - s0);
+    const bool valid = tid < cnt;
+    const bool has_new = s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
+    const bool is_new = has_new && tid == cnt - 1;
     const int grp = n_head / n_kv, kvh = h / grp;
     const int64_t slot0 = ((int64_t)b * n_layer + layer) * max_t;
-    const int4 *K4 = reinterpret_cast<const int4 *>(K8);
-    const int4 *V4 = reinterpret_cast<const int4 *>(V8);
-    // every load of the cache up front (position pos: a row never used)
-    int4 kr[kKPT][HD / 16];
-    float ksc[kKPT], vsc[kKPT];
-#pragma unroll
-    for (int k = 0; k < kKPT; k++) {
-        const int p = tid + k * kAttnT;
-        if (p < npos) {
-            const int64_t sl = (slot0 + p) * n_kv + kvh;
-#pragma unroll
-            for (int i = 0; i < HD / 16; i++) kr[k][i] = K4[sl * (HD / 16) + i];
-            ksc[k] = KS[sl];
-            vsc[k] = VS[sl];
-        }
-    }
-    const int g = tid >> 2, c = tid & 3;
-    int4 vr[kVPT];
-#pragma unroll
-    for (int i = 0; i < kVPT; i++) {
-        const int p = g + i * kVG;
-        if (p < npos) vr[i] = V4[((slot0 + p) * n_kv + kvh) * (HD / 16) + c];
-    }
-    // RoPE: wave 0 rotates the query; wave 1 the new key, then quantizes the
-    // new key and value (rotation of pair (2i, 2i + 1), i = d / 2:
-    // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c))
     const float *r = qkv + (int64_t)b * ld;
-    if (w < 2) {
+    // the query (and new key / value) first, then this split's cache rows
+    float qv = 0.0f, kvx = 0.0f, vvx = 0.0f;
+    if (w == 0) qv = r[h * HD + lane];
+    if (w == 1 && has_new) {
+        kvx = r[(n_head + kvh) * HD + lane];
+        vvx = r[(n_head + n_kv + kvh) * HD + lane];
+    }
+    const int64_t sl = (slot0 + s0 + (valid ? tid : 0)) * n_kv + kvh;
+    int4 kr[HD / 16], vr[HD / 16];
+#pragma unroll
+    for (int i = 0; i < HD / 16; i++) {
+        kr[i] = reinterpret_cast<const int4 *>(K8 + sl * HD)[i];
+        vr[i] = reinterpret_cast<const int4 *>(V8 + sl * HD)[i];
+    }
+    float ks = KS[sl], vs = VS[sl];
+    if (valid && !is_new) {
+#pragma unroll
+        for (int i = 0; i < HD / 16; i++) reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
+    }
+    // RoPE of pair (2i, 2i + 1), i = d / 2, by the table's angle:
+    // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c); wave 0 the query, wave 1 the
+    // new key, which it quantizes with the new value
+    if (w == 0 || (w == 1 && has_new)) {
         const int d = lane;
         const float2 csn = rope[pos * (HD / 2) + (d >> 1)];
-        const float cs = csn.x, sn = csn.y;
-        const float v = r[(w == 0 ? h : n_head + kvh) * HD + d], pv = __shfl_xor(v, 1);
-        const float rot = (d & 1) ? pv * sn + v * cs : v * cs - pv * sn;
+        const float v = w == 0 ? qv : kvx, pv = __shfl_xor(v, 1);
+        const float rot = (d & 1) ? pv * csn.y + v * csn.x : v * csn.x - pv * csn.y;
         if (w == 0) {
             q[d] = rot;
             const float qs = wave_sum(rot);
             if (d == 0) s_qsum = qs;
         } else {
-            const int64_t sn_ = (slot0 + pos) * n_kv + kvh;
+            const int64_t sn = (slot0 + pos) * n_kv + kvh;
             for (int kv = 0; kv < 2; kv++) {
-                const float x = kv == 0 ? rot : r[(n_head + n_kv + kvh) * HD + d];
+                const float x = kv == 0 ? rot : vvx;
                 const float m = wave_max(fabsf(x));
                 float sc = m / 127.0f;
                 if (sc == 0.0f) sc = 1.0f;
                 const float inv = 1.0f / sc;
                 const int8_t code = (int8_t)llmq_to_int(roundf(x * inv));
-                (kv == 0 ? knew : vnew)[d] = code;
+                if (kv == 0)
+                    knew[d] = code;
+                else
+                    vrow[cnt - 1][d] = code;
                 if (d == 0) snew[kv] = sc;
                 if (h % grp == 0) {  // one writer per key / value head
-                    (kv == 0 ? K8 : V8)[sn_ * HD + d] = code;
-                    if (d == 0) (kv == 0 ? KS : VS)[sn_] = sc;
+                    (kv == 0 ? K8 : V8)[sn * HD + d] = code;
+                    if (d == 0) (kv == 0 ? KS : VS)[sn] = sc;
                 }
             }
         }
     }
     __syncthreads();
-    // scores
-    const float q128 = 128.0f * s_qsum;
-    float mx = -INFINITY;
+    if (is_new) {
+        ks = snew[0];
+        vs = snew[1];
+    }
+    float d = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kKPT; k++) {
-        const int p = tid + k * kAttnT;
-        if (p < npos) {
-            const bool nw = p == pos;
-            float d = 0.0f;
+    for (int i = 0; i < HD / 16; i++) {
+        const int4 k4 = is_new ? reinterpret_cast<const int4 *>(knew)[i] : kr[i];
+        const uint32_t kw[4] = {(uint32_t)k4.x ^ 0x80808080u, (uint32_t)k4.y ^ 0x80808080u,
+                                (uint32_t)k4.z ^ 0x80808080u, (uint32_t)k4.w ^ 0x80808080u};
+        const float4 *q4 = reinterpret_cast<const float4 *>(q + 16 * i);
 #pragma unroll
-            for (int i = 0; i < HD / 16; i++) {
-                const int4 k4 = nw ? reinterpret_cast<const int4 *>(knew)[i] : kr[k][i];
-                const uint32_t kw[4] = {(uint32_t)k4.x ^ 0x80808080u, (uint32_t)k4.y ^ 0x80808080u,
-                                        (uint32_t)k4.z ^ 0x80808080u, (uint32_t)k4.w ^ 0x80808080u};
-                const float4 *q4 = reinterpret_cast<const float4 *>(q + 16 * i);
-#pragma unroll
-                for (int e4 = 0; e4 < 4; e4++) {
-                    const float4 qv = q4[e4];
-                    d = fmaf(qv.x, (float)(kw[e4] & 255u), d);
-                    d = fmaf(qv.y, (float)((kw[e4] >> 8) & 255u), d);
-                    d = fmaf(qv.z, (float)((kw[e4] >> 16) & 255u), d);
-                    d = fmaf(qv.w, (float)(kw[e4] >> 24), d);
-                }
-            }
-            const float s = (d - q128) * (nw ? snew[0] : ksc[k]) * (1.0f / sqrtf((float)HD));
-            wts[p] = s;
-            mx = fmaxf(mx, s);
+        for (int e4 = 0; e4 < 4; e4++) {
+            const float4 qq = q4[e4];
+            d = fmaf(qq.x, (float)(kw[e4] & 255u), d);
+            d = fmaf(qq.y, (float)((kw[e4] >> 8) & 255u), d);
+            d = fmaf(qq.z, (float)((kw[e4] >> 16) & 255u), d);
+            d = fmaf(qq.w, (float)(kw[e4] >> 24), d);
         }
     }
-    mx = wave_max(mx);
-    if (lane == 0) red[w] = mx;
+    const float score = valid ? (d - 128.0f * s_qsum) * ks * (1.0f / sqrtf((float)HD)) : -INFINITY;
+    float m = wave_max(score);
+    if (lane == 0) red[w] = m;
     __syncthreads();
-    mx = red[0];
+    m = red[0];
 #pragma unroll
-    for (int i = 1; i < kAttnT / 64; i++) mx = fmaxf(mx, red[i]);
-    float tsum = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kKPT; k++) {
-        const int p = tid + k * kAttnT;
-        if (p < npos) {
-            const float e = expf(wts[p] - mx);
-            wts[p] = e * (p == pos ? snew[1] : vsc[k]);
-            tsum += e;
-        }
-    }
-    tsum = wave_sum(tsum);
-    __syncthreads();  // every max read before red is reused
-    if (lane == 0) red[w] = tsum;
+    for (int i = 1; i < kSW; i++) m = fmaxf(m, red[i]);
+    const float e = valid ? expf(score - m) : 0.0f;
+    wv[tid] = e * vs;
+    float t = wave_sum(e);
+    __syncthreads();  // every read of red done
+    if (lane == 0) red[w] = t;
     __syncthreads();
-    tsum = red[0];
+    t = red[0];
 #pragma unroll
-    for (int i = 1; i < kAttnT / 64; i++) tsum += red[i];
-    // values: dims 16c..16c+15 over positions g, g + kVG, ..
-    float acc[16];
+    for (int i = 1; i < kSW; i++) t += red[i];
+    // values: wave w takes positions w, w + kSW, ..; lane = dim
+    float acc = 0.0f;
+    int sp = w;
+    for (; sp + 7 * kSW < cnt; sp += 8 * kSW) {
+        float pw[8], vv[8];
 #pragma unroll
-    for (int e = 0; e < 16; e++) acc[e] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kVPT; i++) {
-        const int p = g + i * kVG;
-        if (p < npos) {
-            const int4 v4 = p == pos ? reinterpret_cast<const int4 *>(vnew)[c] : vr[i];
-            const uint32_t vw[4] = {(uint32_t)v4.x, (uint32_t)v4.y, (uint32_t)v4.z, (uint32_t)v4.w};
-            const float wp = wts[p];
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[e] = fmaf(wp, (float)(int8_t)((vw[e >> 2] >> (8 * (e & 3))) & 255u), acc[e]);
+        for (int u = 0; u < 8; u++) {
+            pw[u] = wv[sp + kSW * u];
+            vv[u] = (float)vrow[sp + kSW * u][lane];
         }
-    }
 #pragma unroll
-    for (int e4 = 0; e4 < 4; e4++)
-        *reinterpret_cast<float4 *>(&vpart[g][16 * c + 4 * e4]) =
-            make_float4(acc[4 * e4], acc[4 * e4 + 1], acc[4 * e4 + 2], acc[4 * e4 + 3]);
+        for (int u = 0; u < 8; u++) acc = fmaf(pw[u], vv[u], acc);
+    }
+    for (; sp < cnt; sp += kSW) acc = fmaf(wv[sp], (float)vrow[sp][lane], acc);
+    vred[w][lane] = acc;
     __syncthreads();
-    // dim d = tid % 64, group slice tid / 64: 16 groups each, then the 8 slices
-    {
-        const int d = tid & 63, sl = tid >> 6;
-        float v = 0.0f;
+    float *P = part + (((int64_t)b * n_head + h) * NS + j) * kPart;
+    if (tid < HD) {
+        float o = vred[0][tid];
 #pragma unroll
-        for (int i = 0; i < kVG / (kAttnT / 64); i++) v += vpart[sl * (kVG / (kAttnT / 64)) + i][d];
-        __syncthreads();
-        vpart[sl][d] = v;
-        __syncthreads();
-        if (tid < HD) {
-            float o = vpart[0][tid];
+        for (int i = 1; i < kSW; i++) o += vred[i][tid];
+        P[4 + tid] = o;
+    }
+    if (tid == 0) {
+        P[0] = m;
+        P[1] = t;
+    }
+}
+
+// The splits of (head blockIdx.x, sequence blockIdx.y) into the output:
+// out = sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j - M), splits in order
+// (the same arithmetic as the Wo GEMV's staging of them, gguf1.hip).
+__global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int NS, int n_head,
+                                                            const int *__restrict__ state, float *__restrict__ out,
+                                                            int64_t ldo) {
+    const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x;
+    const int ns = min(NS, (state[0] + kSplit) / kSplit);
+    const float *P = part + ((int64_t)b * n_head + h) * NS * kPart;
+    float mj[kMaxSplits], tj[kMaxSplits], aj[kMaxSplits];
 #pragma unroll
-            for (int i = 1; i < kAttnT / 64; i++) o += vpart[i][tid];
-            out[(int64_t)b * ldo + h * HD + tid] = o / tsum;
+    for (int j = 0; j < kMaxSplits; j++) {
+        const bool ok = j < ns;
+        mj[j] = ok ? P[j * kPart] : -INFINITY;
+        tj[j] = ok ? P[j * kPart + 1] : 0.0f;
+        aj[j] = ok ? P[j * kPart + 4 + dd] : 0.0f;
+    }
+    float M = mj[0];
+#pragma unroll
+    for (int j = 1; j < kMaxSplits; j++) M = fmaxf(M, mj[j]);
+    float T = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxSplits; j++) {
+        if (j < ns) {
+            const float f = expf(mj[j] - M);
+            T = fmaf(tj[j], f, T);
+            acc = fmaf(aj[j], f, acc);
         }
     }
+    out[(int64_t)b * ldo + h * HD + dd] = acc / T;
 }
 
 // h[r][i] = silu(g) * u with g = gu[r][i], u = gu[r][F + i].
@@ -391,6 +402,7 @@ struct llmq_llama {
     // activations for up to `rows` tokens
     int rows = 0;
     ArgmaxPart *hparts = nullptr;  // head argmax partials, batch x gguf_head16_parts
+    float *apart = nullptr;        // decode attention split results, batch x heads x splits x kPart
     float2 *rope = nullptr;        // (cos, sin) of position p, pair i at [p * head_dim / 2 + i]
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *hh = nullptr,
           *logits = nullptr;
@@ -472,18 +484,27 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
     const int QC = qkv_cols(c);
     for (int l = 0; l < c.n_layer; l++) {
         RC(norm_linear(m, gain(m, l, 0), m->wqkv[l], R, m->qkv, QC, 0));
-        if (state) {  // RoPE, the cache store and attention in one launch
-            hipLaunchKernelGGL(attend_decode_kernel, dim3(c.n_head, R), dim3(kAttnT), 0, ctx->stream, m->qkv,
+        if (state) {  // RoPE, the cache store and the attention splits in one launch
+            const int NS = (c.max_t + kSplit - 1) / kSplit;
+            hipLaunchKernelGGL(attend_split_kernel, dim3(c.n_head, R, NS), dim3(kSplit), 0, ctx->stream, m->qkv,
                                (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope, m->k8, m->v8,
-                               m->ks, m->vs, m->att, (int64_t)c.dim);
+                               m->ks, m->vs, m->apart, NS);
+            if (R == 1 && gguf_gemv_attn_ok(m->wo[l], NS)) {  // Wo combines the splits as it stages its row
+                RC(launch_gguf_gemv(ctx, m->wo[l], nullptr, m->x, nullptr, LLMQ_RESID, nullptr, 0, nullptr, 0.0f, 0,
+                                    nullptr, nullptr, m->apart, state, kSplit, NS));
+            } else {
+                hipLaunchKernelGGL(attend_combine_kernel, dim3(c.n_head, R), dim3(HD), 0, ctx->stream, m->apart, NS,
+                                   c.n_head, state, m->att, (int64_t)c.dim);
+                RC(linear(m, m->wo[l], m->att, c.dim, R, m->x, c.dim, LLMQ_RESID));
+            }
         } else {
             hipLaunchKernelGGL(rope_store_kernel, dim3(c.n_head + c.n_kv, R), dim3(64), 0, ctx->stream, m->qkv,
                                (int64_t)QC, T, seq0, pos0, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope,
                                m->k8, m->v8, m->ks, m->vs);
             RC(launch_attend_prompt(ctx, m->k8, m->v8, m->ks, m->vs, seq0 * c.n_layer + l, c.max_t, c.n_head,
                                     c.n_kv, m->qkv, QC, pos0, T, m->att, c.dim));
+            RC(linear(m, m->wo[l], m->att, c.dim, R, m->x, c.dim, LLMQ_RESID));
         }
-        RC(linear(m, m->wo[l], m->att, c.dim, R, m->x, c.dim, LLMQ_RESID));
         RC(norm_linear(m, gain(m, l, 1), m->wgu[l], R, m->gu, 2 * c.ffn, 0));
         if (R == 1) {  // the GEMV forms silu(gate) * up as it stages its row
             RC(launch_gguf_gemv(ctx, m->wdown[l], m->gu, m->x, nullptr, LLMQ_RESID, nullptr, 0, nullptr, 0.0f, 1));
@@ -564,7 +585,7 @@ int llmq_llama_free(llmq_llama *m) {
     for (auto *w : m->wo) llmq_mat_free(w);
     for (auto *w : m->wgu) llmq_mat_free(w);
     for (auto *w : m->wdown) llmq_mat_free(w);
-    void *bufs[] = {m->hparts, m->rope, m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
+    void *bufs[] = {m->hparts, m->apart, m->rope, m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
                     m->tokens, m->next, m->gen, m->state};
     for (void *p : bufs) hipFree(p);
     delete m;
@@ -578,7 +599,7 @@ int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *cons
                      c.head_dim == HD && c.n_head * c.head_dim == c.dim && c.ffn > 0 && c.vocab > 0 &&
                      c.max_t > 0 && c.batch > 0,
                  "llama_create: unsupported shape (head_dim must be 64, n_head * head_dim == dim)");
-    LLMQ_REQUIRE(c.max_t <= kMaxT, "llama_create: max_t %d beyond %d", c.max_t, kMaxT);
+    LLMQ_REQUIRE(c.max_t <= kSplit * kMaxSplits, "llama_create: max_t %d beyond %d", c.max_t, kSplit * kMaxSplits);
     for (int ty : {c.layer_type, c.head_type, c.embd_type})
         LLMQ_REQUIRE(gguf_is_supported(ty), "llama_create: ggml type %d is not a supported block format", ty);
     llmq_llama *m = new llmq_llama();
@@ -645,6 +666,9 @@ int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *cons
         if (gguf_has_i16(m->head) &&
             hipMalloc(&m->hparts, sizeof(ArgmaxPart) * c.batch * gguf_head16_parts(m->head)) != hipSuccess)
             GO(llmq_set_error(LLMQ_ENOMEM, "llama: head partials"));
+        if (hipMalloc(&m->apart, sizeof(float) * c.batch * c.n_head * ((c.max_t + kSplit - 1) / kSplit) * kPart) !=
+            hipSuccess)
+            GO(llmq_set_error(LLMQ_ENOMEM, "llama: attention partials"));
         {   // RoPE: angle pos * theta^(-2i / head_dim) (both in float), cos and sin rounded from double
             std::vector<float> tab((size_t)c.max_t * HD);
             for (int p = 0; p < c.max_t; p++)

@@ -230,7 +230,8 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
         // 4 (u % 16).., out = sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j -
         // M) over the ns valid splits, in order (attend_combine_kernel's
         // arithmetic).
-        const int ns = min(a.ans_max, (a.astate[0] + a.asplit) / a.asplit);
+        // (every split of the head is loaded, used or not: the loads go out
+        // with the position's, which they do not wait for)
         const auto rp = make_rsrc(a.apart, (uint32_t)(K / 64) * (uint32_t)a.ans_max * kAPart * 4u);
         float2 mt[kACUnits][kACMax];
         uint4 av[kACUnits][kACMax];
@@ -241,12 +242,13 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
             const uint32_t base = (uint32_t)((u >> 4) * a.ans_max) * kAPart * 4u;
 #pragma unroll
             for (int jj = 0; jj < kACMax; jj++) {
-                const bool lj = ok && jj < ns;
+                const bool lj = ok && jj < a.ans_max;
                 const uint2 w2 = bload8(rp, lj ? base + (uint32_t)jj * kAPart * 4u : kOOB);
                 mt[i][jj] = make_float2(__uint_as_float(w2.x), __uint_as_float(w2.y));
                 av[i][jj] = bload16(rp, lj ? base + (uint32_t)jj * kAPart * 4u + 16u + 16u * (uint32_t)(u & 15) : kOOB);
             }
         }
+        const int ns = min(a.ans_max, (a.astate[0] + a.asplit) / a.asplit);
 #pragma unroll
         for (int i = 0; i < UPT; i++) xv[i] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll

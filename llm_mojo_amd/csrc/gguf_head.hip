@@ -150,24 +150,39 @@ __device__ __forceinline__ void q6k_pairs(const RawUnit<LLMQ_GGML_Q6_K> &w, int 
     }
 }
 
-// quantize_rows (kernels.mojo:400-416) of token t (after the optional
-// RMSNorm): s = max|h| / 32767 (1 if zero), codes round(h / s) as int16
-// pairs into xt, s into *sx.  COOP: the whole workgroup (me = thread),
-// else one wave (me = lane); the row stays in registers, RV float4 a thread.
+// quantize_rows (kernels.mojo:400-416) of a token's row (after the
+// optional RMSNorm): s = max|h| / 32767 (1 if zero), codes round(h / s) as
+// int16 pairs into xt, s into *sx.  COOP: the whole workgroup (me = thread),
+// else one wave (me = lane); the row stays in registers, RV float4 a thread
+// (load_token).
+template <int RV, bool G>
+struct TokenRow {
+    float4 v[RV], g[G ? RV : 1];  // the thread's part of the row (and of the RMSNorm gain, G)
+};
+
 template <int RV, bool COOP>
-__device__ __forceinline__ void quantize_token(const H16Args &a, int t, int me, uint32_t *xt, float *s_red,
-                                               float *sx_out) {
+__device__ __forceinline__ TokenRow<RV, COOP> load_token(const H16Args &a, int t, int me) {
     constexpr int NTH = COOP ? kNW * 64 : 64;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int n4 = a.C / 4;
     const float4 *h4 = reinterpret_cast<const float4 *>(a.h + (size_t)t * a.C);
     const float4 *g4 = reinterpret_cast<const float4 *>(a.rms_g);
-    float4 v[RV];
+    TokenRow<RV, COOP> row;
 #pragma unroll
     for (int k = 0; k < RV; k++) {
         const int i = me + k * NTH;
-        v[k] = i < n4 ? h4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        row.v[k] = i < n4 ? h4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (COOP) row.g[k] = a.rms_g && i < n4 ? g4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+    return row;
+}
+
+template <int RV, bool COOP>
+__device__ __forceinline__ void quantize_token(const H16Args &a, TokenRow<RV, COOP> row, int me, uint32_t *xt,
+                                               float *s_red, float *sx_out) {
+    constexpr int NTH = COOP ? kNW * 64 : 64;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int n4 = a.C / 4;
+    float4 *v = row.v;
     if (a.rms_g) {
         float ss = 0.0f;
 #pragma unroll
@@ -189,7 +204,11 @@ __device__ __forceinline__ void quantize_token(const H16Args &a, int t, int me, 
         for (int k = 0; k < RV; k++) {
             const int i = me + k * NTH;
             if (i < n4) {
-                const float4 gg = g4[i];
+                float4 gg;
+                if constexpr (COOP)
+                    gg = row.g[k];
+                else
+                    gg = reinterpret_cast<const float4 *>(a.rms_g)[i];
                 v[k].x = (v[k].x * rn) * gg.x;
                 v[k].y = (v[k].y * rn) * gg.y;
                 v[k].z = (v[k].z * rn) * gg.z;
@@ -251,6 +270,12 @@ __global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
         return load_unit<TYPE>(a, tile < a.ntiles, tile, s % NU, r, q);
     };
     constexpr int PD = TM <= 2 ? 3 : 2;  // units in flight behind the one computed
+    constexpr int RVC = kMaxC / 4 / (kNW * 64);
+    // The first token's row goes out before the weights when the workgroup
+    // takes fewer tokens than it has waves (loads complete in issue order).
+    const bool coop = TM < kNW || nt < kNW;
+    TokenRow<RVC, true> first;
+    if constexpr (TM < kNW) first = load_token<RVC, true>(a, t0, tid);
     RawUnit<TYPE> ring[PD];
 #pragma unroll
     for (int k = 0; k < PD; k++) ring[k] = load_item(k);
@@ -258,10 +283,14 @@ __global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
     // Tokens: optional RMSNorm, then quantize_rows (kernels.mojo:400-416).
     // Fewer tokens than waves: the workgroup takes them one by one; else a
     // wave per token.
-    if (TM < kNW || nt < kNW) {
-        for (int t = 0; t < nt; t++) quantize_token<kMaxC / 4 / (kNW * 64), true>(a, t0 + t, tid, xq32 + (size_t)t * C2, s_red, &s_sx[t]);
+    if (coop) {
+        for (int t = 0; t < nt; t++)
+            quantize_token<RVC, true>(a, TM < kNW && t == 0 ? first : load_token<RVC, true>(a, t0 + t, tid), tid,
+                                      xq32 + (size_t)t * C2, s_red, &s_sx[t]);
     } else {
-        for (int t = wid; t < nt; t += kNW) quantize_token<kMaxC / 4 / 64, false>(a, t0 + t, lane, xq32 + (size_t)t * C2, s_red, &s_sx[t]);
+        for (int t = wid; t < nt; t += kNW)
+            quantize_token<kMaxC / 4 / 64, false>(a, load_token<kMaxC / 4 / 64, false>(a, t0 + t, lane), lane,
+                                                  xq32 + (size_t)t * C2, s_red, &s_sx[t]);
     }
     __syncthreads();
     float sx[TM];

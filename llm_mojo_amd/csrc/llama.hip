@@ -148,24 +148,19 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
     __shared__ __align__(16) int8_t knew[HD];
     __shared__ float wv[kSplit], red[kSW], vred[kSW][HD], snew[2], s_qsum;
     const int h = blockIdx.x, b = blockIdx.y, j = blockIdx.z, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int pos = state[0], npos = pos + 1;
     const int s0 = j * kSplit;
-    if (s0 >= npos) return;  // an empty split (uniform over the workgroup; never read)
-    const int cnt = min(kSplit, npos - s0);
-    const bool valid = tid < cnt;
-    const bool has_new = s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
-    const bool is_new = has_new && tid == cnt - 1;
     const int grp = n_head / n_kv, kvh = h / grp;
     const int64_t slot0 = ((int64_t)b * n_layer + layer) * max_t;
     const float *r = qkv + (int64_t)b * ld;
-    // the query (and new key / value) first, then this split's cache rows
+    // The query, new key and value and this split's cache rows go out
+    // together with the position, which none of their addresses needs.
     float qv = 0.0f, kvx = 0.0f, vvx = 0.0f;
     if (w == 0) qv = r[h * HD + lane];
-    if (w == 1 && has_new) {
+    if (w == 1) {
         kvx = r[(n_head + kvh) * HD + lane];
         vvx = r[(n_head + n_kv + kvh) * HD + lane];
     }
-    const int64_t sl = (slot0 + s0 + (valid ? tid : 0)) * n_kv + kvh;
+    const int64_t sl = (slot0 + min(s0 + tid, max_t - 1)) * n_kv + kvh;
     int4 kr[HD / 16], vr[HD / 16];
 #pragma unroll
     for (int i = 0; i < HD / 16; i++) {
@@ -173,6 +168,12 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
         vr[i] = reinterpret_cast<const int4 *>(V8 + sl * HD)[i];
     }
     float ks = KS[sl], vs = VS[sl];
+    const int pos = state[0], npos = pos + 1;
+    if (s0 >= npos) return;  // an empty split (uniform over the workgroup; never read)
+    const int cnt = min(kSplit, npos - s0);
+    const bool valid = tid < cnt;
+    const bool has_new = s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
+    const bool is_new = has_new && tid == cnt - 1;
     if (valid && !is_new) {
 #pragma unroll
         for (int i = 0; i < HD / 16; i++) reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];

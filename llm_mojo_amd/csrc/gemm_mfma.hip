@@ -319,10 +319,16 @@ __device__ __forceinline__ void compute_block(const Lds<BITS, MT> &L, int buf, i
         const int64_t b0 = *reinterpret_cast<const int64_t *>(&L.w0[buf][brow + 32 * s]);
         int64_t b1 = 0;
         if (BITS == 8) b1 = *reinterpret_cast<const int64_t *>(&L.w1[buf][brow + 32 * s]);
-        if (SEG32) {  // every sub-step is a segment: the products start from zero
+        if (SEG32) {  // every sub-step is a segment: the products start from zero, the
+                      // lowest-weight accumulator from the 128 * sum w term
+            const int w128 = 128 * L.wsum[buf][s][orow];
+            const v4i wv = {w128, w128, w128, w128};
 #pragma unroll
-            for (int j = 0; j < MT; j++) c.c0[j] = c.c1[j] = c.c2[j] = c.c3[j] = (v4i){};
-            c.wacc = 0;
+            for (int j = 0; j < MT; j++) {
+                c.c0[j] = c.c2[j] = (v4i){};
+                c.c1[j] = BITS == 4 ? wv : (v4i){};
+                c.c3[j] = BITS == 8 ? wv : (v4i){};
+            }
         }
 #pragma unroll
         for (int j = 0; j < MT; j++) {
@@ -338,10 +344,10 @@ __device__ __forceinline__ void compute_block(const Lds<BITS, MT> &L, int buf, i
                 c.c3[j] = mfma16(al, b0, c.c3[j]);
             }
         }
-        c.wacc += L.wsum[buf][s][orow];
+        if (!SEG32) c.wacc += L.wsum[buf][s][orow];
         if (SEG32 || (kb * KB + 32 * (s + 1)) % seg == 0) {  // end of a segment: tile_i16's flush
             const float sc = L.scale[buf][s][orow];
-            const int w128 = 128 * c.wacc;
+            const int w128 = SEG32 ? 0 : 128 * c.wacc;  // (SEG32: already in the accumulators)
 #pragma unroll
             for (int j = 0; j < MT; j++) {
 #pragma unroll

@@ -33,10 +33,12 @@
 // matrix cores; two LDS buffers alternate, one barrier per block.
 //
 // What bounds it: tile_i16's per-group float chain, per output and group
-// of 32 inputs a shift-add, an add, a convert and an fma (4 VALU against
-// 2 MFMA of 8192 products per 16 x 16 outputs), and the round trip of each
-// staged block (~1 us per block per workgroup at 476 tokens, measured with
-// per-workgroup timestamps).
+// of 32 inputs a shift-add, a convert and an fma (3 VALU against 2 MFMA of
+// 8192 products per 16 x 16 outputs; the 128 * sum w term starts the low
+// plane's accumulator), issued by two workgroups of four waves a CU: each
+// staged block takes ~1 us per workgroup at 476 tokens against ~0.35 us of
+// instructions (per-workgroup timestamps), and prefetching four blocks
+// ahead instead of two does not shorten it.
 //
 // Activations come from act_q16_kernel: LayerNorm (kernels.mojo:179-197) when
 // asked, then quantize_rows (kernels.mojo:400-416), one workgroup per token.

@@ -524,6 +524,32 @@ __device__ __forceinline__ int llmq_from_lane_plus32(int v) {
     return (int)r[1];
 }
 
+// Sum / max over the wave in every lane, without LDS: DPP within rows of 16
+// (quad swaps, half-row and row mirrors), then gfx950's row-pair and
+// half-wave swaps.  Every lane forms the same pairs, so all lanes hold the
+// same bits; the order is this butterfly's (for sums where the reference
+// fixes no order).
+__device__ __forceinline__ float llmq_wave_sum_all(float v) {
+    v = v + llmq_dppf<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = v + llmq_dppf<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = v + llmq_dppf<0x141>(v);  // row_half_mirror
+    v = v + llmq_dppf<0x140>(v);  // row_mirror
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+__device__ __forceinline__ float llmq_wave_max_all(float v) {
+    v = fmaxf(v, llmq_dppf<0xB1>(v));
+    v = fmaxf(v, llmq_dppf<0x4E>(v));
+    v = fmaxf(v, llmq_dppf<0x141>(v));
+    v = fmaxf(v, llmq_dppf<0x140>(v));
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
 // max over the wave, in every lane (order-free): DPP within rows of 16, then
 // the four rows' results.
 __device__ __forceinline__ float llmq_wave_max(float v) {

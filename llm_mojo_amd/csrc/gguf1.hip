@@ -362,8 +362,7 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
             ss = fmaf(v.z, v.z, ss);
             ss = fmaf(v.w, v.w, ss);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        ss = llmq_wave_sum_all(ss);
         if (lane == 0) s_red[wid] = ss;
         lds_barrier();
         ss = s_red[0];
@@ -388,8 +387,7 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
             const float4 v = reinterpret_cast<const float4 *>(xs)[u];
             sum += (v.x + v.y) + (v.z + v.w);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        sum = llmq_wave_sum_all(sum);
         if (lane == 0) s_red[wid] = sum;
         lds_barrier();
         sum = s_red[0];
@@ -402,8 +400,7 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
             const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
             sq += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+        sq = llmq_wave_sum_all(sq);
         if (lane == 0) s_red2[wid] = sq;
         lds_barrier();
         sq = s_red2[0];

@@ -192,7 +192,7 @@ __device__ __forceinline__ void quantize_token(const H16Args &a, TokenRow<RV, CO
             ss = fmaf(v[k].z, v[k].z, ss);
             ss = fmaf(v[k].w, v[k].w, ss);
         }
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        ss = llmq_wave_sum_all(ss);
         if (COOP) {
             if (lane == 0) s_red[wid] = ss;
             __syncthreads();
@@ -220,7 +220,7 @@ __device__ __forceinline__ void quantize_token(const H16Args &a, TokenRow<RV, CO
 #pragma unroll
     for (int k = 0; k < RV; k++)
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = llmq_wave_max_all(m);
     if (COOP) {
         if (lane == 0) s_red[wid] = m;
         __syncthreads();
@@ -369,8 +369,13 @@ __global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
                     float v[4];
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        v[j] = accf[t][j] + __shfl_xor(accf[t][j], 32);
-                        v[j] += __shfl_xor(v[j], 16);
+                        // lane ^ 32, then lane ^ 16: gfx950's half-wave and row-pair swaps
+                        const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(accf[t][j]),
+                                                                          __float_as_uint(accf[t][j]), false, false);
+                        v[j] = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+                        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j]),
+                                                                          false, false);
+                        v[j] = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
                         accf[t][j] = 0.0f;
                     }
                     const float lg = ((v[0] + v[2]) + (v[1] + v[3])) * sx[t];

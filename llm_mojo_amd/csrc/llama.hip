@@ -31,16 +31,8 @@ namespace {
 
 constexpr int HD = 64;  // head_dim
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return llmq_wave_sum_all(v); }
+__device__ __forceinline__ float wave_max(float v) { return llmq_wave_max_all(v); }
 // Sum / max over a 256-thread workgroup, waves added in order.
 __device__ __forceinline__ float block_sum(float v, float *red) {
     v = wave_sum(v);
@@ -92,7 +84,7 @@ __global__ __launch_bounds__(64) void rope_store_kernel(float *__restrict__ qkv,
     // rotation of pair (2i, 2i + 1), i = d / 2, by the table's angle
     const float2 cs = rope[pos * (HD / 2) + (d >> 1)];
     const float c = cs.x, s = cs.y;
-    const float v = src[d], p = __shfl_xor(v, 1);
+    const float v = src[d], p = llmq_dppf<0xB1>(v);  // lane d ^ 1
     // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
     const float rot = (d & 1) ? p * s + v * c : v * c - p * s;
     if (is_q) {
@@ -184,7 +176,7 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
     if (w == 0 || (w == 1 && has_new)) {
         const int d = lane;
         const float2 csn = rope[pos * (HD / 2) + (d >> 1)];
-        const float v = w == 0 ? qv : kvx, pv = __shfl_xor(v, 1);
+        const float v = w == 0 ? qv : kvx, pv = llmq_dppf<0xB1>(v);  // lane d ^ 1
         const float rot = (d & 1) ? pv * csn.y + v * csn.x : v * csn.x - pv * csn.y;
         if (w == 0) {
             q[d] = rot;

@@ -6,16 +6,8 @@
 
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
+// max over the wave (order-free, so exact in any pairing), without LDS
+__device__ __forceinline__ float wave_max(float v) { return llmq_wave_max_all(v); }
 
 // QuantKV.store (kvcache.mojo:333-342) for token t = blockIdx.y, head h =
 // blockIdx.x: per head s = max|x| / 127 (1 if zero), codes round(x / s).

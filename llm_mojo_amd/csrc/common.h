@@ -550,6 +550,21 @@ __device__ __forceinline__ float llmq_wave_max_all(float v) {
     return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
+template <int CTRL>
+__device__ __forceinline__ int llmq_dppi(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int llmq_wave_max_all(int v) {
+    v = max(v, llmq_dppi<0xB1>(v));
+    v = max(v, llmq_dppi<0x4E>(v));
+    v = max(v, llmq_dppi<0x141>(v));
+    v = max(v, llmq_dppi<0x140>(v));
+    const auto r16 = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    v = max((int)r16[0], (int)r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return max((int)r32[0], (int)r32[1]);
+}
+
 // max over the wave, in every lane (order-free): DPP within rows of 16, then
 // the four rows' results.
 __device__ __forceinline__ float llmq_wave_max(float v) {

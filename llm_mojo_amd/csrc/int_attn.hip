@@ -26,16 +26,9 @@ constexpr int kThreads = 256;
 // in scratch memory).
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-__device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
-    return v;
-}
+// maxima over the wave (order-free), without LDS
+__device__ __forceinline__ float wave_max_f(float v) { return llmq_wave_max_all(v); }
+__device__ __forceinline__ int wave_max_i(int v) { return llmq_wave_max_all(v); }
 __device__ __forceinline__ int64_t wave_sum_l(int64_t v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);

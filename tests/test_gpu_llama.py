@@ -37,22 +37,27 @@ def test_llama_forward_matches_numpy(gpu):
     m.free()
 
 
-def test_llama_generate_matches_numpy_greedy(gpu):
-    """Two sequences, 12-token prompts, 6 greedy tokens each (5 batched decode
-    steps through the captured graph) against NumPy greedy decoding; a step
-    whose NumPy top-2 margin is under 1e-3 of max |logit| ends the comparison
-    of that sequence."""
+@pytest.mark.parametrize("head_type,B", [(14, 2), (14, 1), (8, 1), (12, 2), (12, 1)])
+def test_llama_generate_matches_numpy_greedy(gpu, head_type, B):
+    """B sequences, 12-token prompts, 6 greedy tokens each (5 decode steps
+    through the captured graph) against NumPy greedy decoding; a step whose
+    NumPy top-2 margin is under 1e-3 of max |logit| ends the comparison of
+    that sequence.  Q6_K / Q8_0 heads take the int16 head with argmax
+    partials and the pick-and-embed kernel, Q4_K the float head and the full
+    argmax; batch 1 stages the attention splits in the Wo GEMV, batch 2 runs
+    the combine kernel."""
     torch, lm, ctx = gpu
     from llm_mojo_amd import synth
 
-    tensors = synth.llama_tensors(SMALL, 6)
-    prompts = synth.llama_prompts(6, 2, 12, SMALL["vocab"])
-    print("llama generate", flush=True)
-    m = lm.Llama(ctx, SMALL, tensors)
+    cfg = dict(SMALL, head_type=head_type)
+    tensors = synth.llama_tensors(cfg, 6)
+    prompts = synth.llama_prompts(6, B, 12, cfg["vocab"])
+    print("llama generate", head_type, B, flush=True)
+    m = lm.Llama(ctx, cfg, tensors)
     toks, pre_ms, dec_ms = m.generate(prompts, 6)
-    assert toks.shape == (6, 2)
-    ref = NumpyLlama(SMALL, tensors, n_seq=2)
-    for b in range(2):
+    assert toks.shape == (6, B)
+    ref = NumpyLlama(cfg, tensors, n_seq=B)
+    for b in range(B):
         logits = ref.forward(b, prompts[b], 0)
         for i in range(6):
             top = np.sort(logits)[-2:]

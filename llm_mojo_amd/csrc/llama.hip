@@ -269,6 +269,177 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
     }
 }
 
+// attend_split_kernel's arithmetic for the G = n_head / n_kv query heads of
+// key / value head blockIdx.x together (sequence blockIdx.y, split
+// blockIdx.z): the split's cache rows are read once for the G heads.  Thread
+// t holds position s0 + t for every head's score; then wave w sums values
+// for positions w, w + kSW, .. of every head (lane = dimension), the waves
+// added in order.  Partials as attend_split_kernel's, per query head.
+template <int G>
+__global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float *__restrict__ qkv, int64_t ld,
+                                                                    const int *__restrict__ state, int n_head,
+                                                                    int n_kv, int n_layer, int layer, int max_t,
+                                                                    const float2 *__restrict__ rope,
+                                                                    int8_t *__restrict__ K8, int8_t *__restrict__ V8,
+                                                                    float *__restrict__ KS, float *__restrict__ VS,
+                                                                    float *__restrict__ part, int NS) {
+    static_assert(G * HD == 2 * kSplit, "two query values a thread");
+    __shared__ __align__(16) float q[G][HD];
+    __shared__ __align__(16) int8_t vrow[kSplit][HD];
+    __shared__ __align__(16) int8_t knew[HD];
+    __shared__ __align__(16) float wv[G][kSplit];
+    __shared__ float red[G][kSW], redt[G][kSW], smax[G], snew[2], s_qsum[G];
+    __shared__ __align__(16) float vred[kSW][G][HD];
+    const int kvh = blockIdx.x, b = blockIdx.y, j = blockIdx.z, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int s0 = j * kSplit, h0 = kvh * G;
+    const int64_t slot0 = ((int64_t)b * n_layer + layer) * max_t;
+    const float *r = qkv + (int64_t)b * ld;
+    // queries (two values a thread: head-major index tid and tid + kSplit,
+    // so a wave holds one head's 64 dimensions), new key and value, cache
+    // rows, all before the position
+    const float qa = r[h0 * HD + tid], qb = r[h0 * HD + kSplit + tid];
+    float kvx = 0.0f, vvx = 0.0f;
+    if (w == 1) {
+        kvx = r[(n_head + kvh) * HD + lane];
+        vvx = r[(n_head + n_kv + kvh) * HD + lane];
+    }
+    const int64_t sl = (slot0 + min(s0 + tid, max_t - 1)) * n_kv + kvh;
+    int4 kr[HD / 16], vr[HD / 16];
+#pragma unroll
+    for (int i = 0; i < HD / 16; i++) {
+        kr[i] = reinterpret_cast<const int4 *>(K8 + sl * HD)[i];
+        vr[i] = reinterpret_cast<const int4 *>(V8 + sl * HD)[i];
+    }
+    float ks = KS[sl], vs = VS[sl];
+    const int pos = state[0], npos = pos + 1;
+    if (s0 >= npos) return;  // an empty split (uniform over the workgroup; never read)
+    const int cnt = min(kSplit, npos - s0);
+    const bool valid = tid < cnt;
+    const bool has_new = s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
+    const bool is_new = has_new && tid == cnt - 1;
+    if (valid && !is_new) {
+#pragma unroll
+        for (int i = 0; i < HD / 16; i++) reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
+    }
+    // RoPE of pair (2i, 2i + 1), i = d / 2: every thread its two query
+    // values (heads w and w + kSW), wave 1 also the new key, which it
+    // quantizes with the new value
+    {
+        const int d = lane;
+        const float2 csn = rope[pos * (HD / 2) + (d >> 1)];
+        const float pa = llmq_dppf<0xB1>(qa), pb = llmq_dppf<0xB1>(qb);  // lane d ^ 1
+        const float ra = (d & 1) ? pa * csn.y + qa * csn.x : qa * csn.x - pa * csn.y;
+        const float rb = (d & 1) ? pb * csn.y + qb * csn.x : qb * csn.x - pb * csn.y;
+        q[w][d] = ra;
+        q[w + kSW][d] = rb;
+        const float sa = wave_sum(ra), sb = wave_sum(rb);
+        if (d == 0) {
+            s_qsum[w] = sa;
+            s_qsum[w + kSW] = sb;
+        }
+        if (w == 1 && has_new) {
+            const float pk = llmq_dppf<0xB1>(kvx);
+            const float rk = (d & 1) ? pk * csn.y + kvx * csn.x : kvx * csn.x - pk * csn.y;
+            const int64_t sn = (slot0 + pos) * n_kv + kvh;
+            for (int kv = 0; kv < 2; kv++) {
+                const float x = kv == 0 ? rk : vvx;
+                const float m = wave_max(fabsf(x));
+                float sc = m / 127.0f;
+                if (sc == 0.0f) sc = 1.0f;
+                const float inv = 1.0f / sc;
+                const int8_t code = (int8_t)llmq_to_int(roundf(x * inv));
+                if (kv == 0)
+                    knew[d] = code;
+                else
+                    vrow[cnt - 1][d] = code;
+                if (d == 0) snew[kv] = sc;
+                (kv == 0 ? K8 : V8)[sn * HD + d] = code;  // this workgroup is the head's only writer
+                if (d == 0) (kv == 0 ? KS : VS)[sn] = sc;
+            }
+        }
+    }
+    __syncthreads();
+    if (is_new) {
+        ks = snew[0];
+        vs = snew[1];
+    }
+    // scores of this position for the G heads: q . (u - 128) over the codes
+    // u = k + 128, the 64 codes converted once
+    float u[HD];
+#pragma unroll
+    for (int i = 0; i < HD / 16; i++) {
+        const int4 k4 = is_new ? reinterpret_cast<const int4 *>(knew)[i] : kr[i];
+        const uint32_t kw[4] = {(uint32_t)k4.x ^ 0x80808080u, (uint32_t)k4.y ^ 0x80808080u,
+                                (uint32_t)k4.z ^ 0x80808080u, (uint32_t)k4.w ^ 0x80808080u};
+#pragma unroll
+        for (int e4 = 0; e4 < 4; e4++) {
+            u[16 * i + 4 * e4] = (float)(kw[e4] & 255u);
+            u[16 * i + 4 * e4 + 1] = (float)((kw[e4] >> 8) & 255u);
+            u[16 * i + 4 * e4 + 2] = (float)((kw[e4] >> 16) & 255u);
+            u[16 * i + 4 * e4 + 3] = (float)(kw[e4] >> 24);
+        }
+    }
+    // one head at a time (the query reads of one head in flight); the score
+    // waits in wv until the head's maximum is known
+#pragma unroll 1
+    for (int g = 0; g < G; g++) {
+        const float4 *q4 = reinterpret_cast<const float4 *>(q[g]);
+        float d = 0.0f;
+#pragma unroll
+        for (int e4 = 0; e4 < HD / 4; e4++) {
+            const float4 qq = q4[e4];
+            d = fmaf(qq.x, u[4 * e4], d);
+            d = fmaf(qq.y, u[4 * e4 + 1], d);
+            d = fmaf(qq.z, u[4 * e4 + 2], d);
+            d = fmaf(qq.w, u[4 * e4 + 3], d);
+        }
+        const float sc = valid ? (d - 128.0f * s_qsum[g]) * ks * (1.0f / sqrtf((float)HD)) : -INFINITY;
+        wv[g][tid] = sc;
+        const float m = wave_max(sc);
+        if (lane == 0) red[g][w] = m;
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int g = 0; g < G; g++) {
+        float m = red[g][0];
+#pragma unroll
+        for (int i = 1; i < kSW; i++) m = fmaxf(m, red[g][i]);
+        const float e = valid ? expf(wv[g][tid] - m) : 0.0f;
+        wv[g][tid] = e * vs;
+        const float t = wave_sum(e);
+        if (lane == 0) redt[g][w] = t;
+        if (tid == 0) smax[g] = m;  // the split's maximum, kept for the partial
+    }
+    __syncthreads();
+    // values: wave w takes positions w, w + kSW, .. of every head; lane = dim
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) acc[g] = 0.0f;
+    for (int sp = w; sp < cnt; sp += kSW) {
+        const float v = (float)vrow[sp][lane];
+#pragma unroll
+        for (int g = 0; g < G; g++) acc[g] = fmaf(wv[g][sp], v, acc[g]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) vred[w][g][lane] = acc[g];
+    __syncthreads();
+    for (int e = tid; e < G * HD; e += kSplit) {
+        const int g = e / HD, dd = e % HD;
+        float o = vred[0][g][dd];
+#pragma unroll
+        for (int i = 1; i < kSW; i++) o += vred[i][g][dd];
+        float *P = part + (((int64_t)b * n_head + h0 + g) * NS + j) * kPart;
+        P[4 + dd] = o;
+        if (dd == 0) {
+            P[0] = smax[g];
+            float t = redt[g][0];
+#pragma unroll
+            for (int i = 1; i < kSW; i++) t += redt[g][i];
+            P[1] = t;
+        }
+    }
+}
+
 // The splits of (head blockIdx.x, sequence blockIdx.y) into the output:
 // out = sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j - M), splits in order
 // (the same arithmetic as the Wo GEMV's staging of them, gguf1.hip).
@@ -479,9 +650,17 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
         RC(norm_linear(m, gain(m, l, 0), m->wqkv[l], R, m->qkv, QC, 0));
         if (state) {  // RoPE, the cache store and the attention splits in one launch
             const int NS = (c.max_t + kSplit - 1) / kSplit;
-            hipLaunchKernelGGL(attend_split_kernel, dim3(c.n_head, R, NS), dim3(kSplit), 0, ctx->stream, m->qkv,
-                               (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope, m->k8, m->v8,
-                               m->ks, m->vs, m->apart, NS);
+            // LLMQ_ATTN_GROUP=1 / 0 forces the grouped / per-head kernel
+            static const char *ge = getenv("LLMQ_ATTN_GROUP");
+            const bool grouped = c.n_head == 8 * c.n_kv && (ge ? ge[0] == '1' : R > 1);
+            if (grouped)  // the 8 query heads of a key / value head in one workgroup
+                hipLaunchKernelGGL(attend_split_group_kernel<8>, dim3(c.n_kv, R, NS), dim3(kSplit), 0, ctx->stream,
+                                   m->qkv, (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope,
+                                   m->k8, m->v8, m->ks, m->vs, m->apart, NS);
+            else
+                hipLaunchKernelGGL(attend_split_kernel, dim3(c.n_head, R, NS), dim3(kSplit), 0, ctx->stream, m->qkv,
+                                   (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope, m->k8,
+                                   m->v8, m->ks, m->vs, m->apart, NS);
             if (R == 1 && gguf_gemv_attn_ok(m->wo[l], NS)) {  // Wo combines the splits as it stages its row
                 RC(launch_gguf_gemv(ctx, m->wo[l], nullptr, m->x, nullptr, LLMQ_RESID, nullptr, 0, nullptr, 0.0f, 0,
                                     nullptr, nullptr, m->apart, state, kSplit, NS));

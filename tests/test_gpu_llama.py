@@ -69,6 +69,31 @@ def test_llama_generate_matches_numpy_greedy(gpu, head_type, B):
     m.free()
 
 
+@pytest.mark.parametrize("B", [1, 2])
+def test_llama_grouped_query_attention_matches_numpy(gpu, B):
+    """Eight query heads a key / value head (the TinyLlama grouping): batch 1
+    takes the per-head split kernel, batch 2 the kernel that serves the 8
+    heads of a group from one read of the cache.  270-token prompts (two
+    256-position splits, the new position in the second), 6 greedy tokens,
+    against NumPy greedy decoding (the margin rule); the same prompt twice in
+    the batch gives the same tokens in both rows."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    cfg = dict(SMALL, dim=512, n_head=8, n_kv=1, max_t=300)
+    tensors = synth.llama_tensors(cfg, 12)
+    prompts = synth.llama_prompts(12, 1, 270, cfg["vocab"])
+    prompts = np.repeat(prompts, B, axis=0)
+    print("llama grouped attention", B, flush=True)
+    m = lm.Llama(ctx, cfg, tensors)
+    toks, _, _ = m.generate(prompts, 6)
+    m.free()
+    for b in range(1, B):
+        assert np.array_equal(toks[:, b], toks[:, 0])
+    n = greedy_vs_numpy(toks[:, 0], NumpyLlama(cfg, tensors), 0, prompts[0], 0)
+    assert n >= 2, n
+
+
 def test_llama_batch_rows_are_independent(gpu):
     """The same prompt in both sequences of a batch gives the same tokens,
     equal to a one-sequence run; a second call (graph replayed) repeats them."""

@@ -47,18 +47,18 @@ int llmq_set_error(int code, const char *fmt, ...) {
 }
 
 
-int ctx_workspace(llmq_ctx *ctx, size_t bytes, void **p) {
-    if (bytes > ctx->ws_bytes) {
+int ctx_workspace(llmq_ctx *ctx, size_t bytes, void **p, int slot) {
+    if (bytes > ctx->ws_bytes[slot]) {
         LLMQ_HIP(hipStreamSynchronize(ctx->stream));
-        if (ctx->ws) hipFree(ctx->ws);
-        ctx->ws = nullptr;
-        ctx->ws_bytes = 0;
+        if (ctx->ws[slot]) hipFree(ctx->ws[slot]);
+        ctx->ws[slot] = nullptr;
+        ctx->ws_bytes[slot] = 0;
         const size_t want = bytes + bytes / 4;
-        if (hipMalloc(&ctx->ws, want) != hipSuccess)
+        if (hipMalloc(&ctx->ws[slot], want) != hipSuccess)
             return llmq_set_error(LLMQ_ENOMEM, "workspace of %zu bytes", want);
-        ctx->ws_bytes = want;
+        ctx->ws_bytes[slot] = want;
     }
-    *p = ctx->ws;
+    *p = ctx->ws[slot];
     return LLMQ_OK;
 }
 
@@ -98,7 +98,8 @@ int llmq_init(int device, llmq_ctx **out) {
 int llmq_destroy(llmq_ctx *ctx) {
     if (!ctx) return LLMQ_OK;
     hipStreamSynchronize(ctx->stream);
-    if (ctx->ws) hipFree(ctx->ws);
+    for (void *p : ctx->ws)
+        if (p) hipFree(p);
     if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return LLMQ_OK;
@@ -484,9 +485,9 @@ int llmq_linear_noalloc(llmq_ctx *ctx, float *out, const float *x, const llmq_ma
     LLMQ_REQUIRE(need <= (int64_t)LLMQ_NOALLOC_SCRATCH_BYTES,
                  "linear_noalloc: %lld tokens x %lld inputs need %lld bytes of scratch, the maximum is %d",
                  (long long)T, (long long)IN, (long long)need, LLMQ_NOALLOC_SCRATCH_BYTES);
-    if (is_float_act(w)) {  // as llmq_linear: these kernels use no scratch
+    if (is_float_act(w)) {  // the one-token GEMV and the fp32-core matmul use no scratch
         if (T == 1) return launch_gguf_gemv(ctx, w, x, out, bias, flags, nullptr, 0);
-        return launch_gguf_gemm(ctx, w, x, IN, T, out, OUT, bias, flags);
+        return launch_gguf_gemm(ctx, w, x, IN, T, out, OUT, bias, flags, nullptr, 0);
     }
     GemvRequest rq;
     rq.w = w;

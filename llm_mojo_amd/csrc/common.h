@@ -34,14 +34,17 @@ struct llmq_ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     hipDeviceProp_t prop{};
-    void *ws = nullptr;  // grow-only workspace (prompt-side int16 activation codes)
-    size_t ws_bytes = 0;
+    // grow-only workspaces: slot 0 the prompt-side int16 activation codes
+    // (and LayerNorm outputs), slot 1 the fp16 activation records of the
+    // several-token Q4_K matmul
+    void *ws[2] = {nullptr, nullptr};
+    size_t ws_bytes[2] = {0, 0};
     void *scratch = nullptr;  // this device's no-allocation scratch (llmq_linear_noalloc), from llmq_init
 };
 
-// The context's workspace of at least `bytes` (api.hip); growing it waits for
-// the context's stream first.  Not for use under graph capture.
-int ctx_workspace(llmq_ctx *ctx, size_t bytes, void **p);
+// The context's workspace `slot` of at least `bytes` (api.hip); growing it
+// waits for the context's stream first.  Not for use under graph capture.
+int ctx_workspace(llmq_ctx *ctx, size_t bytes, void **p, int slot = 0);
 
 enum { MAT_QUANT = 0, MAT_GGUF = 1 };
 
@@ -278,8 +281,21 @@ inline int float_act_type(const llmq_mat *w) {
 // chunk of a row is group 0); groups are powers of two times 32 otherwise.
 int qm_cpg_shift(const llmq_mat *w);
 // Several-token GGUF matmul on the fp32 matrix cores (gguf_gemm.hip).
+// Q4_K matrices with whole superblocks take the fp16 matrix cores over an
+// h16 record of x (gguf_gemm16.hip): `rec` of `rec_cap` bytes when given,
+// the context's workspace slot 1 when rec_cap < 0, and the fp32 kernel when
+// rec_cap == 0 (callers that may not allocate); LLMQ_GEMM_H16=0 forces the
+// fp32 kernel.
 int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t ldx, int64_t T, float *out,
-                     int64_t ldo, const float *bias, int flags);
+                     int64_t ldo, const float *bias, int flags, void *rec = nullptr, int64_t rec_cap = -1);
+// The h16 record (gguf_gemm16.hip): its size for T tokens of K inputs, the
+// record kernel, and the Q4_K matmul over a record.
+int64_t h16_rec_bytes(int64_t T, int64_t K);
+void h16_rec_parts(void *rec, int64_t T, int64_t K, uint8_t **planes, _Float16 **sums, float **inv);
+bool gguf_gemm_h16_ok(const llmq_mat *w);
+int launch_act_h16(llmq_ctx *ctx, const float *x, int64_t ldx, int64_t T, int64_t K, void *rec);
+int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int64_t T, float *out, int64_t ldo,
+                         const float *bias, int flags);
 // int16 output head for Q6_K / Q8_0 (gguf_head.hip).
 int gguf_has_i16(const llmq_mat *w);
 // with rms_g, each row of h is RMS-normalized (times rms_g) first; with
@@ -548,6 +564,65 @@ __device__ __forceinline__ float llmq_wave_max_all(float v) {
     v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
     const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
+// Sum and maximum over the 32 lanes of each half of the wave.
+__device__ __forceinline__ float llmq_half_sum(float v) {
+    v = v + llmq_dppf<0xB1>(v);
+    v = v + llmq_dppf<0x4E>(v);
+    v = v + llmq_dppf<0x141>(v);
+    v = v + llmq_dppf<0x140>(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float llmq_half_max(float v) {
+    v = fmaxf(v, llmq_dppf<0xB1>(v));
+    v = fmaxf(v, llmq_dppf<0x4E>(v));
+    v = fmaxf(v, llmq_dppf<0x141>(v));
+    v = fmaxf(v, llmq_dppf<0x140>(v));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// One superblock (256 inputs) of one token of an h16 activation record (the
+// fp16-plane form of a float row that gemm_h16_q4k_kernel reads; layout in
+// gguf_gemm16.hip), written by one wave: lane k holds inputs k + 64 q,
+// q = 0..3, of superblock sb of token t in v[q] (zeros for padding).  The
+// superblock's scale is the power of two s with max |x| s < 2^10; the
+// input planes get hi = fp16(x s) and lo = fp16(x s - hi), the sum planes
+// the same split of s times each 32-input sub-block's sum, and inv 1 / s.
+// Every lane of the wave calls it (the reductions span the wave); ok = false
+// stores nothing.
+__device__ __forceinline__ void llmq_h16_store(uint8_t *planes, _Float16 *sums, float *inv, int KB, int NSB, int t,
+                                               int sb, const float (&v)[4], bool ok) {
+    const int k = threadIdx.x & 63;
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    m = llmq_wave_max_all(m);
+    int ex = 0;
+    frexpf(m, &ex);  // m < 2^ex
+    const int e = min(126, max(-126, 10 - ex));
+    const float s = ldexpf(1.0f, e);
+    const int kk = k & 31, g = kk >> 3, i = kk & 7, pos = (i & 1) ? 4 + (i >> 1) : (i >> 1);
+    const int64_t tt = t >> 4, c = t & 15;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float sx = llmq_half_sum(v[q]) * s;  // sub-block 2q + k / 32
+        const float xs = v[q] * s;
+        const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
+        const _Float16 shi = (_Float16)sx, slo = (_Float16)(sx - (float)shi);
+        if (ok) {
+            const int j = 2 * q + (k >> 5);
+            _Float16 *p = reinterpret_cast<_Float16 *>(planes) + ((tt * KB + sb * 8 + j) * 1024 + (g * 16 + c) * 8 + pos);
+            p[0] = hi;
+            p[512] = lo;
+            if (kk == 0) {
+                _Float16 *ps = sums + (tt * NSB + sb) * 256 + c * 8 + j;
+                ps[0] = shi;
+                ps[128] = slo;
+            }
+        }
+    }
+    if (ok && k == 0) inv[(tt * NSB + sb) * 16 + c] = ldexpf(1.0f, -e);
 }
 
 template <int CTRL>

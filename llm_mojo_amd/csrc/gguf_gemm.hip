@@ -210,9 +210,20 @@ int launch_t(llmq_ctx *ctx, const GArgs &a, dim3 grid, int nw) {
 }  // namespace
 
 int launch_gguf_gemm(llmq_ctx *ctx, const llmq_mat *w, const float *x, int64_t ldx, int64_t T, float *out,
-                     int64_t ldo, const float *bias, int flags) {
+                     int64_t ldo, const float *bias, int flags, void *rec, int64_t rec_cap) {
     LLMQ_REQUIRE(w && is_float_act(w), "gguf_gemm: not a GGUF or float-activation QuantMatrix");
     LLMQ_REQUIRE(x && out && T > 0, "gguf_gemm: bad arguments");
+    const char *he = getenv("LLMQ_GEMM_H16");
+    if (rec_cap != 0 && gguf_gemm_h16_ok(w) && !(he && he[0] == '0')) {
+        const int64_t need = h16_rec_bytes(T, w->k);
+        if (rec_cap < 0)
+            RC(ctx_workspace(ctx, (size_t)need, &rec, 1));
+        else
+            LLMQ_REQUIRE(rec && need <= rec_cap, "gguf_gemm: %lld tokens need a %lld-byte record, %lld given",
+                         (long long)T, (long long)need, (long long)rec_cap);
+        RC(launch_act_h16(ctx, x, ldx, T, w->k, rec));
+        return launch_gguf_gemm_h16(ctx, w, rec, T, out, ldo, bias, flags);
+    }
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemm: LLMQ_BIAS without a bias");
     LLMQ_REQUIRE(w->k % 32 == 0, "gguf_gemm: cols must be a multiple of 32");
     const int64_t ntc = (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 16;

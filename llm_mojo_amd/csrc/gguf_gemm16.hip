@@ -1,0 +1,299 @@
+// Several-token Q4_K matmul on the fp16 matrix cores: matmul_rows for T > 1
+// over a GGUFMatrix of Q4_K rows (kernels.mojo:314-349; the Q4_K decoder,
+// gguf.mojo:205-250).
+//
+// A Q4_K weight of sub-block j (32 weights) of a superblock is
+// d sc_j u - dmin m_j, with u a 4-bit code, sc_j and m_j 6-bit integers and
+// d, dmin fp16.  Over a superblock of a row,
+//   sum_i w_i x_i = d sum_j sum_i (sc_j u_i) x_i - dmin sum_j m_j X_j,
+// X_j the sub-block's sum of x, and sc_j u_i <= 945 and m_j are exact in
+// fp16.  The activations go in as an "h16 record": per token and superblock
+// a power-of-two scale s (max |x s| < 2^10) and x s as two fp16 planes,
+// hi = fp16(x s), lo = fp16(x s - hi) (together x s to 22 bits), and the
+// same two planes of s X_j.  The matrix cores (v_mfma_f32_16x16x32_f16)
+// form D = sum (sc u)(hi + lo) and D' = sum m (S hi + S lo), every product
+// exact in their fp32 sums, and the kernel adds (d D - dmin D') / s.  The
+// outputs agree with the reference's float matmul to fp32 rounding, not in
+// its summation order.
+//
+// Record layout for T tokens (padded to T16, a multiple of 16), KB = K / 32
+// sub-blocks and NSB = K / 256 superblocks, the 16 tokens of a token tile
+// side by side so that each operand load of a wave is 1 KB in one piece:
+//   planes  fp16 [T16 / 16][KB][hi, lo][4 groups][16 tokens][8]: group g
+//           holds inputs 8g .. 8g + 7 of the sub-block in the order 0, 2, 4,
+//           6, 1, 3, 5, 7 (the order in which a code dword's nibbles decode,
+//           below);
+//   sums    fp16 [T16 / 16][NSB][hi, lo][16 tokens][8]: s X_j, j = 0..7;
+//   inv     float [T16 / 16][NSB][16 tokens]: 1 / s.
+// Padded tokens are zeros throughout, so they add nothing.
+//
+// Mapping: a workgroup owns RT row tiles of 16 rows and a tile of 16 tokens;
+// its NW waves split the row's superblocks into contiguous runs.  In a
+// superblock a wave's lane l takes token / row l % 16 and input group
+// l / 16 of each sub-block: the A operand is that token's group of the
+// record (32 bytes), the B operand the row's code dword for the group (the
+// (chunk, row) entry of the device layout) times sc_j; lane l holds outputs
+// (tokens 4 (l / 16) + i, row l % 16).  The waves' partial sums are added in
+// LDS in wave order.
+#include "common.h"
+
+namespace {
+
+constexpr uint32_t kOOB = 0x80000000u;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+struct HArgs {
+    const uint8_t *codes, *sb, *planes, *sums, *inv;
+    uint32_t codes_bytes, sb_bytes, planes_bytes, sums_bytes, inv_bytes;
+    int n, KB, CK, NSB, ntiles, T, flags;
+    int64_t ldo;
+    const float *bias;
+    float *out;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+struct Rec {
+    uint8_t *planes;
+    _Float16 *sums;
+    float *inv;
+};
+
+Rec rec_parts(void *rec, int64_t T, int64_t K) {
+    const int64_t T16 = (T + 15) / 16 * 16, KB = K / 32, NSB = K / 256;
+    uint8_t *p = static_cast<uint8_t *>(rec);
+    return {p, reinterpret_cast<_Float16 *>(p + T16 * KB * 128),
+            reinterpret_cast<float *>(p + T16 * KB * 128 + T16 * NSB * 32)};
+}
+
+// The record of x (T x K floats, row stride ldx): workgroup (blockIdx.x,
+// token blockIdx.y) covers 4 superblocks, one a wave.
+__global__ __launch_bounds__(256) void act_h16_kernel(const float *__restrict__ x, int64_t ldx, int T, int KB,
+                                                      int NSB, uint8_t *__restrict__ planes,
+                                                      _Float16 *__restrict__ sums, float *__restrict__ inv) {
+    const int t = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int sb = blockIdx.x * 4 + w;
+    const bool ok = sb < NSB, in = ok && t < T;
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) v[q] = in ? x[(int64_t)t * ldx + sb * 256 + 64 * q + lane] : 0.0f;
+    llmq_h16_store(planes, sums, inv, KB, NSB, t, sb, v, ok);
+}
+
+// 1024 + the 8 bytes of (a, b) as fp16 pairs (a0, a1), (a2, a3), (b0, b1),
+// (b2, b3): 0x6400 | n is 1024 + n in fp16 for n < 1024.
+__device__ __forceinline__ void bytes_f16(uint32_t a, uint32_t b, uint32_t (&d)[4]) {
+    d[0] = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
+    d[1] = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
+    d[2] = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+    d[3] = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+}
+
+template <int NW, int RT>
+__global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
+    __shared__ float part[NW][RT][256];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c16 = lane & 15, g = lane >> 4;
+    const int tile0 = blockIdx.x * RT, tt = blockIdx.y;
+    const auto rc = make_rsrc(a.codes, a.codes_bytes), rs = make_rsrc(a.sb, a.sb_bytes);
+    const auto rp = make_rsrc(a.planes, a.planes_bytes), rq = make_rsrc(a.sums, a.sums_bytes);
+    const auto ri = make_rsrc(a.inv, a.inv_bytes);
+    const int per = (a.NSB + NW - 1) / NW;  // superblocks a wave
+    const int s0 = w * per, s1 = min(a.NSB, s0 + per);
+    const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, km1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    float acc[RT][4];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[r][i] = 0.0f;
+    for (int sbi = s0; sbi < s1; sbi++) {
+        uint4 f[RT], ah[8], al[8];
+        uint32_t cw[RT][8];
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const bool ok = tile0 + r < a.ntiles;
+            f[r] = bload16(rs, ok ? (uint32_t)((((tile0 + r) * a.NSB + sbi) * 16 + c16) * 16) : kOOB);
+            // chunk entries of one row tile are 256 bytes apart (kOOB + 256 u stays out of range)
+            const uint32_t cb = ok ? (uint32_t)((((tile0 + r) * a.CK + sbi * 8) * 16 + c16) * 16 + g * 4) : kOOB;
+#pragma unroll
+            for (int u = 0; u < 8; u++) cw[r][u] = bload4(rc, cb + 256u * u);
+        }
+        const uint32_t ab = (uint32_t)((tt * a.KB + sbi * 8) * 2048 + lane * 16);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            ah[u] = bload16(rp, ab + 2048u * u);
+            al[u] = bload16(rp, ab + 2048u * u + 1024u);
+        }
+        // sums planes: hi in group 0, lo in group 1, zeros in groups 2 and 3
+        const uint4 sq = bload16(rq, g < 2 ? (uint32_t)((tt * a.NSB + sbi) * 512 + lane * 16) : kOOB);
+        const uint4 iv = bload16(ri, (uint32_t)(((tt * a.NSB + sbi) * 16 + 4 * g) * 4));
+        __builtin_amdgcn_sched_barrier(0);  // the superblock's loads all issue before its first product
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            // sc_j and m_j as bytes (k_scale_min, gguf.mojo:205-221, four at a time)
+            const uint32_t sc_lo = f[r].y & 0x3F3F3F3Fu, m_lo = f[r].z & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (f[r].w & 0x0F0F0F0Fu) | ((f[r].y >> 2) & 0x30303030u);
+            const uint32_t m_hi = ((f[r].w >> 4) & 0x0F0F0F0Fu) | ((f[r].z >> 2) & 0x30303030u);
+            uint32_t scp[4], mp[4];
+            bytes_f16(sc_lo, sc_hi, scp);
+            bytes_f16(m_lo, m_hi, mp);
+            v2h sc[4], nsc[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sc[i] = __builtin_bit_cast(v2h, scp[i]) - k1024;  // (sc_2i, sc_2i+1)
+                nsc[i] = sc[i] * km1024;
+            }
+            v4f d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t lo = cw[r][u] & 0x0F0F0F0Fu, hi = (cw[r][u] >> 4) & 0x0F0F0F0Fu;
+                uint32_t q[4];
+                bytes_f16(lo, hi, q);  // 1024 + (u0, u2), (u4, u6), (u1, u3), (u5, u7)
+                const _Float16 s1 = sc[u >> 1][u & 1], n1 = nsc[u >> 1][u & 1];
+                const v2h sv = {s1, s1}, nv = {n1, n1};
+                v8h b;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    // (1024 + u) sc - 1024 sc = u sc exactly (both terms and the result fit fp16)
+                    const v2h p = __builtin_elementwise_fma(__builtin_bit_cast(v2h, q[i]), sv, nv);
+                    b[2 * i] = p[0];
+                    b[2 * i + 1] = p[1];
+                }
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah[u]), b, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al[u]), b, d, 0, 0, 0);
+            }
+            // m_j in groups 0 and 1 (against the sums' hi and lo planes)
+            v8h bm;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const v2h p = g < 2 ? __builtin_bit_cast(v2h, mp[i]) - k1024 : (v2h){(_Float16)0.0f, (_Float16)0.0f};
+                bm[2 * i] = p[0];
+                bm[2 * i + 1] = p[1];
+            }
+            v4f dm = {0.0f, 0.0f, 0.0f, 0.0f};
+            dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, sq), bm, dm, 0, 0, 0);
+            const float dd = __half2float(__ushort_as_half((unsigned short)(f[r].x & 0xFFFFu)));
+            const float dmin = __half2float(__ushort_as_half((unsigned short)(f[r].x >> 16)));
+            const float inv[4] = {__uint_as_float(iv.x), __uint_as_float(iv.y), __uint_as_float(iv.z),
+                                  __uint_as_float(iv.w)};
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[r][i] = fmaf(inv[i], fmaf(-dmin, dm[i], dd * d[i]), acc[r][i]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) part[w][r][(4 * g + i) * 16 + c16] = acc[r][i];
+    __syncthreads();
+    for (int e = tid; e < RT * 256; e += NW * 64) {
+        const int r = e >> 8, q = e & 255, tk = tt * 16 + (q >> 4), o = (tile0 + r) * 16 + (q & 15);
+        float v = part[0][r][q];
+#pragma unroll
+        for (int p = 1; p < NW; p++) v += part[p][r][q];
+        if (o < a.n && tk < a.T) {
+            if (a.flags & LLMQ_BIAS) v += a.bias[o];
+            if (a.flags & LLMQ_GELU) v = gelu_ref(v);
+            float *dst = a.out + (int64_t)tk * a.ldo + o;
+            if (a.flags & LLMQ_RESID) v += *dst;
+            *dst = v;
+        }
+    }
+}
+
+}  // namespace
+
+int64_t h16_rec_bytes(int64_t T, int64_t K) {
+    const int64_t T16 = (T + 15) / 16 * 16, KB = K / 32, NSB = K / 256;
+    return T16 * KB * 128 + T16 * NSB * 32 + T16 * NSB * 4;
+}
+
+void h16_rec_parts(void *rec, int64_t T, int64_t K, uint8_t **planes, _Float16 **sums, float **inv) {
+    const Rec p = rec_parts(rec, T, K);
+    *planes = p.planes;
+    *sums = p.sums;
+    *inv = p.inv;
+}
+
+bool gguf_gemm_h16_ok(const llmq_mat *w) {
+    return w && w->kind == MAT_GGUF && w->ggml_type == LLMQ_GGML_Q4_K && w->k % 256 == 0;
+}
+
+int launch_act_h16(llmq_ctx *ctx, const float *x, int64_t ldx, int64_t T, int64_t K, void *rec) {
+    LLMQ_REQUIRE(x && rec && T > 0 && K % 256 == 0, "act_h16: bad arguments");
+    LLMQ_REQUIRE(h16_rec_bytes(T, K) < (int64_t)kOOB, "act_h16: record too large");
+    const int64_t T16 = (T + 15) / 16 * 16, NSB = K / 256;
+    LLMQ_REQUIRE(T16 <= 65535, "act_h16: too many tokens");
+    const Rec p = rec_parts(rec, T, K);
+    hipLaunchKernelGGL(act_h16_kernel, dim3((unsigned)((NSB + 3) / 4), (unsigned)T16), dim3(256), 0, ctx->stream, x,
+                       ldx, (int)T, (int)(K / 32), (int)NSB, p.planes, p.sums, p.inv);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int64_t T, float *out, int64_t ldo,
+                         const float *bias, int flags) {
+    LLMQ_REQUIRE(gguf_gemm_h16_ok(w), "gguf_gemm_h16: not a Q4_K matrix with whole superblocks");
+    LLMQ_REQUIRE(rec && out && T > 0, "gguf_gemm_h16: bad arguments");
+    LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemm_h16: LLMQ_BIAS without a bias");
+    const int64_t T16 = (T + 15) / 16 * 16, KB = w->k / 32, NSB = w->k / 256;
+    const int64_t ntc = (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 16;
+    const int64_t nts = (w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 16;
+    LLMQ_REQUIRE(ntc * 16 < (int64_t)kOOB && h16_rec_bytes(T, w->k) < (int64_t)kOOB && T16 <= 65535,
+                 "gguf_gemm_h16: operands too large");
+    const Rec p = rec_parts(const_cast<void *>(rec), T, w->k);
+    HArgs a{};
+    a.codes = w->codes;
+    a.codes_bytes = (uint32_t)(ntc * 16);
+    a.sb = reinterpret_cast<const uint8_t *>(w->g_sb16);
+    a.sb_bytes = (uint32_t)(nts * 16);
+    a.planes = p.planes;
+    a.planes_bytes = (uint32_t)(T16 * KB * 128);
+    a.sums = reinterpret_cast<const uint8_t *>(p.sums);
+    a.sums_bytes = (uint32_t)(T16 * NSB * 32);
+    a.inv = reinterpret_cast<const uint8_t *>(p.inv);
+    a.inv_bytes = (uint32_t)(T16 * NSB * 4);
+    a.n = (int)w->n;
+    a.KB = (int)KB;
+    a.CK = (int)w->CK;
+    a.NSB = (int)NSB;
+    a.ntiles = (int)w->ntiles;
+    a.T = (int)T;
+    a.flags = flags;
+    a.ldo = ldo;
+    a.bias = bias ? bias : out;
+    a.out = out;
+    const unsigned ntt = (unsigned)(T16 / 16);
+    // waves: the fewest that give every wave per = ceil(NSB / 16) superblocks
+    const int per = (int)((NSB + 15) / 16), nw = (int)((NSB + per - 1) / per);
+    const unsigned nt = (unsigned)w->ntiles;
+    hipStream_t st = ctx->stream;
+    const char *re = getenv("LLMQ_H16_RT");
+    const int rt = re ? atoi(re) : (w->ntiles >= 512 ? 2 : 1);
+    if (nw <= 8 && rt == 4)
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 4>), dim3((nt + 3) / 4, ntt), dim3(512), 0, st, a);
+    else if (nw <= 8 && rt == 2)
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 2>), dim3((nt + 1) / 2, ntt), dim3(512), 0, st, a);
+    else if (nw <= 4)
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<4, 1>), dim3(nt, ntt), dim3(256), 0, st, a);
+    else if (nw <= 8)
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 1>), dim3(nt, ntt), dim3(512), 0, st, a);
+    else if (nw <= 11)
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<11, 1>), dim3(nt, ntt), dim3(704), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<16, 1>), dim3(nt, ntt), dim3(1024), 0, st, a);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}

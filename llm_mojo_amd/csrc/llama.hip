@@ -63,6 +63,31 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     for (int i = threadIdx.x; i < C; i += 256) orow[i] = (xr[i] * r) * g[i];
 }
 
+// rmsnorm_kernel's row (x r) g written as the h16 record of the several-row
+// Q4_K matmul (llmq_h16_store): wave w takes superblocks w, w + 4, ..
+// (C = 256 NSB).
+__global__ __launch_bounds__(256) void rmsnorm_rec_kernel(const float *__restrict__ x, int64_t ldx,
+                                                          const float *__restrict__ g, int C, float eps,
+                                                          uint8_t *__restrict__ planes, _Float16 *__restrict__ sums,
+                                                          float *__restrict__ inv) {
+    __shared__ float red[4];
+    const float *xr = x + (int64_t)blockIdx.x * ldx;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < C; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, red);
+    const float r = 1.0f / sqrtf(ss / (float)C + eps);
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, NSB = C / 256;
+    for (int sb = w; sb < NSB; sb += 4) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int i = sb * 256 + 64 * q + lane;
+            v[q] = (xr[i] * r) * g[i];
+        }
+        llmq_h16_store(planes, sums, inv, C / 32, NSB, blockIdx.x, sb, v, true);
+    }
+}
+
 // RoPE and the cache store of a prompt: row `row` of qkv is token t = row % T
 // of sequence seq0 + row / T, at position pos0 + t.
 // query heads are rotated in place; key heads are rotated, then key and
@@ -472,12 +497,69 @@ __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restr
     out[(int64_t)b * ldo + h * HD + dd] = acc / T;
 }
 
+// attend_combine_kernel for the 4 heads of superblock blockIdx.x (wave w
+// head 4 blockIdx.x + w), the outputs written as the h16 record of the
+// several-row Q4_K matmul (llmq_h16_store, by wave 0 over the 4 heads).
+__global__ __launch_bounds__(256) void attend_combine_rec_kernel(const float *__restrict__ part, int NS, int n_head,
+                                                                 const int *__restrict__ state,
+                                                                 uint8_t *__restrict__ planes,
+                                                                 _Float16 *__restrict__ sums,
+                                                                 float *__restrict__ inv) {
+    __shared__ float o4[4][HD];
+    const int w = threadIdx.x >> 6, dd = threadIdx.x & 63, h = blockIdx.x * 4 + w, b = blockIdx.y;
+    const int ns = min(NS, (state[0] + kSplit) / kSplit);
+    const float *P = part + ((int64_t)b * n_head + h) * NS * kPart;
+    float mj[kMaxSplits], tj[kMaxSplits], aj[kMaxSplits];
+#pragma unroll
+    for (int j = 0; j < kMaxSplits; j++) {
+        const bool ok = j < ns;
+        mj[j] = ok ? P[j * kPart] : -INFINITY;
+        tj[j] = ok ? P[j * kPart + 1] : 0.0f;
+        aj[j] = ok ? P[j * kPart + 4 + dd] : 0.0f;
+    }
+    float M = mj[0];
+#pragma unroll
+    for (int j = 1; j < kMaxSplits; j++) M = fmaxf(M, mj[j]);
+    float T = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxSplits; j++) {
+        if (j < ns) {
+            const float f = expf(mj[j] - M);
+            T = fmaf(tj[j], f, T);
+            acc = fmaf(aj[j], f, acc);
+        }
+    }
+    o4[w][dd] = acc / T;
+    __syncthreads();
+    if (w == 0) {
+        const float v[4] = {o4[0][dd], o4[1][dd], o4[2][dd], o4[3][dd]};
+        llmq_h16_store(planes, sums, inv, n_head * HD / 32, n_head * HD / 256, b, blockIdx.x, v, true);
+    }
+}
+
 // h[r][i] = silu(g) * u with g = gu[r][i], u = gu[r][F + i].
 __global__ void swiglu_kernel(const float *__restrict__ gu, int64_t ldg, float *__restrict__ h, int64_t ldh, int F) {
     const int r = blockIdx.y;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < F; i += gridDim.x * blockDim.x) {
         const float g = gu[(int64_t)r * ldg + i], u = gu[(int64_t)r * ldg + F + i];
         h[(int64_t)r * ldh + i] = (g / (1.0f + expf(-g))) * u;
+    }
+}
+
+// swiglu_kernel's superblock blockIdx.x of row blockIdx.y (F = 256 NSB)
+// written as the h16 record of the several-row Q4_K matmul (by wave 0).
+__global__ __launch_bounds__(256) void swiglu_rec_kernel(const float *__restrict__ gu, int64_t ldg, int F,
+                                                         uint8_t *__restrict__ planes, _Float16 *__restrict__ sums,
+                                                         float *__restrict__ inv) {
+    __shared__ float hv[256];
+    const int r = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    const float g = gu[(int64_t)r * ldg + i], u = gu[(int64_t)r * ldg + F + i];
+    hv[threadIdx.x] = (g / (1.0f + expf(-g))) * u;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int k = threadIdx.x;
+        const float v[4] = {hv[k], hv[64 + k], hv[128 + k], hv[192 + k]};
+        llmq_h16_store(planes, sums, inv, F / 32, F / 256, r, blockIdx.x, v, true);
     }
 }
 
@@ -570,6 +652,8 @@ struct llmq_llama {
     float2 *rope = nullptr;        // (cos, sin) of position p, pair i at [p * head_dim / 2 + i]
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *hh = nullptr,
           *logits = nullptr;
+    void *h16 = nullptr;  // fp16 activation record of a several-row Q4_K matmul's input
+    int64_t h16_cap = 0;
     int64_t *tokens = nullptr, *next = nullptr, *gen = nullptr;
     int64_t gen_cap = 0;
     int graph_B = 0;  // batch size of the captured decode step
@@ -604,8 +688,11 @@ int ensure_rows(llmq_llama *m, int rows) {
     hipFree(m->gu);
     hipFree(m->hh);
     hipFree(m->tokens);
+    hipFree(m->h16);
     m->x = m->xn = m->qkv = m->att = m->gu = m->hh = nullptr;
     m->tokens = nullptr;
+    m->h16 = nullptr;
+    m->h16_cap = 0;
     m->rows = 0;
     const size_t r = (size_t)rows;
     if (hipMalloc(&m->x, r * c.dim * 4) != hipSuccess || hipMalloc(&m->xn, r * c.dim * 4) != hipSuccess ||
@@ -613,6 +700,12 @@ int ensure_rows(llmq_llama *m, int rows) {
         hipMalloc(&m->gu, r * 2 * c.ffn * 4) != hipSuccess || hipMalloc(&m->hh, r * c.ffn * 4) != hipSuccess ||
         hipMalloc(&m->tokens, r * 8) != hipSuccess)
         return llmq_set_error(LLMQ_ENOMEM, "llama: activations for %d tokens", rows);
+    if (rows > 1) {
+        const int64_t cap = h16_rec_bytes(rows, std::max(c.dim, c.ffn));
+        if (hipMalloc(&m->h16, (size_t)cap) != hipSuccess)
+            return llmq_set_error(LLMQ_ENOMEM, "llama: activation record for %d tokens", rows);
+        m->h16_cap = cap;
+    }
     m->rows = rows;
     return LLMQ_OK;
 }
@@ -621,12 +714,20 @@ const float *gain(const llmq_llama *m, int layer, int which) {  // which: 0 attn
     return m->norms + ((size_t)2 * layer + which) * m->cfg.dim;
 }
 
+// Whether the several-row matmul by w takes an h16 record its producer
+// writes (Q4_K rows whose inputs are whole superblocks) and
+// LLMQ_GEMM_H16=0 does not turn the fp16 matrix cores off.
+bool rec_ok(const llmq_llama *m, const llmq_mat *w) {
+    const char *he = getenv("LLMQ_GEMM_H16");
+    return m->h16 && gguf_gemm_h16_ok(w) && !(he && he[0] == '0');
+}
+
 // A GGUF matmul of R rows: the one-token GEMV for R == 1, else the
 // several-token matmul.
 int linear(llmq_llama *m, const llmq_mat *w, const float *x, int64_t ldx, int R, float *out, int64_t ldo,
            int flags) {
     if (R == 1) return launch_gguf_gemv(m->ctx, w, x, out, nullptr, flags, nullptr, 0);
-    return launch_gguf_gemm(m->ctx, w, x, ldx, R, out, ldo, nullptr, flags);
+    return launch_gguf_gemm(m->ctx, w, x, ldx, R, out, ldo, nullptr, flags, m->h16, m->h16_cap);
 }
 
 // rmsnorm(x) * g then the matmul: for one row the GEMV normalizes the row it
@@ -634,9 +735,18 @@ int linear(llmq_llama *m, const llmq_mat *w, const float *x, int64_t ldx, int R,
 int norm_linear(llmq_llama *m, const float *g, const llmq_mat *w, int R, float *out, int64_t ldo, int flags) {
     const llmq_llama_cfg &c = m->cfg;
     if (R == 1) return launch_gguf_gemv(m->ctx, w, m->x, out, nullptr, flags, nullptr, 0, g, c.eps);
+    if (rec_ok(m, w)) {  // the norm writes the Q4_K matmul's fp16 record directly
+        uint8_t *pl;
+        _Float16 *su;
+        float *iv;
+        h16_rec_parts(m->h16, R, c.dim, &pl, &su, &iv);
+        hipLaunchKernelGGL(rmsnorm_rec_kernel, dim3(R), dim3(256), 0, m->ctx->stream, m->x, (int64_t)c.dim, g, c.dim,
+                           c.eps, pl, su, iv);
+        return launch_gguf_gemm_h16(m->ctx, w, m->h16, R, out, ldo, nullptr, flags);
+    }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(256), 0, m->ctx->stream, m->x, (int64_t)c.dim, g, m->xn,
                        (int64_t)c.dim, c.dim, c.eps);
-    return launch_gguf_gemm(m->ctx, w, m->xn, c.dim, R, out, ldo, nullptr, flags);
+    return launch_gguf_gemm(m->ctx, w, m->xn, c.dim, R, out, ldo, nullptr, flags, m->h16, m->h16_cap);
 }
 
 // The layers for R = nseq * T rows in m->x: T tokens of sequences seq0 ..
@@ -664,6 +774,14 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
             if (R == 1 && gguf_gemv_attn_ok(m->wo[l], NS)) {  // Wo combines the splits as it stages its row
                 RC(launch_gguf_gemv(ctx, m->wo[l], nullptr, m->x, nullptr, LLMQ_RESID, nullptr, 0, nullptr, 0.0f, 0,
                                     nullptr, nullptr, m->apart, state, kSplit, NS));
+            } else if (rec_ok(m, m->wo[l]) && c.n_head % 4 == 0) {  // the combination writes Wo's record
+                uint8_t *pl;
+                _Float16 *su;
+                float *iv;
+                h16_rec_parts(m->h16, R, c.dim, &pl, &su, &iv);
+                hipLaunchKernelGGL(attend_combine_rec_kernel, dim3(c.n_head / 4, R), dim3(256), 0, ctx->stream,
+                                   m->apart, NS, c.n_head, state, pl, su, iv);
+                RC(launch_gguf_gemm_h16(ctx, m->wo[l], m->h16, R, m->x, c.dim, nullptr, LLMQ_RESID));
             } else {
                 hipLaunchKernelGGL(attend_combine_kernel, dim3(c.n_head, R), dim3(HD), 0, ctx->stream, m->apart, NS,
                                    c.n_head, state, m->att, (int64_t)c.dim);
@@ -680,6 +798,14 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
         RC(norm_linear(m, gain(m, l, 1), m->wgu[l], R, m->gu, 2 * c.ffn, 0));
         if (R == 1) {  // the GEMV forms silu(gate) * up as it stages its row
             RC(launch_gguf_gemv(ctx, m->wdown[l], m->gu, m->x, nullptr, LLMQ_RESID, nullptr, 0, nullptr, 0.0f, 1));
+        } else if (rec_ok(m, m->wdown[l])) {  // silu(gate) * up written as the down matmul's record
+            uint8_t *pl;
+            _Float16 *su;
+            float *iv;
+            h16_rec_parts(m->h16, R, c.ffn, &pl, &su, &iv);
+            hipLaunchKernelGGL(swiglu_rec_kernel, dim3(c.ffn / 256, R), dim3(256), 0, ctx->stream, m->gu,
+                               (int64_t)2 * c.ffn, c.ffn, pl, su, iv);
+            RC(launch_gguf_gemm_h16(ctx, m->wdown[l], m->h16, R, m->x, c.dim, nullptr, LLMQ_RESID));
         } else {
             hipLaunchKernelGGL(swiglu_kernel, dim3((c.ffn + 255) / 256, R), dim3(256), 0, ctx->stream, m->gu,
                                (int64_t)2 * c.ffn, m->hh, (int64_t)c.ffn, c.ffn);
@@ -758,7 +884,7 @@ int llmq_llama_free(llmq_llama *m) {
     for (auto *w : m->wgu) llmq_mat_free(w);
     for (auto *w : m->wdown) llmq_mat_free(w);
     void *bufs[] = {m->hparts, m->apart, m->rope, m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
-                    m->tokens, m->next, m->gen, m->state};
+                    m->h16, m->tokens, m->next, m->gen, m->state};
     for (void *p : bufs) hipFree(p);
     delete m;
     return LLMQ_OK;

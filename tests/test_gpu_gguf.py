@@ -166,6 +166,43 @@ def test_gguf_matmul_several_tokens(gpu, orc, kind, rows, cols, T):
     assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
 
 
+@pytest.mark.parametrize("h16", ["1", "0"])
+def test_gguf_q4k_matmul_activation_range(gpu, orc, monkeypatch, h16):
+    """The several-token Q4_K matmul over activations of very different
+    sizes: a zero token, tokens of scale 1e-30, 1e-6, 1 and 1e3, and one
+    whose inputs alternate between 1e4 and 1e-4.  Each token's outputs within
+    1e-5 of its own max |out| of the oracle's GEMV (exactly 0 for the zero
+    token), on the fp16 matrix cores (per-sub-block power-of-two scales and
+    two fp16 planes) and, with LLMQ_GEMM_H16=0, on the fp32 ones."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    monkeypatch.setenv("LLMQ_GEMM_H16", h16)
+    t = orc.GGML["Q4_K"]
+    rows, cols = 96, 768
+    blocks = synth.gguf_blocks(t, rows, cols, seed=31)
+    rng = np.random.default_rng(31)
+    x = rng.normal(0, 1, (7, cols)).astype(np.float32)
+    x[0] = 0.0
+    for i, sc in ((1, 1e-30), (2, 1e-6), (3, 1.0), (4, 1e3)):
+        x[i] *= sc
+    x[5] = np.where(np.arange(cols) % 2 == 0, 1e4, 1e-4) * np.sign(x[5])
+    x[6, 100:] = 0.0  # one token nonzero over the first 100 inputs only
+    print("gguf q4k activation range", h16, flush=True)
+    g = lm.HipGGUFMatrix.from_blocks(ctx, t, blocks, rows, cols)
+    out = dev(torch, np.zeros((7, rows), np.float32))
+    lm.linear(ctx, out, dev(torch, x), g)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for i in range(7):
+        want = orc.gguf_gemv(t, blocks, rows, cols, x[i], None, 0)
+        m = np.max(np.abs(want))
+        if m == 0:
+            assert np.all(got[i] == 0), i
+        else:
+            assert np.max(np.abs(got[i] - want)) / m < 1e-5, (i, np.max(np.abs(got[i] - want)) / m)
+
+
 def test_gguf_file_matrices_and_llama(gpu, tmp_path):
     """GGUFFile.matrix (gguf.mojo:622-633) gives the matrix the blocks give,
     and a config-4 decoder read from a GGUF file computes what the same

@@ -294,13 +294,60 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
     }
 }
 
-// attend_split_kernel's arithmetic for the G = n_head / n_kv query heads of
-// key / value head blockIdx.x together (sequence blockIdx.y, split
-// blockIdx.z): the split's cache rows are read once for the G heads.  Thread
-// t holds position s0 + t for every head's score; then wave w sums values
-// for positions w, w + kSW, .. of every head (lane = dimension), the waves
-// added in order.  Partials as attend_split_kernel's, per query head.
-template <int G>
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// Maximum / sum over the 4 rows of 16 lanes (lanes l % 16 + 16 g).
+__device__ __forceinline__ float rows4_max(float v) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+__device__ __forceinline__ float rows4_sum(float v) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// 8 bytes (a, b) as fp16 1024 + byte, in order.
+__device__ __forceinline__ v8h bytes8_f16(uint32_t a, uint32_t b, v2h sub) {
+    const uint32_t d[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
+    v8h r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const v2h h = __builtin_bit_cast(v2h, d[i]) - sub;
+        r[2 * i] = h[0];
+        r[2 * i + 1] = h[1];
+    }
+    return r;
+}
+
+// x as two fp16 planes, hi = fp16(x), lo = fp16(x - hi).
+__device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// Decode attention of the 8 query heads of key / value head blockIdx.x
+// (sequence blockIdx.y, split blockIdx.z of 256 positions) on the fp16
+// matrix cores, for batches: the same scores, softmax and value sums as
+// attend_split_kernel, with its RoPE, cache store and partial layout, and
+// the split's cache rows read once for the 8 heads.  Scores
+// q . (u - 128) ks / 8 over the byte codes u = k + 128 (exact in fp16)
+// against the query as hi / lo fp16 planes; values sum_p (e_p vs_p) v_p
+// with e vs as hi / lo planes under a power-of-two scale of the split (the
+// largest vs below 2^10) and v exact.  Wave w scores positions 64 w ..
+// 64 w + 63 (lane l: head l % 16, positions 4 (l / 16) + i of each
+// 16-position tile, heads 8..15 empty) and forms their value sums for all 64
+// dimensions from the same registers; the waves' sums are added in order.
+// Sums are in the matrix cores' order, so results agree with
+// attend_split_kernel to float rounding, not bit for bit.
 __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float *__restrict__ qkv, int64_t ld,
                                                                     const int *__restrict__ state, int n_head,
                                                                     int n_kv, int n_layer, int layer, int max_t,
@@ -308,19 +355,18 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
                                                                     int8_t *__restrict__ K8, int8_t *__restrict__ V8,
                                                                     float *__restrict__ KS, float *__restrict__ VS,
                                                                     float *__restrict__ part, int NS) {
+    constexpr int G = 8, KR = HD + 8;  // heads; key row stride in LDS (bytes)
     static_assert(G * HD == 2 * kSplit, "two query values a thread");
-    __shared__ __align__(16) float q[G][HD];
+    __shared__ __align__(16) uint8_t ku[kSplit][KR];
     __shared__ __align__(16) int8_t vrow[kSplit][HD];
-    __shared__ __align__(16) int8_t knew[HD];
-    __shared__ __align__(16) float wv[G][kSplit];
-    __shared__ float red[G][kSW], redt[G][kSW], smax[G], snew[2], s_qsum[G];
+    __shared__ __align__(16) _Float16 qh[2][G][HD];  // query hi / lo planes
+    __shared__ float ksv[kSplit], vsv[kSplit], s_qsum[G], red[kSW][G], redt[kSW][G], vmx[kSW];
     __shared__ __align__(16) float vred[kSW][G][HD];
     const int kvh = blockIdx.x, b = blockIdx.y, j = blockIdx.z, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int s0 = j * kSplit, h0 = kvh * G;
     const int64_t slot0 = ((int64_t)b * n_layer + layer) * max_t;
     const float *r = qkv + (int64_t)b * ld;
-    // queries (two values a thread: head-major index tid and tid + kSplit,
-    // so a wave holds one head's 64 dimensions), new key and value, cache
+    // queries (head w and w + 4, dimension lane), new key and value, cache
     // rows, all before the position
     const float qa = r[h0 * HD + tid], qb = r[h0 * HD + kSplit + tid];
     float kvx = 0.0f, vvx = 0.0f;
@@ -342,21 +388,28 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
     const bool valid = tid < cnt;
     const bool has_new = s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
     const bool is_new = has_new && tid == cnt - 1;
-    if (valid && !is_new) {
+    if (!is_new) {
 #pragma unroll
-        for (int i = 0; i < HD / 16; i++) reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
+        for (int i = 0; i < HD / 16; i++) {
+            const int4 k4 = kr[i];
+            reinterpret_cast<int4 *>(&ku[tid][16 * i])[0] =
+                make_int4(k4.x ^ 0x80808080, k4.y ^ 0x80808080, k4.z ^ 0x80808080, k4.w ^ 0x80808080);
+            reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
+        }
+        ksv[tid] = valid ? ks : 0.0f;
+        vsv[tid] = valid ? vs : 0.0f;
     }
-    // RoPE of pair (2i, 2i + 1), i = d / 2: every thread its two query
-    // values (heads w and w + kSW), wave 1 also the new key, which it
-    // quantizes with the new value
+    float vm = wave_max(valid && !is_new ? vs : 0.0f);
+    // RoPE of pair (2i, 2i + 1), i = d / 2, as attend_split_kernel's; wave 1
+    // also rotates the new key and quantizes it with the new value
     {
         const int d = lane;
         const float2 csn = rope[pos * (HD / 2) + (d >> 1)];
         const float pa = llmq_dppf<0xB1>(qa), pb = llmq_dppf<0xB1>(qb);  // lane d ^ 1
         const float ra = (d & 1) ? pa * csn.y + qa * csn.x : qa * csn.x - pa * csn.y;
         const float rb = (d & 1) ? pb * csn.y + qb * csn.x : qb * csn.x - pb * csn.y;
-        q[w][d] = ra;
-        q[w + kSW][d] = rb;
+        split_f16(ra, qh[0][w][d], qh[1][w][d]);
+        split_f16(rb, qh[0][w + kSW][d], qh[1][w + kSW][d]);
         const float sa = wave_sum(ra), sb = wave_sum(rb);
         if (d == 0) {
             s_qsum[w] = sa;
@@ -374,92 +427,116 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
                 const float inv = 1.0f / sc;
                 const int8_t code = (int8_t)llmq_to_int(roundf(x * inv));
                 if (kv == 0)
-                    knew[d] = code;
+                    ku[cnt - 1][d] = (uint8_t)(code ^ 0x80);
                 else
                     vrow[cnt - 1][d] = code;
-                if (d == 0) snew[kv] = sc;
+                if (d == 0) (kv == 0 ? ksv : vsv)[cnt - 1] = sc;
+                vm = kv == 1 ? fmaxf(vm, sc) : vm;
                 (kv == 0 ? K8 : V8)[sn * HD + d] = code;  // this workgroup is the head's only writer
                 if (d == 0) (kv == 0 ? KS : VS)[sn] = sc;
             }
         }
     }
+    if (lane == 0) vmx[w] = vm;
     __syncthreads();
-    if (is_new) {
-        ks = snew[0];
-        vs = snew[1];
-    }
-    // scores of this position for the G heads: q . (u - 128) over the codes
-    // u = k + 128, the 64 codes converted once
-    float u[HD];
+    // the value weights' scale: vs_max sigma < 2^10, a power of two
+    int ex = 0;
+    frexpf(fmaxf(fmaxf(vmx[0], vmx[1]), fmaxf(vmx[2], vmx[3])), &ex);
+    const int sig_e = min(126, max(-126, 10 - ex));
+    const float sigma = ldexpf(1.0f, sig_e);
+    const int hl = lane & 15, g = lane >> 4;
+    const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+    // the query operand (dimensions 32 kb + 8 g .., hi and lo planes), heads 8..15 zero
+    v8h bq[2][2];
 #pragma unroll
-    for (int i = 0; i < HD / 16; i++) {
-        const int4 k4 = is_new ? reinterpret_cast<const int4 *>(knew)[i] : kr[i];
-        const uint32_t kw[4] = {(uint32_t)k4.x ^ 0x80808080u, (uint32_t)k4.y ^ 0x80808080u,
-                                (uint32_t)k4.z ^ 0x80808080u, (uint32_t)k4.w ^ 0x80808080u};
+    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int e4 = 0; e4 < 4; e4++) {
-            u[16 * i + 4 * e4] = (float)(kw[e4] & 255u);
-            u[16 * i + 4 * e4 + 1] = (float)((kw[e4] >> 8) & 255u);
-            u[16 * i + 4 * e4 + 2] = (float)((kw[e4] >> 16) & 255u);
-            u[16 * i + 4 * e4 + 3] = (float)(kw[e4] >> 24);
+        for (int pl = 0; pl < 2; pl++) {
+            const uint4 t = hl < G ? *reinterpret_cast<const uint4 *>(&qh[pl][hl & 7][32 * kb + 8 * g])
+                                   : make_uint4(0u, 0u, 0u, 0u);
+            bq[kb][pl] = __builtin_bit_cast(v8h, t);
+        }
+    const float qs = s_qsum[hl & 7];
+    // scores of the wave's 4 tiles of 16 positions
+    float sc[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int pt = 0; pt < 4; pt++) {
+        const int pb = 64 * w + 16 * pt;
+        v4f d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            const uint2 kk = *reinterpret_cast<const uint2 *>(&ku[pb + hl][32 * kb + 8 * g]);
+            const v8h ak = bytes8_f16(kk.x, kk.y, k1024);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bq[kb][0], d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bq[kb][1], d, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = pb + 4 * g + i;
+            const float v = (d[i] - 128.0f * qs) * ksv[p] * (1.0f / sqrtf((float)HD));
+            sc[pt][i] = p < cnt && hl < G ? v : -INFINITY;
+            mx = fmaxf(mx, sc[pt][i]);
         }
     }
-    // one head at a time (the query reads of one head in flight); the score
-    // waits in wv until the head's maximum is known
-#pragma unroll 1
-    for (int g = 0; g < G; g++) {
-        const float4 *q4 = reinterpret_cast<const float4 *>(q[g]);
-        float d = 0.0f;
+    mx = rows4_max(mx);
+    if (g == 0 && hl < G) red[w][hl] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0][hl & 7], red[1][hl & 7]), fmaxf(red[2][hl & 7], red[3][hl & 7]));
+    float te = 0.0f;
+    // e vs sigma as hi / lo planes, in the value operand's position order:
+    // element e of K-block c is position 64 w + 32 c + 16 (e / 4) + 4 g + e % 4
+    v8h ph[2], plo[2];
 #pragma unroll
-        for (int e4 = 0; e4 < HD / 4; e4++) {
-            const float4 qq = q4[e4];
-            d = fmaf(qq.x, u[4 * e4], d);
-            d = fmaf(qq.y, u[4 * e4 + 1], d);
-            d = fmaf(qq.z, u[4 * e4 + 2], d);
-            d = fmaf(qq.w, u[4 * e4 + 3], d);
+    for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = 64 * w + 16 * pt + 4 * g + i;
+            const float e = sc[pt][i] == -INFINITY ? 0.0f : expf(sc[pt][i] - M);
+            te += e;
+            _Float16 hi, lo;
+            split_f16(e * vsv[p] * sigma, hi, lo);
+            ph[pt >> 1][4 * (pt & 1) + i] = hi;
+            plo[pt >> 1][4 * (pt & 1) + i] = lo;
         }
-        const float sc = valid ? (d - 128.0f * s_qsum[g]) * ks * (1.0f / sqrtf((float)HD)) : -INFINITY;
-        wv[g][tid] = sc;
-        const float m = wave_max(sc);
-        if (lane == 0) red[g][w] = m;
+    te = rows4_sum(te);
+    if (g == 0 && hl < G) redt[w][hl] = te;
+    // value sums of the wave's positions: dimension tile dt, lane (dim 16 dt
+    // + l % 16, group g), D[head 4 g + i][dim]
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+        v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            uint32_t wv[2] = {0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int p = 64 * w + 32 * c + 16 * (e >> 2) + 4 * g + (e & 3);
+                wv[e >> 2] |= (uint32_t)(uint8_t)(vrow[p][16 * dt + hl] ^ 0x80) << (8 * (e & 3));
+            }
+            const v8h bv = bytes8_f16(wv[0], wv[1], k1152);  // v = (v + 128) + 1024 - 1152
+            o = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[c], bv, o, 0, 0, 0);
+            o = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo[c], bv, o, 0, 0, 0);
+        }
+        if (g < 2) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) vred[w][4 * g + i][16 * dt + hl] = o[i];
+        }
     }
     __syncthreads();
-#pragma unroll 1
-    for (int g = 0; g < G; g++) {
-        float m = red[g][0];
-#pragma unroll
-        for (int i = 1; i < kSW; i++) m = fmaxf(m, red[g][i]);
-        const float e = valid ? expf(wv[g][tid] - m) : 0.0f;
-        wv[g][tid] = e * vs;
-        const float t = wave_sum(e);
-        if (lane == 0) redt[g][w] = t;
-        if (tid == 0) smax[g] = m;  // the split's maximum, kept for the partial
-    }
-    __syncthreads();
-    // values: wave w takes positions w, w + kSW, .. of every head; lane = dim
-    float acc[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) acc[g] = 0.0f;
-    for (int sp = w; sp < cnt; sp += kSW) {
-        const float v = (float)vrow[sp][lane];
-#pragma unroll
-        for (int g = 0; g < G; g++) acc[g] = fmaf(wv[g][sp], v, acc[g]);
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++) vred[w][g][lane] = acc[g];
-    __syncthreads();
+    const float isig = ldexpf(1.0f, -sig_e);
     for (int e = tid; e < G * HD; e += kSplit) {
-        const int g = e / HD, dd = e % HD;
-        float o = vred[0][g][dd];
+        const int gg = e / HD, dd = e % HD;
+        float o = vred[0][gg][dd];
 #pragma unroll
-        for (int i = 1; i < kSW; i++) o += vred[i][g][dd];
-        float *P = part + (((int64_t)b * n_head + h0 + g) * NS + j) * kPart;
-        P[4 + dd] = o;
+        for (int i = 1; i < kSW; i++) o += vred[i][gg][dd];
+        float *P = part + (((int64_t)b * n_head + h0 + gg) * NS + j) * kPart;
+        P[4 + dd] = o * isig;
         if (dd == 0) {
-            P[0] = smax[g];
-            float t = redt[g][0];
+            P[0] = fmaxf(fmaxf(red[0][gg], red[1][gg]), fmaxf(red[2][gg], red[3][gg]));
+            float t = redt[0][gg];
 #pragma unroll
-            for (int i = 1; i < kSW; i++) t += redt[g][i];
+            for (int i = 1; i < kSW; i++) t += redt[i][gg];
             P[1] = t;
         }
     }
@@ -764,7 +841,7 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
             static const char *ge = getenv("LLMQ_ATTN_GROUP");
             const bool grouped = c.n_head == 8 * c.n_kv && (ge ? ge[0] == '1' : R > 1);
             if (grouped)  // the 8 query heads of a key / value head in one workgroup
-                hipLaunchKernelGGL(attend_split_group_kernel<8>, dim3(c.n_kv, R, NS), dim3(kSplit), 0, ctx->stream,
+                hipLaunchKernelGGL(attend_split_group_kernel, dim3(c.n_kv, R, NS), dim3(kSplit), 0, ctx->stream,
                                    m->qkv, (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope,
                                    m->k8, m->v8, m->ks, m->vs, m->apart, NS);
             else

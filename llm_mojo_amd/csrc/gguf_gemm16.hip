@@ -280,12 +280,11 @@ int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int6
     const int per = (int)((NSB + 15) / 16), nw = (int)((NSB + per - 1) / per);
     const unsigned nt = (unsigned)w->ntiles;
     hipStream_t st = ctx->stream;
-    const char *re = getenv("LLMQ_H16_RT");
-    const int rt = re ? atoi(re) : (w->ntiles >= 512 ? 2 : 1);
-    if (nw <= 8 && rt == 4)
+    // wide matrices (gate / up): 4 row tiles a workgroup share the record
+    // loads (one round of 176 workgroups at 11264 rows; 1, 2 and 4 tiles
+    // measured 10.5, 11.9 and 10.1 us at 16 tokens)
+    if (nw <= 8 && w->ntiles >= 512)
         hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 4>), dim3((nt + 3) / 4, ntt), dim3(512), 0, st, a);
-    else if (nw <= 8 && rt == 2)
-        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 2>), dim3((nt + 1) / 2, ntt), dim3(512), 0, st, a);
     else if (nw <= 4)
         hipLaunchKernelGGL((gemm_h16_q4k_kernel<4, 1>), dim3(nt, ntt), dim3(256), 0, st, a);
     else if (nw <= 8)

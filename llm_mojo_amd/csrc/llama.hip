@@ -64,28 +64,31 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 }
 
 // rmsnorm_kernel's row (x r) g written as the h16 record of the several-row
-// Q4_K matmul (llmq_h16_store): wave w takes superblocks w, w + 4, ..
-// (C = 256 NSB).
-__global__ __launch_bounds__(256) void rmsnorm_rec_kernel(const float *__restrict__ x, int64_t ldx,
-                                                          const float *__restrict__ g, int C, float eps,
-                                                          uint8_t *__restrict__ planes, _Float16 *__restrict__ sums,
-                                                          float *__restrict__ inv) {
-    __shared__ float red[4];
-    const float *xr = x + (int64_t)blockIdx.x * ldx;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < C; i += 256) ss = fmaf(xr[i], xr[i], ss);
-    ss = block_sum(ss, red);
-    const float r = 1.0f / sqrtf(ss / (float)C + eps);
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, NSB = C / 256;
-    for (int sb = w; sb < NSB; sb += 4) {
-        float v[4];
+// Q4_K matmul (llmq_h16_store): one wave a (superblock blockIdx.x, row
+// blockIdx.y), each wave forming the row's sum of squares itself
+// (C = 256 NSB, a multiple of 256).
+__global__ __launch_bounds__(64) void rmsnorm_rec_kernel(const float *__restrict__ x, int64_t ldx,
+                                                         const float *__restrict__ g, int C, float eps,
+                                                         uint8_t *__restrict__ planes, _Float16 *__restrict__ sums,
+                                                         float *__restrict__ inv) {
+    const float *xr = x + (int64_t)blockIdx.y * ldx;
+    const int lane = threadIdx.x, sb = blockIdx.x;
+    float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int i = sb * 256 + 64 * q + lane;
-            v[q] = (xr[i] * r) * g[i];
-        }
-        llmq_h16_store(planes, sums, inv, C / 32, NSB, blockIdx.x, sb, v, true);
+    for (int q = 0; q < 4; q++) v[q] = xr[sb * 256 + 64 * q + lane];
+    float ss = 0.0f;
+    for (int i = 4 * lane; i < C; i += 256) {
+        const float4 t = *reinterpret_cast<const float4 *>(xr + i);
+        ss = fmaf(t.x, t.x, ss);
+        ss = fmaf(t.y, t.y, ss);
+        ss = fmaf(t.z, t.z, ss);
+        ss = fmaf(t.w, t.w, ss);
     }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)C + eps);
+#pragma unroll
+    for (int q = 0; q < 4; q++) v[q] = (v[q] * r) * g[sb * 256 + 64 * q + lane];
+    llmq_h16_store(planes, sums, inv, C / 32, C / 256, blockIdx.y, sb, v, true);
 }
 
 // RoPE and the cache store of a prompt: row `row` of qkv is token t = row % T
@@ -817,8 +820,8 @@ int norm_linear(llmq_llama *m, const float *g, const llmq_mat *w, int R, float *
         _Float16 *su;
         float *iv;
         h16_rec_parts(m->h16, R, c.dim, &pl, &su, &iv);
-        hipLaunchKernelGGL(rmsnorm_rec_kernel, dim3(R), dim3(256), 0, m->ctx->stream, m->x, (int64_t)c.dim, g, c.dim,
-                           c.eps, pl, su, iv);
+        hipLaunchKernelGGL(rmsnorm_rec_kernel, dim3(c.dim / 256, R), dim3(64), 0, m->ctx->stream, m->x,
+                           (int64_t)c.dim, g, c.dim, c.eps, pl, su, iv);
         return launch_gguf_gemm_h16(m->ctx, w, m->h16, R, out, ldo, nullptr, flags);
     }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(256), 0, m->ctx->stream, m->x, (int64_t)c.dim, g, m->xn,

@@ -188,22 +188,28 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
         vr[i] = reinterpret_cast<const int4 *>(V8 + sl * HD)[i];
     }
     float ks = KS[sl], vs = VS[sl];
+    // The position's read goes out after these loads and before their first
+    // use, and nothing branches on the position before that use (the
+    // compiler would move the loads behind the position's round trip):
+    // every row goes to LDS (the new position's written over its slot
+    // below), and an empty split (s0 > pos) runs with cnt = 0, its result
+    // never read.
+    __builtin_amdgcn_sched_barrier(0);
     const int pos = state[0], npos = pos + 1;
-    if (s0 >= npos) return;  // an empty split (uniform over the workgroup; never read)
-    const int cnt = min(kSplit, npos - s0);
-    const bool valid = tid < cnt;
-    const bool has_new = s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
-    const bool is_new = has_new && tid == cnt - 1;
-    if (valid && !is_new) {
+    const float2 csn = rope[pos * (HD / 2) + (lane >> 1)];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < HD / 16; i++) reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
-    }
+    for (int i = 0; i < HD / 16; i++) reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
+    const int cnt = max(0, min(kSplit, npos - s0));
+    const bool valid = tid < cnt;
+    const bool has_new = cnt > 0 && s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
+    const bool is_new = has_new && tid == cnt - 1;
+    __syncthreads();  // the cached rows are in before the new one goes over its slot
     // RoPE of pair (2i, 2i + 1), i = d / 2, by the table's angle:
     // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c); wave 0 the query, wave 1 the
     // new key, which it quantizes with the new value
     if (w == 0 || (w == 1 && has_new)) {
         const int d = lane;
-        const float2 csn = rope[pos * (HD / 2) + (d >> 1)];
         const float v = w == 0 ? qv : kvx, pv = llmq_dppf<0xB1>(v);  // lane d ^ 1
         const float rot = (d & 1) ? pv * csn.y + v * csn.x : v * csn.x - pv * csn.y;
         if (w == 0) {
@@ -384,30 +390,33 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
         kr[i] = reinterpret_cast<const int4 *>(K8 + sl * HD)[i];
         vr[i] = reinterpret_cast<const int4 *>(V8 + sl * HD)[i];
     }
-    float ks = KS[sl], vs = VS[sl];
+    const float ks = KS[sl], vs = VS[sl];
+    // the position's read between the loads and their first use, as in
+    // attend_split_kernel; scales of positions past the split's end are not
+    // used (scores are masked, the value weights selected to 0)
+    __builtin_amdgcn_sched_barrier(0);
     const int pos = state[0], npos = pos + 1;
-    if (s0 >= npos) return;  // an empty split (uniform over the workgroup; never read)
-    const int cnt = min(kSplit, npos - s0);
-    const bool valid = tid < cnt;
-    const bool has_new = s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
-    const bool is_new = has_new && tid == cnt - 1;
-    if (!is_new) {
+    const float2 csn = rope[pos * (HD / 2) + (lane >> 1)];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < HD / 16; i++) {
-            const int4 k4 = kr[i];
-            reinterpret_cast<int4 *>(&ku[tid][16 * i])[0] =
-                make_int4(k4.x ^ 0x80808080, k4.y ^ 0x80808080, k4.z ^ 0x80808080, k4.w ^ 0x80808080);
-            reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
-        }
-        ksv[tid] = valid ? ks : 0.0f;
-        vsv[tid] = valid ? vs : 0.0f;
+    for (int i = 0; i < HD / 16; i++) {
+        const int4 k4 = kr[i];
+        reinterpret_cast<int4 *>(&ku[tid][16 * i])[0] =
+            make_int4(k4.x ^ 0x80808080, k4.y ^ 0x80808080, k4.z ^ 0x80808080, k4.w ^ 0x80808080);
+        reinterpret_cast<int4 *>(vrow[tid])[i] = vr[i];
     }
+    ksv[tid] = ks;
+    vsv[tid] = vs;
+    const int cnt = max(0, min(kSplit, npos - s0));
+    const bool valid = tid < cnt;
+    const bool has_new = cnt > 0 && s0 + cnt == npos;  // the last split holds pos at tid cnt - 1
+    const bool is_new = has_new && tid == cnt - 1;
     float vm = wave_max(valid && !is_new ? vs : 0.0f);
+    __syncthreads();  // the cached rows are in before the new one goes over its slot
     // RoPE of pair (2i, 2i + 1), i = d / 2, as attend_split_kernel's; wave 1
     // also rotates the new key and quantizes it with the new value
     {
         const int d = lane;
-        const float2 csn = rope[pos * (HD / 2) + (d >> 1)];
         const float pa = llmq_dppf<0xB1>(qa), pb = llmq_dppf<0xB1>(qb);  // lane d ^ 1
         const float ra = (d & 1) ? pa * csn.y + qa * csn.x : qa * csn.x - pa * csn.y;
         const float rb = (d & 1) ? pb * csn.y + qb * csn.x : qb * csn.x - pb * csn.y;
@@ -498,7 +507,7 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
             const float e = sc[pt][i] == -INFINITY ? 0.0f : expf(sc[pt][i] - M);
             te += e;
             _Float16 hi, lo;
-            split_f16(e * vsv[p] * sigma, hi, lo);
+            split_f16(e * (p < cnt ? vsv[p] : 0.0f) * sigma, hi, lo);
             ph[pt >> 1][4 * (pt & 1) + i] = hi;
             plo[pt >> 1][4 * (pt & 1) + i] = lo;
         }

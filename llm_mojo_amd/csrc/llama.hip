@@ -736,7 +736,8 @@ struct llmq_llama {
     float *ks = nullptr, *vs = nullptr;
     // activations for up to `rows` tokens
     int rows = 0;
-    ArgmaxPart *hparts = nullptr;  // head argmax partials, batch x gguf_head16_parts
+    ArgmaxPart *hparts = nullptr;  // head argmax partials, batch x nhparts
+    int nhparts = 0;               // the int16 head's partials a row, fixed at creation
     float *apart = nullptr;        // decode attention split results, batch x heads x splits x kPart
     float2 *rope = nullptr;        // (cos, sin) of position p, pair i at [p * head_dim / 2 + i]
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *hh = nullptr,
@@ -916,9 +917,13 @@ int llama_head(llmq_llama *m, int r0, int nrows, ArgmaxPart *parts = nullptr, bo
     if (has_parts) *has_parts = false;
     // the int16 head normalizes the rows it quantizes
     if (gguf_has_i16(m->head)) {
+        // the pick reads exactly nhparts partials a row
+        LLMQ_REQUIRE(!parts || gguf_head16_parts(m->head) == m->nhparts,
+                     "llama head: %d argmax partials a row, the model reads %d", gguf_head16_parts(m->head),
+                     m->nhparts);
         if (has_parts) *has_parts = parts != nullptr;
         return launch_gguf_head16(ctx, m->head, x, m->logits, nrows, g, c.eps, parts,
-                                  parts ? nrows * gguf_head16_parts(m->head) : 0);
+                                  parts ? nrows * m->nhparts : 0);
     }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(nrows), dim3(256), 0, ctx->stream, x, (int64_t)c.dim, g, m->xn,
                        (int64_t)c.dim, c.dim, c.eps);
@@ -935,7 +940,7 @@ int llama_step(llmq_llama *m, int B) {
     bool parts = false;
     RC(llama_head(m, 0, B, m->hparts, &parts));
     if (parts)
-        return launch_gguf_pick_embed(ctx, m->embd, m->hparts, gguf_head16_parts(m->head), B, m->state, m->next,
+        return launch_gguf_pick_embed(ctx, m->embd, m->hparts, m->nhparts, B, m->state, m->next,
                                       m->gen, m->x, c.dim);
     hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(kArgNT), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab, B,
                        0, m->state, 1, m->next, m->gen);
@@ -1050,8 +1055,9 @@ int llmq_llama_create(llmq_ctx *ctx, const llmq_llama_cfg *cfg, const void *cons
             hipMemset(m->ks, 0, slots * 4) != hipSuccess || hipMemset(m->vs, 0, slots * 4) != hipSuccess)
             GO(llmq_set_error(LLMQ_EHIP, "llama: cache clear"));
         GO(ensure_rows(m, c.batch));
+        if (gguf_has_i16(m->head)) m->nhparts = gguf_head16_parts(m->head);
         if (gguf_has_i16(m->head) &&
-            hipMalloc(&m->hparts, sizeof(ArgmaxPart) * c.batch * gguf_head16_parts(m->head)) != hipSuccess)
+            hipMalloc(&m->hparts, sizeof(ArgmaxPart) * c.batch * m->nhparts) != hipSuccess)
             GO(llmq_set_error(LLMQ_ENOMEM, "llama: head partials"));
         if (hipMalloc(&m->apart, sizeof(float) * c.batch * c.n_head * ((c.max_t + kSplit - 1) / kSplit) * kPart) !=
             hipSuccess)

@@ -138,13 +138,15 @@ def test_gguf_float_heads_take_the_float_path(gpu, orc):
 
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("rows,cols,T", [(70, 512, 5), (300, 2048, 16), (200, 4352, 33), (256, 5632, 17),
-                                         (100, 544, 20)])
+                                         (100, 544, 20), (200, 2048, 130), (72, 4352, 70)])
 def test_gguf_matmul_several_tokens(gpu, orc, kind, rows, cols, T):
     """matmul_rows for T > 1 (kernels.mojo:314-349): every token's outputs
     within 1e-5 of max |out| of the oracle's one-token GEMV (the same
     dequantized weights; float sums in another order).  (200, 4352): 17
     superblocks a row; (256, 5632): TinyLlama's FFN down projection shape;
-    (100, 544): a reduction axis that ends mid-block (Q4_0 / Q4_1 / Q8_0 only)."""
+    (100, 544): a reduction axis that ends mid-block (Q4_0 / Q4_1 / Q8_0 only);
+    130 and 70 tokens: Q4_K's prompt form (records staged in LDS, 4 token
+    tiles a workgroup, the last group part-filled)."""
     torch, lm, ctx = gpu
     from llm_mojo_amd import synth
 

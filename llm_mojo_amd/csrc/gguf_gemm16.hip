@@ -213,150 +213,176 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
     }
 }
 
-// The same matmul for many tokens (prompts): a workgroup of 8 waves owns 4
+// The same matmul for many tokens (prompts): a workgroup of 8 waves owns 8
 // row tiles and kPT token tiles; each superblock's record for those tokens
 // (kPT x 16 KiB of planes, their sums and scales) is copied into LDS by the
 // global-to-LDS loads, double-buffered so the next superblock's copy runs
-// under this one's products, and wave w decodes row tile w % 4's codes once
-// and multiplies them with token tiles 2 (w / 4) and 2 (w / 4) + 1.  Each
+// under this one's products.  Wave w decodes the codes of row tiles w % 4
+// and w % 4 + 4 once and multiplies them with token tiles 2 (w / 4) and
+// 2 (w / 4) + 1, each operand read from LDS serving two products.  Each
 // wave covers the whole reduction axis, so no partial sums are combined.
 constexpr int kPT = 4;                                        // token tiles a workgroup
 constexpr int kPL = 16384;                                    // planes bytes of a token tile's superblock
 constexpr int kStage = kPT * kPL + kPT * 512 + 1024;          // planes, sums, inv (padded)
+constexpr int kRW = 2;                                        // row tiles a wave
 
 __global__ __launch_bounds__(512) void gemm_h16_q4k_lds_kernel(HArgs a, int ntt) {
-    __shared__ __align__(16) uint8_t st[2][kStage];
+    // two separate buffers, so that the compiler sees a copy into one cannot alias reads of the other
+    __shared__ __align__(16) uint8_t st0[kStage], st1[kStage];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c16 = lane & 15, g = lane >> 4;
-    const int rt = blockIdx.x * 4 + (w & 3), th = w >> 2, tt0 = blockIdx.y * kPT;
-    const bool rok = rt < a.ntiles;
+    const int th = w >> 2, tt0 = blockIdx.y * kPT;
+    int rt[kRW];
+    bool rok[kRW];
+#pragma unroll
+    for (int r = 0; r < kRW; r++) {
+        rt[r] = blockIdx.x * 4 * kRW + (w & 3) + 4 * r;
+        rok[r] = rt[r] < a.ntiles;
+    }
     const auto rc = make_rsrc(a.codes, a.codes_bytes), rs = make_rsrc(a.sb, a.sb_bytes);
     const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, km1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     // the copy of superblock s into buffer b: planes in 8 rounds of 512 x 16 bytes, sums by waves 0-1,
     // scales by wave 2 (tiles past the record read tile 0; their outputs are not written)
-    auto stage = [&](int s, int b) {
+    auto stage = [&](int s, uint8_t *buf) {
 #pragma unroll
         for (int r = 0; r < 8; r++) {
             const int t = r >> 1, tt = tt0 + t < ntt ? tt0 + t : 0;
             const uint8_t *src = a.planes + ((int64_t)tt * a.KB + 8 * s) * 2048 + (r & 1) * 8192 + tid * 16;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(&st[b][t * kPL + (r & 1) * 8192 + w * 1024]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(buf + t * kPL + (r & 1) * 8192 + w * 1024), 16, 0, 0);
         }
         if (w < 2) {
             const int t = tid >> 5, tt = tt0 + t < ntt ? tt0 + t : 0;
             const uint8_t *src = a.sums + ((int64_t)tt * a.NSB + s) * 512 + (tid & 31) * 16;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(&st[b][kPT * kPL + w * 1024]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(buf + kPT * kPL + w * 1024), 16, 0, 0);
         } else if (w == 2) {
             const int t = (lane >> 2) & 3, tt = tt0 + t < ntt ? tt0 + t : 0;
             const uint8_t *src = a.inv + ((int64_t)tt * a.NSB + s) * 64 + (lane & 3) * 16;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(&st[b][kPT * kPL + kPT * 512]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(buf + kPT * kPL + kPT * 512), 16, 0, 0);
         }
     };
-    auto load_codes = [&](int s, uint4 &f, uint32_t (&cw)[8]) {
-        f = bload16(rs, rok ? (uint32_t)(((rt * a.NSB + s) * 16 + c16) * 16) : kOOB);
-        const uint32_t cb = rok ? (uint32_t)(((rt * a.CK + s * 8) * 16 + c16) * 16 + g * 4) : kOOB;
+    auto load_codes = [&](int s, uint4 (&f)[kRW], uint32_t (&cw)[kRW][8]) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) cw[u] = bload4(rc, cb + 256u * u);
+        for (int r = 0; r < kRW; r++) {
+            f[r] = bload16(rs, rok[r] ? (uint32_t)(((rt[r] * a.NSB + s) * 16 + c16) * 16) : kOOB);
+            const uint32_t cb = rok[r] ? (uint32_t)(((rt[r] * a.CK + s * 8) * 16 + c16) * 16 + g * 4) : kOOB;
+#pragma unroll
+            for (int u = 0; u < 8; u++) cw[r][u] = bload4(rc, cb + 256u * u);
+        }
     };
-    float acc[2][4];
+    float acc[kRW][2][4];
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+    for (int r = 0; r < kRW; r++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
-    uint4 f;
-    uint32_t cw[8];
-    stage(0, 0);
-    load_codes(0, f, cw);
-    for (int s = 0; s < a.NSB; s++) {
-        const int b = s & 1;
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[r][t][i] = 0.0f;
+    uint4 f[kRW];
+    uint32_t cw[kRW][8];
+    // superblock s from buffer cur, the next one's copy into nxt
+    auto step = [&](int s, const uint8_t *cur, uint8_t *nxt) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies (and codes) have landed
-        __syncthreads();                     // every wave's copy of s is in; buffer b ^ 1 is free
-        uint4 fn = f;
-        uint32_t cwn[8];
+        __syncthreads();                     // every wave's copy of s is in; nxt is free
+        // this superblock's codes times sc_j, and m_j, as fp16 (as gemm_h16_q4k_kernel)
+        v8h bw[kRW][8], bm[kRW];
+        float dd[kRW], dmin[kRW];
 #pragma unroll
-        for (int u = 0; u < 8; u++) cwn[u] = cw[u];
-        if (s + 1 < a.NSB) {
-            stage(s + 1, b ^ 1);
-            load_codes(s + 1, fn, cwn);
-        }
-        // this row tile's codes times sc_j, and m_j, as fp16 (as gemm_h16_q4k_kernel)
-        const uint32_t sc_lo = f.y & 0x3F3F3F3Fu, m_lo = f.z & 0x3F3F3F3Fu;
-        const uint32_t sc_hi = (f.w & 0x0F0F0F0Fu) | ((f.y >> 2) & 0x30303030u);
-        const uint32_t m_hi = ((f.w >> 4) & 0x0F0F0F0Fu) | ((f.z >> 2) & 0x30303030u);
-        uint32_t scp[4], mp[4];
-        bytes_f16(sc_lo, sc_hi, scp);
-        bytes_f16(m_lo, m_hi, mp);
-        v2h sc[4], nsc[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            sc[i] = __builtin_bit_cast(v2h, scp[i]) - k1024;
-            nsc[i] = sc[i] * km1024;
-        }
-        v8h bw[8], bm;
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t lo = cw[u] & 0x0F0F0F0Fu, hi = (cw[u] >> 4) & 0x0F0F0F0Fu;
-            uint32_t q[4];
-            bytes_f16(lo, hi, q);
-            const _Float16 s1 = sc[u >> 1][u & 1], n1 = nsc[u >> 1][u & 1];
-            const v2h sv = {s1, s1}, nv = {n1, n1};
+        for (int r = 0; r < kRW; r++) {
+            const uint32_t sc_lo = f[r].y & 0x3F3F3F3Fu, m_lo = f[r].z & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (f[r].w & 0x0F0F0F0Fu) | ((f[r].y >> 2) & 0x30303030u);
+            const uint32_t m_hi = ((f[r].w >> 4) & 0x0F0F0F0Fu) | ((f[r].z >> 2) & 0x30303030u);
+            uint32_t scp[4], mp[4];
+            bytes_f16(sc_lo, sc_hi, scp);
+            bytes_f16(m_lo, m_hi, mp);
+            v2h sc[4], nsc[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const v2h pp = __builtin_elementwise_fma(__builtin_bit_cast(v2h, q[i]), sv, nv);
-                bw[u][2 * i] = pp[0];
-                bw[u][2 * i + 1] = pp[1];
+                sc[i] = __builtin_bit_cast(v2h, scp[i]) - k1024;
+                nsc[i] = sc[i] * km1024;
             }
-        }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const v2h pp = g < 2 ? __builtin_bit_cast(v2h, mp[i]) - k1024 : (v2h){(_Float16)0.0f, (_Float16)0.0f};
-            bm[2 * i] = pp[0];
-            bm[2 * i + 1] = pp[1];
+            for (int u = 0; u < 8; u++) {
+                const uint32_t lo = cw[r][u] & 0x0F0F0F0Fu, hi = (cw[r][u] >> 4) & 0x0F0F0F0Fu;
+                uint32_t q[4];
+                bytes_f16(lo, hi, q);
+                const _Float16 s1 = sc[u >> 1][u & 1], n1 = nsc[u >> 1][u & 1];
+                const v2h sv = {s1, s1}, nv = {n1, n1};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const v2h pp = __builtin_elementwise_fma(__builtin_bit_cast(v2h, q[i]), sv, nv);
+                    bw[r][u][2 * i] = pp[0];
+                    bw[r][u][2 * i + 1] = pp[1];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const v2h pp = g < 2 ? __builtin_bit_cast(v2h, mp[i]) - k1024 : (v2h){(_Float16)0.0f, (_Float16)0.0f};
+                bm[r][2 * i] = pp[0];
+                bm[r][2 * i + 1] = pp[1];
+            }
+            dd[r] = __half2float(__ushort_as_half((unsigned short)(f[r].x & 0xFFFFu)));
+            dmin[r] = __half2float(__ushort_as_half((unsigned short)(f[r].x >> 16)));
         }
-        const float dd = __half2float(__ushort_as_half((unsigned short)(f.x & 0xFFFFu)));
-        const float dmin = __half2float(__ushort_as_half((unsigned short)(f.x >> 16)));
+        if (s + 1 < a.NSB) {  // the next superblock's copy and codes go out under these products
+            stage(s + 1, nxt);
+            load_codes(s + 1, f, cw);
+        }
 #pragma unroll
         for (int t2 = 0; t2 < 2; t2++) {
             const int t = 2 * th + t2;
-            const uint8_t *base = &st[b][t * kPL];
-            v4f d = {0.0f, 0.0f, 0.0f, 0.0f};
+            const uint8_t *base = cur + t * kPL;
+            v4f d[kRW];
+#pragma unroll
+            for (int r = 0; r < kRW; r++) d[r] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const uint4 ah = *reinterpret_cast<const uint4 *>(base + u * 2048 + lane * 16);
                 const uint4 al = *reinterpret_cast<const uint4 *>(base + u * 2048 + 1024 + lane * 16);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah), bw[u], d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al), bw[u], d, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < kRW; r++) {
+                    d[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah), bw[r][u], d[r], 0, 0, 0);
+                    d[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al), bw[r][u], d[r], 0, 0, 0);
+                }
             }
-            uint4 sq = *reinterpret_cast<const uint4 *>(&st[b][kPT * kPL + t * 512 + (lane & 31) * 16]);
+            uint4 sq = *reinterpret_cast<const uint4 *>(cur + kPT * kPL + t * 512 + (lane & 31) * 16);
             if (g >= 2) sq = make_uint4(0u, 0u, 0u, 0u);
-            const uint4 iv = *reinterpret_cast<const uint4 *>(&st[b][kPT * kPL + kPT * 512 + t * 64 + g * 16]);
-            v4f dm = {0.0f, 0.0f, 0.0f, 0.0f};
-            dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, sq), bm, dm, 0, 0, 0);
+            const uint4 iv = *reinterpret_cast<const uint4 *>(cur + kPT * kPL + kPT * 512 + t * 64 + g * 16);
             const float inv[4] = {__uint_as_float(iv.x), __uint_as_float(iv.y), __uint_as_float(iv.z),
                                   __uint_as_float(iv.w)};
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[t2][i] = fmaf(inv[i], fmaf(-dmin, dm[i], dd * d[i]), acc[t2][i]);
-        }
-        f = fn;
+            for (int r = 0; r < kRW; r++) {
+                v4f dm = {0.0f, 0.0f, 0.0f, 0.0f};
+                dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, sq), bm[r], dm, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 8; u++) cw[u] = cwn[u];
-    }
-#pragma unroll
-    for (int t2 = 0; t2 < 2; t2++) {
-        const int tt = tt0 + 2 * th + t2;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int tk = tt * 16 + 4 * g + i, o = rt * 16 + c16;
-            if (tt < ntt && o < a.n && tk < a.T) {
-                float v = acc[t2][i];
-                if (a.flags & LLMQ_BIAS) v += a.bias[o];
-                if (a.flags & LLMQ_GELU) v = gelu_ref(v);
-                float *dst = a.out + (int64_t)tk * a.ldo + o;
-                if (a.flags & LLMQ_RESID) v += *dst;
-                *dst = v;
+                for (int i = 0; i < 4; i++)
+                    acc[r][t2][i] = fmaf(inv[i], fmaf(-dmin[r], dm[i], dd[r] * d[r][i]), acc[r][t2][i]);
             }
         }
+    };
+    stage(0, st0);
+    load_codes(0, f, cw);
+    for (int s = 0; s < a.NSB; s += 2) {
+        step(s, st0, st1);
+        if (s + 1 < a.NSB) step(s + 1, st1, st0);
     }
+#pragma unroll
+    for (int r = 0; r < kRW; r++)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++) {
+            const int tt = tt0 + 2 * th + t2;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tk = tt * 16 + 4 * g + i, o = rt[r] * 16 + c16;
+                if (tt < ntt && rok[r] && o < a.n && tk < a.T) {
+                    float v = acc[r][t2][i];
+                    if (a.flags & LLMQ_BIAS) v += a.bias[o];
+                    if (a.flags & LLMQ_GELU) v = gelu_ref(v);
+                    float *dst = a.out + (int64_t)tk * a.ldo + o;
+                    if (a.flags & LLMQ_RESID) v += *dst;
+                    *dst = v;
+                }
+            }
+        }
 }
 
 }  // namespace
@@ -430,8 +456,8 @@ int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int6
     // loads (one round of 176 workgroups at 11264 rows; 1, 2 and 4 tiles
     // measured 10.5, 11.9 and 10.1 us at 16 tokens)
     if (ntt >= (unsigned)kPT)  // prompts: the LDS-staged form
-        hipLaunchKernelGGL(gemm_h16_q4k_lds_kernel, dim3((nt + 3) / 4, (ntt + kPT - 1) / kPT), dim3(512), 0, st, a,
-                           (int)ntt);
+        hipLaunchKernelGGL(gemm_h16_q4k_lds_kernel, dim3((nt + 4 * kRW - 1) / (4 * kRW), (ntt + kPT - 1) / kPT),
+                           dim3(512), 0, st, a, (int)ntt);
     else if (nw <= 8 && w->ntiles >= 512)
         hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 4>), dim3((nt + 3) / 4, ntt), dim3(512), 0, st, a);
     else if (nw <= 4)

@@ -334,15 +334,25 @@ __global__ __launch_bounds__(512) void gemm_h16_q4k_lds_kernel(HArgs a, int ntt)
             v4f d[kRW];
 #pragma unroll
             for (int r = 0; r < kRW; r++) d[r] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+            // the token tile's operands read in two groups of 8 (the LDS counter's reach) ahead of their products
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const uint4 ah = *reinterpret_cast<const uint4 *>(base + u * 2048 + lane * 16);
-                const uint4 al = *reinterpret_cast<const uint4 *>(base + u * 2048 + 1024 + lane * 16);
+            for (int h = 0; h < 8; h += 4) {
+                uint4 ah[4], al[4];
 #pragma unroll
-                for (int r = 0; r < kRW; r++) {
-                    d[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah), bw[r][u], d[r], 0, 0, 0);
-                    d[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al), bw[r][u], d[r], 0, 0, 0);
+                for (int u = 0; u < 4; u++) {
+                    ah[u] = *reinterpret_cast<const uint4 *>(base + (h + u) * 2048 + lane * 16);
+                    al[u] = *reinterpret_cast<const uint4 *>(base + (h + u) * 2048 + 1024 + lane * 16);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int r = 0; r < kRW; r++) {
+                        d[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah[u]), bw[r][h + u], d[r], 0,
+                                                                      0, 0);
+                        d[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al[u]), bw[r][h + u], d[r], 0,
+                                                                      0, 0);
+                    }
             }
             uint4 sq = *reinterpret_cast<const uint4 *>(cur + kPT * kPL + t * 512 + (lane & 31) * 16);
             if (g >= 2) sq = make_uint4(0u, 0u, 0u, 0u);

@@ -744,6 +744,236 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
         if (q < nq) out[(int64_t)(q0 + q) * ldo + (int64_t)h * HD + 16 * w + c16] = acc[i];
     }
 }
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// 8 signed int8 codes (a, b) as exact fp16 values: (c ^ 0x80) = c + 128 as a
+// byte, 0x6400 | byte = 1024 + byte, minus 1152.
+__device__ __forceinline__ v8h s8x8_f16(uint32_t a, uint32_t b) {
+    a ^= 0x80808080u;
+    b ^= 0x80808080u;
+    const uint32_t d[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
+    const v2h k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+    v8h r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const v2h h = __builtin_bit_cast(v2h, d[i]) - k1152;
+        r[2 * i] = h[0];
+        r[2 * i + 1] = h[1];
+    }
+    return r;
+}
+__device__ __forceinline__ float rows4_max_p(float v) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+__device__ __forceinline__ float rows4_sum_p(float v) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// attend_prompt_kernel's attention for the 8 query heads of key / value head
+// blockIdx.x and queries q0 .. q0 + 15 (q0 = 16 blockIdx.y) at once, on the
+// fp16 matrix cores: each staged block of 64 key / value rows serves all 8
+// heads.  Scores k . q with the int8 codes exact in fp16 and q as hi / lo
+// planes; a first pass over the keys finds each query's maximum and the
+// largest value scale, the second forms e = exp(s - max), the weights
+// e vs sigma as hi / lo planes (sigma a power of two, max vs sigma < 2^10)
+// and their products with the value codes.  Wave w owns heads 2w and 2w + 1:
+// in the scores lane l holds query l % 16 and keys 4 (l / 16) + i of each
+// 16-key tile, which is the operand layout of the value products, so the
+// weights never leave registers.  Sums are in the matrix cores' order (float
+// rounding, not attend_prompt_kernel's bits).
+__global__ __launch_bounds__(256) void attend_prompt_gqa_kernel(const float *__restrict__ qkv, int64_t ld, int pos0,
+                                                                int T, int layer, int max_t, int n_kv,
+                                                                const int8_t *__restrict__ K8,
+                                                                const int8_t *__restrict__ V8,
+                                                                const float *__restrict__ KS,
+                                                                const float *__restrict__ VS, float *__restrict__ out,
+                                                                int64_t ldo) {
+    constexpr int HD = 64, G = 8, KR = HD + 8, VR = kPB + 4;  // head dim, heads; LDS row strides (bytes)
+    __shared__ __align__(16) int8_t kr[kPB][KR];
+    __shared__ __align__(16) int8_t vt[HD][VR];
+    __shared__ float ksb[kPB], vsb[kPB], vmx[4], tfin[4][2][16];
+    const int kvh = blockIdx.x, q0 = blockIdx.y * kQB, tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, c16 = lane & 15, g = lane >> 4;
+    const int nq = min(kQB, T - q0);
+    const int npos = pos0 + q0 + nq;  // positions any query of the block sees
+    const int64_t base = (int64_t)layer * max_t * n_kv + kvh;
+    const int qpos = pos0 + q0 + c16;  // the lane's query sees positions <= qpos
+    const bool qok = c16 < nq;
+    // the query operand of head 8 kvh + 2w + r: dims 32 kb + 8 g .., hi and lo planes
+    v8h bq[2][2][2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const float *qr = qkv + (int64_t)(q0 + c16) * ld + (int64_t)(kvh * G + 2 * w + r) * HD;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; e += 4) {
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (qok) v = *reinterpret_cast<const float4 *>(qr + 32 * kb + 8 * g + e);
+                x[e] = v.x;
+                x[e + 1] = v.y;
+                x[e + 2] = v.z;
+                x[e + 3] = v.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const _Float16 hi = (_Float16)x[e];
+                bq[r][kb][0][e] = hi;
+                bq[r][kb][1][e] = (_Float16)(x[e] - (float)hi);
+            }
+        }
+    }
+    // Stage block s0: thread (key tid / 4, piece tid % 4) copies 16 bytes of the
+    // key row (and of the value row into the transposed copy), lane 0 of the
+    // key the scales; rows past npos are zero.
+    auto stage = [&](int s0, bool values) {
+        const int row = tid >> 2, piece = tid & 3, sidx = s0 + row;
+        int4 kv = make_int4(0, 0, 0, 0), vv = make_int4(0, 0, 0, 0);
+        float ks = 0.0f, vs = 0.0f;
+        if (sidx < npos) {
+            const int64_t sl = base + (int64_t)sidx * n_kv;
+            kv = *reinterpret_cast<const int4 *>(K8 + sl * HD + 16 * piece);
+            ks = KS[sl];
+            if (values) {
+                vv = *reinterpret_cast<const int4 *>(V8 + sl * HD + 16 * piece);
+                vs = VS[sl];
+            }
+        }
+        __syncthreads();  // the previous block's reads are done
+        *reinterpret_cast<int4 *>(&kr[row][16 * piece]) = kv;
+        if (piece == 0) {
+            ksb[row] = ks;
+            vsb[row] = vs;
+        }
+        if (values) {
+            const uint32_t vw[4] = {(uint32_t)vv.x, (uint32_t)vv.y, (uint32_t)vv.z, (uint32_t)vv.w};
+#pragma unroll
+            for (int j = 0; j < 16; j++) vt[16 * piece + j][row] = (int8_t)((vw[j >> 2] >> (8 * (j & 3))) & 255u);
+        }
+        __syncthreads();
+    };
+    // scores of key tile kt of the staged block for head row tiles r: D[key 4 g + i][query c16]
+    auto scores = [&](int kt, v4f (&d)[2]) {
+#pragma unroll
+        for (int r = 0; r < 2; r++) d[r] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            const uint2 kk = *reinterpret_cast<const uint2 *>(&kr[16 * kt + c16][32 * kb + 8 * g]);
+            const v8h ak = s8x8_f16(kk.x, kk.y);
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                d[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bq[r][kb][0], d[r], 0, 0, 0);
+                d[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bq[r][kb][1], d[r], 0, 0, 0);
+            }
+        }
+    };
+    const float scale = 1.0f / sqrtf((float)HD);
+    // pass 1: each query's maximum, and the largest value scale
+    float mx[2] = {-INFINITY, -INFINITY}, vm = 0.0f;
+    for (int s0 = 0; s0 < npos; s0 += kPB) {
+        stage(s0, false);
+        if ((tid & 3) == 0 && s0 + (tid >> 2) < npos) vm = fmaxf(vm, VS[base + (int64_t)(s0 + (tid >> 2)) * n_kv]);
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            v4f d[2];
+            scores(kt, d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = s0 + 16 * kt + 4 * g + i;
+                const float ks = ksb[16 * kt + 4 * g + i];
+#pragma unroll
+                for (int r = 0; r < 2; r++)
+                    if (qok && p <= qpos) mx[r] = fmaxf(mx[r], d[r][i] * ks * scale);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) mx[r] = rows4_max_p(mx[r]);
+    vm = wave_max(vm);
+    if (lane == 0) vmx[w] = vm;
+    __syncthreads();
+    int ex = 0;
+    frexpf(fmaxf(fmaxf(vmx[0], vmx[1]), fmaxf(vmx[2], vmx[3])), &ex);
+    const int sig_e = min(126, max(-126, 10 - ex));
+    const float sigma = ldexpf(1.0f, sig_e);
+    // pass 2: weights and value sums; o[r][dt]: D[query 4 g + i][dim 16 dt + c16]
+    v4f o[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) o[r][dt] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    float te[2] = {0.0f, 0.0f};
+    for (int s0 = 0; s0 < npos; s0 += kPB) {
+        stage(s0, true);
+        v8h ph[2][2], pl[2][2];  // [r][key half]: element e is key 32 c + 16 (e / 4) + 4 g + e % 4
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            v4f d[2];
+            scores(kt, d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = s0 + 16 * kt + 4 * g + i;
+                const float ks = ksb[16 * kt + 4 * g + i], vs = vsb[16 * kt + 4 * g + i];
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const bool ok = qok && p <= qpos;
+                    const float e = ok ? expf(d[r][i] * ks * scale - mx[r]) : 0.0f;
+                    te[r] += e;
+                    const float x = e * vs * sigma;
+                    const _Float16 hi = (_Float16)x;
+                    ph[r][kt >> 1][4 * (kt & 1) + i] = hi;
+                    pl[r][kt >> 1][4 * (kt & 1) + i] = (_Float16)(x - (float)hi);
+                }
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const uint32_t v0 = *reinterpret_cast<const uint32_t *>(&vt[16 * dt + c16][32 * c + 4 * g]);
+                const uint32_t v1 = *reinterpret_cast<const uint32_t *>(&vt[16 * dt + c16][32 * c + 16 + 4 * g]);
+                const v8h bv = s8x8_f16(v0, v1);
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    o[r][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[r][c], bv, o[r][dt], 0, 0, 0);
+                    o[r][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[r][c], bv, o[r][dt], 0, 0, 0);
+                }
+            }
+    }
+    // each query's total, from the score layout (lane = query) to the value layout (4 g + i)
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        te[r] = rows4_sum_p(te[r]);
+        if (g == 0) tfin[w][r][c16] = te[r];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's own LDS writes are in
+    const float isig = ldexpf(1.0f, -sig_e);
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = 4 * g + i;
+            if (q < nq) {
+                const float t = tfin[w][r][q];
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++)
+                    out[(int64_t)(q0 + q) * ldo + (int64_t)(kvh * G + 2 * w + r) * HD + 16 * dt + c16] =
+                        o[r][dt][i] * isig / t;
+            }
+        }
+}
+
 }  // namespace
 
 int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, const float *KS, const float *VS,
@@ -759,6 +989,12 @@ int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, cons
         LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_prompt_kernel<64>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         granted = lds;
+    }
+    if (n_head == 8 * n_kv) {  // grouped queries: the 8 heads of a key / value head share each staged block
+        hipLaunchKernelGGL(attend_prompt_gqa_kernel, dim3(n_kv, (T + kQB - 1) / kQB), dim3(256), 0, ctx->stream, qkv,
+                           ld, pos0, T, layer, max_t, n_kv, K8, V8, KS, VS, out, ldo);
+        LLMQ_HIP(hipGetLastError());
+        return LLMQ_OK;
     }
     hipLaunchKernelGGL(attend_prompt_kernel<64>, dim3(n_head, (T + kQB - 1) / kQB), dim3(256), lds, ctx->stream, qkv,
                        ld, pos0, T, layer, max_t, n_kv, n_head / n_kv, K8, V8, KS, VS, out, ldo, LT);

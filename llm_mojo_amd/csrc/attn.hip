@@ -834,30 +834,36 @@ __global__ __launch_bounds__(256) void attend_prompt_gqa_kernel(const float *__r
             }
         }
     }
-    // Stage block s0: thread (key tid / 4, piece tid % 4) copies 16 bytes of the
-    // key row (and of the value row into the transposed copy), lane 0 of the
-    // key the scales; rows past npos are zero.
-    auto stage = [&](int s0, bool values) {
+    // Block s0's rows: thread (key tid / 4, piece tid % 4) loads 16 bytes of the
+    // key row (and of the value row), lane 0 of the key the scales; rows past
+    // npos are zero.  fetch() issues the loads (the next block's go out before
+    // this block's products), commit() writes them to LDS, values transposed.
+    struct Rows {
+        int4 kv, vv;
+        float ks, vs;
+    };
+    auto fetch = [&](int s0, bool values) {
+        Rows x{make_int4(0, 0, 0, 0), make_int4(0, 0, 0, 0), 0.0f, 0.0f};
         const int row = tid >> 2, piece = tid & 3, sidx = s0 + row;
-        int4 kv = make_int4(0, 0, 0, 0), vv = make_int4(0, 0, 0, 0);
-        float ks = 0.0f, vs = 0.0f;
         if (sidx < npos) {
             const int64_t sl = base + (int64_t)sidx * n_kv;
-            kv = *reinterpret_cast<const int4 *>(K8 + sl * HD + 16 * piece);
-            ks = KS[sl];
-            if (values) {
-                vv = *reinterpret_cast<const int4 *>(V8 + sl * HD + 16 * piece);
-                vs = VS[sl];
-            }
+            x.kv = *reinterpret_cast<const int4 *>(K8 + sl * HD + 16 * piece);
+            x.ks = KS[sl];
+            x.vs = VS[sl];
+            if (values) x.vv = *reinterpret_cast<const int4 *>(V8 + sl * HD + 16 * piece);
         }
+        return x;
+    };
+    auto commit = [&](const Rows &x, bool values) {
+        const int row = tid >> 2, piece = tid & 3;
         __syncthreads();  // the previous block's reads are done
-        *reinterpret_cast<int4 *>(&kr[row][16 * piece]) = kv;
+        *reinterpret_cast<int4 *>(&kr[row][16 * piece]) = x.kv;
         if (piece == 0) {
-            ksb[row] = ks;
-            vsb[row] = vs;
+            ksb[row] = x.ks;
+            vsb[row] = x.vs;
         }
         if (values) {
-            const uint32_t vw[4] = {(uint32_t)vv.x, (uint32_t)vv.y, (uint32_t)vv.z, (uint32_t)vv.w};
+            const uint32_t vw[4] = {(uint32_t)x.vv.x, (uint32_t)x.vv.y, (uint32_t)x.vv.z, (uint32_t)x.vv.w};
 #pragma unroll
             for (int j = 0; j < 16; j++) vt[16 * piece + j][row] = (int8_t)((vw[j >> 2] >> (8 * (j & 3))) & 255u);
         }
@@ -881,9 +887,11 @@ __global__ __launch_bounds__(256) void attend_prompt_gqa_kernel(const float *__r
     const float scale = 1.0f / sqrtf((float)HD);
     // pass 1: each query's maximum, and the largest value scale
     float mx[2] = {-INFINITY, -INFINITY}, vm = 0.0f;
+    Rows nx = fetch(0, false);
     for (int s0 = 0; s0 < npos; s0 += kPB) {
-        stage(s0, false);
-        if ((tid & 3) == 0 && s0 + (tid >> 2) < npos) vm = fmaxf(vm, VS[base + (int64_t)(s0 + (tid >> 2)) * n_kv]);
+        commit(nx, false);
+        vm = fmaxf(vm, nx.vs);
+        if (s0 + kPB < npos) nx = fetch(s0 + kPB, false);
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             v4f d[2];
@@ -914,8 +922,10 @@ __global__ __launch_bounds__(256) void attend_prompt_gqa_kernel(const float *__r
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) o[r][dt] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     float te[2] = {0.0f, 0.0f};
+    nx = fetch(0, true);
     for (int s0 = 0; s0 < npos; s0 += kPB) {
-        stage(s0, true);
+        commit(nx, true);
+        if (s0 + kPB < npos) nx = fetch(s0 + kPB, true);
         v8h ph[2][2], pl[2][2];  // [r][key half]: element e is key 32 c + 16 (e / 4) + 4 g + e % 4
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {

@@ -25,7 +25,8 @@
 //           below);
 //   sums    fp16 [T16 / 16][NSB][hi, lo][16 tokens][8]: s X_j, j = 0..7;
 //   inv     float [T16 / 16][NSB][16 tokens]: 1 / s.
-// Padded tokens are zeros throughout, so they add nothing.
+// A padded token's record (zeros from the record kernel, anything from
+// other writers) reaches only that token's outputs, which are not stored.
 //
 // Mapping: a workgroup owns RT row tiles of 16 rows and a tile of 16 tokens;
 // its NW waves split the row's superblocks into contiguous runs.  In a
@@ -462,12 +463,12 @@ int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int6
     const int per = (int)((NSB + 15) / 16), nw = (int)((NSB + per - 1) / per);
     const unsigned nt = (unsigned)w->ntiles;
     hipStream_t st = ctx->stream;
-    // wide matrices (gate / up): 4 row tiles a workgroup share the record
-    // loads (one round of 176 workgroups at 11264 rows; 1, 2 and 4 tiles
-    // measured 10.5, 11.9 and 10.1 us at 16 tokens)
     if (ntt >= (unsigned)kPT)  // prompts: the LDS-staged form
         hipLaunchKernelGGL(gemm_h16_q4k_lds_kernel, dim3((nt + 4 * kRW - 1) / (4 * kRW), (ntt + kPT - 1) / kPT),
                            dim3(512), 0, st, a, (int)ntt);
+    // wide matrices (gate / up): 4 row tiles a workgroup share the record
+    // loads (one round of 176 workgroups at 11264 rows; 1, 2 and 4 tiles
+    // measured 10.5, 11.9 and 10.1 us at 16 tokens)
     else if (nw <= 8 && w->ntiles >= 512)
         hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 4>), dim3((nt + 3) / 4, ntt), dim3(512), 0, st, a);
     else if (nw <= 4)

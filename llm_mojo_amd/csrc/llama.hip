@@ -57,9 +57,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     const float *xr = x + (int64_t)blockIdx.x * ldx;
     float *orow = out + (int64_t)blockIdx.x * ldo;
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < C; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    // 8 loads a thread in flight at a time (zeros past C add nothing), in the loop's order
+    for (int i0 = threadIdx.x; i0 < C; i0 += 256 * 8) {
+        float t[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) t[k] = i0 + 256 * k < C ? xr[i0 + 256 * k] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) ss = fmaf(t[k], t[k], ss);
+    }
     ss = block_sum(ss, red);
     const float r = 1.0f / sqrtf(ss / (float)C + eps);
+#pragma unroll 8
     for (int i = threadIdx.x; i < C; i += 256) orow[i] = (xr[i] * r) * g[i];
 }
 
@@ -73,21 +81,34 @@ __global__ __launch_bounds__(64) void rmsnorm_rec_kernel(const float *__restrict
                                                          float *__restrict__ inv) {
     const float *xr = x + (int64_t)blockIdx.y * ldx;
     const int lane = threadIdx.x, sb = blockIdx.x;
-    float v[4];
+    // the superblock's inputs and gains, then the row for its sum of squares,
+    // 8 float4 a lane in flight at a time (zeros past C add nothing), all
+    // before the first use
+    float v[4], gv[4];
 #pragma unroll
-    for (int q = 0; q < 4; q++) v[q] = xr[sb * 256 + 64 * q + lane];
+    for (int q = 0; q < 4; q++) {
+        v[q] = xr[sb * 256 + 64 * q + lane];
+        gv[q] = g[sb * 256 + 64 * q + lane];
+    }
     float ss = 0.0f;
-    for (int i = 4 * lane; i < C; i += 256) {
-        const float4 t = *reinterpret_cast<const float4 *>(xr + i);
-        ss = fmaf(t.x, t.x, ss);
-        ss = fmaf(t.y, t.y, ss);
-        ss = fmaf(t.z, t.z, ss);
-        ss = fmaf(t.w, t.w, ss);
+    for (int i0 = 4 * lane; i0 < C; i0 += 256 * 8) {
+        float4 t[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            t[k] = i0 + 256 * k < C ? *reinterpret_cast<const float4 *>(xr + i0 + 256 * k)
+                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            ss = fmaf(t[k].x, t[k].x, ss);
+            ss = fmaf(t[k].y, t[k].y, ss);
+            ss = fmaf(t[k].z, t[k].z, ss);
+            ss = fmaf(t[k].w, t[k].w, ss);
+        }
     }
     ss = wave_sum(ss);
     const float r = 1.0f / sqrtf(ss / (float)C + eps);
 #pragma unroll
-    for (int q = 0; q < 4; q++) v[q] = (v[q] * r) * g[sb * 256 + 64 * q + lane];
+    for (int q = 0; q < 4; q++) v[q] = (v[q] * r) * gv[q];
     llmq_h16_store(planes, sums, inv, C / 32, C / 256, blockIdx.y, sb, v, true);
 }
 
@@ -554,26 +575,27 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
     }
 }
 
-// The splits of (head blockIdx.x, sequence blockIdx.y) into the output:
-// out = sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j - M), splits in order
-// (the same arithmetic as the Wo GEMV's staging of them, gguf1.hip).
-__global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int NS, int n_head,
-                                                            const int *__restrict__ state, float *__restrict__ out,
-                                                            int64_t ldo) {
-    const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x;
-    const int ns = min(NS, (state[0] + kSplit) / kSplit);
-    const float *P = part + ((int64_t)b * n_head + h) * NS * kPart;
+// Dimension dd of a head's split results P (NS splits of kPart floats):
+// sum_j acc_j exp(m_j - M) / sum_j t_j exp(m_j - M) over the splits j <
+// min(NS, (pos + kSplit) / kSplit) that hold positions, in order (the same
+// arithmetic as the Wo GEMV's staging of them, gguf1.hip).  Every split is
+// loaded, used or not, ahead of the position, so the loads do not wait for
+// it; unused ones are only selected away.
+__device__ __forceinline__ float combine_splits(const float *__restrict__ P, int NS, const int *__restrict__ state,
+                                                int dd) {
     float mj[kMaxSplits], tj[kMaxSplits], aj[kMaxSplits];
 #pragma unroll
     for (int j = 0; j < kMaxSplits; j++) {
-        const bool ok = j < ns;
-        mj[j] = ok ? P[j * kPart] : -INFINITY;
-        tj[j] = ok ? P[j * kPart + 1] : 0.0f;
-        aj[j] = ok ? P[j * kPart + 4 + dd] : 0.0f;
+        const bool in = j < NS;
+        mj[j] = in ? P[j * kPart] : -INFINITY;
+        tj[j] = in ? P[j * kPart + 1] : 0.0f;
+        aj[j] = in ? P[j * kPart + 4 + dd] : 0.0f;
     }
-    float M = mj[0];
+    __builtin_amdgcn_sched_barrier(0);
+    const int ns = min(NS, (state[0] + kSplit) / kSplit);
+    float M = mj[0];  // split 0 always holds positions
 #pragma unroll
-    for (int j = 1; j < kMaxSplits; j++) M = fmaxf(M, mj[j]);
+    for (int j = 1; j < kMaxSplits; j++) M = fmaxf(M, j < ns ? mj[j] : -INFINITY);
     float T = 0.0f, acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxSplits; j++) {
@@ -583,7 +605,15 @@ __global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restr
             acc = fmaf(aj[j], f, acc);
         }
     }
-    out[(int64_t)b * ldo + h * HD + dd] = acc / T;
+    return acc / T;
+}
+
+// The splits of (head blockIdx.x, sequence blockIdx.y) into the output.
+__global__ __launch_bounds__(64) void attend_combine_kernel(const float *__restrict__ part, int NS, int n_head,
+                                                            const int *__restrict__ state, float *__restrict__ out,
+                                                            int64_t ldo) {
+    const int h = blockIdx.x, b = blockIdx.y, dd = threadIdx.x;
+    out[(int64_t)b * ldo + h * HD + dd] = combine_splits(part + ((int64_t)b * n_head + h) * NS * kPart, NS, state, dd);
 }
 
 // attend_combine_kernel for the 4 heads of superblock blockIdx.x (wave w
@@ -596,29 +626,7 @@ __global__ __launch_bounds__(256) void attend_combine_rec_kernel(const float *__
                                                                  float *__restrict__ inv) {
     __shared__ float o4[4][HD];
     const int w = threadIdx.x >> 6, dd = threadIdx.x & 63, h = blockIdx.x * 4 + w, b = blockIdx.y;
-    const int ns = min(NS, (state[0] + kSplit) / kSplit);
-    const float *P = part + ((int64_t)b * n_head + h) * NS * kPart;
-    float mj[kMaxSplits], tj[kMaxSplits], aj[kMaxSplits];
-#pragma unroll
-    for (int j = 0; j < kMaxSplits; j++) {
-        const bool ok = j < ns;
-        mj[j] = ok ? P[j * kPart] : -INFINITY;
-        tj[j] = ok ? P[j * kPart + 1] : 0.0f;
-        aj[j] = ok ? P[j * kPart + 4 + dd] : 0.0f;
-    }
-    float M = mj[0];
-#pragma unroll
-    for (int j = 1; j < kMaxSplits; j++) M = fmaxf(M, mj[j]);
-    float T = 0.0f, acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxSplits; j++) {
-        if (j < ns) {
-            const float f = expf(mj[j] - M);
-            T = fmaf(tj[j], f, T);
-            acc = fmaf(aj[j], f, acc);
-        }
-    }
-    o4[w][dd] = acc / T;
+    o4[w][dd] = combine_splits(part + ((int64_t)b * n_head + h) * NS * kPart, NS, state, dd);
     __syncthreads();
     if (w == 0) {
         const float v[4] = {o4[0][dd], o4[1][dd], o4[2][dd], o4[3][dd]};

@@ -627,7 +627,7 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
                                                             const int8_t *__restrict__ V8,
                                                             const float *__restrict__ KS,
                                                             const float *__restrict__ VS, float *__restrict__ out,
-                                                            int64_t ldo, int LT) {
+                                                            int64_t ldo, int LT, int hm) {
     static_assert(HD == 64, "prompt attention: head_dim 64");
     extern __shared__ __align__(16) float smp[];
     float *S = smp;                                      // [kQB][LT] scores, then e
@@ -639,7 +639,9 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
     const int nq = min(kQB, T - q0);
     const int npos = pos0 + q0 + nq;  // positions any query of the block sees
     const float scale = 1.0f / sqrtf((float)HD);
-    const int64_t base = (int64_t)layer * max_t * n_kv + h / group;  // the query head's key / value head
+    // the query head's key / value head: its position 0 and position stride (rows)
+    const int64_t base = hm ? ((int64_t)layer * n_kv + h / group) * max_t : (int64_t)layer * max_t * n_kv + h / group;
+    const int64_t pstr = hm ? 1 : n_kv;
 
     // A operand of the scores: query c16, dims 16 k4 + t
     float qa[16];
@@ -662,7 +664,7 @@ __global__ __launch_bounds__(256) void attend_prompt_kernel(const float *__restr
         v = make_int4(0, 0, 0, 0);
         f = 0.0f;
         if (s < npos) {
-            const int64_t sl = base + (int64_t)s * n_kv;
+            const int64_t sl = base + (int64_t)s * pstr;
             v = *reinterpret_cast<const int4 *>(src + sl * HD + 16 * piece);
             f = sc[sl];
         }
@@ -797,7 +799,7 @@ __global__ __launch_bounds__(256) void attend_prompt_gqa_kernel(const float *__r
                                                                 const int8_t *__restrict__ V8,
                                                                 const float *__restrict__ KS,
                                                                 const float *__restrict__ VS, float *__restrict__ out,
-                                                                int64_t ldo) {
+                                                                int64_t ldo, int hm) {
     constexpr int HD = 64, G = 8, KR = HD + 8, VR = kPB + 4;  // head dim, heads; LDS row strides (bytes)
     __shared__ __align__(16) int8_t kr[kPB][KR];
     __shared__ __align__(16) int8_t vt[HD][VR];
@@ -806,7 +808,8 @@ __global__ __launch_bounds__(256) void attend_prompt_gqa_kernel(const float *__r
     const int lane = tid & 63, w = tid >> 6, c16 = lane & 15, g = lane >> 4;
     const int nq = min(kQB, T - q0);
     const int npos = pos0 + q0 + nq;  // positions any query of the block sees
-    const int64_t base = (int64_t)layer * max_t * n_kv + kvh;
+    const int64_t base = hm ? ((int64_t)layer * n_kv + kvh) * max_t : (int64_t)layer * max_t * n_kv + kvh;
+    const int64_t pstr = hm ? 1 : n_kv;  // rows between positions
     const int qpos = pos0 + q0 + c16;  // the lane's query sees positions <= qpos
     const bool qok = c16 < nq;
     // the query operand of head 8 kvh + 2w + r: dims 32 kb + 8 g .., hi and lo planes
@@ -846,7 +849,7 @@ __global__ __launch_bounds__(256) void attend_prompt_gqa_kernel(const float *__r
         Rows x{make_int4(0, 0, 0, 0), make_int4(0, 0, 0, 0), 0.0f, 0.0f};
         const int row = tid >> 2, piece = tid & 3, sidx = s0 + row;
         if (sidx < npos) {
-            const int64_t sl = base + (int64_t)sidx * n_kv;
+            const int64_t sl = base + (int64_t)sidx * pstr;
             x.kv = *reinterpret_cast<const int4 *>(K8 + sl * HD + 16 * piece);
             x.ks = KS[sl];
             x.vs = VS[sl];
@@ -988,7 +991,7 @@ __global__ __launch_bounds__(256) void attend_prompt_gqa_kernel(const float *__r
 
 int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, const float *KS, const float *VS,
                          int layer, int max_t, int n_head, int n_kv, const float *qkv, int64_t ld, int pos0, int T,
-                         float *out, int64_t ldo) {
+                         float *out, int64_t ldo, bool head_major) {
     LLMQ_REQUIRE(n_kv > 0 && n_head % n_kv == 0, "attend: %d query heads over %d key / value heads", n_head, n_kv);
     LLMQ_REQUIRE(T >= 1 && pos0 >= 0 && pos0 + T <= max_t, "attend: positions %d..%d beyond %d", pos0, pos0 + T - 1,
                  max_t);
@@ -1002,12 +1005,12 @@ int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, cons
     }
     if (n_head == 8 * n_kv) {  // grouped queries: the 8 heads of a key / value head share each staged block
         hipLaunchKernelGGL(attend_prompt_gqa_kernel, dim3(n_kv, (T + kQB - 1) / kQB), dim3(256), 0, ctx->stream, qkv,
-                           ld, pos0, T, layer, max_t, n_kv, K8, V8, KS, VS, out, ldo);
+                           ld, pos0, T, layer, max_t, n_kv, K8, V8, KS, VS, out, ldo, (int)head_major);
         LLMQ_HIP(hipGetLastError());
         return LLMQ_OK;
     }
     hipLaunchKernelGGL(attend_prompt_kernel<64>, dim3(n_head, (T + kQB - 1) / kQB), dim3(256), lds, ctx->stream, qkv,
-                       ld, pos0, T, layer, max_t, n_kv, n_head / n_kv, K8, V8, KS, VS, out, ldo, LT);
+                       ld, pos0, T, layer, max_t, n_kv, n_head / n_kv, K8, V8, KS, VS, out, ldo, LT, (int)head_major);
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }

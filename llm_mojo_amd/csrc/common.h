@@ -263,10 +263,12 @@ int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *ro
 int launch_gguf_pick_embed(llmq_ctx *ctx, const llmq_mat *E, const ArgmaxPart *parts, int nparts, int B, int *state,
                            int64_t *next, int64_t *gen, float *dst, int64_t ldd);
 // Prompt attention over an int8 cache of n_kv heads (attn.hip): query head h
-// reads cached head h / (n_head / n_kv) of `layer` (a slot index).
+// reads cached head h / (n_head / n_kv) of `layer` (a slot index), the rows
+// position-major (slot * max_t + pos) * n_kv + head (the KVCache layout) or,
+// with head_major, (slot * n_kv + head) * max_t + pos.
 int launch_attend_prompt(llmq_ctx *ctx, const int8_t *K8, const int8_t *V8, const float *KS, const float *VS,
                          int layer, int max_t, int n_head, int n_kv, const float *qkv, int64_t ld, int pos0, int T,
-                         float *out, int64_t ldo);
+                         float *out, int64_t ldo, bool head_major = false);
 // QuantMatrix with float activations (A16 = False) runs on the two GGUF
 // float-activation kernels (launch_gguf_gemv, launch_gguf_gemm) as two
 // internal types past the ggml range, over its own device layout (codes

@@ -16,8 +16,10 @@
 //   pos * theta^(-2i / head_dim);  silu(g) = g / (1 + exp(-g)).
 //
 // Device layout: Wq, Wk, Wv are one matrix of n_head + 2 n_kv heads' rows
-// (one GEMV per layer); Wgate and Wup one of 2 ffn rows.  The cache holds
-// slot (sequence * n_layer + layer) of n_kv heads.  Decoding keeps the
+// (one GEMV per layer); Wgate and Wup one of 2 ffn rows.  The cache is
+// head-major: row ((sequence * n_layer + layer) * n_kv + head) * max_t + pos
+// of HD int8 codes (and one scale), so a split's rows of one head are one
+// contiguous run.  Decoding keeps the
 // position and step on the device, so one captured graph replays every step.
 #include <math.h>
 #include <stdlib.h>
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(64) void rope_store_kernel(float *__restrict__ qkv,
         return;
     }
     const int kvh = hh - n_head;
-    const int64_t sl = (((int64_t)seq * n_layer + layer) * max_t + pos) * n_kv + kvh;
+    const int64_t sl = (((int64_t)seq * n_layer + layer) * n_kv + kvh) * max_t + pos;
     for (int kv = 0; kv < 2; kv++) {
         const float x = kv == 0 ? rot : r[(n_head + n_kv + kvh) * HD + d];
         const float m = wave_max(fabsf(x));
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
     const int h = blockIdx.x, b = blockIdx.y, j = blockIdx.z, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int s0 = j * kSplit;
     const int grp = n_head / n_kv, kvh = h / grp;
-    const int64_t slot0 = ((int64_t)b * n_layer + layer) * max_t;
+    const int64_t row0 = (((int64_t)b * n_layer + layer) * n_kv + kvh) * max_t;  // the head's position 0
     const float *r = qkv + (int64_t)b * ld;
     // The query, new key and value and this split's cache rows go out
     // together with the position, which none of their addresses needs.
@@ -201,7 +203,7 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
         kvx = r[(n_head + kvh) * HD + lane];
         vvx = r[(n_head + n_kv + kvh) * HD + lane];
     }
-    const int64_t sl = (slot0 + min(s0 + tid, max_t - 1)) * n_kv + kvh;
+    const int64_t sl = row0 + min(s0 + tid, max_t - 1);
     int4 kr[HD / 16], vr[HD / 16];
 #pragma unroll
     for (int i = 0; i < HD / 16; i++) {
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__res
             const float qs = wave_sum(rot);
             if (d == 0) s_qsum = qs;
         } else {
-            const int64_t sn = (slot0 + pos) * n_kv + kvh;
+            const int64_t sn = row0 + pos;
             for (int kv = 0; kv < 2; kv++) {
                 const float x = kv == 0 ? rot : vvx;
                 const float m = wave_max(fabsf(x));
@@ -394,7 +396,7 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
     __shared__ __align__(16) float vred[kSW][G][HD];
     const int kvh = blockIdx.x, b = blockIdx.y, j = blockIdx.z, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int s0 = j * kSplit, h0 = kvh * G;
-    const int64_t slot0 = ((int64_t)b * n_layer + layer) * max_t;
+    const int64_t row0 = (((int64_t)b * n_layer + layer) * n_kv + kvh) * max_t;  // the head's position 0
     const float *r = qkv + (int64_t)b * ld;
     // queries (head w and w + 4, dimension lane), new key and value, cache
     // rows, all before the position
@@ -404,7 +406,7 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
         kvx = r[(n_head + kvh) * HD + lane];
         vvx = r[(n_head + n_kv + kvh) * HD + lane];
     }
-    const int64_t sl = (slot0 + min(s0 + tid, max_t - 1)) * n_kv + kvh;
+    const int64_t sl = row0 + min(s0 + tid, max_t - 1);
     int4 kr[HD / 16], vr[HD / 16];
 #pragma unroll
     for (int i = 0; i < HD / 16; i++) {
@@ -451,7 +453,7 @@ __global__ __launch_bounds__(kSplit) void attend_split_group_kernel(const float 
         if (w == 1 && has_new) {
             const float pk = llmq_dppf<0xB1>(kvx);
             const float rk = (d & 1) ? pk * csn.y + kvx * csn.x : kvx * csn.x - pk * csn.y;
-            const int64_t sn = (slot0 + pos) * n_kv + kvh;
+            const int64_t sn = row0 + pos;
             for (int kv = 0; kv < 2; kv++) {
                 const float x = kv == 0 ? rk : vvx;
                 const float m = wave_max(fabsf(x));
@@ -890,7 +892,7 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
                                (int64_t)QC, T, seq0, pos0, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope,
                                m->k8, m->v8, m->ks, m->vs);
             RC(launch_attend_prompt(ctx, m->k8, m->v8, m->ks, m->vs, seq0 * c.n_layer + l, c.max_t, c.n_head,
-                                    c.n_kv, m->qkv, QC, pos0, T, m->att, c.dim));
+                                    c.n_kv, m->qkv, QC, pos0, T, m->att, c.dim, true));
             RC(linear(m, m->wo[l], m->att, c.dim, R, m->x, c.dim, LLMQ_RESID));
         }
         RC(norm_linear(m, gain(m, l, 1), m->wgu[l], R, m->gu, 2 * c.ffn, 0));

@@ -128,7 +128,8 @@ __global__ void gguf_dequant_rows_kernel(GgufArgs a, const int64_t *rows, float 
 // gpt2t.mojo:792-797) is the next token, written to next[b] and
 // gen[state[1] * B + b]; its row of E goes to dst + b * ldd.  The last
 // workgroup to finish moves the decode state on (position and step + 1;
-// state[2] counts the finished workgroups and is cleared again).
+// state[2] counts the finished workgroups and is cleared again; one
+// workgroup advances it directly).
 template <int TYPE>
 __global__ __launch_bounds__(256) void gguf_pick_embed_kernel(GgufArgs a, const ArgmaxPart *__restrict__ parts,
                                                               int nparts, int B, int *__restrict__ state,
@@ -138,14 +139,20 @@ __global__ __launch_bounds__(256) void gguf_pick_embed_kernel(GgufArgs a, const 
     __shared__ int s_pick;
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const ArgmaxPart *P = parts + (int64_t)b * nparts;
+    const int step = state[1];  // read with the partials (this workgroup reads it before any advance)
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = tid; i < nparts; i += 256) {
-        const ArgmaxPart c = P[i];
-        if (c.v > bv || (c.v == bv && c.idx < bi)) {
-            bv = c.v;
-            bi = c.idx;
-        }
+    // 4 partials a thread in flight at a time (the first-maximum rule is order-free)
+    for (int i0 = tid; i0 < nparts; i0 += 4 * 256) {
+        ArgmaxPart c[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) c[k] = i0 + 256 * k < nparts ? P[i0 + 256 * k] : ArgmaxPart{-INFINITY, 0x7fffffff};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (c[k].v > bv || (c[k].v == bv && c[k].idx < bi)) {
+                bv = c[k].v;
+                bi = c[k].idx;
+            }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -162,15 +169,19 @@ __global__ __launch_bounds__(256) void gguf_pick_embed_kernel(GgufArgs a, const 
         ArgmaxPart best = s_b[0];
         for (int w = 1; w < 4; w++)
             if (s_b[w].v > best.v || (s_b[w].v == best.v && s_b[w].idx < best.idx)) best = s_b[w];
-        const int step = state[1];
         next[b] = best.idx;
         gen[(int64_t)step * B + b] = best.idx;
         s_pick = best.idx;
-        __threadfence();
-        if (atomicAdd(&state[2], 1) == (int)gridDim.x - 1) {  // every workgroup has read the step
-            state[2] = 0;
+        if (gridDim.x == 1) {  // the only reader of the step
             state[0] += 1;
-            state[1] += 1;
+            state[1] = step + 1;
+        } else {
+            __threadfence();
+            if (atomicAdd(&state[2], 1) == (int)gridDim.x - 1) {  // every workgroup has read the step
+                state[2] = 0;
+                state[0] += 1;
+                state[1] += 1;
+            }
         }
     }
     __syncthreads();

@@ -66,41 +66,74 @@ template <int TYPE>
 __device__ __forceinline__ void dequant_row_body(const GgufArgs &a, int64_t row, float *dst) {
     using F = Fmt<TYPE>;
     const int64_t tile = row / 16, r = row % 16;
-    for (int k = threadIdx.x; k < a.K; k += blockDim.x) {
+    // The fields input k reads: its chunk's codes and the type's side data.
+    struct Fields {
+        uint4 d, f;
+        uint32_t m;
+        uint2 hb;
+    };
+    auto load = [&](int k) {
+        Fields x{};
         const int c = k / F::WPC, e = k % F::WPC;
-        const uint4 d = a.codes[((size_t)tile * a.CK + c) * 16 + r];
-        const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
         const size_t mi = ((size_t)tile * a.CK + c) * 16 + r;
         const size_t sbi = ((size_t)tile * a.NSB + c / F::CPS) * 16 + r;
-        float v;
-        if (TYPE == LLMQ_GGML_Q8_0) {
-            const int q = (int)(int8_t)((dw[e >> 2] >> (8 * (e & 3))) & 255u);
-            v = h2f(a.meta16[((size_t)tile * (a.CK / 2) + (c >> 1)) * 16 + r]) * (float)q;
+        x.d = a.codes[mi];
+        if constexpr (TYPE == LLMQ_GGML_Q8_0) x.m = a.meta16[((size_t)tile * (a.CK / 2) + (c >> 1)) * 16 + r];
+        if constexpr (TYPE == LLMQ_GGML_Q4_0) x.m = a.meta16[mi];
+        if constexpr (TYPE == LLMQ_GGML_Q4_1) x.m = a.meta32[mi];
+        if constexpr (TYPE == LLMQ_GGML_Q5_K) x.m = a.bits32[mi];
+        if constexpr (TYPE == LLMQ_GGML_Q4_K || TYPE == LLMQ_GGML_Q5_K || TYPE == LLMQ_GGML_Q6_K) x.f = a.sb16[sbi];
+        if constexpr (TYPE == LLMQ_GGML_Q6_K) {
+            x.hb = a.bits64[mi];
+            x.m = a.meta16[sbi];
+        }
+        (void)e;
+        return x;
+    };
+    auto value = [&](int k, const Fields &x) -> float {
+        const int c = k / F::WPC, e = k % F::WPC;
+        // the fields as scalars, chosen by selects (an indexed array or struct would go to scratch)
+        const uint32_t d0 = x.d.x, d1 = x.d.y, d2 = x.d.z, d3 = x.d.w;
+        const uint32_t f0 = x.f.x, f1 = x.f.y, f2 = x.f.z, f3 = x.f.w, h0 = x.hb.x, h1 = x.hb.y, mm = x.m;
+        auto dword = [&](int i) { return i == 0 ? d0 : i == 1 ? d1 : i == 2 ? d2 : d3; };
+        if constexpr (TYPE == LLMQ_GGML_Q8_0) {
+            const int q = (int)(int8_t)((dword(e >> 2) >> (8 * (e & 3))) & 255u);
+            return h2f(mm) * (float)q;
         } else {
-            int u = (int)((dw[e >> 3] >> (4 * (e & 7))) & 15u);
-            if (TYPE == LLMQ_GGML_Q4_0) {
-                v = ((float)u - 8.0f) * h2f(a.meta16[mi]);
-            } else if (TYPE == LLMQ_GGML_Q4_1) {
-                const uint32_t m = a.meta32[mi];
-                v = h2f(m) * (float)u + h2f(m >> 16);
-            } else if (TYPE == LLMQ_GGML_Q4_K || TYPE == LLMQ_GGML_Q5_K) {
-                if (TYPE == LLMQ_GGML_Q5_K) u |= (int)((a.bits32[mi] >> e) & 1u) << 4;
-                const uint4 f = a.sb16[sbi];
+            int u = (int)((dword(e >> 3) >> (4 * (e & 7))) & 15u);
+            if constexpr (TYPE == LLMQ_GGML_Q4_0) {
+                return ((float)u - 8.0f) * h2f(mm);
+            } else if constexpr (TYPE == LLMQ_GGML_Q4_1) {
+                return h2f(mm) * (float)u + h2f(mm >> 16);
+            } else if constexpr (TYPE == LLMQ_GGML_Q4_K || TYPE == LLMQ_GGML_Q5_K) {
+                if constexpr (TYPE == LLMQ_GGML_Q5_K) u |= (int)((mm >> e) & 1u) << 4;
                 int sc, mn;
-                k_scale_min(f.y, f.z, f.w, c & 7, sc, mn);
-                v = (h2f(f.x) * (float)sc) * (float)u - h2f(f.x >> 16) * (float)mn;
+                k_scale_min(f1, f2, f3, c & 7, sc, mn);
+                return (h2f(f0) * (float)sc) * (float)u - h2f(f0 >> 16) * (float)mn;
             } else {
-                const uint2 hb = a.bits64[mi];
-                const uint32_t hw = e < 16 ? hb.x : hb.y;
+                const uint32_t hw = e < 16 ? h0 : h1;
                 u |= (int)((hw >> (2 * (e & 15))) & 3u) << 4;
-                const uint4 f = a.sb16[sbi];
                 const int si = 2 * (c & 7) + (e >= 16);
-                const uint32_t sw = si < 4 ? f.x : (si < 8 ? f.y : (si < 12 ? f.z : f.w));
+                const uint32_t sw = si < 4 ? f0 : (si < 8 ? f1 : (si < 12 ? f2 : f3));
                 const float sc = (float)(int8_t)((sw >> (8 * (si & 3))) & 255u);
-                v = (h2f(a.meta16[sbi]) * sc) * ((float)u - 32.0f);
+                return (h2f(mm) * sc) * ((float)u - 32.0f);
             }
         }
-        dst[k] = v;
+    };
+    // NB inputs a thread at a time: every load of the batch is issued before the first value
+    constexpr int NB = 8;
+    for (int k0 = threadIdx.x; k0 < a.K; k0 += NB * blockDim.x) {
+        Fields x[NB];
+#pragma unroll
+        for (int kk = 0; kk < NB; kk++) {
+            const int k = k0 + kk * (int)blockDim.x;
+            x[kk] = load(k < a.K ? k : k0);  // past K: a repeat of k0's fields, not stored
+        }
+#pragma unroll
+        for (int kk = 0; kk < NB; kk++) {
+            const int k = k0 + kk * (int)blockDim.x;
+            if (k < a.K) dst[k] = value(k, x[kk]);
+        }
     }
 }
 
@@ -139,7 +172,7 @@ __global__ __launch_bounds__(256) void gguf_pick_embed_kernel(GgufArgs a, const 
     __shared__ int s_pick;
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const ArgmaxPart *P = parts + (int64_t)b * nparts;
-    const int step = state[1];  // read with the partials (this workgroup reads it before any advance)
+    const int pos = state[0], step = state[1];  // read with the partials (before any advance)
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     // 4 partials a thread in flight at a time (the first-maximum rule is order-free)
@@ -173,7 +206,7 @@ __global__ __launch_bounds__(256) void gguf_pick_embed_kernel(GgufArgs a, const 
         gen[(int64_t)step * B + b] = best.idx;
         s_pick = best.idx;
         if (gridDim.x == 1) {  // the only reader of the step
-            state[0] += 1;
+            state[0] = pos + 1;
             state[1] = step + 1;
         } else {
             __threadfence();

@@ -315,6 +315,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
             wr[i] = llmq_bload16(rr_, off < (uint32_t)AL.xq ? off : kLlmqOOB);
         }
     }
+    // Codes, and the dwords holding the row's scale (16 bits at 16 (rr & 1)) and
+    // zero point (8 bits at 8 (rr & 3)): whole-dword values in flight need no
+    // masking until they are used.
     uint4 wc[WIN];
     uint32_t wsc[WIN], wzp[WIN];
     __builtin_amdgcn_sched_barrier(0);
@@ -322,8 +325,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     for (int u = 0; u < WIN; u++) {
         wc[u] = bload16_stream(rc, code_off(b_lo + u));
         const uint32_t mo = meta_off(b_lo + u);
-        wsc[u] = llmq_bload2(rs, mo == kLlmqOOB ? kLlmqOOB : mo * 2u);
-        wzp[u] = llmq_bload1(rz, mo);
+        wsc[u] = llmq_bload4(rs, mo == kLlmqOOB ? kLlmqOOB : (mo * 2u) & ~3u);
+        wzp[u] = llmq_bload4(rz, mo & ~3u);
     }
     const bool row_ok = live && ks == 0 && g == 0 && o < a.n;
     const auto rb = llmq_rsrc(a.bias, (uint32_t)a.n * 4u);
@@ -358,56 +361,80 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     float acc0 = 0.0f, acc1 = 0.0f;
     float *hd = hand + (size_t)ol * nb * 192;
     const uint32_t K1 = 0x11111111u;
-    for (int b0 = b_lo; b0 < b_hi; b0 += WIN) {
+    // Block b's codes, scale and zero point (zeros past the wave's blocks).
+    auto fetch = [&](int b, uint4 &w, uint32_t &sv, uint32_t &zv) {
+        w = bload16_stream(rc, code_off(b));
+        const uint32_t mo = meta_off(b);
+        sv = llmq_bload4(rs, mo == kLlmqOOB ? kLlmqOOB : (mo * 2u) & ~3u);
+        zv = llmq_bload4(rz, mo & ~3u);
+    };
+    // Block b's half sums and scale into the hand-off slots.
+    auto block = [&](int b, const uint4 d, uint32_t wscv, uint32_t wzpv) {
+        const int c = 8 * b + g;
+        const float sc = __half2float(__ushort_as_half((unsigned short)(wscv >> (16 * (rr & 1)))));
+        const int zp = (int)((wzpv >> (8 * (rr & 3))) & 255u);
+        const uint4 *P = reinterpret_cast<const uint4 *>(planes + c * kPlaneStride);
+        const uint4 p0 = P[0], p1 = P[1], p2 = P[2], p3 = P[3];
+        const int2 hs = reinterpret_cast<const int2 *>(hsum)[c];
+        // half 0: code dwords 0, 1; half 1: dwords 2, 3
+        uint32_t a0 = __builtin_amdgcn_udot8(p0.x, d.x, 0u, false);
+        a0 = __builtin_amdgcn_udot8(p1.x, d.y, a0, false);
+        uint32_t a1 = __builtin_amdgcn_udot8(p0.y, d.x, 0u, false);
+        a1 = __builtin_amdgcn_udot8(p1.y, d.y, a1, false);
+        uint32_t a2 = __builtin_amdgcn_udot8(p0.z, d.x, 0u, false);
+        a2 = __builtin_amdgcn_udot8(p1.z, d.y, a2, false);
+        uint32_t a3 = __builtin_amdgcn_udot8(p0.w, d.x, 0u, false);
+        a3 = __builtin_amdgcn_udot8(p1.w, d.y, a3, false);
+        uint32_t b0s = __builtin_amdgcn_udot8(p2.x, d.z, 0u, false);
+        b0s = __builtin_amdgcn_udot8(p3.x, d.w, b0s, false);
+        uint32_t b1s = __builtin_amdgcn_udot8(p2.y, d.z, 0u, false);
+        b1s = __builtin_amdgcn_udot8(p3.y, d.w, b1s, false);
+        uint32_t b2s = __builtin_amdgcn_udot8(p2.z, d.z, 0u, false);
+        b2s = __builtin_amdgcn_udot8(p3.z, d.w, b2s, false);
+        uint32_t b3s = __builtin_amdgcn_udot8(p2.w, d.z, 0u, false);
+        b3s = __builtin_amdgcn_udot8(p3.w, d.w, b3s, false);
+        uint32_t su0 = __builtin_amdgcn_udot8(d.x, K1, 0u, false);
+        su0 = __builtin_amdgcn_udot8(d.y, K1, su0, false);
+        uint32_t su1 = __builtin_amdgcn_udot8(d.z, K1, 0u, false);
+        su1 = __builtin_amdgcn_udot8(d.w, K1, su1, false);
+        const uint32_t xu0 = a0 + (a1 << 4) + (a2 << 8) + (a3 << 12);
+        const uint32_t xu1 = b0s + (b1s << 4) + (b2s << 8) + (b3s << 12);
+        const int G0 = (int)(xu0 - 32768u * su0) - zp * hs.x;
+        const int G1 = (int)(xu1 - 32768u * su1) - zp * hs.y;
+        if (DBG && live && o < a.n) a.dbg[(size_t)o * a.CK + c] = G0 + G1;
+        // to LDS: the chains run once every block is in (keeping them
+        // out of the loop leaves its iterations independent)
+        hd[(b * 3 + 0) * 64 + lane] = (float)G0;
+        hd[(b * 3 + 1) * 64 + lane] = (float)G1;
+        hd[(b * 3 + 2) * 64 + lane] = sc;
+    };
+    // Two register sets take turns (blocks b0 .. in wc, b0 + WIN .. in wn), so
+    // a block's loads land in the registers the loop reads them from and the
+    // WIN blocks in flight stay in flight across iterations (one set, re-filled
+    // while its old values were still live, cost a copy, and a wait for the
+    // loads just issued, at every iteration's end).
+    uint4 wn[WIN];
+    uint32_t wsn[WIN], wzn[WIN];
+    for (int b0 = b_lo; b0 < b_hi; b0 += 2 * WIN) {
 #pragma unroll
         for (int u = 0; u < WIN; u++) {
             const int b = b0 + u;
-            if (b < b_hi) {  // wave-uniform
             const uint4 d = wc[u];
-            const int c = 8 * b + g;
-            const float sc = __half2float(__ushort_as_half((unsigned short)wsc[u]));
-            const int zp = (int)wzp[u];
+            const uint32_t sv = wsc[u], zv = wzp[u];
             __builtin_amdgcn_sched_barrier(0);
-            wc[u] = bload16_stream(rc, code_off(b + WIN));
-            const uint32_t mo = meta_off(b + WIN);
-            wsc[u] = llmq_bload2(rs, mo == kLlmqOOB ? kLlmqOOB : mo * 2u);
-            wzp[u] = llmq_bload1(rz, mo);
+            fetch(b + WIN, wn[u], wsn[u], wzn[u]);
             __builtin_amdgcn_sched_barrier(0);
-            const uint4 *P = reinterpret_cast<const uint4 *>(planes + c * kPlaneStride);
-            const uint4 p0 = P[0], p1 = P[1], p2 = P[2], p3 = P[3];
-            const int2 hs = reinterpret_cast<const int2 *>(hsum)[c];
-            // half 0: code dwords 0, 1; half 1: dwords 2, 3
-            uint32_t a0 = __builtin_amdgcn_udot8(p0.x, d.x, 0u, false);
-            a0 = __builtin_amdgcn_udot8(p1.x, d.y, a0, false);
-            uint32_t a1 = __builtin_amdgcn_udot8(p0.y, d.x, 0u, false);
-            a1 = __builtin_amdgcn_udot8(p1.y, d.y, a1, false);
-            uint32_t a2 = __builtin_amdgcn_udot8(p0.z, d.x, 0u, false);
-            a2 = __builtin_amdgcn_udot8(p1.z, d.y, a2, false);
-            uint32_t a3 = __builtin_amdgcn_udot8(p0.w, d.x, 0u, false);
-            a3 = __builtin_amdgcn_udot8(p1.w, d.y, a3, false);
-            uint32_t b0s = __builtin_amdgcn_udot8(p2.x, d.z, 0u, false);
-            b0s = __builtin_amdgcn_udot8(p3.x, d.w, b0s, false);
-            uint32_t b1s = __builtin_amdgcn_udot8(p2.y, d.z, 0u, false);
-            b1s = __builtin_amdgcn_udot8(p3.y, d.w, b1s, false);
-            uint32_t b2s = __builtin_amdgcn_udot8(p2.z, d.z, 0u, false);
-            b2s = __builtin_amdgcn_udot8(p3.z, d.w, b2s, false);
-            uint32_t b3s = __builtin_amdgcn_udot8(p2.w, d.z, 0u, false);
-            b3s = __builtin_amdgcn_udot8(p3.w, d.w, b3s, false);
-            uint32_t su0 = __builtin_amdgcn_udot8(d.x, K1, 0u, false);
-            su0 = __builtin_amdgcn_udot8(d.y, K1, su0, false);
-            uint32_t su1 = __builtin_amdgcn_udot8(d.z, K1, 0u, false);
-            su1 = __builtin_amdgcn_udot8(d.w, K1, su1, false);
-            const uint32_t xu0 = a0 + (a1 << 4) + (a2 << 8) + (a3 << 12);
-            const uint32_t xu1 = b0s + (b1s << 4) + (b2s << 8) + (b3s << 12);
-            const int G0 = (int)(xu0 - 32768u * su0) - zp * hs.x;
-            const int G1 = (int)(xu1 - 32768u * su1) - zp * hs.y;
-            if (DBG && live && o < a.n) a.dbg[(size_t)o * a.CK + c] = G0 + G1;
-            // to LDS: the chains run once every block is in (keeping them
-            // out of the loop leaves its iterations independent)
-            hd[(b * 3 + 0) * 64 + lane] = (float)G0;
-            hd[(b * 3 + 1) * 64 + lane] = (float)G1;
-            hd[(b * 3 + 2) * 64 + lane] = sc;
-            }
+            if (b < b_hi) block(b, d, sv, zv);  // wave-uniform
+        }
+#pragma unroll
+        for (int u = 0; u < WIN; u++) {
+            const int b = b0 + WIN + u;
+            const uint4 d = wn[u];
+            const uint32_t sv = wsn[u], zv = wzn[u];
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(b + WIN, wc[u], wsc[u], wzp[u]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (b < b_hi) block(b, d, sv, zv);
         }
     }
     if constexpr (KS > 1) llmq_lds_barrier();  // (KS == 1: the wave reads its own writes)

@@ -279,6 +279,18 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
             if (a.swiglu) xu[i] = bload16(rx, u < (uint32_t)nunits ? (u + (uint32_t)nunits) * 16u : kOOB);
         }
     }
+    // the RMSNorm gain of the same units, with the row (it is not needed before
+    // the norm); 16-wave forms (128 registers a lane) load it in the norm's loop
+    constexpr int GU = NW <= 8 ? UPT : 0;
+    uint4 gv[GU > 0 ? GU : 1];
+    {
+        const auto rg = make_rsrc(a.rms_g, a.rms_g ? (uint32_t)K * 4u : 0u);
+#pragma unroll
+        for (int i = 0; i < GU; i++) {
+            const uint32_t u = (uint32_t)(tid + NT * i);
+            gv[i] = bload16(rg, a.rms_g && u < (uint32_t)nunits ? u * 16u : kOOB);
+        }
+    }
     // Global chunk indices of the wave's first and last valid chunks.
     const int gE = g0 + max(ns, 1) - 1;
     const int tE = (int)((uint32_t)gE / (uint32_t)S), sE = gE - tE * S;
@@ -370,15 +382,22 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
         for (int i = 1; i < NW; i++) ss += s_red[i];
         const float r = 1.0f / sqrtf(ss / (float)K + a.rms_eps);
         const float4 *g4 = reinterpret_cast<const float4 *>(a.rms_g);
-        for (int u = tid; u < nunits; u += NT) {
+        auto norm = [&](int u, const float4 g) {
             float4 v = reinterpret_cast<const float4 *>(xs)[u];
-            const float4 g = g4[u];
             v.x = (v.x * r) * g.x;
             v.y = (v.y * r) * g.y;
             v.z = (v.z * r) * g.z;
             v.w = (v.w * r) * g.w;
             reinterpret_cast<float4 *>(xs)[u] = v;
+        };
+#pragma unroll
+        for (int i = 0; i < GU; i++) {
+            const int u = tid + NT * i;
+            if (u < nunits)
+                norm(u, make_float4(__uint_as_float(gv[i].x), __uint_as_float(gv[i].y), __uint_as_float(gv[i].z),
+                                    __uint_as_float(gv[i].w)));
         }
+        for (int u = tid + NT * GU; u < nunits; u += NT) norm(u, g4[u]);
         lds_barrier();
     }
     if (a.ln_w) {  // LayerNorm of the staged row (kernels.layernorm, kernels.mojo:179-197), fused

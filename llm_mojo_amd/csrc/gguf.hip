@@ -74,7 +74,7 @@ __device__ __forceinline__ void dequant_row_body(const GgufArgs &a, int64_t row,
     };
     auto load = [&](int k) {
         Fields x{};
-        const int c = k / F::WPC, e = k % F::WPC;
+        const int c = k / F::WPC;
         const size_t mi = ((size_t)tile * a.CK + c) * 16 + r;
         const size_t sbi = ((size_t)tile * a.NSB + c / F::CPS) * 16 + r;
         x.d = a.codes[mi];
@@ -87,7 +87,6 @@ __device__ __forceinline__ void dequant_row_body(const GgufArgs &a, int64_t row,
             x.hb = a.bits64[mi];
             x.m = a.meta16[sbi];
         }
-        (void)e;
         return x;
     };
     auto value = [&](int k, const Fields &x) -> float {

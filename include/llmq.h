@@ -143,6 +143,20 @@ LLMQ_API int llmq_mat_export(llmq_ctx *ctx, const llmq_mat *mat, uint8_t *codes,
 LLMQ_API int llmq_mat_restore(llmq_ctx *ctx, int bits, int group, int sym, int a16, int64_t rows, int64_t cols,
                               const uint8_t *codes, const uint16_t *scales, const uint8_t *zps, llmq_mat **out);
 LLMQ_API int llmq_mat_dequant_row(llmq_ctx *ctx, const llmq_mat *mat, int64_t row, float *dst);
+/* QuantMatrix.dot_row_i16 (tensor.mojo:518-577), the trait's per-row int16
+ * dot (WeightMatrix.dot_row_i16, tensor.mojo:122-125), for rows row ..
+ * row + nrows - 1: out[i] = row (row + i) . xq in weight scale (the caller
+ * multiplies by the activations' sx, as matmul_rows_a16 does,
+ * kernels.mojo:444-452), bit for bit the reference's float result for each
+ * of its three branches (BLOCKED int4-g32, int8 per channel, the general
+ * per-group loop).  xq: K int16 activation codes in natural column order
+ * (device memory, as llmq_quantize_rows writes them): for BLOCKED matrices
+ * permute_x_i16 (tensor.mojo:498-516) is the layout's concern and happens
+ * inside.  out: nrows floats of device memory; stream-ordered.  A16
+ * matrices only (the others abort in the reference, tensor.mojo:120-125:
+ * here LLMQ_EINVAL).  For parity checks; the GEMVs do not use it. */
+LLMQ_API int llmq_dot_row_i16(llmq_ctx *ctx, const llmq_mat *mat, int64_t row, int64_t nrows, const int16_t *xq,
+                              float *out);
 
 /* --------------------------------------------------------- compute (device) */
 
@@ -162,11 +176,13 @@ LLMQ_API int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_m
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  Same arguments, kernels and results
  * (bit for bit) as llmq_linear; where llmq_linear grows the context's
- * workspace (the prompt GEMM's int16 activation codes and row scales), this
- * form uses a fixed per-GPU scratch array of LLMQ_NOALLOC_SCRATCH_BYTES
- * that each GPU the library runs on holds until the process ends.  It
- * calls no hipMalloc / hipFree.  Sizes needing more scratch than that
- * (T x IN x 2 bytes rounded up to 256, plus T x 4) return LLMQ_EINVAL.
+ * workspace (the a16 prompt GEMM's int16 activation codes and row scales,
+ * the Q4_K matmul's fp16 activation record), this form uses a fixed
+ * per-GPU scratch array of LLMQ_NOALLOC_SCRATCH_BYTES that each GPU the
+ * library runs on holds until the process ends.  It calls no hipMalloc /
+ * hipFree.  Sizes needing more scratch than that (a16: T x IN x 2 bytes
+ * rounded up to 256, plus T x 4; Q4_K: the record's ~4.4 x T x IN bytes,
+ * T rounded up to 16) return LLMQ_EINVAL; other formats use no scratch.
  * Every call on one GPU shares the array: calls that overlap in time on one
  * GPU (different streams or threads) race; calls ordered on one stream do
  * not.  Nothing in the scratch needs to start at zero (each call writes all

@@ -44,6 +44,7 @@ SIGNATURES = {
     "llmq_mat_shape": (I32, [P, ctypes.POINTER(I64), ctypes.POINTER(I64)]),
     "llmq_mat_export": (I32, [P, P, P, P, P]),
     "llmq_mat_dequant_row": (I32, [P, P, I64, P]),
+    "llmq_dot_row_i16": (I32, [P, P, I64, I64, P, P]),
     "llmq_quantize_rows": (I32, [P, P, I64, I64, P, P]),
     "llmq_linear": (I32, [P, P, P, P, P, I64, I64, I64, I32]),
     "llmq_linear_noalloc": (I32, [P, P, P, P, P, I64, I64, I64, I32]),

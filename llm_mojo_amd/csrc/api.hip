@@ -383,6 +383,11 @@ int llmq_mat_restore(llmq_ctx *ctx, int bits, int group, int sym, int a16, int64
     return LLMQ_OK;
 }
 
+int llmq_dot_row_i16(llmq_ctx *ctx, const llmq_mat *m, int64_t row, int64_t nrows, const int16_t *xq, float *out) {
+    LLMQ_REQUIRE(ctx && m, "dot_row_i16: bad arguments");
+    return launch_dot_row_i16(ctx, m, row, nrows, xq, out);
+}
+
 int llmq_mat_dequant_row(llmq_ctx *ctx, const llmq_mat *m, int64_t row, float *dst) {
     LLMQ_REQUIRE(ctx && m && dst, "dequant_row: bad arguments");
     LLMQ_REQUIRE(row >= 0 && row < m->n, "dequant_row: row %lld out of range", (long long)row);
@@ -479,16 +484,18 @@ int llmq_linear_noalloc(llmq_ctx *ctx, float *out, const float *x, const llmq_ma
     LLMQ_REQUIRE(ctx && ctx->scratch, "linear_noalloc: null context");
     RC(check_linear(w, IN, OUT));
     LLMQ_REQUIRE(T >= 1, "linear_noalloc: T must be >= 1");
-    // the most the prompt GEMM keeps there: T x IN int16 codes (rounded up to
-    // 256 bytes) and T float scales
+    if (is_float_act(w)) {
+        // the one-token GEMV uses no scratch; several tokens of Q4_K keep
+        // their fp16 activation record there (the other types use none)
+        if (T == 1) return launch_gguf_gemv(ctx, w, x, out, bias, flags, nullptr, 0);
+        return launch_gguf_gemm(ctx, w, x, IN, T, out, OUT, bias, flags, ctx->scratch, LLMQ_NOALLOC_SCRATCH_BYTES);
+    }
+    // the most the int16 prompt GEMM keeps there: T x IN int16 codes
+    // (rounded up to 256 bytes) and T float scales
     const int64_t need = ((T * IN * 2 + 255) & ~(int64_t)255) + T * 4;
     LLMQ_REQUIRE(need <= (int64_t)LLMQ_NOALLOC_SCRATCH_BYTES,
                  "linear_noalloc: %lld tokens x %lld inputs need %lld bytes of scratch, the maximum is %d",
                  (long long)T, (long long)IN, (long long)need, LLMQ_NOALLOC_SCRATCH_BYTES);
-    if (is_float_act(w)) {  // the one-token GEMV and the fp32-core matmul use no scratch
-        if (T == 1) return launch_gguf_gemv(ctx, w, x, out, bias, flags, nullptr, 0);
-        return launch_gguf_gemm(ctx, w, x, IN, T, out, OUT, bias, flags, nullptr, 0);
-    }
     GemvRequest rq;
     rq.w = w;
     rq.x = x;
@@ -877,6 +884,7 @@ int gpt2_finish(llmq_gpt2 *m, int attention, const float *small_host) {
     if (float_act || is_float_act(m->wte)) RC(alloc(m->xn, sizeof(float) * MAXT * C));
     if (!m->gguf) {  // the head's argmax partials for the device-driven decode loop
         m->nparts = m->wte->a16 ? gemv_a16_num_parts(m->wte, true) : gguf_num_parts(m->wte);
+        LLMQ_REQUIRE(m->nparts > 0, "gpt2: the head kernel leaves no argmax partials");
         RC(alloc(m->parts, sizeof(ArgmaxPart) * m->nparts));
         // no stale partial can win an argmax before the first head runs
         const std::vector<ArgmaxPart> none((size_t)m->nparts, ArgmaxPart{-INFINITY, 0x7fffffff});

@@ -1130,6 +1130,8 @@ int launch_layernorm(llmq_ctx *ctx, float *out, const float *x, const float *w, 
 int launch_embed(llmq_ctx *ctx, const llmq_mat *E, const float *wpe, const int64_t *tokens, int T, int pos0,
                  float *x, const ArgmaxPart *parts, int nparts, int64_t *gen, int *state, int do_embed) {
     LLMQ_REQUIRE(E && E->kind == MAT_QUANT, "embed: the embedding must be a QuantMatrix");
+    LLMQ_REQUIRE(parts ? nparts > 0 && gen && state : tokens && T >= 1,
+                 "embed: tokens, or argmax partials with the decode state");
     const int64_t cpg = E->group / (E->bits == 4 ? 32 : 16);
     hipLaunchKernelGGL(embed_kernel, dim3(parts ? 1 : T), dim3(256), 0, ctx->stream,
                        reinterpret_cast<const uint4 *>(E->codes), E->scales, E->zps, E->bits, E->CK, E->NG, cpg, wpe,

@@ -206,6 +206,8 @@ int gemv1_num_parts(const llmq_mat *w, bool ln);
 bool gemv_exact_supports(const llmq_mat *w);
 int gemv_exact_num_parts(const llmq_mat *w);
 int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq);
+// QuantMatrix.dot_row_i16 for rows row0 .. row0 + nrows - 1 (gemv_exact.hip).
+int launch_dot_row_i16(llmq_ctx *ctx, const llmq_mat *w, int64_t row0, int64_t nrows, const int16_t *xq, float *out);
 
 // A prepared activation record (llmq_act_prepare): one token's row after
 // quantize_rows, in the forms the one-token integer GEMVs read, at byte
@@ -247,14 +249,22 @@ int gguf_num_parts(const llmq_mat *w);
 // [gate | up] and the row is silu(gate) * up; with ln_w the row goes through
 // LayerNorm (eps 1e-5, weight ln_w, bias ln_b) first.  With apart, x is
 // not read: the row is the combination of decode attention splits (64-dim
-// heads, ns_max splits of asplit positions a head, position astate[0];
-// llama.hip's attend_split_kernel layout), which gguf_gemv_attn_ok(w,
-// ns_max) says the kernel can take.
+// heads, ns_max splits of asplit positions a head, position astate[0]; the
+// split record above), which gguf_gemv_attn_ok(w, ns_max, head_dim) says
+// the kernel can take.
+// The decode attention split record (written by llama.hip's split kernels,
+// read by its combine kernel and by the Wo GEMV in gguf1.hip): per head of
+// kLlmqSplitHD dimensions and split, the maximum score m, the sum t of
+// exp(score - m), two unused floats, then the head's kLlmqSplitHD partial
+// value sums; at most kLlmqMaxSplits splits a head.
+constexpr int kLlmqSplitHD = 64;
+constexpr int kLlmqSplitRec = 4 + kLlmqSplitHD;  // floats of one record
+constexpr int kLlmqMaxSplits = 8;
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,
                      ArgmaxPart *amax, int amax_cap, const float *rms_g = nullptr, float rms_eps = 0.0f,
                      int swiglu = 0, const float *ln_w = nullptr, const float *ln_b = nullptr,
                      const float *apart = nullptr, const int *astate = nullptr, int asplit = 0, int ans_max = 0);
-bool gguf_gemv_attn_ok(const llmq_mat *w, int ns_max);
+bool gguf_gemv_attn_ok(const llmq_mat *w, int ns_max, int head_dim);
 int launch_gguf_dequant_row(llmq_ctx *ctx, const llmq_mat *w, int64_t row, float *dst);
 int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *rows, int n, float *dst, int64_t ldd);
 // Greedy pick of each of B sequences from a head's argmax partials (nparts

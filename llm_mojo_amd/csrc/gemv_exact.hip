@@ -247,6 +247,7 @@ struct BlkArgs {
     int32_t *dbg;
     int16_t *xq_out;
     float *sx_out;
+    ArgmaxPart *amax;  // per-workgroup argmax partials (a head), or null
 };
 
 // Workgroup: NW waves over NW / KS row octets; the KS waves of an octet
@@ -466,12 +467,39 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     v = v + llmq_from_lane_plus32(v);
     v = v + llmq_from_lane_plus16(v);
     v = v + llmq_dppf<0x108>(v);  // row_shl:8
+    float r = -INFINITY;
     if (row_ok) {
-        float r = v * sx;
+        r = v * sx;
         if (a.flags & LLMQ_BIAS) r += e_bias;
         if (a.flags & LLMQ_GELU) r = gelu_ref(r);
         if (a.flags & LLMQ_RESID) r += e_res;
         a.out[o] = r;
+    }
+    if (a.amax) {  // (uniform over the grid: every wave reaches the barrier)
+        // largest output of the workgroup; equal values keep the smaller
+        // index (argmax's first maximum, gpt2t.mojo:792-797)
+        __shared__ ArgmaxPart s_best[NW];
+        float best_v = r;
+        int best_i = row_ok ? o : 0x7fffffff;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(best_v, off);
+            const int oi = __shfl_xor(best_i, off);
+            if (ov > best_v || (ov == best_v && oi < best_i)) {
+                best_v = ov;
+                best_i = oi;
+            }
+        }
+        if (lane == 0) s_best[wid] = ArgmaxPart{best_v, best_i};
+        llmq_lds_barrier();
+        if (tid == 0) {
+            ArgmaxPart b = s_best[0];
+            for (int q = 1; q < NW; q++) {
+                const ArgmaxPart c = s_best[q];
+                if (c.v > b.v || (c.v == b.v && c.idx < b.idx)) b = c;
+            }
+            a.amax[blockIdx.x] = b;
+        }
     }
 }
 
@@ -780,6 +808,27 @@ void head8_shape(const llmq_mat *w, int *nw, int *tpw, int *grid, int *iters) {
     *grid = (groups + *iters - 1) / *iters;
 }
 
+// Shape of the BLOCKED kernel for w: ks waves a row octet, win blocks in
+// flight a wave, grid workgroups (= argmax partials).  4-wave workgroups; KS
+// waves per row octet split its blocks so that long rows still spread over
+// enough waves (and CUs); two blocks in flight per wave (measured best from
+// 768 to 4096 inputs).  LLMQ_BLK_KS / LLMQ_BLK_WIN override, for measurement.
+void blk_shape(const llmq_mat *w, bool dbg, int *ks_out, int *win_out, int *grid) {
+    const int nb = (int)(w->k / 256);
+    int ks = nb >= 8 ? 4 : nb >= 4 ? 2 : 1;
+    const int64_t bytes = w->ntiles * w->CK * 256;
+    if (bytes >= (20ll << 20)) ks = nb >= 4 ? 2 : 1;
+    if (const char *e = getenv("LLMQ_BLK_KS")) ks = atoi(e) == 1 ? 1 : atoi(e) == 2 ? 2 : 4;
+    if (dbg) ks = 1;
+    int win = 2;
+    if (const char *e = getenv("LLMQ_BLK_WIN")) win = atoi(e);
+    if (dbg) win = 4;
+    const int opw = 4 / ks;
+    *ks_out = ks;
+    *win_out = win;
+    *grid = (int)((2 * w->ntiles + opw - 1) / opw);
+}
+
 // Shared by both activation forms: rq.x (floats) or rec (a prepared record).
 int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     const llmq_mat *w = rq.w;
@@ -788,7 +837,10 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     LLMQ_REQUIRE(!(rec && (ln || rq.dbg || rq.xq_out)), "linear: a prepared record takes no LayerNorm or debug output");
     const int K = (int)w->k;
     if (w->bits == 4) {
-        LLMQ_REQUIRE(!rq.amax, "linear: argmax partials need the int8 head kernel");
+        int ks, win, grid;
+        blk_shape(w, rq.dbg != nullptr, &ks, &win, &grid);
+        LLMQ_REQUIRE(!rq.amax || grid <= rq.amax_cap, "linear: %d argmax partials exceed capacity %d", grid,
+                     rq.amax_cap);
         BlkArgs a;
         a.codes = reinterpret_cast<const uint4 *>(w->codes);
         a.scales = w->scales;
@@ -810,20 +862,8 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
         a.dbg = rq.dbg;
         a.xq_out = rq.xq_out;
         a.sx_out = rq.sx_out;
-        // 4-wave workgroups; KS waves per row octet split its blocks so that
-        // long rows still spread over enough waves (and CUs); two blocks in
-        // flight per wave (measured best from 768 to 4096 inputs)
-        const int nb = K / 256;
-        int ks = nb >= 8 ? 4 : nb >= 4 ? 2 : 1;
-        const int64_t bytes = w->ntiles * w->CK * 256;
-        if (bytes >= (20ll << 20)) ks = nb >= 4 ? 2 : 1;
-        if (const char *e = getenv("LLMQ_BLK_KS")) ks = atoi(e) == 1 ? 1 : atoi(e) == 2 ? 2 : 4;
-        if (a.dbg) ks = 1;
-        int win = 2;
-        if (const char *e = getenv("LLMQ_BLK_WIN")) win = atoi(e);
-        if (a.dbg) win = 4;
-        const int opw = 4 / ks;
-        const int grid = (int)((a.nwaves + opw - 1) / opw);
+        a.amax = rq.amax;
+        const int nb = K / 256, opw = 4 / ks;
         LLMQ_REQUIRE(!rec || llmq_act_layout(K).xq <= 6 * 16 * 256, "linear_act: reduction axis %d too long", K);
         const size_t lds = (size_t)w->CK * (kPlaneStride + 2) * 4 + (ln ? (size_t)K * 4 : 0) +
                            (size_t)opw * nb * 3 * 64 * 4;
@@ -836,6 +876,7 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
         }
         if (rc != LLMQ_OK) return rc;
         LLMQ_HIP(hipGetLastError());
+        if (rq.amax_count) *rq.amax_count = grid;
         return LLMQ_OK;
     }
     // int8 per channel
@@ -913,9 +954,15 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
 bool gemv_exact_supports(const llmq_mat *w) { return exact_supports(w); }
 
 int gemv_exact_num_parts(const llmq_mat *w) {
-    int nw, tpw, grid, iters;
-    head8_shape(w, &nw, &tpw, &grid, &iters);
-    return w->bits == 8 ? grid : 0;
+    int grid;
+    if (w->bits == 4) {
+        int ks, win;
+        blk_shape(w, false, &ks, &win, &grid);
+    } else {
+        int nw, tpw, iters;
+        head8_shape(w, &nw, &tpw, &grid, &iters);
+    }
+    return grid;
 }
 
 int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq) { return launch_exact(ctx, rq, nullptr); }
@@ -954,4 +1001,99 @@ int launch_linear_act(llmq_ctx *ctx, float *out, const void *rec, const llmq_mat
     rq.T = 1;
     rq.flags = flags;
     return launch_exact(ctx, rq, static_cast<const uint8_t *>(rec));
+}
+
+// ------------------------------------------------- dot_row_i16 per row
+
+namespace {
+
+// Code of column k of row `row` in the row-tile layout (16-byte chunks of
+// 32 int4 codes, weight e at dword e >> 3, nibble e & 7; or of 16 int8
+// codes, byte e).
+__device__ __forceinline__ int tile_code(const uint8_t *codes, int bits, int64_t CK, int64_t row, int64_t k) {
+    const int64_t tile = row >> 4, r = row & 15;
+    if (bits == 4) {
+        const int64_t c = k >> 5, e = k & 31;
+        const uint8_t b = codes[((tile * CK + c) * 16 + r) * 16 + 4 * (e >> 3) + ((e & 7) >> 1)];
+        return (e & 1) ? b >> 4 : b & 15;
+    }
+    const int64_t c = k >> 4;
+    return codes[((tile * CK + c) * 16 + r) * 16 + (k & 15)];
+}
+
+// QuantMatrix.dot_row_i16 (tensor.mojo:518-577): four rows a wave, lane
+// L = tid & 15 of a row's 16 standing for the reference's SIMD lane L, with
+// its int32 sums (wrapping, as VPDPWSSD does), its float chain and the
+// 16-lane halving sum, so each result is the reference's bit for bit.
+// xq holds the int16 codes in natural column order; the BLOCKED branch
+// gathers, for lane L, the activations permute_x_i16 would give it
+// (tensor.mojo:498-516: group L % 8, weights 16 (L / 8) .. + 15 of every
+// 256-block) and their float sum.
+__global__ __launch_bounds__(64) void dot_row_i16_kernel(const uint8_t *__restrict__ codes,
+                                                         const uint16_t *__restrict__ scales,
+                                                         const uint8_t *__restrict__ zps, int bits, int blocked,
+                                                         int64_t K, int64_t G, int64_t CK, int64_t NG, int64_t row0,
+                                                         int64_t nrows, const int16_t *__restrict__ xq,
+                                                         float *__restrict__ out) {
+    const int L = threadIdx.x & 15;
+    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 4);
+    const bool live = i < nrows;
+    const int64_t row = row0 + (live ? i : 0);
+    const int64_t tile = row >> 4, r = row & 15;
+    auto scale_of = [&](int64_t g) { return __half2float(__ushort_as_half(scales[(tile * NG + g) * 16 + r])); };
+    auto zp_of = [&](int64_t g) { return (int)zps[(tile * NG + g) * 16 + r]; };
+    float accf = 0.0f;
+    if (blocked) {
+        const int g = L & 7, h = L >> 3;
+        for (int64_t blk = 0; blk < K / 256; blk++) {
+            uint32_t acc = 0;
+            float xs = 0.0f;
+            for (int e = 16 * h; e < 16 * h + 16; e++) {
+                const int64_t col = blk * 256 + 32 * g + e;
+                const int x = xq[col];
+                acc += (uint32_t)(x * tile_code(codes, 4, CK, row, col));
+                xs += (float)x;  // exact: at most 16 * 32767
+            }
+            const int64_t gi = blk * 8 + g;
+            accf = fmaf((float)(int)acc - (float)zp_of(gi) * xs, scale_of(gi), accf);
+        }
+    } else {
+        // lane L: pairs (2L, 2L + 1) of every 32-column piece, minus the
+        // zero point (codes_i16); one float step per group, or per row for
+        // int8 per channel (fma with 0 at the end)
+        const bool ch8 = bits == 8 && NG == 1;
+        for (int64_t g = 0; g < K / G; g++) {
+            const int zp = zp_of(g);
+            uint32_t acc = 0;
+            for (int64_t k0 = g * G; k0 < (g + 1) * G; k0 += 32) {
+                const int64_t k = k0 + 2 * L;
+                acc += (uint32_t)(xq[k] * (tile_code(codes, bits, CK, row, k) - zp));
+                acc += (uint32_t)(xq[k + 1] * (tile_code(codes, bits, CK, row, k + 1) - zp));
+            }
+            accf = ch8 ? fmaf((float)(int)acc, scale_of(g), 0.0f) : fmaf((float)(int)acc, scale_of(g), accf);
+        }
+    }
+    // reduce_add: lanes (L, L + 8), then + 4, + 2, + 1
+    accf += __shfl_xor(accf, 8, 16);
+    accf += __shfl_xor(accf, 4, 16);
+    accf += __shfl_xor(accf, 2, 16);
+    accf += __shfl_xor(accf, 1, 16);
+    if (live && L == 0) out[i] = accf;
+}
+
+}  // namespace
+
+int launch_dot_row_i16(llmq_ctx *ctx, const llmq_mat *w, int64_t row0, int64_t nrows, const int16_t *xq, float *out) {
+    LLMQ_REQUIRE(w && w->kind == MAT_QUANT, "dot_row_i16: not a QuantMatrix");
+    LLMQ_REQUIRE(w->a16, "dot_row_i16: %s has no int16 path (an a16 format is needed)", "the matrix");
+    LLMQ_REQUIRE(xq && out, "dot_row_i16: null pointer");
+    LLMQ_REQUIRE(row0 >= 0 && nrows >= 1 && row0 + nrows <= w->n, "dot_row_i16: rows %lld..%lld beyond %lld",
+                 (long long)row0, (long long)(row0 + nrows), (long long)w->n);
+    const int blocked = w->bits == 4 && w->group_param == 32;  // tensor.mojo:296 (K in whole 256-blocks)
+    const int64_t grid = (nrows + 3) / 4;
+    LLMQ_REQUIRE(grid < (1ll << 31), "dot_row_i16: too many rows");
+    hipLaunchKernelGGL(dot_row_i16_kernel, dim3((unsigned)grid), dim3(64), 0, ctx->stream, w->codes, w->scales, w->zps,
+                       w->bits, blocked, w->k, w->group, w->CK, w->NG, row0, nrows, xq, out);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
 }

@@ -51,10 +51,11 @@ struct G1Args {
     int asplit, ans_max;       // positions a split covers, splits a head in apart
 };
 
-// Attention splits (llama.hip's attend_split_kernel): per 64-dim head,
-// ans_max records of kAPart floats (m, t, 2 unused, 64 partial sums).
-constexpr int kAPart = 68;
-constexpr int kACMax = 8;  // splits an AC kernel combines
+// Attention splits: per head, ans_max split records of kAPart floats (the
+// layout common.h fixes; a head's 64 sums are 16 float4 units).
+constexpr int kAPart = kLlmqSplitRec;
+constexpr int kACMax = kLlmqMaxSplits;  // splits an AC kernel combines
+static_assert(kLlmqSplitHD == 64, "the staging maps a row unit u to head u >> 4 (16 float4 units a head)");
 constexpr int kACUnits = 2;  // float4 row units a thread combines (K <= 2 * 4 * threads)
 
 // silu(g) * u per lane of two activation vectors (llama.hip's swiglu).
@@ -710,7 +711,8 @@ int qm_cpg_shift(const llmq_mat *w) {
 
 int gguf_num_parts(const llmq_mat *w) { return make_plan(w).grid; }
 
-bool gguf_gemv_attn_ok(const llmq_mat *w, int ns_max) {
+bool gguf_gemv_attn_ok(const llmq_mat *w, int ns_max, int head_dim) {
+    if (head_dim != kLlmqSplitHD) return false;
     if (!w || !is_float_act(w) || w->k % 64 != 0 || ns_max < 1 || ns_max > kACMax) return false;
     const Plan p = make_plan(w);
     return p.nw == 4 && (p.steps == 2 || p.steps == 4) && w->k / 4 <= (int64_t)kACUnits * 4 * 64;
@@ -722,7 +724,7 @@ int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *ou
                      int ans_max) {
     LLMQ_REQUIRE(w && is_float_act(w), "gguf_gemv: not a GGUF or float-activation QuantMatrix");
     LLMQ_REQUIRE((x || apart) && out, "gguf_gemv: null pointer");
-    LLMQ_REQUIRE(!apart || (gguf_gemv_attn_ok(w, ans_max) && astate && asplit > 0 && !rms_g && !swiglu && !ln_w),
+    LLMQ_REQUIRE(!apart || (gguf_gemv_attn_ok(w, ans_max, kLlmqSplitHD) && astate && asplit > 0 && !rms_g && !swiglu && !ln_w),
                  "gguf_gemv: attention-split input not supported for %lld x %lld", (long long)w->n, (long long)w->k);
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemv: LLMQ_BIAS without a bias");
     LLMQ_REQUIRE(w->k % 16 == 0, "gguf_gemv: cols must be a multiple of 16");

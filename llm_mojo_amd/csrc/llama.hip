@@ -175,8 +175,9 @@ __global__ __launch_bounds__(64) void rope_store_kernel(float *__restrict__ qkv,
 // read by no workgroup of this launch.  A score is q . (u - 128) over the
 // key's codes u = k + 128 (one byte conversion each): q . u - 128 sum(q).
 constexpr int kSplit = 256;
-constexpr int kPart = 4 + HD;  // floats of one split's result
-constexpr int kMaxSplits = 8;
+constexpr int kPart = kLlmqSplitRec;  // floats of one split's result (common.h's split record)
+constexpr int kMaxSplits = kLlmqMaxSplits;
+static_assert(HD == kLlmqSplitHD, "split records hold one head of HD dimensions");
 constexpr int kSW = kSplit / 64;  // waves of a split
 
 __global__ __launch_bounds__(kSplit) void attend_split_kernel(const float *__restrict__ qkv, int64_t ld,
@@ -871,7 +872,7 @@ int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *sta
                 hipLaunchKernelGGL(attend_split_kernel, dim3(c.n_head, R, NS), dim3(kSplit), 0, ctx->stream, m->qkv,
                                    (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope, m->k8,
                                    m->v8, m->ks, m->vs, m->apart, NS);
-            if (R == 1 && gguf_gemv_attn_ok(m->wo[l], NS)) {  // Wo combines the splits as it stages its row
+            if (R == 1 && gguf_gemv_attn_ok(m->wo[l], NS, HD)) {  // Wo combines the splits as it stages its row
                 RC(launch_gguf_gemv(ctx, m->wo[l], nullptr, m->x, nullptr, LLMQ_RESID, nullptr, 0, nullptr, 0.0f, 0,
                                     nullptr, nullptr, m->apart, state, kSplit, NS));
             } else if (rec_ok(m, m->wo[l]) && c.n_head % 4 == 0) {  // the combination writes Wo's record

@@ -95,6 +95,12 @@ class HipQuantMatrix:
         check(lib().llmq_mat_dequant_row(self.ctx.h, self.h, row, hptr(dst)))
         return dst
 
+    def dot_row_i16(self, row, xq, out, nrows=1):
+        """dot_row_i16 (tensor.mojo:518-577) of rows row .. row + nrows - 1
+        with int16 codes xq (device, natural column order) into out (device
+        floats), in weight scale; stream-ordered."""
+        check(lib().llmq_dot_row_i16(self.ctx.h, self.h, row, nrows, dptr(xq), dptr(out)))
+
     def free(self):
         if getattr(self, "h", None):
             lib().llmq_mat_free(self.h)

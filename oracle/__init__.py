@@ -108,6 +108,7 @@ def _declare(L):
         "orc_gguf_block_bytes": (I32, [I32]),
         "orc_k_scale_min": (None, [P, I32, P, P]),
         "orc_gguf_dequant_row": (None, [I32, P, I64, P]),
+        "orc_gguf_dequant_rows": (None, [I32, P, I64, I64, I64, P]),
         "orc_gguf_dot_row": (ctypes.c_float, [I32, P, I64, P]),
         "orc_gguf_dot_row_i16": (ctypes.c_float, [I32, P, I64, P]),
         "orc_gguf_unpack_row_i16": (None, [I32, P, I64, P, P]),
@@ -355,9 +356,9 @@ def gguf_block_bytes(t):
 def gguf_dequant(t, w, rows, cols):
     w = np.ascontiguousarray(w, np.uint8)
     rb = cols // gguf_block_size(t) * gguf_block_bytes(t)
+    assert w.size >= rows * rb, "gguf_dequant: too few block bytes"
     out = np.zeros((rows, cols), np.float32)
-    for r in range(rows):
-        lib().orc_gguf_dequant_row(t, w[r * rb:].ctypes.data, cols, ptr(out[r]))
+    lib().orc_gguf_dequant_rows(t, w.ctypes.data, rows, rb, cols, ptr(out))
     return out
 
 

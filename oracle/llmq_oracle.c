@@ -809,6 +809,11 @@ static float gguf_row(int t, const uint8_t *p, int64_t cols, float *dst, const f
     return red16(acc);
 }
 void orc_gguf_dequant_row(int t, const uint8_t *row, int64_t cols, float *dst) { (void)gguf_row(t, row, cols, dst, NULL, 0); }
+/* Every row of a GGUF matrix (rows of row_bytes each) into dst[rows, cols]. */
+void orc_gguf_dequant_rows(int t, const uint8_t *blocks, int64_t rows, int64_t row_bytes, int64_t cols, float *dst) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+    for (int64_t r = 0; r < rows; r++) (void)gguf_row(t, blocks + r * row_bytes, cols, dst + r * cols, NULL, 0);
+}
 float orc_gguf_dot_row(int t, const uint8_t *row, int64_t cols, const float *x) { return gguf_row(t, row, cols, NULL, x, 1); }
 
 /* q6_k_i16 (gguf.mojo:322-336): weights 128n + 32k .. +31 as (q - 32) * scale. */

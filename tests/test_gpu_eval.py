@@ -5,6 +5,8 @@ logits on the host."""
 import numpy as np
 import pytest
 
+from tests.gpt2_exact import bits_equal
+
 pytestmark = pytest.mark.gpu
 
 
@@ -42,28 +44,35 @@ def test_score_rows_matches_oracle(gpu, orc):
         assert np.array_equal(got[2], want[2])  # top-1 agreement is exact
 
 
-def test_forward_all_matches_oracle(gpu, orc, weights):
+@pytest.mark.parametrize("T", [40, 476])
+def test_forward_all_matches_oracle(gpu, orc, weights, T):
+    """Model.forward_all (gpt2t.mojo:448-459): every row's logits bit for
+    bit the oracle's (the prompt's exact GEMMs and attention, LN_f on every
+    row, the head as a T-token GEMM in tile_i16's / rows_i16's order), and
+    its last row equal to forward's."""
     torch, lm, ctx = gpu
     from llm_mojo_amd import gpt2, synth
 
-    ids = synth.prompt_ids(21, 40)
+    orc.set_threads(16)
+    ids = synth.prompt_ids(21, T)
     model = lm.GPT2(ctx, weights)
     ref = orc.GPT2(gpt2.params_list(weights))
-    out = torch.zeros((40, 50257), device="cuda")
-    note("forward_all")
+    out = torch.zeros((T, 50257), device="cuda")
+    note("forward_all", T)
     model.forward_all(ids, out)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     want = ref.forward_all(ids)
+    rows_equal = int(sum(bits_equal(got[t], want[t]) for t in range(T)))
     rel = np.abs(got - want).max(axis=1) / np.abs(want).max(axis=1)
-    note("row rel err max", rel.max(), "mean", rel.mean())
-    # one-step int16 code flips between float summation orders spread
-    # through 12 layers: the oracle's own two integer paths differ by
-    # ~1.5e-3 on one row; over 40 rows the largest reaches ~2.5e-3
-    assert rel.max() < 4e-3 and rel.mean() < 1e-3
-    assert np.mean(got.argmax(1) == want.argmax(1)) >= 0.95
+    note("forward_all", T, "rows bit-identical", rows_equal, "max rel err", rel.max())
+    assert rows_equal == T
+    # forward's head is the one-token dot_row_i16 (another float order than
+    # the T-token GEMM's, in the reference too)
     last = model.forward(ids, 0)
+    assert bits_equal(last, ref.forward(ids, 0))
     assert np.abs(last - got[-1]).max() / np.abs(got[-1]).max() < 1e-4
+    model.free()
 
 
 def test_eval_loop_windows(gpu, weights):

@@ -238,3 +238,51 @@ def test_linear_act_bit_exact(gpu, orc, fmt, IN, OUT):
     want = orc.matmul_rows_a16(x, o, b, orc.EPI_BIAS | (orc.EPI_GELU if bits == 4 else 0))
     same_bits(out1.cpu().numpy(), want)
     g.free()
+
+
+DOT_ROW_CASES = [  # (bits, group, sym, IN, OUT, reduce_rows): every dot_row_i16 branch
+    (4, 32, False, 768, 2304, True), (4, 32, True, 3072, 768, True),  # BLOCKED
+    (8, 0, False, 768, 50257, False), (8, 0, False, 3072, 64, True),  # int8 per channel
+    (4, 64, False, 768, 70, True), (4, 128, True, 3072, 40, True), (4, 0, False, 768, 33, True),  # general loop
+    (8, 32, False, 768, 64, True), (8, 128, True, 1024, 17, True),
+]
+
+
+@pytest.mark.parametrize("bits,group,sym,IN,OUT,rr", DOT_ROW_CASES)
+@pytest.mark.parametrize("big", [False, True])
+def test_dot_row_i16_bit_exact(gpu, orc, bits, group, sym, IN, OUT, rr, big):
+    """llmq_dot_row_i16 against the oracle's QuantMatrix.dot_row_i16 row by
+    row (BLOCKED rows fed permute_x_i16's activations and lane sums), for
+    normal codes and for +-32767 codes (the int32 sums' extremes)."""
+    torch, lm, ctx = gpu
+    rng = np.random.default_rng(bits * 1000 + group + IN + OUT + big)
+    shape = (IN, OUT) if rr else (OUT, IN)
+    w = rng.normal(0, 0.02, shape).astype(np.float32)
+    xq = (rng.choice([-32767, 32767], IN) if big else rng.integers(-32767, 32768, IN)).astype(np.int16)
+    note("dot_row_i16", bits, group, sym, IN, OUT, "big" if big else "")
+    g = lm.HipQuantMatrix.from_f32(ctx, w, bits, group, sym, True, reduce_rows=rr)
+    o = orc.QuantMatrix.from_f32(w, bits, group, sym, True, reduce_rows=rr)
+    out = torch.full((OUT,), float("nan"), dtype=torch.float32, device="cuda")
+    g.dot_row_i16(0, dev(torch, xq), out, nrows=OUT)
+    one = torch.zeros(1, dtype=torch.float32, device="cuda")
+    g.dot_row_i16(OUT - 1, dev(torch, xq), one)  # a single row, the last
+    torch.cuda.synchronize()
+    ok, x1, xs = o.permute_x_i16(xq)
+    if not ok:
+        x1 = xq
+    want = np.array([o.dot_row_i16(r, x1, xs) for r in range(OUT)], np.float32)
+    same_bits(out.cpu().numpy(), want)
+    same_bits(one.cpu().numpy(), want[-1:])
+    with pytest.raises(lm.LlmqError, match="beyond"):
+        g.dot_row_i16(OUT - 1, dev(torch, xq), out, nrows=2)
+    g.free()
+
+
+def test_dot_row_i16_needs_int16_format(gpu):
+    torch, lm, ctx = gpu
+    w = np.zeros((64, 16), np.float32)
+    g = lm.HipQuantMatrix.from_f32(ctx, w, 4, 32, False, False)
+    out = torch.zeros(16, dtype=torch.float32, device="cuda")
+    with pytest.raises(lm.LlmqError, match="int16 path"):
+        g.dot_row_i16(0, torch.zeros(64, dtype=torch.int16, device="cuda"), out)
+    g.free()

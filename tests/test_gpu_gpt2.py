@@ -15,13 +15,12 @@ oracle's tokens.
 import numpy as np
 import pytest
 
+from tests.gpt2_exact import bits_equal, check_decode_exact
+
 pytestmark = pytest.mark.gpu
 
 STEPS = 100  # generated tokens per prompt (99 decode forwards)
 PROMPTS = 10
-SLOTS, SLOT = 49, 3072  # llmq_gpt2_debug_codes / orc set_capture layout
-IN_OF_SLOT = [768, 768, 768, 3072] * 12 + [768]
-NAMES = ["qkv", "proj", "fc", "fcproj"]
 
 
 @pytest.fixture(scope="module")
@@ -45,11 +44,6 @@ def models(gpu, orc, weights):
     model.free()
 
 
-def bits_equal(a, b):
-    return np.array_equal(np.ascontiguousarray(a, np.float32).view(np.uint32),
-                          np.ascontiguousarray(b, np.float32).view(np.uint32))
-
-
 @pytest.mark.parametrize("seed", range(PROMPTS))
 def test_gpt2_decode_matches_oracle_exactly(gpu, orc, models, seed):
     torch, lm, ctx = gpu
@@ -57,50 +51,7 @@ def test_gpt2_decode_matches_oracle_exactly(gpu, orc, models, seed):
 
     model, ref = models
     prompt = [int(v) for v in synth.prompt_ids(1000 + seed, 12)]
-    codes_g = torch.zeros(SLOTS * SLOT, dtype=torch.int16, device="cuda")
-    codes_o = np.zeros(SLOTS * SLOT, np.int16)
-    model.debug_codes(codes_g)
-    ref.set_capture(codes_o)
-    flips = np.zeros(SLOTS, np.int64)
-    counted = np.zeros(SLOTS, np.int64)
-    exact = agree = 0
-    worst = 0.0
-    print(f"prompt {seed}: prefill", flush=True)
-    lg, lo = model.forward(prompt, 0), ref.forward(prompt, 0)
-    steps = [(lg, lo)]
-    toks = []
-    pos = len(prompt)
-    for i in range(STEPS - 1):
-        nxt = orc.argmax(lo)
-        toks.append(nxt)
-        lg, lo = model.forward([nxt], pos), ref.forward([nxt], pos)
-        pos += 1
-        torch.cuda.synchronize()
-        g = codes_g.cpu().numpy().reshape(SLOTS, SLOT)
-        o = codes_o.reshape(SLOTS, SLOT)
-        for s in range(SLOTS):
-            k = IN_OF_SLOT[s]
-            flips[s] += int(np.count_nonzero(g[s, :k] != o[s, :k]))
-            counted[s] += k
-        steps.append((lg, lo))
-    toks.append(orc.argmax(lo))
-    for lg, lo in steps:
-        exact += int(bits_equal(lg, lo))
-        agree += int(int(np.argmax(lg)) == orc.argmax(lo))
-        worst = max(worst, float(np.max(np.abs(lg - lo)) / np.max(np.abs(lo))))
-    model.debug_codes(None)
-    ref.set_capture(None)
-    per_layer = [int(flips[4 * l:4 * l + 4].sum()) for l in range(12)] + [int(flips[48])]
-    print(f"prompt {seed}: {len(steps)} steps, logits bit-identical {exact}, top-1 agree {agree}, "
-          f"max rel err {worst:.1e}; int16 code flips {int(flips.sum())} of {int(counted.sum())} "
-          f"(per layer {per_layer[:12]}, head {per_layer[12]})", flush=True)
-    # the device-driven loop (argmax on the GPU, graph per token)
-    gen, _, _ = model.generate(prompt, STEPS)
-    want = toks[:next((i for i, t in enumerate(toks) if t == 50256), len(toks))]
-    assert int(flips.sum()) == 0, dict(zip([f"{NAMES[s % 4]}{s // 4}" if s < 48 else "head" for s in range(SLOTS)],
-                                          flips.tolist()))
-    assert exact == len(steps) and agree == len(steps)
-    assert gen.tolist() == want
+    check_decode_exact(torch, orc, model, ref, prompt, STEPS, f"prompt {seed}")
 
 
 def test_gpt2_fused_qkv_attention(gpu, orc, weights, monkeypatch):
@@ -138,3 +89,35 @@ def test_gpt2_fused_qkv_attention(gpu, orc, weights, monkeypatch):
     assert next((i for i in range(n) if tf[i] != tu[i]), n) >= n - 2, (tf.tolist(), tu.tolist())
     mf.free()
     mu.free()
+
+
+def test_gpt2_int4_same_head_exact(gpu, orc, weights):
+    """--dtype int4-g32-a16 --head same (run[W, W], gpt2t.mojo:1289-1290):
+    the head is a BLOCKED int4-g32 matrix, whose exact GEMV leaves the argmax
+    partials the device-driven loop picks from.  Teacher-forced logits are
+    bit-identical to the oracle's with the same head, and the device's
+    greedy tokens are the oracle's."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import gpt2, synth
+
+    print("gpt2 int4 head: load", flush=True)
+    model = lm.GPT2(ctx, weights, dtype="int4-g32-a16", head="same")
+    assert model.name() == "int4-g32-a16+kv-int8"
+    ref = orc.GPT2(gpt2.params_list(weights), head=(4, 32, False, True))
+    prompt = [int(v) for v in synth.prompt_ids(2024, 12)]
+    lg, lo = model.forward(prompt, 0), ref.forward(prompt, 0)
+    exact = [bits_equal(lg, lo)]
+    toks, pos = [], len(prompt)
+    for i in range(39):
+        nxt = orc.argmax(lo)
+        toks.append(nxt)
+        lg, lo = model.forward([nxt], pos), ref.forward([nxt], pos)
+        pos += 1
+        exact.append(bits_equal(lg, lo))
+    toks.append(orc.argmax(lo))
+    print(f"gpt2 int4 head: {sum(exact)} / {len(exact)} steps bit-identical", flush=True)
+    assert all(exact)
+    gen, _, _ = model.generate(prompt, 40)
+    want = toks[:next((i for i, t in enumerate(toks) if t == 50256), len(toks))]
+    assert gen.tolist() == want
+    model.free()

@@ -6,11 +6,13 @@ perform in the reference's order, so codes, scales and outputs must match
 the oracle bit for bit.  Cases: tests/int_attention_check.mojo's context
 lengths and token counts, a 476-token prompt, the last positions of the
 cache, head_dim 128, and a cache too long to stage in LDS.  The GPT-2 model
-with --attention int is checked like the float-attention model (top-1 per
-teacher-forced decode step, logit error, device-driven generate).
+with --attention int is held to the float-attention model's exact bar
+(bit-identical logits, no int16 code flips, the device's greedy tokens).
 """
 import numpy as np
 import pytest
+
+from tests.gpt2_exact import check_decode_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -76,8 +78,7 @@ def test_ikv_shape_checks(gpu):
         lm.QuantKV8.export(kv)
 
 
-STEPS = 12
-LOGIT_REL = 2e-3
+PROMPTS = 10
 
 
 @pytest.fixture(scope="module")
@@ -87,47 +88,41 @@ def weights():
     return synth.gpt2_tensors(seed=1337)
 
 
-def test_gpt2_int_attention_decode(gpu, orc, weights):
-    """GPT-2 int4-g32-a16 with --attention int: prompt and teacher-forced
-    decode steps (the decode steps take the fused store path) against the
-    oracle model with IntAttnKV."""
+@pytest.fixture(scope="module")
+def models(gpu, orc, weights):
     torch, lm, ctx = gpu
-    from llm_mojo_amd import gpt2, synth
+    from llm_mojo_amd import gpt2
 
-    prompt = synth.prompt_ids(1337, 40)
+    orc.set_threads(16)
+    note("gpt2 int attention: load")
     model = lm.GPT2(ctx, weights, attention="int")
     assert model.name().endswith("+kv-int8-intattn")
     ref = orc.GPT2(gpt2.params_list(weights), attention="int")
-    note("gpt2 int attention prefill")
-    lg = model.forward(prompt, 0)
-    lo = ref.forward(prompt, 0)
-    errs = [np.max(np.abs(lg - lo)) / np.max(np.abs(lo))]
-    agree = [int(np.argmax(lg) == orc.argmax(lo))]
-    pos = len(prompt)
-    for i in range(STEPS):
-        nxt = orc.argmax(lo)
-        note("gpt2 int attention decode step", i)
-        lg = model.forward([nxt], pos)
-        lo = ref.forward([nxt], pos)
-        pos += 1
-        errs.append(np.max(np.abs(lg - lo)) / np.max(np.abs(lo)))
-        agree.append(int(np.argmax(lg) == orc.argmax(lo)))
-    note("max logit rel err", max(errs), "top-1 agreement", sum(agree), "/", len(agree))
-    assert max(errs) < LOGIT_REL
-    assert sum(agree) >= len(agree) - 1
+    yield model, ref
+    model.free()
 
 
-def test_gpt2_int_attention_generate(gpu, orc, weights):
+@pytest.mark.parametrize("seed", range(PROMPTS))
+def test_gpt2_int_attention_exact(gpu, orc, models, seed):
+    """GPT-2 int4-g32-a16 with --attention int (run_with[..., IntAttnKV],
+    gpt2t.mojo:1251-1257; int_attention.mojo:170-269) held to config 0's
+    bar: 12-token prompt, 100 greedy tokens, logits bit-identical at every
+    step, zero int16 code flips, device greedy tokens equal."""
     torch, lm, ctx = gpu
-    from llm_mojo_amd import gpt2, synth
+    from llm_mojo_amd import synth
 
-    prompt = synth.prompt_ids(7, 12)
-    model = lm.GPT2(ctx, weights, attention="int")
-    ref = orc.GPT2(gpt2.params_list(weights), attention="int")
-    note("gpt2 int attention generate")
-    toks, pre_ms, dec_ms = model.generate(prompt, STEPS)
-    want = ref.generate(prompt, STEPS)
-    note("tokens", toks.tolist(), "oracle", want.tolist())
-    n = min(len(toks), len(want))
-    first_diff = next((i for i in range(n) if toks[i] != want[i]), n)
-    assert first_diff >= n - 2, (toks.tolist(), want.tolist())
+    model, ref = models
+    prompt = [int(v) for v in synth.prompt_ids(1000 + seed, 12)]
+    check_decode_exact(torch, orc, model, ref, prompt, 100, f"int attention prompt {seed}")
+
+
+def test_gpt2_int_attention_long_prompt_exact(gpu, orc, models):
+    """The same bar after a 476-token prompt (the README's long-context
+    decode), 24 generated tokens: prompt attention and decode attention over
+    two 256-position segments."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    model, ref = models
+    prompt = [int(v) for v in synth.prompt_ids(1337, 476)]
+    check_decode_exact(torch, orc, model, ref, prompt, 24, "int attention 476-token prompt")

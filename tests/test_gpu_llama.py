@@ -153,11 +153,13 @@ def test_llama_long_context_decode(gpu):
     m.free()
 
 
-def greedy_vs_numpy(toks, ref, seq, prompt, pos0):
-    """Compare greedy tokens with NumPy greedy decoding from `prompt`; a step
-    whose NumPy top-2 margin is under 1e-3 of max |logit| ends the comparison.
-    Returns the number of tokens compared."""
-    logits = ref.forward(seq, prompt, pos0)
+def greedy_vs_numpy(toks, ref, seq, prompt, pos0, logits=None):
+    """Compare greedy tokens with NumPy greedy decoding from `prompt` (whose
+    logits, if given, ref has already computed); a step whose NumPy top-2
+    margin is under 1e-3 of max |logit| ends the comparison.  Returns the
+    number of tokens compared."""
+    if logits is None:
+        logits = ref.forward(seq, prompt, pos0)
     for i in range(len(toks)):
         top = np.sort(logits)[-2:]
         want = int(np.argmax(logits))
@@ -168,70 +170,100 @@ def greedy_vs_numpy(toks, ref, seq, prompt, pos0):
     return len(toks)
 
 
-def test_llama_full_width_layers_match_numpy(gpu):
+PROMPT_1024 = 1024  # a 1024-token prompt, then greedy tokens
+
+
+def top1_ok(got, want):
+    """Same top-1, unless the NumPy top-2 margin is within the logit bar
+    (then either pick is within tolerance)."""
+    top = np.sort(want)[-2:]
+    if top[1] - top[0] < 2e-3 * np.max(np.abs(want)):
+        return True
+    return int(np.argmax(got)) == int(np.argmax(want))
+
+
+@pytest.mark.timeout(300)
+def test_llama_full_width_prompt_1024(gpu):
     """Two layers at the TinyLlama width (d 2048, 32 query / 4 key-value
-    heads, FFN 5632, Q4_K) under its 32000 x 2048 Q6_K int16 head: a
-    40-token prompt, then 4 positions more on the same cache, logits within
-    1e-3 of max |logit| and the same top-1."""
+    heads, FFN 5632, Q4_K) under its 32000 x 2048 Q6_K int16 head, at config
+    4's own context: a 1024-token prompt in one call (the LDS-staged Q4_K
+    matmul for 64+ tokens at the 2560 / 2048 / 11264 / 5632-input widths, the
+    grouped prompt attention over 1024 positions), then 8 decode positions
+    on the same cache (attention over 4-5 splits of 256 positions): logits
+    within 1e-3 of max |logit| and the same top-1 at each of the 9."""
     torch, lm, ctx = gpu
     from llm_mojo_amd import synth
     from llm_mojo_amd.llama import TINYLLAMA
 
-    cfg = dict(TINYLLAMA, n_layer=2, max_t=64)
+    cfg = dict(TINYLLAMA, n_layer=2, max_t=1152)
     tensors = synth.llama_tensors(cfg, 9)
-    toks = synth.llama_prompts(9, 1, 44, cfg["vocab"])[0]
-    print("llama full width: load", flush=True)
+    toks = synth.llama_prompts(9, 1, PROMPT_1024 + 8, cfg["vocab"])[0]
+    print("llama full width, 1024-token prompt: load", flush=True)
     m = lm.Llama(ctx, cfg, tensors)
     ref = NumpyLlama(cfg, tensors)
-    for lo, hi in ((0, 40), (40, 41), (41, 44)):
-        print(f"llama full width: tokens {lo}..{hi}", flush=True)
+    spans = [(0, PROMPT_1024)] + [(PROMPT_1024 + i, PROMPT_1024 + i + 1) for i in range(8)]
+    errs = []
+    for lo, hi in spans:
         got = m.forward(0, toks[lo:hi], lo)
         want = ref.forward(0, toks[lo:hi], lo)
-        assert rel(got, want) < 1e-3, (lo, rel(got, want))
-        assert int(np.argmax(got)) == int(np.argmax(want))
+        errs.append(rel(got, want))
+        print(f"llama full width: tokens {lo}..{hi} rel err {errs[-1]:.2e}", flush=True)
+        assert errs[-1] < 1e-3, (lo, errs[-1])
+        assert top1_ok(got, want), (lo, int(np.argmax(got)), int(np.argmax(want)))
     m.free()
 
 
-@pytest.mark.timeout(400)
-def test_llama_full_depth_greedy_matches_numpy(gpu):
-    """All 22 layers of the TinyLlama shape: a 16-token prompt and 4 greedy
-    tokens from the device loop against NumPy greedy decoding (the margin
-    rule above)."""
+@pytest.mark.timeout(600)
+def test_llama_full_depth_prompt_1024_greedy(gpu):
+    """All 22 layers of the TinyLlama shape at config 4's context: the
+    1024-token prompt's logits within 1e-3 of NumPy's, then 16 greedy tokens
+    from the device loop against NumPy greedy decoding (the margin rule
+    above), at least 8 of them compared."""
     torch, lm, ctx = gpu
     from llm_mojo_amd import synth
     from llm_mojo_amd.llama import TINYLLAMA
 
-    cfg = dict(TINYLLAMA, max_t=64)
+    cfg = dict(TINYLLAMA, max_t=1152)
     tensors = synth.llama_tensors(cfg, 11)
-    prompt = synth.llama_prompts(11, 1, 16, cfg["vocab"])
-    print("llama full depth: generate", flush=True)
+    prompt = synth.llama_prompts(11, 1, PROMPT_1024, cfg["vocab"])
+    print("llama full depth: load", flush=True)
     m = lm.Llama(ctx, cfg, tensors)
-    toks, _, _ = m.generate(prompt, 4)
+    print("llama full depth: prompt", flush=True)
+    got = m.forward(0, prompt[0], 0)
+    toks, _, _ = m.generate(prompt, 16)
     m.free()
     print("llama full depth: numpy", flush=True)
     ref = NumpyLlama(cfg, tensors)
-    n = greedy_vs_numpy(toks[:, 0], ref, 0, prompt[0], 0)
+    want = ref.forward(0, prompt[0], 0)
+    print(f"llama full depth: prompt logits rel err {rel(got, want):.2e}", flush=True)
+    assert rel(got, want) < 1e-3 and top1_ok(got, want)
+    n = greedy_vs_numpy(toks[:, 0], ref, 0, prompt[0], 0, logits=want)
     print("llama full depth: tokens compared", n, flush=True)
-    assert n >= 2
+    assert n >= 8
 
 
-def test_llama_full_shape_batch16_equals_batch1(gpu):
-    """The full TinyLlama shape at batch 16: 16 different 24-token prompts,
-    12 greedy tokens each through the captured batch-16 step; each
-    sequence's tokens equal its own batch-1 run."""
+@pytest.mark.timeout(300)
+def test_llama_batch16_full_context_equals_batch1(gpu):
+    """Batch 16 at config 4's workload: 16 different 1024-token prompts, 128
+    greedy tokens each through the captured batch-16 step (the batched
+    Q4_K matmuls and grouped attention on the fp16 matrix cores, up to 1152
+    positions); each sequence's tokens equal its own batch-1 run (the "many
+    == one" pattern of tests/gguf_int_head.mojo:49-54)."""
     torch, lm, ctx = gpu
     from llm_mojo_amd import synth
     from llm_mojo_amd.llama import TINYLLAMA
 
-    cfg = dict(TINYLLAMA, batch=16, max_t=64)
+    cfg = dict(TINYLLAMA, batch=16, max_t=1152)
     tensors = synth.llama_tensors(cfg, 10)
-    prompts = synth.llama_prompts(10, 16, 24, cfg["vocab"])
-    print("llama batch 16: generate", flush=True)
+    prompts = synth.llama_prompts(10, 16, PROMPT_1024, cfg["vocab"])
+    print("llama batch 16, 1024-token prompts: load", flush=True)
     m = lm.Llama(ctx, cfg, tensors)
-    many, _, _ = m.generate(prompts, 12)
-    assert many.shape == (12, 16)
+    many, _, _ = m.generate(prompts, 128)
+    assert many.shape == (128, 16)
     for b in range(16):
-        one, _, _ = m.generate(prompts[b:b + 1], 12)
+        one, _, _ = m.generate(prompts[b:b + 1], 128)
         assert np.array_equal(one[:, 0], many[:, b]), (b, one[:, 0].tolist(), many[:, b].tolist())
-    print("llama batch 16: 16 sequences equal their batch-1 runs", flush=True)
+        print(f"llama batch 16: sequence {b} equals its batch-1 run", flush=True)
+    distinct = len({tuple(many[:, b]) for b in range(16)})
+    print(f"llama batch 16: {distinct} distinct token sequences", flush=True)
     m.free()

@@ -35,12 +35,44 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def read_floor(torch, lm, ctx, stream, nbytes, nbuf, grid=2048, reps=None):
+def graph_us(torch, ctx, stream, fn, n, replays=3):
+    """Device time per launch of fn(0) .. fn(n - 1): the n launches captured
+    once into a HIP graph and replayed, timed with HIP events on `stream`, so
+    the host's enqueue rate (a ctypes call per launch from Python) cannot set
+    the rate of short kernels.  fn must issue its work on ctx's stream."""
+    with torch.cuda.stream(stream):
+        ctx.set_stream(stream)
+        for i in range(n):  # first launches (lazy set-up) outside the capture
+            fn(i)
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+            for i in range(n):
+                fn(i)
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(replays):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        del g
+    return e0.elapsed_time(e1) * 1000.0 / (replays * n)
+
+
+def read_floor(torch, lm, ctx, stream, nbytes, nbuf, grid=2048, reps=None, graph=False):
     """Average duration of a pure read of nbytes (llmq_debug_read: 128-bit
-    loads, no arithmetic) over nbuf distinct buffers, on `stream`."""
+    loads, no arithmetic) over nbuf distinct buffers, on `stream`; with
+    graph, each launch's device time (graph_us), else HIP events over
+    back-to-back launches from the host."""
     bufs = [torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
     out = torch.zeros(grid, dtype=torch.int32, device="cuda")
     reps = reps or max(60, 4 * nbuf)
+    if graph:
+        us = graph_us(torch, ctx, stream, lambda i: lm.debug_read(ctx, bufs[i % nbuf], out, grid),
+                      max(nbuf, min(reps, 4 * nbuf)))
+        del bufs
+        return us
     for i in range(2 * nbuf):
         lm.debug_read(ctx, bufs[i % nbuf], out, grid)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -51,6 +83,41 @@ def read_floor(torch, lm, ctx, stream, nbytes, nbuf, grid=2048, reps=None):
     e1.synchronize()
     del bufs
     return e0.elapsed_time(e1) * 1000.0 / reps
+
+
+READ_SWEEP_MB = [4, 8, 16, 26.82368, 64, 128, 256, 512, 1024]
+READ_GRIDS = [256, 1024, 2048, 4096]
+
+
+def read_sweep(torch, lm, ctx, rot_bytes=1 << 30):
+    """What one launch of a pure read of n bytes takes from HBM on this box,
+    n from 4 MB to 1 GiB (26.82 MB: the roofline GEMV's bytes), each over
+    distinct buffers totalling >= 1 GiB (beyond the 256 MB Infinity Cache),
+    best of four grid sizes, device time per launch (graph replay); and
+    hipMemcpyAsync device-to-device of the same 26.82 MB (read + write)."""
+    stream = torch.cuda.Stream()
+    res = {}
+    for mb in READ_SWEEP_MB:
+        nbytes = int(mb * 1e6) // 16 * 16
+        nbuf = max(2, -(-rot_bytes // nbytes))
+        best = None
+        for grid in READ_GRIDS:
+            us = read_floor(torch, lm, ctx, stream, nbytes, nbuf, grid=grid, graph=True)
+            if best is None or us < best[0]:
+                best = (us, grid)
+        res[f"{mb:g}MB"] = {"bytes": nbytes, "us": round(best[0], 3), "gbs": round(nbytes / best[0] / 1e3, 1),
+                            "frac": round(nbytes / best[0] / 1e3 / HBM_PEAK_GBS, 4), "grid": best[1]}
+        log("read sweep", mb, res[f"{mb:g}MB"])
+    nbytes = int(26.82368e6) // 16 * 16
+    nbuf = max(2, -(-rot_bytes // nbytes))
+    src = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
+    dst = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
+    us = graph_us(torch, ctx, stream, lambda i: dst[i % nbuf].copy_(src[i % nbuf]), 2 * nbuf)
+    res["memcpy_d2d_26.82MB"] = {"bytes_read": nbytes, "us": round(us, 3),
+                                 "read_plus_write_gbs": round(2 * nbytes / us / 1e3, 1)}
+    del src, dst
+    ctx.set_stream(None)
+    return res
 
 
 def gemv_roofline(torch, lm, ctx, K=4096, N=11008, nbuf=36, reps=360):
@@ -106,13 +173,15 @@ def gemv_roofline(torch, lm, ctx, K=4096, N=11008, nbuf=36, reps=360):
 def measured_traffic():
     """HBM bytes per launch of the roofline GEMV from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/), scaled by what the
-    same counters read for a 1 GiB copy; None if absent."""
+    same counters read for a 1 GiB copy, and the kernel trace's average
+    duration of the same command; (None, None) if absent."""
     p = os.path.join(HERE, "profiles", "gemv_a16_int4_g32_4096x11008.traffic.json")
     try:
         with open(p) as f:
-            return json.load(f)["traffic_bytes_per_launch"]
+            d = json.load(f)
+        return d["traffic_bytes_per_launch"], d.get("kernel_trace_avg_us")
     except (OSError, KeyError, ValueError):
-        return None
+        return None, None
 
 
 def copy_bandwidth(torch, nbytes=1 << 30, reps=20):
@@ -139,9 +208,12 @@ def gemv_micro(torch, lm, ctx, reps=200, rot_bytes=320 << 20):
     groups 32 / 64 / 128, and the int8 per-channel head (768 x 50257), two
     ways: one matrix launched back to back (it stays in the 256 MB Infinity
     Cache, as in decode: `llc`), and over distinct copies totalling > 320 MiB
-    (`hbm`, more than the 256 MB cache).  GB/s of nbytes + 2K + 4N per launch; each is set beside a pure
-    read of the same bytes the same way (`*_floor_us`: the memory system's
-    time for those bytes in one launch, LLC-resident or rotated)."""
+    (`hbm`, more than the 256 MB cache).  GB/s of nbytes + 2K + 4N per
+    launch; each is set beside a pure read of the same bytes the same way
+    (`*_floor_us`: the memory system's time for those bytes in one launch,
+    LLC-resident or rotated).  Every time is device time per launch from a
+    replayed HIP graph of the launches (graph_us): launched from Python one
+    by one, these 3-10 us kernels would be timed at the host's enqueue rate."""
     stream = torch.cuda.Stream()
     res = {}
     with torch.cuda.stream(stream):
@@ -152,15 +224,7 @@ def gemv_micro(torch, lm, ctx, reps=200, rot_bytes=320 << 20):
         cases.insert(0, ("warm-up", 768, 2304, 4, 32))  # first launches of the process, not reported
 
         def timed(fn, n):
-            for i in range(max(10, 2 * n)):
-                fn(i)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for i in range(reps):
-                fn(i)
-            e1.record(stream)
-            e1.synchronize()
-            return e0.elapsed_time(e1) * 1000.0 / reps
+            return graph_us(torch, ctx, stream, fn, max(n, 64))
 
         for name, K, N, bits, group in cases:
             src = torch.randn((K, N), device="cuda", generator=g) * 0.02
@@ -178,8 +242,8 @@ def gemv_micro(torch, lm, ctx, reps=200, rot_bytes=320 << 20):
             us_hbm = timed(lambda i: lm.linear(ctx, out, x, ws[i % nrot]), nrot)
             for m in ws:
                 m.free()
-            llc_floor = read_floor(torch, lm, ctx, stream, nb, 1, grid=256, reps=reps)
-            hbm_floor = read_floor(torch, lm, ctx, stream, nb, nrot, grid=256, reps=reps)
+            llc_floor = read_floor(torch, lm, ctx, stream, nb, 1, grid=256, reps=64, graph=True)
+            hbm_floor = read_floor(torch, lm, ctx, stream, nb, nrot, grid=256, reps=nrot, graph=True)
             res[name] = {"llc_us": round(us, 2), "llc_gbs": round(alg / us / 1e3, 1),
                          "llc_floor_us": round(llc_floor, 2),
                          "hbm_us": round(us_hbm, 2), "hbm_gbs": round(alg / us_hbm / 1e3, 1),
@@ -448,6 +512,9 @@ def main():
     ap.add_argument("--no-gguf-sweep", action="store_true", help="skip the GGUF GEMV sweep (config 2)")
     ap.add_argument("--no-intattn", action="store_true", help="skip the integer-attention decode comparison")
     ap.add_argument("--no-formats", action="store_true", help="skip the decode table of the other formats")
+    ap.add_argument("--no-read-sweep", action="store_true", help="skip the pure-read size sweep")
+    ap.add_argument("--micro-only", action="store_true",
+                    help="only config 1's GEMVs and the read sweep (for rocprofv3 runs)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline GEMV and the reference copy (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -467,6 +534,13 @@ def main():
         ctx = lm.Context(0)
         r = gemv_roofline(torch, lm, ctx)
         print(json.dumps({"roofline_kernel": r, "copy_gbs": round(copy_bandwidth(torch), 1)}), flush=True)
+        return
+    if args.micro_only:
+        ctx = lm.Context(0)
+        out = {"gemv_micro_llc": gemv_micro(torch, lm, ctx)}
+        if not args.no_read_sweep:
+            out["read_sweep"] = read_sweep(torch, lm, ctx)
+        print(json.dumps(out), flush=True)
         return
     log("generating synthetic GPT-2 weights")
     tensors = synth.gpt2_tensors(SEED)
@@ -495,8 +569,15 @@ def main():
     extra = {}
     if not args.no_roofline:
         r = gemv_roofline(torch, lm, ctx)
+        traffic, trace_us = measured_traffic()
         roof = {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic()}
+                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "timing": "HIP events over 360 back-to-back launches on the kernel's stream (36 rotated weight "
+                          "buffers, 965 MB); a launch's dispatch overlaps the previous one's tail, so this sits "
+                          "below a single dispatch's start-to-end time in a kernel trace"}
+        if trace_us:
+            roof["trace_avg_us"] = trace_us
+            roof["trace_frac"] = round(r["alg_bytes"] / trace_us / 1e3 / HBM_PEAK_GBS, 4)
         r["traffic_source"] = ("profiles/gemv_a16_int4_g32_4096x11008.traffic.json: rocprofv3 --pmc FETCH_SIZE "
                                "and WRITE_SIZE of this kernel, scaled by the same counters on a copy of known size")
         extra["roofline_kernel"] = r
@@ -508,6 +589,9 @@ def main():
     extra["decode_bytes_per_token"] = int(token_bytes)
     extra["decode_gbs_effective"] = round(token_bytes * tok_s / 1e9, 1)
 
+    if not args.no_read_sweep:
+        log("read sweep")
+        extra["read_sweep"] = read_sweep(torch, lm, ctx)
     log("gemv micro")
     extra["gemv_micro_llc"] = gemv_micro(torch, lm, ctx)
     if not args.no_intattn:

@@ -158,6 +158,55 @@ int llmq_capture(hipStream_t s, F &&enqueue, hipGraph_t *def, hipGraphExec_t *ex
 }
 
 // Argmax partial of one workgroup: the largest value and its (smallest) index.
+// Code of column k of row `row` in the QuantMatrix row-tile layout (16-byte
+// chunks of 32 int4 codes, weight e at dword e >> 3, nibble e & 7; or of 16
+// int8 codes, byte e).  Scalar: for the few rows the reference leaves out of
+// its tiles and for parity entry points.
+__device__ __forceinline__ int llmq_tile_code(const uint8_t *codes, int bits, int64_t CK, int64_t row, int64_t k) {
+    const int64_t tile = row >> 4, r = row & 15;
+    if (bits == 4) {
+        const int64_t c = k >> 5, e = k & 31;
+        const uint8_t b = codes[((tile * CK + c) * 16 + r) * 16 + 4 * (e >> 3) + ((e & 7) >> 1)];
+        return (e & 1) ? b >> 4 : b & 15;
+    }
+    const int64_t c = k >> 4;
+    return codes[((tile * CK + c) * 16 + r) * 16 + (k & 15)];
+}
+
+// Reference SIMD lane L (0..15) of dot1_i16 (kernels.mojo:617-629), which is
+// also QuantMatrix.dot_row_i16's general loop (tensor.mojo:567-577): per
+// group an int32 sum (wrapping, as VPDPWSSD) of the lane's pairs
+// (2L, 2L + 1) of each 32-input piece of xq * (u - zp), then
+// accf = fma(f32(sum), scale, accf) in group order.
+__device__ inline float llmq_dot1_lane(const uint8_t *codes, const uint16_t *scales, const uint8_t *zps, int bits,
+                                       int64_t K, int64_t G, int64_t CK, int64_t NG, int64_t row, const int16_t *xq,
+                                       int L) {
+    const int64_t tile = row >> 4, r = row & 15;
+    float accf = 0.0f;
+    for (int64_t g = 0; g < K / G; g++) {
+        const int64_t gi = (tile * NG + g) * 16 + r;
+        const int zp = zps[gi];
+        uint32_t acc = 0;
+        for (int64_t k0 = g * G; k0 < (g + 1) * G; k0 += 32) {
+            const int64_t k = k0 + 2 * L;
+            acc += (uint32_t)(xq[k] * (llmq_tile_code(codes, bits, CK, row, k) - zp));
+            acc += (uint32_t)(xq[k + 1] * (llmq_tile_code(codes, bits, CK, row, k + 1) - zp));
+        }
+        accf = fmaf((float)(int)acc, __half2float(__ushort_as_half(scales[gi])), accf);
+    }
+    return accf;
+}
+
+// SIMD reduce_add over 16 consecutive lanes as the reference's halving tree:
+// (L, L + 8), then + 4, + 2, + 1; every lane of the 16 gets the sum.
+__device__ __forceinline__ float llmq_reduce16(float v) {
+    v += __shfl_xor(v, 8, 16);
+    v += __shfl_xor(v, 4, 16);
+    v += __shfl_xor(v, 2, 16);
+    v += __shfl_xor(v, 1, 16);
+    return v;
+}
+
 struct ArgmaxPart {
     float v;
     int idx;

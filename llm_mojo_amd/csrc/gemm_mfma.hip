@@ -434,6 +434,28 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(MfArgs a) {
     }
 }
 
+// rows_i16 (kernels.mojo:576-614): the last n % 32 output rows, which the
+// reference leaves out of its 32-row tiles (matmul_rows_a16, 468-476) and
+// dots one at a time: per (row, token) 16 lanes in dot1_i16's order, the
+// 16-lane halving sum, times sx, plus bias, then finish (GELU, residual).
+// Four (row, token) items a wave; item i is row o0 + i % nrows, token
+// i / nrows.
+__global__ __launch_bounds__(64) void rows_i16_kernel(MfArgs a, int bits, int o0, int nrows) {
+    const int L = threadIdx.x & 15;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 4);
+    const bool live = item < (int64_t)nrows * a.T;
+    const int o = o0 + (live ? (int)(item % nrows) : 0), tok = live ? (int)(item / nrows) : 0;
+    float d = llmq_dot1_lane(a.codes, a.scales, a.zps, bits, a.K, a.G, a.CK, a.NG, o, a.xq + (int64_t)tok * a.K, L);
+    d = llmq_reduce16(d);
+    if (!live || L != 0) return;
+    float v = d * a.sx[tok];
+    if (a.flags & LLMQ_BIAS) v += a.bias[o];
+    if (a.flags & LLMQ_GELU) v = gelu_ref(v);
+    float *dst = a.out + (int64_t)tok * a.ldo + o;
+    if (a.flags & LLMQ_RESID) v += *dst;
+    *dst = v;
+}
+
 }  // namespace
 
 bool gemm_mfma_supports(const llmq_mat *w, int64_t T) {
@@ -478,7 +500,10 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     a.zps_bytes = (uint32_t)((w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * LLMQ_TILE_ROWS);
     a.T = (int)T;
     a.K = (int)K;
-    a.n = (int)w->n;
+    // the 32-row tiles; the rest (n % 32 rows: the vocabulary's last 17)
+    // go through rows_i16 below
+    const int full = (int)(w->n / 32 * 32);
+    a.n = full;
     a.ntiles = (int)w->ntiles;
     a.CK = (int)w->CK;
     a.NG = (int)w->NG;
@@ -490,7 +515,7 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     // workgroups); LLMQ_MFMA_MT overrides, for measurement
     int mt = w->n >= 2048 ? 2 : 1;
     if (const char *e = getenv("LLMQ_MFMA_MT")) mt = atoi(e) == 1 ? 1 : atoi(e) == 4 ? 4 : 2;
-    dim3 grid((unsigned)((w->n + TN - 1) / TN), (unsigned)((T + 16 * mt - 1) / (16 * mt)));
+    dim3 grid((unsigned)((full + TN - 1) / TN), (unsigned)((T + 16 * mt - 1) / (16 * mt)));
     const bool seg32 = a.seg == 32;
 #define GK(B, S, M) hipLaunchKernelGGL((gemm_i8_kernel<B, S, M>), grid, dim3(256), 0, ctx->stream, a)
 #define GKM(B, S)                        \
@@ -499,13 +524,21 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
         else if (mt == 2) GK(B, S, 2);   \
         else GK(B, S, 4);                \
     } while (0)
-    if (w->bits == 4) {
-        if (seg32) GKM(4, true); else GKM(4, false);
-    } else {
-        if (seg32) GKM(8, true); else GKM(8, false);
+    if (full > 0) {
+        if (w->bits == 4) {
+            if (seg32) GKM(4, true); else GKM(4, false);
+        } else {
+            if (seg32) GKM(8, true); else GKM(8, false);
+        }
     }
 #undef GKM
 #undef GK
     LLMQ_HIP(hipGetLastError());
+    if (w->n > full) {
+        const int nt = (int)(w->n - full);
+        hipLaunchKernelGGL(rows_i16_kernel, dim3((unsigned)(((int64_t)nt * T + 3) / 4)), dim3(64), 0, ctx->stream, a,
+                           w->bits, full, nt);
+        LLMQ_HIP(hipGetLastError());
+    }
     return LLMQ_OK;
 }

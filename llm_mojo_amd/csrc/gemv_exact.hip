@@ -1007,20 +1007,6 @@ int launch_linear_act(llmq_ctx *ctx, float *out, const void *rec, const llmq_mat
 
 namespace {
 
-// Code of column k of row `row` in the row-tile layout (16-byte chunks of
-// 32 int4 codes, weight e at dword e >> 3, nibble e & 7; or of 16 int8
-// codes, byte e).
-__device__ __forceinline__ int tile_code(const uint8_t *codes, int bits, int64_t CK, int64_t row, int64_t k) {
-    const int64_t tile = row >> 4, r = row & 15;
-    if (bits == 4) {
-        const int64_t c = k >> 5, e = k & 31;
-        const uint8_t b = codes[((tile * CK + c) * 16 + r) * 16 + 4 * (e >> 3) + ((e & 7) >> 1)];
-        return (e & 1) ? b >> 4 : b & 15;
-    }
-    const int64_t c = k >> 4;
-    return codes[((tile * CK + c) * 16 + r) * 16 + (k & 15)];
-}
-
 // QuantMatrix.dot_row_i16 (tensor.mojo:518-577): four rows a wave, lane
 // L = tid & 15 of a row's 16 standing for the reference's SIMD lane L, with
 // its int32 sums (wrapping, as VPDPWSSD does), its float chain and the
@@ -1028,7 +1014,8 @@ __device__ __forceinline__ int tile_code(const uint8_t *codes, int bits, int64_t
 // xq holds the int16 codes in natural column order; the BLOCKED branch
 // gathers, for lane L, the activations permute_x_i16 would give it
 // (tensor.mojo:498-516: group L % 8, weights 16 (L / 8) .. + 15 of every
-// 256-block) and their float sum.
+// 256-block) and their float sum.  The int8 per-channel branch
+// (f32(acc).fma(s, 0)) is the general loop's single group.
 __global__ __launch_bounds__(64) void dot_row_i16_kernel(const uint8_t *__restrict__ codes,
                                                          const uint16_t *__restrict__ scales,
                                                          const uint8_t *__restrict__ zps, int bits, int blocked,
@@ -1039,11 +1026,9 @@ __global__ __launch_bounds__(64) void dot_row_i16_kernel(const uint8_t *__restri
     const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 4);
     const bool live = i < nrows;
     const int64_t row = row0 + (live ? i : 0);
-    const int64_t tile = row >> 4, r = row & 15;
-    auto scale_of = [&](int64_t g) { return __half2float(__ushort_as_half(scales[(tile * NG + g) * 16 + r])); };
-    auto zp_of = [&](int64_t g) { return (int)zps[(tile * NG + g) * 16 + r]; };
     float accf = 0.0f;
     if (blocked) {
+        const int64_t tile = row >> 4, r = row & 15;
         const int g = L & 7, h = L >> 3;
         for (int64_t blk = 0; blk < K / 256; blk++) {
             uint32_t acc = 0;
@@ -1051,33 +1036,17 @@ __global__ __launch_bounds__(64) void dot_row_i16_kernel(const uint8_t *__restri
             for (int e = 16 * h; e < 16 * h + 16; e++) {
                 const int64_t col = blk * 256 + 32 * g + e;
                 const int x = xq[col];
-                acc += (uint32_t)(x * tile_code(codes, 4, CK, row, col));
+                acc += (uint32_t)(x * llmq_tile_code(codes, 4, CK, row, col));
                 xs += (float)x;  // exact: at most 16 * 32767
             }
-            const int64_t gi = blk * 8 + g;
-            accf = fmaf((float)(int)acc - (float)zp_of(gi) * xs, scale_of(gi), accf);
+            const int64_t gi = (tile * NG + blk * 8 + g) * 16 + r;
+            const float sc = __half2float(__ushort_as_half(scales[gi]));
+            accf = fmaf((float)(int)acc - (float)zps[gi] * xs, sc, accf);
         }
     } else {
-        // lane L: pairs (2L, 2L + 1) of every 32-column piece, minus the
-        // zero point (codes_i16); one float step per group, or per row for
-        // int8 per channel (fma with 0 at the end)
-        const bool ch8 = bits == 8 && NG == 1;
-        for (int64_t g = 0; g < K / G; g++) {
-            const int zp = zp_of(g);
-            uint32_t acc = 0;
-            for (int64_t k0 = g * G; k0 < (g + 1) * G; k0 += 32) {
-                const int64_t k = k0 + 2 * L;
-                acc += (uint32_t)(xq[k] * (tile_code(codes, bits, CK, row, k) - zp));
-                acc += (uint32_t)(xq[k + 1] * (tile_code(codes, bits, CK, row, k + 1) - zp));
-            }
-            accf = ch8 ? fmaf((float)(int)acc, scale_of(g), 0.0f) : fmaf((float)(int)acc, scale_of(g), accf);
-        }
+        accf = llmq_dot1_lane(codes, scales, zps, bits, K, G, CK, NG, row, xq, L);
     }
-    // reduce_add: lanes (L, L + 8), then + 4, + 2, + 1
-    accf += __shfl_xor(accf, 8, 16);
-    accf += __shfl_xor(accf, 4, 16);
-    accf += __shfl_xor(accf, 2, 16);
-    accf += __shfl_xor(accf, 1, 16);
+    accf = llmq_reduce16(accf);
     if (live && L == 0) out[i] = accf;
 }
 

@@ -90,14 +90,39 @@ GGUF_BLOCK = {  # ggml type id: (weights per block, bytes per block), gguf.mojo:
     2: (32, 18), 3: (32, 20), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
 
 
-def gguf_blocks(kind, rows, cols, seed, scale=0.01):
+def k_scales_bytes(sc, m):
+    """The 12 bytes of a K-quant superblock's eight 6-bit sub-block scales sc
+    and mins m ([n, 8] each): the packing k_scale_min reads (gguf.mojo:205-221)."""
+    sc = np.asarray(sc, np.uint8)
+    m = np.asarray(m, np.uint8)
+    q = np.zeros((sc.shape[0], 12), np.uint8)
+    for j in range(4):
+        q[:, j] = sc[:, j] | ((sc[:, j + 4] >> 4) << 6)
+        q[:, j + 4] = m[:, j] | ((m[:, j + 4] >> 4) << 6)
+        q[:, j + 8] = (sc[:, j + 4] & 0xF) | ((m[:, j + 4] & 0xF) << 4)
+    return q
+
+
+def gguf_blocks(kind, rows, cols, seed, scale=0.01, centered=False):
     """Random GGUF blocks of the Llama GEMV sweep: every code field uniform over
     its range (random bytes), 6-bit sub-scales / mins uniform (random bytes),
-    and the float16 scales |N(0, scale)| (Q4_1's min negative, as a min is)."""
+    and the float16 scales |N(0, scale)| (Q4_1's min negative, as a min is).
+    centered (Q4_K / Q5_K): each sub-block's min equals its scale and dmin is
+    d times the codes' mean (7.5 / 15.5), so the weights d sc (q - mean) have
+    mean ~0, as trained weights do; uniform codes with random mins give every
+    row a common positive offset that swamps a model's dependence on its input."""
     bs, bb = GGUF_BLOCK[kind]
     nb = rows * (cols // bs)
     rng = np.random.default_rng(seed)
     b = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+    if centered and kind in (12, 13):
+        d = np.abs(rng.normal(0, scale, nb)).astype(np.float16)
+        dmin = (d.astype(np.float32) * (7.5 if kind == 12 else 15.5)).astype(np.float16)
+        b[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        b[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+        sc = rng.integers(1, 64, (nb, 8), dtype=np.uint8)
+        b[:, 4:16] = k_scales_bytes(sc, sc)
+        return b.reshape(-1)
 
     def f16(col, neg=False):
         v = np.abs(rng.normal(0, scale, nb)).astype(np.float16)
@@ -118,7 +143,7 @@ def gguf_blocks(kind, rows, cols, seed, scale=0.01):
     return b.reshape(-1)
 
 
-def llama_tensors(cfg, seed):
+def llama_tensors(cfg, seed, centered=False):
     """Seeded random weights of the config-4 decoder, in llmq_llama_create's
     order (llm_mojo_amd.llama.tensor_names): GGUF blocks whose float16 scales
     keep weights near N(0, 0.02) in size (Q4_K d |N(0, 1e-4)|, Q6_K d
@@ -134,7 +159,7 @@ def llama_tensors(cfg, seed):
             continue
         t = cfg["head_type"] if kind == "output" else (cfg["embd_type"] if kind == "token_embd" else cfg["layer_type"])
         rows, cols = shapes[kind]
-        out.append(gguf_blocks(t, rows, cols, seed * 1000 + i, scale=2e-5 if t == 14 else 1e-4))
+        out.append(gguf_blocks(t, rows, cols, seed * 1000 + i, scale=2e-5 if t == 14 else 1e-4, centered=centered))
     return out
 
 

@@ -129,11 +129,13 @@ def test_int8_channel_head_bit_exact(gpu, orc, V, C, ln):
 @pytest.mark.parametrize("fmt", [(4, 32, False), (8, 32, False), (8, 0, False)])
 @pytest.mark.parametrize("T", [2, 3, 5, 7, 12, 33])
 def test_prompt_gemm_bit_exact(gpu, orc, fmt, T):
-    """Several tokens (prompts) in tile_i16's order, GPT-2 layer shapes."""
+    """Several tokens (prompts) in tile_i16's order, GPT-2 layer shapes, and
+    row counts that leave n % 32 rows to rows_i16's order (kernels.mojo:
+    576-614): 70 and 50 rows, and 17 (fewer than one tile)."""
     torch, lm, ctx = gpu
     bits, group, sym = fmt
     rng = np.random.default_rng(T * 3 + bits)
-    for IN, OUT, flags in ((768, 2304, 0), (3072, 768, 1), (768, 3072, 2)):
+    for IN, OUT, flags in ((768, 2304, 0), (3072, 768, 1), (768, 3072, 2), (768, 70, 2), (3072, 50, 1), (768, 17, 0)):
         w = rng.normal(0, 0.02, (IN, OUT)).astype(np.float32)
         x = rng.normal(0, 1, (T, IN)).astype(np.float32)
         b = rng.normal(0, 0.1, OUT).astype(np.float32)

@@ -1,10 +1,16 @@
 """Exact .5 ties in config 0: the codes whose value the tie rule of Mojo's
 round() decides (tensor.mojo:377,381; kernels.mojo:415; kvcache.mojo:330).
-That rule is parity unpinned (no Mojo here); the oracle and the GPU round
-half away from zero.  On the synthetic checkpoint the weights meet 136 ties
-and the int16 activation codes about 31 per forward, so the rule is not
-moot: these tests pin the counts and show what the other rule (half to
-even) changes: the same greedy tokens, logits within 3e-3 of max |logit|.
+The oracle and the GPU round half away from zero.  The reference's own
+evidence on the rule is textual: PLAN.md:394-397 reports that its NumPy
+restatement (tests/reference.py --act16, whose np.round is half to even)
+matches the Mojo run to 5 digits, "the remaining difference is rounding of
+exact .5 ties", so Mojo's round() is not half to even; half away from zero
+is the other rule in use (and LLVM's llvm.round, which a SIMD round lowers
+to, is defined that way).  No run of Mojo here can settle it beyond that
+text.  On the synthetic checkpoint the weights meet 136 ties and the int16
+activation codes about 31 per forward, so the rule is not moot: these tests
+pin the counts and show what half to even would change: the same greedy
+tokens, logits within 3e-3 of max |logit|.
 """
 import numpy as np
 import pytest

@@ -68,9 +68,9 @@ def read_floor(torch, lm, ctx, stream, nbytes, nbuf, grid=2048, reps=None, graph
     bufs = [torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
     out = torch.zeros(grid, dtype=torch.int32, device="cuda")
     reps = reps or max(60, 4 * nbuf)
-    if graph:
+    if graph:  # (at least 64 launches a graph: a replay's own start-up is then a small share)
         us = graph_us(torch, ctx, stream, lambda i: lm.debug_read(ctx, bufs[i % nbuf], out, grid),
-                      max(nbuf, min(reps, 4 * nbuf)))
+                      max(nbuf, 64, min(reps, 4 * nbuf)))
         del bufs
         return us
     for i in range(2 * nbuf):
@@ -242,8 +242,10 @@ def gemv_micro(torch, lm, ctx, reps=200, rot_bytes=320 << 20):
             us_hbm = timed(lambda i: lm.linear(ctx, out, x, ws[i % nrot]), nrot)
             for m in ws:
                 m.free()
-            llc_floor = read_floor(torch, lm, ctx, stream, nb, 1, grid=256, reps=64, graph=True)
-            hbm_floor = read_floor(torch, lm, ctx, stream, nb, nrot, grid=256, reps=nrot, graph=True)
+            llc_floor = min(read_floor(torch, lm, ctx, stream, nb, 1, grid=gr, reps=64, graph=True)
+                            for gr in (256, 1024, 2048))
+            hbm_floor = min(read_floor(torch, lm, ctx, stream, nb, nrot, grid=gr, reps=nrot, graph=True)
+                            for gr in (256, 1024, 2048))
             res[name] = {"llc_us": round(us, 2), "llc_gbs": round(alg / us / 1e3, 1),
                          "llc_floor_us": round(llc_floor, 2),
                          "hbm_us": round(us_hbm, 2), "hbm_gbs": round(alg / us_hbm / 1e3, 1),

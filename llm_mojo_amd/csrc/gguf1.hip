@@ -74,6 +74,12 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
+// Streamed weight codes: non-temporal (no reuse expected; the caches keep
+// the activations instead).
+__device__ __forceinline__ uint4 bload16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
 __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
     return make_uint2(v[0], v[1]);
@@ -335,7 +341,7 @@ __global__ __launch_bounds__(NW * 64) void gguf1_kernel(G1Args a) {
     uint2 wb[T::BITS_ESZ > 0 ? STEPS : 1];
     auto load_step = [&](int u) {
         const uint32_t cr = offA + (uint32_t)u * 64u + (sA + u >= S ? wrap_adj : 0u) + lane_cr;
-        wc[u] = bload16(rc, u < ns ? cr * 16u : kOOB);
+        wc[u] = bload16_nt(rc, u < ns ? cr * 16u : kOOB);
         if constexpr (T::BITS_ESZ == 8) wb[u] = bload8(rb, u < ns ? cr * 8u : kOOB);
         if constexpr (T::BITS_ESZ == 4) wb[u] = make_uint2(bload4(rb, u < ns ? cr * 4u : kOOB), 0u);
     };
@@ -621,16 +627,23 @@ int max_steps(const llmq_mat *w) {
 Plan make_plan(const llmq_mat *w) {
     Plan p{};
     const int S = (int)((w->CK + 3) / 4);
-    // 16 waves for matrices streamed from HBM or with more than 4 steps a
-    // wave in one tile; 4-wave workgroups of one row tile otherwise (they
-    // launch faster; with 8 steps a wave the K-quants' decode work runs one
-    // wave per SIMD and is slower: Q5_K 4096x4096 7.22 -> 7.84 us).
-    int nw = w->ntiles * w->CK * 256 >= kStreamBytes ? 16 : 4;
-    if (const char *e = getenv("LLMQ_GEMV1_NW")) {
-        const int v = atoi(e);
-        if (v == 4 || v == 16) nw = v;
+    const int64_t bytes = w->ntiles * w->CK * 256;
+    // 4-wave workgroups of one row tile for matrices up to 4 steps a wave
+    // (they launch faster; with 8 steps a wave the K-quants' decode work
+    // runs one wave per SIMD and is slower: Q5_K 4096x4096 7.22 -> 7.84 us),
+    // and for matrices streamed from HBM up to 8 steps a wave (4096 inputs:
+    // 688-2000 workgroups; Q4_K 4096x11008 10.3 -> 9.7 us, Q6_K 12.6 ->
+    // 11.8 us, Q4_K 4096x32000 23.4 -> 21.9 us against the 16-wave form);
+    // 16 waves otherwise.  LLMQ_GEMV1_NW=4|8|16 forces the shape, for
+    // measurement.
+    const int cap4 = bytes >= kStreamBytes ? 8 : 4;
+    int nw = (S + 3) / 4 <= cap4 ? 4 : 16;
+    const char *force = getenv("LLMQ_GEMV1_NW");
+    if (force) {
+        const int v = atoi(force);
+        if (v == 4 || v == 8 || v == 16) nw = v;
+        if (nw < 16 && (S + nw - 1) / nw > 8) nw = 16;
     }
-    if (nw == 4 && (S + 3) / 4 > 4) nw = 16;
     int64_t grid = w->ntiles;
     if (nw == 16) {
         grid = std::min<int64_t>(w->ntiles, 256);
@@ -646,8 +659,15 @@ Plan make_plan(const llmq_mat *w) {
     p.tmax = (int)((w->ntiles + grid - 1) / grid);
     p.spw = (p.tmax * S + nw - 1) / nw;
     p.steps = steps_for(p.spw);
-    p.win = (nw == 16 && w->ntiles * w->CK * 256 >= kStreamBytes) ? kStreamWin : p.steps;
-    if (const char *e = getenv("LLMQ_GGUF1_WIN")) p.win = (nw == 16 && atoi(e) == kStreamWin) ? kStreamWin : p.steps;
+    // Two code steps in flight a wave, the next issued as each is consumed,
+    // for 16-wave plans and matrices of 8 MB or more (fewer bytes queued
+    // ahead of the activation row's fetch: config 4's down 6.90 -> 6.75 us,
+    // gate / up 6.70 -> 6.62 us); every step up front for the small ones
+    // (qkv-sized: 4.18 against 4.33 us).  LLMQ_GGUF1_WIN=2 forces the
+    // window, any other value every step up front.
+    p.win = (nw == 16 || bytes >= (8ll << 20)) ? kStreamWin : p.steps;
+    if (const char *e = getenv("LLMQ_GGUF1_WIN")) p.win = atoi(e) == kStreamWin ? kStreamWin : p.steps;
+    if (p.win > p.steps) p.win = p.steps;
     return p;
 }
 
@@ -676,7 +696,7 @@ int launch_w(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
 
 template <int TYPE, int NW, int STEPS>
 int launch_t(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
-    if constexpr (NW == 16 && STEPS > kStreamWin)
+    if constexpr (STEPS > kStreamWin)
         if (p.win == kStreamWin) return launch_w<TYPE, NW, STEPS, kStreamWin>(ctx, a, p, lds);
     return launch_w<TYPE, NW, STEPS, STEPS>(ctx, a, p, lds);
 }
@@ -684,12 +704,21 @@ int launch_t(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
 template <int TYPE>
 int launch_type(llmq_ctx *ctx, const G1Args &a, const Plan &p, size_t lds) {
     if (p.nw == 4) {
-        if (a.apart) {  // attention-combine staging: 4-wave plans only (gguf_gemv_attn_ok)
+        if (a.apart) {  // attention-combine staging: 4- and 8-wave plans only (gguf_gemv_attn_ok)
             if (p.steps == 2) return launch_w<TYPE, 4, 2, 2, true>(ctx, a, p, lds);
             if (p.steps == 4) return launch_w<TYPE, 4, 4, 4, true>(ctx, a, p, lds);
         }
         if (p.steps == 2) return launch_t<TYPE, 4, 2>(ctx, a, p, lds);
         if (p.steps == 4) return launch_t<TYPE, 4, 4>(ctx, a, p, lds);
+        if (p.steps == 8) return launch_t<TYPE, 4, 8>(ctx, a, p, lds);
+    } else if (p.nw == 8) {
+        if (a.apart) {
+            if (p.steps == 2) return launch_w<TYPE, 8, 2, 2, true>(ctx, a, p, lds);
+            if (p.steps == 4) return launch_w<TYPE, 8, 4, 4, true>(ctx, a, p, lds);
+        }
+        if (p.steps == 2) return launch_t<TYPE, 8, 2>(ctx, a, p, lds);
+        if (p.steps == 4) return launch_t<TYPE, 8, 4>(ctx, a, p, lds);
+        if (p.steps == 8) return launch_t<TYPE, 8, 8>(ctx, a, p, lds);
     } else {
         if (p.steps == 2) return launch_t<TYPE, 16, 2>(ctx, a, p, lds);
         if (p.steps == 4) return launch_t<TYPE, 16, 4>(ctx, a, p, lds);
@@ -715,7 +744,7 @@ bool gguf_gemv_attn_ok(const llmq_mat *w, int ns_max, int head_dim) {
     if (head_dim != kLlmqSplitHD) return false;
     if (!w || !is_float_act(w) || w->k % 64 != 0 || ns_max < 1 || ns_max > kACMax) return false;
     const Plan p = make_plan(w);
-    return p.nw == 4 && (p.steps == 2 || p.steps == 4) && w->k / 4 <= (int64_t)kACUnits * 4 * 64;
+    return (p.nw == 4 || p.nw == 8) && (p.steps == 2 || p.steps == 4) && w->k / 4 <= (int64_t)kACUnits * 4 * 64;
 }
 
 int launch_gguf_gemv(llmq_ctx *ctx, const llmq_mat *w, const float *x, float *out, const float *bias, int flags,

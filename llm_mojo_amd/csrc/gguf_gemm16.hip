@@ -50,6 +50,7 @@ struct HArgs {
     const uint8_t *codes, *sb, *planes, *sums, *inv;
     uint32_t codes_bytes, sb_bytes, planes_bytes, sums_bytes, inv_bytes;
     int n, KB, CK, NSB, ntiles, T, flags;
+    int stream;  // weights read by one token tile only: non-temporal loads
     int64_t ldo;
     const float *bias;
     float *out;
@@ -61,6 +62,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint3
 __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// Weight loads: non-temporal when no other workgroup reads the same weights
+// (`nt`, uniform), else cached for the other token tiles.
+__device__ __forceinline__ uint4 wload16(__amdgpu_buffer_rsrc_t r, uint32_t off, bool nt) {
+    const auto v = nt ? __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2)
+                      : __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t wload4(__amdgpu_buffer_rsrc_t r, uint32_t off, bool nt) {
+    return nt ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 2)
+              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
@@ -126,11 +138,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             const bool ok = tile0 + r < a.ntiles;
-            f[r] = bload16(rs, ok ? (uint32_t)((((tile0 + r) * a.NSB + sbi) * 16 + c16) * 16) : kOOB);
+            f[r] = wload16(rs, ok ? (uint32_t)((((tile0 + r) * a.NSB + sbi) * 16 + c16) * 16) : kOOB, a.stream);
             // chunk entries of one row tile are 256 bytes apart (kOOB + 256 u stays out of range)
             const uint32_t cb = ok ? (uint32_t)((((tile0 + r) * a.CK + sbi * 8) * 16 + c16) * 16 + g * 4) : kOOB;
 #pragma unroll
-            for (int u = 0; u < 8; u++) cw[r][u] = bload4(rc, cb + 256u * u);
+            for (int u = 0; u < 8; u++) cw[r][u] = wload4(rc, cb + 256u * u, a.stream);
         }
         const uint32_t ab = (uint32_t)((tt * a.KB + sbi * 8) * 2048 + lane * 16);
 #pragma unroll
@@ -459,6 +471,7 @@ int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int6
     a.bias = bias ? bias : out;
     a.out = out;
     const unsigned ntt = (unsigned)(T16 / 16);
+    a.stream = ntt == 1;
     // waves: the fewest that give every wave per = ceil(NSB / 16) superblocks
     const int per = (int)((NSB + 15) / 16), nw = (int)((NSB + per - 1) / per);
     const unsigned nt = (unsigned)w->ntiles;

@@ -48,6 +48,19 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
+// The head's weights, read once a step: non-temporal loads (the caches keep
+// the activations and the small tensors instead).
+__device__ __forceinline__ uint4 bload16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bload8_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 2);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t bload4_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 2);
+}
 __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
     return make_uint2(v[0], v[1]);
@@ -111,17 +124,17 @@ __device__ __forceinline__ RawUnit<TYPE> load_unit(const H16Args &a, bool ok, in
 #pragma unroll
         for (int c = 0; c < 8; c++) {
             const uint32_t e = (c0 + c) * 16u + (uint32_t)r;  // (chunk, row) entry
-            w.cw[c] = bload4(rc, ok ? e * 16u + 4u * (uint32_t)q : kOOB);
-            w.hw[c] = bload4(rb, ok ? e * 8u + 4u * (uint32_t)(q >> 1) : kOOB);
+            w.cw[c] = bload4_nt(rc, ok ? e * 16u + 4u * (uint32_t)q : kOOB);
+            w.hw[c] = bload4_nt(rb, ok ? e * 8u + 4u * (uint32_t)(q >> 1) : kOOB);
         }
         const uint32_t se = ((uint32_t)tile * (uint32_t)a.NU + (uint32_t)u) * 16u + (uint32_t)r;
-        w.sc = bload16(rs, ok ? se * 16u : kOOB);
-        w.dw = bload4(rd, ok ? (se * 2u) & ~3u : kOOB);
+        w.sc = bload16_nt(rs, ok ? se * 16u : kOOB);
+        w.dw = bload4_nt(rd, ok ? (se * 2u) & ~3u : kOOB);
     } else {
         const uint32_t e = ((uint32_t)tile * (uint32_t)a.CK + 2u * (uint32_t)u + (uint32_t)(q >> 1)) * 16u + (uint32_t)r;
-        w.cw = bload8(rc, ok ? e * 16u + 8u * (uint32_t)(q & 1) : kOOB);
+        w.cw = bload8_nt(rc, ok ? e * 16u + 8u * (uint32_t)(q & 1) : kOOB);
         const uint32_t de = ((uint32_t)tile * (uint32_t)(a.CK / 2) + (uint32_t)u) * 16u + (uint32_t)r;
-        w.dw = bload4(rd, ok ? (de * 2u) & ~3u : kOOB);
+        w.dw = bload4_nt(rd, ok ? (de * 2u) & ~3u : kOOB);
     }
     return w;
 }

@@ -491,6 +491,7 @@ def cpu_baseline(tensors, prompt):
         log(f"cpu baseline: {t} threads {sweep[t]} tok/s")
     best = max(sweep, key=sweep.get)
     head_ms = round(m.cpu_head_seconds(min(4, nt), 30) * 1e3, 3)
+    extra = cpu_kernels(oracle, tensors, nt)
     return {"value": sweep[nt], "unit": "tok/s", "cores": nt, "kind": "port",
             "label": "C restatement of llm_mojo's CPU path",
             "sample": f"GPT-2 124M int4-g32-a16 (int8-ch head, int8 KV): {len(prompt)}-token prompt through the "
@@ -499,7 +500,59 @@ def cpu_baseline(tensors, prompt):
                       f" on {nt} threads",
             "vnni": vnni, "threads_sweep_tok_s": sweep, "best": {"threads": best, "tok_s": sweep[best]},
             "head_int8_ch_ms": {"threads": min(4, nt), "ms": head_ms, "reference_4t_ms": "0.96-1.00"},
-            "host": host}
+            **extra, "host": host}
+
+
+def cpu_kernels(oracle, tensors, nt, reps=100, rot_bytes=256 << 20):
+    """The CPU baseline's per-config kernels on nt threads, beside the GPU's:
+    config 3's 476-token prompt (Model.forward with tile_i16 on VPDPWSSD,
+    kernels.mojo:512-573, and the vector attention; median of 3 after a
+    warm-up), config 1's one-token GEMVs (linear_team, kernels.mojo:774-866,
+    with dot_row_i16's VNNI branches) and config 2's GGUF GEMVs (dot_row's
+    block decoders on AVX-512, gguf.mojo:178-297, 388-417): median of `reps`
+    calls over copies totalling >= rot_bytes, so codes come from memory.
+    Every form is bit-identical to the scalar oracle (tests/)."""
+    import numpy as np
+
+    from llm_mojo_amd import gpt2, synth
+
+    res = {}
+    m = oracle.GPT2(gpt2.params_list(tensors))
+    prompt = synth.prompt_ids(SEED, PREFILL_T)
+    secs = []
+    for _ in range(4):
+        _, s = m.cpu_prompt(prompt, nt)
+        secs.append(s)
+    s = sorted(secs[1:])[1]
+    res["prompt_476"] = {"tok_s": round(PREFILL_T / s, 1), "ms": round(s * 1e3, 1), "threads": nt}
+    log("cpu baseline: 476-token prompt", res["prompt_476"])
+    rng = np.random.default_rng(1001)
+    g1 = {}
+    cases = [(f"int{b}-g{gr} {n}", K, N, b, gr) for b, gr in GEMV_FORMATS for n, K, N in GPT2_SHAPES]
+    cases.append(("int8-ch head", 768, 50257, 8, 0))
+    for name, K, N, bits, group in cases:
+        w = rng.normal(0, 0.02, (K, N)).astype(np.float32)
+        q = oracle.QuantMatrix.from_f32(w, bits, group, False, True)
+        mats = [q] + [q.clone() for _ in range(max(1, rot_bytes // max(1, q.nbytes())) - 1)]
+        x = rng.normal(0, 1, (1, K)).astype(np.float32)
+        sec, _ = oracle.cpu_gemv_seconds(mats, x, nt, reps)
+        g1[name] = round(sec * 1e3, 4)
+        del mats
+    res["gemv_cfg1_ms"] = g1
+    log("cpu baseline: config-1 GEMVs (ms)", g1)
+    g2 = {}
+    for tname, t in GGUF_KINDS.items():
+        for K, N in GGUF_SHAPES:
+            bs, bb = synth.GGUF_BLOCK[t]
+            base = synth.gguf_blocks(t, N, K, seed=7)
+            copies = [base] + [base.copy() for _ in range(max(1, rot_bytes // base.nbytes) - 1)]
+            x = rng.normal(0, 1, K).astype(np.float32)
+            sec, _ = oracle.cpu_gguf_gemv_seconds(t, copies, N, K, x, nt, reps)
+            g2[f"{tname} {K}x{N}"] = round(sec * 1e3, 3)
+            del copies
+    res["gguf_cfg2_ms"] = g2
+    log("cpu baseline: config-2 GGUF GEMVs (ms)", g2)
+    return res
 
 
 def main():

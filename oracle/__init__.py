@@ -81,6 +81,11 @@ def _declare(L):
         "orc_cpu_generate": (I32, [P, P, I32, I32, I32, P, P]),
         "orc_cpu_decode": (P, [P, I64, I32, I32]),
         "orc_cpu_head_seconds": (ctypes.c_double, [P, I32, I32]),
+        "orc_cpu_set_fast": (I32, [I32]),
+        "orc_cpu_prompt": (P, [P, P, I32, I32, P]),
+        "orc_cpu_gemv_seconds": (ctypes.c_double, [P, I32, P, P, I32, I32]),
+        "orc_cpu_gguf_gemv_seconds": (ctypes.c_double, [I32, P, I32, I64, I64, P, P, I32, I32]),
+        "orc_cpu_gguf_dot_row": (ctypes.c_float, [I32, P, I64, P]),
         "orc_reset_ties": (None, []),
         "orc_exp": (ctypes.c_float, [ctypes.c_float]),
         "orc_tanh": (ctypes.c_float, [ctypes.c_float]),
@@ -178,6 +183,41 @@ def set_threads(n):
     lib().orc_set_threads(int(n))
 
 
+def cpu_set_fast(on):
+    """Switches the oracle's matmuls, quantizer and attention to their AVX-512
+    VNNI forms (bit-identical; the CPU baseline) or back; returns whether on."""
+    return bool(lib().orc_cpu_set_fast(1 if on else 0))
+
+
+def cpu_gemv_seconds(mats, x, threads, reps=100):
+    """linear_team of one token (kernels.mojo:774-866) on a team of
+    `threads`: median seconds over `reps` calls cycling over `mats` (copies
+    of one QuantMatrix, from memory rather than cache)."""
+    arr = (ctypes.c_void_p * len(mats))(*[ctypes.addressof(m.s) for m in mats])
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(mats[0].n, np.float32)
+    t = lib().orc_cpu_gemv_seconds(arr, len(mats), ptr(x), ptr(out), int(threads), int(reps))
+    return float(t), out
+
+
+def cpu_gguf_gemv_seconds(t, blocks_list, rows, cols, x, threads, reps=100):
+    """GGUFMatrix.dot_row over every row (AVX-512 decoders) on a team of
+    `threads`: median seconds over `reps` calls cycling over the copies."""
+    keep = [np.ascontiguousarray(b, np.uint8) for b in blocks_list]
+    arr = (ctypes.c_void_p * len(keep))(*[b.ctypes.data for b in keep])
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(rows, np.float32)
+    sec = lib().orc_cpu_gguf_gemv_seconds(int(t), arr, len(keep), int(rows), int(cols), ptr(x), ptr(out),
+                                          int(threads), int(reps))
+    return float(sec), out
+
+
+def cpu_gguf_dot_row(t, row_bytes, cols, x):
+    """One row through the baseline's AVX-512 GGUF decoder."""
+    return lib().orc_cpu_gguf_dot_row(t, ptr(np.ascontiguousarray(row_bytes, np.uint8)), cols,
+                                      ptr(np.ascontiguousarray(x, np.float32)))
+
+
 def f32_to_f16_bits(v):
     return lib().orc_f32_to_f16(ctypes.c_float(v))
 
@@ -213,6 +253,16 @@ class QuantMatrix:
         self.n, self.k, self.group = self.s.n, self.s.k, self.s.group
         self.blocked = bool(self.s.blocked)
         return self
+
+    def clone(self):
+        """A copy with its own codes, scales and zero points (for timing over
+        rotated buffers)."""
+        c = QuantMatrix(self.bits, self.group_param, self.sym, self.a16)
+        c.data, c.scale, c.zp = self.data.copy(), self.scale.copy(), self.zp.copy()
+        c.s = QM(self.s.bits, self.s.sym, self.s.a16, self.s.blocked, self.s.perch, self.s.n, self.s.k, self.s.group,
+                 c.data.ctypes.data, c.scale.ctypes.data, c.zp.ctypes.data)
+        c.n, c.k, c.group, c.blocked = self.n, self.k, self.group, self.blocked
+        return c
 
     @property
     def ref(self):
@@ -750,6 +800,17 @@ class GPT2:
         if not p:
             raise ValueError("cpu_decode: bad arguments or no threads")
         return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(50257,)).copy()
+
+    def cpu_prompt(self, tokens, threads):
+        """Model.forward of a prompt on the CPU baseline's AVX-512 VNNI forms
+        over `threads` threads: (logits, seconds); logits equal forward()'s."""
+        toks = np.ascontiguousarray(tokens, np.int64)
+        secs = np.zeros(1, np.float64)
+        p = lib().orc_cpu_prompt(self.h, ptr(toks), len(toks), int(threads), ptr(secs))
+        if not p:
+            raise ValueError("cpu_prompt: bad arguments")
+        lg = np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(50257,)).copy()
+        return lg, float(secs[0])
 
     def cpu_head_seconds(self, threads, reps=50):
         """Median seconds of the int8 per-channel head on a team of `threads`."""

@@ -599,6 +599,16 @@ static void tile_i16(int TM, float *out, const int16_t *xq, const float *sx, con
     }
 }
 
+/* CPU-baseline hooks (orc_cpu_set_fast, in the baseline section below):
+ * AVX-512 VNNI forms of the tile, the one-token row dot, the row quantizer
+ * and one head's attention, each bit-identical to the scalar code it
+ * stands in for (tests/test_cpu_baseline.py).  NULL: the scalar oracle. */
+typedef void (*orc_tile_fn)(int, float *, const int16_t *, const float *, const int16_t *, const float *,
+                            const float *, int64_t, int64_t, int64_t, int64_t, int64_t, int);
+static orc_tile_fn g_fast_tile = NULL;
+static float (*g_fast_row)(const orc_qm *, int64_t, const int16_t *, const float *) = NULL;
+static void (*g_fast_quant)(const float *, int64_t, int16_t *, float *) = NULL;
+
 /* matmul_rows_a16 (kernels.mojo:419-509): out[T, OUT] (+)= act(x @ w^T + b).
  * flags: EPI_BIAS | EPI_GELU | EPI_RESID.  Rows (T == 1) or 32-row tiles
  * (T > 1) are split across g_threads threads; the arithmetic per output does
@@ -607,7 +617,12 @@ void orc_matmul_rows_a16(float *out, const float *x, const orc_qm *w, const floa
                          int64_t OUT, int flags) {
     int16_t *xq = (int16_t *)malloc(sizeof(int16_t) * (size_t)(T * IN));
     float *sx = (float *)malloc(sizeof(float) * (size_t)T);
-    orc_quantize_rows(x, T, IN, xq, sx);
+    if (g_fast_quant && IN % 16 == 0) {
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && T > 1)
+        for (int64_t t = 0; t < T; t++) g_fast_quant(x + t * IN, IN, xq + t * IN, sx + t);
+    } else {
+        orc_quantize_rows(x, T, IN, xq, sx);
+    }
     if (T == 1) {
         int16_t *xp = (int16_t *)malloc(sizeof(int16_t) * (size_t)IN);
         float *xs = (float *)malloc(sizeof(float) * (size_t)(IN / 16 + 1));
@@ -615,7 +630,7 @@ void orc_matmul_rows_a16(float *out, const float *x, const orc_qm *w, const floa
         float s = sx[0];
 #pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
         for (int64_t o = 0; o < OUT; o++) {
-            float r = orc_qm_dot_row_i16(w, o, x1, xs) * s;
+            float r = (g_fast_row ? g_fast_row(w, o, x1, xs) : orc_qm_dot_row_i16(w, o, x1, xs)) * s;
             if (flags & EPI_BIAS) r += b[o];
             finish(out, o, r, flags);
         }
@@ -649,8 +664,9 @@ void orc_matmul_rows_a16(float *out, const float *x, const orc_qm *w, const floa
                     for (int64_t g = 0; g < IN / G; g++) st[g * TN + j] = rs[g];
                 }
                 int64_t t = 0;
-                for (; t + 4 <= T; t += 4) tile_i16(4, out, xq, sx, wt, st, b, t, o0, IN, OUT, G, flags);
-                for (; t < T; t++) tile_i16(1, out, xq, sx, wt, st, b, t, o0, IN, OUT, G, flags);
+                const orc_tile_fn tile = g_fast_tile ? g_fast_tile : tile_i16;
+                for (; t + 4 <= T; t += 4) tile(4, out, xq, sx, wt, st, b, t, o0, IN, OUT, G, flags);
+                for (; t < T; t++) tile(1, out, xq, sx, wt, st, b, t, o0, IN, OUT, G, flags);
                 free(wt);
                 free(st);
             }
@@ -1054,9 +1070,19 @@ void orc_kv_attend_one(const orc_kv *kv, float *out, const float *qkv, int layer
 }
 
 /* KVCache.attend (kvcache.mojo:62-79): every token and head. */
+/* (CPU baseline: one head of one token at a position below ORC_FAST_MAXT) */
+#define ORC_FAST_MAXT 1024
+static void (*g_fast_attend)(const orc_kv *, float *, const float *, int, int, int) = NULL;
 void orc_kv_attend(const orc_kv *kv, float *out, const float *qkv, int layer, int T, int pos0) {
+    const int C = kv->n_head * kv->head_dim;
 #pragma omp parallel for schedule(dynamic) num_threads(g_threads) if (g_threads > 1 && T * (pos0 + T) >= 256)
-    for (int idx = 0; idx < kv->n_head * T; idx++) orc_kv_attend_one(kv, out, qkv, layer, idx / kv->n_head, idx % kv->n_head, pos0);
+    for (int idx = 0; idx < kv->n_head * T; idx++) {
+        const int t = idx / kv->n_head, h = idx % kv->n_head;
+        if (g_fast_attend && kv->head_dim == 64 && pos0 + t < ORC_FAST_MAXT)
+            g_fast_attend(kv, out + (int64_t)t * C, qkv + (int64_t)t * 3 * C, layer, h, pos0 + t);
+        else
+            orc_kv_attend_one(kv, out, qkv, layer, t, h, pos0);
+    }
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1246,6 +1272,7 @@ void orc_ikv_attend(const orc_ikv *kv, float *out, const float *qkv, int layer, 
 #define G_C 768
 #define G_HS 64
 #define G_MAXT 1024
+_Static_assert(G_MAXT == ORC_FAST_MAXT, "the fast attention's score buffer holds G_MAXT positions");
 #define G_V 50257
 
 /* Rng (gpt2t.mojo:777-789): xorshift64*. */
@@ -1733,6 +1760,196 @@ VNNI static void attend_one_vnni(const orc_kv *kv, float *out, const float *qkv,
     _mm512_storeu_ps(o + 48, a3);
 }
 
+/* dot_row_i16's general loop (tensor.mojo:567-577) for the formats that are
+ * neither BLOCKED nor int8 per channel: per group, VPDPWSSD over its 32-code
+ * pieces (codes_i16: int4 low nibbles of 16 bytes, then their high
+ * nibbles; int8 bytes; minus the zero point), then fma(f32(acc), scale). */
+VNNI static float dot_generic_vnni(const orc_qm *m, int64_t row, const int16_t *xq) {
+    const int64_t gpr = m->k / m->group;
+    const uint8_t *p = m->data + row * m->k * m->bits / 8;
+    const __m128i nib = _mm_set1_epi8(0x0f);
+    __m512 accf = _mm512_setzero_ps();
+    for (int64_t g = 0; g < gpr; g++) {
+        const __m512i zp = _mm512_set1_epi16((short)m->zp[row * gpr + g]);
+        __m512i acc = _mm512_setzero_si512();
+        for (int64_t k0 = g * m->group; k0 < (g + 1) * m->group; k0 += 32) {
+            __m512i u;
+            if (m->bits == 4) {
+                const __m128i b = _mm_loadu_si128((const __m128i *)(p + k0 / 2));
+                const __m256i lo = _mm256_cvtepu8_epi16(_mm_and_si128(b, nib));
+                const __m256i hi = _mm256_cvtepu8_epi16(_mm_and_si128(_mm_srli_epi16(b, 4), nib));
+                u = _mm512_inserti64x4(_mm512_castsi256_si512(lo), hi, 1);
+            } else {
+                u = _mm512_cvtepu8_epi16(_mm256_loadu_si256((const __m256i *)(p + k0)));
+            }
+            acc = _mm512_dpwssd_epi32(acc, _mm512_loadu_si512((const void *)(xq + k0)), _mm512_sub_epi16(u, zp));
+        }
+        const float sc = orc_f16_to_f32(m->scale[row * gpr + g]);
+        accf = _mm512_fmadd_ps(_mm512_cvtepi32_ps(acc), _mm512_set1_ps(sc), accf);
+    }
+    float v[L16];
+    _mm512_storeu_ps(v, accf);
+    return red16(v);
+}
+
+/* One row of dot_row_i16 by its branch (the scalar oracle's arithmetic). */
+VNNI static float fast_row(const orc_qm *m, int64_t row, const int16_t *x1, const float *xs) {
+    if (m->blocked) return dot_blocked_vnni(m, row, x1, xs);
+    if (m->perch && m->bits == 8) return dot_ch8_vnni1(m, row, x1);
+    if (m->group % 32 == 0) return dot_generic_vnni(m, row, x1);
+    return orc_qm_dot_row_i16(m, row, x1, xs);
+}
+
+/* tile_i16 (kernels.mojo:512-573) on VPDPWSSD: per input pair one token's
+ * two int16 activations broadcast as an int32 against 16 outputs x 2
+ * inputs of wt, per token two accumulators (32 outputs); at each segment
+ * end fma(f32(acc), scale, accf); the epilogue as the scalar tile. */
+VNNI static inline __attribute__((always_inline)) void tile_i16_vnni_tm(
+    const int TM, float *out, const int16_t *xq, const float *sx, const int16_t *wt, const float *st,
+    const float *b, int64_t t0, int64_t o0, int64_t IN, int64_t OUT, int64_t G, int flags) {
+    const int TN = 32, SEG = 256;
+    __m512 accf[4][2];
+    for (int m = 0; m < 4; m++) accf[m][0] = accf[m][1] = _mm512_setzero_ps();
+    const int64_t seg = G < SEG ? G : SEG;
+    for (int64_t k0 = 0; k0 < IN; k0 += seg) {
+        const int64_t g = k0 / G;
+        __m512i acc[4][2];
+        for (int m = 0; m < 4; m++) acc[m][0] = acc[m][1] = _mm512_setzero_si512();
+        for (int64_t kp = k0 / 2; kp < (k0 + seg) / 2; kp++) {
+            const __m512i w0 = _mm512_loadu_si512((const void *)(wt + kp * TN * 2));
+            const __m512i w1 = _mm512_loadu_si512((const void *)(wt + kp * TN * 2 + 32));
+            for (int m = 0; m < TM; m++) {
+                int32_t pair;
+                memcpy(&pair, xq + (t0 + m) * IN + 2 * kp, 4);
+                const __m512i xb = _mm512_set1_epi32(pair);
+                acc[m][0] = _mm512_dpwssd_epi32(acc[m][0], xb, w0);
+                acc[m][1] = _mm512_dpwssd_epi32(acc[m][1], xb, w1);
+            }
+        }
+        const __m512 s0 = _mm512_loadu_ps(st + g * TN), s1 = _mm512_loadu_ps(st + g * TN + 16);
+        for (int m = 0; m < TM; m++) {
+            accf[m][0] = _mm512_fmadd_ps(_mm512_cvtepi32_ps(acc[m][0]), s0, accf[m][0]);
+            accf[m][1] = _mm512_fmadd_ps(_mm512_cvtepi32_ps(acc[m][1]), s1, accf[m][1]);
+        }
+    }
+    for (int m = 0; m < TM; m++) {
+        const __m512 sxm = _mm512_set1_ps(sx[t0 + m]);
+        float r[32];
+        __m512 r0 = _mm512_mul_ps(accf[m][0], sxm), r1 = _mm512_mul_ps(accf[m][1], sxm);
+        if (flags & EPI_BIAS) {
+            r0 = _mm512_add_ps(r0, _mm512_loadu_ps(b + o0));
+            r1 = _mm512_add_ps(r1, _mm512_loadu_ps(b + o0 + 16));
+        }
+        _mm512_storeu_ps(r, r0);
+        _mm512_storeu_ps(r + 16, r1);
+        for (int j = 0; j < TN; j++) finish(out, (t0 + m) * OUT + o0 + j, r[j], flags);
+    }
+}
+/* (TM a compile-time constant in each call, so the accumulators stay in registers) */
+VNNI static void tile_i16_vnni(int TM, float *out, const int16_t *xq, const float *sx, const int16_t *wt,
+                               const float *st, const float *b, int64_t t0, int64_t o0, int64_t IN, int64_t OUT,
+                               int64_t G, int flags) {
+    if (TM == 4)
+        tile_i16_vnni_tm(4, out, xq, sx, wt, st, b, t0, o0, IN, OUT, G, flags);
+    else
+        for (int m = 0; m < TM; m++) tile_i16_vnni_tm(1, out, xq, sx, wt, st, b, t0 + m, o0, IN, OUT, G, flags);
+}
+
+/* Switches the oracle's matmuls, row quantizer and attention to their AVX-512
+ * VNNI forms (on == 1, where the CPU has them) or back to the scalar code.
+ * Returns whether the fast forms are on. */
+int orc_cpu_set_fast(int on) {
+    on = on && orc_cpu_vnni();
+    g_fast_tile = on ? tile_i16_vnni : NULL;
+    g_fast_row = on ? fast_row : NULL;
+    g_fast_quant = on ? quantize_row_vnni : NULL;
+    g_fast_attend = on ? attend_one_vnni : NULL;
+    return on;
+}
+
+/* GGUFMatrix.dot_row (gguf.mojo:388-417) on AVX-512: per 16 weights the
+ * block decoder's floats (gguf.mojo:178-297, the scalar oracle's operations
+ * in its order) and one fma into the 16 lanes, then the 16-lane sum.  The
+ * block formats Q4_0 / Q4_1 / Q8_0 / Q4_K / Q5_K / Q6_K. */
+VNNI static inline __m512 u8f(const uint8_t *p) { return _mm512_cvtepi32_ps(_mm512_cvtepu8_epi32(_mm_loadu_si128((const __m128i *)p))); }
+VNNI static inline __m512i u8i(const uint8_t *p) { return _mm512_cvtepu8_epi32(_mm_loadu_si128((const __m128i *)p)); }
+VNNI static float gguf_dot_row_avx512(int t, const uint8_t *p, int64_t cols, const float *x) {
+    const int bs = orc_gguf_block_size(t), bb = orc_gguf_block_bytes(t);
+    const __m512i m4 = _mm512_set1_epi32(0xf);
+    __m512 acc = _mm512_setzero_ps();
+#define PUT(off, v) acc = _mm512_fmadd_ps((v), _mm512_loadu_ps(xb + (off)), acc)
+    for (int64_t blk = 0; blk < cols / bs; blk++) {
+        const uint8_t *b = p + blk * bb;
+        const float *xb = x + blk * bs;
+        if (t == GGML_Q4_0) {
+            const __m512 d = _mm512_set1_ps(f16_at(b, 0)), e8 = _mm512_set1_ps(8.0f);
+            const __m512i q = u8i(b + 2);
+            PUT(0, _mm512_mul_ps(_mm512_sub_ps(_mm512_cvtepi32_ps(_mm512_and_si512(q, m4)), e8), d));
+            PUT(16, _mm512_mul_ps(_mm512_sub_ps(_mm512_cvtepi32_ps(_mm512_srli_epi32(q, 4)), e8), d));
+        } else if (t == GGML_Q4_1) {
+            const __m512 d = _mm512_set1_ps(f16_at(b, 0)), mm = _mm512_set1_ps(f16_at(b, 2));
+            const __m512i q = u8i(b + 4);
+            PUT(0, _mm512_add_ps(_mm512_mul_ps(d, _mm512_cvtepi32_ps(_mm512_and_si512(q, m4))), mm));
+            PUT(16, _mm512_add_ps(_mm512_mul_ps(d, _mm512_cvtepi32_ps(_mm512_srli_epi32(q, 4))), mm));
+        } else if (t == GGML_Q8_0) {
+            const __m512 d = _mm512_set1_ps(f16_at(b, 0));
+            for (int h = 0; h < 2; h++)
+                PUT(16 * h, _mm512_mul_ps(d, _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i *)(b + 2 + 16 * h))))));
+        } else if (t == GGML_Q4_K || t == GGML_Q5_K) {
+            const float d = f16_at(b, 0), dmin = f16_at(b, 2);
+            const uint8_t *scales = b + 4;
+            const int five = t == GGML_Q5_K;
+            for (int j = 0; j < 4; j++) {
+                int sc1, m1i, sc2, m2i;
+                k_scale_min(scales, 2 * j, &sc1, &m1i);
+                k_scale_min(scales, 2 * j + 1, &sc2, &m2i);
+                const __m512 d1 = _mm512_set1_ps(d * (float)sc1), m1 = _mm512_set1_ps(dmin * (float)m1i);
+                const __m512 d2 = _mm512_set1_ps(d * (float)sc2), m2 = _mm512_set1_ps(dmin * (float)m2i);
+                for (int h = 0; h < 2; h++) {
+                    const __m512i q = u8i(five ? b + 48 + 32 * j + 16 * h : b + 16 + 32 * j + 16 * h);
+                    __m512i lo = _mm512_and_si512(q, m4), hi = _mm512_srli_epi32(q, 4);
+                    if (five) {
+                        const __m512i qh = u8i(b + 16 + 16 * h);
+                        lo = _mm512_or_si512(lo, _mm512_slli_epi32(_mm512_and_si512(_mm512_srli_epi32(qh, 2 * j), _mm512_set1_epi32(1)), 4));
+                        hi = _mm512_or_si512(hi, _mm512_slli_epi32(_mm512_and_si512(_mm512_srli_epi32(qh, 2 * j + 1), _mm512_set1_epi32(1)), 4));
+                    }
+                    PUT(64 * j + 16 * h, _mm512_sub_ps(_mm512_mul_ps(d1, _mm512_cvtepi32_ps(lo)), m1));
+                    PUT(64 * j + 32 + 16 * h, _mm512_sub_ps(_mm512_mul_ps(d2, _mm512_cvtepi32_ps(hi)), m2));
+                }
+            }
+        } else if (t == GGML_Q6_K) {
+            const float d = f16_at(b, 208);
+            const __m512 e32 = _mm512_set1_ps(32.0f);
+            const __m512i m3 = _mm512_set1_epi32(3);
+            for (int n = 0; n < 2; n++) {
+                const int ql = 64 * n, qhoff = 128 + 32 * n, sc = 192 + 8 * n;
+                for (int h = 0; h < 2; h++) {
+                    const __m512i lo0 = u8i(b + ql + 16 * h), lo1 = u8i(b + ql + 32 + 16 * h), hi = u8i(b + qhoff + 16 * h);
+                    const int base = 128 * n + 16 * h;
+                    for (int k = 0; k < 4; k++) {
+                        const float ds = d * (float)(int8_t)b[sc + h + 2 * k];
+                        const __m512i l = k == 0 ? _mm512_and_si512(lo0, m4) : k == 1 ? _mm512_and_si512(lo1, m4)
+                                        : k == 2 ? _mm512_srli_epi32(lo0, 4) : _mm512_srli_epi32(lo1, 4);
+                        const __m512i q = _mm512_or_si512(l, _mm512_slli_epi32(_mm512_and_si512(_mm512_srli_epi32(hi, 2 * k), m3), 4));
+                        PUT(base + 32 * k, _mm512_mul_ps(_mm512_set1_ps(ds), _mm512_sub_ps(_mm512_cvtepi32_ps(q), e32)));
+                    }
+                }
+            }
+        }
+    }
+#undef PUT
+    (void)u8f;
+    float v[L16];
+    _mm512_storeu_ps(v, acc);
+    return red16(v);
+}
+
+/* One row through the AVX-512 decoder (tests: equal to orc_gguf_dot_row). */
+float orc_cpu_gguf_dot_row(int t, const uint8_t *row, int64_t cols, const float *x) {
+    if (!orc_cpu_vnni()) return orc_gguf_dot_row(t, row, cols, x);
+    return gguf_dot_row_avx512(t, row, cols, x);
+}
+
 /* Team (team.mojo:36-82): arrival count and generation on separate cache
  * lines; the last arrival resets the count, then advances the generation;
  * the others spin (PAUSE) for up to 1000 polls, then yield. */
@@ -1763,7 +1980,14 @@ static void team_wait(orc_team_bar *t) {
 typedef struct {
     orc_gpt2 *m;
     orc_team_bar bar;
-    int vnni, stop, job; /* job 0: a decode step; 1: the head alone */
+    int vnni, stop, job; /* job 0: a decode step; 1: the head alone; 2: one GEMV; 3: one GGUF GEMV */
+    /* jobs 2 and 3: the matrix, activations and outputs */
+    const orc_qm *gw;
+    int gtype;
+    const uint8_t *gblocks;
+    int64_t grows, gcols, growbytes;
+    const float *gx;
+    float *gout;
     int64_t token;
     int pos;
     /* linear_team's shared activations (gpt2t.mojo:370-373) */
@@ -1809,7 +2033,7 @@ static void team_linear(orc_team *c, int tid, float *out, const float *x, const 
         }
     } else {
         for (int64_t o = o0; o < o1; o++) {
-            float r = (c->vnni && w->blocked ? dot_blocked_vnni(w, o, x1, c->xs) : orc_qm_dot_row_i16(w, o, x1, c->xs)) * s;
+            float r = (c->vnni ? fast_row(w, o, x1, c->xs) : orc_qm_dot_row_i16(w, o, x1, c->xs)) * s;
             if (flags & EPI_BIAS) r += b[o];
             finish(out, o, r, flags);
         }
@@ -1854,10 +2078,20 @@ static void team_decode(orc_team *c, int tid) {
 
 /* The team's work for one start: a decode step, or the head alone. */
 static void team_job(orc_team *c, int tid) {
-    if (c->job == 0)
+    if (c->job == 0) {
         team_decode(c, tid);
-    else
+    } else if (c->job == 1) {
         team_linear(c, tid, c->m->logits, c->m->xn, &c->m->wte, NULL, G_C, G_V, 0);
+    } else if (c->job == 2) {
+        team_linear(c, tid, c->gout, c->gx, c->gw, NULL, c->gw->k, c->gw->n, 0);
+    } else { /* linear_team's OUT_MAJOR branch (kernels.mojo:817-826): dot_row per row, contiguous ranges */
+        int64_t o0, o1;
+        team_split(c->grows, tid, c->bar.nt, &o0, &o1);
+        for (int64_t o = o0; o < o1; o++)
+            c->gout[o] = c->vnni ? gguf_dot_row_avx512(c->gtype, c->gblocks + o * c->growbytes, c->gcols, c->gx)
+                                 : orc_gguf_dot_row(c->gtype, c->gblocks + o * c->growbytes, c->gcols, c->gx);
+        team_wait(&c->bar);
+    }
 }
 
 typedef struct {
@@ -2008,4 +2242,86 @@ double orc_cpu_head_seconds(orc_gpt2 *m, int nt, int reps) {
     const double med = t[reps / 2];
     free(t);
     return med;
+}
+
+static double median_of(double *t, int n) {
+    for (int i = 1; i < n; i++)
+        for (int j = i; j > 0 && t[j] < t[j - 1]; j--) {
+            const double x = t[j];
+            t[j] = t[j - 1];
+            t[j - 1] = x;
+        }
+    return t[n / 2];
+}
+
+/* linear_team (kernels.mojo:774-866) of one token on a team of nt: the
+ * median seconds of `reps` calls cycling over the nrot matrices ws (copies
+ * of one, so that their codes come from memory rather than cache), x and
+ * out of ws[0]'s shape.  -1 on a bad argument. */
+double orc_cpu_gemv_seconds(const orc_qm *const *ws, int nrot, const float *x, float *out, int nt, int reps) {
+    if (reps < 1 || reps > 100000 || nrot < 1 || !ws || !x || !out) return -1.0;
+    if (ws[0]->k > 4 * G_C) return -1.0; /* the team's activation buffers */
+    orc_team_threads *T = team_start(NULL, nt);
+    if (!T) return -1.0;
+    double *t = (double *)malloc(sizeof(double) * (size_t)reps);
+    T->c->gx = x;
+    T->c->gout = out;
+    for (int r = -2; r < reps; r++) {
+        T->c->gw = ws[(r + 2) % nrot];
+        const double a = now_s();
+        team_run(T->c, 2);
+        if (r >= 0) t[r] = now_s() - a;
+    }
+    team_stop(T);
+    const double med = median_of(t, reps);
+    free(t);
+    return med;
+}
+
+/* GGUFMatrix.dot_row over every row (linear_team's OUT_MAJOR branch) of a
+ * rows x cols matrix of ggml type t on a team of nt: the median seconds of
+ * `reps` calls cycling over the nrot copies blocks[i].  -1 on a bad argument. */
+double orc_cpu_gguf_gemv_seconds(int t, const uint8_t *const *blocks, int nrot, int64_t rows, int64_t cols,
+                                 const float *x, float *out, int nt, int reps) {
+    const int bs = orc_gguf_block_size(t), bb = orc_gguf_block_bytes(t);
+    if (reps < 1 || reps > 100000 || nrot < 1 || !blocks || bs < 32 || cols % bs) return -1.0;
+    orc_team_threads *T = team_start(NULL, nt);
+    if (!T) return -1.0;
+    double *tt = (double *)malloc(sizeof(double) * (size_t)reps);
+    T->c->gtype = t;
+    T->c->grows = rows;
+    T->c->gcols = cols;
+    T->c->growbytes = cols / bs * bb;
+    T->c->gx = x;
+    T->c->gout = out;
+    for (int r = -2; r < reps; r++) {
+        T->c->gblocks = blocks[(r + 2) % nrot];
+        const double a = now_s();
+        team_run(T->c, 3);
+        if (r >= 0) tt[r] = now_s() - a;
+    }
+    team_stop(T);
+    const double med = median_of(tt, reps);
+    free(tt);
+    return med;
+}
+
+/* Model.forward of a T-token prompt from position 0 (gpt2t.mojo:329-342) with
+ * the matmuls on VPDPWSSD tiles and the attention, quantizer and one-token
+ * head on their AVX-512 forms (orc_cpu_set_fast), parallel over g_threads =
+ * nt OpenMP threads as the reference's parallelize is over its tasks; the
+ * logits are the scalar oracle's bit for bit.  secs[0] = wall time.  Returns
+ * the logits (the model's buffer), NULL on a bad argument. */
+const float *orc_cpu_prompt(orc_gpt2 *m, const int64_t *tokens, int T, int nt, double *secs) {
+    if (!m || !tokens || T < 1 || T > G_MAXT || nt < 1 || nt > 256) return NULL;
+    const int saved = g_threads;
+    g_threads = nt;
+    orc_cpu_set_fast(1);
+    const double t0 = now_s();
+    const float *lg = orc_gpt2_forward(m, tokens, T, 0);
+    const double t1 = now_s();
+    orc_cpu_set_fast(0);
+    g_threads = saved;
+    if (secs) secs[0] = t1 - t0;
+    return lg;
 }

@@ -234,12 +234,16 @@ def gemv_micro(torch, lm, ctx, reps=200, rot_bytes=320 << 20):
             x = torch.randn((1, K), device="cuda", generator=g)
             out = torch.empty((1, N), device="cuda")
             alg = nb + 2 * K + 4 * N
+            torch.cuda.nvtx.range_push(f"c1 {name} llc")  # (a marker range for kernel traces)
             us = timed(lambda i: lm.linear(ctx, out, x, w), 1)
+            torch.cuda.nvtx.range_pop()
             if name == "warm-up":
                 w.free()
                 continue
             ws = [w] + [lm.HipQuantMatrix.from_f32(ctx, src, bits, group, False, True) for _ in range(nrot - 1)]
+            torch.cuda.nvtx.range_push(f"c1 {name} hbm")
             us_hbm = timed(lambda i: lm.linear(ctx, out, x, ws[i % nrot]), nrot)
+            torch.cuda.nvtx.range_pop()
             for m in ws:
                 m.free()
             llc_floor = min(read_floor(torch, lm, ctx, stream, nb, 1, grid=gr, reps=64, graph=True)
@@ -407,6 +411,41 @@ def gguf_sweep(torch, lm, synth, ctx, rot_bytes=512 << 20):
 LLAMA_PROMPT, LLAMA_GEN, LLAMA_SEED = 1024, 128, 4004
 
 
+def llama_kernels(torch, lm, synth, ctx, nbuf=8, reps=40):
+    """Config 4's matrix kernels called directly through the C ABI (for
+    counter passes): the Q6_K 32000 x 2048 int16 head at 1 and 16 tokens,
+    and the Q4_K gate / up matrix (11264 x 2048) at 1, 16 and 1024 tokens
+    (one-token GEMV; fp16 matrix-core matmul over its activation record;
+    the LDS-staged form for 64+ tokens), each over nbuf rotated copies."""
+    cfg = lm.TINYLLAMA
+    res = {}
+    stream = torch.cuda.Stream()
+    for name, t, N, K, Ts in (("head Q6_K", 14, cfg["vocab"], cfg["dim"], (1, 16)),
+                              ("gate/up Q4_K", 12, 2 * cfg["ffn"], cfg["dim"], (1, 16, 1024))):
+        base = synth.gguf_blocks(t, N, K, seed=5, scale=2e-5 if t == 14 else 1e-4)
+        mats = [lm.HipGGUFMatrix.from_blocks(ctx, t, base, N, K) for _ in range(nbuf)]
+        with torch.cuda.stream(stream):
+            ctx.set_stream(stream)
+            for T in Ts:
+                x = torch.randn((T, K), device="cuda")
+                out = torch.empty((T, N), device="cuda")
+                fn = (lambda i: lm.head(ctx, out, x, mats[i % nbuf])) if t == 14 else \
+                     (lambda i: lm.linear(ctx, out, x, mats[i % nbuf]))
+                for i in range(nbuf):
+                    fn(i)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for i in range(reps):
+                    fn(i)
+                e1.record(stream)
+                e1.synchronize()
+                res[f"{name} T={T}"] = round(e0.elapsed_time(e1) * 1000.0 / reps, 2)
+        ctx.set_stream(None)
+        for m in mats:
+            m.free()
+    return res
+
+
 def llama_decode(lm, synth, ctx):
     """Config 4: the TinyLlama-shaped decoder (Q4_K layers, Q6_K head, int8
     KV cache) with seeded random weights; a 1024-token random prompt per
@@ -570,6 +609,14 @@ def main():
     ap.add_argument("--no-read-sweep", action="store_true", help="skip the pure-read size sweep")
     ap.add_argument("--micro-only", action="store_true",
                     help="only config 1's GEMVs and the read sweep (for rocprofv3 runs)")
+    ap.add_argument("--gguf-only", action="store_true",
+                    help="only config 2's GGUF GEMV sweep and the 1 GiB reference copy (for rocprofv3 runs)")
+    ap.add_argument("--llama-only", action="store_true",
+                    help="only config 4's decoder and the 1 GiB reference copy (for rocprofv3 runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only config 3's 476-token prompts and layer GEMMs (for rocprofv3 runs)")
+    ap.add_argument("--llama-kernels", action="store_true",
+                    help="only config 4's head and gate/up kernels through the C ABI, and the 1 GiB reference copy")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline GEMV and the reference copy (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -590,6 +637,17 @@ def main():
         r = gemv_roofline(torch, lm, ctx)
         print(json.dumps({"roofline_kernel": r, "copy_gbs": round(copy_bandwidth(torch), 1)}), flush=True)
         return
+    if args.gguf_only or args.llama_only or args.llama_kernels:
+        ctx = lm.Context(0)
+        out = {"copy_gbs": round(copy_bandwidth(torch), 1)}
+        if args.llama_kernels:
+            out["llama_kernels_us"] = llama_kernels(torch, lm, synth, ctx)
+        if args.gguf_only:
+            out["gguf_gemv_sweep"] = gguf_sweep(torch, lm, synth, ctx)
+        if args.llama_only:
+            out["tinyllama_q4k_q6k"] = llama_decode(lm, synth, ctx)
+        print(json.dumps(out), flush=True)
+        return
     if args.micro_only:
         ctx = lm.Context(0)
         out = {"gemv_micro_llc": gemv_micro(torch, lm, ctx)}
@@ -602,6 +660,9 @@ def main():
     prompt = synth.prompt_ids(SEED, PROMPT)
     ctx = lm.Context(0)
     model = lm.GPT2(ctx, tensors)
+    if args.prefill_only:
+        print(json.dumps({"prefill_476": prefill(torch, lm, synth, ctx, tensors, model)}), flush=True)
+        return
     log("model", model.name(), "weight bytes", model.weight_bytes())
 
     for _ in range(args.warmup):

@@ -659,13 +659,16 @@ Plan make_plan(const llmq_mat *w) {
     p.tmax = (int)((w->ntiles + grid - 1) / grid);
     p.spw = (p.tmax * S + nw - 1) / nw;
     p.steps = steps_for(p.spw);
-    // Two code steps in flight a wave, the next issued as each is consumed,
-    // for 16-wave plans and matrices of 8 MB or more (fewer bytes queued
-    // ahead of the activation row's fetch: config 4's down 6.90 -> 6.75 us,
-    // gate / up 6.70 -> 6.62 us); every step up front for the small ones
-    // (qkv-sized: 4.18 against 4.33 us).  LLMQ_GGUF1_WIN=2 forces the
-    // window, any other value every step up front.
-    p.win = (nw == 16 || bytes >= (8ll << 20)) ? kStreamWin : p.steps;
+    // Two code steps in flight a wave, the next issued as each is consumed
+    // (fewer bytes queued ahead of the activation row's fetch), where it
+    // measured faster: 4-wave plans of 8 MB or more (config 4's gate / up
+    // 6.70 -> 6.62 us), 16-wave plans from 20 MB and below 8 MB (long rows of
+    // few tiles: config 4's down 6.90 -> 6.75 us); every step up front
+    // otherwise (qkv-sized matrices: 4.18 against 4.33 us; Q8_0 4096 x 4096
+    // 7.64 against 8.24 us).  LLMQ_GGUF1_WIN=2 forces the window, any other
+    // value every step up front.
+    const bool win2 = nw == 16 ? (bytes >= kStreamBytes || bytes < (8ll << 20)) : bytes >= (8ll << 20);
+    p.win = win2 ? kStreamWin : p.steps;
     if (const char *e = getenv("LLMQ_GGUF1_WIN")) p.win = atoi(e) == kStreamWin ? kStreamWin : p.steps;
     if (p.win > p.steps) p.win = p.steps;
     return p;

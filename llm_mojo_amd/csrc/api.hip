@@ -490,9 +490,10 @@ int llmq_linear_noalloc(llmq_ctx *ctx, float *out, const float *x, const llmq_ma
         if (T == 1) return launch_gguf_gemv(ctx, w, x, out, bias, flags, nullptr, 0);
         return launch_gguf_gemm(ctx, w, x, IN, T, out, OUT, bias, flags, ctx->scratch, LLMQ_NOALLOC_SCRATCH_BYTES);
     }
-    // the most the int16 prompt GEMM keeps there: T x IN int16 codes
-    // (rounded up to 256 bytes) and T float scales
-    const int64_t need = ((T * IN * 2 + 255) & ~(int64_t)255) + T * 4;
+    // the least the prompt GEMM keeps there: T x IN int16 codes and T float
+    // scales, each rounded up to 256 bytes (int4-g32 matrices also put their
+    // fp16 planes there when they fit, else take the int8-MFMA form)
+    const int64_t need = ((T * IN * 2 + 255) & ~(int64_t)255) + ((T * 4 + 255) & ~(int64_t)255);
     LLMQ_REQUIRE(need <= (int64_t)LLMQ_NOALLOC_SCRATCH_BYTES,
                  "linear_noalloc: %lld tokens x %lld inputs need %lld bytes of scratch, the maximum is %d",
                  (long long)T, (long long)IN, (long long)need, LLMQ_NOALLOC_SCRATCH_BYTES);

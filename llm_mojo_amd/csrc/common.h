@@ -244,9 +244,13 @@ int gemv_a16_num_parts(const llmq_mat *w, bool ln);
 // The T == 1 kernel (gemv1.hip) behind launch_gemv_a16.
 bool gemv1_supports(const llmq_mat *w, bool ln);
 // The prompt-side int8-MFMA GEMM (gemm_mfma.hip): xq / sx are T x K int16
-// codes and T scales of workspace.
+// codes and T scales of workspace; with `planes` (gemm_f16_planes_bytes of
+// workspace, for matrices gemm_f16_supports takes: int4 in groups of 32)
+// the codes also go there as fp16 planes and the fp16 matrix-core form runs.
 bool gemm_mfma_supports(const llmq_mat *w, int64_t T);
-int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *sx);
+bool gemm_f16_supports(const llmq_mat *w, int64_t T);
+size_t gemm_f16_planes_bytes(const llmq_mat *w, int64_t T);
+int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *sx, uint8_t *planes);
 int launch_gemv1(llmq_ctx *ctx, const GemvRequest &rq);
 int gemv1_num_parts(const llmq_mat *w, bool ln);
 // One-token kernels in the reference's float order (gemv_exact.hip) for

@@ -40,6 +40,10 @@
 // instructions (per-workgroup timestamps), and prefetching four blocks
 // ahead instead of two does not shorten it.
 //
+// int4 weights in groups of 32 take gemm_f16_kernel instead (below): the
+// same G on the fp16 matrix cores, exact in their fp32 sums, so the flush is
+// one fma per output and group.
+//
 // Activations come from act_q16_kernel: LayerNorm (kernels.mojo:179-197) when
 // asked, then quantize_rows (kernels.mojo:400-416), one workgroup per token.
 #include "common.h"
@@ -87,12 +91,38 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
     return is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : ((red[0] + red[1]) + red[2]) + red[3];
 }
 
+// The fp16 planes of int16 codes q (gemm_f16_kernel's A operand): q =
+// 256 hi + lo with hi = q >> 8 and lo = q & 255, as fp16 values 256 hi and
+// lo (both exact).  Layout for T tokens (padded to T16) and CK chunks of 32
+// inputs, the 16 tokens of a token tile side by side so that a wave's
+// operand load is 1 KB in one piece:
+//     fp16 [T16 / 16][CK][hi, lo][4 groups][16 tokens][8]
+// group g holding inputs 8 g .. 8 g + 7 of the chunk in the order 0, 2, 4,
+// 6, 1, 3, 5, 7 (the order in which a code dword's nibbles decode).
+__device__ __forceinline__ uint32_t f16_pair(int a, int b) {
+    const _Float16 ha = (_Float16)(float)a, hb = (_Float16)(float)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+// Unit u (inputs 4 u .. 4 u + 3) of token t: slots (2 h, 2 h + 1) take
+// inputs 0 and 2 of the unit, slots (4 + 2 h, 5 + 2 h) inputs 1 and 3
+// (h = u & 1, the unit's half of its group of 8).
+__device__ __forceinline__ void store_planes(uint8_t *planes, int CK, int t, int u, int q0, int q1, int q2, int q3) {
+    const int c = u >> 3, g = (u & 7) >> 1, h = u & 1;
+    uint32_t *p = reinterpret_cast<uint32_t *>(planes + ((int64_t)(t >> 4) * CK + c) * 2048 + (g * 16 + (t & 15)) * 16);
+    p[h] = f16_pair(q0 & ~255, q2 & ~255);
+    p[2 + h] = f16_pair(q1 & ~255, q3 & ~255);
+    p[256 + h] = f16_pair(q0 & 255, q2 & 255);
+    p[258 + h] = f16_pair(q1 & 255, q3 & 255);
+}
+
 // One workgroup (256 threads) per token row: optional LayerNorm, then
 // quantize_rows.  Values are held in registers, 4 per unit of a float4.
+// With `planes` set, the codes are also written there as fp16 planes.
 template <bool LN, int UPT>
 __global__ __launch_bounds__(256) void act_q16_kernel(const float *__restrict__ x, int64_t ldx,
                                                       const float *__restrict__ lw, const float *__restrict__ lb,
-                                                      int K, int16_t *__restrict__ xq, float *__restrict__ sx) {
+                                                      int K, int16_t *__restrict__ xq, float *__restrict__ sx,
+                                                      uint8_t *__restrict__ planes) {
     __shared__ float red[4], bc[2];
     extern __shared__ __align__(16) float xs[];  // [K] with LayerNorm
     const int t = blockIdx.x, tid = threadIdx.x, nunits = K / 4;
@@ -142,6 +172,8 @@ __global__ __launch_bounds__(256) void act_q16_kernel(const float *__restrict__ 
         const uint32_t lo = ((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16);
         const uint32_t hi = ((uint32_t)q2 & 0xFFFFu) | ((uint32_t)q3 << 16);
         reinterpret_cast<uint2 *>(xq + (int64_t)t * K)[u] = make_uint2(lo, hi);
+        if (planes)  // from the stored int16 codes
+            store_planes(planes, K / 32, t, u, (int16_t)q0, (int16_t)q1, (int16_t)q2, (int16_t)q3);
     }
 }
 
@@ -456,6 +488,227 @@ __global__ __launch_bounds__(64) void rows_i16_kernel(MfArgs a, int bits, int o0
     *dst = v;
 }
 
+// ------------------------------------------------------- int4-g32 on fp16
+//
+// tile_i16 for int4 weights in groups of 32 (a segment is a group): per
+// token t, output row o and group g,
+//     G = sum_{k in g} q[t, k] (u[o, k] - zp[o, g]),   acc = fma(float(G), scale[o, g], acc)
+// with q = 256 hi + lo from the fp16 planes and w = u - zp (|w| <= 15)
+// decoded to fp16, the matrix cores (v_mfma_f32_16x16x32_f16, fp32 sums)
+// form sum (256 hi) w + sum lo w.  Every product is an integer of magnitude
+// <= 32768 * 15, and every partial sum is bounded by 32 * (32768 + 255) * 15
+// < 2^24, so each intermediate value is exact and the result is G itself:
+// the float the reference converts G to (exactly, as |G| < 2^24).  The
+// flush is then one fma per output and group.
+//
+// Mapping: a workgroup of NW waves owns MT token tiles of 16 tokens and
+// NW NR row tiles of 16 rows (wave w: row tiles w NR ..) and walks the K / 32
+// groups in steps of S.  Per step it copies, with the global-to-LDS loads
+// (16 bytes a lane), the token tiles' planes (MT S 2 KB), the row tiles'
+// code blocks (NW NR S 256 B), zero points and scales into one of two LDS
+// buffers while the waves compute the previous step from the other: one
+// barrier a step.  Per group lane l of a wave reads, for each token tile, 16
+// bytes of each plane (token l % 16, inputs 8 (l / 16) ..) and, for each row
+// tile, the code dword of row l % 16 and inputs 8 (l / 16) .. with that
+// row's zero point and scale; it then holds outputs (tokens 4 (l / 16) + i,
+// row l % 16).  Workgroups go to the XCDs in an order that keeps the ones
+// sharing a token block's planes on one XCD.  At 476 tokens this runs the
+// GPT-2 layer GEMMs in 12-13 us (qkv, fc, proj, fcproj), against 15-19 us for
+// the int8-MFMA form: the planes are read once a workgroup instead of once a
+// wave (a form loading them per wave took 15-18 us), and register-staged
+// copies measured slower than the global-to-LDS ones.
+struct F16Args {
+    const uint8_t *planes, *codes, *zps;
+    const uint16_t *scales;
+    const float *sx, *bias;
+    float *out;
+    int64_t ldo;
+    int T, n, ntiles, CK, flags;
+    int xcd;  // XCD-aware workgroup order
+};
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// 1024 + the 8 bytes of (a, b) as fp16 pairs (a0, a1), (a2, a3), (b0, b1),
+// (b2, b3): 0x6400 | n is 1024 + n in fp16 for n < 1024.
+__device__ __forceinline__ void bytes_f16(uint32_t a, uint32_t b, uint32_t (&d)[4]) {
+    d[0] = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
+    d[1] = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
+    d[2] = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+    d[3] = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+}
+
+// Bytes of one staged step.
+template <int MT, int NR, int S, int NW>
+struct F16Lds {
+    static constexpr int A = MT * S * 2048, C = NW * NR * S * 256, Z = NW * NR * S * 16, SC = NW * NR * S * 32;
+    static constexpr int BYTES = A + C + Z + SC;
+};
+
+template <int MT, int NR, int S, int NW>
+__global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
+    using LY = F16Lds<MT, NR, S, NW>;
+    constexpr int RB = NW * 1024;  // bytes a copy round: 16 a lane
+    // separate arrays, so that the compiler sees a copy into one cannot alias reads of the other
+    __shared__ __align__(16) uint8_t b0[LY::BYTES], b1[LY::BYTES];
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c16 = lane & 15, g = lane >> 4;
+    // Workgroups go to the 8 XCDs in turn (linear id mod 8); each XCD gets
+    // a contiguous run of (token block, row block) pairs in token-block
+    // order, so that the workgroups sharing a token block's planes share an
+    // L2.
+    int bx = blockIdx.x, by = blockIdx.y;
+    if (a.xcd) {
+        const int nb = gridDim.x * gridDim.y, L = blockIdx.y * gridDim.x + blockIdx.x;
+        const int x = L & 7, q = nb >> 3, rem = nb & 7;
+        const int pos = x * q + min(x, rem) + (L >> 3);
+        bx = pos % gridDim.x;
+        by = pos / gridDim.x;
+    }
+    const int rt0 = bx * NW * NR, tt0 = by * MT, ttiles = (a.T + 15) >> 4;
+    const int tile0 = rt0 + w * NR;  // this wave's row tiles
+    const int NG = a.CK;             // groups of 32: one scale and zero point a chunk
+    // Copy of step s (groups s S ..) into buf, region by region: lane i of
+    // wave w brings the 16 bytes at offset q RB + 1024 w + 16 i of the
+    // region (the global-to-LDS load writes a wave's 64 x 16 bytes to
+    // consecutive LDS).  A token tile past the planes or a row tile past the
+    // matrix copies tile 0 instead (its outputs are not stored).
+    auto stage = [&](int s, uint8_t *buf) {
+        const int c0 = s * S;
+#pragma unroll
+        for (int q = 0; q < (LY::A + RB - 1) / RB; q++) {
+            const int x = q * RB + tid * 16;
+            if (x < LY::A) {
+                const int j = x / (S * 2048), tt = tt0 + j < ttiles ? tt0 + j : 0;
+                __builtin_amdgcn_global_load_lds(a.planes + ((int64_t)tt * a.CK + c0) * 2048 + x % (S * 2048),
+                                                 (__attribute__((address_space(3))) void *)(buf + q * RB + w * 1024), 16, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < (LY::C + RB - 1) / RB; q++) {
+            const int x = q * RB + tid * 16;
+            if (x < LY::C) {
+                const int r = x / (S * 256), tile = rt0 + r < a.ntiles ? rt0 + r : 0;
+                __builtin_amdgcn_global_load_lds(a.codes + ((int64_t)tile * a.CK + c0) * 256 + x % (S * 256),
+                                                 (__attribute__((address_space(3))) void *)(buf + LY::A + q * RB + w * 1024), 16, 0,
+                                                 0);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < (LY::Z + LY::SC + RB - 1) / RB; q++) {  // zero points, then scales
+            const int x = q * RB + tid * 16;
+            if (x < LY::Z + LY::SC) {
+                const uint8_t *src;
+                if (x < LY::Z) {
+                    const int r = x / (S * 16), tile = rt0 + r < a.ntiles ? rt0 + r : 0;
+                    src = a.zps + ((int64_t)tile * NG + c0) * 16 + x % (S * 16);
+                } else {
+                    const int y = x - LY::Z, r = y / (S * 32), tile = rt0 + r < a.ntiles ? rt0 + r : 0;
+                    src = reinterpret_cast<const uint8_t *>(a.scales) + ((int64_t)tile * NG + c0) * 32 + y % (S * 32);
+                }
+                __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(buf + LY::A + LY::C + q * RB + w * 1024),
+                                                 16, 0, 0);
+            }
+        }
+    };
+    // the epilogue's token scales and biases, loaded first
+    float sxr[MT][4], bor[NR];
+#pragma unroll
+    for (int j = 0; j < MT; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tok = (tt0 + j) * 16 + 4 * g + i;
+            sxr[j][i] = tok < a.T ? a.sx[tok] : 0.0f;
+        }
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int o = (tile0 + r) * 16 + c16;
+        bor[r] = (a.flags & LLMQ_BIAS) && o < a.n ? a.bias[o] : 0.0f;
+    }
+    float acc[MT][NR][4];
+#pragma unroll
+    for (int j = 0; j < MT; j++)
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[j][r][i] = 0.0f;
+    // The S groups of a staged step.
+    auto compute = [&](const uint8_t *cur) {
+#pragma unroll
+        for (int gi = 0; gi < S; gi++) {
+            uint4 ah[MT], al[MT];
+#pragma unroll
+            for (int j = 0; j < MT; j++) {
+                ah[j] = *reinterpret_cast<const uint4 *>(cur + (j * S + gi) * 2048 + lane * 16);
+                al[j] = *reinterpret_cast<const uint4 *>(cur + (j * S + gi) * 2048 + 1024 + lane * 16);
+            }
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const int e = (w * NR + r) * S + gi;  // (row tile of the workgroup, group) entry
+                const uint32_t cw = *reinterpret_cast<const uint32_t *>(cur + LY::A + e * 256 + c16 * 16 + g * 4);
+                const uint32_t zp = cur[LY::A + LY::C + e * 16 + c16];
+                const float sc = __half2float(
+                    *reinterpret_cast<const __half *>(cur + LY::A + LY::C + LY::Z + e * 32 + c16 * 2));
+                // w = u - zp in fp16: (1024 + u) - (1024 + zp), both exact; inputs 0 2 4 6 1 3 5 7
+                const uint32_t z2 = zp * 0x10001u + 0x64006400u;
+                uint32_t q4[4];
+                bytes_f16(cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, q4);
+                v8h b;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const v2h p = __builtin_bit_cast(v2h, q4[i]) - __builtin_bit_cast(v2h, z2);
+                    b[2 * i] = p[0];
+                    b[2 * i + 1] = p[1];
+                }
+#pragma unroll
+                for (int j = 0; j < MT; j++) {
+                    const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    v4f d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah[j]), b, z, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al[j]), b, d, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[j][r][i] = fmaf(d[i], sc, acc[j][r][i]);  // tile_i16's flush
+                }
+            }
+        }
+    };
+    const int nsteps = a.CK / S;  // (the launcher picks S dividing the number of groups)
+    stage(0, b0);
+    for (int s = 0; s < nsteps; s += 2) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies have landed
+        __syncthreads();                     // every wave's copy of step s is in; b1 is free
+        if (s + 1 < nsteps) stage(s + 1, b1);
+        compute(b0);
+        if (s + 1 >= nsteps) break;
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (s + 2 < nsteps) stage(s + 2, b0);
+        compute(b1);
+    }
+    // Epilogue (store_out): tile_i16's acc * sx + b, then GELU / residual.
+    if (tile0 * 16 >= a.n) return;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int o = (tile0 + r) * 16 + c16;
+        if (o >= a.n) continue;
+#pragma unroll
+        for (int j = 0; j < MT; j++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tok = (tt0 + j) * 16 + 4 * g + i;
+                if (tok >= a.T) continue;
+                float v = acc[j][r][i] * sxr[j][i];
+                if (a.flags & LLMQ_BIAS) v += bor[r];
+                if (a.flags & LLMQ_GELU) v = gelu_ref(v);
+                float *dst = a.out + (int64_t)tok * a.ldo + o;
+                if (a.flags & LLMQ_RESID) v += *dst;
+                *dst = v;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 bool gemm_mfma_supports(const llmq_mat *w, int64_t T) {
@@ -465,15 +718,24 @@ bool gemm_mfma_supports(const llmq_mat *w, int64_t T) {
            (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 256 < (int64_t)kOOB && T * w->k * 2 < (int64_t)kOOB;
 }
 
-int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *sx) {
+bool gemm_f16_supports(const llmq_mat *w, int64_t T) {
+    if (const char *e = getenv("LLMQ_MFMA_F16"))
+        if (atoi(e) == 0) return false;
+    return gemm_mfma_supports(w, T) && w->bits == 4 && w->group == 32 && (T + 15) / 16 * 16 * w->k * 4 < (int64_t)kOOB;
+}
+
+size_t gemm_f16_planes_bytes(const llmq_mat *w, int64_t T) { return (size_t)((T + 15) / 16 * 16) * w->k * 4; }
+
+int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *sx, uint8_t *planes) {
     const llmq_mat *w = rq.w;
     const int64_t T = rq.T, K = w->k;
     const int64_t ldx = rq.ldx ? rq.ldx : K;
     LLMQ_REQUIRE(gemm_mfma_supports(w, T), "linear: no MFMA GEMM for this matrix");
+    LLMQ_REQUIRE(!planes || gemm_f16_supports(w, T), "linear: fp16 planes given for a matrix the fp16 GEMM does not take");
     const int upt = (int)((K / 4 + 255) / 256);
     const bool ln = rq.ln_w != nullptr;
 #define ACTQ(L, U) hipLaunchKernelGGL((act_q16_kernel<L, U>), dim3((unsigned)T), dim3(256), L ? K * 4 : 0, ctx->stream, rq.x, ldx, \
-                                       rq.ln_w, rq.ln_b, (int)K, xq, sx)
+                                       rq.ln_w, rq.ln_b, (int)K, xq, sx, planes)
     if (upt <= 1) {
         if (ln) ACTQ(true, 1); else ACTQ(false, 1);
     } else if (upt <= 4) {
@@ -485,6 +747,50 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     }
 #undef ACTQ
     LLMQ_HIP(hipGetLastError());
+    // the 32-row tiles; the rest (n % 32 rows: the vocabulary's last 17)
+    // go through rows_i16 below
+    const int full = (int)(w->n / 32 * 32);
+    if (planes && full > 0) {
+        F16Args f;
+        f.planes = planes;
+        f.codes = w->codes;
+        f.zps = w->zps;
+        f.scales = w->scales;
+        f.sx = sx;
+        f.bias = rq.bias ? rq.bias : rq.out;
+        f.out = rq.out;
+        f.ldo = rq.ldo ? rq.ldo : w->n;
+        f.T = (int)T;
+        f.n = full;
+        f.ntiles = (int)w->ntiles;
+        f.CK = (int)w->CK;
+        f.flags = rq.flags;
+        f.xcd = 1;
+        if (const char *e = getenv("LLMQ_F16_XCD")) f.xcd = atoi(e) != 0;
+        // a workgroup's tile: MT token tiles x NW NR row tiles, S groups a
+        // step (S divides the number of groups); LLMQ_F16_TILE=MT,NR,S[,NW]
+        // picks another instantiation, for measurement
+        int mt = 1, nr = 1, st = 4, nw = 4;
+        if (const char *e = getenv("LLMQ_F16_TILE")) {
+            int x = 0, y = 0, z = 0, v = 4;
+            if (sscanf(e, "%d,%d,%d,%d", &x, &y, &z, &v) >= 3) mt = x, nr = y, st = z, nw = v;
+        }
+        if (w->CK % st != 0) mt = 1, nr = 1, nw = 4, st = w->CK % 2 == 0 ? 2 : 1;
+        const int rtiles = full / 16, ttiles = (int)((T + 15) / 16);
+        bool ok = false;
+#define F16K(M, R, SS, NW)                                                                                          \
+    if (!ok && mt == M && nr == R && st == SS && nw == NW) {                                                         \
+        hipLaunchKernelGGL((gemm_f16_kernel<M, R, SS, NW>),                                                           \
+                           dim3((unsigned)((rtiles + NW * R - 1) / (NW * R)), (unsigned)((ttiles + M - 1) / M)),       \
+                           dim3(NW * 64), 0, ctx->stream, f);                                                        \
+        ok = true;                                                                                                   \
+    }
+        F16K(1, 1, 4, 4) F16K(1, 1, 2, 4) F16K(1, 1, 1, 4) F16K(2, 1, 4, 4) F16K(1, 2, 4, 4) F16K(1, 1, 8, 4)
+        F16K(1, 1, 4, 8) F16K(2, 1, 4, 8) F16K(1, 1, 8, 8)
+#undef F16K
+        LLMQ_REQUIRE(ok, "linear: no fp16 GEMM instantiation for LLMQ_F16_TILE=%d,%d,%d,%d", mt, nr, st, nw);
+        LLMQ_HIP(hipGetLastError());
+    }
     MfArgs a;
     a.xq = xq;
     a.sx = sx;
@@ -500,9 +806,6 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     a.zps_bytes = (uint32_t)((w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * LLMQ_TILE_ROWS);
     a.T = (int)T;
     a.K = (int)K;
-    // the 32-row tiles; the rest (n % 32 rows: the vocabulary's last 17)
-    // go through rows_i16 below
-    const int full = (int)(w->n / 32 * 32);
     a.n = full;
     a.ntiles = (int)w->ntiles;
     a.CK = (int)w->CK;
@@ -524,7 +827,7 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
         else if (mt == 2) GK(B, S, 2);   \
         else GK(B, S, 4);                \
     } while (0)
-    if (full > 0) {
+    if (full > 0 && !planes) {
         if (w->bits == 4) {
             if (seg32) GKM(4, true); else GKM(4, false);
         } else {

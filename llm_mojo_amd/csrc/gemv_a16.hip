@@ -497,17 +497,25 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
         int min_t = exact_order() ? 2 : 8;
         if (const char *e = getenv("LLMQ_MFMA_MIN_T")) min_t = atoi(e);
         if (rq.T >= min_t && min_t > 0 && gemm_mfma_supports(w, rq.T)) {
+            // workspace: int16 codes, token scales, then (int4-g32) the fp16
+            // planes; a caller-given workspace too small for the planes runs
+            // the int8-MFMA form, whose results are the same bits
             const size_t xb = ((size_t)rq.T * w->k * 2 + 255) & ~(size_t)255;
-            const size_t need = xb + (size_t)rq.T * 4;
+            const size_t sb = ((size_t)rq.T * 4 + 255) & ~(size_t)255;
+            const size_t need = xb + sb;
+            const size_t need16 = gemm_f16_supports(w, rq.T) ? need + gemm_f16_planes_bytes(w, rq.T) : 0;
             void *ws = rq.ws;
+            bool f16 = need16 > 0;
             if (ws) {
                 LLMQ_REQUIRE(need <= rq.ws_cap, "linear: %lld tokens x %lld inputs need %zu bytes of workspace, %zu given",
                              (long long)rq.T, (long long)w->k, need, rq.ws_cap);
+                f16 = f16 && need16 <= rq.ws_cap;
             } else {
-                RC(ctx_workspace(ctx, need, &ws));
+                RC(ctx_workspace(ctx, f16 ? need16 : need, &ws));
             }
-            return launch_gemm_mfma(ctx, rq, reinterpret_cast<int16_t *>(ws),
-                                    reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ws) + xb));
+            uint8_t *base = reinterpret_cast<uint8_t *>(ws);
+            return launch_gemm_mfma(ctx, rq, reinterpret_cast<int16_t *>(base), reinterpret_cast<float *>(base + xb),
+                                    f16 ? base + need : nullptr);
         }
     }
     const size_t max_lds = 64 * 1024;

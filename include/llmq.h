@@ -181,8 +181,11 @@ LLMQ_API int llmq_linear(llmq_ctx *ctx, float *out, const float *x, const llmq_m
  * per-GPU scratch array of LLMQ_NOALLOC_SCRATCH_BYTES that each GPU the
  * library runs on holds until the process ends.  It calls no hipMalloc /
  * hipFree.  Sizes needing more scratch than that (a16: T x IN x 2 bytes
- * rounded up to 256, plus T x 4; Q4_K: the record's ~4.4 x T x IN bytes,
- * T rounded up to 16) return LLMQ_EINVAL; other formats use no scratch.
+ * and T x 4, each rounded up to 256; Q4_K: the record's ~4.4 x T x IN
+ * bytes, T rounded up to 16) return LLMQ_EINVAL; other formats use no
+ * scratch.  An int4-g32 a16 matrix also puts its prompt GEMM's fp16
+ * activation planes there (T x IN x 4 bytes, T rounded up to 16) when they
+ * fit, else runs the int8-MFMA form of the same GEMM (the same bits).
  * Every call on one GPU shares the array: calls that overlap in time on one
  * GPU (different streams or threads) race; calls ordered on one stream do
  * not.  Nothing in the scratch needs to start at zero (each call writes all

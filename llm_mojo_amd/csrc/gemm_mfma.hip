@@ -103,16 +103,24 @@ __device__ __forceinline__ uint32_t f16_pair(int a, int b) {
     const _Float16 ha = (_Float16)(float)a, hb = (_Float16)(float)b;
     return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
 }
-// Unit u (inputs 4 u .. 4 u + 3) of token t: slots (2 h, 2 h + 1) take
-// inputs 0 and 2 of the unit, slots (4 + 2 h, 5 + 2 h) inputs 1 and 3
-// (h = u & 1, the unit's half of its group of 8).
+// Unit u (inputs 4 u .. 4 u + 3) of token t, held by a lane whose
+// neighbour (lane ^ 1) holds unit u ^ 1, the other half of the same group of
+// 8 inputs: the pair swaps codes, then the even lane stores the group's 16
+// bytes of the hi plane and the odd lane those of the lo plane.  Both lanes
+// of a pair call this together (K is a multiple of 32).
 __device__ __forceinline__ void store_planes(uint8_t *planes, int CK, int t, int u, int q0, int q1, int q2, int q3) {
     const int c = u >> 3, g = (u & 7) >> 1, h = u & 1;
-    uint32_t *p = reinterpret_cast<uint32_t *>(planes + ((int64_t)(t >> 4) * CK + c) * 2048 + (g * 16 + (t & 15)) * 16);
-    p[h] = f16_pair(q0 & ~255, q2 & ~255);
-    p[2 + h] = f16_pair(q1 & ~255, q3 & ~255);
-    p[256 + h] = f16_pair(q0 & 255, q2 & 255);
-    p[258 + h] = f16_pair(q1 & 255, q3 & 255);
+    const int p0 = __shfl_xor(q0, 1), p1 = __shfl_xor(q1, 1), p2 = __shfl_xor(q2, 1), p3 = __shfl_xor(q3, 1);
+    // inputs 0..7 of the group
+    const int e0 = h ? p0 : q0, e1 = h ? p1 : q1, e2 = h ? p2 : q2, e3 = h ? p3 : q3;
+    const int e4 = h ? q0 : p0, e5 = h ? q1 : p1, e6 = h ? q2 : p2, e7 = h ? q3 : p3;
+    const int m = h ? 255 : ~255;  // lo plane (q & 255) from the odd lane, hi (q & ~255) from the even one
+    uint4 v;
+    v.x = f16_pair(e0 & m, e2 & m);  // slots 0 1: inputs 0 2
+    v.y = f16_pair(e4 & m, e6 & m);  // slots 2 3: inputs 4 6
+    v.z = f16_pair(e1 & m, e3 & m);  // slots 4 5: inputs 1 3
+    v.w = f16_pair(e5 & m, e7 & m);  // slots 6 7: inputs 5 7
+    *reinterpret_cast<uint4 *>(planes + ((int64_t)(t >> 4) * CK + c) * 2048 + h * 1024 + (g * 16 + (t & 15)) * 16) = v;
 }
 
 // One workgroup (256 threads) per token row: optional LayerNorm, then

@@ -359,8 +359,27 @@ int64_t h16_rec_bytes(int64_t T, int64_t K);
 void h16_rec_parts(void *rec, int64_t T, int64_t K, uint8_t **planes, _Float16 **sums, float **inv);
 bool gguf_gemm_h16_ok(const llmq_mat *w);
 int launch_act_h16(llmq_ctx *ctx, const float *x, int64_t ldx, int64_t T, int64_t K, void *rec);
+// The batch-decode chain's forms of that matmul (gguf_gemm16.hip): the
+// input may be an "h16s" record (a scale per 16 inputs of a token, written
+// by the previous matmul's epilogue), its outputs then times each token's
+// 1 / rms from the record's sums of squares (norm); the epilogue may write
+// the next matmul's h16s record: of (out + residual) * gain (LLMQ_RESID),
+// or, swiglu (rows [gate; up]), of silu(gate) * up alone.
+struct H16Fuse {
+    bool in_s = false;
+    bool norm = false;
+    float eps = 0.0f;
+    void *out_rec = nullptr;
+    const float *gain = nullptr;
+    bool swiglu = false;
+};
 int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int64_t T, float *out, int64_t ldo,
-                         const float *bias, int flags);
+                         const float *bias, int flags, const H16Fuse *fz = nullptr);
+int64_t h16s_rec_bytes(int64_t T, int64_t K);
+// the h16s record of x * gain (with the sums of squares of x)
+int launch_rec_h16s(llmq_ctx *ctx, const float *x, int64_t ldx, int64_t T, int64_t K, const float *gain, void *rec);
+// whether the fused forms take w at T tokens (swiglu: as the [gate; up] matrix)
+bool gguf_gemm_h16s_ok(const llmq_mat *w, bool swiglu, int64_t T);
 // int16 output head for Q6_K / Q8_0 (gguf_head.hip).
 int gguf_has_i16(const llmq_mat *w);
 // with rms_g, each row of h is RMS-normalized (times rms_g) first; with

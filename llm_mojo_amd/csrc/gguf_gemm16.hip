@@ -46,6 +46,46 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
+// The "h16s" record, which the batch-decode chain's matmul epilogues write:
+// the h16 record with a scale per half sub-block (16 inputs) of a token
+// instead of one per superblock, so that a workgroup owning 16 consecutive
+// outputs of one matmul writes its part of the next one's input.  Per token
+// and half h (inputs 16h .. 16h + 15) a power of two s_h = 2^e_h with
+// max |x s_h| < 2^10; the planes hold x s_h as hi / lo in the h16 layout;
+//   sums  fp16 [T16 / 16][NSB][4 groups][16 tokens][8]: groups 0 and 1 the
+//         hi of s_h X_h for the superblock's halves 0..7 and 8..15, groups
+//         2 and 3 their lo (X_h the half's sum of x);
+//   exps  int8 [T16 / 16][NSB][16 tokens][16]: e_h;
+//   ssq   float [T16][K / 16]: the half's sum of x^2, for an RMSNorm of the
+//         row that the reading matmul applies to its outputs (a factor per
+//         token: W (x r g) = r W (x g)).
+// The reader brings each superblock of a token to the common scale 2^c,
+// c = min e_h (its largest half's), multiplying each half's planes and sums
+// by 2^(c - e_h) in fp16: exact wherever the products stay normal, and then
+// equal to the h16 record's x 2^c.
+struct HSRec {
+    uint8_t *planes;
+    _Float16 *sums;
+    int8_t *exps;
+    float *ssq;
+    int KB, NSB, NH;
+};
+
+HSRec hs_parts(void *rec, int64_t T, int64_t K) {
+    const int64_t T16 = (T + 15) / 16 * 16, KB = K / 32, NSB = K / 256;
+    uint8_t *p = static_cast<uint8_t *>(rec);
+    HSRec r{};
+    if (!p) return r;
+    r.planes = p;
+    r.sums = reinterpret_cast<_Float16 *>(p + T16 * KB * 128);
+    r.exps = reinterpret_cast<int8_t *>(p + T16 * KB * 128 + T16 * NSB * 64);
+    r.ssq = reinterpret_cast<float *>(p + T16 * KB * 128 + T16 * NSB * 80);
+    r.KB = (int)KB;
+    r.NSB = (int)NSB;
+    r.NH = (int)(K / 16);
+    return r;
+}
+
 struct HArgs {
     const uint8_t *codes, *sb, *planes, *sums, *inv;
     uint32_t codes_bytes, sb_bytes, planes_bytes, sums_bytes, inv_bytes;
@@ -54,6 +94,15 @@ struct HArgs {
     int64_t ldo;
     const float *bias;
     float *out;
+    // h16s input: the exponents (inv is then unused, sums in the h16s layout);
+    // with ssq, outputs times 1 / sqrt(sum x^2 / C + eps) of their token
+    const uint8_t *exps;
+    uint32_t exps_bytes;
+    const float *ssq;
+    int C;
+    float eps;
+    HSRec orec;          // the h16s record an epilogue writes (planes null: none)
+    const float *ogain;  // of (out + residual) * ogain
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
@@ -114,16 +163,140 @@ __device__ __forceinline__ void bytes_f16(uint32_t a, uint32_t b, uint32_t (&d)[
     d[3] = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
 }
 
-template <int NW, int RT>
+// Every lane of a 16-lane row gets the row's maximum / sum (the same bits
+// in each lane: the pairings are symmetric).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, llmq_dppf<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, llmq_dppf<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, llmq_dppf<0x141>(v));  // row_half_mirror
+    return fmaxf(v, llmq_dppf<0x140>(v));  // row_mirror
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v = v + llmq_dppf<0xB1>(v);
+    v = v + llmq_dppf<0x4E>(v);
+    v = v + llmq_dppf<0x141>(v);
+    return v + llmq_dppf<0x140>(v);
+}
+
+// Half hb (inputs 16 hb .. 16 hb + 15) of token t of an h16s record, by the
+// 16 lanes of a row of the wave, lane i % 16 holding input 16 hb + i % 16
+// in v; with o.ssq, the half's sum of xn^2 goes there (xn: the row before
+// the RMSNorm gain that v carries).
+__device__ __forceinline__ void hs_store_half(const HSRec &o, int t, int hb, float v, float xn) {
+    const int i = threadIdx.x & 15;
+    const float m = row16_max(fabsf(v));
+    int ex = 0;
+    frexpf(m, &ex);  // m < 2^ex
+    const int e = min(126, max(-126, 10 - ex));
+    const float s = ldexpf(1.0f, e);
+    const float xs = v * s, X = row16_sum(v) * s;
+    const float sq = o.ssq ? row16_sum(xn * xn) : 0.0f;
+    const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
+    const _Float16 shi = (_Float16)X, slo = (_Float16)(X - (float)shi);
+    const int64_t tt = t >> 4, c = t & 15;
+    const int j = hb >> 1, kk = (hb & 1) * 16 + i, g = kk >> 3, ii = kk & 7;
+    const int pos = (ii & 1) ? 4 + (ii >> 1) : (ii >> 1);
+    _Float16 *p = reinterpret_cast<_Float16 *>(o.planes) + ((tt * o.KB + j) * 1024 + (g * 16 + c) * 8 + pos);
+    p[0] = hi;
+    p[512] = lo;
+    if (i == 0) {
+        const int sb = hb >> 4, hs = hb & 15;
+        _Float16 *ps = o.sums + ((tt * o.NSB + sb) * 4 + (hs >> 3)) * 128 + c * 8 + (hs & 7);
+        ps[0] = shi;
+        ps[256] = slo;
+        o.exps[((tt * o.NSB + sb) * 16 + c) * 16 + hs] = (int8_t)e;
+        if (o.ssq) o.ssq[t * (int64_t)o.NH + hb] = sq;
+    }
+}
+
+// An h16s superblock for lane (token c16, group g): its 16 exponents ev
+// (bytes), its A operands ah / al (group g of each sub-block: half
+// 2u + g / 2) and sum operand sq (halves 8 (g % 2) + i) brought to the
+// common scale 2^c; inv[i] = 2^-c of output token 4g + i.
+__device__ __forceinline__ uint32_t pk_mul(uint32_t x, uint32_t f) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, x) * __builtin_bit_cast(v2h, f));
+}
+__device__ __forceinline__ uint4 pk_mul4(uint4 x, uint32_t f) {
+    return make_uint4(pk_mul(x.x, f), pk_mul(x.y, f), pk_mul(x.z, f), pk_mul(x.w, f));
+}
+// Signed byte (shift / 8) of w, shift a multiple of 8 (may vary by lane).
+__device__ __forceinline__ int sbyte(uint32_t w, uint32_t shift) { return (int)(w << (24u - shift)) >> 24; }
+
+__device__ __forceinline__ void hs_rescale(uint4 ev, int g, uint4 (&ah)[8], uint4 (&al)[8], uint4 &sq,
+                                           float (&inv)[4]) {
+    const uint32_t ew[4] = {ev.x, ev.y, ev.z, ev.w};
+    int c = sbyte(ew[0], 0);
+#pragma unroll
+    for (int i = 0; i < 16; i++) c = min(c, sbyte(ew[i >> 2], 8u * (i & 3)));
+    // 2^(c - eh) as fp16 bits: 2^-d as a float, rounded to fp16 (subnormal
+    // from d = 15, 0 from d = 25)
+    auto f16 = [&](int eh) -> uint32_t {
+        const float f = __uint_as_float((uint32_t)max(0, 127 - (eh - c)) << 23);
+        return (uint32_t)__half_as_ushort(__float2half(f));
+    };
+    // the lane's A operand of sub-block u: half 2u + g / 2, byte 2 (u % 2) + g / 2 of word u / 2
+    const uint32_t oA = (g >> 1) ? 8u : 0u;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const uint32_t f = f16(sbyte(ew[u >> 1], 16u * (u & 1) + oA)), fp = f | (f << 16);
+        ah[u] = pk_mul4(ah[u], fp);
+        al[u] = pk_mul4(al[u], fp);
+    }
+    // its sums: halves 8 (g % 2) .. + 7, words 2 (g % 2) and 2 (g % 2) + 1
+    const uint32_t s0 = (g & 1) ? ev.z : ev.x, s1 = (g & 1) ? ev.w : ev.y;
+    uint32_t fs[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t wv = k < 2 ? s0 : s1;
+        fs[k] = f16(sbyte(wv, 16u * (k & 1))) | (f16(sbyte(wv, 16u * (k & 1) + 8u)) << 16);
+    }
+    sq = make_uint4(pk_mul(sq.x, fs[0]), pk_mul(sq.y, fs[1]), pk_mul(sq.z, fs[2]), pk_mul(sq.w, fs[3]));
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int co = __shfl(c, 4 * g + i);
+        inv[i] = __uint_as_float((uint32_t)(127 - co) << 23);
+    }
+}
+
+// SIN: the record is an h16s record (with a.ssq: outputs RMS-normalized).
+// OUT 1 (RT 1, LLMQ_RESID): the epilogue also writes the h16s record of
+// (out + residual) * ogain to a.orec (when set), this matmul's 16-row tile
+// being a half of the next one's input.  OUT 2 (RT 4, the rows are
+// [gate; up]): slots 0, 1 take gate tiles 2b, 2b + 1, slots 2, 3 the up
+// tiles of the same rows, and the epilogue writes only the h16s record of
+// silu(gate) * up (a.orec).
+template <int NW, int RT, bool SIN, int OUT>
 __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
+    static_assert(OUT != 1 || (RT == 1 && NW >= 4), "record epilogue: one row tile, a thread an output");
+    static_assert(OUT != 2 || (RT == 4 && NW * 64 >= 512), "SwiGLU epilogue: two gate and two up tiles");
     __shared__ float part[NW][RT][256];
+    __shared__ float s_r[16];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c16 = lane & 15, g = lane >> 4;
-    const int tile0 = blockIdx.x * RT, tt = blockIdx.y;
+    const int tt = blockIdx.y;
+    auto tile_of = [&](int r) {
+        return OUT == 2 ? (r < 2 ? 2 * (int)blockIdx.x + r : a.ntiles / 2 + 2 * (int)blockIdx.x + r - 2)
+                        : (int)blockIdx.x * RT + r;
+    };
     const auto rc = make_rsrc(a.codes, a.codes_bytes), rs = make_rsrc(a.sb, a.sb_bytes);
     const auto rp = make_rsrc(a.planes, a.planes_bytes), rq = make_rsrc(a.sums, a.sums_bytes);
-    const auto ri = make_rsrc(a.inv, a.inv_bytes);
+    const auto ri = make_rsrc(a.inv, a.inv_bytes), re = make_rsrc(a.exps, a.exps_bytes);
+    // epilogue operands, in flight from the start: the record gain of this
+    // thread's output (OUT 1) and, wave 0, the token's sums of squares (lane:
+    // token c16, quarter g of the halves)
+    float og = 0.0f;
+    if (OUT == 1 && a.orec.planes && tid < 256) og = a.ogain[tile_of(0) * 16 + (tid & 15)];
+    float ssum = 0.0f;
+    if (SIN && a.ssq && w == 0) {
+        const int nq = a.C / 64;  // halves a quarter
+        const float4 *p4 = reinterpret_cast<const float4 *>(a.ssq + (int64_t)(tt * 16 + c16) * (a.C / 16) + g * nq);
+#pragma unroll 8
+        for (int k = 0; k < nq / 4; k++) {
+            const float4 v = p4[k];
+            ssum += (v.x + v.y) + (v.z + v.w);
+        }
+    }
     const int per = (a.NSB + NW - 1) / NW;  // superblocks a wave
     const int s0 = w * per, s1 = min(a.NSB, s0 + per);
     const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, km1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
@@ -136,10 +309,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
     auto load_w = [&](int sbi, uint4 (&f)[RT], uint32_t (&cw)[RT][8]) {
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            const bool ok = tile0 + r < a.ntiles;
-            f[r] = wload16(rs, ok ? (uint32_t)((((tile0 + r) * a.NSB + sbi) * 16 + c16) * 16) : kOOB, a.stream);
+            const int tl = tile_of(r);
+            const bool ok = tl < a.ntiles;
+            f[r] = wload16(rs, ok ? (uint32_t)(((tl * a.NSB + sbi) * 16 + c16) * 16) : kOOB, a.stream);
             // chunk entries of one row tile are 256 bytes apart (kOOB + 256 u stays out of range)
-            const uint32_t cb = ok ? (uint32_t)((((tile0 + r) * a.CK + sbi * 8) * 16 + c16) * 16 + g * 4) : kOOB;
+            const uint32_t cb = ok ? (uint32_t)(((tl * a.CK + sbi * 8) * 16 + c16) * 16 + g * 4) : kOOB;
 #pragma unroll
             for (int u = 0; u < 8; u++) cw[r][u] = wload4(rc, cb + 256u * u, a.stream);
         }
@@ -162,8 +336,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
             al[u] = bload16(rp, ab + 2048u * u + 1024u);
         }
         // sums planes: hi in group 0, lo in group 1, zeros in groups 2 and 3
-        const uint4 sq = bload16(rq, g < 2 ? (uint32_t)((tt * a.NSB + sbi) * 512 + lane * 16) : kOOB);
-        const uint4 iv = bload16(ri, (uint32_t)(((tt * a.NSB + sbi) * 16 + 4 * g) * 4));
+        // (h16s: all four groups); the scales (h16s: the token's exponents)
+        uint4 sq = SIN ? bload16(rq, (uint32_t)(((tt * a.NSB + sbi) * 64 + g * 16 + c16) * 16))
+                       : bload16(rq, g < 2 ? (uint32_t)((tt * a.NSB + sbi) * 512 + lane * 16) : kOOB);
+        const uint4 iv = SIN ? bload16(re, (uint32_t)(((tt * a.NSB + sbi) * 16 + c16) * 16))
+                             : bload16(ri, (uint32_t)(((tt * a.NSB + sbi) * 16 + 4 * g) * 4));
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             f[r] = fn[r];
@@ -173,6 +350,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (sbi + 1 < s1) load_w(sbi + 1, fn, cwn);
         __builtin_amdgcn_sched_barrier(0);  // the superblock's loads all issue before its first product
+        float inv[4];
+        if constexpr (SIN) {
+            hs_rescale(iv, g, ah, al, sq, inv);
+        } else {
+            inv[0] = __uint_as_float(iv.x);
+            inv[1] = __uint_as_float(iv.y);
+            inv[2] = __uint_as_float(iv.z);
+            inv[3] = __uint_as_float(iv.w);
+        }
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             // sc_j and m_j as bytes (k_scale_min, gguf.mojo:205-221, four at a time)
@@ -207,42 +393,93 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah[u]), b, d, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al[u]), b, d, 0, 0, 0);
             }
-            // m_j in groups 0 and 1 (against the sums' hi and lo planes)
+            // m_j in groups 0 and 1 (against the sums' hi and lo planes); h16s:
+            // m of half 8 (g % 2) + i's sub-block in every group
             v8h bm;
+            if constexpr (SIN) {
+                const uint32_t ma = (g & 1) ? mp[2] : mp[0], mb = (g & 1) ? mp[3] : mp[1];
+                const uint32_t dup[4] = {__builtin_amdgcn_perm(ma, ma, 0x01000100u), __builtin_amdgcn_perm(ma, ma, 0x03020302u),
+                                         __builtin_amdgcn_perm(mb, mb, 0x01000100u), __builtin_amdgcn_perm(mb, mb, 0x03020302u)};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const v2h p = g < 2 ? __builtin_bit_cast(v2h, mp[i]) - k1024 : (v2h){(_Float16)0.0f, (_Float16)0.0f};
-                bm[2 * i] = p[0];
-                bm[2 * i + 1] = p[1];
+                for (int i = 0; i < 4; i++) {
+                    const v2h p = __builtin_bit_cast(v2h, dup[i]) - k1024;
+                    bm[2 * i] = p[0];
+                    bm[2 * i + 1] = p[1];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const v2h p = g < 2 ? __builtin_bit_cast(v2h, mp[i]) - k1024 : (v2h){(_Float16)0.0f, (_Float16)0.0f};
+                    bm[2 * i] = p[0];
+                    bm[2 * i + 1] = p[1];
+                }
             }
             v4f dm = {0.0f, 0.0f, 0.0f, 0.0f};
             dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, sq), bm, dm, 0, 0, 0);
             const float dd = __half2float(__ushort_as_half((unsigned short)(f[r].x & 0xFFFFu)));
             const float dmin = __half2float(__ushort_as_half((unsigned short)(f[r].x >> 16)));
-            const float inv[4] = {__uint_as_float(iv.x), __uint_as_float(iv.y), __uint_as_float(iv.z),
-                                  __uint_as_float(iv.w)};
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[r][i] = fmaf(inv[i], fmaf(-dmin, dm[i], dd * d[i]), acc[r][i]);
         }
+    }
+    if (SIN && a.ssq && w == 0) {  // 1 / rms of token c16: the quarters in a fixed order
+        ssum += __shfl_xor(ssum, 16);
+        ssum += __shfl_xor(ssum, 32);
+        if (g == 0) s_r[c16] = 1.0f / sqrtf(ssum / (float)a.C + a.eps);
     }
 #pragma unroll
     for (int r = 0; r < RT; r++)
 #pragma unroll
         for (int i = 0; i < 4; i++) part[w][r][(4 * g + i) * 16 + c16] = acc[r][i];
     __syncthreads();
+    if constexpr (OUT == 2) {
+        // gate tile r2 and the up tile of the same rows: silu(gate) * up is
+        // half 2b + r2 of the next matmul's input (zeros for padded tokens)
+        if (tid < 512) {
+            const int r2 = tid >> 8, q = tid & 255, tk = tt * 16 + (q >> 4);
+            float gt = part[0][r2][q], up = part[0][r2 + 2][q];
+#pragma unroll
+            for (int p = 1; p < NW; p++) {
+                gt += part[p][r2][q];
+                up += part[p][r2 + 2][q];
+            }
+            if (SIN && a.ssq) {
+                gt *= s_r[q >> 4];
+                up *= s_r[q >> 4];
+            }
+            const float h = (gt / (1.0f + expf(-gt))) * up;
+            hs_store_half(a.orec, tk, 2 * (int)blockIdx.x + r2, tk < a.T ? h : 0.0f, 0.0f);
+        }
+        return;
+    }
     for (int e = tid; e < RT * 256; e += NW * 64) {
-        const int r = e >> 8, q = e & 255, tk = tt * 16 + (q >> 4), o = (tile0 + r) * 16 + (q & 15);
+        const int r = e >> 8, q = e & 255, tk = tt * 16 + (q >> 4), o = tile_of(r) * 16 + (q & 15);
         float v = part[0][r][q];
 #pragma unroll
         for (int p = 1; p < NW; p++) v += part[p][r][q];
-        if (o < a.n && tk < a.T) {
+        if (SIN && a.ssq) v *= s_r[q >> 4];
+        const bool live = o < a.n && tk < a.T;
+        if (live) {
             if (a.flags & LLMQ_BIAS) v += a.bias[o];
             if (a.flags & LLMQ_GELU) v = gelu_ref(v);
             float *dst = a.out + (int64_t)tk * a.ldo + o;
             if (a.flags & LLMQ_RESID) v += *dst;
             *dst = v;
         }
+        // (the next matmul's input row (out + residual) * gain, zeros for
+        // padded tokens and rows)
+        if (OUT == 1 && a.orec.planes) hs_store_half(a.orec, tk, tile_of(r), live ? v * og : 0.0f, live ? v : 0.0f);
     }
+}
+
+// The h16s record of x * gain with the sums of squares of x (T x K floats,
+// row stride ldx): workgroup (blockIdx.x, token blockIdx.y) covers a
+// superblock, wave w inputs 64 w .. 64 w + 63 (four halves).
+__global__ __launch_bounds__(256) void rec_h16s_kernel(const float *__restrict__ x, int64_t ldx, int T,
+                                                       const float *__restrict__ gain, HSRec o) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    const float xv = t < T ? x[(int64_t)t * ldx + i] : 0.0f;
+    hs_store_half(o, t, i >> 4, xv * gain[i], xv);
 }
 
 // The same matmul for many tokens (prompts): a workgroup of 8 waves owns 8
@@ -457,28 +694,99 @@ int launch_act_h16(llmq_ctx *ctx, const float *x, int64_t ldx, int64_t T, int64_
     return LLMQ_OK;
 }
 
+int64_t h16s_rec_bytes(int64_t T, int64_t K) {
+    const int64_t T16 = (T + 15) / 16 * 16, KB = K / 32, NSB = K / 256;
+    return T16 * KB * 128 + T16 * NSB * 80 + T16 * (K / 16) * 4;
+}
+
+int launch_rec_h16s(llmq_ctx *ctx, const float *x, int64_t ldx, int64_t T, int64_t K, const float *gain, void *rec) {
+    LLMQ_REQUIRE(x && gain && rec && T > 0 && K % 256 == 0, "rec_h16s: bad arguments");
+    const int64_t T16 = (T + 15) / 16 * 16;
+    LLMQ_REQUIRE(T16 <= 65535 && h16s_rec_bytes(T, K) < (int64_t)kOOB, "rec_h16s: record too large");
+    hipLaunchKernelGGL(rec_h16s_kernel, dim3((unsigned)(K / 256), (unsigned)T16), dim3(256), 0, ctx->stream, x, ldx,
+                       (int)T, gain, hs_parts(rec, T, K));
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+namespace {
+
+// Waves of the one-token-tile matmul: the fewest that give every wave
+// per = ceil(NSB / 16) superblocks.
+int h16_waves(int64_t NSB) {
+    const int per = (int)((NSB + 15) / 16);
+    return (int)((NSB + per - 1) / per);
+}
+
+template <bool SIN, int OUT>
+void launch_rt1(hipStream_t st, int nw, unsigned nt, unsigned ntt, const HArgs &a) {
+    if (nw <= 4)
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<4, 1, SIN, OUT>), dim3(nt, ntt), dim3(256), 0, st, a);
+    else if (nw <= 8)
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 1, SIN, OUT>), dim3(nt, ntt), dim3(512), 0, st, a);
+    else if (nw <= 11)
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<11, 1, SIN, OUT>), dim3(nt, ntt), dim3(704), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<16, 1, SIN, OUT>), dim3(nt, ntt), dim3(1024), 0, st, a);
+}
+
+}  // namespace
+
+bool gguf_gemm_h16s_ok(const llmq_mat *w, bool swiglu, int64_t T) {
+    if (!gguf_gemm_h16_ok(w) || (T + 15) / 16 >= kPT || w->n % 16) return false;
+    return !swiglu || (h16_waves(w->k / 256) <= 8 && w->n % 64 == 0);
+}
+
 int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int64_t T, float *out, int64_t ldo,
-                         const float *bias, int flags) {
+                         const float *bias, int flags, const H16Fuse *fz) {
+    const H16Fuse none{};
+    if (!fz) fz = &none;
+    const bool fused = fz->in_s || fz->out_rec || fz->swiglu;
     LLMQ_REQUIRE(gguf_gemm_h16_ok(w), "gguf_gemm_h16: not a Q4_K matrix with whole superblocks");
-    LLMQ_REQUIRE(rec && out && T > 0, "gguf_gemm_h16: bad arguments");
+    LLMQ_REQUIRE(rec && (out || fz->swiglu) && T > 0, "gguf_gemm_h16: bad arguments");
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemm_h16: LLMQ_BIAS without a bias");
+    LLMQ_REQUIRE(!fused || gguf_gemm_h16s_ok(w, fz->swiglu, T), "gguf_gemm_h16: the fused forms take this matrix only "
+                 "for fewer than %d token tiles", kPT);
+    LLMQ_REQUIRE(!fz->norm || fz->in_s, "gguf_gemm_h16: the RMSNorm factor comes with an h16s record");
+    LLMQ_REQUIRE(!fz->swiglu || (fz->in_s && fz->out_rec && !flags), "gguf_gemm_h16: SwiGLU takes an h16s record in "
+                 "and writes one, nothing else");
+    LLMQ_REQUIRE(!fz->out_rec || fz->swiglu || ((flags & LLMQ_RESID) && fz->gain), "gguf_gemm_h16: a record "
+                 "epilogue needs LLMQ_RESID and the gain");
     const int64_t T16 = (T + 15) / 16 * 16, KB = w->k / 32, NSB = w->k / 256;
     const int64_t ntc = (w->ntiles * w->CK + LLMQ_PAD_CHUNKS) * 16;
     const int64_t nts = (w->ntiles * w->NG + LLMQ_PAD_CHUNKS) * 16;
-    LLMQ_REQUIRE(ntc * 16 < (int64_t)kOOB && h16_rec_bytes(T, w->k) < (int64_t)kOOB && T16 <= 65535,
+    LLMQ_REQUIRE(ntc * 16 < (int64_t)kOOB && h16s_rec_bytes(T, std::max<int64_t>(w->k, w->n)) < (int64_t)kOOB &&
+                     T16 <= 65535,
                  "gguf_gemm_h16: operands too large");
-    const Rec p = rec_parts(const_cast<void *>(rec), T, w->k);
     HArgs a{};
     a.codes = w->codes;
     a.codes_bytes = (uint32_t)(ntc * 16);
     a.sb = reinterpret_cast<const uint8_t *>(w->g_sb16);
     a.sb_bytes = (uint32_t)(nts * 16);
-    a.planes = p.planes;
+    if (fz->in_s) {
+        const HSRec p = hs_parts(const_cast<void *>(rec), T, w->k);
+        a.planes = p.planes;
+        a.sums = reinterpret_cast<const uint8_t *>(p.sums);
+        a.sums_bytes = (uint32_t)(T16 * NSB * 64);
+        a.exps = reinterpret_cast<const uint8_t *>(p.exps);
+        a.exps_bytes = (uint32_t)(T16 * NSB * 16);
+        a.ssq = fz->norm ? p.ssq : nullptr;
+        a.C = (int)w->k;
+        a.eps = fz->eps;
+    } else {
+        const Rec p = rec_parts(const_cast<void *>(rec), T, w->k);
+        a.planes = p.planes;
+        a.sums = reinterpret_cast<const uint8_t *>(p.sums);
+        a.sums_bytes = (uint32_t)(T16 * NSB * 32);
+        a.inv = reinterpret_cast<const uint8_t *>(p.inv);
+        a.inv_bytes = (uint32_t)(T16 * NSB * 4);
+    }
     a.planes_bytes = (uint32_t)(T16 * KB * 128);
-    a.sums = reinterpret_cast<const uint8_t *>(p.sums);
-    a.sums_bytes = (uint32_t)(T16 * NSB * 32);
-    a.inv = reinterpret_cast<const uint8_t *>(p.inv);
-    a.inv_bytes = (uint32_t)(T16 * NSB * 4);
+    if (fz->out_rec) {
+        a.orec = hs_parts(fz->out_rec, T, fz->swiglu ? w->n / 2 : w->n);
+        if (fz->swiglu) a.orec.ssq = nullptr;  // down's input: no norm
+        a.ogain = fz->gain;
+    }
     a.n = (int)w->n;
     a.KB = (int)KB;
     a.CK = (int)w->CK;
@@ -491,26 +799,25 @@ int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int6
     a.out = out;
     const unsigned ntt = (unsigned)(T16 / 16);
     a.stream = ntt == 1;
-    // waves: the fewest that give every wave per = ceil(NSB / 16) superblocks
-    const int per = (int)((NSB + 15) / 16), nw = (int)((NSB + per - 1) / per);
+    const int nw = h16_waves(NSB);
     const unsigned nt = (unsigned)w->ntiles;
     hipStream_t st = ctx->stream;
-    if (ntt >= (unsigned)kPT)  // prompts: the LDS-staged form
+    if (fz->swiglu)  // two gate and two up tiles a workgroup
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 4, true, 2>), dim3(nt / 4, ntt), dim3(512), 0, st, a);
+    else if (fused && fz->in_s)
+        fz->out_rec ? launch_rt1<true, 1>(st, nw, nt, ntt, a) : launch_rt1<true, 0>(st, nw, nt, ntt, a);
+    else if (fused)
+        launch_rt1<false, 1>(st, nw, nt, ntt, a);
+    else if (ntt >= (unsigned)kPT)  // prompts: the LDS-staged form
         hipLaunchKernelGGL(gemm_h16_q4k_lds_kernel, dim3((nt + 4 * kRW - 1) / (4 * kRW), (ntt + kPT - 1) / kPT),
                            dim3(512), 0, st, a, (int)ntt);
     // wide matrices (gate / up): 4 row tiles a workgroup share the record
     // loads (one round of 176 workgroups at 11264 rows; 1, 2 and 4 tiles
     // measured 10.5, 11.9 and 10.1 us at 16 tokens)
     else if (nw <= 8 && w->ntiles >= 512)
-        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 4>), dim3((nt + 3) / 4, ntt), dim3(512), 0, st, a);
-    else if (nw <= 4)
-        hipLaunchKernelGGL((gemm_h16_q4k_kernel<4, 1>), dim3(nt, ntt), dim3(256), 0, st, a);
-    else if (nw <= 8)
-        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 1>), dim3(nt, ntt), dim3(512), 0, st, a);
-    else if (nw <= 11)
-        hipLaunchKernelGGL((gemm_h16_q4k_kernel<11, 1>), dim3(nt, ntt), dim3(704), 0, st, a);
+        hipLaunchKernelGGL((gemm_h16_q4k_kernel<8, 4, false, 0>), dim3((nt + 3) / 4, ntt), dim3(512), 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_h16_q4k_kernel<16, 1>), dim3(nt, ntt), dim3(1024), 0, st, a);
+        launch_rt1<false, 0>(st, nw, nt, ntt, a);
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }

@@ -755,6 +755,7 @@ struct llmq_llama {
           *logits = nullptr;
     void *h16 = nullptr;  // fp16 activation record of a several-row Q4_K matmul's input
     int64_t h16_cap = 0;
+    void *hs[2] = {nullptr, nullptr};  // the batch-decode chain's h16s records (the matmul epilogues write them)
     int64_t *tokens = nullptr, *next = nullptr, *gen = nullptr;
     int64_t gen_cap = 0;
     int graph_B = 0;  // batch size of the captured decode step
@@ -790,9 +791,11 @@ int ensure_rows(llmq_llama *m, int rows) {
     hipFree(m->hh);
     hipFree(m->tokens);
     hipFree(m->h16);
+    hipFree(m->hs[0]);
+    hipFree(m->hs[1]);
     m->x = m->xn = m->qkv = m->att = m->gu = m->hh = nullptr;
     m->tokens = nullptr;
-    m->h16 = nullptr;
+    m->h16 = m->hs[0] = m->hs[1] = nullptr;
     m->h16_cap = 0;
     m->rows = 0;
     const size_t r = (size_t)rows;
@@ -803,8 +806,10 @@ int ensure_rows(llmq_llama *m, int rows) {
         return llmq_set_error(LLMQ_ENOMEM, "llama: activations for %d tokens", rows);
     if (rows > 1) {
         const int64_t cap = h16_rec_bytes(rows, std::max(c.dim, c.ffn));
-        if (hipMalloc(&m->h16, (size_t)cap) != hipSuccess)
-            return llmq_set_error(LLMQ_ENOMEM, "llama: activation record for %d tokens", rows);
+        const size_t scap = (size_t)h16s_rec_bytes(rows, std::max(c.dim, c.ffn));
+        if (hipMalloc(&m->h16, (size_t)cap) != hipSuccess || hipMalloc(&m->hs[0], scap) != hipSuccess ||
+            hipMalloc(&m->hs[1], scap) != hipSuccess)
+            return llmq_set_error(LLMQ_ENOMEM, "llama: activation records for %d tokens", rows);
         m->h16_cap = cap;
     }
     m->rows = rows;
@@ -853,25 +858,85 @@ int norm_linear(llmq_llama *m, const float *g, const llmq_mat *w, int R, float *
 // The layers for R = nseq * T rows in m->x: T tokens of sequences seq0 ..
 // at positions pos0 + t (prefill: nseq = 1), or one token of every
 // sequence at position state[0] (decode: T = 1, state given).
+// Decode attention of layer l for R sequences (RoPE, the cache store and
+// the attention over splits of kSplit positions in one launch); returns the
+// split count.
+int attend_splits(llmq_llama *m, int R, int l, const int *state) {
+    const llmq_llama_cfg &c = m->cfg;
+    const int NS = (c.max_t + kSplit - 1) / kSplit, QC = qkv_cols(c);
+    // LLMQ_ATTN_GROUP=1 / 0 forces the grouped / per-head kernel
+    static const char *ge = getenv("LLMQ_ATTN_GROUP");
+    const bool grouped = c.n_head == 8 * c.n_kv && (ge ? ge[0] == '1' : R > 1);
+    if (grouped)  // the 8 query heads of a key / value head in one workgroup
+        hipLaunchKernelGGL(attend_split_group_kernel, dim3(c.n_kv, R, NS), dim3(kSplit), 0, m->ctx->stream, m->qkv,
+                           (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope, m->k8, m->v8, m->ks,
+                           m->vs, m->apart, NS);
+    else
+        hipLaunchKernelGGL(attend_split_kernel, dim3(c.n_head, R, NS), dim3(kSplit), 0, m->ctx->stream, m->qkv,
+                           (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope, m->k8, m->v8, m->ks,
+                           m->vs, m->apart, NS);
+    return NS;
+}
+
+// Whether the batch-decode step of R sequences takes the fused chain: each
+// Q4_K matmul's epilogue writes the next one's h16s record (RMSNorm as a
+// factor on the reading matmul's outputs, SwiGLU in the gate / up
+// epilogue), instead of the record kernels between them; LLMQ_FUSE_REC=0
+// turns it off.
+bool fused_chain(const llmq_llama *m, int R, const int *state) {
+    const char *fe = getenv("LLMQ_FUSE_REC");
+    if (!state || R < 2 || !m->hs[0] || (fe && fe[0] == '0')) return false;
+    return rec_ok(m, m->wqkv[0]) && rec_ok(m, m->wo[0]) && rec_ok(m, m->wgu[0]) && rec_ok(m, m->wdown[0]) &&
+           gguf_gemm_h16s_ok(m->wqkv[0], false, R) && gguf_gemm_h16s_ok(m->wo[0], false, R) &&
+           gguf_gemm_h16s_ok(m->wgu[0], true, R) && gguf_gemm_h16s_ok(m->wdown[0], false, R) &&
+           m->cfg.n_head % 4 == 0;
+}
+
 int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *state) {
     llmq_ctx *ctx = m->ctx;
     const llmq_llama_cfg &c = m->cfg;
     const int QC = qkv_cols(c);
+    const bool fused = fused_chain(m, R, state);
+    int cur = 0;  // fused: m->hs[cur] holds the next qkv matmul's input record
+    if (fused) RC(launch_rec_h16s(ctx, m->x, c.dim, R, c.dim, gain(m, 0, 0), m->hs[cur]));
     for (int l = 0; l < c.n_layer; l++) {
+        if (fused) {
+            H16Fuse fq;
+            fq.in_s = fq.norm = true;
+            fq.eps = c.eps;
+            RC(launch_gguf_gemm_h16(ctx, m->wqkv[l], m->hs[cur], R, m->qkv, QC, nullptr, 0, &fq));
+            const int NS = attend_splits(m, R, l, state);
+            uint8_t *pl;
+            _Float16 *su;
+            float *iv;
+            h16_rec_parts(m->h16, R, c.dim, &pl, &su, &iv);
+            hipLaunchKernelGGL(attend_combine_rec_kernel, dim3(c.n_head / 4, R), dim3(256), 0, ctx->stream, m->apart,
+                               NS, c.n_head, state, pl, su, iv);
+            // Wo + residual, writing the ffn norm's record of the new x
+            H16Fuse fo;
+            fo.out_rec = m->hs[cur ^ 1];
+            fo.gain = gain(m, l, 1);
+            RC(launch_gguf_gemm_h16(ctx, m->wo[l], m->h16, R, m->x, c.dim, nullptr, LLMQ_RESID, &fo));
+            // gate / up (normalized), writing silu(gate) * up as down's record
+            H16Fuse fg;
+            fg.in_s = fg.norm = fg.swiglu = true;
+            fg.eps = c.eps;
+            fg.out_rec = m->hs[cur];
+            RC(launch_gguf_gemm_h16(ctx, m->wgu[l], m->hs[cur ^ 1], R, nullptr, 0, nullptr, 0, &fg));
+            // down + residual, writing the next layer's attention norm record
+            H16Fuse fd;
+            fd.in_s = true;
+            if (l + 1 < c.n_layer) {
+                fd.out_rec = m->hs[cur ^ 1];
+                fd.gain = gain(m, l + 1, 0);
+            }
+            RC(launch_gguf_gemm_h16(ctx, m->wdown[l], m->hs[cur], R, m->x, c.dim, nullptr, LLMQ_RESID, &fd));
+            cur ^= 1;
+            continue;
+        }
         RC(norm_linear(m, gain(m, l, 0), m->wqkv[l], R, m->qkv, QC, 0));
         if (state) {  // RoPE, the cache store and the attention splits in one launch
-            const int NS = (c.max_t + kSplit - 1) / kSplit;
-            // LLMQ_ATTN_GROUP=1 / 0 forces the grouped / per-head kernel
-            static const char *ge = getenv("LLMQ_ATTN_GROUP");
-            const bool grouped = c.n_head == 8 * c.n_kv && (ge ? ge[0] == '1' : R > 1);
-            if (grouped)  // the 8 query heads of a key / value head in one workgroup
-                hipLaunchKernelGGL(attend_split_group_kernel, dim3(c.n_kv, R, NS), dim3(kSplit), 0, ctx->stream,
-                                   m->qkv, (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope,
-                                   m->k8, m->v8, m->ks, m->vs, m->apart, NS);
-            else
-                hipLaunchKernelGGL(attend_split_kernel, dim3(c.n_head, R, NS), dim3(kSplit), 0, ctx->stream, m->qkv,
-                                   (int64_t)QC, state, c.n_head, c.n_kv, c.n_layer, l, c.max_t, m->rope, m->k8,
-                                   m->v8, m->ks, m->vs, m->apart, NS);
+            const int NS = attend_splits(m, R, l, state);
             if (R == 1 && gguf_gemv_attn_ok(m->wo[l], NS, HD)) {  // Wo combines the splits as it stages its row
                 RC(launch_gguf_gemv(ctx, m->wo[l], nullptr, m->x, nullptr, LLMQ_RESID, nullptr, 0, nullptr, 0.0f, 0,
                                     nullptr, nullptr, m->apart, state, kSplit, NS));
@@ -989,7 +1054,7 @@ int llmq_llama_free(llmq_llama *m) {
     for (auto *w : m->wgu) llmq_mat_free(w);
     for (auto *w : m->wdown) llmq_mat_free(w);
     void *bufs[] = {m->hparts, m->apart, m->rope, m->norms, m->k8, m->v8, m->ks, m->vs, m->x, m->xn, m->qkv, m->att, m->gu, m->hh, m->logits,
-                    m->h16, m->tokens, m->next, m->gen, m->state};
+                    m->h16, m->hs[0], m->hs[1], m->tokens, m->next, m->gen, m->state};
     for (void *p : bufs) hipFree(p);
     delete m;
     return LLMQ_OK;

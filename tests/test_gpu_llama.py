@@ -273,3 +273,38 @@ def test_llama_batch16_full_context_equals_batch1(gpu):
     print(f"llama batch 16: {distinct} distinct token sequences", flush=True)
     assert distinct >= 12  # (zero-mean weights: each prompt leads its own way)
     m.free()
+
+
+@pytest.mark.parametrize("B", [3, 16])
+def test_llama_batch_fused_records_match_numpy(gpu, monkeypatch, B):
+    """The batch-decode chain whose Q4_K matmul epilogues write the next
+    matmul's input record (h16s: a scale per 16 inputs; the RMSNorm as a
+    factor on the reading matmul's outputs from the record's sums of
+    squares, SwiGLU in the gate / up epilogue): two layers at the TinyLlama
+    width, B sequences with their own 40-token prompts (B = 3: a padded
+    token tile), 10 greedy tokens each against NumPy greedy decoding (the
+    margin rule), and the tokens of the chain with the record kernels
+    (LLMQ_FUSE_REC=0) up to the first NumPy near-tie."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+    from llm_mojo_amd.llama import TINYLLAMA
+
+    cfg = dict(TINYLLAMA, n_layer=2, batch=B, max_t=64)
+    tensors = synth.llama_tensors(cfg, 21, centered=True)
+    prompts = synth.llama_prompts(21, B, 40, cfg["vocab"])
+    print("llama fused batch records", B, flush=True)
+    m = lm.Llama(ctx, cfg, tensors)
+    fused, _, _ = m.generate(prompts, 10)
+    m.free()
+    monkeypatch.setenv("LLMQ_FUSE_REC", "0")
+    m = lm.Llama(ctx, cfg, tensors)
+    plain, _, _ = m.generate(prompts, 10)
+    m.free()
+    ref = NumpyLlama(cfg, tensors, n_seq=B)
+    compared = []
+    for b in range(B):
+        n = greedy_vs_numpy(fused[:, b], ref, b, prompts[b], 0)
+        assert np.array_equal(fused[:n, b], plain[:n, b]), (b, fused[:, b], plain[:, b])
+        compared.append(n)
+    print("llama fused batch records: tokens compared", compared, flush=True)
+    assert sum(compared) >= 6 * B, compared

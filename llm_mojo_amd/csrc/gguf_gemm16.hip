@@ -228,11 +228,10 @@ __device__ __forceinline__ void hs_rescale(uint4 ev, int g, uint4 (&ah)[8], uint
     int c = sbyte(ew[0], 0);
 #pragma unroll
     for (int i = 0; i < 16; i++) c = min(c, sbyte(ew[i >> 2], 8u * (i & 3)));
-    // 2^(c - eh) as fp16 bits: 2^-d as a float, rounded to fp16 (subnormal
-    // from d = 15, 0 from d = 25)
+    // 2^(c - eh) as fp16 bits (v_ldexp_f16: subnormal from c - eh = -15, 0
+    // from -25)
     auto f16 = [&](int eh) -> uint32_t {
-        const float f = __uint_as_float((uint32_t)max(0, 127 - (eh - c)) << 23);
-        return (uint32_t)__half_as_ushort(__float2half(f));
+        return (uint32_t)__builtin_bit_cast(unsigned short, __builtin_amdgcn_ldexph((_Float16)1.0f, c - eh));
     };
     // the lane's A operand of sub-block u: half 2u + g / 2, byte 2 (u % 2) + g / 2 of word u / 2
     const uint32_t oA = (g >> 1) ? 8u : 0u;
@@ -287,16 +286,26 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
     // token c16, quarter g of the halves)
     float og = 0.0f;
     if (OUT == 1 && a.orec.planes && tid < 256) og = a.ogain[tile_of(0) * 16 + (tid & 15)];
-    float ssum = 0.0f;
-    if (SIN && a.ssq && w == 0) {
-        const int nq = a.C / 64;  // halves a quarter
-        const float4 *p4 = reinterpret_cast<const float4 *>(a.ssq + (int64_t)(tt * 16 + c16) * (a.C / 16) + g * nq);
-#pragma unroll 8
-        for (int k = 0; k < nq / 4; k++) {
-            const float4 v = p4[k];
-            ssum += (v.x + v.y) + (v.z + v.w);
-        }
+    // the residual of each output this thread writes (LLMQ_RESID), likewise
+    constexpr int NIT = (RT * 256 + NW * 64 - 1) / (NW * 64);
+    float res[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int e = tid + it * NW * 64, r = e >> 8, q = e & 255, tk = tt * 16 + (q >> 4), o = tile_of(r) * 16 + (q & 15);
+        const bool rd = OUT != 2 && (a.flags & LLMQ_RESID) && e < RT * 256 && o < a.n && tk < a.T;
+        res[it] = rd ? a.out[(int64_t)tk * a.ldo + o] : 0.0f;
     }
+    // (the first kSq float4 in registers, added after the main loop: wave 0
+    // does not wait for them before its own loads; the record epilogue's
+    // matmuls take no norm, 16-wave ones no registers to spare)
+    constexpr bool NRM = SIN && OUT != 1;
+    constexpr int kSq = NRM && NW < 16 ? 8 : 1;
+    const bool nrm = NRM && a.ssq && w == 0;
+    const int nq4 = a.C / 256;  // float4 a lane: a quarter of the token's C / 16 halves
+    const float4 *p4 = reinterpret_cast<const float4 *>(a.ssq + (int64_t)(tt * 16 + c16) * (a.C / 16) + g * 4 * nq4);
+    float4 sqv[kSq];
+#pragma unroll
+    for (int k = 0; k < kSq; k++) sqv[k] = nrm && kSq > 1 && k < nq4 ? p4[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const int per = (a.NSB + NW - 1) / NW;  // superblocks a wave
     const int s0 = w * per, s1 = min(a.NSB, s0 + per);
     const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, km1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
@@ -422,7 +431,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
             for (int i = 0; i < 4; i++) acc[r][i] = fmaf(inv[i], fmaf(-dmin, dm[i], dd * d[i]), acc[r][i]);
         }
     }
-    if (SIN && a.ssq && w == 0) {  // 1 / rms of token c16: the quarters in a fixed order
+    if (nrm) {  // 1 / rms of token c16: the quarters in a fixed order
+        float ssum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kSq; k++) ssum += (sqv[k].x + sqv[k].y) + (sqv[k].z + sqv[k].w);
+        for (int k = kSq > 1 ? kSq : 0; k < nq4; k++) {
+            const float4 v = p4[k];
+            ssum += (v.x + v.y) + (v.z + v.w);
+        }
         ssum += __shfl_xor(ssum, 16);
         ssum += __shfl_xor(ssum, 32);
         if (g == 0) s_r[c16] = 1.0f / sqrtf(ssum / (float)a.C + a.eps);
@@ -443,7 +459,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
                 gt += part[p][r2][q];
                 up += part[p][r2 + 2][q];
             }
-            if (SIN && a.ssq) {
+            if (NRM && a.ssq) {
                 gt *= s_r[q >> 4];
                 up *= s_r[q >> 4];
             }
@@ -452,19 +468,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
         }
         return;
     }
-    for (int e = tid; e < RT * 256; e += NW * 64) {
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int e = tid + it * NW * 64;
+        if (e >= RT * 256) break;
         const int r = e >> 8, q = e & 255, tk = tt * 16 + (q >> 4), o = tile_of(r) * 16 + (q & 15);
         float v = part[0][r][q];
 #pragma unroll
         for (int p = 1; p < NW; p++) v += part[p][r][q];
-        if (SIN && a.ssq) v *= s_r[q >> 4];
+        if (NRM && a.ssq) v *= s_r[q >> 4];
         const bool live = o < a.n && tk < a.T;
         if (live) {
             if (a.flags & LLMQ_BIAS) v += a.bias[o];
             if (a.flags & LLMQ_GELU) v = gelu_ref(v);
-            float *dst = a.out + (int64_t)tk * a.ldo + o;
-            if (a.flags & LLMQ_RESID) v += *dst;
-            *dst = v;
+            if (a.flags & LLMQ_RESID) v += res[it];
+            a.out[(int64_t)tk * a.ldo + o] = v;
         }
         // (the next matmul's input row (out + residual) * gain, zeros for
         // padded tokens and rows)
@@ -747,7 +765,8 @@ int launch_gguf_gemm_h16(llmq_ctx *ctx, const llmq_mat *w, const void *rec, int6
     LLMQ_REQUIRE(!(flags & LLMQ_BIAS) || bias, "gguf_gemm_h16: LLMQ_BIAS without a bias");
     LLMQ_REQUIRE(!fused || gguf_gemm_h16s_ok(w, fz->swiglu, T), "gguf_gemm_h16: the fused forms take this matrix only "
                  "for fewer than %d token tiles", kPT);
-    LLMQ_REQUIRE(!fz->norm || fz->in_s, "gguf_gemm_h16: the RMSNorm factor comes with an h16s record");
+    LLMQ_REQUIRE(!fz->norm || (fz->in_s && (!fz->out_rec || fz->swiglu)),
+                 "gguf_gemm_h16: the RMSNorm factor comes with an h16s record and no residual record epilogue");
     LLMQ_REQUIRE(!fz->swiglu || (fz->in_s && fz->out_rec && !flags), "gguf_gemm_h16: SwiGLU takes an h16s record in "
                  "and writes one, nothing else");
     LLMQ_REQUIRE(!fz->out_rec || fz->swiglu || ((flags & LLMQ_RESID) && fz->gain), "gguf_gemm_h16: a record "

@@ -275,14 +275,14 @@ def test_llama_batch16_full_context_equals_batch1(gpu):
     m.free()
 
 
-@pytest.mark.parametrize("B", [3, 16])
+@pytest.mark.parametrize("B", [2, 3, 16, 20])
 def test_llama_batch_fused_records_match_numpy(gpu, monkeypatch, B):
     """The batch-decode chain whose Q4_K matmul epilogues write the next
     matmul's input record (h16s: a scale per 16 inputs; the RMSNorm as a
     factor on the reading matmul's outputs from the record's sums of
     squares, SwiGLU in the gate / up epilogue): two layers at the TinyLlama
-    width, B sequences with their own 40-token prompts (B = 3: a padded
-    token tile), 10 greedy tokens each against NumPy greedy decoding (the
+    width, B sequences with their own 40-token prompts (B = 2, 3: a padded
+    token tile; B = 20: two token tiles), 10 greedy tokens each against NumPy greedy decoding (the
     margin rule), and the tokens of the chain with the record kernels
     (LLMQ_FUSE_REC=0) up to the first NumPy near-tie."""
     torch, lm, ctx = gpu

@@ -218,6 +218,23 @@ struct ArgmaxPart {
 int launch_quant_weights(llmq_ctx *ctx, llmq_mat *m, const float *dsrc, int64_t rows, int64_t cols, int reduce_rows);
 int launch_quantize_rows(llmq_ctx *ctx, const float *x, int64_t T, int64_t K, int16_t *xq, float *sx);
 
+// Decode's embed step (embed_kernel, attn.hip) done in the prologue of the
+// first layer's qkv GEMV: every workgroup picks the token from the previous
+// head's argmax partials and forms its embedding row plus position row;
+// workgroup 0 also stores the row to x, the token to gen[step] and the
+// advanced position and step to state[2], state[3] (state[0], state[1] are
+// the ones read; the step's head copies the new pair back).
+struct EmbedFold {
+    const llmq_mat *E = nullptr;  // the embedding (int4 or int8 codes)
+    const float *wpe = nullptr;   // [wpe_rows, E->k] position rows
+    int64_t wpe_rows = 0;
+    const ArgmaxPart *parts = nullptr;
+    int nparts = 0;
+    int64_t *gen = nullptr;
+    int *state = nullptr;
+    float *x = nullptr;
+};
+
 struct GemvRequest {
     const llmq_mat *w = nullptr;
     const float *x = nullptr;  // [T, ldx]
@@ -236,6 +253,8 @@ struct GemvRequest {
     float *sx_out = nullptr;
     void *ws = nullptr;            // caller-given workspace in place of the context's (never grown)
     size_t ws_cap = 0;             // its size in bytes
+    const EmbedFold *emb = nullptr;  // the embed step in the prologue (x unused; exact one-token kernel)
+    int *state_copy = nullptr;       // the kernel copies state_copy[2..3] to [0..1] (exact one-token kernel)
 };
 int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq);
 // Number of argmax partials launch_gemv_a16 writes for a T == 1 GEMV of w
@@ -258,6 +277,9 @@ int gemv1_num_parts(const llmq_mat *w, bool ln);
 // LLMQ_EXACT=0 (then gemv1, whose float sums run in another order).
 bool gemv_exact_supports(const llmq_mat *w);
 int gemv_exact_num_parts(const llmq_mat *w);
+// Whether the exact kernel of w (with LayerNorm) can take the embed step of
+// embedding E in its prologue (GemvRequest::emb).
+bool gemv_exact_embed_ok(const llmq_mat *w, const llmq_mat *E);
 int launch_gemv_exact(llmq_ctx *ctx, const GemvRequest &rq);
 // QuantMatrix.dot_row_i16 for rows row0 .. row0 + nrows - 1 (gemv_exact.hip).
 int launch_dot_row_i16(llmq_ctx *ctx, const llmq_mat *w, int64_t row0, int64_t nrows, const int16_t *xq, float *out);

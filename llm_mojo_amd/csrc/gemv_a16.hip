@@ -488,8 +488,9 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
     LLMQ_REQUIRE(!rq.dbg || (rq.T == 1 && !rq.ln_w), "linear: chunk sums need T == 1 without LayerNorm");
     // (the int8 head kernel keeps no per-chunk sums: chunk-sum requests for
     // it take gemv1)
-    if (rq.T == 1 && exact_order() && gemv_exact_supports(w) && !(rq.dbg && w->bits == 8))
-        return launch_gemv_exact(ctx, rq);
+    const bool exact = rq.T == 1 && exact_order() && gemv_exact_supports(w) && !(rq.dbg && w->bits == 8);
+    LLMQ_REQUIRE(exact || !(rq.emb || rq.state_copy), "linear: the embed step and the state copy need the exact kernel");
+    if (exact) return launch_gemv_exact(ctx, rq);
     if (rq.T == 1 && gemv1_supports(w, rq.ln_w != nullptr)) return launch_gemv1(ctx, rq);
     {
         // Prompts: the int8-MFMA GEMM (LN + quantize_rows into workspace

@@ -235,6 +235,23 @@ __global__ __launch_bounds__(NT) void act_prep_kernel(const float *__restrict__ 
 
 // ---------------------------------------------------------------- BLOCKED
 
+// The embed step taken into the prologue (EMB): the embedding's codes (int8,
+// or int4 nibbles, in tiles of 16 rows as embed_kernel reads them), scales
+// and zero points, the position rows, the previous head's argmax partials
+// and the decode state.
+struct EmbArgs {
+    const uint8_t *codes;
+    const uint16_t *scales;
+    const uint8_t *zps;
+    const float *wpe;
+    const ArgmaxPart *parts;
+    int64_t *gen;
+    int *state;
+    float *x;
+    uint32_t codes_bytes, meta_rows, wpe_bytes;  // meta_rows: scale / zero-point entries
+    int bits, CK, NG, cpg, n_rows, nparts;
+};
+
 struct BlkArgs {
     const uint4 *codes;
     const uint16_t *scales;
@@ -248,7 +265,121 @@ struct BlkArgs {
     int16_t *xq_out;
     float *sx_out;
     ArgmaxPart *amax;  // per-workgroup argmax partials (a head), or null
+    int *state_copy;   // state[0..1] = state[2..3] by one thread, or null
+    EmbArgs e;
 };
+
+// EMB, the loads issued first: the decode state and the first 4 NT argmax
+// partials (indices past the end re-read the last partial, which cannot
+// change the pick).
+template <int NT>
+__device__ __forceinline__ void emb_issue(const EmbArgs &e, int &st0, int &st1, ArgmaxPart (&ep)[4]) {
+    st0 = e.state[0];
+    st1 = e.state[1];
+#pragma unroll
+    for (int k = 0; k < 4; k++) ep[k] = e.parts[min((int)threadIdx.x + NT * k, e.nparts - 1)];
+}
+
+// EMB, the rest of embed_kernel's work for this workgroup: the pick (the
+// larger value wins, equal values keep the smaller index: a total order, so
+// any reduction order gives embed_kernel's token), then this thread's units
+// of the row, x = ((u - zp) * s) + wpe[pos] (row_op, tensor.mojo:463-473),
+// staged in xs; wave 0's LayerNorm copy (lnv: lane l holds x[16 i + l]) is
+// read back from there.  Workgroup 0 stores the row, gen[step] and the new
+// position and step (state[2], state[3]).  Ends with a barrier.
+template <int NT, int UPT, int NV>
+__device__ __forceinline__ void emb_row(const EmbArgs &e, int st0, int st1, const ArgmaxPart (&ep)[4],
+                                        float4 (&xv)[UPT], float (&lnv)[NV > 0 ? NV : 1], float *xs, int nunits) {
+    constexpr int NW = NT / 64;
+    __shared__ float s_v[NW];
+    __shared__ int s_i[NW];
+    const int tid = threadIdx.x;
+    const int pos = st0 + 1, step = st1 + 1;
+    // the position row first: it needs only the state
+    const auto rp = llmq_rsrc(e.wpe, e.wpe_bytes);
+    float4 wp[UPT];
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const uint32_t u = (uint32_t)(tid + NT * i);
+        const uint4 f = llmq_bload16(rp, u < (uint32_t)nunits ? ((uint32_t)pos * (uint32_t)nunits + u) * 16u : kLlmqOOB);
+        wp[i] = make_float4(__uint_as_float(f.x), __uint_as_float(f.y), __uint_as_float(f.z), __uint_as_float(f.w));
+    }
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    auto take = [&](float cv, int ci) {
+        if (cv > v || (cv == v && ci < idx)) {
+            v = cv;
+            idx = ci;
+        }
+    };
+#pragma unroll
+    for (int k = 0; k < 4; k++) take(ep[k].v, ep[k].idx);
+    for (int p = tid + 4 * NT; p < e.nparts; p += NT) take(e.parts[p].v, e.parts[p].idx);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int oi = __shfl_xor(idx, off);
+        take(ov, oi);
+    }
+    if ((tid & 63) == 0) {
+        s_v[tid >> 6] = v;
+        s_i[tid >> 6] = idx;
+    }
+    llmq_lds_barrier();
+    v = s_v[0];
+    idx = s_i[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) take(s_v[w], s_i[w]);
+    // an argmax over logits that are all NaN has no index: token 0's row
+    const int row = (idx >= 0 && idx < e.n_rows) ? idx : 0;
+    const uint32_t tile = (uint32_t)row >> 4, r = (uint32_t)row & 15u;
+    const auto rc = llmq_rsrc(e.codes, e.codes_bytes);
+    const auto rs = llmq_rsrc(e.scales, e.meta_rows * 2u);
+    const auto rz = llmq_rsrc(e.zps, e.meta_rows);
+    uint32_t cw[UPT], sb[UPT], zb[UPT];
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const uint32_t u = (uint32_t)(tid + NT * i), k0 = 4u * u;
+        const bool ok = u < (uint32_t)nunits;
+        // the unit's four codes: bytes k0 % 16 .. + 3 of a 16-code chunk, or
+        // nibbles k0 % 32 .. + 3 (two bytes) of a 32-code one
+        const uint32_t c = e.bits == 4 ? k0 >> 5 : k0 >> 4;
+        const uint32_t off = ((tile * (uint32_t)e.CK + c) * 16u + r) * 16u + (e.bits == 4 ? (k0 & 31u) >> 1 : k0 & 15u);
+        cw[i] = llmq_bload4(rc, ok ? off & ~3u : kLlmqOOB) >> (8u * (off & 3u));
+        const uint32_t gi = (tile * (uint32_t)e.NG + c / (uint32_t)e.cpg) * 16u + r;
+        sb[i] = llmq_bload2(rs, ok ? gi * 2u : kLlmqOOB);
+        zb[i] = llmq_bload1(rz, ok ? gi : kLlmqOOB);
+    }
+#pragma unroll
+    for (int i = 0; i < UPT; i++) {
+        const float s = __half2float(__ushort_as_half((unsigned short)sb[i]));
+        const float zp = (float)zb[i];
+        float q[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t u = e.bits == 4 ? (cw[i] >> (4 * j)) & 15u : (cw[i] >> (8 * j)) & 255u;
+            q[j] = ((float)u - zp) * s;
+        }
+        xv[i] = make_float4(q[0] + wp[i].x, q[1] + wp[i].y, q[2] + wp[i].z, q[3] + wp[i].w);
+        const int u = tid + NT * i;
+        if (u < nunits) {
+            reinterpret_cast<float4 *>(xs)[u] = xv[i];
+            if (blockIdx.x == 0) reinterpret_cast<float4 *>(e.x)[u] = xv[i];
+        }
+    }
+    if (blockIdx.x == 0 && tid == 0) {
+        e.gen[step] = idx;
+        e.state[2] = pos;
+        e.state[3] = step;
+    }
+    llmq_lds_barrier();
+    if constexpr (NV > 0) {
+        if (tid < 64) {
+#pragma unroll
+            for (int i = 0; i < NV; i++) lnv[i] = xs[16 * i + (tid & 15)];
+        }
+    }
+}
 
 // Workgroup: NW waves over NW / KS row octets; the KS waves of an octet
 // split its blocks into contiguous runs and leave each block's exact
@@ -256,7 +387,7 @@ struct BlkArgs {
 // the two fma chains over all blocks in order.  REC: the activations'
 // planes and half sums are read from the prepared record, a block's worth
 // with its codes.
-template <int NW, int KS, bool LN, int UPT, int WIN, bool DBG, bool REC, int NV>
+template <int NW, int KS, bool LN, int UPT, int WIN, bool DBG, bool REC, int NV, bool EMB>
 __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     constexpr int NT = NW * 64, OPW = NW / KS;
     extern __shared__ __align__(16) uint32_t smem[];
@@ -284,13 +415,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     // before any wait.
     float4 xv[UPT], lw[UPT], lb[UPT];
     float lnv[NV > 0 ? NV : 1];
+    int e_st0 = 0, e_st1 = 0;  // EMB: the decode state and the first argmax partials instead of a row
+    ArgmaxPart ep[4];
     if (!REC) {
-        if (LN) load_lnv<NV>(a.x, lnv);
-        load_row<NT, UPT>(a.x, nunits, xv);
+        if constexpr (EMB) {
+            emb_issue<NT>(a.e, e_st0, e_st1, ep);
+        } else {
+            if (LN) load_lnv<NV>(a.x, lnv);
+            load_row<NT, UPT>(a.x, nunits, xv);
+        }
         if (LN) {
             load_row<NT, UPT>(a.ln_w, nunits, lw);
             load_row<NT, UPT>(a.ln_b, nunits, lb);
         }
+    }
+    if (a.state_copy && blockIdx.x == 0 && tid == 0) {
+        a.state_copy[0] = a.state_copy[2];
+        a.state_copy[1] = a.state_copy[3];
     }
     const auto rc = llmq_rsrc(a.codes, a.codes_bytes);
     const auto rs = llmq_rsrc(a.scales, a.scales_bytes);
@@ -339,6 +480,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_blk_kernel(BlkArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (!REC) {
+        if constexpr (EMB) emb_row<NT, UPT, NV>(a.e, e_st0, e_st1, ep, xv, lnv, xs, nunits);
         // Prologue: LayerNorm, quantize_rows, nibble planes and half sums.
         sx = act_prologue<NT, UPT, LN, NV>(xv, lw, lb, lnv, a.K, xs, bc, red);
         const bool xq_dbg = a.xq_out != nullptr && blockIdx.x == 0;
@@ -517,7 +659,8 @@ struct Ch8Args {
     ArgmaxPart *amax;
     int16_t *xq_out;
     float *sx_out;
-    int iters;  // tile groups a workgroup takes
+    int iters;         // tile groups a workgroup takes
+    int *state_copy;   // state[0..1] = state[2..3] by one thread, or null
 };
 
 // Workgroup: NW waves over TPW row tiles at a time (NW / TPW waves share a
@@ -558,6 +701,10 @@ __global__ __launch_bounds__(NW * 64) void head8_kernel(Ch8Args a) {
             load_row<NT, UPT>(a.ln_w, nunits, lw);
             load_row<NT, UPT>(a.ln_b, nunits, lb);
         }
+    }
+    if (a.state_copy && blockIdx.x == 0 && tid == 0) {
+        a.state_copy[0] = a.state_copy[2];
+        a.state_copy[1] = a.state_copy[3];
     }
     const auto rc = llmq_rsrc(a.codes, a.codes_bytes);
     const auto rs = llmq_rsrc(a.scales, (uint32_t)a.ntiles * 32u);
@@ -733,15 +880,22 @@ inline int ln_nv(int K) { return K == 768 ? 48 : K == 1024 ? 64 : 0; }
 
 template <int NW, int KS, bool LN, int UPT, bool REC, int NV>
 void blk_launch_nv(llmq_ctx *ctx, const BlkArgs &a, int grid, size_t lds, int win) {
-#define BLK(W, D) hipLaunchKernelGGL((gemv_blk_kernel<NW, KS, LN, UPT, W, D, REC, NV>), dim3((unsigned)grid), \
-                                     dim3(NW * 64), lds, ctx->stream, a)
+#define BLK(W, D, E) hipLaunchKernelGGL((gemv_blk_kernel<NW, KS, LN, UPT, W, D, REC, NV, E>), dim3((unsigned)grid), \
+                                        dim3(NW * 64), lds, ctx->stream, a)
     if (a.dbg) {
         if constexpr (!LN && !REC) {
-            BLK(4, true);
+            BLK(4, true, false);
             return;
         }
     }
-    if (win <= 2) BLK(2, false); else if (win <= 4) BLK(4, false); else if (win <= 8) BLK(8, false); else BLK(16, false);
+    if constexpr (LN && !REC && NV > 0) {
+        if (a.e.parts) {  // (launch_exact admits the embed step only here)
+            if (win <= 2) BLK(2, false, true); else BLK(4, false, true);
+            return;
+        }
+    }
+    if (win <= 2) BLK(2, false, false); else if (win <= 4) BLK(4, false, false);
+    else if (win <= 8) BLK(8, false, false); else BLK(16, false, false);
 #undef BLK
 }
 
@@ -863,6 +1017,31 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
         a.xq_out = rq.xq_out;
         a.sx_out = rq.sx_out;
         a.amax = rq.amax;
+        a.state_copy = rq.state_copy;
+        a.e = EmbArgs{};
+        if (const EmbedFold *f = rq.emb) {
+            const llmq_mat *E = f->E;
+            LLMQ_REQUIRE(!rec && gemv_exact_embed_ok(w, E) && ln && !rq.dbg && f->wpe && f->parts && f->nparts > 0 &&
+                             f->gen && f->state && f->x && f->wpe_rows > 0 && f->wpe_rows * K * 4 < (int64_t)kLlmqOOB,
+                         "linear: no embed step in this kernel's prologue");
+            a.e.codes = E->codes;
+            a.e.scales = E->scales;
+            a.e.zps = E->zps;
+            a.e.wpe = f->wpe;
+            a.e.parts = f->parts;
+            a.e.gen = f->gen;
+            a.e.state = f->state;
+            a.e.x = f->x;
+            a.e.codes_bytes = (uint32_t)((E->ntiles * E->CK + LLMQ_PAD_CHUNKS) * 256);
+            a.e.meta_rows = (uint32_t)((E->ntiles * E->NG + LLMQ_PAD_CHUNKS) * LLMQ_TILE_ROWS);
+            a.e.wpe_bytes = (uint32_t)(f->wpe_rows * K * 4);
+            a.e.bits = E->bits;
+            a.e.CK = (int)E->CK;
+            a.e.NG = (int)E->NG;
+            a.e.cpg = (int)(E->group / (E->bits == 4 ? 32 : 16));
+            a.e.n_rows = (int)E->n;
+            a.e.nparts = f->nparts;
+        }
         const int nb = K / 256, opw = 4 / ks;
         LLMQ_REQUIRE(!rec || llmq_act_layout(K).xq <= 6 * 16 * 256, "linear_act: reduction axis %d too long", K);
         const size_t lds = (size_t)w->CK * (kPlaneStride + 2) * 4 + (ln ? (size_t)K * 4 : 0) +
@@ -881,6 +1060,7 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     }
     // int8 per channel
     LLMQ_REQUIRE(!rq.dbg, "linear: chunk sums are not kept by the int8 head kernel");
+    LLMQ_REQUIRE(!rq.emb, "linear: no embed step in the int8 head kernel's prologue");
     int nw, tpw, grid, iters;
     head8_shape(w, &nw, &tpw, &grid, &iters);
     LLMQ_REQUIRE(!rq.amax || grid <= rq.amax_cap, "linear: %d argmax partials exceed capacity %d", grid, rq.amax_cap);
@@ -904,6 +1084,7 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
     a.xq_out = rq.xq_out;
     a.sx_out = rq.sx_out;
     a.iters = iters;
+    a.state_copy = rq.state_copy;
     const int S = (int)(w->CK / 4), spw = (S + (nw / tpw) - 1) / (nw / tpw);
     const size_t lds = (rec ? 0 : (size_t)K * 2) + (size_t)tpw * (nw / tpw) * 2 * 16 * 8 * 4 + (ln ? (size_t)K * 4 : 0);
     LLMQ_REQUIRE(lds <= 64 * 1024, "head: %zu bytes of LDS", lds);
@@ -952,6 +1133,15 @@ int launch_exact(llmq_ctx *ctx, const GemvRequest &rq, const uint8_t *rec) {
 }  // namespace
 
 bool gemv_exact_supports(const llmq_mat *w) { return exact_supports(w); }
+
+bool gemv_exact_embed_ok(const llmq_mat *w, const llmq_mat *E) {
+    if (!w || !exact_supports(w) || w->bits != 4 || ln_nv((int)w->k) == 0 || upt_for((int)w->k, 256) != 1) return false;
+    if (!E || E->kind != MAT_QUANT || (E->bits != 4 && E->bits != 8) || E->k != w->k || E->n > INT32_MAX) return false;
+    const int64_t cpc = E->bits == 4 ? 32 : 16;  // codes a chunk
+    if (E->group % cpc != 0 || E->group / cpc < 1) return false;
+    return (E->ntiles * E->CK + LLMQ_PAD_CHUNKS) * 256 < (int64_t)kLlmqOOB &&
+           (E->ntiles * E->NG + LLMQ_PAD_CHUNKS) * LLMQ_TILE_ROWS * 2 < (int64_t)kLlmqOOB;
+}
 
 int gemv_exact_num_parts(const llmq_mat *w) {
     int grid;

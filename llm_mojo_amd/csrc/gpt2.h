@@ -29,8 +29,10 @@ struct llmq_gpt2 {
     int nparts = 0;
     int64_t *tokens = nullptr, *gen = nullptr;
     int *state = nullptr;  // {pos, step} of the device-driven decode loop
-    hipGraphExec_t step_graph = nullptr;
-    hipGraph_t step_graph_def = nullptr;
+    // captured decode steps: [0] one step, [1] step_k steps
+    hipGraphExec_t step_graph[2] = {};
+    hipGraph_t step_graph_def[2] = {};
+    int step_k = 0;
     // Model[GGUFMatrix, GGUFMatrix] (load_gguf, gpt2t.mojo:728-760): layers
     // and head as stored in a GGUF file, float activations, LayerNorm into xn
     // Decode tokens run qkv + attention as one kernel (qkv_attn.hip) past

@@ -54,6 +54,50 @@ def test_gpt2_decode_matches_oracle_exactly(gpu, orc, models, seed):
     check_decode_exact(torch, orc, model, ref, prompt, STEPS, f"prompt {seed}")
 
 
+def test_gpt2_embed_fold_same_tokens(gpu, orc, models, weights, monkeypatch):
+    """The decode step's embed step (the pick from the head's argmax
+    partials, the embedding and position rows) runs in the first qkv GEMV's
+    prologue by default, with embed_kernel under LLMQ_EMBED_FOLD=0: both
+    loops emit the oracle's greedy tokens, for 1, 2 and 30 tokens (the first
+    has no decode forward, the second one), twice in a row on one model (the
+    captured step graph replayed from a new prompt's state)."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    model, ref = models
+    monkeypatch.setenv("LLMQ_EMBED_FOLD", "0")
+    plain = lm.GPT2(ctx, weights)
+    for seed, steps in ((7, 1), (8, 2), (9, 30), (10, 30)):
+        prompt = [int(v) for v in synth.prompt_ids(3000 + seed, 12)]
+        want = list(ref.generate(prompt, steps))
+        want = want[:next((i for i, t in enumerate(want) if t == 50256), len(want))]
+        print("embed fold: prompt", seed, "steps", steps, flush=True)
+        monkeypatch.setenv("LLMQ_EMBED_FOLD", "0")
+        a, _, _ = plain.generate(prompt, steps)
+        monkeypatch.delenv("LLMQ_EMBED_FOLD")
+        b, _, _ = model.generate(prompt, steps)
+        assert a.tolist() == want and b.tolist() == want, (a.tolist(), b.tolist(), want)
+    plain.free()
+
+
+@pytest.mark.parametrize("k", [1, 3, 64])
+def test_gpt2_steps_per_graph_same_tokens(gpu, orc, models, monkeypatch, k):
+    """k decode steps captured as one graph (LLMQ_GRAPH_STEPS; the remainder
+    below k as one-step graphs): 30 tokens are 29 decode steps, so k = 3
+    replays the 3-step graph 9 times and the one-step graph twice, k = 64
+    only the one-step graph.  The tokens are the oracle's greedy ones."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    model, ref = models
+    prompt = [int(v) for v in synth.prompt_ids(3100 + k, 12)]
+    want = list(ref.generate(prompt, 30))
+    monkeypatch.setenv("LLMQ_GRAPH_STEPS", str(k))
+    print("steps per graph", k, flush=True)
+    got, _, _ = model.generate(prompt, 30)
+    assert got.tolist() == want
+
+
 def test_gpt2_fused_qkv_attention(gpu, orc, weights, monkeypatch):
     """Decode tokens through the fused qkv + attention kernel (a faster form
     for long contexts, whose attention sums run in another order: not the

@@ -760,8 +760,10 @@ struct llmq_llama {
     int64_t gen_cap = 0;
     int graph_B = 0;  // batch size of the captured decode step
     int *state = nullptr;
-    hipGraphExec_t step_graph = nullptr;
-    hipGraph_t step_graph_def = nullptr;
+    // captured decode steps: [0] one step, [1] step_k steps
+    hipGraphExec_t step_graph[2] = {};
+    hipGraph_t step_graph_def[2] = {};
+    int step_k = 0;
 };
 
 namespace {
@@ -769,10 +771,13 @@ namespace {
 int qkv_cols(const llmq_llama_cfg &c) { return (c.n_head + 2 * c.n_kv) * c.head_dim; }
 
 void drop_graph(llmq_llama *m) {
-    if (m->step_graph) hipGraphExecDestroy(m->step_graph);
-    if (m->step_graph_def) hipGraphDestroy(m->step_graph_def);
-    m->step_graph = nullptr;
-    m->step_graph_def = nullptr;
+    for (int i = 0; i < 2; i++) {
+        if (m->step_graph[i]) hipGraphExecDestroy(m->step_graph[i]);
+        if (m->step_graph_def[i]) hipGraphDestroy(m->step_graph_def[i]);
+        m->step_graph[i] = nullptr;
+        m->step_graph_def[i] = nullptr;
+    }
+    m->step_k = 0;
     m->graph_B = 0;
 }
 
@@ -1213,8 +1218,32 @@ int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int B, int n_prom
     RC(ensure_rows(m, n_prompt));
     const char *ge = getenv("LLMQ_GRAPH");
     const bool use_graph = !(ge && ge[0] == '0');  // LLMQ_GRAPH=0: steps launched one by one
-    if (use_graph && steps > 1 && !m->step_graph) {
-        RC(llmq_capture(ctx->stream, [&] { return llama_step(m, B); }, &m->step_graph_def, &m->step_graph));
+    // Each step picks its tokens and positions on the device, so k steps
+    // capture as one graph, replayed while k or more remain, then the
+    // one-step graph (k = LLMQ_GRAPH_STEPS, default 4, as for GPT-2).
+    int k = 4;
+    if (const char *e = getenv("LLMQ_GRAPH_STEPS")) k = atoi(e);
+    k = k < 1 ? 1 : k > 64 ? 64 : k;
+    const int n_steps = steps - 1, n_multi = k > 1 ? n_steps / k : 0, n_one = n_steps - n_multi * k;
+    if (use_graph && n_multi > 0 && m->step_k != k && m->step_graph[1]) {
+        hipGraphExecDestroy(m->step_graph[1]);
+        hipGraphDestroy(m->step_graph_def[1]);
+        m->step_graph[1] = nullptr;
+        m->step_graph_def[1] = nullptr;
+    }
+    if (use_graph && n_multi > 0 && !m->step_graph[1]) {
+        RC(llmq_capture(
+            ctx->stream,
+            [&]() -> int {
+                for (int i = 0; i < k; i++) RC(llama_step(m, B));
+                return LLMQ_OK;
+            },
+            &m->step_graph_def[1], &m->step_graph[1]));
+        m->step_k = k;
+        m->graph_B = B;
+    }
+    if (use_graph && n_one > 0 && !m->step_graph[0]) {
+        RC(llmq_capture(ctx->stream, [&] { return llama_step(m, B); }, &m->step_graph_def[0], &m->step_graph[0]));
         m->graph_B = B;
     }
     ScopedEvents ev;
@@ -1227,11 +1256,11 @@ int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int B, int n_prom
     const int init_state[4] = {n_prompt, 1, 0, 0};  // position of the first pick, gen row of the next
     LLMQ_HIP(hipMemcpyAsync(m->state, init_state, sizeof(init_state), hipMemcpyHostToDevice, ctx->stream));
     RC(launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim));  // the first picks, embedded
-    for (int i = 1; i < steps; i++) {
-        if (use_graph)
-            LLMQ_HIP(hipGraphLaunch(m->step_graph, ctx->stream));
-        else
-            RC(llama_step(m, B));
+    if (use_graph) {
+        for (int i = 0; i < n_multi; i++) LLMQ_HIP(hipGraphLaunch(m->step_graph[1], ctx->stream));
+        for (int i = 0; i < n_one; i++) LLMQ_HIP(hipGraphLaunch(m->step_graph[0], ctx->stream));
+    } else {
+        for (int i = 1; i < steps; i++) RC(llama_step(m, B));
     }
     LLMQ_HIP(hipEventRecord(e2, ctx->stream));
     LLMQ_HIP(hipEventSynchronize(e2));

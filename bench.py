@@ -250,7 +250,6 @@ def gemv_micro(torch, lm, ctx, reps=200, rot_bytes=320 << 20):
 
 
 PREFILL_T = 476
-INT8_MFMA_PEAK = 5.0e15  # dense int8 MFMA ops/s of MI355X
 F16_MFMA_PEAK = 2.5e15   # dense fp16 MFMA flop/s of MI355X
 LAYER_SHAPES = [("qkv", 768, 2304), ("proj", 768, 768), ("fc", 768, 3072), ("fcproj", 3072, 768)]
 
@@ -259,11 +258,9 @@ def prefill(torch, lm, synth, ctx, tensors, model4, reps=5):
     """Config 3: a 476-token prompt through the GPT-2 weights in int4-g32 and
     int8-g32 A16 form (tok/s = T / prefill span, gpt2t.mojo:949-967), and the
     four layer GEMMs alone at M = 476: time, algorithmic int16 x intN ops
-    (2 M K N) and executed matrix-core ops against their peak: int4-g32 on
-    the fp16 matrix cores (the hi / lo activation planes: 2 products per MAC,
-    M padded to 16, against 2.5 PFLOP/s), int8 on the int8 ones (planes and
-    the weights' two nibbles: 4 products per MAC, N padded to the 64-row
-    workgroup tile, against 5 POP/s)."""
+    (2 M K N) and executed matrix-core ops against their peak: both forms
+    on the fp16 matrix cores (the hi / lo activation planes: 2 products per
+    MAC, M padded to 16, against 2.5 PFLOP/s)."""
     prompt = synth.prompt_ids(1337, PREFILL_T)
     res = {}
     for bits in (4, 8):
@@ -301,11 +298,11 @@ def prefill(torch, lm, synth, ctx, tensors, model4, reps=5):
                 w.free()
                 tot_us += us
                 alg += 2 * PREFILL_T * K * N
-                exe += 2 * (-(-PREFILL_T // 16) * 16) * (N if bits == 4 else -(-N // 64) * 64) * K * (2 if bits == 4 else 4)
+                exe += 2 * (-(-PREFILL_T // 16) * 16) * N * K * 2
                 gemm[f"int{bits}_{name}_us"] = round(us, 2)
             gemm[f"int{bits}_layer_us"] = round(tot_us, 2)
             gemm[f"int{bits}_alg_tops"] = round(alg / tot_us / 1e6, 1)
-            gemm[f"int{bits}_mfma_util"] = round(exe / (tot_us * 1e-6) / (F16_MFMA_PEAK if bits == 4 else INT8_MFMA_PEAK), 4)
+            gemm[f"int{bits}_mfma_util"] = round(exe / (tot_us * 1e-6) / F16_MFMA_PEAK, 4)
     ctx.set_stream(None)
     res["layer_gemms_m476"] = gemm
     return res

@@ -548,16 +548,18 @@ __device__ __forceinline__ void bytes_f16(uint32_t a, uint32_t b, uint32_t (&d)[
     d[3] = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
 }
 
-// Bytes of one staged step.
-template <int MT, int NR, int S, int NW>
+// Bytes of one staged step (CPG code chunks of 16 bytes a row and group:
+// 1 for int4, 2 for int8).
+template <int MT, int NR, int S, int NW, int CPG>
 struct F16Lds {
-    static constexpr int A = MT * S * 2048, C = NW * NR * S * 256, Z = NW * NR * S * 16, SC = NW * NR * S * 32;
+    static constexpr int A = MT * S * 2048, C = NW * NR * S * 256 * CPG, Z = NW * NR * S * 16, SC = NW * NR * S * 32;
     static constexpr int BYTES = A + C + Z + SC;
 };
 
-template <int MT, int NR, int S, int NW>
+template <int MT, int NR, int S, int NW, int BITS>
 __global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
-    using LY = F16Lds<MT, NR, S, NW>;
+    constexpr int CPG = BITS / 4;  // code chunks a group of 32
+    using LY = F16Lds<MT, NR, S, NW, CPG>;
     constexpr int RB = NW * 1024;  // bytes a copy round: 16 a lane
     // separate arrays, so that the compiler sees a copy into one cannot alias reads of the other
     __shared__ __align__(16) uint8_t b0[LY::BYTES], b1[LY::BYTES];
@@ -577,7 +579,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
     }
     const int rt0 = bx * NW * NR, tt0 = by * MT, ttiles = (a.T + 15) >> 4;
     const int tile0 = rt0 + w * NR;  // this wave's row tiles
-    const int NG = a.CK;             // groups of 32: one scale and zero point a chunk
+    const int NG = a.CK / CPG;       // groups of 32: one scale and zero point each; the planes' chunks
     // Copy of step s (groups s S ..) into buf, region by region: lane i of
     // wave w brings the 16 bytes at offset q RB + 1024 w + 16 i of the
     // region (the global-to-LDS load writes a wave's 64 x 16 bytes to
@@ -590,7 +592,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
             const int x = q * RB + tid * 16;
             if (x < LY::A) {
                 const int j = x / (S * 2048), tt = tt0 + j < ttiles ? tt0 + j : 0;
-                __builtin_amdgcn_global_load_lds(a.planes + ((int64_t)tt * a.CK + c0) * 2048 + x % (S * 2048),
+                __builtin_amdgcn_global_load_lds(a.planes + ((int64_t)tt * NG + c0) * 2048 + x % (S * 2048),
                                                  (__attribute__((address_space(3))) void *)(buf + q * RB + w * 1024), 16, 0, 0);
             }
         }
@@ -598,8 +600,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
         for (int q = 0; q < (LY::C + RB - 1) / RB; q++) {
             const int x = q * RB + tid * 16;
             if (x < LY::C) {
-                const int r = x / (S * 256), tile = rt0 + r < a.ntiles ? rt0 + r : 0;
-                __builtin_amdgcn_global_load_lds(a.codes + ((int64_t)tile * a.CK + c0) * 256 + x % (S * 256),
+                const int r = x / (S * 256 * CPG), tile = rt0 + r < a.ntiles ? rt0 + r : 0;
+                __builtin_amdgcn_global_load_lds(a.codes + ((int64_t)tile * a.CK + c0 * CPG) * 256 + x % (S * 256 * CPG),
                                                  (__attribute__((address_space(3))) void *)(buf + LY::A + q * RB + w * 1024), 16, 0,
                                                  0);
             }
@@ -655,14 +657,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
             for (int r = 0; r < NR; r++) {
                 const int e = (w * NR + r) * S + gi;  // (row tile of the workgroup, group) entry
-                const uint32_t cw = *reinterpret_cast<const uint32_t *>(cur + LY::A + e * 256 + c16 * 16 + g * 4);
                 const uint32_t zp = cur[LY::A + LY::C + e * 16 + c16];
                 const float sc = __half2float(
                     *reinterpret_cast<const __half *>(cur + LY::A + LY::C + LY::Z + e * 32 + c16 * 2));
                 // w = u - zp in fp16: (1024 + u) - (1024 + zp), both exact; inputs 0 2 4 6 1 3 5 7
                 const uint32_t z2 = zp * 0x10001u + 0x64006400u;
                 uint32_t q4[4];
-                bytes_f16(cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, q4);
+                if constexpr (BITS == 4) {  // a code dword: the 8 inputs' nibbles, even inputs low
+                    const uint32_t cw = *reinterpret_cast<const uint32_t *>(cur + LY::A + e * 256 + c16 * 16 + g * 4);
+                    bytes_f16(cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, q4);
+                } else {  // 8 code bytes (chunk g / 2 of the group, half g % 2), even inputs picked first
+                    const uint2 cw = *reinterpret_cast<const uint2 *>(cur + LY::A + e * 512 + (g >> 1) * 256 + c16 * 16 +
+                                                                      (g & 1) * 8);
+                    bytes_f16(__builtin_amdgcn_perm(cw.y, cw.x, 0x06040200u), __builtin_amdgcn_perm(cw.y, cw.x, 0x07050301u),
+                              q4);
+                }
                 v8h b;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -673,15 +682,25 @@ __global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
                 for (int j = 0; j < MT; j++) {
                     const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    v4f d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah[j]), b, z, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al[j]), b, d, 0, 0, 0);
+                    if constexpr (BITS == 4) {  // |G| < 2^24: one exact chain
+                        v4f d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah[j]), b, z, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al[j]), b, d, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[j][r][i] = fmaf(d[i], sc, acc[j][r][i]);  // tile_i16's flush
+                        for (int i = 0; i < 4; i++) acc[j][r][i] = fmaf(d[i], sc, acc[j][r][i]);  // tile_i16's flush
+                    } else {
+                        // |w| <= 255: sum 256 hi w (multiples of 256 below 2^32) and sum
+                        // lo w (below 2^21) are each exact, and their one rounded
+                        // sum is float(G), the reference's conversion of G
+                        const v4f dh = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, ah[j]), b, z, 0, 0, 0);
+                        const v4f dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, al[j]), b, z, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[j][r][i] = fmaf(dh[i] + dl[i], sc, acc[j][r][i]);
+                    }
                 }
             }
         }
     };
-    const int nsteps = a.CK / S;  // (the launcher picks S dividing the number of groups)
+    const int nsteps = NG / S;  // (the launcher picks S dividing the number of groups)
     stage(0, b0);
     for (int s = 0; s < nsteps; s += 2) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies have landed
@@ -729,7 +748,8 @@ bool gemm_mfma_supports(const llmq_mat *w, int64_t T) {
 bool gemm_f16_supports(const llmq_mat *w, int64_t T) {
     if (const char *e = getenv("LLMQ_MFMA_F16"))
         if (atoi(e) == 0) return false;
-    return gemm_mfma_supports(w, T) && w->bits == 4 && w->group == 32 && (T + 15) / 16 * 16 * w->k * 4 < (int64_t)kOOB;
+    return gemm_mfma_supports(w, T) && (w->bits == 4 || w->bits == 8) && w->group == 32 &&
+           (T + 15) / 16 * 16 * w->k * 4 < (int64_t)kOOB;
 }
 
 size_t gemm_f16_planes_bytes(const llmq_mat *w, int64_t T) { return (size_t)((T + 15) / 16 * 16) * w->k * 4; }
@@ -783,14 +803,17 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
             int x = 0, y = 0, z = 0, v = 4;
             if (sscanf(e, "%d,%d,%d,%d", &x, &y, &z, &v) >= 3) mt = x, nr = y, st = z, nw = v;
         }
-        if (w->CK % st != 0) mt = 1, nr = 1, nw = 4, st = w->CK % 2 == 0 ? 2 : 1;
+        const int ngroups = (int)(w->k / 32);
+        if (ngroups % st != 0) mt = 1, nr = 1, nw = 4, st = ngroups % 2 == 0 ? 2 : 1;
         const int rtiles = full / 16, ttiles = (int)((T + 15) / 16);
         bool ok = false;
 #define F16K(M, R, SS, NW)                                                                                          \
     if (!ok && mt == M && nr == R && st == SS && nw == NW) {                                                         \
-        hipLaunchKernelGGL((gemm_f16_kernel<M, R, SS, NW>),                                                           \
-                           dim3((unsigned)((rtiles + NW * R - 1) / (NW * R)), (unsigned)((ttiles + M - 1) / M)),       \
-                           dim3(NW * 64), 0, ctx->stream, f);                                                        \
+        const dim3 grid((unsigned)((rtiles + NW * R - 1) / (NW * R)), (unsigned)((ttiles + M - 1) / M));              \
+        if (w->bits == 4)                                                                                            \
+            hipLaunchKernelGGL((gemm_f16_kernel<M, R, SS, NW, 4>), grid, dim3(NW * 64), 0, ctx->stream, f);          \
+        else                                                                                                         \
+            hipLaunchKernelGGL((gemm_f16_kernel<M, R, SS, NW, 8>), grid, dim3(NW * 64), 0, ctx->stream, f);          \
         ok = true;                                                                                                   \
     }
         F16K(1, 1, 4, 4) F16K(1, 1, 2, 4) F16K(1, 1, 1, 4) F16K(2, 1, 4, 4) F16K(1, 2, 4, 4) F16K(1, 1, 8, 4)

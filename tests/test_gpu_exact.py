@@ -152,28 +152,29 @@ def test_prompt_gemm_bit_exact(gpu, orc, fmt, T):
         g.free()
 
 
-# Instantiations of the int4-g32 fp16 matrix-core GEMM: token tiles, row
+# Instantiations of the group-32 fp16 matrix-core GEMM: token tiles, row
 # tiles a wave, groups a step, waves a workgroup.
 F16_TILES = ["1,1,4", "1,1,2", "1,1,1", "2,1,4", "1,2,4", "1,1,8", "1,1,4,8", "2,1,4,8", "1,1,8,8"]
 
 
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("tile", F16_TILES)
-def test_prompt_gemm_f16_tiles(gpu, orc, tile, monkeypatch):
-    """Every instantiation of the int4-g32 prompt GEMM on the fp16 matrix
-    cores (LLMQ_F16_TILE) in tile_i16's order, with ragged token counts (a
-    partial token tile, a partial workgroup of row tiles) and 16 rows left
-    to rows_i16."""
+def test_prompt_gemm_f16_tiles(gpu, orc, tile, bits, monkeypatch):
+    """Every instantiation of the int4-g32 and int8-g32 prompt GEMM on the
+    fp16 matrix cores (LLMQ_F16_TILE) in tile_i16's order, with ragged token
+    counts (a partial token tile, a partial workgroup of row tiles) and 16
+    rows left to rows_i16."""
     torch, lm, ctx = gpu
     monkeypatch.setenv("LLMQ_F16_TILE", tile)
-    rng = np.random.default_rng(sum(map(int, tile.split(","))))
+    rng = np.random.default_rng(sum(map(int, tile.split(","))) + bits)
     for T, IN, OUT, flags in ((37, 768, 2304, 2), (19, 3072, 816, 1), (2, 256, 48, 0)):
         w = rng.normal(0, 0.02, (IN, OUT)).astype(np.float32)
         x = rng.normal(0, 1, (T, IN)).astype(np.float32)
         b = rng.normal(0, 0.1, OUT).astype(np.float32)
         r0 = rng.normal(0, 1, (T, OUT)).astype(np.float32)
-        note("prompt gemm f16", tile, T, IN, OUT, flags)
-        g = lm.HipQuantMatrix.from_f32(ctx, w, 4, 32, False, True)
-        o = orc.QuantMatrix.from_f32(w, 4, 32, False, True)
+        note("prompt gemm f16", bits, tile, T, IN, OUT, flags)
+        g = lm.HipQuantMatrix.from_f32(ctx, w, bits, 32, False, True)
+        o = orc.QuantMatrix.from_f32(w, bits, 32, False, True)
         out = dev(torch, r0)
         lm.linear(ctx, out, dev(torch, x), g, dev(torch, b), resid=flags == 1, gelu=flags == 2)
         ef = orc.EPI_BIAS | (orc.EPI_RESID if flags == 1 else 0) | (orc.EPI_GELU if flags == 2 else 0)
@@ -183,14 +184,17 @@ def test_prompt_gemm_f16_tiles(gpu, orc, tile, monkeypatch):
         g.free()
 
 
-def test_prompt_gemm_f16_extremes(gpu, orc):
-    """The fp16 form at the largest sums it has to hold exactly: every
-    |x| equal (codes +-32767: planes 256 * 127 + 255 and 256 * -128 + 1)
-    against groups whose weights are 31 of +a (or -a) and one 0, which
-    quantize to u - zp = +-15, so |G| = 31 * 15 * 32767 (~15.2 M, of the
-    2^24 an fp32 sum holds exactly); also the sign mixes in between."""
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prompt_gemm_f16_extremes(gpu, orc, bits):
+    """The fp16 form at the largest sums it has to hold: every |x| equal
+    (codes +-32767: planes 256 * 127 + 255 and 256 * -128 + 1) against
+    groups whose weights are 31 of +a (or -a) and one 0, which quantize to
+    u - zp = +-15 (int4: |G| = 31 * 15 * 32767, ~15.2 M, of the 2^24 one
+    exact fp32 chain holds) or +-255 (int8: |G| ~259 M, so the hi and lo
+    sums, each exact, meet in one rounded add that must equal the
+    reference's float(G)); also the sign mixes in between."""
     torch, lm, ctx = gpu
-    rng = np.random.default_rng(77)
+    rng = np.random.default_rng(77 + bits)
     IN, OUT, T = 768, 256 + 17, 20
     sign = np.where(rng.random(OUT) < 0.5, -1.0, 1.0)
     w = np.tile(0.03 * sign, (IN, 1)).astype(np.float32)
@@ -199,8 +203,8 @@ def test_prompt_gemm_f16_extremes(gpu, orc):
     x = np.where(rng.random((T, IN)) < 0.5, -1.0, 1.0).astype(np.float32)
     x[0] = 1.0
     x[1] = -1.0
-    g = lm.HipQuantMatrix.from_f32(ctx, w, 4, 32, False, True)
-    o = orc.QuantMatrix.from_f32(w, 4, 32, False, True)
+    g = lm.HipQuantMatrix.from_f32(ctx, w, bits, 32, False, True)
+    o = orc.QuantMatrix.from_f32(w, bits, 32, False, True)
     out = torch.zeros((T, OUT), dtype=torch.float32, device="cuda")
     lm.linear(ctx, out, dev(torch, x), g, None)
     want = orc.matmul_rows_a16(x, o, None, 0)
@@ -212,23 +216,25 @@ def test_prompt_gemm_f16_extremes(gpu, orc):
     g.free()
 
 
-def test_prompt_gemm_f16_matches_int8_form(gpu, orc, monkeypatch):
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prompt_gemm_f16_matches_int8_form(gpu, orc, monkeypatch, bits):
     """A 476-token prompt with the LayerNorm in front (the qkv GEMM of
-    config 3): the fp16 matrix-core form and the int8-MFMA form
-    (LLMQ_MFMA_F16=0) give the same bits, and both the oracle's."""
+    config 3, int4-g32 and int8-g32): the fp16 matrix-core form and the
+    int8-MFMA form (LLMQ_MFMA_F16=0) give the same bits, and both the
+    oracle's."""
     torch, lm, ctx = gpu
-    rng = np.random.default_rng(476)
+    rng = np.random.default_rng(476 + bits)
     T, IN, OUT = 476, 768, 2304
     w = rng.normal(0, 0.02, (IN, OUT)).astype(np.float32)
     x = rng.normal(0, 1, (T, IN)).astype(np.float32)
     lw = rng.normal(1, 0.1, IN).astype(np.float32)
     lb = rng.normal(0, 0.1, IN).astype(np.float32)
     b = rng.normal(0, 0.1, OUT).astype(np.float32)
-    g = lm.HipQuantMatrix.from_f32(ctx, w, 4, 32, False, True)
-    o = orc.QuantMatrix.from_f32(w, 4, 32, False, True)
+    g = lm.HipQuantMatrix.from_f32(ctx, w, bits, 32, False, True)
+    o = orc.QuantMatrix.from_f32(w, bits, 32, False, True)
     outs = []
     for f16 in ("1", "0"):
-        note("prompt gemm 476, LLMQ_MFMA_F16 =", f16)
+        note("prompt gemm 476", bits, "LLMQ_MFMA_F16 =", f16)
         monkeypatch.setenv("LLMQ_MFMA_F16", f16)
         out = torch.zeros((T, OUT), dtype=torch.float32, device="cuda")
         lm.linear(ctx, out, dev(torch, x), g, dev(torch, b), ln=(dev(torch, lw), dev(torch, lb)))

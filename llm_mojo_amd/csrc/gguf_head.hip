@@ -39,6 +39,7 @@ struct H16Args {
     const float *rms_g;  // optional RMSNorm gain applied to h first
     float rms_eps;
     ArgmaxPart *amax;    // optional per-workgroup argmax partials
+    int vgrid;           // gguf_head16_mf_kernel: the workgroups of gguf_head16_kernel it stands in for
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
@@ -189,8 +190,8 @@ __device__ __forceinline__ TokenRow<RV, COOP> load_token(const H16Args &a, int t
     return row;
 }
 
-template <int RV, bool COOP>
-__device__ __forceinline__ void quantize_token(const H16Args &a, TokenRow<RV, COOP> row, int me, uint32_t *xt,
+template <int RV, bool COOP, class ST>
+__device__ __forceinline__ void quantize_token(const H16Args &a, TokenRow<RV, COOP> row, int me, ST &&store,
                                                float *s_red, float *sx_out) {
     constexpr int NTH = COOP ? kNW * 64 : 64;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -249,12 +250,20 @@ __device__ __forceinline__ void quantize_token(const H16Args &a, TokenRow<RV, CO
         if (i < n4) {
             const int q0 = round_to_int(v[k].x * inv), q1 = round_to_int(v[k].y * inv);
             const int q2 = round_to_int(v[k].z * inv), q3 = round_to_int(v[k].w * inv);
-            *reinterpret_cast<uint2 *>(xt + 2 * i) = make_uint2(((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16),
-                                                                ((uint32_t)q2 & 0xFFFFu) | ((uint32_t)q3 << 16));
+            store(i, q0, q1, q2, q3);
         }
     }
     if (me == 0) *sx_out = sx;
 }
+
+// quantize_token's store into int16 pairs: inputs 4 i .. 4 i + 3 of the row.
+struct PairStore {
+    uint32_t *xt;
+    __device__ __forceinline__ void operator()(int i, int q0, int q1, int q2, int q3) const {
+        *reinterpret_cast<uint2 *>(xt + 2 * i) = make_uint2(((uint32_t)q0 & 0xFFFFu) | ((uint32_t)q1 << 16),
+                                                            ((uint32_t)q2 & 0xFFFFu) | ((uint32_t)q3 << 16));
+    }
+};
 
 // One workgroup of kNW waves; wave g = blockIdx.x * kNW + wid takes tiles
 // g, g + G, .. (G = gridDim.x * kNW) and streams their units in order, the
@@ -299,11 +308,11 @@ __global__ __launch_bounds__(kNW * 64) void gguf_head16_kernel(H16Args a) {
     if (coop) {
         for (int t = 0; t < nt; t++)
             quantize_token<RVC, true>(a, TM < kNW && t == 0 ? first : load_token<RVC, true>(a, t0 + t, tid), tid,
-                                      xq32 + (size_t)t * C2, s_red, &s_sx[t]);
+                                      PairStore{xq32 + (size_t)t * C2}, s_red, &s_sx[t]);
     } else {
         for (int t = wid; t < nt; t += kNW)
             quantize_token<kMaxC / 4 / 64, false>(a, load_token<kMaxC / 4 / 64, false>(a, t0 + t, lane), lane,
-                                                  xq32 + (size_t)t * C2, s_red, &s_sx[t]);
+                                                  PairStore{xq32 + (size_t)t * C2}, s_red, &s_sx[t]);
     }
     __syncthreads();
     float sx[TM];
@@ -433,6 +442,251 @@ done:
     }
 }
 
+// ------------------------------------------- Q6_K on the fp16 matrix cores
+//
+// A token tile of 9 to 16 tokens (the rest zero) over a Q6_K head of up to
+// 2048 columns, with the integers and float steps of gguf_head16_kernel and
+// the lane sums on the matrix cores.  Lane L of superblock u sums
+// acc[L] = sum x_k w_k over the 16 inputs k = 32 c + 2 L + i (chunks c =
+// 0..7, i = 0, 1), w = (q - 32) s with s the int8 scale of the input's
+// 16-weight half.  Split x = 256 xh + xl (xh = x >> 8, xl = x & 255) and
+// s = 8 sh + sl (sh = s >> 3, sl = s & 7): xh, xl, q' (8 sh) and q' sl
+// (q' = q - 32) are exact in fp16 and w = q' (8 sh) + q' sl, so two
+// chained v_mfma_f32_16x16x16_f16 a plane form
+//     P = sum xh w  (|P| <= 16 * 128 * 4096 = 2^23)
+//     Q = sum xl w  (|Q| <= 16 * 255 * 4096 < 2^24; every partial sum stays
+//                    below 2^24 too: |q' (8 sh)| >= |q' sl| wherever the
+//                    two differ in sign)
+// exactly, and fma(256, P, Q) is acc rounded once, the reference's
+// (float)acc[L]; then accf[L] = fma(., d, accf[L]) and red16 as there.
+//
+// Lane l (r = l % 16, g = l / 16), lane sum L: A (tokens x the 16 inputs)
+// holds 4 fp16 of token r, inputs m = 0..3 = (chunk 2 g + m / 2, weight
+// 2 L + m % 2); B the same inputs of row r; D rows r, tokens 4 g .. 4 g + 3.
+// The tokens' hi / lo planes sit in LDS as fp16 [plane][u][L][g][token][4]
+// (128 KB at 2048 columns), written by the prologue (a wave a token, the
+// arithmetic of gguf_head16_kernel's).  Workgroups of 8 waves: waves 0-3
+// and 4-7 stand in for workgroups 2 b and 2 b + 1 of gguf_head16_kernel's
+// grid (a.vgrid), taking its tiles and leaving its argmax partials.
+constexpr int kMfNW = 8;
+constexpr int kMfMaxC = 2048;
+
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// The prologue's store: codes q of inputs 4 i .. 4 i + 3 of token t as
+// their hi and lo fp16 values at the A operand's places.
+struct PlaneStore {
+    uint32_t *pl;  // [2][plane_dw]
+    uint32_t plane_dw;
+    int t;
+    __device__ __forceinline__ static uint32_t pair(int a, int b) {
+        const _Float16 ha = (_Float16)(float)a, hb = (_Float16)(float)b;
+        return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+    }
+    __device__ __forceinline__ void operator()(int i, int q0, int q1, int q2, int q3) const {
+        const int k = 4 * i, u = k >> 8, c = (k >> 5) & 7, L = (k & 31) >> 1;
+        // fp16 index of (u, L, g = c / 2, t, m = 2 (c % 2)); pair L + 1 is 256 further
+        const uint32_t f = ((((uint32_t)u * 16u + (uint32_t)L) * 4u + (uint32_t)(c >> 1)) * 16u + (uint32_t)t) * 4u +
+                           2u * (uint32_t)(c & 1);
+        pl[f / 2] = pair(q0 >> 8, q1 >> 8);
+        pl[f / 2 + 128] = pair(q2 >> 8, q3 >> 8);
+        pl[plane_dw + f / 2] = pair(q0 & 255, q1 & 255);
+        pl[plane_dw + f / 2 + 128] = pair(q2 & 255, q3 & 255);
+    }
+};
+
+// A unit's fields for lane (r, g): chunks 2 g and 2 g + 1 of row r (codes
+// and high bits), the four scales of their halves, d.
+struct MfUnit {
+    uint4 c0, c1;
+    uint2 h0, h1;
+    uint32_t sc, dw;
+};
+
+__global__ __launch_bounds__(kMfNW * 64) void gguf_head16_mf_kernel(H16Args a) {
+    extern __shared__ __align__(16) uint32_t pl[];  // fp16 [2][NU][16][4][16][4]
+    __shared__ float s_sx[16];
+    __shared__ ArgmaxPart s_best[kMfNW][16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int t0 = blockIdx.y * 16, nt = min(16, a.T - t0);
+    const int NU = a.NU;
+    const uint32_t plane_dw = (uint32_t)NU * 2048u;
+    const int v = 2 * (int)blockIdx.x + (wid >> 2);  // the gguf_head16_kernel workgroup this wave belongs to
+    const bool vlive = v < a.vgrid;
+    const int vw = v * kNW + (wid & 3), G = a.vgrid * kNW;
+    const auto rc = make_rsrc(a.codes, a.codes_bytes);
+    const auto rb = make_rsrc(a.bits, a.bits_bytes);
+    const auto rs = make_rsrc(a.sb, a.sb_bytes);
+    const auto rd = make_rsrc(a.d, a.d_bytes);
+    auto item_tile = [&](int s) { return vw + (s / NU) * G; };
+    auto load_mf = [&](int s) {
+        const int tile = item_tile(s), u = s % NU;
+        const bool ok = vlive && tile < a.ntiles;
+        const uint32_t e0 = ((uint32_t)tile * (uint32_t)a.CK + 8u * (uint32_t)u + 2u * (uint32_t)g) * 16u + (uint32_t)r;
+        const uint32_t se = ((uint32_t)tile * (uint32_t)NU + (uint32_t)u) * 16u + (uint32_t)r;
+        MfUnit w;
+        w.c0 = bload16_nt(rc, ok ? e0 * 16u : kOOB);
+        w.c1 = bload16_nt(rc, ok ? (e0 + 16u) * 16u : kOOB);
+        w.h0 = bload8_nt(rb, ok ? e0 * 8u : kOOB);
+        w.h1 = bload8_nt(rb, ok ? (e0 + 16u) * 8u : kOOB);
+        w.sc = bload4_nt(rs, ok ? se * 16u + 4u * (uint32_t)g : kOOB);
+        w.dw = bload4_nt(rd, ok ? (se * 2u) & ~3u : kOOB);
+        return w;
+    };
+    constexpr int PD = 2;
+    MfUnit ring[PD];
+#pragma unroll
+    for (int k = 0; k < PD; k++) ring[k] = load_mf(k);
+
+    // Tokens wid and wid + 8: optional RMSNorm, quantize_rows, the planes
+    // (zeros for tokens past the batch).
+    for (int t = wid; t < 16; t += kMfNW) {
+        if (t < nt) {
+            quantize_token<kMaxC / 4 / 64, false>(a, load_token<kMaxC / 4 / 64, false>(a, t0 + t, lane), lane,
+                                                  PlaneStore{pl, plane_dw, t}, nullptr, &s_sx[t]);
+        } else {
+            for (uint32_t e = (uint32_t)lane; e < (uint32_t)NU * 64u; e += 64u) {  // entries (u, L, g) of token t
+                const uint32_t f = (e * 16u + (uint32_t)t) * 2u;
+                pl[f] = 0u;
+                pl[f + 1] = 0u;
+                pl[plane_dw + f] = 0u;
+                pl[plane_dw + f + 1] = 0u;
+            }
+            if (lane == 0) s_sx[t] = 0.0f;
+        }
+    }
+    __syncthreads();
+    float sxl[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sxl[i] = s_sx[4 * g + i];
+
+    float accf[16][4];
+    float best_v[4];
+    int best_i[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int L = 0; L < 16; L++) accf[L][i] = 0.0f;
+        best_v[i] = -INFINITY;
+        best_i[i] = 0x7fffffff;
+    }
+    const v4h k1056 = {(_Float16)1056.0f, (_Float16)1056.0f, (_Float16)1056.0f, (_Float16)1056.0f};
+    for (int s0 = 0;; s0 += PD) {
+#pragma unroll
+    for (int k = 0; k < PD; k++) {
+        const int s = s0 + k;
+        const int tile = item_tile(s);
+        if (!vlive || tile >= a.ntiles) goto done;  // uniform over the wave
+        const int u = s % NU;
+        const MfUnit w = ring[k];
+        ring[k] = load_mf(s + PD);
+        const float d = h2f(w.dw >> (16 * (r & 1)));
+        // scale pieces of half h of chunks 2 g, 2 g + 1 (bytes h, 2 + h of sc),
+        // laid out as B's four inputs
+        v4h m1[2], m2[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int s0 = (int)(int8_t)((w.sc >> (8 * h)) & 255u), s1 = (int)(int8_t)((w.sc >> (8 * (2 + h))) & 255u);
+            const _Float16 a0 = (_Float16)(float)(8 * (s0 >> 3)), a1 = (_Float16)(float)(8 * (s1 >> 3));
+            const _Float16 b0 = (_Float16)(float)(s0 & 7), b1 = (_Float16)(float)(s1 & 7);
+            m1[h] = (v4h){a0, a0, a1, a1};
+            m2[h] = (v4h){b0, b0, b1, b1};
+        }
+        // 6-bit codes, bytes: qe[cc][j] byte k = weight 2 (4 j + k), qo the next one
+        uint32_t qe[2][4], qo[2][4];
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+            const uint32_t cw[4] = {cc ? w.c1.x : w.c0.x, cc ? w.c1.y : w.c0.y, cc ? w.c1.z : w.c0.z,
+                                    cc ? w.c1.w : w.c0.w};
+            const uint32_t hw[2] = {cc ? w.h1.x : w.h0.x, cc ? w.h1.y : w.h0.y};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t hb = hw[j >> 1] >> (16 * (j & 1));
+                qe[cc][j] = (cw[j] & 0x0F0F0F0Fu) | spread2(hb);
+                qo[cc][j] = ((cw[j] >> 4) & 0x0F0F0F0Fu) | spread2(hb >> 2);
+            }
+        }
+        const uint32_t *ph = pl + (uint32_t)u * 2048u + (uint32_t)lane * 2u;  // (u, L = 0, g, token r)
+#pragma unroll
+        for (int L = 0; L < 16; L++) {
+            const int j = L >> 2, kk = L & 3, h = L >> 3;
+            const uint32_t sel = (uint32_t)kk | (0x0Cu << 8) | ((uint32_t)(4 + kk) << 16) | (0x0Cu << 24);
+            // q' of B's inputs m = 0..3 (chunk 2 g + m / 2, weight 2 L + m % 2)
+            const uint2 raw = make_uint2(__builtin_amdgcn_perm(qo[0][j], qe[0][j], sel) | 0x64006400u,
+                                         __builtin_amdgcn_perm(qo[1][j], qe[1][j], sel) | 0x64006400u);
+            const v4h q4 = __builtin_bit_cast(v4h, raw) - k1056;
+            const v4h B1 = q4 * m1[h], B2 = q4 * m2[h];
+            const uint2 xh = *reinterpret_cast<const uint2 *>(ph + L * 128);
+            const uint2 xl = *reinterpret_cast<const uint2 *>(ph + plane_dw + L * 128);
+            const v4h Ah = __builtin_bit_cast(v4h, xh), Al = __builtin_bit_cast(v4h, xl);
+            const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+            v4f P = __builtin_amdgcn_mfma_f32_16x16x16f16(Ah, B1, z, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x16f16(Ah, B2, P, 0, 0, 0);
+            v4f Q = __builtin_amdgcn_mfma_f32_16x16x16f16(Al, B1, z, 0, 0, 0);
+            Q = __builtin_amdgcn_mfma_f32_16x16x16f16(Al, B2, Q, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) accf[L][i] = fmaf(fmaf(256.0f, P[i], Q[i]), d, accf[L][i]);
+        }
+        if (u == NU - 1) {  // red16 (kernels.mojo red16's halving order), times sx
+            const int row = tile * 16 + r;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 4 * g + i;
+                float a8[8], b4[4];
+#pragma unroll
+                for (int L = 0; L < 8; L++) a8[L] = accf[L][i] + accf[L + 8][i];
+#pragma unroll
+                for (int L = 0; L < 4; L++) b4[L] = a8[L] + a8[L + 4];
+                const float lg = ((b4[0] + b4[2]) + (b4[1] + b4[3])) * sxl[i];
+#pragma unroll
+                for (int L = 0; L < 16; L++) accf[L][i] = 0.0f;
+                if (t < nt && row < a.V) {
+                    a.logits[(size_t)(t0 + t) * a.V + row] = lg;
+                    if (lg > best_v[i] || (lg == best_v[i] && row < best_i[i])) {
+                        best_v[i] = lg;
+                        best_i[i] = row;
+                    }
+                }
+            }
+        }
+    }
+    }
+done:
+    if (!a.amax) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float bv = best_v[i];
+        int bi = best_i[i];
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {  // over the 16 rows of the lane group
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (r == 0) s_best[wid][4 * g + i] = ArgmaxPart{bv, bi};
+    }
+    __syncthreads();
+    if (tid < 32) {
+        const int half = tid >> 4, t = tid & 15, vv = 2 * (int)blockIdx.x + half;
+        if (vv < a.vgrid && t < nt) {
+            ArgmaxPart b = s_best[4 * half][t];
+#pragma unroll
+            for (int w = 1; w < kNW; w++) {
+                const ArgmaxPart c = s_best[4 * half + w][t];
+                if (c.v > b.v || (c.v == b.v && c.idx < b.idx)) b = c;
+            }
+            a.amax[(size_t)(t0 + t) * a.vgrid + vv] = b;
+        }
+    }
+}
+
 // Tokens a workgroup takes (the register chains per thread).
 int head16_tm(int64_t T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16; }
 
@@ -462,8 +716,33 @@ int launch_tm(llmq_ctx *ctx, const H16Args &a, int grid, int T) {
     return LLMQ_OK;
 }
 
+// gguf_head16_mf_kernel for 9 to 16 tokens a tile of a Q6_K head of up to
+// 2048 columns (LLMQ_HEAD16_MF=0: gguf_head16_kernel throughout).
+int launch_mf(llmq_ctx *ctx, H16Args a, int grid, int T) {
+    a.vgrid = grid;
+    const size_t lds = (size_t)a.NU * 16384;  // two fp16 planes of 16 tokens
+    static size_t granted = 64 * 1024;      // one host thread per context
+    if (lds > granted) {
+        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gguf_head16_mf_kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        granted = lds;
+    }
+    hipLaunchKernelGGL(gguf_head16_mf_kernel, dim3((grid + 1) / 2, (T + 15) / 16), dim3(kMfNW * 64), lds, ctx->stream,
+                       a);
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+bool mf_ok(const H16Args &a, int T, int lds_cap) {
+    if (const char *e = getenv("LLMQ_HEAD16_MF"))
+        if (e[0] == '0') return false;
+    return head16_tm(T) == 16 && a.C <= kMfMaxC && a.C % 256 == 0 && (size_t)a.NU * 16384 + 2048 <= (size_t)lds_cap;
+}
+
 template <int TYPE>
-int launch_t(llmq_ctx *ctx, const H16Args &a, int grid, int T) {
+int launch_t(llmq_ctx *ctx, const H16Args &a, int grid, int T, int lds_cap) {
+    if constexpr (TYPE == LLMQ_GGML_Q6_K)
+        if (mf_ok(a, T, lds_cap)) return launch_mf(ctx, a, grid, T);
     switch (head16_tm(T)) {
     case 1: return launch_tm<TYPE, 1>(ctx, a, grid, T);
     case 2: return launch_tm<TYPE, 2>(ctx, a, grid, T);
@@ -519,10 +798,10 @@ int launch_gguf_head16(llmq_ctx *ctx, const llmq_mat *w, const float *h, float *
         a.d = reinterpret_cast<const uint8_t *>(w->g_meta16);
         a.d_bytes = (uint32_t)(nts * 2);
         a.NU = (int)w->NG;
-        return launch_t<LLMQ_GGML_Q6_K>(ctx, a, grid, (int)T);
+        return launch_t<LLMQ_GGML_Q6_K>(ctx, a, grid, (int)T, cap);
     }
     a.d = reinterpret_cast<const uint8_t *>(w->g_meta16);
     a.d_bytes = (uint32_t)(ntc * 2);
     a.NU = (int)(w->k / 32);
-    return launch_t<LLMQ_GGML_Q8_0>(ctx, a, grid, (int)T);
+    return launch_t<LLMQ_GGML_Q8_0>(ctx, a, grid, (int)T, cap);
 }

@@ -88,13 +88,17 @@ def test_gguf_unsupported_type(gpu):
 
 @pytest.mark.parametrize("kind", ["Q6_K", "Q8_0"])
 @pytest.mark.parametrize("V,C,T,big", [(70, 512, 1, False), (300, 768, 5, False), (1000, 2048, 1, True),
-                                       (4000, 4096, 2, False), (32000, 2048, 1, False), (300, 768, 20, False)])
+                                       (4000, 4096, 2, False), (32000, 2048, 1, False), (300, 768, 20, False),
+                                       (32000, 2048, 16, False), (32000, 2048, 16, True), (1000, 2048, 9, True),
+                                       (600, 2048, 33, False)])
 def test_gguf_int16_head_exact(gpu, orc, kind, V, C, T, big):
     """head_i16 (kernels.mojo:693-736) for Q6_K / Q8_0 heads: the logits equal
     the oracle's dot_row_i16 * sx bit for bit (same int32 lanes, same float
     chain over superblocks / blocks, same 16-lane sum).  (32000, 2048) is the
     TinyLlama Q6_K head; "big" alternates +-(0.9..1) so the int16 codes sit
-    near +-32767 and Q6_K's lane sums near 2^31."""
+    near +-32767 and Q6_K's lane sums near 2^31.  From 9 tokens a Q6_K head
+    takes the fp16 matrix-core kernel (token tiles of 16, the last one
+    partial at 9, 20 and 33 tokens)."""
     torch, lm, ctx = gpu
     from llm_mojo_amd import synth
 

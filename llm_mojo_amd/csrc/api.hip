@@ -814,8 +814,15 @@ static int gpt2_enqueue(llmq_gpt2 *m, int T, int pos0, bool device_step, bool wi
             q.flags = LLMQ_BIAS;
             q.xq_out = dbg_slot(m, T, 4 * l);
             if (fold && l == 0) q.emb = &ef;
+            // prompts: the GEMM's epilogue stores the keys and values (else kv_store_kernel)
+            KvFold kf;
+            kf.cache = m->kv;
+            kf.layer = l;
+            kf.pos0 = pos0;
+            const bool kv_fold = T > 1 && w[0]->a16 && gemm_kv_fold_ok(w[0], T, m->kv);
+            if (kv_fold) q.kv = &kf;
             RC(gpt2_linear(m, q));
-            if (T > 1) RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
+            if (T > 1 && !kv_fold) RC(launch_kv_store(ctx, m->kv, l, pos0, pos_dev, m->qkv, T, 3 * C));
             RC(launch_kv_attend(ctx, m->kv, m->att, m->qkv, l, T, pos0, pos_dev, 3 * C, T == 1));
         }
         GemvRequest p;

@@ -235,6 +235,14 @@ struct EmbedFold {
     float *x = nullptr;
 };
 
+// A prompt's QuantKV.store (kv_store_kernel, attn.hip) done by the qkv
+// GEMM's epilogue: the workgroups whose 64 rows are one head's keys or
+// values quantize them for positions pos0 .. pos0 + T - 1 of `layer`.
+struct KvFold {
+    llmq_kv *cache = nullptr;  // QuantKV (float scales), head_dim 64
+    int layer = 0, pos0 = 0;
+};
+
 struct GemvRequest {
     const llmq_mat *w = nullptr;
     const float *x = nullptr;  // [T, ldx]
@@ -255,6 +263,7 @@ struct GemvRequest {
     size_t ws_cap = 0;             // its size in bytes
     const EmbedFold *emb = nullptr;  // the embed step in the prologue (x unused; exact one-token kernel)
     int *state_copy = nullptr;       // the kernel copies state_copy[2..3] to [0..1] (exact one-token kernel)
+    const KvFold *kv = nullptr;      // the cache store in the prompt GEMM's epilogue (gemm_kv_fold_ok)
 };
 int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq);
 // Number of argmax partials launch_gemv_a16 writes for a T == 1 GEMV of w
@@ -268,6 +277,9 @@ bool gemv1_supports(const llmq_mat *w, bool ln);
 // the codes also go there as fp16 planes and the fp16 matrix-core form runs.
 bool gemm_mfma_supports(const llmq_mat *w, int64_t T);
 bool gemm_f16_supports(const llmq_mat *w, int64_t T);
+// Whether launch_gemv_a16 takes w's T-token product on the fp16 GEMM in the
+// tile whose epilogue can store the key / value rows (GemvRequest::kv).
+bool gemm_kv_fold_ok(const llmq_mat *w, int64_t T, const llmq_kv *cache);
 size_t gemm_f16_planes_bytes(const llmq_mat *w, int64_t T);
 int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *sx, uint8_t *planes);
 int launch_gemv1(llmq_ctx *ctx, const GemvRequest &rq);

@@ -533,6 +533,11 @@ struct F16Args {
     int64_t ldo;
     int T, n, ntiles, CK, flags;
     int xcd;  // XCD-aware workgroup order
+    // KV: QuantKV.store of the key / value rows (a workgroup's 64 rows are
+    // one head's q, k or v: rows 64 b of the qkv matrix, b = part * heads + head)
+    int8_t *k8, *v8;
+    float *ks, *vs;
+    int kv_layer, kv_pos0, kv_max_t, kv_heads;
 };
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -556,8 +561,9 @@ struct F16Lds {
     static constexpr int BYTES = A + C + Z + SC;
 };
 
-template <int MT, int NR, int S, int NW, int BITS>
+template <int MT, int NR, int S, int NW, int BITS, bool KV>
 __global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
+    static_assert(!KV || (MT == 1 && NR == 1 && NW == 4), "the cache store takes 64-row workgroups");
     constexpr int CPG = BITS / 4;  // code chunks a group of 32
     using LY = F16Lds<MT, NR, S, NW, CPG>;
     constexpr int RB = NW * 1024;  // bytes a copy round: 16 a lane
@@ -713,6 +719,55 @@ __global__ __launch_bounds__(NW * 64) void gemm_f16_kernel(F16Args a) {
         if (s + 2 < nsteps) stage(s + 2, b0);
         compute(b1);
     }
+    if constexpr (KV) {
+        // QuantKV.store (kvcache.mojo:333-342) of a key / value head: per
+        // token s = max|x| / 127 over its 64 rows (1 if zero), codes
+        // round(x / s), from the values the epilogue below stores (bias only).
+        const int blk = (rt0 * 16) >> 6, part = blk / a.kv_heads, head = blk % a.kv_heads;
+        if (part >= 1 && part <= 2 && rt0 * 16 + 64 <= a.n) {  // (uniform over the workgroup)
+            float xv[4], m[4];
+            const int o = tile0 * 16 + c16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = acc[0][0][i] * sxr[0][i];
+                if (a.flags & LLMQ_BIAS) v += bor[0];
+                xv[i] = v;
+                m[i] = fmaxf(0.0f, fabsf(v));  // kv_store_kernel's running max from 0
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int off = 8; off > 0; off >>= 1) m[i] = fmaxf(m[i], __shfl_xor(m[i], off));  // the 16 rows
+            __shared__ float mx[4 * 16];                   // [wave][token]
+            __shared__ __align__(16) int8_t cq[16 * 64];   // [token][row of the head]
+            if (c16 == 0)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx[w * 16 + 4 * g + i] = m[i];
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tl = 4 * g + i;
+                const float mm = fmaxf(fmaxf(mx[tl], mx[16 + tl]), fmaxf(mx[32 + tl], mx[48 + tl]));
+                float sc = mm / 127.0f;
+                if (sc == 0.0f) sc = 1.0f;
+                const float inv = 1.0f / sc;
+                cq[tl * 64 + (o & 63)] = (int8_t)llmq_to_int(roundf(xv[i] * inv));
+                if (w == 0 && c16 == 0) {
+                    const int tok = tt0 * 16 + tl;
+                    const int64_t sl = ((int64_t)a.kv_layer * a.kv_max_t + a.kv_pos0 + tok) * a.kv_heads + head;
+                    if (tok < a.T) (part == 1 ? a.ks : a.vs)[sl] = sc;
+                }
+            }
+            __syncthreads();
+            // each thread one dword: token tid / 16, rows 4 (tid % 16) ..
+            const int tl = tid >> 4, tok = tt0 * 16 + tl;
+            if (tok < a.T) {
+                const int64_t sl = ((int64_t)a.kv_layer * a.kv_max_t + a.kv_pos0 + tok) * a.kv_heads + head;
+                reinterpret_cast<uint32_t *>((part == 1 ? a.k8 : a.v8) + sl * 64)[tid & 15] =
+                    reinterpret_cast<const uint32_t *>(cq)[tid];
+            }
+        }
+    }
     // Epilogue (store_out): tile_i16's acc * sx + b, then GELU / residual.
     if (tile0 * 16 >= a.n) return;
 #pragma unroll
@@ -754,12 +809,25 @@ bool gemm_f16_supports(const llmq_mat *w, int64_t T) {
 
 size_t gemm_f16_planes_bytes(const llmq_mat *w, int64_t T) { return (size_t)((T + 15) / 16 * 16) * w->k * 4; }
 
+bool gemm_kv_fold_ok(const llmq_mat *w, int64_t T, const llmq_kv *cache) {
+    if (const char *e = getenv("LLMQ_KV_FOLD"))
+        if (e[0] == '0') return false;
+    if (const char *e = getenv("LLMQ_F16_TILE"))  // measurement tiles keep kv_store_kernel
+        if (e[0]) return false;
+    const int min_t = exact_order() ? 2 : 8;
+    if (getenv("LLMQ_MFMA_MIN_T")) return false;
+    if (!cache || cache->integer || cache->head_dim != 64 || T < min_t || !w->a16) return false;
+    const int64_t C = (int64_t)cache->n_head * 64;
+    return gemm_f16_supports(w, T) && w->n == 3 * C && w->n % 64 == 0;
+}
+
 int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *sx, uint8_t *planes) {
     const llmq_mat *w = rq.w;
     const int64_t T = rq.T, K = w->k;
     const int64_t ldx = rq.ldx ? rq.ldx : K;
     LLMQ_REQUIRE(gemm_mfma_supports(w, T), "linear: no MFMA GEMM for this matrix");
     LLMQ_REQUIRE(!planes || gemm_f16_supports(w, T), "linear: fp16 planes given for a matrix the fp16 GEMM does not take");
+    LLMQ_REQUIRE(!rq.kv || planes, "linear: the key / value store needs the fp16 GEMM");
     const int upt = (int)((K / 4 + 255) / 256);
     const bool ln = rq.ln_w != nullptr;
 #define ACTQ(L, U) hipLaunchKernelGGL((act_q16_kernel<L, U>), dim3((unsigned)T), dim3(256), L ? K * 4 : 0, ctx->stream, rq.x, ldx, \
@@ -807,13 +875,41 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
         if (ngroups % st != 0) mt = 1, nr = 1, nw = 4, st = ngroups % 2 == 0 ? 2 : 1;
         const int rtiles = full / 16, ttiles = (int)((T + 15) / 16);
         bool ok = false;
+        if (rq.kv) {  // the default tile with the cache store in its epilogue
+            LLMQ_REQUIRE(gemm_kv_fold_ok(w, T, rq.kv->cache) && mt == 1 && nr == 1 && nw == 4 && full == w->n,
+                         "linear: no key / value store in this GEMM's epilogue");
+            const llmq_kv *kv = rq.kv->cache;
+            LLMQ_REQUIRE(rq.kv->layer >= 0 && rq.kv->layer < kv->n_layer && rq.kv->pos0 >= 0 &&
+                             rq.kv->pos0 + T <= kv->max_t,
+                         "linear: cache positions %d..%lld of layer %d out of range", rq.kv->pos0,
+                         (long long)(rq.kv->pos0 + T - 1), rq.kv->layer);
+            f.k8 = kv->k;
+            f.v8 = kv->v;
+            f.ks = kv->ks;
+            f.vs = kv->vs;
+            f.kv_layer = rq.kv->layer;
+            f.kv_pos0 = rq.kv->pos0;
+            f.kv_max_t = kv->max_t;
+            f.kv_heads = kv->n_head;
+            const dim3 grid((unsigned)(rtiles / 4), (unsigned)ttiles);
+#define F16KV(SS)                                                                                                   \
+    if (!ok && st == SS) {                                                                                          \
+        if (w->bits == 4)                                                                                           \
+            hipLaunchKernelGGL((gemm_f16_kernel<1, 1, SS, 4, 4, true>), grid, dim3(256), 0, ctx->stream, f);        \
+        else                                                                                                        \
+            hipLaunchKernelGGL((gemm_f16_kernel<1, 1, SS, 4, 8, true>), grid, dim3(256), 0, ctx->stream, f);        \
+        ok = true;                                                                                                  \
+    }
+            F16KV(4) F16KV(2) F16KV(1)
+#undef F16KV
+        }
 #define F16K(M, R, SS, NW)                                                                                          \
     if (!ok && mt == M && nr == R && st == SS && nw == NW) {                                                         \
         const dim3 grid((unsigned)((rtiles + NW * R - 1) / (NW * R)), (unsigned)((ttiles + M - 1) / M));              \
         if (w->bits == 4)                                                                                            \
-            hipLaunchKernelGGL((gemm_f16_kernel<M, R, SS, NW, 4>), grid, dim3(NW * 64), 0, ctx->stream, f);          \
+            hipLaunchKernelGGL((gemm_f16_kernel<M, R, SS, NW, 4, false>), grid, dim3(NW * 64), 0, ctx->stream, f);   \
         else                                                                                                         \
-            hipLaunchKernelGGL((gemm_f16_kernel<M, R, SS, NW, 8>), grid, dim3(NW * 64), 0, ctx->stream, f);          \
+            hipLaunchKernelGGL((gemm_f16_kernel<M, R, SS, NW, 8, false>), grid, dim3(NW * 64), 0, ctx->stream, f);   \
         ok = true;                                                                                                   \
     }
         F16K(1, 1, 4, 4) F16K(1, 1, 2, 4) F16K(1, 1, 1, 4) F16K(2, 1, 4, 4) F16K(1, 2, 4, 4) F16K(1, 1, 8, 4)

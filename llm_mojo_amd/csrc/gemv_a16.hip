@@ -488,6 +488,7 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
     LLMQ_REQUIRE(!rq.dbg || (rq.T == 1 && !rq.ln_w), "linear: chunk sums need T == 1 without LayerNorm");
     // (the int8 head kernel keeps no per-chunk sums: chunk-sum requests for
     // it take gemv1)
+    LLMQ_REQUIRE(!rq.kv || rq.T > 1, "linear: the key / value store is for prompts");
     const bool exact = rq.T == 1 && exact_order() && gemv_exact_supports(w) && !(rq.dbg && w->bits == 8);
     LLMQ_REQUIRE(exact || !(rq.emb || rq.state_copy), "linear: the embed step and the state copy need the exact kernel");
     if (exact) return launch_gemv_exact(ctx, rq);
@@ -519,6 +520,7 @@ int launch_gemv_a16(llmq_ctx *ctx, const GemvRequest &rq) {
                                     f16 ? base + need : nullptr);
         }
     }
+    LLMQ_REQUIRE(!rq.kv, "linear: the key / value store needs the prompt GEMM");
     const size_t max_lds = 64 * 1024;
     int mt = 1;
     if (rq.T > 1) {

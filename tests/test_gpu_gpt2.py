@@ -98,6 +98,45 @@ def test_gpt2_steps_per_graph_same_tokens(gpu, orc, models, monkeypatch, k):
     assert got.tolist() == want
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gpt2_prompt_kv_store_in_gemm(gpu, orc, weights, monkeypatch, bits):
+    """A prompt's keys and values go to the int8 cache from the qkv GEMM's
+    epilogue (the workgroups whose 64 rows are one head's keys or values)
+    instead of kv_store_kernel (LLMQ_KV_FOLD=0): after a 40-token prompt
+    (a partial last token tile) and two decode tokens, both models' logits
+    are the same bits at every step.  The prompt's logits are the oracle's
+    bits for both formats; so are the decode steps' for int4-g32 (int8-g32's
+    one-token GEMV runs in free order: its int16 codes can flip, so its bar
+    is the code-flip spread, 2e-3 of max |logit|, and top-1)."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import gpt2, synth
+
+    prompt = [int(v) for v in synth.prompt_ids(4040 + bits, 40)]
+    monkeypatch.setenv("LLMQ_KV_FOLD", "0")
+    plain = lm.GPT2(ctx, weights, bits=bits, group=32)
+    monkeypatch.delenv("LLMQ_KV_FOLD")
+    fold = lm.GPT2(ctx, weights, bits=bits, group=32)
+    ref = orc.GPT2(gpt2.params_list(weights), bits=bits, group=32)
+    print("kv store in gemm: prompt", bits, flush=True)
+    monkeypatch.setenv("LLMQ_KV_FOLD", "0")
+    la = plain.forward(prompt, 0)
+    monkeypatch.delenv("LLMQ_KV_FOLD")
+    lb, lo = fold.forward(prompt, 0), ref.forward(prompt, 0)
+    assert bits_equal(la, lb) and bits_equal(lb, lo)
+    pos = len(prompt)
+    for i in range(2):
+        nxt = orc.argmax(lo)
+        la, lb, lo = plain.forward([nxt], pos), fold.forward([nxt], pos), ref.forward([nxt], pos)
+        pos += 1
+        assert bits_equal(la, lb), i
+        if bits == 4:
+            assert bits_equal(lb, lo), i
+        else:
+            assert np.max(np.abs(lb - lo)) / np.max(np.abs(lo)) < 2e-3 and int(np.argmax(lb)) == orc.argmax(lo), i
+    plain.free()
+    fold.free()
+
+
 def test_gpt2_fused_qkv_attention(gpu, orc, weights, monkeypatch):
     """Decode tokens through the fused qkv + attention kernel (a faster form
     for long contexts, whose attention sums run in another order: not the

@@ -266,12 +266,15 @@ __global__ __launch_bounds__(kAttnThreads) void kv_attend_kernel(const float *__
 //  2. per token (NTH / TQ threads): maximum, exponentials, the total added
 //     in position order by one lane, the weights (e / total) * vs;
 //  3. per token and dimension the fma chain over positions in order, values
-//     staged as floats, 64 TQ / NTH dimensions of one token a thread.
+//     staged as floats: with 16 tokens and SV, 256 threads each run four
+//     chains, tokens j and j + 8 times dimensions 2 d and 2 d + 1 (one read
+//     of a value pair for two tokens); else 64 TQ / NTH dimensions of one
+//     token a thread.
 // One wave issues a VALU instruction every ~6 cycles, so the larger
 // workgroup (two waves a SIMD) is the faster one.
 constexpr int kKStr = 68;  // floats per staged key row (bank spread)
 
-template <int NTH, int TQ>
+template <int NTH, int TQ, bool SV>
 __global__ __launch_bounds__(NTH) void attend_prompt_exact_kernel(const float *__restrict__ qkv, int64_t ld, int pos0,
                                                                   int T, int layer, int max_t, int n_head,
                                                                   const int8_t *__restrict__ K8,
@@ -417,8 +420,80 @@ __global__ __launch_bounds__(NTH) void attend_prompt_exact_kernel(const float *_
         }
         lds_barrier();
 
-        // 3. the value chains: thread (token ti, dimensions DPT dg ..)
-        {
+        // 3. the value chains
+        if constexpr (SV && TQ == 16) {
+            // thread (tokens j, j + 8; dimensions 2 d, 2 d + 1), j = tid / 32, d = tid % 32
+            const bool act = tid < 256;
+            const int ja = (tid >> 5) & 7, jb = ja + 8, dd = 2 * (tid & 31);
+            const int pa = act && t0 + ja < T ? pos0 + t0 + ja : -1, pb = act && t0 + jb < T ? pos0 + t0 + jb : -1;
+            const float *wa = sc + ja * NPS, *wb = sc + jb * NPS;
+            float aa0 = 0.0f, aa1 = 0.0f, ab0 = 0.0f, ab1 = 0.0f;
+            for (int c0 = 0; c0 < npb; c0 += PC) {
+                commit(c0, HD, false);
+                lds_barrier();
+                if (c0 + PC < npb) fetch(V8, c0 + PC, false);
+                // this chunk's positions of each token (pb >= pa)
+                const int ca = pa + 1 - c0 < PC ? pa + 1 - c0 : PC, cb = pb + 1 - c0 < PC ? pb + 1 - c0 : PC;
+                int sl = 0;
+                for (; sl + 8 <= ca; sl += 8) {  // both tokens: a batch's reads, then the fmas in order
+                    float xa[8], xb[8];
+                    float2 v[8];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        xa[k] = wa[c0 + sl + k];
+                        xb[k] = wb[c0 + sl + k];
+                        v[k] = *reinterpret_cast<const float2 *>(kf + (sl + k) * HD + dd);
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        aa0 = fmaf(xa[k], v[k].x, aa0);
+                        aa1 = fmaf(xa[k], v[k].y, aa1);
+                        ab0 = fmaf(xb[k], v[k].x, ab0);
+                        ab1 = fmaf(xb[k], v[k].y, ab1);
+                    }
+                }
+                for (; sl < ca; sl++) {
+                    const float2 v = *reinterpret_cast<const float2 *>(kf + sl * HD + dd);
+                    const float xa = wa[c0 + sl], xb = wb[c0 + sl];
+                    aa0 = fmaf(xa, v.x, aa0);
+                    aa1 = fmaf(xa, v.y, aa1);
+                    ab0 = fmaf(xb, v.x, ab0);
+                    ab1 = fmaf(xb, v.y, ab1);
+                }
+                for (; sl + 8 <= cb; sl += 8) {  // token j + 8's further positions
+                    float xb[8];
+                    float2 v[8];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        xb[k] = wb[c0 + sl + k];
+                        v[k] = *reinterpret_cast<const float2 *>(kf + (sl + k) * HD + dd);
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        ab0 = fmaf(xb[k], v[k].x, ab0);
+                        ab1 = fmaf(xb[k], v[k].y, ab1);
+                    }
+                }
+                for (; sl < cb; sl++) {
+                    const float2 v = *reinterpret_cast<const float2 *>(kf + sl * HD + dd);
+                    const float xb = wb[c0 + sl];
+                    ab0 = fmaf(xb, v.x, ab0);
+                    ab1 = fmaf(xb, v.y, ab1);
+                }
+                lds_barrier();
+            }
+            if (pa >= 0) {
+                float *o = out + (int64_t)(t0 + ja) * ldo + (int64_t)h * HD + dd;
+                o[0] = aa0;
+                o[1] = aa1;
+            }
+            if (pb >= 0) {
+                float *o = out + (int64_t)(t0 + jb) * ldo + (int64_t)h * HD + dd;
+                o[0] = ab0;
+                o[1] = ab1;
+            }
+        } else {
+            // thread (token ti, dimensions DPT dg ..)
             const int ti = tid / TPT, dg = tid % TPT;
             const int ipos = t0 + ti < T ? pos0 + t0 + ti : -1;
             const float *wr = sc + ti * NPS;
@@ -1070,7 +1145,7 @@ static int attend_hd(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
 
 // The exact-order prompt attention (head_dim 64); LLMQ_PROMPT_NTH /
 // LLMQ_PROMPT_TQ choose other workgroup shapes, for measurement.
-template <int NTH, int TQ>
+template <int NTH, int TQ, bool SV = false>
 static int prompt_exact_launch(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *qkv, int layer, int T,
                                int pos0, int64_t ld) {
     const int C = kv->n_head * 64;
@@ -1079,12 +1154,12 @@ static int prompt_exact_launch(llmq_ctx *ctx, const llmq_kv *kv, float *out, con
     const size_t lds = sizeof(float) * ((size_t)PC * kKStr + PC + NP + (size_t)TQ * (NP + 1));
     static size_t granted = 64 * 1024;
     if (lds > granted) {
-        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_prompt_exact_kernel<NTH, TQ>),
+        LLMQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_prompt_exact_kernel<NTH, TQ, SV>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         granted = lds;
     }
     const int nblk = (T + TQ - 1) / TQ;
-    hipLaunchKernelGGL((attend_prompt_exact_kernel<NTH, TQ>), dim3(kv->n_head, (nblk + 1) / 2), dim3(NTH), lds,
+    hipLaunchKernelGGL((attend_prompt_exact_kernel<NTH, TQ, SV>), dim3(kv->n_head, (nblk + 1) / 2), dim3(NTH), lds,
                        ctx->stream, qkv, ld ? ld : 3 * C, pos0, T, layer, kv->max_t, kv->n_head, kv->k, kv->v, kv->ks,
                        kv->vs, out, (int64_t)C, NP);
     LLMQ_HIP(hipGetLastError());
@@ -1111,8 +1186,13 @@ int launch_kv_attend(llmq_ctx *ctx, const llmq_kv *kv, float *out, const float *
         const int tq = e ? atoi(e) : 16, nth = n ? atoi(n) : 512;
         if (nth == 256) return tq == 8 ? prompt_exact_launch<256, 8>(ctx, kv, out, qkv, layer, T, pos0, ld)
                                        : prompt_exact_launch<256, 16>(ctx, kv, out, qkv, layer, T, pos0, ld);
-        return tq == 8 ? prompt_exact_launch<512, 8>(ctx, kv, out, qkv, layer, T, pos0, ld)
-                       : prompt_exact_launch<512, 16>(ctx, kv, out, qkv, layer, T, pos0, ld);
+        if (tq == 8) return prompt_exact_launch<512, 8>(ctx, kv, out, qkv, layer, T, pos0, ld);
+        // value chains four a thread (LLMQ_PROMPT_SV=0: two a thread): 476
+        // tokens, same box, 1.50 / 1.62 ms against 1.51 / 1.64 (int4 / int8
+        // prefill); two queries a lane in the scores measured slower (1.58)
+        const char *sv = getenv("LLMQ_PROMPT_SV");
+        if (sv && sv[0] == '0') return prompt_exact_launch<512, 16, false>(ctx, kv, out, qkv, layer, T, pos0, ld);
+        return prompt_exact_launch<512, 16, true>(ctx, kv, out, qkv, layer, T, pos0, ld);
     }
     if (kv->head_dim == 64) return attend_hd<64>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);
     if (kv->head_dim == 128) return attend_hd<128>(ctx, kv, out, qkv, layer, T, pos0, pos_dev, ld, store);

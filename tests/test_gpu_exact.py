@@ -271,6 +271,15 @@ def test_attention_bit_exact(gpu, orc, T, pos0):
     kv.free()
 
 
+@pytest.mark.parametrize("T,pos0", [(476, 0), (37, 300)])
+def test_prompt_attention_two_chain_form(gpu, orc, T, pos0, monkeypatch):
+    """The prompt attention's value pass with two chains a thread
+    (LLMQ_PROMPT_SV=0; the default runs four, two tokens x two
+    dimensions): the same bits as attend_float_one's."""
+    monkeypatch.setenv("LLMQ_PROMPT_SV", "0")
+    test_attention_bit_exact(gpu, orc, T, pos0)
+
+
 def act_layout(K):
     ck = K // 32
     xq = ck * 72

@@ -828,6 +828,8 @@ int launch_gemm_mfma(llmq_ctx *ctx, const GemvRequest &rq, int16_t *xq, float *s
     LLMQ_REQUIRE(gemm_mfma_supports(w, T), "linear: no MFMA GEMM for this matrix");
     LLMQ_REQUIRE(!planes || gemm_f16_supports(w, T), "linear: fp16 planes given for a matrix the fp16 GEMM does not take");
     LLMQ_REQUIRE(!rq.kv || planes, "linear: the key / value store needs the fp16 GEMM");
+    LLMQ_REQUIRE(!rq.kv || !(rq.flags & (LLMQ_GELU | LLMQ_RESID)),
+                 "linear: the key / value store takes the product plus bias only");
     const int upt = (int)((K / 4 + 255) / 256);
     const bool ln = rq.ln_w != nullptr;
 #define ACTQ(L, U) hipLaunchKernelGGL((act_q16_kernel<L, U>), dim3((unsigned)T), dim3(256), L ? K * 4 : 0, ctx->stream, rq.x, ldx, \

@@ -121,6 +121,15 @@ def test_gguf_int16_head_exact(gpu, orc, kind, V, C, T, big):
     assert np.array_equal(got, want), np.max(np.abs(got - want))
 
 
+@pytest.mark.parametrize("V,C,T,big", [(32000, 2048, 16, True), (300, 768, 20, False)])
+def test_gguf_int16_head_valu_form(gpu, orc, V, C, T, big, monkeypatch):
+    """The Q6_K head's VALU kernel at 9-16 tokens a tile (LLMQ_HEAD16_MF=0;
+    the default takes the matrix cores there): the same bits as the
+    oracle's."""
+    monkeypatch.setenv("LLMQ_HEAD16_MF", "0")
+    test_gguf_int16_head_exact(gpu, orc, "Q6_K", V, C, T, big)
+
+
 def test_gguf_float_heads_take_the_float_path(gpu, orc):
     """kernels.head: Q4_K has no int16 kernel, so its head is the float GEMV."""
     torch, lm, ctx = gpu

@@ -80,6 +80,24 @@ def test_gpt2_embed_fold_same_tokens(gpu, orc, models, weights, monkeypatch):
     plain.free()
 
 
+@pytest.mark.parametrize("n_prompt,steps", [(1, 20), (1000, 30)])
+def test_gpt2_generate_edges(gpu, orc, models, n_prompt, steps):
+    """generate at the edges of its range: a one-token prompt (its forward
+    takes the one-token kernels; the decode graph starts at position 1), and
+    a 1000-token prompt asked for 30 tokens, which gpt2t.mojo:945 clamps to
+    the 24 that fit the 1024 positions (the last decode step writes the
+    cache's last slot).  The tokens are the oracle's greedy ones."""
+    torch, lm, ctx = gpu
+    from llm_mojo_amd import synth
+
+    model, ref = models
+    prompt = [int(v) for v in synth.prompt_ids(5000 + n_prompt, n_prompt)]
+    want = list(ref.generate(prompt, min(steps, 1024 - n_prompt)))  # the oracle takes the clamped count
+    print("generate edges", n_prompt, steps, flush=True)
+    got, _, _ = model.generate(prompt, steps)
+    assert got.tolist() == want
+
+
 @pytest.mark.parametrize("k", [1, 3, 64])
 def test_gpt2_steps_per_graph_same_tokens(gpu, orc, models, monkeypatch, k):
     """k decode steps captured as one graph (LLMQ_GRAPH_STEPS; the remainder

@@ -37,6 +37,7 @@
 // (tokens 4 (l / 16) + i, row l % 16).  The waves' partial sums are added in
 // LDS in wave order.
 #include "common.h"
+#include <type_traits>
 
 namespace {
 
@@ -112,16 +113,22 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
-// Weight loads: non-temporal when no other workgroup reads the same weights
-// (`nt`, uniform), else cached for the other token tiles.
-__device__ __forceinline__ uint4 wload16(__amdgpu_buffer_rsrc_t r, uint32_t off, bool nt) {
-    const auto v = nt ? __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2)
-                      : __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+// Weight loads with cache policy AUX: 2 (non-temporal) when no other
+// workgroup reads the same weights, else 0 (cached for the other token
+// tiles).  A constant part of the offset goes in the scalar offset, so that
+// the loads of one base share its vector register.
+template <int AUX>
+__device__ __forceinline__ uint4 wload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ uint32_t wload4(__amdgpu_buffer_rsrc_t r, uint32_t off, bool nt) {
-    return nt ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 2)
-              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+template <int AUX>
+__device__ __forceinline__ uint32_t wload4(__amdgpu_buffer_rsrc_t r, uint32_t off, int soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, soff, AUX);
+}
+__device__ __forceinline__ uint4 bload16s(__amdgpu_buffer_rsrc_t r, uint32_t off, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
 }
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
@@ -303,9 +310,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
     const bool nrm = NRM && a.ssq && w == 0;
     const int nq4 = a.C / 256;  // float4 a lane: a quarter of the token's C / 16 halves
     const float4 *p4 = reinterpret_cast<const float4 *>(a.ssq + (int64_t)(tt * 16 + c16) * (a.C / 16) + g * 4 * nq4);
-    float4 sqv[kSq];
+    float4 sqv[kSq];  // (set and read by wave 0 only)
+    if (nrm && kSq > 1) {
 #pragma unroll
-    for (int k = 0; k < kSq; k++) sqv[k] = nrm && kSq > 1 && k < nq4 ? p4[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int k = 0; k < kSq; k++) sqv[k] = k < nq4 ? p4[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     const int per = (a.NSB + NW - 1) / NW;  // superblocks a wave
     const int s0 = w * per, s1 = min(a.NSB, s0 + per);
     const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, km1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
@@ -314,18 +323,26 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
     for (int r = 0; r < RT; r++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[r][i] = 0.0f;
-    // the weights (block fields and code dwords) of superblock sbi
-    auto load_w = [&](int sbi, uint4 (&f)[RT], uint32_t (&cw)[RT][8]) {
+    // the weights (block fields and code dwords) of superblock sbi, the
+    // cache policy chosen once for all of them
+    auto load_w_pol = [&](auto pol, int sbi, uint4 (&f)[RT], uint32_t (&cw)[RT][8]) {
+        constexpr int AUX = decltype(pol)::value;
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             const int tl = tile_of(r);
             const bool ok = tl < a.ntiles;
-            f[r] = wload16(rs, ok ? (uint32_t)(((tl * a.NSB + sbi) * 16 + c16) * 16) : kOOB, a.stream);
+            f[r] = wload16<AUX>(rs, ok ? (uint32_t)(((tl * a.NSB + sbi) * 16 + c16) * 16) : kOOB);
             // chunk entries of one row tile are 256 bytes apart (kOOB + 256 u stays out of range)
             const uint32_t cb = ok ? (uint32_t)(((tl * a.CK + sbi * 8) * 16 + c16) * 16 + g * 4) : kOOB;
 #pragma unroll
-            for (int u = 0; u < 8; u++) cw[r][u] = wload4(rc, cb + 256u * u, a.stream);
+            for (int u = 0; u < 8; u++) cw[r][u] = wload4<AUX>(rc, cb, 256 * u);
         }
+    };
+    auto load_w = [&](int sbi, uint4 (&f)[RT], uint32_t (&cw)[RT][8]) {
+        if (a.stream)
+            load_w_pol(std::integral_constant<int, 2>{}, sbi, f, cw);
+        else
+            load_w_pol(std::integral_constant<int, 0>{}, sbi, f, cw);
     };
     // A wave with several superblocks (the down matrix at batch 16) has the
     // next one's weights in flight while it computes one, issued after the
@@ -341,8 +358,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_h16_q4k_kernel(HArgs a) {
         const uint32_t ab = (uint32_t)((tt * a.KB + sbi * 8) * 2048 + lane * 16);
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            ah[u] = bload16(rp, ab + 2048u * u);
-            al[u] = bload16(rp, ab + 2048u * u + 1024u);
+            ah[u] = bload16s(rp, ab, 2048 * u);
+            al[u] = bload16s(rp, ab, 2048 * u + 1024);
         }
         // sums planes: hi in group 0, lo in group 1, zeros in groups 2 and 3
         // (h16s: all four groups); the scales (h16s: the token's exponents)

@@ -357,6 +357,9 @@ int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *ro
 // Greedy pick of each of B sequences from a head's argmax partials (nparts
 // per sequence), the decode state advanced, and the picked rows of the GGUF
 // embedding E into dst + b * ldd (gguf.hip).
+int launch_gguf_pick_embed_rec(llmq_ctx *ctx, const llmq_mat *E, const ArgmaxPart *parts, int nparts, int B,
+                               int *state, int64_t *next, int64_t *gen, float *dst, int64_t ldd, void *rec,
+                               const float *rgain);
 int launch_gguf_pick_embed(llmq_ctx *ctx, const llmq_mat *E, const ArgmaxPart *parts, int nparts, int B, int *state,
                            int64_t *next, int64_t *gen, float *dst, int64_t ldd);
 // Prompt attention over an int8 cache of n_kv heads (attn.hip): query head h

@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "common.h"
+#include "hs_rec.h"
 
 namespace {
 
@@ -61,18 +62,21 @@ __device__ __forceinline__ void k_scale_min(uint32_t s0, uint32_t s1, uint32_t s
     }
 }
 
-// Dequantize one row into float32 (GGUFMatrix.dequant_row, gguf.mojo:381-382).
+// The fields input k of a row reads (its chunk's codes and the type's side
+// data) and the input's value from them (GGUFMatrix.dequant_row,
+// gguf.mojo:381-382).
 template <int TYPE>
-__device__ __forceinline__ void dequant_row_body(const GgufArgs &a, int64_t row, float *dst) {
+struct RowDeq {
     using F = Fmt<TYPE>;
-    const int64_t tile = row / 16, r = row % 16;
-    // The fields input k reads: its chunk's codes and the type's side data.
     struct Fields {
         uint4 d, f;
         uint32_t m;
         uint2 hb;
     };
-    auto load = [&](int k) {
+    const GgufArgs &a;
+    int64_t tile, r;
+    __device__ RowDeq(const GgufArgs &a_, int64_t row) : a(a_), tile(row / 16), r(row % 16) {}
+    __device__ __forceinline__ Fields load(int k) const {
         Fields x{};
         const int c = k / F::WPC;
         const size_t mi = ((size_t)tile * a.CK + c) * 16 + r;
@@ -88,8 +92,8 @@ __device__ __forceinline__ void dequant_row_body(const GgufArgs &a, int64_t row,
             x.m = a.meta16[sbi];
         }
         return x;
-    };
-    auto value = [&](int k, const Fields &x) -> float {
+    }
+    __device__ __forceinline__ float value(int k, const Fields &x) const {
         const int c = k / F::WPC, e = k % F::WPC;
         // the fields as scalars, chosen by selects (an indexed array or struct would go to scratch)
         const uint32_t d0 = x.d.x, d1 = x.d.y, d2 = x.d.z, d3 = x.d.w;
@@ -118,20 +122,26 @@ __device__ __forceinline__ void dequant_row_body(const GgufArgs &a, int64_t row,
                 return (h2f(mm) * sc) * ((float)u - 32.0f);
             }
         }
-    };
+    }
+};
+
+// Dequantize one row into float32 (GGUFMatrix.dequant_row, gguf.mojo:381-382).
+template <int TYPE>
+__device__ __forceinline__ void dequant_row_body(const GgufArgs &a, int64_t row, float *dst) {
+    const RowDeq<TYPE> rd(a, row);
     // NB inputs a thread at a time: every load of the batch is issued before the first value
     constexpr int NB = 8;
     for (int k0 = threadIdx.x; k0 < a.K; k0 += NB * blockDim.x) {
-        Fields x[NB];
+        typename RowDeq<TYPE>::Fields x[NB];
 #pragma unroll
         for (int kk = 0; kk < NB; kk++) {
             const int k = k0 + kk * (int)blockDim.x;
-            x[kk] = load(k < a.K ? k : k0);  // past K: a repeat of k0's fields, not stored
+            x[kk] = rd.load(k < a.K ? k : k0);  // past K: a repeat of k0's fields, not stored
         }
 #pragma unroll
         for (int kk = 0; kk < NB; kk++) {
             const int k = k0 + kk * (int)blockDim.x;
-            if (k < a.K) dst[k] = value(k, x[kk]);
+            if (k < a.K) dst[k] = rd.value(k, x[kk]);
         }
     }
 }
@@ -224,6 +234,84 @@ __global__ __launch_bounds__(256) void gguf_pick_embed_kernel(GgufArgs a, const 
         return;
     }
     dequant_row_body<TYPE>(a, row, d);
+}
+
+// The batch decode chain's pick, embedding and first record in one launch:
+// workgroup (j, b), b < B, picks sequence b's token from its argmax partials
+// (every workgroup of the sequence by the same first-maximum rule,
+// gpt2t.mojo:792-797), writes inputs 256 j .. 256 j + 255 of the token's row
+// of E to dst + b * ldd and the same inputs times rgain to token b of the
+// h16s record rec (the first matmul's input of the next step, with the sums
+// of squares for its RMSNorm); workgroup (0, b) writes next[b] and
+// gen[state[1] * B + b]; the last of the B * gridDim.x workgroups to finish
+// moves the decode state on (state[2] counts them and is cleared again).
+// Workgroups b >= B write zero record rows for the padded tokens.
+template <int TYPE>
+__global__ __launch_bounds__(256) void gguf_pick_embed_rec_kernel(GgufArgs a, const ArgmaxPart *__restrict__ parts,
+                                                                  int nparts, int B, int *__restrict__ state,
+                                                                  int64_t *__restrict__ next,
+                                                                  int64_t *__restrict__ gen, float *__restrict__ dst,
+                                                                  int64_t ldd, HSRec rec,
+                                                                  const float *__restrict__ rgain) {
+    __shared__ ArgmaxPart s_b[4];
+    __shared__ int s_pick;
+    const int j = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int k = j * 256 + tid;
+    if (b >= B) {  // (uniform over the workgroup)
+        hs_store_half(rec, b, k >> 4, 0.0f, 0.0f);
+        return;
+    }
+    const ArgmaxPart *P = parts + (int64_t)b * nparts;
+    const int step = state[1];  // read with the partials (before any advance)
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i0 = tid; i0 < nparts; i0 += 4 * 256) {
+        ArgmaxPart c[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) c[q] = i0 + 256 * q < nparts ? P[i0 + 256 * q] : ArgmaxPart{-INFINITY, 0x7fffffff};
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (c[q].v > bv || (c[q].v == bv && c[q].idx < bi)) {
+                bv = c[q].v;
+                bi = c[q].idx;
+            }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) s_b[tid >> 6] = ArgmaxPart{bv, bi};
+    __syncthreads();
+    if (tid == 0) {
+        ArgmaxPart best = s_b[0];
+        for (int w = 1; w < 4; w++)
+            if (s_b[w].v > best.v || (s_b[w].v == best.v && s_b[w].idx < best.idx)) best = s_b[w];
+        if (j == 0) {
+            next[b] = best.idx;
+            gen[(int64_t)step * B + b] = best.idx;
+        }
+        s_pick = best.idx;
+        __threadfence();
+        if (atomicAdd(&state[2], 1) == (int)gridDim.x * B - 1) {  // every workgroup has read the step
+            state[2] = 0;
+            state[0] += 1;
+            state[1] += 1;
+        }
+    }
+    __syncthreads();
+    const int64_t row = s_pick;
+    float v = 0.0f;
+    if (row >= 0 && row < a.n) {
+        const RowDeq<TYPE> rd(a, row);
+        v = rd.value(k, rd.load(k));
+    }
+    dst[(int64_t)b * ldd + k] = v;
+    hs_store_half(rec, b, k >> 4, v * rgain[k], v);
 }
 
 GgufArgs make_args(const llmq_mat *m) {
@@ -401,6 +489,32 @@ int launch_gguf_dequant_rows(llmq_ctx *ctx, const llmq_mat *w, const int64_t *ro
     case LLMQ_GGML_Q6_K: hipLaunchKernelGGL(gguf_dequant_rows_kernel<LLMQ_GGML_Q6_K>, dim3(n), dim3(256), 0, ctx->stream, a, rows, dst, ldd); break;
     default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf dequant: type %d", w->ggml_type);
     }
+    LLMQ_HIP(hipGetLastError());
+    return LLMQ_OK;
+}
+
+int launch_gguf_pick_embed_rec(llmq_ctx *ctx, const llmq_mat *E, const ArgmaxPart *parts, int nparts, int B,
+                               int *state, int64_t *next, int64_t *gen, float *dst, int64_t ldd, void *rec,
+                               const float *rgain) {
+    LLMQ_REQUIRE(E && E->kind == MAT_GGUF && parts && nparts > 0 && B > 0 && state && next && gen && dst && rec &&
+                     rgain && E->k % 256 == 0 && B <= 65535,
+                 "gguf pick embed rec: bad arguments");
+    GgufArgs a = make_args(E);
+    const HSRec hr = hs_parts(rec, B, E->k);
+    const dim3 grid((unsigned)(E->k / 256), (unsigned)((B + 15) / 16 * 16));
+#define PR(T)                                                                                                     \
+    hipLaunchKernelGGL(gguf_pick_embed_rec_kernel<T>, grid, dim3(256), 0, ctx->stream, a, parts, nparts, B, state, \
+                       next, gen, dst, ldd, hr, rgain)
+    switch (E->ggml_type) {
+    case LLMQ_GGML_Q4_0: PR(LLMQ_GGML_Q4_0); break;
+    case LLMQ_GGML_Q4_1: PR(LLMQ_GGML_Q4_1); break;
+    case LLMQ_GGML_Q8_0: PR(LLMQ_GGML_Q8_0); break;
+    case LLMQ_GGML_Q4_K: PR(LLMQ_GGML_Q4_K); break;
+    case LLMQ_GGML_Q5_K: PR(LLMQ_GGML_Q5_K); break;
+    case LLMQ_GGML_Q6_K: PR(LLMQ_GGML_Q6_K); break;
+    default: return llmq_set_error(LLMQ_EUNSUPPORTED, "gguf pick embed rec: type %d", E->ggml_type);
+    }
+#undef PR
     LLMQ_HIP(hipGetLastError());
     return LLMQ_OK;
 }

@@ -759,6 +759,7 @@ struct llmq_llama {
     int64_t *tokens = nullptr, *next = nullptr, *gen = nullptr;
     int64_t gen_cap = 0;
     int graph_B = 0;  // batch size of the captured decode step
+    bool graph_fused = false;  // whether it was captured as the fused chain
     int *state = nullptr;
     // captured decode steps: [0] one step, [1] step_k steps
     hipGraphExec_t step_graph[2] = {};
@@ -897,13 +898,16 @@ bool fused_chain(const llmq_llama *m, int R, const int *state) {
            m->cfg.n_head % 4 == 0;
 }
 
-int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *state) {
+// Fused: layer 0's record (of m->x times the attention norm gain) is
+// formed here, or, with rec_ready, is already in m->hs[0] (the previous
+// step's pick wrote it).
+int llama_layers(llmq_llama *m, int R, int T, int seq0, int pos0, const int *state, bool rec_ready = false) {
     llmq_ctx *ctx = m->ctx;
     const llmq_llama_cfg &c = m->cfg;
     const int QC = qkv_cols(c);
     const bool fused = fused_chain(m, R, state);
     int cur = 0;  // fused: m->hs[cur] holds the next qkv matmul's input record
-    if (fused) RC(launch_rec_h16s(ctx, m->x, c.dim, R, c.dim, gain(m, 0, 0), m->hs[cur]));
+    if (fused && !rec_ready) RC(launch_rec_h16s(ctx, m->x, c.dim, R, c.dim, gain(m, 0, 0), m->hs[cur]));
     for (int l = 0; l < c.n_layer; l++) {
         if (fused) {
             H16Fuse fq;
@@ -1011,22 +1015,36 @@ int llama_head(llmq_llama *m, int r0, int nrows, ArgmaxPart *parts = nullptr, bo
     return linear(m, m->head, m->xn, c.dim, nrows, m->logits, c.vocab, 0);
 }
 
+// The fused chain's first record, of the embedded picks in m->x (nothing
+// outside the fused chain).
+int decode_rec(llmq_llama *m, int B) {
+    if (!fused_chain(m, B, m->state)) return LLMQ_OK;
+    return launch_rec_h16s(m->ctx, m->x, m->cfg.dim, B, m->cfg.dim, gain(m, 0, 0), m->hs[0]);
+}
+
 // One decode step of every sequence from the embedded picks in m->x: the
 // layers, the head, the picks with the position and step advance, and the
 // picks' embeddings for the next step.
+// In the fused chain the step starts from layer 0's record, which the
+// previous step's pick (or, before the first step, decode_rec) wrote.
 int llama_step(llmq_llama *m, int B) {
     llmq_ctx *ctx = m->ctx;
     const llmq_llama_cfg &c = m->cfg;
-    RC(llama_layers(m, B, 1, 0, 0, m->state));
+    const bool fused = fused_chain(m, B, m->state);
+    RC(llama_layers(m, B, 1, 0, 0, m->state, fused));
     bool parts = false;
     RC(llama_head(m, 0, B, m->hparts, &parts));
+    if (parts && fused)  // the picks, their embeddings and the next step's first record in one launch
+        return launch_gguf_pick_embed_rec(ctx, m->embd, m->hparts, m->nhparts, B, m->state, m->next, m->gen, m->x,
+                                          c.dim, m->hs[0], gain(m, 0, 0));
     if (parts)
         return launch_gguf_pick_embed(ctx, m->embd, m->hparts, m->nhparts, B, m->state, m->next,
                                       m->gen, m->x, c.dim);
     hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(kArgNT), 0, ctx->stream, m->logits, (int64_t)c.vocab, c.vocab, B,
                        0, m->state, 1, m->next, m->gen);
     LLMQ_HIP(hipGetLastError());
-    return launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim);
+    RC(launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim));
+    return decode_rec(m, B);
 }
 
 // Prefill of sequence seq: T tokens (host) at positions pos0.., then its
@@ -1216,6 +1234,11 @@ int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int B, int n_prom
         drop_graph(m);  // it holds the old buffer's address
     }
     RC(ensure_rows(m, n_prompt));
+    // a captured step starts from the fused chain's record only if it was
+    // captured with the chain
+    const bool fz = fused_chain(m, B, m->state);
+    if (fz != m->graph_fused) drop_graph(m);
+    m->graph_fused = fz;
     const char *ge = getenv("LLMQ_GRAPH");
     const bool use_graph = !(ge && ge[0] == '0');  // LLMQ_GRAPH=0: steps launched one by one
     // Each step picks its tokens and positions on the device, so k steps
@@ -1256,6 +1279,7 @@ int llmq_llama_generate(llmq_llama *m, const int64_t *prompts, int B, int n_prom
     const int init_state[4] = {n_prompt, 1, 0, 0};  // position of the first pick, gen row of the next
     LLMQ_HIP(hipMemcpyAsync(m->state, init_state, sizeof(init_state), hipMemcpyHostToDevice, ctx->stream));
     RC(launch_gguf_dequant_rows(ctx, m->embd, m->next, B, m->x, c.dim));  // the first picks, embedded
+    RC(decode_rec(m, B));
     if (use_graph) {
         for (int i = 0; i < n_multi; i++) LLMQ_HIP(hipGraphLaunch(m->step_graph[1], ctx->stream));
         for (int i = 0; i < n_one; i++) LLMQ_HIP(hipGraphLaunch(m->step_graph[0], ctx->stream));
